@@ -1,0 +1,368 @@
+// ffn_capi.hip -- the extern "C" boundary of libffnerf_hip.so (declared in
+// include/ffnerf_hip.h).  Owns a handle per model configuration, the scratch
+// buffers of one step, and the launch sequence of a training step.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "ffn_device.h"
+#include "ffn_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define FFN_HIP(call)                                                                     \
+  do {                                                                                    \
+    hipError_t e_ = (call);                                                               \
+    if (e_ != hipSuccess) return fail(-3, "%s: %s", #call, hipGetErrorString(e_));        \
+  } while (0)
+
+struct Scratch {
+  void* p = nullptr;
+  size_t bytes = 0;
+  hipError_t ensure(size_t need) {
+    if (need <= bytes) return hipSuccess;
+    if (p) {
+      hipError_t e = hipFree(p);
+      if (e != hipSuccess) return e;
+      p = nullptr;
+      bytes = 0;
+    }
+    hipError_t e = hipMalloc(&p, need);
+    if (e != hipSuccess) return e;
+    bytes = need;
+    return hipSuccess;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+struct Handle {
+  ffn_config cfg;
+  ffn::DevCfg dc;
+  ffn::PackedLayout lay;
+  ffn_params params;
+  bool bound = false;
+  int64_t table_floats = 0;
+  int n_cu = 0;
+  Scratch Ts, DTs, flags, a0, dLda0, partials, gtable;
+};
+
+bool is_pow2(uint32_t v) { return v && !(v & (v - 1)); }
+
+int validate_config(const ffn_config* c, int64_t* table_entries) {
+  if (!c) return fail(-1, "config is NULL");
+  if (c->n_levels < 1 || c->n_levels > FFN_MAX_LEVELS) return fail(-1, "n_levels=%d out of [1,%d]", c->n_levels, FFN_MAX_LEVELS);
+  if (c->f_per_level != 1 && c->f_per_level != 2 && c->f_per_level != 4)
+    return fail(-1, "f_per_level=%d unsupported (1, 2 or 4)", c->f_per_level);
+  int64_t tot = 0;
+  for (int l = 0; l < c->n_levels; ++l) {
+    if (c->log2_T[l] < 1 || c->log2_T[l] > 26) return fail(-1, "log2_T[%d]=%u out of [1,26]", l, c->log2_T[l]);
+    if (c->res[l] < 2) return fail(-1, "res[%d]=%d must be >= 2", l, c->res[l]);
+    tot += (int64_t)1 << c->log2_T[l];
+  }
+  if (tot * c->f_per_level >= ((int64_t)1 << 32)) return fail(-1, "hash table too large for 32-bit feature indices");
+  *table_entries = tot;
+  if (c->nd < 1 || c->nd > 3) return fail(-1, "nd=%d out of [1,3]", c->nd);
+  if (c->nc < 1 || c->nc > 4) return fail(-1, "nc=%d out of [1,4]", c->nc);
+  if (c->occ_G < 1 || c->occ_G > 1024) return fail(-1, "occ_G=%d out of [1,1024]", c->occ_G);
+  for (int i = 0; i < 3; ++i)
+    if (!(c->box_max[i] > c->box_min[i])) return fail(-1, "box_max must exceed box_min on every axis");
+  if (c->background < 0 || c->background > 2) return fail(-1, "background=%d unknown", c->background);
+  if (c->hash_opt != FFN_HASH_SGD && c->hash_opt != FFN_HASH_ADAM) return fail(-1, "hash_opt=%d unknown", c->hash_opt);
+  if (c->mlp_precision != FFN_MLP_FP32) return fail(-1, "mlp_precision=%d not built (fp32 only)", c->mlp_precision);
+  return 0;
+}
+
+ffn::DevCfg make_devcfg(const ffn_config* c) {
+  ffn::DevCfg d{};
+  d.L = c->n_levels;
+  d.F = c->f_per_level;
+  d.LF = c->n_levels * c->f_per_level;
+  uint32_t off = 0;
+  for (int l = 0; l < c->n_levels; ++l) {
+    d.mask[l] = (1u << c->log2_T[l]) - 1u;
+    d.offset[l] = off;
+    off += 1u << c->log2_T[l];
+    d.res[l] = c->res[l];
+    d.lvl_lr_scale[l] = c->lvl_lr_scale[l];
+  }
+  d.nd = c->nd;
+  d.nc = c->nc;
+  d.G = c->occ_G;
+  for (int i = 0; i < 3; ++i) {
+    d.bmin[i] = c->box_min[i];
+    d.bmax[i] = c->box_max[i];
+  }
+  d.rho_min = c->rho_min;
+  d.rho_max = c->rho_max;
+  d.dt_min = c->dt_min;
+  d.dt_max = c->dt_max;
+  d.t_near = c->t_near;
+  d.t_far = c->t_far;
+  d.background = c->background;
+  d.hash_opt = c->hash_opt;
+  return d;
+}
+
+Handle* as_handle(void* h) { return static_cast<Handle*>(h); }
+
+}  // namespace
+
+extern "C" {
+
+int ffn_version(void) { return FFN_ABI_VERSION; }
+
+const char* ffn_last_error(void) { return g_err.c_str(); }
+
+int ffn_create(const ffn_config* cfg, void** handle) {
+  if (!handle) return fail(-1, "handle out-pointer is NULL");
+  *handle = nullptr;
+  int64_t entries = 0;
+  int rc = validate_config(cfg, &entries);
+  if (rc) return rc;
+  Handle* h = new Handle();
+  h->cfg = *cfg;
+  h->dc = make_devcfg(cfg);
+  h->lay = ffn::make_layout(h->dc.LF, cfg->nd, cfg->nc);
+  h->table_floats = entries * cfg->f_per_level;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&h->n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) {
+    delete h;
+    return fail(-3, "no HIP device: %s", hipGetErrorString(e));
+  }
+  *handle = h;
+  g_err.clear();
+  return 0;
+}
+
+int ffn_destroy(void* handle) {
+  Handle* h = as_handle(handle);
+  if (!h) return 0;
+  (void)hipDeviceSynchronize();
+  h->Ts.release();
+  h->DTs.release();
+  h->flags.release();
+  h->a0.release();
+  h->dLda0.release();
+  h->partials.release();
+  h->gtable.release();
+  delete h;
+  return 0;
+}
+
+int ffn_bind_params(void* handle, const ffn_params* p) {
+  Handle* h = as_handle(handle);
+  if (!h || !p) return fail(-1, "NULL handle or params");
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    if (!ffn::layer_active(k, h->cfg.nd, h->cfg.nc)) continue;
+    if (!p->W[k] || !p->b[k] || !p->mW[k] || !p->vW[k] || !p->mb[k] || !p->vb[k])
+      return fail(-1, "layer slot %d is active but a parameter/optimizer pointer is NULL", k);
+  }
+  if (!p->table) return fail(-1, "table is NULL");
+  if (h->cfg.hash_opt == FFN_HASH_ADAM && (!p->m_table || !p->v_table))
+    return fail(-1, "FFN_HASH_ADAM needs m_table and v_table");
+  if (!p->occ_in) return fail(-1, "occ_in is NULL");
+  h->params = *p;
+  h->bound = true;
+  return 0;
+}
+
+int ffn_occ_decay(uint32_t* occ_in, uint32_t* occ_st, uint32_t n_words, uint32_t decay_q24, uint32_t iter_seed,
+                  void* stream) {
+  if (!occ_in || !occ_st) return fail(-1, "occupancy grids must not be NULL");
+  if (decay_q24 > (1u << 24)) return fail(-1, "decay_q24=%u exceeds 2^24", decay_q24);
+  FFN_HIP(ffn::launch_occ_decay(occ_in, occ_st, n_words, decay_q24, iter_seed, (hipStream_t)stream));
+  return 0;
+}
+
+int ffn_adam(float* p, float* m, float* v, float* g, int64_t n, float lr_t, float beta1, float beta2, float eps,
+             int32_t zero_grad, void* stream) {
+  if (n < 0) return fail(-1, "negative size");
+  if (n > 0 && (!p || !m || !v || !g)) return fail(-1, "NULL buffer");
+  FFN_HIP(ffn::launch_adam(p, m, v, g, n, lr_t, beta1, beta2, eps, zero_grad, (hipStream_t)stream));
+  return 0;
+}
+
+int ffn_sample(void* handle, const void* rays, uint32_t num_rays, uint32_t spr, uint32_t rng_seed, int32_t do_train,
+               float* Ts, float* DTs, uint32_t* flags, void* stream) {
+  Handle* h = as_handle(handle);
+  if (!h) return fail(-1, "NULL handle");
+  if (!is_pow2(spr) || spr > FFN_S_MAX) return fail(-1, "samples_per_ray=%u must be a power of two <= %d", spr, FFN_S_MAX);
+  if (!rays || !Ts || !DTs || !flags) return fail(-1, "NULL buffer");
+  if (!h->params.occ_in) return fail(-1, "bind params (occ_in) first");
+  if (num_rays == 0) return 0;
+  FFN_HIP(ffn::launch_sample(h->dc, (const float4*)rays, num_rays, (int)spr, rng_seed, h->params.occ_in, do_train, Ts,
+                             DTs, flags, (hipStream_t)stream));
+  return 0;
+}
+
+int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint32_t* idx_out, void* stream) {
+  Handle* h = as_handle(handle);
+  if (!h) return fail(-1, "NULL handle");
+  if (n < 0) return fail(-1, "negative size");
+  if (n > 0 && (!x || !a0)) return fail(-1, "NULL buffer");
+  if (!h->params.table) return fail(-1, "bind params (table) first");
+  FFN_HIP(ffn::launch_hash_fwd(h->dc, x, nullptr, nullptr, 0, n, h->params.table, a0, idx_out, (hipStream_t)stream));
+  return 0;
+}
+
+int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n, float* grad, void* stream) {
+  Handle* h = as_handle(handle);
+  if (!h) return fail(-1, "NULL handle");
+  if (n < 0) return fail(-1, "negative size");
+  if (n > 0 && (!x || !g || !grad)) return fail(-1, "NULL buffer");
+  FFN_HIP(ffn::launch_hash_bwd(h->dc, x, nullptr, nullptr, 0, n, g, grad, 0, 0.0f, (hipStream_t)stream));
+  return 0;
+}
+
+int ffn_train_step(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
+                   uint32_t spr, const ffn_step_scalars* sc, const ffn_taps* taps, void* stream) {
+  Handle* h = as_handle(handle);
+  if (!h) return fail(-1, "NULL handle");
+  if (!h->bound) return fail(-1, "ffn_bind_params must be called before ffn_train_step");
+  if (!sc) return fail(-1, "NULL scalars");
+  if (!is_pow2(spr) || spr > FFN_S_MAX) return fail(-1, "samples_per_ray=%u must be a power of two <= %d", spr, FFN_S_MAX);
+  if (num_rays == 0) return fail(-1, "num_rays must be > 0");
+  if (!rays || !out_rgb) return fail(-1, "NULL rays/out_rgb");
+  const bool train = sc->do_train != 0;
+  if (train && !targets) return fail(-1, "training needs targets");
+  if (train && sc->occ_strength > 0.0f && !h->params.occ_st) return fail(-1, "proposals need occ_st");
+  const int LF = h->dc.LF;
+  if (!ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
+    return fail(-2, "MLP shape LF=%d nd=%d nc=%d is not built", LF, h->cfg.nd, h->cfg.nc);
+  hipStream_t st = (hipStream_t)stream;
+  int log2S = 0;
+  while ((1u << log2S) < spr) ++log2S;
+  const int64_t N = (int64_t)num_rays * spr;
+  const int64_t n_tiles = (N + 63) / 64;
+  int n_blocks = h->n_cu > 0 ? h->n_cu : 256;
+  if (n_blocks > n_tiles) n_blocks = (int)n_tiles;
+
+  FFN_HIP(h->Ts.ensure(sizeof(float) * N));
+  FFN_HIP(h->DTs.ensure(sizeof(float) * N));
+  FFN_HIP(h->flags.ensure(sizeof(uint32_t) * 2 * (size_t)num_rays));
+  FFN_HIP(h->a0.ensure(sizeof(float) * N * LF));
+  if (train) {
+    FFN_HIP(h->dLda0.ensure(sizeof(float) * N * LF));
+    FFN_HIP(h->partials.ensure(sizeof(float) * (size_t)n_blocks * h->lay.total));
+    if (h->cfg.hash_opt == FFN_HASH_ADAM && h->gtable.bytes < sizeof(float) * (size_t)h->table_floats) {
+      FFN_HIP(h->gtable.ensure(sizeof(float) * (size_t)h->table_floats));
+      FFN_HIP(ffn::launch_fill((float*)h->gtable.p, h->table_floats, 0.0f, st));
+    }
+  }
+  float* Ts = (float*)h->Ts.p;
+  float* DTs = (float*)h->DTs.p;
+  uint32_t* flags = (uint32_t*)h->flags.p;
+  float* a0 = (float*)h->a0.p;
+  float* dLda0 = (float*)h->dLda0.p;
+  const ffn_params& P = h->params;
+
+  FFN_HIP(ffn::launch_sample(h->dc, (const float4*)rays, num_rays, (int)spr, sc->rng_seed, P.occ_in, train ? 1 : 0,
+                             Ts, DTs, flags, st));
+  FFN_HIP(ffn::launch_hash_fwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, P.table, a0, nullptr, st));
+
+  ffn::MlpArgs a{};
+  a.c = h->dc;
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    a.w.W[k] = P.W[k];
+    a.w.b[k] = P.b[k];
+  }
+  a.rays = (const float4*)rays;
+  a.targets = (const float4*)targets;
+  a.out_rgb = (float4*)out_rgb;
+  a.Ts = Ts;
+  a.DTs = DTs;
+  a.flags = flags;
+  a.a0 = a0;
+  a.dL_da0 = dLda0;
+  a.partials = (float*)h->partials.p;
+  a.occ_in = P.occ_in;
+  a.occ_st = P.occ_st;
+  a.num_rays = num_rays;
+  a.S = (int)spr;
+  a.log2S = log2S;
+  a.n_tiles = n_tiles;
+  a.sh_mult = sc->sh_multiplier;
+  a.occ_strength = sc->occ_strength;
+  a.seed = sc->rng_seed;
+  a.do_train = train ? 1 : 0;
+  if (taps) {
+    a.t_sigma = taps->sigma;
+    a.t_rgb = taps->rgb;
+    a.t_Tr = taps->Tr;
+    a.t_dLds = taps->dL_dsigma;
+    a.t_dLdc = taps->dL_dc;
+  }
+  FFN_HIP(ffn::launch_mlp(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+
+  if (taps) {
+    if (taps->Ts) FFN_HIP(hipMemcpyAsync(taps->Ts, Ts, sizeof(float) * N, hipMemcpyDeviceToDevice, st));
+    if (taps->DTs) FFN_HIP(hipMemcpyAsync(taps->DTs, DTs, sizeof(float) * N, hipMemcpyDeviceToDevice, st));
+    if (taps->flags)
+      FFN_HIP(hipMemcpyAsync(taps->flags, flags, sizeof(uint32_t) * 2 * num_rays, hipMemcpyDeviceToDevice, st));
+    if (taps->a0) FFN_HIP(hipMemcpyAsync(taps->a0, a0, sizeof(float) * N * LF, hipMemcpyDeviceToDevice, st));
+    if (train && taps->dL_da0)
+      FFN_HIP(hipMemcpyAsync(taps->dL_da0, dLda0, sizeof(float) * N * LF, hipMemcpyDeviceToDevice, st));
+  }
+  if (!train) return 0;
+
+  if (h->cfg.hash_opt == FFN_HASH_SGD) {
+    FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, P.table, 1, sc->lr, st));
+  } else {
+    FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, (float*)h->gtable.p, 0,
+                                 0.0f, st));
+  }
+
+  ffn::MlpOptArgs o{};
+  o.lay = h->lay;
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    o.W[k] = P.W[k];
+    o.b[k] = P.b[k];
+    o.mW[k] = P.mW[k];
+    o.vW[k] = P.vW[k];
+    o.mb[k] = P.mb[k];
+    o.vb[k] = P.vb[k];
+    if (taps) {
+      o.gW[k] = taps->gW[k];
+      o.gb[k] = taps->gb[k];
+    }
+  }
+  o.partials = (const float*)h->partials.p;
+  o.n_partials = n_blocks;
+  o.lr_t = sc->lr_t;
+  o.color_rel_lr = sc->color_rel_lr;
+  o.beta1 = sc->beta1;
+  o.beta2 = sc->beta2;
+  o.eps = sc->eps;
+  FFN_HIP(ffn::launch_mlp_adam(o, st));
+
+  if (h->cfg.hash_opt == FFN_HASH_ADAM) {
+    if (taps && taps->g_table)
+      FFN_HIP(hipMemcpyAsync(taps->g_table, h->gtable.p, sizeof(float) * (size_t)h->table_floats,
+                             hipMemcpyDeviceToDevice, st));
+    FFN_HIP(ffn::launch_adam(P.table, P.m_table, P.v_table, (float*)h->gtable.p, h->table_floats, sc->lr_t,
+                             sc->beta1, sc->beta2, sc->eps, 1, st));
+  }
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,376 @@
+// ffn_device.h -- device-side helpers shared by the gfx950 kernels.
+//
+// All kernels of this library are compiled with -ffp-contract=off: every
+// multiply and add rounds on its own, so the integer-valued outputs that
+// depend on floats (sample positions, hash corner indices, occupancy words)
+// are reproducible operation for operation.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ffnerf_hip.h"
+
+#define FFN_M 64
+#define FFN_D_OUT 16
+#define FFN_L_DIR 16
+#define FFN_C_IN 32
+#define FFN_C_OUT 3
+#define FFN_S_MAX 64
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+namespace ffn {
+
+// Everything a kernel needs from ffn_config, flattened into a kernel argument.
+struct DevCfg {
+  int L, F, LF;
+  uint32_t mask[FFN_MAX_LEVELS];    // 2^log2_T - 1
+  uint32_t offset[FFN_MAX_LEVELS];  // level offset in entries
+  int res[FFN_MAX_LEVELS];
+  float lvl_lr_scale[FFN_MAX_LEVELS];
+  int nd, nc, G;
+  float bmin[3], bmax[3];
+  float rho_min, rho_max, dt_min, dt_max, t_near, t_far;
+  int background, hash_opt;
+};
+
+// ---------------------------------------------------------------------------
+// integer hash and xorshift (ffnerf_OG.cl:293-311)
+
+__device__ __forceinline__ uint32_t hash_u32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+__device__ __forceinline__ float rand01(uint32_t& state) {
+  uint32_t x = state;
+  x ^= x << 13;
+  x ^= x >> 17;
+  x ^= x << 5;
+  state = x;
+  return (float)(x & 0x00FFFFFFu) * (1.0f / 16777216.0f);
+}
+
+// ---------------------------------------------------------------------------
+// powr(x, y) for the sampler weights: double-precision exp(y * log(x)) from
+// + - * / only (log: exponent split + atanh series; exp: Cody-Waite reduction
+// by ln2 + Taylor series to degree 13), then rounded once to float.
+// Deterministic across CPU and GPU; within one float ulp of the true power.
+
+__device__ __forceinline__ double det_log(double x) {
+  const double LN2_HI = 6.93147180369123816490e-01;
+  const double LN2_LO = 1.90821492927058770002e-10;
+  uint64_t bits = (uint64_t)__double_as_longlong(x);
+  int e = (int)((bits >> 52) & 0x7ff) - 1023;
+  bits = (bits & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL;
+  double m = __longlong_as_double((long long)bits);
+  if (m > 1.4142135623730951) {
+    m = m * 0.5;
+    e += 1;
+  }
+  double s = (m - 1.0) / (m + 1.0);
+  double s2 = s * s;
+  double p = 1.0 / 25.0;
+  p = p * s2 + 1.0 / 23.0;
+  p = p * s2 + 1.0 / 21.0;
+  p = p * s2 + 1.0 / 19.0;
+  p = p * s2 + 1.0 / 17.0;
+  p = p * s2 + 1.0 / 15.0;
+  p = p * s2 + 1.0 / 13.0;
+  p = p * s2 + 1.0 / 11.0;
+  p = p * s2 + 1.0 / 9.0;
+  p = p * s2 + 1.0 / 7.0;
+  p = p * s2 + 1.0 / 5.0;
+  p = p * s2 + 1.0 / 3.0;
+  p = p * s2 + 1.0;
+  double lnm = 2.0 * s * p;
+  double de = (double)e;
+  return de * LN2_HI + (de * LN2_LO + lnm);
+}
+
+__device__ __forceinline__ double det_exp(double z) {
+  const double LN2_HI = 6.93147180369123816490e-01;
+  const double LN2_LO = 1.90821492927058770002e-10;
+  double k = floor(z * 1.4426950408889634 + 0.5);
+  double r = (z - k * LN2_HI) - k * LN2_LO;
+  double p = 1.0 / 6227020800.0;
+  p = p * r + 1.0 / 479001600.0;
+  p = p * r + 1.0 / 39916800.0;
+  p = p * r + 1.0 / 3628800.0;
+  p = p * r + 1.0 / 362880.0;
+  p = p * r + 1.0 / 40320.0;
+  p = p * r + 1.0 / 5040.0;
+  p = p * r + 1.0 / 720.0;
+  p = p * r + 1.0 / 120.0;
+  p = p * r + 1.0 / 24.0;
+  p = p * r + 1.0 / 6.0;
+  p = p * r + 0.5;
+  p = p * r + 1.0;
+  p = p * r + 1.0;
+  int ki = (int)k;
+  if (ki < -1022) return 0.0;
+  if (ki > 1023) return __longlong_as_double(0x7ff0000000000000LL);
+  double two_k = __longlong_as_double((long long)((uint64_t)(ki + 1023) << 52));
+  return p * two_k;
+}
+
+__device__ __forceinline__ float safe_pow_pos(float x, float y) {  // ffnerf_OG.cl:665-671
+  x = fmaxf(x, 0.0f);
+  if (x <= 0.0f) return 0.0f;
+  if (!(x < __builtin_huge_valf())) return x;
+  return (float)det_exp((double)y * det_log((double)x));
+}
+
+// ---------------------------------------------------------------------------
+// ray / box slab test (ffnerf_OG.cl:322-343)
+
+__device__ __forceinline__ bool ray_aabb(const float o[3], const float d[3], const float bmin[3],
+                                         const float bmax[3], float& t0, float& t1) {
+  float tmin3[3], tmax3[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    float invd = (d[i] != 0.0f) ? (1.0f / d[i]) : __builtin_huge_valf();
+    float tb = (bmin[i] - o[i]) * invd;
+    float tt = (bmax[i] - o[i]) * invd;
+    tmin3[i] = fminf(tb, tt);
+    tmax3[i] = fmaxf(tb, tt);
+  }
+  float tmin = fmaxf(tmin3[0], fmaxf(tmin3[1], tmin3[2]));
+  float tmax = fminf(tmax3[0], fminf(tmax3[1], tmax3[2]));
+  if (tmax < tmin) return false;
+  t0 = tmin;
+  t1 = tmax;
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// hash grid corner math (ffnerf_OG.cl:1286-1364); bit-identical to the oracle
+
+__device__ __forceinline__ void normalize_pos(const DevCfg& c, const float x[3], float p[3]) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    float bs = c.bmax[i] - c.bmin[i];
+    float v = (x[i] - c.bmin[i]) / bs;
+    p[i] = fminf(fmaxf(v, 0.0f), 1.0f - 1.0e-6f);
+  }
+}
+
+struct LevelCell {
+  int i0[3];
+  float f[3];
+};
+
+__device__ __forceinline__ LevelCell level_cell(int R, const float p[3]) {
+  LevelCell lc;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    float u = p[i] * (float)R;
+    int v = (int)floorf(u);
+    v = v < 0 ? 0 : (v > R - 2 ? R - 2 : v);
+    lc.i0[i] = v;
+    lc.f[i] = u - (float)v;
+  }
+  return lc;
+}
+
+__device__ __forceinline__ float corner_weight(const LevelCell& lc, int cc) {
+  float wx = (cc & 1) ? lc.f[0] : 1.0f - lc.f[0];
+  float wy = (cc & 2) ? lc.f[1] : 1.0f - lc.f[1];
+  float wz = (cc & 4) ? lc.f[2] : 1.0f - lc.f[2];
+  return wx * wy * wz;
+}
+
+__device__ __forceinline__ uint32_t corner_entry(const LevelCell& lc, int cc, int lvl, uint32_t mask) {
+  uint32_t ix = (uint32_t)(lc.i0[0] + (cc & 1));
+  uint32_t iy = (uint32_t)(lc.i0[1] + ((cc >> 1) & 1));
+  uint32_t iz = (uint32_t)(lc.i0[2] + ((cc >> 2) & 1));
+  return hash_u32(ix * 73856093u ^ iy * 19349663u ^ iz * 83492791u ^ (uint32_t)lvl * 2654435761u) & mask;
+}
+
+// ---------------------------------------------------------------------------
+// activations (ffnerf_OG.cl:214-253) and SH degree 3 (ffnerf_OG.cl:572-602)
+
+__device__ __forceinline__ float softplus(float x) {
+  if (x > 20.0f) return x;
+  if (x < -20.0f) return expf(x);
+  return log1pf(expf(x));
+}
+__device__ __forceinline__ float softplus_prime_from_pre(float x) {
+  if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+  float e = expf(x);
+  return e / (1.0f + e);
+}
+__device__ __forceinline__ float sigmoid_soft(float x) {
+  x *= 0.5f;
+  x = fminf(fmaxf(x, -18.0f), 18.0f);
+  if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+  float e = expf(x);
+  return e / (1.0f + e);
+}
+__device__ __forceinline__ float charbonnier_prime(float x) {
+  const float e2 = 1.0e-3f * 1.0e-3f;
+  return x * (1.0f / sqrtf(x * x + e2));
+}
+
+__device__ __forceinline__ float sh_component(const float d[3], int i) {
+  const float x = d[0], y = d[1], z = d[2];
+  switch (i) {
+    case 0: return 0.28209479177387814f;
+    case 1: return 0.4886025119029199f * y;
+    case 2: return 0.4886025119029199f * z;
+    case 3: return 0.4886025119029199f * x;
+    case 4: return 1.0925484305920792f * x * y;
+    case 5: return 1.0925484305920792f * y * z;
+    case 6: return 0.31539156525252005f * (3.0f * z * z - 1.0f);
+    case 7: return 1.0925484305920792f * x * z;
+    case 8: return 0.5462742152960396f * (x * x - y * y);
+    case 9: return 0.5900435899266435f * y * (3.0f * x * x - y * y);
+    case 10: return 2.890611442640554f * x * y * z;
+    case 11: return 0.4570457994644658f * y * (5.0f * z * z - 1.0f);
+    case 12: return 0.3731763325901154f * (5.0f * z * z * z - 3.0f * z);
+    case 13: return 0.4570457994644658f * x * (5.0f * z * z - 1.0f);
+    case 14: return 1.445305721320277f * z * (x * x - y * y);
+    default: return 0.5900435899266435f * x * (x * x - 3.0f * y * y);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Work-group scans of the reference restated on wave lanes.  A "segment" is
+// S consecutive lanes (S a power of two <= 64) holding one ray; lid is the
+// lane's index inside it and base the segment's first lane.  The trees and
+// the operand order of every combine are those of ffnerf_OG.cl:619-646 and
+// 691-735 (including the down-sweep's new_right = combine(old_left,
+// old_right)), so results are bit-identical to the CPU restatement.
+
+__device__ __forceinline__ bool is_right(int lid, int stride) { return ((lid + 1) & (2 * stride - 1)) == 0; }
+__device__ __forceinline__ bool is_left(int lid, int stride) {
+  return ((lid + 1 + stride) & (2 * stride - 1)) == 0;
+}
+
+__device__ __forceinline__ float seg_scan_excl_add(float v, int lid, int S, int base) {
+  for (int stride = 1; stride < S; stride <<= 1) {
+    float o = __shfl(v, base + lid - stride);
+    if (is_right(lid, stride)) v = v + o;
+  }
+  if (lid == S - 1) v = 0.0f;
+  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
+    float from_l = __shfl(v, base + lid - stride);
+    float from_r = __shfl(v, base + lid + stride);
+    if (is_right(lid, stride)) v = v + from_l;
+    else if (is_left(lid, stride)) v = from_r;
+  }
+  return v;
+}
+
+// ffnerf_OG.cl:639-646: a[lid] += a[lid + stride] for lid < stride; result a[0] broadcast
+__device__ __forceinline__ float seg_reduce_add(float v, int lid, int S, int base) {
+  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
+    float o = __shfl(v, base + lid + stride);
+    if (lid < stride) v = v + o;
+  }
+  return __shfl(v, base);
+}
+
+struct Seg {
+  float a, v0, v1, v2;
+};
+__device__ __forceinline__ Seg seg_combine(const Seg& L, const Seg& R) {
+  Seg O;
+  O.a = L.a * R.a;
+  O.v0 = L.v0 + L.a * R.v0;
+  O.v1 = L.v1 + L.a * R.v1;
+  O.v2 = L.v2 + L.a * R.v2;
+  return O;
+}
+__device__ __forceinline__ Seg shfl_seg(const Seg& s, int src) {
+  Seg o;
+  o.a = __shfl(s.a, src);
+  o.v0 = __shfl(s.v0, src);
+  o.v1 = __shfl(s.v1, src);
+  o.v2 = __shfl(s.v2, src);
+  return o;
+}
+
+// exclusive Seg scan; returns the lane's prefix, total of the segment in *total
+__device__ __forceinline__ Seg seg_scan_excl_seg(Seg v, int lid, int S, int base, Seg* total) {
+  for (int stride = 1; stride < S; stride <<= 1) {
+    Seg o = shfl_seg(v, base + lid - stride);
+    if (is_right(lid, stride)) v = seg_combine(o, v);
+  }
+  *total = shfl_seg(v, base + S - 1);
+  if (lid == S - 1) {
+    v.a = 1.0f;
+    v.v0 = v.v1 = v.v2 = 0.0f;
+  }
+  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
+    Seg from_l = shfl_seg(v, base + lid - stride);
+    Seg from_r = shfl_seg(v, base + lid + stride);
+    if (is_right(lid, stride)) v = seg_combine(from_l, v);
+    else if (is_left(lid, stride)) v = from_r;
+  }
+  return v;
+}
+
+struct Aff {
+  float a, b;
+};
+__device__ __forceinline__ Aff aff_combine_rev(const Aff& L, const Aff& R) {
+  Aff O;
+  O.a = R.a * L.a;
+  O.b = R.a * L.b + R.b;
+  return O;
+}
+__device__ __forceinline__ Aff shfl_aff(const Aff& s, int src) {
+  Aff o;
+  o.a = __shfl(s.a, src);
+  o.b = __shfl(s.b, src);
+  return o;
+}
+// exclusive scan with aff_combine_rev over the segment's lanes in lane order
+__device__ __forceinline__ Aff seg_scan_excl_aff_rev(Aff v, int lid, int S, int base) {
+  for (int stride = 1; stride < S; stride <<= 1) {
+    Aff o = shfl_aff(v, base + lid - stride);
+    if (is_right(lid, stride)) v = aff_combine_rev(o, v);
+  }
+  if (lid == S - 1) {
+    v.a = 1.0f;
+    v.b = 0.0f;
+  }
+  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
+    Aff from_l = shfl_aff(v, base + lid - stride);
+    Aff from_r = shfl_aff(v, base + lid + stride);
+    if (is_right(lid, stride)) v = aff_combine_rev(from_l, v);
+    else if (is_left(lid, stride)) v = from_r;
+  }
+  return v;
+}
+
+// next set bit strictly after lid inside the segment's 64-bit run mask, or S
+__device__ __forceinline__ int find_next_flag(uint64_t segmask, int lid, int S) {
+  if (lid + 1 >= S) return S;
+  uint64_t m = segmask >> (lid + 1);
+  if (m == 0) return S;
+  int r = lid + 1 + (int)__builtin_ctzll(m);
+  return r < S ? r : S;
+}
+
+// CAS nibble max into an occupancy word (ffnerf_OG.cl:486-512)
+__device__ __forceinline__ void occ_nibble_atomic_max(uint32_t* grid, int cell, uint32_t sub, uint32_t proposed_q) {
+  const uint32_t shift = 4u * sub;
+  const uint32_t mask = 0xFu << shift;
+  uint32_t old_u = __hip_atomic_load(grid + cell, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    uint32_t old_q = ((old_u >> shift) & 0xFu) + 1u;
+    if (proposed_q <= old_q) return;
+    uint32_t new_u = (old_u & ~mask) | (((proposed_q - 1u) & 0xFu) << shift);
+    uint32_t prev = atomicCAS(grid + cell, old_u, new_u);
+    if (prev == old_u) return;
+    old_u = prev;
+  }
+}
+
+}  // namespace ffn

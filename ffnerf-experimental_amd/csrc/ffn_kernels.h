@@ -1,0 +1,121 @@
+// ffn_kernels.h -- launchers of the gfx950 kernels (internal to the library).
+#pragma once
+#include "ffn_device.h"
+
+namespace ffn {
+
+// packed layout of the MLP parameters: per active layer slot, W [out][in] then b [out]
+struct __attribute__((packed)) PackedLayout {
+  int active[FFN_N_LAYERS];
+  int out[FFN_N_LAYERS];
+  int in[FFN_N_LAYERS];
+  int w_off[FFN_N_LAYERS];
+  int b_off[FFN_N_LAYERS];
+  int total;
+};
+
+__host__ __device__ constexpr bool layer_active(int k, int nd, int nc) {
+  return k == FFN_WD_IN || k == FFN_WD_OUT || k == FFN_WC_IN || k == FFN_WC_OUT || (k == FFN_WD_01 && nd >= 2) ||
+         (k == FFN_WD_12 && nd >= 3) || (k == FFN_WC_01 && nc >= 2) || (k == FFN_WC_12 && nc >= 3) ||
+         (k == FFN_WC_23 && nc >= 4);
+}
+__host__ __device__ constexpr int layer_out(int k) {
+  return k == FFN_WD_OUT ? FFN_D_OUT : (k == FFN_WC_OUT ? FFN_C_OUT : FFN_M);
+}
+__host__ __device__ constexpr int layer_in(int k, int LF) {
+  return k == FFN_WD_IN ? LF : (k == FFN_WC_IN ? FFN_C_IN : FFN_M);
+}
+
+inline PackedLayout make_layout(int LF, int nd, int nc) {
+  PackedLayout p{};
+  int o = 0;
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    p.active[k] = layer_active(k, nd, nc) ? 1 : 0;
+    p.out[k] = layer_out(k);
+    p.in[k] = layer_in(k, LF);
+    if (!p.active[k]) {
+      p.w_off[k] = p.b_off[k] = -1;
+      continue;
+    }
+    p.w_off[k] = o;
+    o += p.out[k] * p.in[k];
+    p.b_off[k] = o;
+    o += p.out[k];
+  }
+  p.total = o;
+  return p;
+}
+
+struct MlpPtrs {
+  const float* W[FFN_N_LAYERS];
+  const float* b[FFN_N_LAYERS];
+};
+
+struct MlpArgs {
+  DevCfg c;
+  MlpPtrs w;
+  const float4* rays;
+  const float4* targets;
+  float4* out_rgb;
+  const float* Ts;
+  const float* DTs;
+  const uint32_t* flags;
+  const float* a0;
+  float* dL_da0;
+  float* partials;  // [gridDim.x][layout.total]
+  const uint32_t* occ_in;
+  uint32_t* occ_st;
+  uint32_t num_rays;
+  int S, log2S;
+  int64_t n_tiles;
+  float sh_mult, occ_strength;
+  uint32_t seed;
+  int do_train;
+  // taps
+  float* t_sigma;
+  float* t_rgb;
+  float* t_Tr;
+  float* t_dLds;
+  float* t_dLdc;
+};
+
+hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays, int S, uint32_t seed,
+                         const uint32_t* occ_in, int do_train, float* Ts, float* DTs, uint32_t* flags,
+                         hipStream_t st);
+
+// positions either x[n][3] (rays == nullptr) or o + Ts[b] d of ray b >> log2S
+hipError_t launch_hash_fwd(const DevCfg& c, const float* x, const float4* rays, const float* Ts, int log2S,
+                           int64_t n, const float* table, float* a0, uint32_t* idx_out, hipStream_t st);
+// mode 0: grad[...] += g*w ; mode 1: table[...] += (-lr*scale_l*0.5*g)*w (reference SGD)
+hipError_t launch_hash_bwd(const DevCfg& c, const float* x, const float4* rays, const float* Ts, int log2S,
+                           int64_t n, const float* g, float* dst, int mode, float lr, hipStream_t st);
+
+hipError_t launch_adam(float* p, float* m, float* v, float* g, int64_t n, float lr_t, float b1, float b2, float eps,
+                       int zero_grad, hipStream_t st);
+hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st);
+hipError_t launch_occ_decay(uint32_t* occ_in, uint32_t* occ_st, uint32_t n_words, uint32_t decay_q24,
+                            uint32_t seed, hipStream_t st);
+
+// fused MLP forward + compositing + loss + backward + proposals, per 64-sample tile
+bool mlp_supported(int LF, int nd, int nc);
+size_t mlp_lds_bytes(int LF, int nd, int nc);
+hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+
+// sum the per-block gradient partials and apply Adam to the MLP parameters
+struct MlpOptArgs {
+  PackedLayout lay;
+  float* W[FFN_N_LAYERS];
+  float* b[FFN_N_LAYERS];
+  float* mW[FFN_N_LAYERS];
+  float* vW[FFN_N_LAYERS];
+  float* mb[FFN_N_LAYERS];
+  float* vb[FFN_N_LAYERS];
+  float* gW[FFN_N_LAYERS];  // optional taps
+  float* gb[FFN_N_LAYERS];
+  const float* partials;
+  int n_partials;
+  float lr_t, color_rel_lr, beta1, beta2, eps;
+};
+hipError_t launch_mlp_adam(const MlpOptArgs& a, hipStream_t st);
+
+}  // namespace ffn

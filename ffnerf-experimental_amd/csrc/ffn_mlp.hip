@@ -1,0 +1,651 @@
+// ffn_mlp.hip -- fused density+color MLP forward, volume compositing,
+// photometric loss gradient, compositing backward, occupancy proposals, MLP
+// backward and weight-gradient accumulation.
+//
+// Reference: ffnerf_OG.cl:1373-1466 (MLP fwd), 1505-1634 (compositing, loss,
+// reverse affine scan), 1640-1821 (proposals), 1863-2082 (deltas, backward),
+// weight_update.cl:210-341 (weight-gradient GEMM over the staged SoA buffers).
+//
+// MI355X design
+//   * A 256-thread block (4 wavefronts) walks 64-sample tiles in a persistent
+//     loop.  Each wavefront owns 16 samples of the tile and runs every layer
+//     as 16x16x4 fp32 MFMAs with the samples as the N dimension
+//     (out[o][s] = W[o][:] . act[:][s]).
+//   * An MFMA result tile leaves lane (g, s) holding neurons 16t+4g+r of
+//     sample s.  The next layer consumes it unchanged: its K index is
+//     permuted so that k-step (t, r) takes neuron 16t+4g+r from lane group g
+//     and the weights are read with the same permutation.  Activations and
+//     deltas therefore never move between lanes.
+//   * Compositing needs the whole ray: sigma/rgb go to LDS, one barrier, and
+//     every wavefront runs the reference's scan trees on 64 lanes (one lane
+//     per sample, S lanes per ray) and picks its own samples' gradients.
+//   * Weight gradients dW = sum_s delta[o][s] act[i][s] are MFMAs with the
+//     samples as K: each 16x16 tile is transposed through a per-wave LDS
+//     scratch (4 ds_write_b32 + 1 ds_read_b128) and accumulated with
+//     ds_add_f32 into a per-block LDS copy of the gradient; each block writes
+//     one partial at the end (no staging buffers in HBM, unlike the
+//     reference's ~1.8 KB/sample SoA traffic).
+#include "ffn_device.h"
+#include "ffn_kernels.h"
+
+namespace ffn {
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Make LDS writes of this wavefront visible to its own later LDS reads and
+// keep the compiler from moving LDS accesses across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int LF_, int ND_, int NC_>
+struct Arch {
+  static constexpr int LF = LF_, ND = ND_, NC = NC_;
+  static constexpr int rows_pad(int k) { return k == FFN_WC_OUT ? 16 : layer_out(k); }
+  static constexpr int pitch(int k) { return layer_in(k, LF) + 1; }
+  static constexpr int wsz(int k) { return layer_active(k, ND, NC) ? rows_pad(k) * pitch(k) + rows_pad(k) : 0; }
+  static constexpr int w_off(int k) {
+    int o = 0;
+    for (int j = 0; j < k; ++j) o += wsz(j);
+    return o;
+  }
+  static constexpr int b_off(int k) { return w_off(k) + rows_pad(k) * pitch(k); }
+  static constexpr int w_total() { return w_off(FFN_N_LAYERS); }
+  static constexpr int gsz(int k) {
+    return layer_active(k, ND, NC) ? layer_out(k) * layer_in(k, LF) + layer_out(k) : 0;
+  }
+  static constexpr int g_off(int k) {
+    int o = 0;
+    for (int j = 0; j < k; ++j) o += gsz(j);
+    return o;
+  }
+  static constexpr int gb_off(int k) { return g_off(k) + layer_out(k) * layer_in(k, LF); }
+  static constexpr int g_total() { return g_off(FFN_N_LAYERS); }
+  static constexpr int XP = 20;  // transpose scratch pitch: 16 samples + 4 pad
+  static constexpr int x_per_wave = 64 * XP;
+  static constexpr int comp_floats = 2 * 256;  // double-buffered sigma[64] + rgb[64][3]
+  static constexpr int lds_floats() { return w_total() + g_total() + 4 * x_per_wave + comp_floats; }
+};
+
+// out tiles (D layout) = act(W . in + b), in given as D-layout tiles
+template <int OT, int IT>
+__device__ __forceinline__ void fwd_tiles(const float* __restrict__ W, const float* __restrict__ B, int P,
+                                          const floatx4 (&in)[IT], floatx4 (&out)[OT], int g, int s, bool relu) {
+#pragma unroll
+  for (int t = 0; t < OT; ++t) {
+    floatx4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
+    const float* wrow = W + (16 * t + s) * P + 4 * g;
+#pragma unroll
+    for (int tp = 0; tp < IT; ++tp)
+#pragma unroll
+      for (int rp = 0; rp < 4; ++rp) acc = mfma4(wrow[16 * tp + rp], in[tp][rp], acc);
+    if (relu) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
+    }
+    out[t] = acc;
+  }
+}
+
+// res tiles (D layout over input neurons, first RT tiles) = W^T . delta (+ init)
+template <int RT, int DT>
+__device__ __forceinline__ void bwd_tiles(const float* __restrict__ W, int P, const floatx4 (&delta)[DT],
+                                          floatx4 (&res)[RT], int g, int s) {
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    floatx4 acc = res[t];
+#pragma unroll
+    for (int tp = 0; tp < DT; ++tp)
+#pragma unroll
+      for (int rp = 0; rp < 4; ++rp) acc = mfma4(W[(16 * tp + 4 * g + rp) * P + 16 * t + s], delta[tp][rp], acc);
+    res[t] = acc;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void relu_mask(floatx4 (&d)[NT], const floatx4 (&act)[NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d[t][r] = act[t][r] > 0.0f ? d[t][r] : 0.0f;
+}
+
+template <int NT>
+__device__ __forceinline__ void stash_D(float* __restrict__ sx, const floatx4 (&v)[NT], int g, int s) {
+  constexpr int XP = 20;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sx[(16 * t + 4 * g + r) * XP + s] = v[t][r];
+}
+
+template <int NT>
+__device__ __forceinline__ void load_op(const float* __restrict__ sx, floatx4 (&op)[NT], int g, int m) {
+  constexpr int XP = 20;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) op[t] = *reinterpret_cast<const floatx4*>(sx + (16 * t + m) * XP + 4 * g);
+}
+
+// dW[o][i] += sum_s delta[o][s] act[i][s] and db[o] += sum_s delta[o][s] over the wave's 16 samples.
+// dop: delta operands (OT tiles), aop: activation operands (IT tiles), already transposed.
+template <int OT, int IT>
+__device__ __forceinline__ void accum_dW(float* __restrict__ gW, float* __restrict__ gB, int out_dim, int in_dim,
+                                         const floatx4 (&dop)[OT], const floatx4 (&aop)[IT], int g, int s) {
+#pragma unroll
+  for (int T = 0; T < OT; ++T) {
+    float bs = (dop[T][0] + dop[T][1]) + (dop[T][2] + dop[T][3]);
+    bs += __shfl_xor(bs, 16);
+    bs += __shfl_xor(bs, 32);
+    if (g == 0 && 16 * T + s < out_dim) atomicAdd(gB + 16 * T + s, bs);
+  }
+#pragma unroll
+  for (int T = 0; T < OT; ++T) {
+#pragma unroll
+    for (int Tp = 0; Tp < IT; ++Tp) {
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = mfma4(dop[T][q], aop[Tp][q], acc);
+      const int col = 16 * Tp + s;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * T + 4 * g + r;
+        if (row < out_dim && col < in_dim) atomicAdd(gW + row * in_dim + col, acc[r]);
+      }
+    }
+  }
+}
+
+template <int OT, int IT>
+__device__ __forceinline__ void layer_grad(float* __restrict__ sx, float* __restrict__ gW, float* __restrict__ gB,
+                                           int out_dim, int in_dim, const floatx4 (&delta)[OT],
+                                           const floatx4 (&act)[IT], int g, int s) {
+  floatx4 dop[OT], aop[IT];
+  stash_D(sx, delta, g, s);
+  wave_lds_sync();
+  load_op(sx, dop, g, s);
+  wave_lds_sync();
+  stash_D(sx, act, g, s);
+  wave_lds_sync();
+  load_op(sx, aop, g, s);
+  wave_lds_sync();
+  accum_dW(gW, gB, out_dim, in_dim, dop, aop, g, s);
+}
+
+template <int LF, int ND, int NC>
+__global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
+  using A = Arch<LF, ND, NC>;
+  constexpr int KA = LF / 4;  // a0 values per lane (k-steps of the first layer)
+  extern __shared__ float smem[];
+  float* sW = smem;
+  float* sG = smem + A::w_total();
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+  float* sX = sG + A::g_total() + wave * A::x_per_wave;
+  float* sC = smem + A::w_total() + A::g_total() + 4 * A::x_per_wave;
+  const bool train = a.do_train != 0;
+  const DevCfg& c = a.c;
+  const int S = a.S, log2S = a.log2S;
+  const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
+
+  // stage weights (zero-padded rows, pitch in+1) and clear the gradient accumulators
+#pragma unroll
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    if (!layer_active(k, ND, NC)) continue;
+    const int O = layer_out(k), I = layer_in(k, LF), R = A::rows_pad(k), P = A::pitch(k);
+    float* w = sW + A::w_off(k);
+    float* bb = sW + A::b_off(k);
+    const float* gw = a.w.W[k];
+    const float* gbias = a.w.b[k];
+    for (int e = tid; e < R * P; e += 256) {
+      const int r = e / P, col = e - r * P;
+      w[e] = (r < O && col < I) ? gw[r * I + col] : 0.0f;
+    }
+    for (int e = tid; e < R; e += 256) bb[e] = e < O ? gbias[e] : 0.0f;
+  }
+  if (train)
+    for (int e = tid; e < A::g_total(); e += 256) sG[e] = 0.0f;
+  __syncthreads();
+
+  float Dhalf;
+  {
+    const float dx = c.bmax[0] - c.bmin[0], dy = c.bmax[1] - c.bmin[1], dz = c.bmax[2] - c.bmin[2];
+    Dhalf = 0.5f * sqrtf(dx * dx + dy * dy + dz * dz);
+  }
+
+  int parity = 0;
+  for (int64_t tile = blockIdx.x; tile < a.n_tiles; tile += gridDim.x, parity ^= 1) {
+    float* sSig = sC + parity * 256;
+    float* sRgb = sSig + 64;
+    // ------------------------------------------------------------------
+    // forward: this lane's sample in the MLP layout
+    const int64_t b = tile * 64 + wave * 16 + s;
+    const bool valid = (uint64_t)b < n_samples;
+    const int64_t ray = valid ? (b >> log2S) : 0;
+    float a0r[KA];
+    if (valid) {
+      const floatx4* src = reinterpret_cast<const floatx4*>(a.a0 + b * LF + KA * g);
+#pragma unroll
+      for (int q = 0; q < KA / 4; ++q) {
+        floatx4 v = src[q];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a0r[4 * q + r] = v[r];
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < KA; ++q) a0r[q] = 0.0f;
+    }
+    float dirv[3];
+    {
+      const float4 rd = a.rays[2 * ray + 1];
+      dirv[0] = rd.x;
+      dirv[1] = rd.y;
+      dirv[2] = rd.z;
+    }
+    const float dt_b = valid ? a.DTs[b] : 0.0f;
+    const float t_b = valid ? a.Ts[b] : 0.0f;
+
+    floatx4 hd[ND][4];
+    {
+      const float* W = sW + A::w_off(FFN_WD_IN);
+      const float* B = sW + A::b_off(FFN_WD_IN);
+      constexpr int P = A::pitch(FFN_WD_IN);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        floatx4 acc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
+        const float* wrow = W + (16 * t + s) * P + KA * g;
+#pragma unroll
+        for (int kk = 0; kk < KA; ++kk) acc = mfma4(wrow[kk], a0r[kk], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
+        hd[0][t] = acc;
+      }
+    }
+    if constexpr (ND >= 2)
+      fwd_tiles<4, 4>(sW + A::w_off(FFN_WD_01), sW + A::b_off(FFN_WD_01), A::pitch(FFN_WD_01), hd[0], hd[1], g, s,
+                      true);
+    if constexpr (ND >= 3)
+      fwd_tiles<4, 4>(sW + A::w_off(FFN_WD_12), sW + A::b_off(FFN_WD_12), A::pitch(FFN_WD_12), hd[1], hd[2], g, s,
+                      true);
+    floatx4 acin[2];  // [dout(16) | SH*mult(16)] as two D-layout tiles
+    {
+      floatx4 o1[1];
+      fwd_tiles<1, 4>(sW + A::w_off(FFN_WD_OUT), sW + A::b_off(FFN_WD_OUT), A::pitch(FFN_WD_OUT), hd[ND - 1], o1, g,
+                      s, false);
+      acin[0] = o1[0];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acin[1][r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
+    }
+    floatx4 hc[NC][4];
+    fwd_tiles<4, 2>(sW + A::w_off(FFN_WC_IN), sW + A::b_off(FFN_WC_IN), A::pitch(FFN_WC_IN), acin, hc[0], g, s,
+                    true);
+    if constexpr (NC >= 2)
+      fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_01), sW + A::b_off(FFN_WC_01), A::pitch(FFN_WC_01), hc[0], hc[1], g, s,
+                      true);
+    if constexpr (NC >= 3)
+      fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_12), sW + A::b_off(FFN_WC_12), A::pitch(FFN_WC_12), hc[1], hc[2], g, s,
+                      true);
+    if constexpr (NC >= 4)
+      fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_23), sW + A::b_off(FFN_WC_23), A::pitch(FFN_WC_23), hc[2], hc[3], g, s,
+                      true);
+    float rgb_s[3];
+    {
+      floatx4 co[1];
+      fwd_tiles<1, 4>(sW + A::w_off(FFN_WC_OUT), sW + A::b_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), hc[NC - 1], co, g,
+                      s, false);
+      rgb_s[0] = sigmoid_soft(co[0][0]);
+      rgb_s[1] = sigmoid_soft(co[0][1]);
+      rgb_s[2] = sigmoid_soft(co[0][2]);
+    }
+    const float dout0 = acin[0][0];
+    if (g == 0) {
+      float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
+      if (dt_b <= 0.0f) sig = 0.0f;
+      sSig[wave * 16 + s] = sig;
+      sRgb[(wave * 16 + s) * 3 + 0] = rgb_s[0];
+      sRgb[(wave * 16 + s) * 3 + 1] = rgb_s[1];
+      sRgb[(wave * 16 + s) * 3 + 2] = rgb_s[2];
+    }
+    __syncthreads();
+
+    // ------------------------------------------------------------------
+    // compositing on 64 lanes: lane j = sample j of the tile (every wave)
+    float dLds_j, dLdc_j[3];
+    {
+      const int j = lane;
+      const int64_t bj = tile * 64 + j;
+      const bool vj = (uint64_t)bj < n_samples;
+      const int lid = j & (S - 1);
+      const int base = j - lid;
+      const int64_t rj = vj ? (bj >> log2S) : 0;
+      const float sig_j = sSig[j];
+      const float c0 = sRgb[3 * j], c1 = sRgb[3 * j + 1], c2 = sRgb[3 * j + 2];
+      const float dt_j = vj ? a.DTs[bj] : 0.0f;
+      float alpha = 0.0f;
+      if (dt_j > 0.0f) alpha = 1.0f - expf(fminf(fmaxf(-sig_j * dt_j, -5.0f), 18.0f));
+      const float oma = 1.0f - alpha;
+      Seg my;
+      my.a = oma;
+      my.v0 = alpha * c0;
+      my.v1 = alpha * c1;
+      my.v2 = alpha * c2;
+      Seg tot;
+      const Seg pre = seg_scan_excl_seg(my, lid, S, base, &tot);
+      const float Tr = pre.a, T_final = tot.a;
+      float bg[3] = {0.0f, 0.0f, 0.0f};
+      if (train) {
+        if (c.background == FFN_BG_WHITE) {
+          bg[0] = bg[1] = bg[2] = 1.0f;
+        } else if (c.background == FFN_BG_RANDOM) {
+          uint32_t rb = hash_u32(a.seed ^ (uint32_t)rj * 747796405u ^ 0xA511E9B3u);
+          bg[0] = rand01(rb);
+          bg[1] = rand01(rb);
+          bg[2] = rand01(rb);
+        }
+      }
+      float4 tg = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (vj && a.targets) tg = a.targets[rj];
+      const float Cf0 = tot.v0 + T_final * bg[0];
+      const float Cf1 = tot.v1 + T_final * bg[1];
+      const float Cf2 = tot.v2 + T_final * bg[2];
+      const float gr0 = charbonnier_prime(Cf0 - tg.x);
+      const float gr1 = charbonnier_prime(Cf1 - tg.y);
+      const float gr2 = charbonnier_prime(Cf2 - tg.z);
+      const float gT_end = gr0 * bg[0] + gr1 * bg[1] + gr2 * bg[2];
+      if (wave == 0 && lid == 0 && vj)
+        a.out_rgb[rj] = make_float4(fminf(fmaxf(Cf0, 0.0f), 1.0f), fminf(fmaxf(Cf1, 0.0f), 1.0f),
+                                    fminf(fmaxf(Cf2, 0.0f), 1.0f), train ? 4.0f : 0.0f);
+      const float ws = Tr * alpha;
+      dLdc_j[0] = ws * gr0;
+      dLdc_j[1] = ws * gr1;
+      dLdc_j[2] = ws * gr2;
+      Aff f;
+      f.a = oma;
+      f.b = gr0 * (alpha * c0) + gr1 * (alpha * c1) + gr2 * (alpha * c2);
+      const Aff f_rev = shfl_aff(f, base + (S - 1 - lid));  // lane k holds the element of sample S-1-k
+      const Aff scn = seg_scan_excl_aff_rev(f_rev, lid, S, base);
+      const int m = (lid <= S - 2) ? (S - 2 - lid) : 0;
+      const Aff sm = shfl_aff(scn, base + m);
+      const Aff em = shfl_aff(f_rev, base + m);
+      float gT_next = gT_end;
+      if (lid <= S - 2) {
+        const Aff incl = aff_combine_rev(sm, em);
+        gT_next = incl.a * gT_end + incl.b;
+      }
+      const float gA = gr0 * (Tr * c0) + gr1 * (Tr * c1) + gr2 * (Tr * c2);
+      const float gAlpha = gA - gT_next * Tr;
+      const float dads = (dt_j > 0.0f) ? (dt_j * oma) : 0.0f;
+      const float regu = (dt_j > 0.0f) ? (5e-3f * dt_j / (float)(uint32_t)S) : 0.0f;
+      dLds_j = gAlpha * dads + regu;
+
+      if (wave == 0) {
+        if (vj) {
+          if (a.t_sigma) a.t_sigma[bj] = sig_j;
+          if (a.t_rgb) {
+            a.t_rgb[3 * bj] = c0;
+            a.t_rgb[3 * bj + 1] = c1;
+            a.t_rgb[3 * bj + 2] = c2;
+          }
+          if (a.t_Tr) a.t_Tr[bj] = Tr;
+          if (a.t_dLds) a.t_dLds[bj] = dLds_j;
+          if (a.t_dLdc) {
+            a.t_dLdc[3 * bj] = dLdc_j[0];
+            a.t_dLdc[3 * bj + 1] = dLdc_j[1];
+            a.t_dLdc[3 * bj + 2] = dLdc_j[2];
+          }
+        }
+        // occupancy proposals for run-representative samples (ffnerf_OG.cl:1640-1821)
+        if (train && a.occ_strength > 0.0f) {
+          const float t_j = vj ? a.Ts[bj] : 0.0f;
+          uint64_t segmask = 0;
+          if (vj) segmask = (uint64_t)a.flags[2 * rj] | ((uint64_t)a.flags[2 * rj + 1] << 32);
+          const int nxt = find_next_flag(segmask, lid, S);
+          const int prev_end = lid > 0 ? lid - 1 : 0;
+          const int last = nxt < S ? nxt - 1 : S - 1;
+          const int nsrc = nxt < S ? nxt : lid;
+          const float t_prev = __shfl(t_j, base + prev_end), T_prev = __shfl(Tr, base + prev_end);
+          const float t_last = __shfl(t_j, base + last), T_last = __shfl(Tr, base + last);
+          const float t_nx = __shfl(t_j, base + nsrc), T_nx = __shfl(Tr, base + nsrc);
+          const bool is_rep = (segmask >> lid) & 1ull;
+          if (vj && is_rep && dt_j > 0.0f) {
+            const float4 ro = a.rays[2 * rj], rdv = a.rays[2 * rj + 1];
+            const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
+            const int G = c.G;
+            float gpos[3], cell_size[3];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+              const float bs = c.bmax[i] - c.bmin[i];
+              const float xi = o[i] + t_j * d[i];
+              gpos[i] = (xi - c.bmin[i]) * (1.0f / bs) * (float)G;
+              cell_size[i] = bs * (1.0f / (float)G);
+            }
+            const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
+            if ((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G) {
+              uint32_t sub = 0;
+#pragma unroll
+              for (int i = 0; i < 3; ++i) sub += ((gpos[i] - floorf(gpos[i])) >= 0.5f ? 1u : 0u) << i;
+              const int cell = ix + G * (iy + G * iz);
+              float pred = 0.0f;
+              {
+                const int ii[3] = {ix, iy, iz};
+                float cmin[3], cmax[3];
+#pragma unroll
+                for (int i = 0; i < 3; ++i) {
+                  cmin[i] = c.bmin[i] + (float)ii[i] * cell_size[i];
+                  cmax[i] = cmin[i] + cell_size[i];
+                }
+                float t_enter, t_exit;
+                if (ray_aabb(o, d, cmin, cmax, t_enter, t_exit)) {
+                  t_enter = fmaxf(t_enter, c.t_near);
+                  t_exit = fminf(t_exit, c.t_far);
+                  if (t_exit > t_enter) {
+                    const float denom0 = t_j - t_prev;
+                    float u0 = (fabsf(denom0) > 1.0e-8f) ? (t_enter - t_prev) / denom0 : 0.0f;
+                    u0 = fminf(fmaxf(u0, 0.0f), 1.0f);
+                    const float T_enter = T_prev + (Tr - T_prev) * u0;
+                    const float t_next = (nxt < S) ? t_nx : t_exit;
+                    const float T_next = (nxt < S) ? T_nx : T_final;
+                    const float denom1 = t_next - t_last;
+                    float u1 = (fabsf(denom1) > 1.0e-8f) ? (t_exit - t_last) / denom1 : 1.0f;
+                    u1 = fminf(fmaxf(u1, 0.0f), 1.0f);
+                    const float T_exit = T_last + (T_next - T_last) * u1;
+                    pred = fminf(1.0f, fmaxf(0.0f, (T_enter - T_exit) / fmaxf(T_enter, 1.0e-12f)));
+                  }
+                }
+              }
+              const uint32_t old_q = ((a.occ_in[cell] >> (4u * sub)) & 0xFu) + 1u;
+              uint32_t proposed_q = old_q;
+              const float pred16 = pred * 16.0f;
+              const uint32_t hseed = hash_u32(a.seed ^ (uint32_t)rj * 747796405u ^ (uint32_t)lid * 2891336453u ^
+                                              (uint32_t)cell * 9781u ^ sub * 6271u);
+              if (pred16 > (float)old_q && old_q < 16u) {
+                const float f0 = floorf(pred16);
+                const float frac = pred16 - f0;
+                const uint32_t q0 = (uint32_t)f0;
+                const uint32_t thresh = (uint32_t)(frac * 16777216.0f);
+                uint32_t q_stoch = ((hseed & 0x00FFFFFFu) < thresh) ? (q0 + 1u) : q0;
+                proposed_q = q_stoch > 16u ? 16u : q_stoch;
+              }
+              const float lat = (c.bmax[0] - c.bmin[0]) * (1.0f / (float)G);
+              const float tl = t_j / fmaxf(lat, 1.0e-12f);
+              const float Dl = Dhalf / fmaxf(lat, 1.0e-12f);
+              const float num = tl * tl + tl + (1.0f / 3.0f);
+              const float den = Dl * Dl + Dl + (1.0f / 3.0f);
+              const float keep_p = fminf(num / fmaxf(den, 1.0e-12f), 1.0f);
+              bool keep = keep_p >= 1.0f;
+              if (!keep) {
+                uint32_t rk = hseed;
+                keep = rand01(rk) <= keep_p;
+              }
+              if (keep) occ_nibble_atomic_max(a.occ_st, cell, sub, proposed_q);
+            }
+          }
+        }
+      }
+    }
+    if (!train) continue;
+
+    // ------------------------------------------------------------------
+    // backward of this wave's 16 samples
+    const int src = wave * 16 + s;
+    const float dLds = __shfl(dLds_j, src);
+    const float dLdc0 = __shfl(dLdc_j[0], src), dLdc1 = __shfl(dLdc_j[1], src), dLdc2 = __shfl(dLdc_j[2], src);
+    floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
+    floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
+    if (g == 0 && valid) {
+      const float num = t_b * t_b + t_b * dt_b + (dt_b * dt_b / 3.0f);
+      const float den = Dhalf * Dhalf + Dhalf * dt_b + (dt_b * dt_b / 3.0f);
+      const float xg = t_b / fmaxf(Dhalf, 1.0e-12f);
+      const float sg = (xg >= 1.0f) ? 0.0f : 1.0f;
+      const float gate = (1.0f - sg) * 1.0f + sg * powf(fmaxf(xg, 1.0e-12f), 0.2f);
+      const float f_vol = gate * num / fmaxf(den, 1.0e-12f);
+      dco[0][0] = (f_vol * dLdc0) * ((rgb_s[0] * (1.0f - rgb_s[0])) * 0.5f);
+      dco[0][1] = (f_vol * dLdc1) * ((rgb_s[1] * (1.0f - rgb_s[1])) * 0.5f);
+      dco[0][2] = (f_vol * dLdc2) * ((rgb_s[2] * (1.0f - rgb_s[2])) * 0.5f);
+      ddo[0][0] = 1.0f * (f_vol * dLds) * softplus_prime_from_pre(fminf(fmaxf(dout0, -18.0f), 18.0f));
+    }
+    // color backward
+    floatx4 dc[NC][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dc[NC - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    bwd_tiles<4, 1>(sW + A::w_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), dco, dc[NC - 1], g, s);
+    relu_mask(dc[NC - 1], hc[NC - 1]);
+    layer_grad<1, 4>(sX, sG + A::g_off(FFN_WC_OUT), sG + A::gb_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, dco, hc[NC - 1],
+                     g, s);
+    if constexpr (NC >= 4) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dc[2][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_23), A::pitch(FFN_WC_23), dc[3], dc[2], g, s);
+      relu_mask(dc[2], hc[2]);
+      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_23), sG + A::gb_off(FFN_WC_23), FFN_M, FFN_M, dc[3], hc[2], g, s);
+    }
+    if constexpr (NC >= 3) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dc[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_12), A::pitch(FFN_WC_12), dc[2], dc[1], g, s);
+      relu_mask(dc[1], hc[1]);
+      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_12), sG + A::gb_off(FFN_WC_12), FFN_M, FFN_M, dc[2], hc[1], g, s);
+    }
+    if constexpr (NC >= 2) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dc[0][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_01), A::pitch(FFN_WC_01), dc[1], dc[0], g, s);
+      relu_mask(dc[0], hc[0]);
+      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_01), sG + A::gb_off(FFN_WC_01), FFN_M, FFN_M, dc[1], hc[0], g, s);
+    }
+    // color input layer: its gradient, and the dout part of its input delta
+    layer_grad<4, 2>(sX, sG + A::g_off(FFN_WC_IN), sG + A::gb_off(FFN_WC_IN), FFN_M, FFN_C_IN, dc[0], acin, g, s);
+    bwd_tiles<1, 4>(sW + A::w_off(FFN_WC_IN), A::pitch(FFN_WC_IN), dc[0], ddo, g, s);
+    // density backward
+    floatx4 dd[ND][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dd[ND - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    bwd_tiles<4, 1>(sW + A::w_off(FFN_WD_OUT), A::pitch(FFN_WD_OUT), ddo, dd[ND - 1], g, s);
+    relu_mask(dd[ND - 1], hd[ND - 1]);
+    layer_grad<1, 4>(sX, sG + A::g_off(FFN_WD_OUT), sG + A::gb_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, ddo, hd[ND - 1],
+                     g, s);
+    if constexpr (ND >= 3) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dd[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<4, 4>(sW + A::w_off(FFN_WD_12), A::pitch(FFN_WD_12), dd[2], dd[1], g, s);
+      relu_mask(dd[1], hd[1]);
+      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_12), sG + A::gb_off(FFN_WD_12), FFN_M, FFN_M, dd[2], hd[1], g, s);
+    }
+    if constexpr (ND >= 2) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dd[0][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<4, 4>(sW + A::w_off(FFN_WD_01), A::pitch(FFN_WD_01), dd[1], dd[0], g, s);
+      relu_mask(dd[0], hd[0]);
+      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_01), sG + A::gb_off(FFN_WD_01), FFN_M, FFN_M, dd[1], hd[0], g, s);
+    }
+    // encoding gradient dL/da0 = Wd_in^T . delta_d1 -> HBM for the hash scatter
+    {
+      floatx4 ga[LF / 16];
+#pragma unroll
+      for (int t = 0; t < LF / 16; ++t) ga[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<LF / 16, 4>(sW + A::w_off(FFN_WD_IN), A::pitch(FFN_WD_IN), dd[0], ga, g, s);
+      if (valid) {
+#pragma unroll
+        for (int t = 0; t < LF / 16; ++t)
+          *reinterpret_cast<floatx4*>(a.dL_da0 + b * LF + 16 * t + 4 * g) = ga[t];
+      }
+    }
+    // first-layer weight gradient: a0 is held with the permuted neuron order
+    {
+      floatx4 dop[4], aop[LF / 16];
+      stash_D(sX, dd[0], g, s);
+      wave_lds_sync();
+      load_op(sX, dop, g, s);
+      wave_lds_sync();
+#pragma unroll
+      for (int kk = 0; kk < KA; ++kk) sX[(KA * g + kk) * A::XP + s] = a0r[kk];
+      wave_lds_sync();
+      load_op(sX, aop, g, s);
+      wave_lds_sync();
+      accum_dW(sG + A::g_off(FFN_WD_IN), sG + A::gb_off(FFN_WD_IN), FFN_M, LF, dop, aop, g, s);
+    }
+  }
+
+  if (train) {
+    __syncthreads();
+    float* dst = a.partials + (int64_t)blockIdx.x * A::g_total();
+    for (int e = tid; e < A::g_total(); e += 256) dst[e] = sG[e];
+  }
+}
+
+// ---------------------------------------------------------------------------
+
+template <int LF, int ND, int NC>
+static hipError_t launch_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
+  using A = Arch<LF, ND, NC>;
+  const size_t lds = sizeof(float) * (size_t)A::lds_floats();
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_mlp<LF, ND, NC>), dim3(n_blocks), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+#define FFN_MLP_CONFIGS(X) \
+  X(16, 1, 2)              \
+  X(32, 1, 2)              \
+  X(64, 1, 2)              \
+  X(16, 2, 2)              \
+  X(32, 2, 2)              \
+  X(64, 2, 2)
+
+bool mlp_supported(int LF, int nd, int nc) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return true;
+  FFN_MLP_CONFIGS(X)
+#undef X
+  return false;
+}
+
+size_t mlp_lds_bytes(int LF, int nd, int nc) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return sizeof(float) * (size_t)Arch<l, d, n>::lds_floats();
+  FFN_MLP_CONFIGS(X)
+#undef X
+  return 0;
+}
+
+hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return launch_t<l, d, n>(a, n_blocks, st);
+  FFN_MLP_CONFIGS(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ffn

@@ -1,0 +1,163 @@
+// ffn_optim.hip -- Adam (weight_update.cl:177-201), the MLP gradient
+// reduction that replaces the reference's staging GEMM (weight_update.cl:
+// 210-341), and the occupancy decay/merge (decay_occ_grid_in-st.cl:13-113).
+#include "ffn_device.h"
+#include "ffn_kernels.h"
+
+namespace ffn {
+
+__device__ __forceinline__ void adam1(float& p, float& m, float& v, float g, float lr_t, float b1, float b2,
+                                      float eps) {
+  float mi = fmaf(1.0f - b1, g, b1 * m);
+  float vi = fmaf(1.0f - b2, g * g, b2 * v);
+  float denom = sqrtf(vi) + eps;
+  p = p - lr_t * (mi / denom);
+  m = mi;
+  v = vi;
+}
+
+// Elementwise Adam, float4-wide where the buffers allow it.  28 B of HBM
+// traffic per parameter (+4 B when the gradient is cleared in the same pass).
+__global__ __launch_bounds__(256) void k_adam4(float4* __restrict__ p, float4* __restrict__ m,
+                                               float4* __restrict__ v, float4* __restrict__ g, int64_t n4,
+                                               float lr_t, float b1, float b2, float eps, int zero_grad) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+    float4 pp = p[i], mm = m[i], vv = v[i], gg = g[i];
+    adam1(pp.x, mm.x, vv.x, gg.x, lr_t, b1, b2, eps);
+    adam1(pp.y, mm.y, vv.y, gg.y, lr_t, b1, b2, eps);
+    adam1(pp.z, mm.z, vv.z, gg.z, lr_t, b1, b2, eps);
+    adam1(pp.w, mm.w, vv.w, gg.w, lr_t, b1, b2, eps);
+    p[i] = pp;
+    m[i] = mm;
+    v[i] = vv;
+    if (zero_grad) g[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_adam1(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
+                                               float* __restrict__ g, int64_t n0, int64_t n, float lr_t, float b1,
+                                               float b2, float eps, int zero_grad) {
+  const int64_t i = n0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float pp = p[i], mm = m[i], vv = v[i];
+  adam1(pp, mm, vv, g[i], lr_t, b1, b2, eps);
+  p[i] = pp;
+  m[i] = mm;
+  v[i] = vv;
+  if (zero_grad) g[i] = 0.0f;
+}
+
+hipError_t launch_adam(float* p, float* m, float* v, float* g, int64_t n, float lr_t, float b1, float b2, float eps,
+                       int zero_grad, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const bool aligned = (((uintptr_t)p | (uintptr_t)m | (uintptr_t)v | (uintptr_t)g) & 15) == 0;
+  int64_t n4 = aligned ? n / 4 : 0;
+  if (n4 > 0) {
+    int64_t blocks = (n4 + 255) / 256;
+    if (blocks > 256 * 64) blocks = 256 * 64;
+    hipLaunchKernelGGL(k_adam4, dim3((unsigned)blocks), dim3(256), 0, st, (float4*)p, (float4*)m, (float4*)v,
+                       (float4*)g, n4, lr_t, b1, b2, eps, zero_grad);
+  }
+  const int64_t rest = n - 4 * n4;
+  if (rest > 0)
+    hipLaunchKernelGGL(k_adam1, dim3((unsigned)((rest + 255) / 256)), dim3(256), 0, st, p, m, v, g, 4 * n4, n, lr_t,
+                       b1, b2, eps, zero_grad);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_fill(float* __restrict__ p, int64_t n, float val) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = val;
+}
+
+hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 256 * 64) blocks = 256 * 64;
+  hipLaunchKernelGGL(k_fill, dim3((unsigned)blocks), dim3(256), 0, st, p, n, v);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// occupancy decay/merge: one thread per 32-bit word of 8 nibbles
+
+__global__ __launch_bounds__(256) void k_occ_decay(uint32_t* __restrict__ occ_in, uint32_t* __restrict__ occ_st,
+                                                   uint32_t n_words, uint32_t decay_q24, uint32_t seed) {
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_words) return;
+  const uint32_t win = occ_in[gid], wst = occ_st[gid];
+  const uint32_t x = wst ^ win;
+  const bool same = (wst == win);
+  uint32_t out = wst;
+#pragma unroll
+  for (uint32_t s = 0; s < 8; ++s) {
+    const uint32_t shift = s * 4u;
+    if (!same && ((x >> shift) & 0xFu) != 0u) continue;  // raised by a proposal: keep
+    const uint32_t q = ((wst >> shift) & 0xFu) + 1u;
+    if (q <= 1u) continue;
+    const uint32_t qd24 = q * decay_q24;
+    uint32_t cand = (qd24 >> 24) + 1u;
+    const uint32_t thresh = 0x01000000u - (qd24 & 0x00FFFFFFu);
+    uint32_t hx = seed ^ (gid * 9781u) ^ (s * 6271u) ^ wst;
+    if (!same) hx ^= (win * 1597u);
+    const uint32_t r24 = hash_u32(hx) & 0x00FFFFFFu;
+    if (cand > 1u && r24 < thresh) cand -= 1u;
+    cand = cand < 1u ? 1u : (cand > 16u ? 16u : cand);
+    out = (out & ~(0xFu << shift)) | (((cand - 1u) & 0xFu) << shift);
+  }
+  occ_st[gid] = out;
+  occ_in[gid] = out;
+}
+
+hipError_t launch_occ_decay(uint32_t* occ_in, uint32_t* occ_st, uint32_t n_words, uint32_t decay_q24,
+                            uint32_t seed, hipStream_t st) {
+  if (n_words == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_occ_decay, dim3((n_words + 255) / 256), dim3(256), 0, st, occ_in, occ_st, n_words, decay_q24,
+                     seed);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// MLP: sum the per-block gradient partials (fixed block order, so the result
+// is deterministic) and apply Adam; color layers step at lr_t * color_rel_lr.
+
+__global__ __launch_bounds__(256) void k_mlp_adam(MlpOptArgs a) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.lay.total) return;
+  int k = -1, j = 0;
+  bool is_b = false;
+  for (int s = 0; s < FFN_N_LAYERS; ++s) {
+    if (!a.lay.active[s]) continue;
+    const int nw = a.lay.out[s] * a.lay.in[s];
+    if (i >= a.lay.w_off[s] && i < a.lay.w_off[s] + nw) {
+      k = s;
+      j = i - a.lay.w_off[s];
+    } else if (i >= a.lay.b_off[s] && i < a.lay.b_off[s] + a.lay.out[s]) {
+      k = s;
+      j = i - a.lay.b_off[s];
+      is_b = true;
+    }
+  }
+  if (k < 0) return;
+  float g = 0.0f;
+  const int stride = a.lay.total;
+  for (int blk = 0; blk < a.n_partials; ++blk) g += a.partials[(int64_t)blk * stride + i];
+  const float lr = (k >= FFN_WC_IN) ? a.lr_t * a.color_rel_lr : a.lr_t;
+  float* P = is_b ? a.b[k] : a.W[k];
+  float* Mm = is_b ? a.mb[k] : a.mW[k];
+  float* V = is_b ? a.vb[k] : a.vW[k];
+  float* tap = is_b ? a.gb[k] : a.gW[k];
+  if (tap) tap[j] = g;
+  float pp = P[j], mm = Mm[j], vv = V[j];
+  adam1(pp, mm, vv, g, lr, a.beta1, a.beta2, a.eps);
+  P[j] = pp;
+  Mm[j] = mm;
+  V[j] = vv;
+}
+
+hipError_t launch_mlp_adam(const MlpOptArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_mlp_adam, dim3((a.lay.total + 255) / 256), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace ffn

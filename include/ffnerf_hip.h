@@ -1,0 +1,160 @@
+/*
+ * ffnerf_hip.h -- C ABI of libffnerf_hip.so, the MI355X (gfx950) implementation
+ * of the ffnerf fused NeRF training step.
+ *
+ * Plain C: no C++ or torch types cross this boundary.  Every buffer argument is
+ * a caller-owned device pointer (hipMalloc / torch-ROCm storage); sizes are
+ * passed explicitly; every call enqueues on the caller's hipStream_t (passed as
+ * void*, NULL = default stream) and returns immediately.  Return value: 0 on
+ * success, < 0 on failure with a message in ffn_last_error() (thread-local).
+ * Unlike the reference kernels, nothing fails silently: a bad shape or an
+ * unsupported configuration is an error.
+ *
+ * What each entry point replaces in the reference (/root/reference):
+ *   ffn_create / ffn_bind_params   Nerf.from_kernels + Nerf.setup_buffers
+ *                                  (ffnerf_tools.py:583-671, 926-977): program
+ *                                  build options become a config struct,
+ *                                  parameter buffers are bound, scratch sized.
+ *   ffn_train_step                 the kernel pair enqueued by Nerf.step
+ *                                  (ffnerf_tools.py:1439-1445 and 1479-1519):
+ *                                  ffnerf_train_step (ffnerf_OG.cl:838-922) +
+ *                                  update_ffnerf_oneWG (weight_update.cl:346-454),
+ *                                  fused, without the SoA staging buffers.
+ *   ffn_occ_decay                  occ_nibble_decay_write_both_q24
+ *                                  (decay_occ_grid_in-st.cl:13-19), same
+ *                                  arguments; launched by Nerf.step at
+ *                                  ffnerf_tools.py:1452-1476.
+ *   ffn_sample / ffn_hash_encode_fwd / ffn_hash_encode_bwd / ffn_adam
+ *                                  stage entry points of the same path
+ *                                  (ffnerf_OG.cl:1002-1250, 1286-1364,
+ *                                  2090-2173; weight_update.cl:177-201) for
+ *                                  parity tests and micro-benchmarks.
+ */
+#ifndef FFNERF_HIP_H
+#define FFNERF_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FFN_ABI_VERSION 1
+#define FFN_MAX_LEVELS 32
+
+/* layer slots (reference kernel-argument order, ffnerf_tools.py:1210-1232) */
+enum {
+  FFN_WD_IN = 0, FFN_WD_01, FFN_WD_12, FFN_WD_OUT,
+  FFN_WC_IN, FFN_WC_01, FFN_WC_12, FFN_WC_23, FFN_WC_OUT,
+  FFN_N_LAYERS
+};
+
+enum { FFN_BG_BLACK = 0, FFN_BG_WHITE = 1, FFN_BG_RANDOM = 2 };     /* -DBACKGROUND_COLOR */
+enum { FFN_HASH_SGD = 0, FFN_HASH_ADAM = 1 };                       /* table optimizer */
+enum { FFN_MLP_FP32 = 0, FFN_MLP_FP16 = 1 };                        /* MLP arithmetic */
+
+/* Build-time constants of the reference (ffnerf_OG.cl:16-81,161-200;
+ * ffnerf_tools.py:23-69; run_ffnerf_OG.py:1044-1057) as runtime values. */
+typedef struct ffn_config {
+  int32_t n_levels;                     /* L   (reference: 16) */
+  int32_t f_per_level;                  /* F   (reference: 4) */
+  uint32_t log2_T[FFN_MAX_LEVELS];      /* per-level table size (reference LEVEL_LOG2) */
+  int32_t res[FFN_MAX_LEVELS];          /* per-level resolution R_l, >= 2 */
+  float lvl_lr_scale[FFN_MAX_LEVELS];   /* 2^(-0.1 l): per-level SGD scale */
+  int32_t nd, nc;                       /* hidden layers: density 1..3, color 1..4 */
+  int32_t occ_G;                        /* occupancy words per axis (8 nibbles each) */
+  float box_min[3], box_max[3];
+  float rho_min, rho_max, dt_min, dt_max, t_near, t_far;
+  int32_t background;                   /* FFN_BG_* (training only; render is black) */
+  int32_t hash_opt;                     /* FFN_HASH_* */
+  int32_t mlp_precision;                /* FFN_MLP_* */
+  int32_t reserved[8];
+} ffn_config;
+
+/* Caller-owned device buffers of one model.  Weights are row-major
+ * [out][in] float32 (the reference stores the same floats as int32 bit
+ * patterns).  Inactive layers (depending on nd/nc) may be NULL. */
+typedef struct ffn_params {
+  float* W[FFN_N_LAYERS];
+  float* b[FFN_N_LAYERS];
+  float* mW[FFN_N_LAYERS];
+  float* vW[FFN_N_LAYERS];
+  float* mb[FFN_N_LAYERS];
+  float* vb[FFN_N_LAYERS];
+  float* table;                         /* [sum_l 2^log2_T[l]][F] */
+  float* m_table;                       /* Adam state, required for FFN_HASH_ADAM */
+  float* v_table;
+  uint32_t* occ_in;                     /* [G^3] 8 nibbles per word */
+  uint32_t* occ_st;                     /* [G^3] proposals (training) */
+} ffn_params;
+
+/* Per-step scalars (ffnerf_tools.py:1197-1275, 1479-1482). */
+typedef struct ffn_step_scalars {
+  float lr;             /* lr_f; the table SGD uses lr * lvl_lr_scale[l] * 0.5 */
+  float lr_t;           /* bias-corrected Adam step */
+  float color_rel_lr;   /* color-MLP multiplier of lr_t */
+  float sh_multiplier;
+  float occ_strength;   /* proposals only if > 0 and training */
+  float beta1, beta2, eps;
+  uint32_t rng_seed;
+  int32_t do_train;     /* 0: forward-only render (inference occupancy, black bg) */
+} ffn_step_scalars;
+
+/* Optional device taps of intermediate values (any pointer may be NULL).
+ * N = num_rays * samples_per_ray; LF = n_levels * f_per_level. */
+typedef struct ffn_taps {
+  float* Ts;            /* [N] sample t */
+  float* DTs;           /* [N] sample dt */
+  uint32_t* flags;      /* [num_rays][2] run-start bits */
+  float* a0;            /* [N][LF] encoding */
+  float* sigma;         /* [N] */
+  float* rgb;           /* [N][3] */
+  float* Tr;            /* [N] transmittance before each sample */
+  float* dL_dsigma;     /* [N] */
+  float* dL_dc;         /* [N][3] */
+  float* dL_da0;        /* [N][LF] */
+  float* gW[FFN_N_LAYERS];  /* summed weight gradients (before Adam) */
+  float* gb[FFN_N_LAYERS];
+  float* g_table;       /* table gradient (FFN_HASH_ADAM), before Adam */
+} ffn_taps;
+
+int ffn_version(void);
+const char* ffn_last_error(void);
+
+int ffn_create(const ffn_config* cfg, void** handle);
+int ffn_destroy(void* handle);
+int ffn_bind_params(void* handle, const ffn_params* params);
+
+/* One training step (do_train=1) or forward-only render (do_train=0).
+ * rays: [num_rays] {float4 o (w=1), float4 d (w=0)} (ffnerf_tools.py:170-172);
+ * targets, out_rgb: [num_rays] float4.  samples_per_ray: power of two <= 64. */
+int ffn_train_step(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
+                   uint32_t samples_per_ray, const ffn_step_scalars* scalars, const ffn_taps* taps,
+                   void* stream);
+
+/* Occupancy decay/merge: same arguments as the reference kernel. */
+int ffn_occ_decay(uint32_t* occ_grid_in, uint32_t* occ_grid_st, uint32_t n_words, uint32_t decay_q24,
+                  uint32_t iter_seed, void* stream);
+
+/* Sampler only: Ts/DTs [num_rays*spr], flags [num_rays][2]. */
+int ffn_sample(void* handle, const void* rays, uint32_t num_rays, uint32_t samples_per_ray, uint32_t rng_seed,
+               int32_t do_train, float* Ts, float* DTs, uint32_t* flags, void* stream);
+
+/* Hash-grid encoding of n points x [n][3] (world space) with the bound table:
+ * a0 [n][LF].  idx_out (optional) [n][L][8]: feature base index per corner. */
+int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint32_t* idx_out, void* stream);
+
+/* Scatter-add of the encoding gradient g [n][LF] of points x into grad
+ * (table-shaped, caller-zeroed).  Non-finite gradients are skipped. */
+int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n, float* grad, void* stream);
+
+/* Adam over n parameters (weight_update.cl:177-201 form).  If zero_grad,
+ * g is cleared after it is read. */
+int ffn_adam(float* p, float* m, float* v, float* g, int64_t n, float lr_t, float beta1, float beta2, float eps,
+             int32_t zero_grad, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFNERF_HIP_H */

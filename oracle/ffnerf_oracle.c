@@ -1,0 +1,1150 @@
+/*
+ * ffnerf_oracle.c -- CPU restatement of the reference fused NeRF training step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or the timed CPU baseline).  The product path (the HIP library) never calls
+ * anything in here.
+ *
+ * It restates, sequentially and in plain C, the semantics of
+ *   /root/reference/ffnerf_OG.cl            ffnerf_train_step        (:838-2174)
+ *   /root/reference/weight_update.cl        update_ffnerf_oneWG      (:346-577)
+ *   /root/reference/decay_occ_grid_in-st.cl occ_nibble_decay_write_both_q24 (:13-113)
+ * with every compile-time constant of the reference turned into a runtime
+ * parameter (levels, features, per-level table sizes, per-level resolutions,
+ * MLP depths, occupancy resolution, background, table optimizer).
+ *
+ * Floating-point rules (so the HIP path can be compared bit-for-bit where the
+ * north star demands it):
+ *   - built with -ffp-contract=off; every multiply and add rounds separately,
+ *     explicit fmaf only where the reference writes fma();
+ *   - work-group scans follow the reference's Blelloch trees operand for
+ *     operand, including the reference's down-sweep operand order
+ *     (new_right = combine(old_left, old_right), ffnerf_OG.cl:632-634,708-710,
+ *     730-732), which composes non-commutative operators out of order;
+ *   - powr(x, 1.3) of the sampler (ffnerf_OG.cl:665-671) is evaluated by a
+ *     deterministic double-precision exp(y*log(x)) built from + - * / only
+ *     (log: exponent split + atanh series; exp: Cody-Waite reduction by ln2 +
+ *     Taylor series), identical to the device implementation;
+ *   - other transcendentals use the C library (single precision).
+ *
+ * Where the reference's result depends on work-item interleaving (the Hogwild
+ * CAS scatter into the hash table, ffnerf_OG.cl:2090-2173), the oracle uses
+ * the synchronous interleaving: every forward read sees the table as it was
+ * at the start of the step; updates are applied afterwards in sample order.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORA_M 64
+#define ORA_D_OUT 16
+#define ORA_L_DIR 16
+#define ORA_C_IN 32
+#define ORA_C_OUT 3
+#define ORA_S_MAX 64
+#define ORA_MAX_LEVELS 32
+
+/* layer slots, in the reference's kernel-argument order (ffnerf_tools.py:1210-1232) */
+enum { L_WD_IN = 0, L_WD_01, L_WD_12, L_WD_OUT, L_WC_IN, L_WC_01, L_WC_12, L_WC_23, L_WC_OUT, L_COUNT };
+
+typedef struct {
+  int32_t n_levels;
+  int32_t f_per_level;
+  uint32_t log2_T[ORA_MAX_LEVELS];
+  uint32_t offset[ORA_MAX_LEVELS];   /* entry offset of each level in the concatenated table */
+  int32_t res[ORA_MAX_LEVELS];       /* per-level grid resolution R_l (host computed) */
+  float lvl_lr_scale[ORA_MAX_LEVELS];/* 2^(-0.1*l) of the reference SGD (ffnerf_OG.cl:2108) */
+  int32_t nd, nc;                    /* hidden layers of the density / color MLP */
+  int32_t occ_G;
+  float box_min[3], box_max[3];
+  float rho_min, rho_max, dt_min, dt_max, t_near, t_far;
+  int32_t background;                /* 0 black, 1 white, 2 random (train only) */
+  int32_t hash_opt;                  /* 0 reference SGD in the step, 1 Adam */
+} ora_cfg;
+
+typedef struct {
+  float lr;              /* lr_f: un-bias-corrected (used by the table SGD) */
+  float lr_t;            /* bias-corrected Adam step (ffnerf_tools.py:1479-1482) */
+  float color_rel_lr;
+  float sh_multiplier;
+  float occ_strength;
+  float beta1, beta2, eps;
+  uint32_t rng_seed;
+  int32_t do_train;
+} ora_scalars;
+
+typedef struct {
+  float* W[L_COUNT];
+  float* b[L_COUNT];
+  float* mW[L_COUNT];
+  float* vW[L_COUNT];
+  float* mb[L_COUNT];
+  float* vb[L_COUNT];
+  float* table;
+  float* m_table;        /* Adam state of the table (hash_opt == 1) */
+  float* v_table;
+  uint32_t* occ_in;
+  uint32_t* occ_st;
+} ora_params;
+
+/* optional intermediate taps; every pointer may be NULL */
+typedef struct {
+  float* Ts;          /* [N*S]        sample times */
+  float* DTs;         /* [N*S]        sample dt */
+  uint32_t* flags;    /* [N*2]        run-start bit flags */
+  float* a0;          /* [N*S*LF]     hash encoding */
+  float* sigma;       /* [N*S] */
+  float* rgb;         /* [N*S*3] */
+  float* Tr;          /* [N*S]        transmittance before each sample */
+  float* T_final;     /* [N] */
+  float* dL_dsigma;   /* [N*S] */
+  float* dL_dc;       /* [N*S*3] */
+  float* dL_da0;      /* [N*S*LF]     gradient of the encoding (gf of :2154-2156) */
+  float* gW[L_COUNT]; /* weight gradients (sum over samples), sized like W */
+  float* gb[L_COUNT];
+  float* g_table;     /* table gradient (hash_opt == 1), sized like table */
+} ora_debug;
+
+/* ------------------------------------------------------------------ */
+/* integer helpers (ffnerf_OG.cl:293-311, decay_occ_grid_in-st.cl:2-10) */
+
+uint32_t ora_hash_u32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+static float rand01(uint32_t* state) {
+  uint32_t x = *state;
+  x ^= x << 13;
+  x ^= x >> 17;
+  x ^= x << 5;
+  *state = x;
+  return (float)(x & 0x00FFFFFFu) * (1.0f / 16777216.0f);
+}
+
+float ora_rand01_first(uint32_t seed) { uint32_t s = seed; return rand01(&s); }
+uint32_t ora_xorshift32(uint32_t x) { x ^= x << 13; x ^= x >> 17; x ^= x << 5; return x; }
+
+/* ------------------------------------------------------------------ */
+/* deterministic powr for the sampler weights (ffnerf_OG.cl:665-671)   */
+
+static const double ORA_LN2_HI = 6.93147180369123816490e-01; /* 0x3fe62e42fee00000 */
+static const double ORA_LN2_LO = 1.90821492927058770002e-10; /* 0x3dea39ef35793c76 */
+
+double ora_det_log(double x) {
+  uint64_t bits;
+  memcpy(&bits, &x, 8);
+  int e = (int)((bits >> 52) & 0x7ff) - 1023;
+  bits = (bits & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL;
+  double m;
+  memcpy(&m, &bits, 8);
+  if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
+  double s = (m - 1.0) / (m + 1.0);
+  double s2 = s * s;
+  double p = 1.0 / 25.0;
+  p = p * s2 + 1.0 / 23.0;
+  p = p * s2 + 1.0 / 21.0;
+  p = p * s2 + 1.0 / 19.0;
+  p = p * s2 + 1.0 / 17.0;
+  p = p * s2 + 1.0 / 15.0;
+  p = p * s2 + 1.0 / 13.0;
+  p = p * s2 + 1.0 / 11.0;
+  p = p * s2 + 1.0 / 9.0;
+  p = p * s2 + 1.0 / 7.0;
+  p = p * s2 + 1.0 / 5.0;
+  p = p * s2 + 1.0 / 3.0;
+  p = p * s2 + 1.0;
+  double lnm = 2.0 * s * p;
+  double de = (double)e;
+  return de * ORA_LN2_HI + (de * ORA_LN2_LO + lnm);
+}
+
+double ora_det_exp(double z) {
+  double k = floor(z * 1.4426950408889634 + 0.5);
+  double r = (z - k * ORA_LN2_HI) - k * ORA_LN2_LO;
+  double p = 1.0 / 6227020800.0;        /* 1/13! */
+  p = p * r + 1.0 / 479001600.0;        /* 1/12! */
+  p = p * r + 1.0 / 39916800.0;
+  p = p * r + 1.0 / 3628800.0;
+  p = p * r + 1.0 / 362880.0;
+  p = p * r + 1.0 / 40320.0;
+  p = p * r + 1.0 / 5040.0;
+  p = p * r + 1.0 / 720.0;
+  p = p * r + 1.0 / 120.0;
+  p = p * r + 1.0 / 24.0;
+  p = p * r + 1.0 / 6.0;
+  p = p * r + 0.5;
+  p = p * r + 1.0;
+  p = p * r + 1.0;
+  int ki = (int)k;
+  if (ki < -1022) return 0.0;
+  if (ki > 1023) return INFINITY;
+  uint64_t b = (uint64_t)(ki + 1023) << 52;
+  double two_k;
+  memcpy(&two_k, &b, 8);
+  return p * two_k;
+}
+
+/* powr(x, y) for finite x > 0 */
+float ora_det_powr(float x, float y) {
+  return (float)ora_det_exp((double)y * ora_det_log((double)x));
+}
+
+static float safe_pow_pos(float x, float gamma) {
+  x = fmaxf(x, 0.0f);
+  if (x <= 0.0f) return 0.0f;
+  if (!(x < INFINITY)) return x;
+  return ora_det_powr(x, gamma);
+}
+
+/* ------------------------------------------------------------------ */
+/* ray / AABB (ffnerf_OG.cl:322-343)                                  */
+
+int ora_ray_aabb(const float o[3], const float d[3], const float bmin[3], const float bmax[3],
+                 float* t0, float* t1) {
+  float tmin3[3], tmax3[3];
+  for (int i = 0; i < 3; ++i) {
+    float invd = (d[i] != 0.0f) ? (1.0f / d[i]) : INFINITY;
+    float tb = (bmin[i] - o[i]) * invd;
+    float tt = (bmax[i] - o[i]) * invd;
+    tmin3[i] = fminf(tb, tt);
+    tmax3[i] = fmaxf(tb, tt);
+  }
+  float tmin = fmaxf(tmin3[0], fmaxf(tmin3[1], tmin3[2]));
+  float tmax = fminf(tmax3[0], fminf(tmax3[1], tmax3[2]));
+  if (tmax < tmin) return 0;
+  *t0 = tmin;
+  *t1 = tmax;
+  return 1;
+}
+
+/* ------------------------------------------------------------------ */
+/* work-group scans, restated sequentially phase by phase              */
+
+static void scan_excl_f(float* a, int n) { /* ffnerf_OG.cl:619-637 */
+  for (int stride = 1; stride < n; stride <<= 1)
+    for (int lid = 0; lid < n; ++lid) {
+      int idx = (lid + 1) * (stride << 1) - 1;
+      if (idx < n) a[idx] += a[idx - stride];
+    }
+  a[n - 1] = 0.0f;
+  for (int stride = n >> 1; stride >= 1; stride >>= 1) {
+    for (int lid = 0; lid < n; ++lid) {
+      int idx = (lid + 1) * (stride << 1) - 1;
+      if (idx < n) {
+        float t = a[idx - stride];
+        a[idx - stride] = a[idx];
+        a[idx] += t;
+      }
+    }
+    if (stride == 1) break;
+  }
+}
+
+static float reduce_sum_f(float* a, int n) { /* ffnerf_OG.cl:639-646 */
+  for (int stride = n >> 1; stride >= 1; stride >>= 1) {
+    for (int lid = 0; lid < stride; ++lid) a[lid] += a[lid + stride];
+    if (stride == 1) break;
+  }
+  return a[0];
+}
+
+static int lower_bound_cdf(const float* cdf, int n, float u) { /* ffnerf_OG.cl:648-656 */
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (cdf[mid] >= u) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
+}
+
+typedef struct { float a; float v[3]; } Seg;
+static Seg seg_combine(Seg L, Seg R) { /* ffnerf_OG.cl:683-684 */
+  Seg O;
+  O.a = L.a * R.a;
+  for (int c = 0; c < 3; ++c) O.v[c] = L.v[c] + L.a * R.v[c];
+  return O;
+}
+
+static void scan_excl_seg(Seg* s, int n, Seg* total) { /* ffnerf_OG.cl:691-713 */
+  for (int stride = 1; stride < n; stride <<= 1)
+    for (int lid = 0; lid < n; ++lid) {
+      int idx = (lid + 1) * (stride << 1) - 1;
+      if (idx < n) s[idx] = seg_combine(s[idx - stride], s[idx]);
+    }
+  *total = s[n - 1];
+  s[n - 1].a = 1.0f;
+  s[n - 1].v[0] = s[n - 1].v[1] = s[n - 1].v[2] = 0.0f;
+  for (int stride = n >> 1; stride >= 1; stride >>= 1) {
+    for (int lid = 0; lid < n; ++lid) {
+      int idx = (lid + 1) * (stride << 1) - 1;
+      if (idx < n) {
+        Seg t = s[idx - stride];
+        s[idx - stride] = s[idx];
+        s[idx] = seg_combine(t, s[idx]);
+      }
+    }
+    if (stride == 1) break;
+  }
+}
+
+typedef struct { float a; float b; } Aff;
+static Aff aff_combine_rev(Aff L, Aff R) { /* ffnerf_OG.cl:687-689 */
+  Aff O;
+  O.a = R.a * L.a;
+  O.b = R.a * L.b + R.b;
+  return O;
+}
+
+static void scan_excl_aff_rev(Aff* s, int n, Aff* total) { /* ffnerf_OG.cl:715-735 */
+  for (int stride = 1; stride < n; stride <<= 1)
+    for (int lid = 0; lid < n; ++lid) {
+      int idx = (lid + 1) * (stride << 1) - 1;
+      if (idx < n) s[idx] = aff_combine_rev(s[idx - stride], s[idx]);
+    }
+  *total = s[n - 1];
+  s[n - 1].a = 1.0f;
+  s[n - 1].b = 0.0f;
+  for (int stride = n >> 1; stride >= 1; stride >>= 1) {
+    for (int lid = 0; lid < n; ++lid) {
+      int idx = (lid + 1) * (stride << 1) - 1;
+      if (idx < n) {
+        Aff t = s[idx - stride];
+        s[idx - stride] = s[idx];
+        s[idx] = aff_combine_rev(t, s[idx]);
+      }
+    }
+    if (stride == 1) break;
+  }
+}
+
+/* exported for tests: the two composite scans on plain arrays */
+void ora_scan_excl_f(float* a, int n) { scan_excl_f(a, n); }
+float ora_reduce_sum_f(float* a, int n) { return reduce_sum_f(a, n); }
+void ora_scan_excl_aff_rev(float* a, float* b, int n, float* tot_a, float* tot_b) {
+  Aff s[ORA_S_MAX], t;
+  for (int i = 0; i < n; ++i) { s[i].a = a[i]; s[i].b = b[i]; }
+  scan_excl_aff_rev(s, n, &t);
+  for (int i = 0; i < n; ++i) { a[i] = s[i].a; b[i] = s[i].b; }
+  *tot_a = t.a;
+  *tot_b = t.b;
+}
+
+/* ------------------------------------------------------------------ */
+/* occupancy nibble helpers (ffnerf_OG.cl:446-512)                    */
+
+static uint32_t chg_get(const uint32_t* f, uint32_t idx) { return (f[idx >> 5] >> (idx & 31u)) & 1u; }
+
+static uint32_t chg_find_next(const uint32_t* f, uint32_t idx, uint32_t WG) {
+  uint32_t i = idx + 1u;
+  if (i >= WG) return WG;
+  uint32_t w = i >> 5, b = i & 31u;
+  uint32_t mask = f[w] & (~0u << b);
+  for (;;) {
+    if (mask) {
+      uint32_t off = (uint32_t)__builtin_ctz(mask);
+      uint32_t res = (w << 5) + off;
+      return (res < WG) ? res : WG;
+    }
+    w++;
+    if ((w << 5) >= WG) break;
+    mask = f[w];
+  }
+  return WG;
+}
+
+static void occ_nibble_max(uint32_t* grid, int cell, uint32_t sub, uint32_t proposed_q) {
+  uint32_t shift = 4u * sub;
+  uint32_t old_u = grid[cell];
+  uint32_t old_q = ((old_u >> shift) & 0xFu) + 1u;
+  if (proposed_q <= old_q) return;
+  grid[cell] = (old_u & ~(0xFu << shift)) | (((proposed_q - 1u) & 0xFu) << shift);
+}
+
+/* ------------------------------------------------------------------ */
+/* sampler: occupancy-weighted importance resampling (ffnerf_OG.cl:1002-1250) */
+
+void ora_sample_ray(const ora_cfg* c, const float* ray, uint32_t ray_id, int S, uint32_t seed,
+                    const uint32_t* occ_in, int do_train, float* Ts, float* DTs, uint32_t* flags) {
+  const float* o = ray;
+  const float* d = ray + 4;
+  const uint32_t WG = (uint32_t)S;
+  flags[0] = flags[1] = 0u;
+
+  float t0 = 0.0f, t1 = 0.0f;
+  int hit = ora_ray_aabb(o, d, c->box_min, c->box_max, &t0, &t1);
+  float t0_l = 0.0f, t1_l = 0.0f;
+  int hit_l = 0;
+  if (hit) {
+    t0 = fmaxf(t0, c->t_near);
+    t1 = fminf(t1, c->t_far);
+    if (t1 <= t0) {
+      hit_l = 0;
+    } else {
+      hit_l = 1;
+      t0_l = t0 + 1.0e-6f;
+      t1_l = t1;
+    }
+  }
+  float dtb = hit_l ? ((t1_l - t0_l) * (1.0f / (float)WG)) : 0.0f;
+  dtb = fminf(c->dt_max, fmaxf(c->dt_min, dtb));
+  const float dt_base = hit_l ? dtb : 0.0f;
+
+  if (!hit_l) {
+    for (uint32_t i = 0; i < WG; ++i) {
+      Ts[i] = 0.0f;
+      DTs[i] = 0.0f;
+      flags[i >> 5] |= 1u << (i & 31u);
+    }
+    return;
+  }
+  uint32_t rng0 = ora_hash_u32(seed ^ ray_id * 1597334677u);
+  const float u0 = rand01(&rng0) * (1.0f / (float)WG);
+
+  const int G = c->occ_G;
+  float box_size[3], inv_box[3];
+  for (int i = 0; i < 3; ++i) {
+    box_size[i] = c->box_max[i] - c->box_min[i];
+    inv_box[i] = 1.0f / box_size[i];
+  }
+
+  float cand_t[ORA_S_MAX], wp[ORA_S_MAX], act[ORA_S_MAX], buf[ORA_S_MAX];
+  for (uint32_t lid = 0; lid < WG; ++lid) {
+    uint32_t rng = ora_hash_u32(seed ^ ray_id * 747796405u ^ lid * 2891336453u);
+    float u = ((float)lid + rand01(&rng)) * (1.0f / (float)WG);
+    float tk = t0_l + (t1_l - t0_l) * u;
+    cand_t[lid] = tk;
+    float gm[3];
+    for (int i = 0; i < 3; ++i) {
+      float xk = o[i] + tk * d[i];
+      gm[i] = (xk - c->box_min[i]) * inv_box[i] * (float)G;
+    }
+    float occ = 0.0f;
+    if (gm[0] >= 0.0f && gm[0] < (float)G && gm[1] >= 0.0f && gm[1] < (float)G && gm[2] >= 0.0f &&
+        gm[2] < (float)G) {
+      int im[3];
+      uint32_t sub = 0;
+      for (int i = 0; i < 3; ++i) {
+        int v = (int)floorf(gm[i]);
+        im[i] = v < 0 ? 0 : (v > G - 1 ? G - 1 : v);
+        float f = gm[i] - floorf(gm[i]);
+        f = fminf(fmaxf(f, 0.0f), 1.0f - 1e-7f);
+        sub += (f > 0.5f ? 1u : 0u) << i;
+      }
+      int cell = im[0] + G * (im[1] + G * im[2]);
+      uint32_t occ4 = (occ_in[cell] >> (4u * sub)) & 0xFu;
+      uint32_t q_train = occ4 + 1u;
+      uint32_t q_infer = (occ4 > 2u) ? (occ4 - 2u) : 0u;
+      uint32_t q_eff = do_train ? q_train : q_infer;
+      occ = (float)q_eff * (1.0f / 16.0f);
+    }
+    float infer_f = do_train ? 0.0f : 1.0f;
+    float active = (occ > 0.0f) ? 1.0f : 0.0f;
+    float rho_base = c->rho_min + (c->rho_max - c->rho_min) * occ;
+    float rho = rho_base * (1.0f - infer_f + infer_f * active);
+    float w_raw = rho * dt_base;
+    wp[lid] = safe_pow_pos(w_raw, 1.3f);
+    act[lid] = active;
+  }
+
+  /* pref = exclusive scan of wp; Wtot; gtot (LAMBDA_FOCUS = 0 => exp(-0*pi) = 1); active count */
+  float pref[ORA_S_MAX];
+  memcpy(buf, wp, sizeof(float) * WG);
+  scan_excl_f(buf, (int)WG);
+  memcpy(pref, buf, sizeof(float) * WG);
+  memcpy(buf, wp, sizeof(float) * WG);
+  float Wtot = fmaxf(reduce_sum_f(buf, (int)WG), 1.0e-12f);
+  /* g = wp * exp(-LAMBDA_FOCUS * pref/Wtot); LAMBDA_FOCUS is 0 (ffnerf_OG.cl:57), so the gain is exactly 1 */
+  float g[ORA_S_MAX];
+  for (uint32_t lid = 0; lid < WG; ++lid) g[lid] = wp[lid];
+  (void)pref;
+  (void)Wtot;
+  memcpy(buf, g, sizeof(float) * WG);
+  float gtot = fmaxf(reduce_sum_f(buf, (int)WG), 1.0e-12f);
+  memcpy(buf, act, sizeof(float) * WG);
+  float active_count = reduce_sum_f(buf, (int)WG);
+  float any_active = (active_count > 0.5f) ? 1.0f : 0.0f;
+  float inv_active = 1.0f / fmaxf(active_count, 1.0f);
+
+  float p[ORA_S_MAX];
+  const float uniform_part = 0.3f;
+  for (uint32_t lid = 0; lid < WG; ++lid) {
+    float uta = act[lid] * inv_active;
+    float lo = 1.0f / (float)WG;
+    float uniform_term = lo + (uta - lo) * any_active; /* mix() */
+    float proposal_term = any_active * (g[lid] / gtot);
+    p[lid] = uniform_part * uniform_term + (1.0f - uniform_part) * proposal_term;
+  }
+  float cdf[ORA_S_MAX];
+  memcpy(buf, p, sizeof(float) * WG);
+  scan_excl_f(buf, (int)WG);
+  for (uint32_t lid = 0; lid < WG; ++lid) cdf[lid] = buf[lid] + p[lid];
+
+  uint32_t key[ORA_S_MAX];
+  for (uint32_t lid = 0; lid < WG; ++lid) {
+    float uk = u0 + (float)lid * (1.0f / (float)WG);
+    uk = fminf(uk, 0.99999994f);
+    int idx = lower_bound_cdf(cdf, (int)WG, uk);
+    float t_out = cand_t[idx];
+    Ts[lid] = t_out;
+    DTs[lid] = dt_base;
+    float go[3];
+    for (int i = 0; i < 3; ++i) {
+      float xo = o[i] + t_out * d[i];
+      go[i] = (xo - c->box_min[i]) * inv_box[i] * (float)G;
+    }
+    uint32_t k = 0xFFFFFFFEu;
+    int ix = (int)floorf(go[0]), iy = (int)floorf(go[1]), iz = (int)floorf(go[2]);
+    if ((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G) {
+      uint32_t sub = 0;
+      for (int i = 0; i < 3; ++i) {
+        float f = go[i] - floorf(go[i]);
+        f = fminf(fmaxf(f, 0.0f), 1.0f - 1e-7f);
+        sub += (f >= 0.5f ? 1u : 0u) << i;
+      }
+      int cell = ix + G * (iy + G * iz);
+      k = (((uint32_t)cell) << 3) | (sub & 7u);
+    }
+    key[lid] = k;
+  }
+  for (uint32_t lid = 0; lid < WG; ++lid)
+    if (lid == 0 || key[lid] != key[lid - 1]) flags[lid >> 5] |= 1u << (lid & 31u);
+}
+
+/* ------------------------------------------------------------------ */
+/* hash grid (ffnerf_OG.cl:1286-1364 fwd, :2090-2173 bwd)              */
+
+static void normalize_pos(const ora_cfg* c, const float x[3], float p[3]) {
+  for (int i = 0; i < 3; ++i) {
+    float bs = c->box_max[i] - c->box_min[i];
+    float v = (x[i] - c->box_min[i]) / bs;
+    p[i] = fminf(fmaxf(v, 0.0f), 1.0f - 1.0e-6f);
+  }
+}
+
+static void level_corners(const ora_cfg* c, int lvl, const float p[3], uint32_t feat[8], float w[8]) {
+  int R = c->res[lvl];
+  int i0[3];
+  float f[3];
+  for (int i = 0; i < 3; ++i) {
+    float u = p[i] * (float)R;
+    int v = (int)floorf(u);
+    v = v < 0 ? 0 : (v > R - 2 ? R - 2 : v);
+    i0[i] = v;
+    f[i] = u - (float)v;
+  }
+  const uint32_t mask = (1u << c->log2_T[lvl]) - 1u;
+  for (int cc = 0; cc < 8; ++cc) {
+    int dx = cc & 1, dy = (cc >> 1) & 1, dz = (cc >> 2) & 1;
+    float wx = dx ? f[0] : 1.0f - f[0];
+    float wy = dy ? f[1] : 1.0f - f[1];
+    float wz = dz ? f[2] : 1.0f - f[2];
+    w[cc] = wx * wy * wz;
+    uint32_t h = ora_hash_u32((uint32_t)(i0[0] + dx) * 73856093u ^ (uint32_t)(i0[1] + dy) * 19349663u ^
+                              (uint32_t)(i0[2] + dz) * 83492791u ^ (uint32_t)lvl * 2654435761u) & mask;
+    feat[cc] = (c->offset[lvl] + h) * (uint32_t)c->f_per_level;
+  }
+}
+
+/* encode n points x[n*3] -> a0[n*LF]; optionally the feature base index [n*L*8] and weights [n*L*8] */
+void ora_hash_encode(const ora_cfg* c, const float* table, const float* x, int64_t n, float* a0,
+                     uint32_t* idx_out, float* w_out) {
+  const int L = c->n_levels, F = c->f_per_level, LF = L * F;
+  for (int64_t s = 0; s < n; ++s) {
+    float p[3];
+    normalize_pos(c, x + 3 * s, p);
+    for (int l = 0; l < L; ++l) {
+      uint32_t feat[8];
+      float w[8];
+      level_corners(c, l, p, feat, w);
+      for (int f = 0; f < F; ++f) {
+        float acc = 0.0f;
+        for (int cc = 0; cc < 8; ++cc) acc += w[cc] * table[feat[cc] + (uint32_t)f];
+        a0[s * LF + l * F + f] = acc;
+      }
+      if (idx_out)
+        for (int cc = 0; cc < 8; ++cc) idx_out[(s * L + l) * 8 + cc] = feat[cc];
+      if (w_out)
+        for (int cc = 0; cc < 8; ++cc) w_out[(s * L + l) * 8 + cc] = w[cc];
+    }
+  }
+}
+
+/* scatter the encoding gradient g[n*LF] of points x into grad (plain sum, double accumulators) */
+void ora_hash_backward(const ora_cfg* c, const float* x, const float* g, int64_t n, double* grad) {
+  const int L = c->n_levels, F = c->f_per_level, LF = L * F;
+  for (int64_t s = 0; s < n; ++s) {
+    float p[3];
+    normalize_pos(c, x + 3 * s, p);
+    for (int l = 0; l < L; ++l) {
+      uint32_t feat[8];
+      float w[8];
+      level_corners(c, l, p, feat, w);
+      for (int f = 0; f < F; ++f) {
+        float gf = g[s * LF + l * F + f];
+        if (!isfinite(gf)) continue;
+        for (int cc = 0; cc < 8; ++cc) grad[feat[cc] + (uint32_t)f] += (double)(gf * w[cc]);
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* activations (ffnerf_OG.cl:214-253)                                 */
+
+static float softplus(float x) {
+  if (x > 20.0f) return x;
+  if (x < -20.0f) return expf(x);
+  return log1pf(expf(x));
+}
+static float softplus_prime_from_pre(float x) {
+  if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+  return expf(x) / (1.0f + expf(x));
+}
+static float sigmoid_soft(float x) {
+  x *= 0.5f;
+  x = fminf(fmaxf(x, -18.0f), 18.0f);
+  if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+  return expf(x) / (1.0f + expf(x));
+}
+static float charbonnier_prime(float x) {
+  const float e2 = 1.0e-3f * 1.0e-3f;
+  return x * (1.0f / sqrtf(x * x + e2));
+}
+
+void ora_sh_encode(const float d[3], float* sh) { /* ffnerf_OG.cl:572-602 */
+  float x = d[0], y = d[1], z = d[2];
+  sh[0] = 0.28209479177387814f;
+  sh[1] = 0.4886025119029199f * y;
+  sh[2] = 0.4886025119029199f * z;
+  sh[3] = 0.4886025119029199f * x;
+  sh[4] = 1.0925484305920792f * x * y;
+  sh[5] = 1.0925484305920792f * y * z;
+  sh[6] = 0.31539156525252005f * (3.0f * z * z - 1.0f);
+  sh[7] = 1.0925484305920792f * x * z;
+  sh[8] = 0.5462742152960396f * (x * x - y * y);
+  sh[9] = 0.5900435899266435f * y * (3.0f * x * x - y * y);
+  sh[10] = 2.890611442640554f * x * y * z;
+  sh[11] = 0.4570457994644658f * y * (5.0f * z * z - 1.0f);
+  sh[12] = 0.3731763325901154f * (5.0f * z * z * z - 3.0f * z);
+  sh[13] = 0.4570457994644658f * x * (5.0f * z * z - 1.0f);
+  sh[14] = 1.445305721320277f * z * (x * x - y * y);
+  sh[15] = 0.5900435899266435f * x * (x * x - 3.0f * y * y);
+}
+
+/* out[i] = act(b[i] + sum_j W[i*in + j] * in[j]), sequential from the bias (ffnerf_OG.cl:754-806) */
+static void fc(float* out, const float* in, int in_dim, int out_dim, const float* W, const float* b, int relu) {
+  for (int i = 0; i < out_dim; ++i) {
+    float sum = b ? b[i] : 0.0f;
+    for (int j = 0; j < in_dim; ++j) sum += W[i * in_dim + j] * in[j];
+    out[i] = relu ? (sum > 0.0f ? sum : 0.0f) : sum;
+  }
+}
+
+/* delta_in[j] = sum_i W[i*in_dim + j] * delta_out[i] (ffnerf_OG.cl:811-835) */
+static void fc_bwd(float* din, const float* dout, int out_dim, int in_dim, const float* W) {
+  for (int j = 0; j < in_dim; ++j) {
+    float s = 0.0f;
+    for (int i = 0; i < out_dim; ++i) s += W[i * in_dim + j] * dout[i];
+    din[j] = s;
+  }
+}
+
+/* per-sample MLP state */
+typedef struct {
+  float a0[ORA_M];          /* LF <= 64 */
+  float hd[3][ORA_M];       /* density hidden activations */
+  float acin[ORA_C_IN];     /* [dout(16), SH*mult(16)] */
+  float hc[4][ORA_M];       /* color hidden activations */
+  float sigma;
+  float rgb[3];
+} mlp_state;
+
+static void mlp_forward(const ora_cfg* c, const ora_params* P, const float* dir, float sh_mult, mlp_state* st) {
+  const int LF = c->n_levels * c->f_per_level;
+  const int nd = c->nd, nc = c->nc;
+  fc(st->hd[0], st->a0, LF, ORA_M, P->W[L_WD_IN], P->b[L_WD_IN], 1);
+  if (nd >= 2) fc(st->hd[1], st->hd[0], ORA_M, ORA_M, P->W[L_WD_01], P->b[L_WD_01], 1);
+  if (nd >= 3) fc(st->hd[2], st->hd[1], ORA_M, ORA_M, P->W[L_WD_12], P->b[L_WD_12], 1);
+  float dout[ORA_D_OUT];
+  fc(dout, st->hd[nd - 1], ORA_M, ORA_D_OUT, P->W[L_WD_OUT], P->b[L_WD_OUT], 0);
+  for (int i = 0; i < ORA_D_OUT; ++i) st->acin[i] = dout[i];
+  st->sigma = softplus(fminf(fmaxf(dout[0], -10.0f), 10.0f));
+  ora_sh_encode(dir, st->acin + ORA_D_OUT);
+  for (int i = 0; i < ORA_L_DIR; ++i) st->acin[ORA_D_OUT + i] *= sh_mult;
+  fc(st->hc[0], st->acin, ORA_C_IN, ORA_M, P->W[L_WC_IN], P->b[L_WC_IN], 1);
+  static const int slot[4] = {0, L_WC_01, L_WC_12, L_WC_23};
+  for (int k = 1; k < nc; ++k) fc(st->hc[k], st->hc[k - 1], ORA_M, ORA_M, P->W[slot[k]], P->b[slot[k]], 1);
+  float cout[ORA_C_OUT];
+  fc(cout, st->hc[nc - 1], ORA_M, ORA_C_OUT, P->W[L_WC_OUT], P->b[L_WC_OUT], 0);
+  for (int i = 0; i < 3; ++i) st->rgb[i] = sigmoid_soft(cout[i]);
+}
+
+/* exported: forward of one sample given its encoding (for MLP tests) */
+void ora_mlp_forward(const ora_cfg* c, const ora_params* P, const float* a0, const float* dir, float sh_mult,
+                     float* sigma, float* rgb, float* dout) {
+  mlp_state st;
+  const int LF = c->n_levels * c->f_per_level;
+  memcpy(st.a0, a0, sizeof(float) * LF);
+  mlp_forward(c, P, dir, sh_mult, &st);
+  *sigma = st.sigma;
+  for (int i = 0; i < 3; ++i) rgb[i] = st.rgb[i];
+  if (dout) memcpy(dout, st.acin, sizeof(float) * ORA_D_OUT);
+}
+
+static int dim_out(int slot, const ora_cfg* c, int* in_dim) {
+  const int LF = c->n_levels * c->f_per_level;
+  switch (slot) {
+    case L_WD_IN: *in_dim = LF; return ORA_M;
+    case L_WD_OUT: *in_dim = ORA_M; return ORA_D_OUT;
+    case L_WC_IN: *in_dim = ORA_C_IN; return ORA_M;
+    case L_WC_OUT: *in_dim = ORA_M; return ORA_C_OUT;
+    default: *in_dim = ORA_M; return ORA_M;
+  }
+}
+
+static int slot_active(int slot, const ora_cfg* c) {
+  switch (slot) {
+    case L_WD_01: return c->nd >= 2;
+    case L_WD_12: return c->nd >= 3;
+    case L_WC_01: return c->nc >= 2;
+    case L_WC_12: return c->nc >= 3;
+    case L_WC_23: return c->nc >= 4;
+    default: return 1;
+  }
+}
+
+int ora_layer_shape(const ora_cfg* c, int slot, int* out_dim, int* in_dim) {
+  if (!slot_active(slot, c)) { *out_dim = 0; *in_dim = 0; return 0; }
+  *out_dim = dim_out(slot, c, in_dim);
+  return 1;
+}
+
+/* ------------------------------------------------------------------ */
+/* occupancy proposals of one ray (ffnerf_OG.cl:1640-1821)            */
+
+void ora_occ_propose_ray(const ora_cfg* c, const float* ray, uint32_t ray_id, int S, uint32_t seed,
+                         const float* Ts, const float* DTs, const float* Tr, float T_final, const uint32_t* flags,
+                         const uint32_t* occ_in, uint32_t* occ_st) {
+  const float* o = ray;
+  const float* d = ray + 4;
+  const int G = c->occ_G;
+  const uint32_t WG = (uint32_t)S;
+  float box_size[3], inv_box[3], cell_size[3];
+  for (int i = 0; i < 3; ++i) {
+    box_size[i] = c->box_max[i] - c->box_min[i];
+    inv_box[i] = 1.0f / box_size[i];
+    cell_size[i] = box_size[i] * (1.0f / (float)G);
+  }
+  for (uint32_t lid = 0; lid < WG; ++lid) {
+    float dt_s = DTs[lid];
+    if (!(dt_s > 0.0f)) continue;
+    if (!chg_get(flags, lid)) continue;
+    float t = Ts[lid];
+    float x[3], gpos[3];
+    for (int i = 0; i < 3; ++i) {
+      x[i] = o[i] + t * d[i];
+      gpos[i] = (x[i] - c->box_min[i]) * inv_box[i] * (float)G;
+    }
+    int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
+    if (!((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G)) continue;
+    uint32_t sub = 0;
+    for (int i = 0; i < 3; ++i) {
+      float f = gpos[i] - floorf(gpos[i]);
+      sub += (f >= 0.5f ? 1u : 0u) << i;
+    }
+    int cell = ix + G * (iy + G * iz);
+    uint32_t next = chg_find_next(flags, lid, WG);
+
+    float pred = 0.0f;
+    {
+      float cmin[3], cmax[3];
+      int ii[3] = {ix, iy, iz};
+      for (int i = 0; i < 3; ++i) {
+        cmin[i] = c->box_min[i] + (float)ii[i] * cell_size[i];
+        cmax[i] = cmin[i] + cell_size[i];
+      }
+      float t_enter, t_exit;
+      if (ora_ray_aabb(o, d, cmin, cmax, &t_enter, &t_exit)) {
+        t_enter = fmaxf(t_enter, c->t_near);
+        t_exit = fminf(t_exit, c->t_far);
+        if (t_exit > t_enter) {
+          uint32_t prev_end = lid > 0 ? lid - 1 : 0;
+          float t_prev = Ts[prev_end], T_prev = Tr[prev_end];
+          float t_cur = Ts[lid], T_cur = Tr[lid];
+          float denom0 = t_cur - t_prev;
+          float u0 = (fabsf(denom0) > 1.0e-8f) ? (t_enter - t_prev) / denom0 : 0.0f;
+          u0 = fminf(fmaxf(u0, 0.0f), 1.0f);
+          float T_enter = T_prev + (T_cur - T_prev) * u0;
+          uint32_t last = (next < WG) ? (next - 1u) : (WG - 1u);
+          float t_last = Ts[last], T_last = Tr[last];
+          float t_next = (next < WG) ? Ts[next] : t_exit;
+          float T_next = (next < WG) ? Tr[next] : T_final;
+          float denom1 = t_next - t_last;
+          float u1 = (fabsf(denom1) > 1.0e-8f) ? (t_exit - t_last) / denom1 : 1.0f;
+          u1 = fminf(fmaxf(u1, 0.0f), 1.0f);
+          float T_exit = T_last + (T_next - T_last) * u1;
+          float pv = (T_enter - T_exit) / fmaxf(T_enter, 1.0e-12f);
+          pred = fminf(1.0f, fmaxf(0.0f, pv));
+        }
+      }
+    }
+    uint32_t old_q = ((occ_in[cell] >> (4u * sub)) & 0xFu) + 1u;
+    uint32_t proposed_q = old_q;
+    float pred16 = pred * 16.0f;
+    uint32_t hseed = ora_hash_u32(seed ^ ray_id * 747796405u ^ lid * 2891336453u ^ (uint32_t)cell * 9781u ^
+                                  sub * 6271u);
+    if (pred16 > (float)old_q && old_q < 16u) {
+      float f0 = floorf(pred16);
+      float frac = pred16 - f0;
+      uint32_t q0 = (uint32_t)f0;
+      uint32_t r24 = hseed & 0x00FFFFFFu;
+      uint32_t thresh = (uint32_t)(frac * 16777216.0f);
+      uint32_t q_stoch = (r24 < thresh) ? (q0 + 1u) : q0;
+      if (q_stoch > 16u) q_stoch = 16u;
+      proposed_q = q_stoch;
+    }
+    float lat = (c->box_max[0] - c->box_min[0]) * (1.0f / (float)G);
+    float dd[3] = {c->box_max[0] - c->box_min[0], c->box_max[1] - c->box_min[1], c->box_max[2] - c->box_min[2]};
+    float D = 0.5f * sqrtf(dd[0] * dd[0] + dd[1] * dd[1] + dd[2] * dd[2]);
+    float tl = t / fmaxf(lat, 1.0e-12f);
+    float Dl = D / fmaxf(lat, 1.0e-12f);
+    float num = tl * tl + tl + (1.0f / 3.0f);
+    float den = Dl * Dl + Dl + (1.0f / 3.0f);
+    float f_keep = num / fmaxf(den, 1.0e-12f);
+    float keep_p = fminf(f_keep, 1.0f);
+    if (keep_p >= 1.0f) {
+      occ_nibble_max(occ_st, cell, sub, proposed_q);
+    } else {
+      uint32_t rk = hseed;
+      if (rand01(&rk) <= keep_p) occ_nibble_max(occ_st, cell, sub, proposed_q);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* compositing, loss gradient and its backward of one ray (ffnerf_OG.cl:1505-1634) */
+
+void ora_composite_ray(const ora_cfg* c, uint32_t ray_id, int S, uint32_t seed, int do_train,
+                       const float* sigma, const float* rgb, const float* DTs, const float* target, float* out4,
+                       float* Tr, float* T_final_out, float* dL_dc, float* dL_dsigma) {
+  const uint32_t WG = (uint32_t)S;
+  Seg segs[ORA_S_MAX], total;
+  float alpha[ORA_S_MAX];
+  for (uint32_t lid = 0; lid < WG; ++lid) {
+    float dt_s = DTs[lid];
+    float sg = (dt_s <= 0.0f) ? 0.0f : sigma[lid];
+    float a = 0.0f;
+    if (dt_s > 0.0f) {
+      float xx = fminf(fmaxf(-sg * dt_s, -5.0f), 18.0f);
+      a = 1.0f - expf(xx);
+    }
+    alpha[lid] = a;
+    segs[lid].a = 1.0f - a;
+    for (int k = 0; k < 3; ++k) segs[lid].v[k] = a * rgb[3 * lid + k];
+  }
+  scan_excl_seg(segs, (int)WG, &total);
+  for (uint32_t lid = 0; lid < WG; ++lid) Tr[lid] = segs[lid].a;
+  float T_final = total.a;
+  *T_final_out = T_final;
+  float bg[3] = {0.0f, 0.0f, 0.0f};
+  if (do_train) {
+    if (c->background == 1) {
+      bg[0] = bg[1] = bg[2] = 1.0f;
+    } else if (c->background == 2) {
+      uint32_t r = ora_hash_u32(seed ^ ray_id * 747796405u ^ 0xA511E9B3u);
+      bg[0] = rand01(&r);
+      bg[1] = rand01(&r);
+      bg[2] = rand01(&r);
+    }
+  }
+  float gr[3];
+  for (int k = 0; k < 3; ++k) {
+    float Cf = total.v[k] + T_final * bg[k];
+    out4[k] = fminf(fmaxf(Cf, 0.0f), 1.0f);
+    gr[k] = charbonnier_prime(Cf - target[k]);
+  }
+  out4[3] = 0.0f;
+  float gT_end = gr[0] * bg[0] + gr[1] * bg[1] + gr[2] * bg[2];
+
+  Aff elem[ORA_S_MAX], scan[ORA_S_MAX], tot_aff;
+  for (uint32_t lid = 0; lid < WG; ++lid) {
+    float a = alpha[lid];
+    const float* cs = rgb + 3 * lid;
+    float B = gr[0] * (a * cs[0]) + gr[1] * (a * cs[1]) + gr[2] * (a * cs[2]);
+    uint32_t k = (WG - 1u) - lid;
+    elem[k].a = 1.0f - a;
+    elem[k].b = B;
+    float ws = Tr[lid] * a;
+    for (int q = 0; q < 3; ++q) dL_dc[3 * lid + q] = ws * gr[q];
+  }
+  memcpy(scan, elem, sizeof(Aff) * WG);
+  scan_excl_aff_rev(scan, (int)WG, &tot_aff);
+  for (uint32_t lid = 0; lid < WG; ++lid) {
+    uint32_t k = (WG - 1u) - lid;
+    float gT_next = gT_end;
+    if (k >= 1u) {
+      uint32_t m = k - 1u;
+      Aff incl = aff_combine_rev(scan[m], elem[m]);
+      gT_next = incl.a * gT_end + incl.b;
+    }
+    float a = alpha[lid];
+    float Ts_ = Tr[lid];
+    const float* cs = rgb + 3 * lid;
+    float gA = gr[0] * (Ts_ * cs[0]) + gr[1] * (Ts_ * cs[1]) + gr[2] * (Ts_ * cs[2]);
+    float gAlpha = gA - gT_next * Ts_;
+    float dt_s = DTs[lid];
+    float dads = (dt_s > 0.0f) ? (dt_s * (1.0f - a)) : 0.0f;
+    float regu = (dt_s > 0.0f) ? (5e-3f * dt_s / (float)(uint32_t)S) : 0.0f;
+    dL_dsigma[lid] = gAlpha * dads + regu;
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* Adam, reference form (weight_update.cl:177-201)                    */
+
+void ora_adam(float* p, float* m, float* v, const float* g, int64_t n, float lr_t, float beta1, float beta2,
+              float eps) {
+  for (int64_t i = 0; i < n; ++i) {
+    float mi = fmaf(1.0f - beta1, g[i], beta1 * m[i]);
+    float vi = fmaf(1.0f - beta2, g[i] * g[i], beta2 * v[i]);
+    float denom = sqrtf(vi) + eps;
+    p[i] = p[i] - lr_t * (mi / denom);
+    m[i] = mi;
+    v[i] = vi;
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* occupancy decay/merge (decay_occ_grid_in-st.cl:13-113)            */
+
+void ora_occ_decay(uint32_t* occ_in, uint32_t* occ_st, uint32_t n_words, uint32_t decay_q24, uint32_t seed) {
+  for (uint32_t gid = 0; gid < n_words; ++gid) {
+    const uint32_t win = occ_in[gid], wst = occ_st[gid];
+    uint32_t out = wst;
+    const uint32_t x = wst ^ win;
+    for (uint32_t s = 0; s < 8; ++s) {
+      const uint32_t shift = s * 4u;
+      if (wst != win && ((x >> shift) & 0xFu) != 0u) continue;
+      const uint32_t q = ((wst >> shift) & 0xFu) + 1u;
+      if (q <= 1u) continue;
+      const uint32_t qd24 = q * decay_q24;
+      uint32_t cand = (qd24 >> 24) + 1u;
+      const uint32_t thresh = 0x01000000u - (qd24 & 0x00FFFFFFu);
+      uint32_t hx = seed ^ (gid * 9781u) ^ (s * 6271u) ^ wst;
+      if (wst != win) hx ^= (win * 1597u);
+      const uint32_t r24 = ora_hash_u32(hx) & 0x00FFFFFFu;
+      if (cand > 1u && r24 < thresh) cand -= 1u;
+      if (cand < 1u) cand = 1u;
+      if (cand > 16u) cand = 16u;
+      out = (out & ~(0xFu << shift)) | (((cand - 1u) & 0xFu) << shift);
+    }
+    occ_st[gid] = out;
+    occ_in[gid] = out;
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* the full step: sampler -> encode -> MLPs -> composite -> proposals  */
+/* -> deltas -> MLP backward -> table update -> weight grads -> Adam   */
+
+int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const float* targets, float* out_rgb,
+                   int32_t num_rays, int32_t S, const ora_scalars* sc, ora_debug* dbg) {
+  if (S <= 0 || S > ORA_S_MAX || (S & (S - 1)) != 0) return -1;
+  const int L = c->n_levels, F = c->f_per_level, LF = L * F;
+  if (LF > ORA_M || c->nd < 1 || c->nd > 3 || c->nc < 1 || c->nc > 4) return -2;
+  const int nd = c->nd, nc = c->nc;
+  const int do_train = sc->do_train != 0;
+  int64_t table_entries = 0;
+  for (int l = 0; l < L; ++l) {
+    int64_t e = (int64_t)c->offset[l] + ((int64_t)1 << c->log2_T[l]);
+    if (e > table_entries) table_entries = e;
+  }
+  const int64_t table_n = table_entries * F;
+
+  /* forward reads use the table as of the step start */
+  float* table_read = (float*)malloc(sizeof(float) * (size_t)table_n);
+  if (!table_read) return -3;
+  memcpy(table_read, P->table, sizeof(float) * (size_t)table_n);
+
+  double* gW[L_COUNT];
+  double* gb[L_COUNT];
+  int odim[L_COUNT], idim[L_COUNT];
+  for (int k = 0; k < L_COUNT; ++k) {
+    gW[k] = NULL;
+    gb[k] = NULL;
+    if (!ora_layer_shape(c, k, &odim[k], &idim[k])) continue;
+    gW[k] = (double*)calloc((size_t)odim[k] * idim[k], sizeof(double));
+    gb[k] = (double*)calloc((size_t)odim[k], sizeof(double));
+  }
+  double* gtab = (c->hash_opt == 1 && do_train) ? (double*)calloc((size_t)table_n, sizeof(double)) : NULL;
+
+  ora_params PR = *P;
+  PR.table = table_read;
+
+  mlp_state* st = (mlp_state*)malloc(sizeof(mlp_state) * (size_t)S);
+  const float D = 0.5f * sqrtf((c->box_max[0] - c->box_min[0]) * (c->box_max[0] - c->box_min[0]) +
+                               (c->box_max[1] - c->box_min[1]) * (c->box_max[1] - c->box_min[1]) +
+                               (c->box_max[2] - c->box_min[2]) * (c->box_max[2] - c->box_min[2]));
+  static const int cslot[4] = {L_WC_IN, L_WC_01, L_WC_12, L_WC_23};
+  static const int dslot[3] = {L_WD_IN, L_WD_01, L_WD_12};
+
+  for (int32_t r = 0; r < num_rays; ++r) {
+    const float* ray = rays + 8 * (int64_t)r;
+    float Ts[ORA_S_MAX], DTs[ORA_S_MAX], Tr[ORA_S_MAX], sig[ORA_S_MAX], rgb[3 * ORA_S_MAX];
+    float dLdc[3 * ORA_S_MAX], dLds[ORA_S_MAX], T_final;
+    uint32_t flags[2];
+    ora_sample_ray(c, ray, (uint32_t)r, S, sc->rng_seed, P->occ_in, do_train, Ts, DTs, flags);
+    for (int s = 0; s < S; ++s) {
+      float x[3];
+      for (int i = 0; i < 3; ++i) x[i] = ray[i] + Ts[s] * ray[4 + i];
+      ora_hash_encode(c, table_read, x, 1, st[s].a0, NULL, NULL);
+      mlp_forward(c, &PR, ray + 4, sc->sh_multiplier, &st[s]);
+      sig[s] = (DTs[s] <= 0.0f) ? 0.0f : st[s].sigma;
+      for (int k = 0; k < 3; ++k) rgb[3 * s + k] = st[s].rgb[k];
+    }
+    float* o4 = out_rgb + 4 * (int64_t)r;
+    ora_composite_ray(c, (uint32_t)r, S, sc->rng_seed, do_train, sig, rgb, DTs, targets + 4 * (int64_t)r, o4, Tr,
+                      &T_final, dLdc, dLds);
+    if (sc->occ_strength > 0.0f && do_train)
+      ora_occ_propose_ray(c, ray, (uint32_t)r, S, sc->rng_seed, Ts, DTs, Tr, T_final, flags, P->occ_in, P->occ_st);
+
+    if (dbg) {
+      int64_t b0 = (int64_t)r * S;
+      if (dbg->Ts) memcpy(dbg->Ts + b0, Ts, sizeof(float) * S);
+      if (dbg->DTs) memcpy(dbg->DTs + b0, DTs, sizeof(float) * S);
+      if (dbg->flags) { dbg->flags[2 * r] = flags[0]; dbg->flags[2 * r + 1] = flags[1]; }
+      if (dbg->sigma) memcpy(dbg->sigma + b0, sig, sizeof(float) * S);
+      if (dbg->rgb) memcpy(dbg->rgb + 3 * b0, rgb, sizeof(float) * 3 * S);
+      if (dbg->Tr) memcpy(dbg->Tr + b0, Tr, sizeof(float) * S);
+      if (dbg->T_final) dbg->T_final[r] = T_final;
+      if (dbg->dL_dsigma) memcpy(dbg->dL_dsigma + b0, dLds, sizeof(float) * S);
+      if (dbg->dL_dc) memcpy(dbg->dL_dc + 3 * b0, dLdc, sizeof(float) * 3 * S);
+      if (dbg->a0)
+        for (int s = 0; s < S; ++s) memcpy(dbg->a0 + (b0 + s) * LF, st[s].a0, sizeof(float) * LF);
+    }
+    if (!do_train) continue;
+    o4[3] += 4.0f; /* ffnerf_OG.cl:2091 */
+
+    for (int s = 0; s < S; ++s) {
+      mlp_state* m = &st[s];
+      const float t = Ts[s], dtl = DTs[s];
+      /* output deltas with the distance gate f_vol (ffnerf_OG.cl:1863-1891) */
+      float num = t * t + t * dtl + (dtl * dtl / 3.0f);
+      float den = D * D + D * dtl + (dtl * dtl / 3.0f);
+      float xg = t / fmaxf(D, 1.0e-12f);
+      float sg = (xg >= 1.0f) ? 0.0f : 1.0f;
+      float gate = (1.0f - sg) * 1.0f + sg * powf(fmaxf(xg, 1.0e-12f), 0.2f);
+      float f_vol = gate * num / fmaxf(den, 1.0e-12f);
+      float d_sigma = f_vol * dLds[s];
+      float dcout[ORA_C_OUT], ddout[ORA_D_OUT];
+      for (int k = 0; k < 3; ++k) {
+        float sk = m->rgb[k];
+        dcout[k] = (f_vol * dLdc[3 * s + k]) * ((sk * (1.0f - sk)) * 0.5f);
+      }
+      ddout[0] = 1.0f * d_sigma * softplus_prime_from_pre(fminf(fmaxf(m->acin[0], -18.0f), 18.0f));
+      for (int i = 1; i < ORA_D_OUT; ++i) ddout[i] = 0.0f;
+
+      /* color backward */
+      float dc[4][ORA_M];
+      fc_bwd(dc[nc - 1], dcout, ORA_C_OUT, ORA_M, P->W[L_WC_OUT]);
+      for (int j = 0; j < ORA_M; ++j) dc[nc - 1][j] = m->hc[nc - 1][j] > 0.0f ? dc[nc - 1][j] : 0.0f;
+      for (int k = nc - 1; k >= 1; --k) {
+        fc_bwd(dc[k - 1], dc[k], ORA_M, ORA_M, P->W[cslot[k]]);
+        for (int j = 0; j < ORA_M; ++j) dc[k - 1][j] = m->hc[k - 1][j] > 0.0f ? dc[k - 1][j] : 0.0f;
+      }
+      for (int i = 0; i < ORA_D_OUT; ++i) {
+        float sacc = 0.0f;
+        for (int j = 0; j < ORA_M; ++j) sacc += P->W[L_WC_IN][j * ORA_C_IN + i] * dc[0][j];
+        ddout[i] += sacc;
+      }
+      /* density backward */
+      float dd[3][ORA_M];
+      fc_bwd(dd[nd - 1], ddout, ORA_D_OUT, ORA_M, P->W[L_WD_OUT]);
+      for (int j = 0; j < ORA_M; ++j) dd[nd - 1][j] = m->hd[nd - 1][j] > 0.0f ? dd[nd - 1][j] : 0.0f;
+      for (int k = nd - 1; k >= 1; --k) {
+        fc_bwd(dd[k - 1], dd[k], ORA_M, ORA_M, P->W[dslot[k]]);
+        for (int j = 0; j < ORA_M; ++j) dd[k - 1][j] = m->hd[k - 1][j] > 0.0f ? dd[k - 1][j] : 0.0f;
+      }
+      /* weight gradients: dW[o][i] += delta[o] * act_in[i] (weight_update.cl:260-314) */
+#define ACC(slot, delta, act, od, id)                                                         \
+  do {                                                                                        \
+    for (int o_ = 0; o_ < (od); ++o_) {                                                       \
+      double dv = (double)(delta)[o_];                                                        \
+      gb[slot][o_] += dv;                                                                     \
+      for (int i_ = 0; i_ < (id); ++i_) gW[slot][o_ * (id) + i_] += dv * (double)(act)[i_]; \
+    }                                                                                         \
+  } while (0)
+      ACC(L_WC_OUT, dcout, m->hc[nc - 1], ORA_C_OUT, ORA_M);
+      for (int k = nc - 1; k >= 1; --k) ACC(cslot[k], dc[k], m->hc[k - 1], ORA_M, ORA_M);
+      ACC(L_WC_IN, dc[0], m->acin, ORA_M, ORA_C_IN);
+      ACC(L_WD_OUT, ddout, m->hd[nd - 1], ORA_D_OUT, ORA_M);
+      for (int k = nd - 1; k >= 1; --k) ACC(dslot[k], dd[k], m->hd[k - 1], ORA_M, ORA_M);
+      ACC(L_WD_IN, dd[0], m->a0, ORA_M, LF);
+#undef ACC
+      /* encoding gradient and table update (ffnerf_OG.cl:2090-2173) */
+      float gf[ORA_M];
+      for (int k = 0; k < LF; ++k) {
+        float sacc = 0.0f;
+        for (int j = 0; j < ORA_M; ++j) sacc += P->W[L_WD_IN][j * LF + k] * dd[0][j];
+        gf[k] = sacc;
+      }
+      if (dbg && dbg->dL_da0) memcpy(dbg->dL_da0 + ((int64_t)r * S + s) * LF, gf, sizeof(float) * LF);
+      float x[3], p[3];
+      for (int i = 0; i < 3; ++i) x[i] = ray[i] + Ts[s] * ray[4 + i];
+      normalize_pos(c, x, p);
+      for (int l = 0; l < L; ++l) {
+        uint32_t feat[8];
+        float w[8];
+        level_corners(c, l, p, feat, w);
+        float lr_lvl = sc->lr * c->lvl_lr_scale[l];
+        for (int f = 0; f < F; ++f) {
+          float g = gf[l * F + f];
+          if (!isfinite(g)) continue;
+          for (int cc = 0; cc < 8; ++cc) {
+            if (c->hash_opt == 1) gtab[feat[cc] + (uint32_t)f] += (double)(g * w[cc]);
+            else P->table[feat[cc] + (uint32_t)f] += -lr_lvl * 0.5f * g * w[cc];
+          }
+        }
+      }
+    }
+  }
+
+  if (do_train) {
+    /* MLP Adam; color layers at lr_t * color_rel_lr (weight_update.cl:487-573) */
+    for (int k = 0; k < L_COUNT; ++k) {
+      if (!gW[k]) continue;
+      int n = odim[k] * idim[k];
+      float* gwf = (float*)malloc(sizeof(float) * n);
+      float* gbf = (float*)malloc(sizeof(float) * odim[k]);
+      for (int i = 0; i < n; ++i) gwf[i] = (float)gW[k][i];
+      for (int i = 0; i < odim[k]; ++i) gbf[i] = (float)gb[k][i];
+      float lrk = (k >= L_WC_IN) ? sc->lr_t * sc->color_rel_lr : sc->lr_t;
+      if (dbg && dbg->gW[k]) memcpy(dbg->gW[k], gwf, sizeof(float) * n);
+      if (dbg && dbg->gb[k]) memcpy(dbg->gb[k], gbf, sizeof(float) * odim[k]);
+      ora_adam(P->W[k], P->mW[k], P->vW[k], gwf, n, lrk, sc->beta1, sc->beta2, sc->eps);
+      ora_adam(P->b[k], P->mb[k], P->vb[k], gbf, odim[k], lrk, sc->beta1, sc->beta2, sc->eps);
+      free(gwf);
+      free(gbf);
+    }
+    if (gtab) {
+      float* gtf = (float*)malloc(sizeof(float) * (size_t)table_n);
+      for (int64_t i = 0; i < table_n; ++i) gtf[i] = (float)gtab[i];
+      if (dbg && dbg->g_table) memcpy(dbg->g_table, gtf, sizeof(float) * (size_t)table_n);
+      ora_adam(P->table, P->m_table, P->v_table, gtf, table_n, sc->lr_t, sc->beta1, sc->beta2, sc->eps);
+      free(gtf);
+    }
+  }
+  for (int k = 0; k < L_COUNT; ++k) { free(gW[k]); free(gb[k]); }
+  free(gtab);
+  free(st);
+  free(table_read);
+  return 0;
+}

@@ -1,0 +1,121 @@
+"""Drive libffnerf_hip.so through its C ABI from the tests (torch tensors as
+device buffers), with the same spec/parameter dictionaries the oracle takes."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+import ffn_lib as fl
+
+DEV = "cuda"
+
+
+def to_dev(a: np.ndarray):
+    if a.dtype == np.uint32:
+        return torch.from_numpy(a.view(np.int32).copy()).to(DEV)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def to_np(t, dtype=None):
+    a = t.detach().cpu().numpy()
+    return a.view(dtype) if dtype is not None else a
+
+
+class GpuModel:
+    def __init__(self, spec: dict, params: dict):
+        self.spec = dict(spec)
+        self.h = fl.Handle(spec)
+        self.t = {k: to_dev(v) for k, v in params.items()}
+        P = fl.FfnParams()
+        for i, (wn, bn) in enumerate(zip(fl.LAYER_NAMES, fl.BIAS_NAMES)):
+            if wn in self.t:
+                P.W[i] = fl.ptr(self.t[wn])
+                P.b[i] = fl.ptr(self.t[bn])
+                P.mW[i] = fl.ptr(self.t["m" + wn])
+                P.vW[i] = fl.ptr(self.t["v" + wn])
+                P.mb[i] = fl.ptr(self.t["m" + bn])
+                P.vb[i] = fl.ptr(self.t["v" + bn])
+        P.table = fl.ptr(self.t["table"])
+        P.m_table = fl.ptr(self.t["m_table"])
+        P.v_table = fl.ptr(self.t["v_table"])
+        P.occ_in = fl.ptr(self.t["occ_in"])
+        P.occ_st = fl.ptr(self.t["occ_st"])
+        self.h.bind(P, keep=self.t)
+        self.lib = self.h.lib
+
+    def state(self) -> dict:
+        torch.cuda.synchronize()
+        return {k: to_np(v, np.uint32 if k.startswith("occ_") else None).copy() for k, v in self.t.items()}
+
+    def train_step(self, rays, targets, S, scalars: dict, taps=False):
+        rays_t = to_dev(np.ascontiguousarray(rays, np.float32).reshape(-1, 8))
+        tg_t = to_dev(np.ascontiguousarray(targets, np.float32).reshape(-1, 4))
+        N = rays_t.shape[0]
+        out = torch.zeros((N, 4), dtype=torch.float32, device=DEV)
+        sc = fl.FfnStepScalars()
+        for k in ("lr", "lr_t", "color_rel_lr", "sh_multiplier", "occ_strength", "beta1", "beta2", "eps"):
+            setattr(sc, k, float(scalars[k]))
+        sc.rng_seed = int(scalars["rng_seed"]) & 0xFFFFFFFF
+        sc.do_train = int(bool(scalars.get("do_train", 1)))
+        tp = None
+        td = None
+        if taps:
+            LF = self.spec["n_levels"] * self.spec["f_per_level"]
+            z = lambda *s: torch.zeros(s, dtype=torch.float32, device=DEV)
+            td = dict(Ts=z(N * S), DTs=z(N * S), flags=torch.zeros(N * 2, dtype=torch.int32, device=DEV),
+                      a0=z(N * S, LF), sigma=z(N * S), rgb=z(N * S, 3), Tr=z(N * S), dL_dsigma=z(N * S),
+                      dL_dc=z(N * S, 3), dL_da0=z(N * S, LF))
+            tp = fl.FfnTaps()
+            for k, v in td.items():
+                setattr(tp, k, fl.ptr(v))
+            for i, wn in enumerate(fl.LAYER_NAMES):
+                if wn in self.t:
+                    bn = fl.BIAS_NAMES[i]
+                    td["g" + wn] = torch.zeros_like(self.t[wn])
+                    td["g" + bn] = torch.zeros_like(self.t[bn])
+                    tp.gW[i] = fl.ptr(td["g" + wn])
+                    tp.gb[i] = fl.ptr(td["g" + bn])
+            if self.spec.get("hash_opt", 0) == 1:
+                td["g_table"] = torch.zeros_like(self.t["table"])
+                tp.g_table = fl.ptr(td["g_table"])
+        fl.check(self.lib.ffn_train_step(self.h.h, fl.ptr(rays_t), fl.ptr(tg_t), fl.ptr(out), N, S, C.byref(sc),
+                                         C.byref(tp) if tp is not None else None, fl.stream_ptr()), "ffn_train_step")
+        torch.cuda.synchronize()
+        res = None
+        if taps:
+            res = {k: to_np(v) for k, v in td.items()}
+            res["flags"] = res["flags"].view(np.uint32)
+        return to_np(out), res
+
+    def sample(self, rays, S, seed, do_train=1):
+        rays_t = to_dev(np.ascontiguousarray(rays, np.float32).reshape(-1, 8))
+        N = rays_t.shape[0]
+        Ts = torch.zeros(N * S, dtype=torch.float32, device=DEV)
+        DTs = torch.zeros(N * S, dtype=torch.float32, device=DEV)
+        flags = torch.zeros(N * 2, dtype=torch.int32, device=DEV)
+        fl.check(self.lib.ffn_sample(self.h.h, fl.ptr(rays_t), N, S, seed & 0xFFFFFFFF, do_train, fl.ptr(Ts),
+                                     fl.ptr(DTs), fl.ptr(flags), fl.stream_ptr()), "ffn_sample")
+        torch.cuda.synchronize()
+        return to_np(Ts).reshape(N, S), to_np(DTs).reshape(N, S), to_np(flags, np.uint32).reshape(N, 2)
+
+    def encode(self, x, with_idx=False):
+        x_t = to_dev(np.ascontiguousarray(x, np.float32).reshape(-1, 3))
+        n = x_t.shape[0]
+        LF = self.spec["n_levels"] * self.spec["f_per_level"]
+        a0 = torch.zeros((n, LF), dtype=torch.float32, device=DEV)
+        idx = torch.zeros((n, self.spec["n_levels"], 8), dtype=torch.int32, device=DEV) if with_idx else None
+        fl.check(self.lib.ffn_hash_encode_fwd(self.h.h, fl.ptr(x_t), n, fl.ptr(a0), fl.ptr(idx), fl.stream_ptr()),
+                 "ffn_hash_encode_fwd")
+        torch.cuda.synchronize()
+        return (to_np(a0), to_np(idx, np.uint32)) if with_idx else to_np(a0)
+
+    def encode_bwd(self, x, g, table_n):
+        x_t = to_dev(np.ascontiguousarray(x, np.float32).reshape(-1, 3))
+        g_t = to_dev(np.ascontiguousarray(g, np.float32))
+        grad = torch.zeros(table_n, dtype=torch.float32, device=DEV)
+        fl.check(self.lib.ffn_hash_encode_bwd(self.h.h, fl.ptr(x_t), fl.ptr(g_t), x_t.shape[0], fl.ptr(grad),
+                                              fl.stream_ptr()), "ffn_hash_encode_bwd")
+        torch.cuda.synchronize()
+        return to_np(grad)

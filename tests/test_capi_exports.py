@@ -1,0 +1,45 @@
+"""The C-ABI library loads and exports every entry point include/ffnerf_hip.h
+declares (no compute calls: this runs on the CPU-only container too)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    text = (ROOT / "include" / "ffnerf_hip.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(ffn_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for n in ("ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step", "ffn_occ_decay", "ffn_sample",
+              "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam", "ffn_last_error", "ffn_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    import ffn_lib
+    if not ffn_lib.LIB_PATH.exists():
+        pytest.fail("libffnerf_hip.so is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(ffn_lib.LIB_PATH))
+    for n in declared_functions():
+        assert hasattr(lib, n), n
+    assert sorted(ffn_lib.EXPORTS) == declared_functions()
+    assert ffn_lib.load().ffn_version() == 1
+
+
+def test_invalid_config_is_an_error_not_a_silent_return():
+    import ffn_lib as fl
+    from common import spec_cfg0
+    lib = fl.load()
+    cfg = fl.make_config(spec_cfg0(nd=5))
+    h = ctypes.c_void_p()
+    rc = lib.ffn_create(ctypes.byref(cfg), ctypes.byref(h))
+    assert rc < 0 and b"nd=5" in lib.ffn_last_error()
+    cfg = fl.make_config(spec_cfg0(f_per_level=3))
+    assert lib.ffn_create(ctypes.byref(cfg), ctypes.byref(h)) < 0
+    assert b"f_per_level" in lib.ffn_last_error()

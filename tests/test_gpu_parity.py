@@ -1,0 +1,222 @@
+"""GPU parity of libffnerf_hip.so against the CPU oracle on the same seeded
+inputs.  Bit-exact where the north star asks for it (sample times, run flags,
+hash indices and encodings, occupancy words, Adam); fp32 tolerances elsewhere
+(the MLP runs as MFMA tiles, so its sums associate differently)."""
+import numpy as np
+import pytest
+
+from common import (LAYERS, BIASES, default_scalars, layer_shapes, look_at_rays, random_params, spec_cfg0,
+                    spec_cfg1, spec_ref, sphere_targets, table_floats)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gh():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("a GPU test ran without a visible GPU")
+    import gpu_helpers
+    return gpu_helpers
+
+
+def _flag_bits(flags, S):
+    return [[(int(f[i >> 5]) >> (i & 31)) & 1 for i in range(S)] for f in flags]
+
+
+@pytest.mark.parametrize("S", [64, 32, 16, 8, 4, 2, 1])
+@pytest.mark.parametrize("do_train", [1, 0])
+def test_sampler_bit_exact(gh, ora, S, do_train):
+    print(f"[case] sampler S={S} do_train={do_train}", flush=True)
+    spec = spec_cfg0()
+    p = random_params(spec, seed=11)
+    m = gh.GpuModel(spec, p)
+    rays = look_at_rays(257, spec, seed=12, miss_frac=0.2)
+    seed = 0x9E3779B9
+    Ts, DTs, flags = m.sample(rays, S, seed, do_train)
+    cfg = ora.make_cfg(spec)
+    for r in range(rays.shape[0]):
+        t_o, dt_o, f_o = ora.sample_ray(cfg, rays[r], r, S, seed, p["occ_in"], do_train)
+        assert np.array_equal(Ts[r], t_o), r
+        assert np.array_equal(DTs[r], dt_o), r
+        mask = (1 << S) - 1 if S < 64 else 0xFFFFFFFFFFFFFFFF
+        g64 = (int(flags[r, 0]) | (int(flags[r, 1]) << 32)) & mask
+        o64 = (int(f_o[0]) | (int(f_o[1]) << 32)) & mask
+        assert g64 == o64, r
+
+
+@pytest.mark.parametrize("which", ["cfg0", "cfg1", "ref"])
+def test_hash_forward_bit_exact(gh, ora, which):
+    print(f"[case] hash fwd {which}", flush=True)
+    spec = {"cfg0": spec_cfg0, "cfg1": spec_cfg1, "ref": spec_ref}[which]()
+    p = random_params(spec, seed=21)
+    m = gh.GpuModel(spec, p)
+    rng = np.random.default_rng(22)
+    lo, hi = np.array(spec["box_min"]), np.array(spec["box_max"])
+    x = (lo + (hi - lo) * rng.uniform(-0.05, 1.05, (20000, 3))).astype(np.float32)
+    x[:16] = hi  # the top face: extrapolated last cell
+    a0_g, idx_g = m.encode(x, with_idx=True)
+    a0_o, idx_o, _ = ora.hash_encode(ora.make_cfg(spec), p["table"], x, with_idx=True)
+    assert np.array_equal(idx_g, idx_o)
+    assert np.array_equal(a0_g.view(np.uint32), a0_o.view(np.uint32))
+
+
+@pytest.mark.parametrize("which", ["cfg0", "ref"])
+def test_hash_backward_matches_oracle(gh, ora, which):
+    print(f"[case] hash bwd {which}", flush=True)
+    spec = {"cfg0": spec_cfg0, "ref": spec_ref}[which]()
+    p = random_params(spec, seed=31)
+    m = gh.GpuModel(spec, p)
+    rng = np.random.default_rng(32)
+    lo, hi = np.array(spec["box_min"]), np.array(spec["box_max"])
+    n = 30000
+    x = (lo + (hi - lo) * rng.uniform(0, 1, (n, 3))).astype(np.float32)
+    LF = spec["n_levels"] * spec["f_per_level"]
+    g = rng.normal(size=(n, LF)).astype(np.float32)
+    g[5, 3] = np.nan  # dropped, like the reference's isfinite guard
+    grad_g = m.encode_bwd(x, g, table_floats(spec))
+    grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
+    scale = np.abs(grad_o).max()
+    assert np.isfinite(grad_g).all()
+    assert np.abs(grad_g - grad_o).max() <= 1e-5 * scale
+    touched_g, touched_o = grad_g != 0, grad_o != 0
+    assert (touched_g == touched_o).mean() > 0.9999
+
+
+def test_occ_decay_bit_exact(gh, ora):
+    import ctypes
+    import torch
+    import ffn_lib as fl
+    print("[case] occ decay", flush=True)
+    rng = np.random.default_rng(41)
+    n = 64 ** 3
+    win = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+    wst = win.copy()
+    raise_ = rng.random(n) < 0.3
+    wst[raise_] |= rng.integers(0, 2 ** 32, int(raise_.sum()), dtype=np.uint64).astype(np.uint32)
+    for q24, seed in ((int(round(0.9 * (1 << 24))), 1234), (int(round(0.95 * (1 << 24))), 99), (1 << 24, 7), (0, 3)):
+        gi, gs = gh.to_dev(win), gh.to_dev(wst)
+        fl.check(fl.load().ffn_occ_decay(fl.ptr(gi), fl.ptr(gs), n, q24, seed, fl.stream_ptr()), "decay")
+        torch.cuda.synchronize()
+        oi, os_ = win.copy(), wst.copy()
+        ora.occ_decay(oi, os_, q24, seed)
+        assert np.array_equal(gh.to_np(gi, np.uint32), oi)
+        assert np.array_equal(gh.to_np(gs, np.uint32), os_)
+
+
+def test_adam_bit_exact(gh, ora):
+    import torch
+    import ffn_lib as fl
+    print("[case] adam", flush=True)
+    rng = np.random.default_rng(51)
+    n = 1_000_003
+    p, m, v = (rng.normal(size=n).astype(np.float32) for _ in range(3))
+    v = np.abs(v)
+    g = (rng.normal(size=n) * (rng.random(n) < 0.3)).astype(np.float32)
+    t = [gh.to_dev(a) for a in (p, m, v, g)]
+    fl.check(fl.load().ffn_adam(*[fl.ptr(x) for x in t], n, 0.01, 0.9, 0.99, 1e-15, 1, fl.stream_ptr()), "adam")
+    torch.cuda.synchronize()
+    ora.adam(p, m, v, g, 0.01, 0.9, 0.99, 1e-15)
+    assert np.array_equal(gh.to_np(t[0]), p)
+    assert np.array_equal(gh.to_np(t[1]), m)
+    assert np.array_equal(gh.to_np(t[2]), v)
+    assert not gh.to_np(t[3]).any()  # gradient cleared in the same pass
+
+
+def _rel(a, b):
+    return np.abs(a - b).max() / (np.abs(b).max() + 1e-30)
+
+
+def _compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
+    m = gh.GpuModel(spec, p)
+    o = ora.OracleModel(spec, {k: v.copy() for k, v in p.items()})
+    out_g, tg_ = m.train_step(rays, tg, S, sc, taps=True)
+    out_o, to_ = o.train_step(rays, tg, S, sc, taps=True)
+    # bit-exact: sampling and encoding
+    assert np.array_equal(tg_["Ts"], to_["Ts"])
+    assert np.array_equal(tg_["DTs"], to_["DTs"])
+    assert np.array_equal(tg_["flags"], to_["flags"])
+    assert np.array_equal(tg_["a0"].view(np.uint32), to_["a0"].view(np.uint32))
+    # fp32 path: MFMA sums vs sequential sums
+    assert np.allclose(tg_["sigma"], to_["sigma"], rtol=1e-4, atol=1e-5)
+    assert np.allclose(tg_["rgb"], to_["rgb"], rtol=1e-4, atol=1e-5)
+    assert np.allclose(tg_["Tr"], to_["Tr"], rtol=1e-4, atol=1e-5)
+    assert np.allclose(out_g, out_o, atol=1e-4)
+    if not sc.get("do_train", 1):
+        return m, o
+    assert _rel(tg_["dL_dsigma"], to_["dL_dsigma"]) < 1e-3
+    assert _rel(tg_["dL_dc"], to_["dL_dc"]) < 1e-3
+    assert _rel(tg_["dL_da0"], to_["dL_da0"]) < 1e-3
+    for wn in layer_shapes(spec):
+        bn = BIASES[LAYERS.index(wn)]
+        assert _rel(tg_["g" + wn], to_["g" + wn]) < 1e-3, wn
+        assert _rel(tg_["g" + bn], to_["g" + bn]) < 1e-3, bn
+    if "g_table" in to_:
+        assert _rel(tg_["g_table"], to_["g_table"]) < 1e-3
+    if check_params:
+        sg, so = m.state(), o.p
+        for k in list(layer_shapes(spec)) + ["table"]:
+            d_g = sg[k].astype(np.float64) - p[k]
+            d_o = so[k].astype(np.float64) - p[k]
+            big = np.abs(d_o) > 1e-3 * np.abs(d_o).max()
+            # Adam's first step is sign-like: compare where the update is not vanishing
+            assert np.allclose(d_g[big], d_o[big], rtol=1e-3, atol=1e-3 * np.abs(d_o).max()), k
+        words_same = np.mean(sg["occ_st"] == so["occ_st"])
+        assert words_same > 0.995, words_same
+        assert np.array_equal(sg["occ_in"], so["occ_in"])
+    return m, o
+
+
+@pytest.mark.parametrize("S", [64, 32, 16])
+def test_train_step_cfg0_adam(gh, ora, S):
+    print(f"[case] train step cfg0 adam S={S}", flush=True)
+    spec = spec_cfg0(hash_opt=1)
+    p = random_params(spec, seed=61)
+    rays = look_at_rays(96 * 64 // S, spec, seed=62, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    _compare_step(spec, p, rays, tg, S, default_scalars(), gh, ora)
+
+
+def test_train_step_empty_grid_proposals(gh, ora):
+    print("[case] train step proposals", flush=True)
+    spec = spec_cfg0(hash_opt=1)
+    p = random_params(spec, seed=71)
+    p["occ_in"][:] = 0
+    p["occ_st"][:] = 0
+    p["bd_out"][0] = 4.0
+    rays = look_at_rays(128, spec, seed=72, miss_frac=0.0)
+    tg = sphere_targets(rays, spec)
+    m, o = _compare_step(spec, p, rays, tg, 64, default_scalars(), gh, ora)
+    assert not np.array_equal(o.p["occ_st"], p["occ_st"])
+
+
+@pytest.mark.parametrize("bg", [1, 2])
+def test_train_step_backgrounds_and_sgd(gh, ora, bg):
+    print(f"[case] train step sgd bg={bg}", flush=True)
+    spec = spec_cfg0(hash_opt=0, background=bg)
+    p = random_params(spec, seed=81)
+    rays = look_at_rays(64, spec, seed=82, miss_frac=0.2)
+    tg = sphere_targets(rays, spec)
+    _compare_step(spec, p, rays, tg, 64, default_scalars(lr=0.05), gh, ora)
+
+
+def test_train_step_reference_shape(gh, ora):
+    """The reference's compiled-in shape: L=16, F=4 (LF=64), per-level T, ND=NC=2, SGD table."""
+    print("[case] train step reference shape", flush=True)
+    spec = spec_ref(hash_opt=0)
+    p = random_params(spec, seed=91)
+    rays = look_at_rays(48, spec, seed=92, miss_frac=0.1, radius=1.2)
+    tg = np.random.default_rng(93).uniform(0, 1, (48, 4)).astype(np.float32)
+    _compare_step(spec, p, rays, tg, 64, default_scalars(lr=0.01, lr_t=0.01, beta2=0.999, eps=1e-6), gh, ora)
+
+
+def test_render_mode(gh, ora):
+    print("[case] render", flush=True)
+    spec = spec_cfg0(hash_opt=1)
+    p = random_params(spec, seed=101)
+    rays = look_at_rays(64, spec, seed=102)
+    tg = np.zeros((64, 4), np.float32)
+    m, o = _compare_step(spec, p, rays, tg, 64, default_scalars(do_train=0), gh, ora)
+    st = m.state()
+    for k in ("table", "Wd_in", "Wc_out", "occ_in", "occ_st"):
+        assert np.array_equal(st[k], p[k]), k
