@@ -1,0 +1,183 @@
+"""Benchmark of the fused NeRF training step on one MI355X.
+
+Workload (the GPU-saturating batch): 2^18 rays x 64
+samples per step (16.8M samples), hash grid 16 levels x 2 features, T = 2^19
+per level, resolutions 16 -> 2048; density MLP 32->64->16, colour MLP
+32->64->64->3, Xavier init; Adam (lr 1e-2, betas 0.9/0.99, eps 1e-15) on the
+MLP and the table; 128^3 occupancy (64^3 words) with proposals every step and
+decay 0.95 every 16 steps.  Rays and targets come from the synthetic ball scene
+(56 cameras, 450x800, f=640) and are resident in HBM before timing starts.
+
+One step = sampler + hash encode + fused MLP/compositing/backward + hash
+scatter + Adam (MLP and table) [+ occupancy decay].  Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "ffnerf-experimental_amd"
+for p in (str(ROOT), str(PKG)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def cfg2_spec(mlp="fp32"):
+    import ffnerf_tools as ft
+    L = 16
+    spec = ft.ModelSpec(n_levels=L, f_per_level=2, log2_T=[19] * L,
+                        res=ft.level_resolutions(L, 16.0, finest=2048.0), nd=1, nc=2, background="black",
+                        hash_opt="adam", mlp_precision=mlp, init="xavier", beta1=0.9, beta2=0.99, eps=1e-15)
+    S = 64
+    occ = ft.OccParams(G_occ=64, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32),
+                       rho_min=1.0, rho_max=16.0, dt_min=np.float32(1.0 / 8192), dt_max=np.float32(12.8 / S / 6),
+                       t_near_clip=0.3, t_far_clip=1e9, occ_update_strength0=1.0, decay=0.95,
+                       maintenance_period=16)
+    return spec, occ, S
+
+
+def algorithmic(spec):
+    L, F = spec.n_levels, spec.f_per_level
+    LF = L * F
+    fwd_b = L * 8 * F * 4 + 12 + LF * 4            # corner gathers + xyz + features out
+    bwd_b = 2 * L * 8 * F * 4 + 12 + LF * 4        # atomic read-modify-write + xyz + upstream grad
+    macs = LF * 64 + 64 * 16 + 32 * 64 + (spec.nc - 1) * 64 * 64 + 64 * 3 + (spec.nd - 1) * 64 * 64
+    mlp_flops = 6 * macs                           # fwd + dX + dW
+    adam_b = 28                                    # per parameter: r p,g,m,v; w p,m,v
+    return fwd_b, bwd_b, mlp_flops, adam_b
+
+
+def cpu_baseline(seconds=12.0):
+    """The oracle (single-threaded C restatement of the reference step) on a
+    bounded sample: steps of 512 rays x 64 samples at the cfg1 shapes."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle import oracle as ora
+    import ffnerf_tools as ft
+    import synthetic_scene as sc
+    spec, occ, S = cfg2_spec()
+    sd = ft.spec_dict(spec, occ)
+    rng = np.random.default_rng(0)
+    p = ft.init_params(spec, occ, rng)
+    model = ora.OracleModel(sd, {k: v.reshape(spec.layer_shapes()[k]) if k in spec.layer_shapes() else v
+                                 for k, v in p.items()})
+    cams = sc.cameras_for("cfg1")
+    scal = dict(lr=1e-2, lr_t=1e-2, color_rel_lr=1.0, sh_multiplier=1.0, occ_strength=1.0, beta1=0.9, beta2=0.99,
+                eps=1e-15, rng_seed=1, do_train=1)
+    rays, tg = sc.uniform_batch(cams, 512, rng)
+    model.train_step(rays, tg, S, scal)  # warm-up
+    n_steps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds or n_steps < 2:
+        rays, tg = sc.uniform_batch(cams, 512, rng)
+        scal["rng_seed"] = n_steps + 2
+        model.train_step(rays, tg, S, scal)
+        n_steps += 1
+    dt = time.perf_counter() - t0
+    return dict(value=n_steps * 512 * S / dt, unit="samples/s", cores=1, kind="port",
+                sample=f"{n_steps} oracle steps of 512 rays x {S} samples (cfg1 shapes: L16 F2 T2^19, Adam), "
+                       f"{dt:.1f} s, 1 thread")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--mlp", default="fp32", choices=["fp32", "fp16"])
+    ap.add_argument("--rays", type=int, default=1 << 18)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested); the multi-GPU design is "
+              f"described in DESIGN.md and is not run here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import ffnerf_tools as ft
+    import synthetic_scene as sc
+
+    spec, occ, S = cfg2_spec(args.mlp)
+    n_rays = int(args.rays)
+    import tempfile
+    nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_bench_"), "bench", spec=spec, occ=occ, rng_seed=0)
+    print(f"[bench] cfg2 model built: table {spec.table_entries() * spec.f_per_level / 1e6:.1f}M params", flush=True)
+    cams = sc.cameras_for("cfg2")
+    rng = np.random.default_rng(123)
+    pool = []
+    for _ in range(4):
+        rays, tg = sc.uniform_batch(cams, n_rays, rng)
+        io = ft.RayBatch.init(n_rays, S)
+        io.upload_rays(rays)
+        io.upload_targets(tg)
+        pool.append(io)
+    torch.cuda.synchronize()
+    print(f"[bench] {len(pool)} ray batches of {n_rays} resident; warm-up {args.warmup}", flush=True)
+
+    def one(i):
+        nerf.step(pool[i % len(pool)], lr_f=1e-2, do_train=True, occ_update_strength=1.0, sh_multiplier=1.0,
+                  color_MLP_rel_lr=1.0)
+
+    for i in range(args.warmup):
+        one(i)
+    torch.cuda.synchronize()
+    nerf.handle.set_profiling(True)
+    nerf.handle.stage_times(reset=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        one(args.warmup + i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    stages = nerf.handle.stage_times(reset=True)
+    nerf.handle.set_profiling(False)
+    print(f"[bench] timed {args.steps} steps in {t1 - t0:.3f} s", flush=True)
+
+    N = n_rays * S
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    value = N * args.steps / (t1 - t0)
+    fwd_b, bwd_b, mlp_flops, adam_b = algorithmic(spec)
+    avg = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
+    per = {
+        "hash_fwd": ("hbm", fwd_b * N / (avg["hash_fwd"] * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", fwd_b * N),
+        "hash_bwd": ("hbm", bwd_b * N / (avg["hash_bwd"] * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", bwd_b * N),
+        "mlp": ("mfma", mlp_flops * N / (avg["mlp"] * 1e-3) / 1e12,
+                FP16_PEAK_TFLOPS if args.mlp == "fp16" else FP32_PEAK_TFLOPS, "TFLOP/s", mlp_flops * N),
+    }
+    dominant = max(per, key=lambda k: avg[k])
+    bound, ach, peak, unit, alg = per[dominant]
+    hash_gbs = (fwd_b + bwd_b) * N / ((avg["hash_fwd"] + avg["hash_bwd"]) * 1e-3) / 1e9
+    line = {
+        "metric": "train samples/sec (fwd+bwd+Adam) per step; hash-grid gather/scatter HBM GB/s",
+        "value": value, "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32" if args.mlp == "fp32" else "fp16-mfma/fp32", "data": "synthetic",
+        "config": {"workload": "BASELINE configs[2]: 2^18 rays x 64 samples/step, hash L16 F2 T2^19 16->2048 fp32, "
+                               "MLP 32-64-16 / 32-64-64-3, Adam table+MLP, occupancy 128^3, decay 0.95 every 16",
+                   "global_batch": n_rays, "samples_per_ray": S, "samples_per_step": N, "mlp": args.mlp},
+        "hash_grid_gbs": hash_gbs,
+        "roofline": {"kernel": dominant, "bound": bound, "achieved": ach, "peak": peak, "unit": unit,
+                     "frac": ach / peak, "algorithmic_per_launch": alg, "traffic": None},
+        "stages_ms_avg": {k: round(v, 4) for k, v in avg.items()},
+        "stage_rooflines": {k: {"achieved": v[1], "unit": v[3], "frac": v[1] / v[2]} for k, v in per.items()},
+    }
+    if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:
+        print("[bench] timing the CPU oracle on a bounded sample", flush=True)
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

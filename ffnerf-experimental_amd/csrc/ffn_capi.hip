@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <string>
+#include <vector>
 
 #include "ffn_device.h"
 #include "ffn_kernels.h"
@@ -53,7 +54,14 @@ struct Scratch {
   }
 };
 
+struct StageEvent {
+  int stage;
+  hipEvent_t start, stop;
+};
+
 struct Handle {
+  bool prof = false;
+  std::vector<StageEvent> events;
   ffn_config cfg;
   ffn::DevCfg dc;
   ffn::PackedLayout lay;
@@ -123,6 +131,36 @@ ffn::DevCfg make_devcfg(const ffn_config* c) {
 
 Handle* as_handle(void* h) { return static_cast<Handle*>(h); }
 
+// Brackets one stage of a step with HIP events when profiling is on.
+struct StageTimer {
+  Handle* h;
+  hipStream_t st;
+  StageEvent ev{};
+  bool on;
+  StageTimer(Handle* h_, int stage, hipStream_t s) : h(h_), st(s), on(h_->prof) {
+    if (!on) return;
+    ev.stage = stage;
+    if (hipEventCreate(&ev.start) != hipSuccess || hipEventCreate(&ev.stop) != hipSuccess) {
+      on = false;
+      return;
+    }
+    (void)hipEventRecord(ev.start, st);
+  }
+  ~StageTimer() {
+    if (!on) return;
+    (void)hipEventRecord(ev.stop, st);
+    h->events.push_back(ev);
+  }
+};
+
+void clear_events(Handle* h) {
+  for (auto& e : h->events) {
+    (void)hipEventDestroy(e.start);
+    (void)hipEventDestroy(e.stop);
+  }
+  h->events.clear();
+}
+
 }  // namespace
 
 extern "C" {
@@ -158,6 +196,7 @@ int ffn_destroy(void* handle) {
   Handle* h = as_handle(handle);
   if (!h) return 0;
   (void)hipDeviceSynchronize();
+  clear_events(h);
   h->Ts.release();
   h->DTs.release();
   h->flags.release();
@@ -276,9 +315,15 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   float* dLda0 = (float*)h->dLda0.p;
   const ffn_params& P = h->params;
 
-  FFN_HIP(ffn::launch_sample(h->dc, (const float4*)rays, num_rays, (int)spr, sc->rng_seed, P.occ_in, train ? 1 : 0,
-                             Ts, DTs, flags, st));
-  FFN_HIP(ffn::launch_hash_fwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, P.table, a0, nullptr, st));
+  {
+    StageTimer tm(h, 0, st);
+    FFN_HIP(ffn::launch_sample(h->dc, (const float4*)rays, num_rays, (int)spr, sc->rng_seed, P.occ_in,
+                               train ? 1 : 0, Ts, DTs, flags, st));
+  }
+  {
+    StageTimer tm(h, 1, st);
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, P.table, a0, nullptr, st));
+  }
 
   ffn::MlpArgs a{};
   a.c = h->dc;
@@ -312,7 +357,10 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     a.t_dLds = taps->dL_dsigma;
     a.t_dLdc = taps->dL_dc;
   }
-  FFN_HIP(ffn::launch_mlp(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+  {
+    StageTimer tm(h, 2, st);
+    FFN_HIP(ffn::launch_mlp(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+  }
 
   if (taps) {
     if (taps->Ts) FFN_HIP(hipMemcpyAsync(taps->Ts, Ts, sizeof(float) * N, hipMemcpyDeviceToDevice, st));
@@ -325,11 +373,15 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   }
   if (!train) return 0;
 
-  if (h->cfg.hash_opt == FFN_HASH_SGD) {
-    FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, P.table, 1, sc->lr, st));
-  } else {
-    FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, (float*)h->gtable.p, 0,
-                                 0.0f, st));
+  {
+    StageTimer tm(h, 3, st);
+    if (h->cfg.hash_opt == FFN_HASH_SGD) {
+      FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, P.table, 1, sc->lr,
+                                   st));
+    } else {
+      FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, (float*)h->gtable.p, 0,
+                                   0.0f, st));
+    }
   }
 
   ffn::MlpOptArgs o{};
@@ -353,15 +405,44 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   o.beta1 = sc->beta1;
   o.beta2 = sc->beta2;
   o.eps = sc->eps;
-  FFN_HIP(ffn::launch_mlp_adam(o, st));
+  {
+    StageTimer tm(h, 4, st);
+    FFN_HIP(ffn::launch_mlp_adam(o, st));
+  }
 
   if (h->cfg.hash_opt == FFN_HASH_ADAM) {
     if (taps && taps->g_table)
       FFN_HIP(hipMemcpyAsync(taps->g_table, h->gtable.p, sizeof(float) * (size_t)h->table_floats,
                              hipMemcpyDeviceToDevice, st));
+    StageTimer tm(h, 5, st);
     FFN_HIP(ffn::launch_adam(P.table, P.m_table, P.v_table, (float*)h->gtable.p, h->table_floats, sc->lr_t,
                              sc->beta1, sc->beta2, sc->eps, 1, st));
   }
+  return 0;
+}
+
+int ffn_set_profiling(void* handle, int32_t enable) {
+  Handle* h = as_handle(handle);
+  if (!h) return fail(-1, "NULL handle");
+  h->prof = enable != 0;
+  return 0;
+}
+
+int ffn_stage_times(void* handle, float* total_ms, int32_t* launches, int32_t reset) {
+  Handle* h = as_handle(handle);
+  if (!h || !total_ms || !launches) return fail(-1, "NULL argument");
+  for (int i = 0; i < FFN_N_STAGES; ++i) {
+    total_ms[i] = 0.0f;
+    launches[i] = 0;
+  }
+  for (auto& e : h->events) {
+    FFN_HIP(hipEventSynchronize(e.stop));
+    float ms = 0.0f;
+    FFN_HIP(hipEventElapsedTime(&ms, e.start, e.stop));
+    total_ms[e.stage] += ms;
+    launches[e.stage] += 1;
+  }
+  if (reset) clear_events(h);
   return 0;
 }
 

@@ -23,7 +23,9 @@ MLP_PRECISION = {"fp32": 0, "fp16": 1}
 EXPORTS = [
     "ffn_version", "ffn_last_error", "ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step",
     "ffn_occ_decay", "ffn_sample", "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam",
+    "ffn_set_profiling", "ffn_stage_times",
 ]
+STAGES = ["sample", "hash_fwd", "mlp", "hash_bwd", "mlp_adam", "table_adam"]
 
 _vp = C.c_void_p
 _fp = C.POINTER(C.c_float)
@@ -96,8 +98,10 @@ def load(path: Path | str | None = None) -> C.CDLL:
     lib.ffn_hash_encode_bwd.argtypes = [_vp, _vp, _vp, C.c_int64, _vp, _vp]
     lib.ffn_adam.argtypes = [_vp, _vp, _vp, _vp, C.c_int64, C.c_float, C.c_float, C.c_float, C.c_float, C.c_int32,
                              _vp]
+    lib.ffn_set_profiling.argtypes = [_vp, C.c_int32]
+    lib.ffn_stage_times.argtypes = [_vp, _fp, C.POINTER(C.c_int32), C.c_int32]
     for name in ("ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step", "ffn_occ_decay", "ffn_sample",
-                 "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam"):
+                 "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam", "ffn_set_profiling", "ffn_stage_times"):
         getattr(lib, name).restype = C.c_int
     if path is None:
         _LIB = lib
@@ -174,6 +178,16 @@ class Handle:
     def bind(self, params: FfnParams, keep=None):
         check(self.lib.ffn_bind_params(self.h, C.byref(params)), "ffn_bind_params")
         self._keep = keep
+
+    def set_profiling(self, on: bool):
+        check(self.lib.ffn_set_profiling(self.h, 1 if on else 0), "ffn_set_profiling")
+
+    def stage_times(self, reset: bool = True) -> dict:
+        """{stage: (total_ms, launches)} since the last reset (waits for the work)."""
+        ms = (C.c_float * len(STAGES))()
+        n = (C.c_int32 * len(STAGES))()
+        check(self.lib.ffn_stage_times(self.h, ms, n, 1 if reset else 0), "ffn_stage_times")
+        return {s: (float(ms[i]), int(n[i])) for i, s in enumerate(STAGES)}
 
     def close(self):
         if getattr(self, "h", None):

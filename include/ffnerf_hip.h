@@ -153,6 +153,18 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
 int ffn_adam(float* p, float* m, float* v, float* g, int64_t n, float lr_t, float beta1, float beta2, float eps,
              int32_t zero_grad, void* stream);
 
+/* Stage timing (the counterpart of the reference's profiling queue and
+ * event_ms, ffnerf_tools.py:11-13,127-138,1521-1530).  When enabled, every
+ * ffn_train_step records HIP events around its kernels on the caller's stream;
+ * ffn_stage_times waits for the last step and returns the accumulated
+ * milliseconds and launch counts per stage since the last reset.  Stages:
+ * 0 sample, 1 hash_fwd, 2 mlp, 3 hash_bwd, 4 mlp_adam, 5 table_adam.  No
+ * counterpart in the reference's kernel ABI: it replaces the host-side event
+ * reads above. */
+#define FFN_N_STAGES 6
+int ffn_set_profiling(void* handle, int32_t enable);
+int ffn_stage_times(void* handle, float* total_ms, int32_t* launches, int32_t reset);
+
 #ifdef __cplusplus
 }
 #endif
