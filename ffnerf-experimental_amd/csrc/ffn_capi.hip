@@ -3,6 +3,7 @@
 // buffers of one step, and the launch sequence of a training step.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -69,8 +70,35 @@ struct Handle {
   bool bound = false;
   int64_t table_floats = 0;
   int n_cu = 0;
-  Scratch Ts, DTs, flags, a0, dLda0, partials, gtable;
+  Scratch Ts, DTs, flags, a0, dLda0, partials;
+  Scratch bin_cnt, bin_off, bin_sums, bin_total, bin_idx, bin_val;
 };
+
+size_t bin_budget_bytes() {
+  const char* e = getenv("FFN_BIN_BUDGET_MB");
+  size_t mb = e ? (size_t)atoll(e) : (size_t)6144;
+  if (mb < 64) mb = 64;
+  return mb << 20;
+}
+
+// size the bucketed-scatter scratch for n samples and fill the views
+hipError_t ensure_bins(Handle* h, int64_t n, ffn::BinPlan* plan, ffn::BinScratch* s) {
+  *plan = ffn::plan_bins(h->dc, n, bin_budget_bytes());
+  hipError_t e;
+  if ((e = h->bin_cnt.ensure(sizeof(uint32_t) * (size_t)plan->cnt_elems)) != hipSuccess) return e;
+  if ((e = h->bin_off.ensure(sizeof(uint32_t) * (size_t)plan->cnt_elems)) != hipSuccess) return e;
+  if ((e = h->bin_sums.ensure(sizeof(uint32_t) * (size_t)plan->tiles)) != hipSuccess) return e;
+  if ((e = h->bin_total.ensure(sizeof(uint32_t) * 4)) != hipSuccess) return e;
+  if ((e = h->bin_idx.ensure(sizeof(uint16_t) * (size_t)plan->max_pairs)) != hipSuccess) return e;
+  if ((e = h->bin_val.ensure(sizeof(float) * (size_t)plan->max_pairs * h->dc.F)) != hipSuccess) return e;
+  s->cnt = (uint32_t*)h->bin_cnt.p;
+  s->off = (uint32_t*)h->bin_off.p;
+  s->sums = (uint32_t*)h->bin_sums.p;
+  s->total = (uint32_t*)h->bin_total.p;
+  s->pair_idx = (uint16_t*)h->bin_idx.p;
+  s->pair_val = (float*)h->bin_val.p;
+  return hipSuccess;
+}
 
 bool is_pow2(uint32_t v) { return v && !(v & (v - 1)); }
 
@@ -203,7 +231,12 @@ int ffn_destroy(void* handle) {
   h->a0.release();
   h->dLda0.release();
   h->partials.release();
-  h->gtable.release();
+  h->bin_cnt.release();
+  h->bin_off.release();
+  h->bin_sums.release();
+  h->bin_total.release();
+  h->bin_idx.release();
+  h->bin_val.release();
   delete h;
   return 0;
 }
@@ -260,7 +293,9 @@ int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint
   if (n < 0) return fail(-1, "negative size");
   if (n > 0 && (!x || !a0)) return fail(-1, "NULL buffer");
   if (!h->params.table) return fail(-1, "bind params (table) first");
-  FFN_HIP(ffn::launch_hash_fwd(h->dc, x, nullptr, nullptr, 0, n, h->params.table, a0, idx_out, (hipStream_t)stream));
+  ffn::PosSrc src{x, nullptr, nullptr, 0};
+  FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, a0, ffn::sample_major(h->dc.L, h->dc.F), idx_out,
+                               (hipStream_t)stream));
   return 0;
 }
 
@@ -269,7 +304,15 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
   if (!h) return fail(-1, "NULL handle");
   if (n < 0) return fail(-1, "negative size");
   if (n > 0 && (!x || !g || !grad)) return fail(-1, "NULL buffer");
-  FFN_HIP(ffn::launch_hash_bwd(h->dc, x, nullptr, nullptr, 0, n, g, grad, 0, 0.0f, (hipStream_t)stream));
+  if (n == 0) return 0;
+  ffn::BinPlan plan;
+  ffn::BinScratch bs;
+  FFN_HIP(ensure_bins(h, n, &plan, &bs));
+  ffn::PosSrc src{x, nullptr, nullptr, 0};
+  ffn::BinApply ap{};
+  ap.dst = grad;
+  FFN_HIP(ffn::launch_hash_bwd(h->dc, src, n, g, ffn::sample_major(h->dc.L, h->dc.F), ffn::BIN_GRAD, 0.0f, ap, plan,
+                               bs, (hipStream_t)stream));
   return 0;
 }
 
@@ -303,11 +346,12 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   if (train) {
     FFN_HIP(h->dLda0.ensure(sizeof(float) * N * LF));
     FFN_HIP(h->partials.ensure(sizeof(float) * (size_t)n_blocks * h->lay.total));
-    if (h->cfg.hash_opt == FFN_HASH_ADAM && h->gtable.bytes < sizeof(float) * (size_t)h->table_floats) {
-      FFN_HIP(h->gtable.ensure(sizeof(float) * (size_t)h->table_floats));
-      FFN_HIP(ffn::launch_fill((float*)h->gtable.p, h->table_floats, 0.0f, st));
-    }
   }
+  ffn::BinPlan plan{};
+  ffn::BinScratch bs{};
+  if (train) FFN_HIP(ensure_bins(h, N, &plan, &bs));
+  const ffn::FeatLayout feat = ffn::level_major(N, h->dc.F);
+  const ffn::PosSrc src{nullptr, (const float4*)rays, nullptr, log2S};
   float* Ts = (float*)h->Ts.p;
   float* DTs = (float*)h->DTs.p;
   uint32_t* flags = (uint32_t*)h->flags.p;
@@ -322,7 +366,9 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   }
   {
     StageTimer tm(h, 1, st);
-    FFN_HIP(ffn::launch_hash_fwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, P.table, a0, nullptr, st));
+    ffn::PosSrc s2 = src;
+    s2.Ts = Ts;
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, s2, N, P.table, a0, feat, nullptr, st));
   }
 
   ffn::MlpArgs a{};
@@ -339,6 +385,7 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   a.flags = flags;
   a.a0 = a0;
   a.dL_da0 = dLda0;
+  a.feat = feat;
   a.partials = (float*)h->partials.p;
   a.occ_in = P.occ_in;
   a.occ_st = P.occ_st;
@@ -367,21 +414,31 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     if (taps->DTs) FFN_HIP(hipMemcpyAsync(taps->DTs, DTs, sizeof(float) * N, hipMemcpyDeviceToDevice, st));
     if (taps->flags)
       FFN_HIP(hipMemcpyAsync(taps->flags, flags, sizeof(uint32_t) * 2 * num_rays, hipMemcpyDeviceToDevice, st));
-    if (taps->a0) FFN_HIP(hipMemcpyAsync(taps->a0, a0, sizeof(float) * N * LF, hipMemcpyDeviceToDevice, st));
+    const ffn::FeatLayout sm = ffn::sample_major(h->dc.L, h->dc.F);
+    if (taps->a0) FFN_HIP(ffn::launch_feat_relayout(a0, feat, taps->a0, sm, N, h->dc.L, h->dc.F, st));
     if (train && taps->dL_da0)
-      FFN_HIP(hipMemcpyAsync(taps->dL_da0, dLda0, sizeof(float) * N * LF, hipMemcpyDeviceToDevice, st));
+      FFN_HIP(ffn::launch_feat_relayout(dLda0, feat, taps->dL_da0, sm, N, h->dc.L, h->dc.F, st));
   }
   if (!train) return 0;
 
   {
     StageTimer tm(h, 3, st);
-    if (h->cfg.hash_opt == FFN_HASH_SGD) {
-      FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, P.table, 1, sc->lr,
-                                   st));
-    } else {
-      FFN_HIP(ffn::launch_hash_bwd(h->dc, nullptr, (const float4*)rays, Ts, log2S, N, dLda0, (float*)h->gtable.p, 0,
-                                   0.0f, st));
+    ffn::PosSrc s2 = src;
+    s2.Ts = Ts;
+    ffn::BinApply ap{};
+    ap.dst = P.table;
+    int mode = ffn::BIN_SGD;
+    if (h->cfg.hash_opt == FFN_HASH_ADAM) {
+      mode = ffn::BIN_ADAM;
+      ap.m = P.m_table;
+      ap.v = P.v_table;
+      ap.g_tap = taps ? taps->g_table : nullptr;
+      ap.lr_t = sc->lr_t;
+      ap.beta1 = sc->beta1;
+      ap.beta2 = sc->beta2;
+      ap.eps = sc->eps;
     }
+    FFN_HIP(ffn::launch_hash_bwd(h->dc, s2, N, dLda0, feat, mode, sc->lr, ap, plan, bs, st));
   }
 
   ffn::MlpOptArgs o{};
@@ -410,14 +467,6 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     FFN_HIP(ffn::launch_mlp_adam(o, st));
   }
 
-  if (h->cfg.hash_opt == FFN_HASH_ADAM) {
-    if (taps && taps->g_table)
-      FFN_HIP(hipMemcpyAsync(taps->g_table, h->gtable.p, sizeof(float) * (size_t)h->table_floats,
-                             hipMemcpyDeviceToDevice, st));
-    StageTimer tm(h, 5, st);
-    FFN_HIP(ffn::launch_adam(P.table, P.m_table, P.v_table, (float*)h->gtable.p, h->table_floats, sc->lr_t,
-                             sc->beta1, sc->beta2, sc->eps, 1, st));
-  }
   return 0;
 }
 

@@ -1,11 +1,29 @@
-// ffn_hash.hip -- multiresolution hash-grid encoding, forward gather and
-// backward scatter-add (reference: ffnerf_OG.cl:1286-1364 and 2090-2173).
+// ffn_hash.hip -- multiresolution hash-grid encoding: forward gather and
+// backward scatter (reference: ffnerf_OG.cl:1286-1364 and 2090-2173).
 //
-// One thread per sample.  Per level the 8 corner indices are formed first and
-// the 8 corner loads (one F-wide vector each) are issued back to back before
-// the trilinear sums, so each thread keeps 8 independent gathers in flight.
-// The sums run corner by corner without FMA contraction, which makes the
-// encodings bit-identical to the CPU restatement.
+// MI355X design
+//   Forward: one pass per level (grid.y = level).  A level's table (2^19
+//   entries x F floats = 4 MiB at the benchmark shape) then stays resident in
+//   every XCD's 4 MB L2 while all samples gather from it; the encodings are
+//   stored level-major ([L][N][F]), so each pass writes one contiguous array.
+//   The trilinear sums run corner by corner without FMA contraction, which
+//   makes them bit-identical to the CPU restatement.
+//
+//   Backward: scattered float atomics run at ~21 G lanes/s on this chip
+//   (measured), far below what the HBM can stream, so the scatter is done
+//   without global atomics, as a bucketed reduction:
+//     1. count  -- per (level, sample chunk), how many corner contributions
+//                  land in each bucket (BE consecutive table entries of one
+//                  level); LDS histogram, one row of counts per block;
+//     2. scan   -- exclusive prefix over the (bucket, block) counts, so every
+//                  block owns a contiguous slot range inside every bucket;
+//     3. emit   -- recompute the corners and write (entry-in-bucket, value)
+//                  pairs to the slots (LDS cursors, streaming writes);
+//     4. reduce -- one block per bucket sums its pairs into an LDS copy of
+//                  the bucket (ds_add_f32) and applies the update to its own
+//                  slice of the table: gradient add, the reference SGD, or
+//                  Adam.  No gradient table is materialised for Adam.
+//   Levels are processed in groups so the pair buffer stays bounded.
 #include "ffn_device.h"
 #include "ffn_kernels.h"
 
@@ -17,6 +35,7 @@ template <>
 struct FVec<1> {
   typedef float T;
   static __device__ __forceinline__ void unpack(const T& v, float* o) { o[0] = v; }
+  static __device__ __forceinline__ T pack(const float* o) { return o[0]; }
 };
 template <>
 struct FVec<2> {
@@ -25,6 +44,7 @@ struct FVec<2> {
     o[0] = v.x;
     o[1] = v.y;
   }
+  static __device__ __forceinline__ T pack(const float* o) { return make_float2(o[0], o[1]); }
 };
 template <>
 struct FVec<4> {
@@ -35,139 +55,400 @@ struct FVec<4> {
     o[2] = v.z;
     o[3] = v.w;
   }
+  static __device__ __forceinline__ T pack(const float* o) { return make_float4(o[0], o[1], o[2], o[3]); }
 };
 
-__device__ __forceinline__ void sample_position(const float* __restrict__ x, const float4* __restrict__ rays,
-                                                const float* __restrict__ Ts, int log2S, int64_t b, float pos[3]) {
-  if (rays) {
-    const int64_t r = b >> log2S;
-    const float4 o = rays[2 * r], d = rays[2 * r + 1];
-    const float t = Ts[b];
+__device__ __forceinline__ void sample_position(const PosSrc& s, int64_t b, float pos[3]) {
+  if (s.rays) {
+    const int64_t r = b >> s.log2S;
+    const float4 o = s.rays[2 * r], d = s.rays[2 * r + 1];
+    const float t = s.Ts[b];
     pos[0] = o.x + t * d.x;
     pos[1] = o.y + t * d.y;
     pos[2] = o.z + t * d.z;
   } else {
-    pos[0] = x[3 * b + 0];
-    pos[1] = x[3 * b + 1];
-    pos[2] = x[3 * b + 2];
+    pos[0] = s.x[3 * b + 0];
+    pos[1] = s.x[3 * b + 1];
+    pos[2] = s.x[3 * b + 2];
   }
 }
 
+// ---------------------------------------------------------------------------
+// forward
+
 template <int F>
-__global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, const float* __restrict__ x,
-                                                  const float4* __restrict__ rays, const float* __restrict__ Ts,
-                                                  int log2S, int64_t n, const float* __restrict__ table,
-                                                  float* __restrict__ a0, uint32_t* __restrict__ idx_out) {
+__global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t n, int level0,
+                                                  const float* __restrict__ table, float* __restrict__ a0,
+                                                  FeatLayout lay, uint32_t* __restrict__ idx_out) {
   typedef typename FVec<F>::T V;
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= n) return;
+  const int l = level0 + (int)blockIdx.y;
   float pos[3], p[3];
-  sample_position(x, rays, Ts, log2S, b, pos);
+  sample_position(src, b, pos);
   normalize_pos(c, pos, p);
-  const int L = c.L, LF = c.LF;
-  float* out = a0 + b * LF;
-  for (int l = 0; l < L; ++l) {
+  const LevelCell lc = level_cell(c.res[l], p);
+  const uint32_t mask = c.mask[l], off = c.offset[l];
+  uint32_t fb[8];
+  V val[8];
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+    fb[cc] = (off + corner_entry(lc, cc, l, mask)) * (uint32_t)F;
+    val[cc] = *reinterpret_cast<const V*>(table + fb[cc]);
+  }
+  float acc[F];
+#pragma unroll
+  for (int f = 0; f < F; ++f) acc[f] = 0.0f;
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+    const float w = corner_weight(lc, cc);
+    float t[F];
+    FVec<F>::unpack(val[cc], t);
+#pragma unroll
+    for (int f = 0; f < F; ++f) acc[f] += w * t[f];
+  }
+  *reinterpret_cast<V*>(a0 + l * lay.stride_l + b * lay.stride_b) = FVec<F>::pack(acc);
+  if (idx_out) {
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) idx_out[(b * c.L + l) * 8 + cc] = fb[cc];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward: bucketed scatter
+
+// The gradient of one (sample, level): scaled as the mode needs, non-finite
+// components dropped (ffnerf_OG.cl:2162).  Returns false when it is all zero.
+template <int F, int MODE>
+__device__ __forceinline__ bool level_grad(const DevCfg& c, const float* __restrict__ g, const FeatLayout& lay,
+                                           int64_t b, int l, float lr, float gf[F]) {
+  typedef typename FVec<F>::T V;
+  float v[F];
+  FVec<F>::unpack(*reinterpret_cast<const V*>(g + l * lay.stride_l + b * lay.stride_b), v);
+  bool any = false;
+#pragma unroll
+  for (int f = 0; f < F; ++f) {
+    float x = v[f];
+    if (!isfinite(x)) x = 0.0f;
+    if (MODE == BIN_SGD) x = -(lr * c.lvl_lr_scale[l]) * 0.5f * x;
+    gf[f] = x;
+    any |= (x != 0.0f);
+  }
+  return any;
+}
+
+template <int F, int MODE>
+__global__ __launch_bounds__(256) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
+                                                   const float* __restrict__ g, FeatLayout lay, float lr,
+                                                   uint32_t* __restrict__ cnt) {
+  extern __shared__ uint32_t hist[];
+  const int l = grp.level0 + (int)blockIdx.y;
+  const int nbl = grp.nbl[l - grp.level0];
+  const int chunk = blockIdx.x;
+  for (int j = threadIdx.x; j < nbl; j += blockDim.x) hist[j] = 0u;
+  __syncthreads();
+  const int64_t b0 = (int64_t)chunk * grp.chunk;
+  const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
+  for (int64_t b = b0 + threadIdx.x; b < b1; b += blockDim.x) {
+    float gf[F];
+    if (!level_grad<F, MODE>(c, g, lay, b, l, lr, gf)) continue;
+    float pos[3], p[3];
+    sample_position(src, b, pos);
+    normalize_pos(c, pos, p);
     const LevelCell lc = level_cell(c.res[l], p);
-    const uint32_t mask = c.mask[l], off = c.offset[l];
-    uint32_t fb[8];
-    V val[8];
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) atomicAdd(&hist[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
+  }
+  __syncthreads();
+  const int rel0 = grp.bucket_rel[l - grp.level0];
+  for (int j = threadIdx.x; j < nbl; j += blockDim.x) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
+}
+
+template <int F, int MODE>
+__global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
+                                                  const float* __restrict__ g, FeatLayout lay, float lr,
+                                                  const uint32_t* __restrict__ off, uint16_t* __restrict__ pair_idx,
+                                                  float* __restrict__ pair_val) {
+  typedef typename FVec<F>::T V;
+  extern __shared__ uint32_t cursor[];
+  const int l = grp.level0 + (int)blockIdx.y;
+  const int nbl = grp.nbl[l - grp.level0];
+  const int chunk = blockIdx.x;
+  const int rel0 = grp.bucket_rel[l - grp.level0];
+  for (int j = threadIdx.x; j < nbl; j += blockDim.x) cursor[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
+  __syncthreads();
+  const uint32_t be_mask = (1u << grp.log2_be) - 1u;
+  const int64_t b0 = (int64_t)chunk * grp.chunk;
+  const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
+  V* vals = reinterpret_cast<V*>(pair_val);
+  for (int64_t b = b0 + threadIdx.x; b < b1; b += blockDim.x) {
+    float gf[F];
+    if (!level_grad<F, MODE>(c, g, lay, b, l, lr, gf)) continue;
+    float pos[3], p[3];
+    sample_position(src, b, pos);
+    normalize_pos(c, pos, p);
+    const LevelCell lc = level_cell(c.res[l], p);
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) {
-      fb[cc] = (off + corner_entry(lc, cc, l, mask)) * (uint32_t)F;
-      val[cc] = *reinterpret_cast<const V*>(table + fb[cc]);
-    }
-    float acc[F];
-#pragma unroll
-    for (int f = 0; f < F; ++f) acc[f] = 0.0f;
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
+      const uint32_t e = corner_entry(lc, cc, l, c.mask[l]);
+      const uint32_t slot = atomicAdd(&cursor[e >> grp.log2_be], 1u);
       const float w = corner_weight(lc, cc);
-      float t[F];
-      FVec<F>::unpack(val[cc], t);
+      float v[F];
 #pragma unroll
-      for (int f = 0; f < F; ++f) acc[f] += w * t[f];
-    }
-#pragma unroll
-    for (int f = 0; f < F; ++f) out[l * F + f] = acc[f];
-    if (idx_out) {
-#pragma unroll
-      for (int cc = 0; cc < 8; ++cc) idx_out[(b * L + l) * 8 + cc] = fb[cc];
+      for (int f = 0; f < F; ++f) v[f] = gf[f] * w;
+      pair_idx[slot] = (uint16_t)(e & be_mask);
+      vals[slot] = FVec<F>::pack(v);
     }
   }
 }
 
 template <int F, int MODE>
-__global__ __launch_bounds__(256) void k_hash_bwd(DevCfg c, const float* __restrict__ x,
-                                                  const float4* __restrict__ rays, const float* __restrict__ Ts,
-                                                  int log2S, int64_t n, const float* __restrict__ g,
-                                                  float* __restrict__ dst, float lr) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= n) return;
-  float pos[3], p[3];
-  sample_position(x, rays, Ts, log2S, b, pos);
-  normalize_pos(c, pos, p);
-  const int L = c.L, LF = c.LF;
-  const float* gin = g + b * LF;
-  for (int l = 0; l < L; ++l) {
-    float gf[F];
-    bool any = false;
+__global__ __launch_bounds__(256) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ off,
+                                                    const uint16_t* __restrict__ pair_idx,
+                                                    const float* __restrict__ pair_val, BinApply ap) {
+  typedef typename FVec<F>::T V;
+  extern __shared__ float acc[];
+  const int j = blockIdx.x;  // bucket, relative to the group
+  int li = 0;
+  while (li + 1 < grp.n_levels && j >= grp.bucket_rel[li + 1]) ++li;
+  const int l = grp.level0 + li;
+  const int be = 1 << grp.log2_be;
+  const uint32_t entry_lo = (uint32_t)(j - grp.bucket_rel[li]) << grp.log2_be;
+  const uint32_t level_T = c.mask[l] + 1u;
+  const int count = (int)((level_T - entry_lo) < (uint32_t)be ? (level_T - entry_lo) : (uint32_t)be);
+  for (int e = threadIdx.x; e < count * F; e += blockDim.x) acc[e] = 0.0f;
+  __syncthreads();
+  const uint32_t start = off[(int64_t)j * grp.nblk];
+  const uint32_t end = off[(int64_t)(j + 1) * grp.nblk];
+  const V* vals = reinterpret_cast<const V*>(pair_val);
+  for (uint32_t i = start + threadIdx.x; i < end; i += blockDim.x) {
+    const uint32_t e = pair_idx[i];
+    float v[F];
+    FVec<F>::unpack(vals[i], v);
 #pragma unroll
-    for (int f = 0; f < F; ++f) {
-      float v = gin[l * F + f];
-      // non-finite gradients are dropped (ffnerf_OG.cl:2162); exact zeros add nothing
-      if (!isfinite(v)) v = 0.0f;
-      if (MODE == 1) v = -(lr * c.lvl_lr_scale[l]) * 0.5f * v;
-      gf[f] = v;
-      any |= (v != 0.0f);
-    }
-    if (!any) continue;
-    const LevelCell lc = level_cell(c.res[l], p);
-    const uint32_t mask = c.mask[l], off = c.offset[l];
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-      const float w = corner_weight(lc, cc);
-      const uint32_t fb = (off + corner_entry(lc, cc, l, mask)) * (uint32_t)F;
-#pragma unroll
-      for (int f = 0; f < F; ++f)
-        if (gf[f] != 0.0f) unsafeAtomicAdd(dst + fb + f, gf[f] * w);
+    for (int f = 0; f < F; ++f) atomicAdd(&acc[e * F + f], v[f]);
+  }
+  __syncthreads();
+  const int64_t base = ((int64_t)c.offset[l] + entry_lo) * F;
+  for (int e = threadIdx.x; e < count * F; e += blockDim.x) {
+    const int64_t gi = base + e;
+    const float gsum = acc[e];
+    if (MODE == BIN_GRAD || MODE == BIN_SGD) {
+      ap.dst[gi] += gsum;
+    } else {
+      if (ap.g_tap) ap.g_tap[gi] = gsum;
+      float pp = ap.dst[gi], mm = ap.m[gi], vv = ap.v[gi];
+      float mi = fmaf(1.0f - ap.beta1, gsum, ap.beta1 * mm);
+      float vi = fmaf(1.0f - ap.beta2, gsum * gsum, ap.beta2 * vv);
+      pp = pp - ap.lr_t * (mi / (sqrtf(vi) + ap.eps));
+      ap.dst[gi] = pp;
+      ap.m[gi] = mi;
+      ap.v[gi] = vi;
     }
   }
 }
 
-hipError_t launch_hash_fwd(const DevCfg& c, const float* x, const float4* rays, const float* Ts, int log2S,
-                           int64_t n, const float* table, float* a0, uint32_t* idx_out, hipStream_t st) {
+// ---------------------------------------------------------------------------
+// exclusive scan of n uint32 (n + 1 outputs: the last one is the total)
+
+// in has n_in elements; out gets n elements (n >= n_in; the missing inputs count as 0)
+__global__ __launch_bounds__(1024) void k_scan_tiles(const uint32_t* __restrict__ in, int64_t n_in,
+                                                     uint32_t* __restrict__ out, int64_t n,
+                                                     uint32_t* __restrict__ tile_sums) {
+  __shared__ uint32_t wsum[16];
+  const int64_t base = (int64_t)blockIdx.x * 4096;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t v[4], s = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t i = base + tid * 4 + q;
+    v[q] = i < n_in ? in[i] : 0u;
+    s += v[q];
+  }
+  uint32_t incl = s;
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[wv] = incl;
+  __syncthreads();
+  uint32_t wpre = 0;
+  for (int k = 0; k < wv; ++k) wpre += wsum[k];
+  uint32_t run = wpre + incl - s;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t i = base + tid * 4 + q;
+    if (i < n) out[i] = run;
+    run += v[q];
+  }
+  if (tid == 1023) tile_sums[blockIdx.x] = wpre + incl;
+}
+
+__global__ __launch_bounds__(1024) void k_scan_sums(uint32_t* __restrict__ sums, int64_t n_tiles,
+                                                    uint32_t* __restrict__ total_out) {
+  __shared__ uint32_t wsum[16];
+  __shared__ uint32_t carry;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n_tiles; c0 += 1024) {
+    const int64_t i = c0 + tid;
+    const uint32_t s = i < n_tiles ? sums[i] : 0u;
+    uint32_t incl = s;
+    for (int d = 1; d < 64; d <<= 1) {
+      uint32_t o = __shfl_up(incl, d);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    uint32_t wpre = 0;
+    for (int k = 0; k < wv; ++k) wpre += wsum[k];
+    const uint32_t cbase = carry;
+    if (i < n_tiles) sums[i] = cbase + wpre + incl - s;
+    __syncthreads();
+    if (tid == 1023) carry = cbase + wpre + incl;
+    __syncthreads();
+  }
+  if (tid == 0) *total_out = carry;
+}
+
+__global__ __launch_bounds__(1024) void k_scan_add(uint32_t* __restrict__ out, int64_t n,
+                                                   const uint32_t* __restrict__ tile_pre) {
+  const int64_t base = (int64_t)blockIdx.x * 4096;
+  const uint32_t add = tile_pre[blockIdx.x];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t i = base + threadIdx.x * 4 + q;
+    if (i < n) out[i] += add;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+
+hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* table, float* a0,
+                           const FeatLayout& lay, uint32_t* idx_out, hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  const dim3 grid((unsigned)((n + 255) / 256), (unsigned)c.L), block(256);
   switch (c.F) {
-    case 1: hipLaunchKernelGGL(k_hash_fwd<1>, grid, block, 0, st, c, x, rays, Ts, log2S, n, table, a0, idx_out); break;
-    case 2: hipLaunchKernelGGL(k_hash_fwd<2>, grid, block, 0, st, c, x, rays, Ts, log2S, n, table, a0, idx_out); break;
-    case 4: hipLaunchKernelGGL(k_hash_fwd<4>, grid, block, 0, st, c, x, rays, Ts, log2S, n, table, a0, idx_out); break;
+    case 1: hipLaunchKernelGGL(k_hash_fwd<1>, grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
+    case 2: hipLaunchKernelGGL(k_hash_fwd<2>, grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
+    case 4: hipLaunchKernelGGL(k_hash_fwd<4>, grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-hipError_t launch_hash_bwd(const DevCfg& c, const float* x, const float4* rays, const float* Ts, int log2S,
-                           int64_t n, const float* g, float* dst, int mode, float lr, hipStream_t st) {
-  if (n <= 0) return hipSuccess;
-  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
-#define FFN_BWD(FV, MV) hipLaunchKernelGGL((k_hash_bwd<FV, MV>), grid, block, 0, st, c, x, rays, Ts, log2S, n, g, dst, lr)
-  if (mode == 0) {
-    switch (c.F) {
-      case 1: FFN_BWD(1, 0); break;
-      case 2: FFN_BWD(2, 0); break;
-      case 4: FFN_BWD(4, 0); break;
-      default: return hipErrorInvalidValue;
+BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
+  BinPlan p{};
+  p.log2_be = c.F == 4 ? 12 : 13;
+  p.chunk = 4096;
+  p.nblk = (int)((n + p.chunk - 1) / p.chunk);
+  const int64_t per_level_pairs = n * 8;
+  const int64_t pair_bytes = 2 + 4 * (int64_t)c.F;
+  int lg = (int)(pair_budget_bytes / (size_t)(per_level_pairs * pair_bytes));
+  // slot offsets are 32-bit: keep a group's pair count below 2^32
+  const int lg32 = (int)((((int64_t)1 << 32) - 1) / per_level_pairs);
+  if (lg > lg32) lg = lg32;
+  if (lg < 1) lg = 1;
+  if (lg > c.L) lg = c.L;
+  p.levels_per_group = lg;
+  int max_buckets = 0, max_nbl = 0;
+  for (int g0 = 0; g0 < c.L; g0 += lg) {
+    int nb = 0;
+    for (int l = g0; l < g0 + lg && l < c.L; ++l) {
+      const int nbl = (int)(((int64_t)c.mask[l] + 1 + (1 << p.log2_be) - 1) >> p.log2_be);
+      nb += nbl;
+      if (nbl > max_nbl) max_nbl = nbl;
     }
-  } else {
-    switch (c.F) {
-      case 1: FFN_BWD(1, 1); break;
-      case 2: FFN_BWD(2, 1); break;
-      case 4: FFN_BWD(4, 1); break;
-      default: return hipErrorInvalidValue;
-    }
+    if (nb > max_buckets) max_buckets = nb;
   }
-#undef FFN_BWD
+  p.max_buckets = max_buckets;
+  p.max_nbl = max_nbl;
+  p.max_pairs = per_level_pairs * lg;
+  p.cnt_elems = (int64_t)max_buckets * p.nblk + 1;
+  p.tiles = (p.cnt_elems + 4095) / 4096;
+  return p;
+}
+
+hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* g, const FeatLayout& lay,
+                           int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
+                           hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  for (int g0 = 0; g0 < c.L; g0 += plan.levels_per_group) {
+    BinGroup grp{};
+    grp.level0 = g0;
+    grp.n_levels = (g0 + plan.levels_per_group <= c.L) ? plan.levels_per_group : c.L - g0;
+    grp.log2_be = plan.log2_be;
+    grp.chunk = plan.chunk;
+    grp.nblk = plan.nblk;
+    int rel = 0;
+    for (int li = 0; li < grp.n_levels; ++li) {
+      const int l = g0 + li;
+      grp.nbl[li] = (int)(((int64_t)c.mask[l] + 1 + (1 << plan.log2_be) - 1) >> plan.log2_be);
+      grp.bucket_rel[li] = rel;
+      rel += grp.nbl[li];
+    }
+    grp.bucket_rel[grp.n_levels] = rel;
+    const int n_buckets = rel;
+    const int64_t n_cnt = (int64_t)n_buckets * plan.nblk;
+    int max_nbl = 0;
+    for (int li = 0; li < grp.n_levels; ++li) max_nbl = grp.nbl[li] > max_nbl ? grp.nbl[li] : max_nbl;
+    const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
+    const size_t lds_hist = sizeof(uint32_t) * (size_t)max_nbl;
+    const size_t lds_acc = sizeof(float) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
+#define FFN_BIN(FV, MV)                                                                                             \
+  do {                                                                                                              \
+    hipLaunchKernelGGL((k_bin_count<FV, MV>), grid_bl, dim3(256), lds_hist, st, c, src, n, grp, g, lay, lr,       \
+                       s.cnt);                                                                                      \
+    const int64_t tiles = (n_cnt + 1 + 4095) / 4096;                                                                \
+    hipLaunchKernelGGL(k_scan_tiles, dim3((unsigned)tiles), dim3(1024), 0, st, s.cnt, n_cnt, s.off, n_cnt + 1,     \
+                       s.sums);                                                                                     \
+    hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, st, s.sums, tiles, s.total);                           \
+    hipLaunchKernelGGL(k_scan_add, dim3((unsigned)tiles), dim3(1024), 0, st, s.off, n_cnt + 1, s.sums);            \
+    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(256), lds_hist, st, c, src, n, grp, g, lay, lr, s.off, \
+                       s.pair_idx, s.pair_val);                                                                     \
+    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(256), lds_acc, st, c, grp, s.off,  \
+                       s.pair_idx, s.pair_val, ap);                                                                 \
+  } while (0)
+#define FFN_BIN_F(MV)                  \
+  switch (c.F) {                       \
+    case 1: FFN_BIN(1, MV); break;     \
+    case 2: FFN_BIN(2, MV); break;     \
+    case 4: FFN_BIN(4, MV); break;     \
+    default: return hipErrorInvalidValue; \
+  }
+    // the scan writes n_cnt + 1 offsets: the last one is the group's pair total
+    if (mode == BIN_GRAD) {
+      FFN_BIN_F(BIN_GRAD)
+    } else if (mode == BIN_SGD) {
+      FFN_BIN_F(BIN_SGD)
+    } else {
+      FFN_BIN_F(BIN_ADAM)
+    }
+#undef FFN_BIN_F
+#undef FFN_BIN
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// level-major [L][N][F] <-> sample-major [N][L*F] copies (for taps)
+__global__ __launch_bounds__(256) void k_feat_relayout(const float* __restrict__ src, FeatLayout ls,
+                                                       float* __restrict__ dst, FeatLayout ld, int64_t n, int L,
+                                                       int F) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= n) return;
+  for (int l = 0; l < L; ++l)
+    for (int f = 0; f < F; ++f) dst[l * ld.stride_l + b * ld.stride_b + f] = src[l * ls.stride_l + b * ls.stride_b + f];
+}
+
+hipError_t launch_feat_relayout(const float* src, const FeatLayout& ls, float* dst, const FeatLayout& ld, int64_t n,
+                                int L, int F, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_feat_relayout, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, ls, dst, ld, n, L,
+                     F);
   return hipGetLastError();
 }
 

@@ -46,6 +46,22 @@ inline PackedLayout make_layout(int LF, int nd, int nc) {
   return p;
 }
 
+// where sample positions come from: x[n][3], or o + Ts[b] d of ray b >> log2S
+struct PosSrc {
+  const float* x;
+  const float4* rays;
+  const float* Ts;
+  int log2S;
+};
+
+// element (sample b, level l, feature f) of an encoding-shaped array is at
+// l * stride_l + b * stride_b + f: sample-major [N][L*F] or level-major [L][N][F]
+struct FeatLayout {
+  int64_t stride_l, stride_b;
+};
+inline FeatLayout sample_major(int L, int F) { return FeatLayout{F, (int64_t)L * F}; }
+inline FeatLayout level_major(int64_t n, int F) { return FeatLayout{n * F, F}; }
+
 struct MlpPtrs {
   const float* W[FFN_N_LAYERS];
   const float* b[FFN_N_LAYERS];
@@ -62,6 +78,7 @@ struct MlpArgs {
   const uint32_t* flags;
   const float* a0;
   float* dL_da0;
+  FeatLayout feat;  // layout of a0 and dL_da0
   float* partials;  // [gridDim.x][layout.total]
   const uint32_t* occ_in;
   uint32_t* occ_st;
@@ -79,16 +96,52 @@ struct MlpArgs {
   float* t_dLdc;
 };
 
+// bucketed backward scatter
+enum { BIN_GRAD = 0, BIN_SGD = 1, BIN_ADAM = 2 };
+
+struct BinGroup {
+  int level0, n_levels, log2_be, chunk, nblk;
+  int nbl[FFN_MAX_LEVELS];             // buckets of each level of the group
+  int bucket_rel[FFN_MAX_LEVELS + 1];  // first bucket of each level, relative to the group
+};
+
+struct BinPlan {
+  int log2_be, chunk, nblk, levels_per_group, max_buckets, max_nbl;
+  int64_t max_pairs, cnt_elems, tiles;
+};
+
+struct BinScratch {
+  uint32_t* cnt;       // [cnt_elems]
+  uint32_t* off;       // [cnt_elems]
+  uint32_t* sums;      // [tiles]
+  uint32_t* total;     // [1]
+  uint16_t* pair_idx;  // [max_pairs]
+  float* pair_val;     // [max_pairs * F]
+};
+
+struct BinApply {
+  float* dst;  // grad (BIN_GRAD), table (BIN_SGD, BIN_ADAM)
+  float* m;
+  float* v;
+  float* g_tap;  // optional: the summed table gradient (BIN_ADAM)
+  float lr_t, beta1, beta2, eps;
+};
+
+BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes);
+
 hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays, int S, uint32_t seed,
                          const uint32_t* occ_in, int do_train, float* Ts, float* DTs, uint32_t* flags,
                          hipStream_t st);
 
-// positions either x[n][3] (rays == nullptr) or o + Ts[b] d of ray b >> log2S
-hipError_t launch_hash_fwd(const DevCfg& c, const float* x, const float4* rays, const float* Ts, int log2S,
-                           int64_t n, const float* table, float* a0, uint32_t* idx_out, hipStream_t st);
-// mode 0: grad[...] += g*w ; mode 1: table[...] += (-lr*scale_l*0.5*g)*w (reference SGD)
-hipError_t launch_hash_bwd(const DevCfg& c, const float* x, const float4* rays, const float* Ts, int log2S,
-                           int64_t n, const float* g, float* dst, int mode, float lr, hipStream_t st);
+hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* table, float* a0,
+                           const FeatLayout& lay, uint32_t* idx_out, hipStream_t st);
+// BIN_GRAD: dst += scatter(g); BIN_SGD: table += scatter(-lr 2^(-0.1 l) 0.5 g) (reference SGD);
+// BIN_ADAM: Adam on the table with the scattered gradient
+hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* g, const FeatLayout& lay,
+                           int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
+                           hipStream_t st);
+hipError_t launch_feat_relayout(const float* src, const FeatLayout& ls, float* dst, const FeatLayout& ld, int64_t n,
+                                int L, int F, hipStream_t st);
 
 hipError_t launch_adam(float* p, float* m, float* v, float* g, int64_t n, float lr_t, float b1, float b2, float eps,
                        int zero_grad, hipStream_t st);

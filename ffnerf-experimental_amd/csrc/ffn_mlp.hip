@@ -177,7 +177,7 @@ __device__ __forceinline__ void layer_grad(float* __restrict__ sx, float* __rest
   accum_dW(gW, gB, out_dim, in_dim, dop, aop, g, s);
 }
 
-template <int LF, int ND, int NC>
+template <int LF, int ND, int NC, int FEAT>
 __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
   using A = Arch<LF, ND, NC>;
   constexpr int KA = LF / 4;  // a0 values per lane (k-steps of the first layer)
@@ -228,12 +228,23 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     const int64_t ray = valid ? (b >> log2S) : 0;
     float a0r[KA];
     if (valid) {
-      const floatx4* src = reinterpret_cast<const floatx4*>(a.a0 + b * LF + KA * g);
+      // a0r[kk] = encoding neuron KA*g + kk (= level n / F, feature n % F) of sample b
+      if constexpr (FEAT >= 2 && KA % 2 == 0) {
 #pragma unroll
-      for (int q = 0; q < KA / 4; ++q) {
-        floatx4 v = src[q];
+        for (int kk = 0; kk < KA; kk += 2) {
+          const int nn = KA * g + kk;
+          const int l = nn / FEAT, f = nn - l * FEAT;
+          const float2 v = *reinterpret_cast<const float2*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b + f);
+          a0r[kk] = v.x;
+          a0r[kk + 1] = v.y;
+        }
+      } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) a0r[4 * q + r] = v[r];
+        for (int kk = 0; kk < KA; ++kk) {
+          const int nn = KA * g + kk;
+          const int l = nn / FEAT, f = nn - l * FEAT;
+          a0r[kk] = a.a0[l * a.feat.stride_l + b * a.feat.stride_b + f];
+        }
       }
     } else {
 #pragma unroll
@@ -572,8 +583,20 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
       bwd_tiles<LF / 16, 4>(sW + A::w_off(FFN_WD_IN), A::pitch(FFN_WD_IN), dd[0], ga, g, s);
       if (valid) {
 #pragma unroll
-        for (int t = 0; t < LF / 16; ++t)
-          *reinterpret_cast<floatx4*>(a.dL_da0 + b * LF + 16 * t + 4 * g) = ga[t];
+        for (int t = 0; t < LF / 16; ++t) {
+#pragma unroll
+          for (int r = 0; r < 4; r += 2) {  // neurons 16t+4g+r, r+1: one level when F >= 2
+            const int nn = 16 * t + 4 * g + r;
+            const int l = nn / FEAT, f = nn - l * FEAT;
+            float* dst = a.dL_da0 + l * a.feat.stride_l + b * a.feat.stride_b + f;
+            if constexpr (FEAT >= 2) {
+              *reinterpret_cast<float2*>(dst) = make_float2(ga[t][r], ga[t][r + 1]);
+            } else {
+              dst[0] = ga[t][r];
+              a.dL_da0[(l + 1) * a.feat.stride_l + b * a.feat.stride_b] = ga[t][r + 1];
+            }
+          }
+        }
       }
     }
     // first-layer weight gradient: a0 is held with the permuted neuron order
@@ -601,19 +624,29 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC>
-static hipError_t launch_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
+template <int LF, int ND, int NC, int FEAT>
+static hipError_t launch_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch<LF, ND, NC>;
   const size_t lds = sizeof(float) * (size_t)A::lds_floats();
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp<LF, ND, NC>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
+}
+
+template <int LF, int ND, int NC>
+static hipError_t launch_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
+  switch (a.c.F) {
+    case 1: return launch_f<LF, ND, NC, 1>(a, n_blocks, st);
+    case 2: return launch_f<LF, ND, NC, 2>(a, n_blocks, st);
+    case 4: return launch_f<LF, ND, NC, 4>(a, n_blocks, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 #define FFN_MLP_CONFIGS(X) \
