@@ -164,15 +164,27 @@ def _compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
         assert _rel(tg_["g" + wn], to_["g" + wn]) < 1e-3, wn
         assert _rel(tg_["g" + bn], to_["g" + bn]) < 1e-3, bn
     if "g_table" in to_:
-        assert _rel(tg_["g_table"], to_["g_table"]) < 1e-3
+        # table gradient = scatter of dL/da0: inherits the rare ReLU-boundary samples
+        _per_sample_close(tg_["g_table"], to_["g_table"])
     if check_params:
         sg, so = m.state(), o.p
         for k in list(layer_shapes(spec)) + ["table"]:
             d_g = sg[k].astype(np.float64) - p[k]
             d_o = so[k].astype(np.float64) - p[k]
-            big = np.abs(d_o) > 1e-3 * np.abs(d_o).max()
-            # Adam's first step is sign-like: compare where the update is not vanishing
-            assert np.allclose(d_g[big], d_o[big], rtol=1e-3, atol=1e-3 * np.abs(d_o).max()), k
+            ulp = np.spacing(np.abs(p[k]).astype(np.float32)).astype(np.float64)
+            adam = k != "table" or spec.get("hash_opt", 0) == 1
+            if adam:
+                # Adam's first step is sign-like (|update| ~ lr): compare where the gradient is well
+                # determined; an entry fed mostly by a ReLU-boundary sample may legitimately flip.
+                g = to_["g_table"] if k == "table" else to_["g" + k]
+                sel = np.abs(g) > 1e-3 * np.abs(g).max()
+            else:
+                sel = np.abs(d_o) > 1e-3 * np.abs(d_o).max()
+            # the GPU adds a bucket's summed update once, the oracle adds contributions one by one:
+            # p + delta may round differently by an ulp of p
+            err = np.abs(d_g[sel] - d_o[sel])
+            lim = 1e-3 * np.abs(d_o[sel]) + 1e-4 * np.abs(d_o).max() + 2 * ulp[sel]
+            assert (err <= lim).mean() > 0.999, (k, (err <= lim).mean())
         words_same = np.mean(sg["occ_st"] == so["occ_st"])
         assert words_same > 0.995, words_same
         assert np.array_equal(sg["occ_in"], so["occ_in"])
