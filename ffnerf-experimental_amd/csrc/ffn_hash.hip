@@ -164,48 +164,110 @@ __global__ __launch_bounds__(256) void k_bin_count(DevCfg c, PosSrc src, int64_t
   for (int j = threadIdx.x; j < nbl; j += blockDim.x) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
 }
 
+// Block-wide exclusive scan of cnt[0..n) into off[0..n) (256 threads; n may exceed 256).
+__device__ __forceinline__ uint32_t block_scan_excl(const uint32_t* cnt, uint32_t* off, int n, uint32_t* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int per = (n + 255) / 256;
+  const int j0 = tid * per;
+  uint32_t s = 0;
+  for (int j = j0; j < j0 + per && j < n; ++j) s += cnt[j];
+  uint32_t incl = s;
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[wv] = incl;
+  __syncthreads();
+  uint32_t run = incl - s;
+  for (int k = 0; k < wv; ++k) run += wsum[k];
+  const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  for (int j = j0; j < j0 + per && j < n; ++j) {
+    off[j] = run;
+    run += cnt[j];
+  }
+  return total;
+}
+
+// Emit the (entry, value) pairs of 256 samples at a time: rank them by bucket
+// in LDS (a local counting sort), then copy each bucket's run to its slots
+// with consecutive lanes on consecutive addresses.
 template <int F, int MODE>
 __global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                   const float* __restrict__ g, FeatLayout lay, float lr,
                                                   const uint32_t* __restrict__ off, uint16_t* __restrict__ pair_idx,
                                                   float* __restrict__ pair_val) {
   typedef typename FVec<F>::T V;
-  extern __shared__ uint32_t cursor[];
+  extern __shared__ uint32_t sm[];
   const int l = grp.level0 + (int)blockIdx.y;
   const int nbl = grp.nbl[l - grp.level0];
   const int chunk = blockIdx.x;
   const int rel0 = grp.bucket_rel[l - grp.level0];
-  for (int j = threadIdx.x; j < nbl; j += blockDim.x) cursor[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
-  __syncthreads();
+  uint32_t* gcur = sm;             // [nbl] next global slot of each bucket
+  uint32_t* lcnt = gcur + nbl;     // [nbl] pairs of the round per bucket
+  uint32_t* loff = lcnt + nbl;     // [nbl] their offsets in the stage
+  uint32_t* wsum = loff + nbl;     // [4]
+  // the stage starts 16-byte aligned: (3 nbl + 4) header words rounded up to a multiple of 4
+  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + ((3 * nbl + 4 + 3) & ~3));  // [2048]
+  uint16_t* st_bkt = st_idx + 2048;                          // [2048]
+  V* st_val = reinterpret_cast<V*>(st_bkt + 2048);           // [2048]
+  const int tid = threadIdx.x;
+  for (int j = tid; j < nbl; j += 256) gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
-  const int64_t b0 = (int64_t)chunk * grp.chunk;
-  const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
   V* vals = reinterpret_cast<V*>(pair_val);
-  for (int64_t b = b0 + threadIdx.x; b < b1; b += blockDim.x) {
+  const int64_t b_begin = (int64_t)chunk * grp.chunk;
+  const int64_t b_end = b_begin + grp.chunk < n ? b_begin + grp.chunk : n;
+  for (int64_t rb = b_begin; rb < b_end; rb += 256) {
+    for (int j = tid; j < nbl; j += 256) lcnt[j] = 0u;
+    __syncthreads();
+    const int64_t b = rb + tid;
     float gf[F];
-    if (!level_grad<F, MODE>(c, g, lay, b, l, lr, gf)) continue;
-    float pos[3], p[3];
-    sample_position(src, b, pos);
-    normalize_pos(c, pos, p);
-    const LevelCell lc = level_cell(c.res[l], p);
+    bool act = b < b_end && level_grad<F, MODE>(c, g, lay, b, l, lr, gf);
+    uint32_t ent[8], rank[8];
+    LevelCell lc;
+    if (act) {
+      float pos[3], p[3];
+      sample_position(src, b, pos);
+      normalize_pos(c, pos, p);
+      lc = level_cell(c.res[l], p);
 #pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-      const uint32_t e = corner_entry(lc, cc, l, c.mask[l]);
-      const uint32_t slot = atomicAdd(&cursor[e >> grp.log2_be], 1u);
-      const float w = corner_weight(lc, cc);
-      float v[F];
-#pragma unroll
-      for (int f = 0; f < F; ++f) v[f] = gf[f] * w;
-      pair_idx[slot] = (uint16_t)(e & be_mask);
-      vals[slot] = FVec<F>::pack(v);
+      for (int cc = 0; cc < 8; ++cc) {
+        ent[cc] = corner_entry(lc, cc, l, c.mask[l]);
+        rank[cc] = atomicAdd(&lcnt[ent[cc] >> grp.log2_be], 1u);
+      }
     }
+    __syncthreads();
+    const uint32_t total = block_scan_excl(lcnt, loff, nbl, wsum);
+    __syncthreads();
+    if (act) {
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {
+        const uint32_t bk = ent[cc] >> grp.log2_be;
+        const uint32_t pos = loff[bk] + rank[cc];
+        const float w = corner_weight(lc, cc);
+        float v[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) v[f] = gf[f] * w;
+        st_idx[pos] = (uint16_t)(ent[cc] & be_mask);
+        st_bkt[pos] = (uint16_t)bk;
+        st_val[pos] = FVec<F>::pack(v);
+      }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < total; i += 256) {
+      const uint32_t bk = st_bkt[i];
+      const uint32_t dst = gcur[bk] + (i - loff[bk]);
+      pair_idx[dst] = st_idx[i];
+      vals[dst] = st_val[i];
+    }
+    __syncthreads();
+    for (int j = tid; j < nbl; j += 256) gcur[j] += lcnt[j];
   }
 }
 
 template <int F, int MODE>
-__global__ __launch_bounds__(256) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ off,
-                                                    const uint16_t* __restrict__ pair_idx,
-                                                    const float* __restrict__ pair_val, BinApply ap) {
+__global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ off,
+                                                     const uint16_t* __restrict__ pair_idx,
+                                                     const float* __restrict__ pair_val, BinApply ap) {
   typedef typename FVec<F>::T V;
   extern __shared__ float acc[];
   const int j = blockIdx.x;  // bucket, relative to the group
@@ -216,21 +278,45 @@ __global__ __launch_bounds__(256) void k_bin_reduce(DevCfg c, BinGroup grp, cons
   const uint32_t entry_lo = (uint32_t)(j - grp.bucket_rel[li]) << grp.log2_be;
   const uint32_t level_T = c.mask[l] + 1u;
   const int count = (int)((level_T - entry_lo) < (uint32_t)be ? (level_T - entry_lo) : (uint32_t)be);
-  for (int e = threadIdx.x; e < count * F; e += blockDim.x) acc[e] = 0.0f;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < count * F; e += 1024) acc[e] = 0.0f;
   __syncthreads();
   const uint32_t start = off[(int64_t)j * grp.nblk];
   const uint32_t end = off[(int64_t)(j + 1) * grp.nblk];
   const V* vals = reinterpret_cast<const V*>(pair_val);
-  for (uint32_t i = start + threadIdx.x; i < end; i += blockDim.x) {
+  // head up to a multiple of 4, then 4 pairs per thread per step, then the tail
+  const uint32_t body0 = (start + 3u) & ~3u;
+  const uint32_t body1 = end & ~3u;
+  auto add1 = [&](uint32_t i) {
     const uint32_t e = pair_idx[i];
     float v[F];
     FVec<F>::unpack(vals[i], v);
 #pragma unroll
     for (int f = 0; f < F; ++f) atomicAdd(&acc[e * F + f], v[f]);
+  };
+  if (body0 >= body1) {
+    for (uint32_t i = start + tid; i < end; i += 1024) add1(i);
+  } else {
+    if (start + tid < body0) add1(start + tid);
+    if (body1 + tid < end) add1(body1 + tid);
+    for (uint32_t i = body0 + 4u * tid; i < body1; i += 4096u) {
+      const ushort4 e4 = *reinterpret_cast<const ushort4*>(pair_idx + i);
+      V v4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v4[q] = vals[i + q];
+      const uint32_t es[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v[F];
+        FVec<F>::unpack(v4[q], v);
+#pragma unroll
+        for (int f = 0; f < F; ++f) atomicAdd(&acc[es[q] * F + f], v[f]);
+      }
+    }
   }
   __syncthreads();
   const int64_t base = ((int64_t)c.offset[l] + entry_lo) * F;
-  for (int e = threadIdx.x; e < count * F; e += blockDim.x) {
+  for (int e = tid; e < count * F; e += 1024) {
     const int64_t gi = base + e;
     const float gsum = acc[e];
     if (MODE == BIN_GRAD || MODE == BIN_SGD) {
@@ -397,6 +483,8 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
     const size_t lds_hist = sizeof(uint32_t) * (size_t)max_nbl;
     const size_t lds_acc = sizeof(float) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
+    const size_t lds_emit =
+        sizeof(uint32_t) * ((3 * (size_t)max_nbl + 4 + 3) & ~(size_t)3) + 2048 * (4 + sizeof(float) * (size_t)c.F);
 #define FFN_BIN(FV, MV)                                                                                             \
   do {                                                                                                              \
     hipLaunchKernelGGL((k_bin_count<FV, MV>), grid_bl, dim3(256), lds_hist, st, c, src, n, grp, g, lay, lr,       \
@@ -406,9 +494,9 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                        s.sums);                                                                                     \
     hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, st, s.sums, tiles, s.total);                           \
     hipLaunchKernelGGL(k_scan_add, dim3((unsigned)tiles), dim3(1024), 0, st, s.off, n_cnt + 1, s.sums);            \
-    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(256), lds_hist, st, c, src, n, grp, g, lay, lr, s.off, \
+    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(256), lds_emit, st, c, src, n, grp, g, lay, lr, s.off, \
                        s.pair_idx, s.pair_val);                                                                     \
-    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(256), lds_acc, st, c, grp, s.off,  \
+    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp, s.off, \
                        s.pair_idx, s.pair_val, ap);                                                                 \
   } while (0)
 #define FFN_BIN_F(MV)                  \
