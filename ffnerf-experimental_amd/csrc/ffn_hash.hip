@@ -20,9 +20,15 @@
 //     3. emit   -- recompute the corners and write (entry-in-bucket, value)
 //                  pairs to the slots (LDS cursors, streaming writes);
 //     4. reduce -- one block per bucket sums its pairs into an LDS copy of
-//                  the bucket (ds_add_f32) and applies the update to its own
-//                  slice of the table: gradient add, the reference SGD, or
-//                  Adam.  No gradient table is materialised for Adam.
+//                  the bucket and applies the update to its own slice of the
+//                  table: gradient add, the reference SGD, or Adam.  No
+//                  gradient table is materialised for Adam.
+//   LDS float atomics (ds_add_f32) sustain only ~0.33 lanes/clk/CU here while
+//   ds_add_u64 sustains ~4.9 (both measured), so the reduce accumulates in
+//   64-bit fixed point: the emit pass records each bucket's largest |value|
+//   (integer max on the float bits), and the reduce scales by the power of two
+//   that keeps the bucket's total below 2^62 -- an exact scaling, one
+//   round-to-nearest per pair, ~2^-34 of the bucket's largest value per entry.
 //   Levels are processed in groups so the pair buffer stays bounded.
 #include "ffn_device.h"
 #include "ffn_kernels.h"
@@ -140,11 +146,13 @@ __device__ __forceinline__ bool level_grad(const DevCfg& c, const float* __restr
 template <int F, int MODE>
 __global__ __launch_bounds__(256) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                    const float* __restrict__ g, FeatLayout lay, float lr,
-                                                   uint32_t* __restrict__ cnt) {
+                                                   uint32_t* __restrict__ cnt, uint32_t* __restrict__ bmax) {
   extern __shared__ uint32_t hist[];
   const int l = grp.level0 + (int)blockIdx.y;
   const int nbl = grp.nbl[l - grp.level0];
   const int chunk = blockIdx.x;
+  if (chunk == 0)
+    for (int j = threadIdx.x; j < nbl; j += blockDim.x) bmax[grp.bucket_rel[l - grp.level0] + j] = 0u;
   for (int j = threadIdx.x; j < nbl; j += blockDim.x) hist[j] = 0u;
   __syncthreads();
   const int64_t b0 = (int64_t)chunk * grp.chunk;
@@ -195,7 +203,7 @@ template <int F, int MODE>
 __global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                   const float* __restrict__ g, FeatLayout lay, float lr,
                                                   const uint32_t* __restrict__ off, uint16_t* __restrict__ pair_idx,
-                                                  float* __restrict__ pair_val) {
+                                                  float* __restrict__ pair_val, uint32_t* __restrict__ bmax) {
   typedef typename FVec<F>::T V;
   extern __shared__ uint32_t sm[];
   const int l = grp.level0 + (int)blockIdx.y;
@@ -205,13 +213,17 @@ __global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t 
   uint32_t* gcur = sm;             // [nbl] next global slot of each bucket
   uint32_t* lcnt = gcur + nbl;     // [nbl] pairs of the round per bucket
   uint32_t* loff = lcnt + nbl;     // [nbl] their offsets in the stage
-  uint32_t* wsum = loff + nbl;     // [4]
-  // the stage starts 16-byte aligned: (3 nbl + 4) header words rounded up to a multiple of 4
-  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + ((3 * nbl + 4 + 3) & ~3));  // [2048]
+  uint32_t* lmax = loff + nbl;     // [nbl] float bits of the largest |value| per bucket
+  uint32_t* wsum = lmax + nbl;     // [4]
+  // the stage starts 16-byte aligned: (4 nbl + 4) header words rounded up to a multiple of 4
+  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + ((4 * nbl + 4 + 3) & ~3));  // [2048]
   uint16_t* st_bkt = st_idx + 2048;                          // [2048]
   V* st_val = reinterpret_cast<V*>(st_bkt + 2048);           // [2048]
   const int tid = threadIdx.x;
-  for (int j = tid; j < nbl; j += 256) gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
+  for (int j = tid; j < nbl; j += 256) {
+    gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
+    lmax[j] = 0u;
+  }
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
   V* vals = reinterpret_cast<V*>(pair_val);
   const int64_t b_begin = (int64_t)chunk * grp.chunk;
@@ -245,11 +257,16 @@ __global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t 
         const uint32_t pos = loff[bk] + rank[cc];
         const float w = corner_weight(lc, cc);
         float v[F];
+        float amax = 0.0f;
 #pragma unroll
-        for (int f = 0; f < F; ++f) v[f] = gf[f] * w;
+        for (int f = 0; f < F; ++f) {
+          v[f] = gf[f] * w;
+          amax = fmaxf(amax, fabsf(v[f]));
+        }
         st_idx[pos] = (uint16_t)(ent[cc] & be_mask);
         st_bkt[pos] = (uint16_t)bk;
         st_val[pos] = FVec<F>::pack(v);
+        atomicMax(&lmax[bk], __float_as_uint(amax));
       }
     }
     __syncthreads();
@@ -262,14 +279,18 @@ __global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t 
     __syncthreads();
     for (int j = tid; j < nbl; j += 256) gcur[j] += lcnt[j];
   }
+  __syncthreads();
+  for (int j = tid; j < nbl; j += 256)
+    if (lmax[j]) atomicMax(&bmax[rel0 + j], lmax[j]);
 }
 
 template <int F, int MODE>
 __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ off,
                                                      const uint16_t* __restrict__ pair_idx,
-                                                     const float* __restrict__ pair_val, BinApply ap) {
+                                                     const float* __restrict__ pair_val,
+                                                     const uint32_t* __restrict__ bmax, BinApply ap) {
   typedef typename FVec<F>::T V;
-  extern __shared__ float acc[];
+  extern __shared__ unsigned long long acc[];
   const int j = blockIdx.x;  // bucket, relative to the group
   int li = 0;
   while (li + 1 < grp.n_levels && j >= grp.bucket_rel[li + 1]) ++li;
@@ -279,46 +300,75 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   const uint32_t level_T = c.mask[l] + 1u;
   const int count = (int)((level_T - entry_lo) < (uint32_t)be ? (level_T - entry_lo) : (uint32_t)be);
   const int tid = threadIdx.x;
-  for (int e = tid; e < count * F; e += 1024) acc[e] = 0.0f;
+  for (int e = tid; e < count * F; e += 1024) acc[e] = 0ull;
   __syncthreads();
   const uint32_t start = off[(int64_t)j * grp.nblk];
   const uint32_t end = off[(int64_t)(j + 1) * grp.nblk];
+  // fixed-point scale 2^k with (pairs + 1) * max|v| * 2^k < 2^62: no partial sum can overflow
+  const float mx = __uint_as_float(bmax[j]);
+  int k = 0;
+  if (mx > 0.0f) {
+    int e_mx, e_n;
+    frexpf(mx, &e_mx);                       // mx < 2^e_mx
+    frexp((double)(end - start) + 1.0, &e_n);  // pairs + 1 <= 2^e_n
+    k = 62 - e_mx - e_n;
+  }
+  const double scale = ldexp(1.0, k);
   const V* vals = reinterpret_cast<const V*>(pair_val);
-  // head up to a multiple of 4, then 4 pairs per thread per step, then the tail
-  const uint32_t body0 = (start + 3u) & ~3u;
-  const uint32_t body1 = end & ~3u;
+  auto q = [&](float v) -> unsigned long long { return (unsigned long long)__double2ll_rn((double)v * scale); };
   auto add1 = [&](uint32_t i) {
     const uint32_t e = pair_idx[i];
     float v[F];
     FVec<F>::unpack(vals[i], v);
 #pragma unroll
-    for (int f = 0; f < F; ++f) atomicAdd(&acc[e * F + f], v[f]);
+    for (int f = 0; f < F; ++f) atomicAdd(&acc[e * F + f], q(v[f]));
   };
-  if (body0 >= body1) {
-    for (uint32_t i = start + tid; i < end; i += 1024) add1(i);
-  } else {
-    if (start + tid < body0) add1(start + tid);
-    if (body1 + tid < end) add1(body1 + tid);
-    for (uint32_t i = body0 + 4u * tid; i < body1; i += 4096u) {
-      const ushort4 e4 = *reinterpret_cast<const ushort4*>(pair_idx + i);
-      V v4[4];
+  if (mx > 0.0f) {
+    if constexpr (F == 2) {
+      // two pairs per 16-byte load; a block step covers 4 rows of 2048 pairs and every thread issues its
+      // 8 loads before its 16 LDS adds (each wave load reads 1 KiB / 256 B of contiguous memory)
+      const uint32_t even0 = (start + 1u) & ~1u;
+      if (start < even0 && start < end && tid == 0) add1(start);
+      uint32_t i = even0;
+      for (; i + 8192u <= end; i += 8192u) {
+        uint32_t e2[4];
+        float4 v4[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) v4[q] = vals[i + q];
-      const uint32_t es[4] = {e4.x, e4.y, e4.z, e4.w};
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t kk = i + (uint32_t)r * 2048u + 2u * (uint32_t)tid;
+          e2[r] = *reinterpret_cast<const uint32_t*>(pair_idx + kk);
+          v4[r] = *reinterpret_cast<const float4*>(pair_val + 2 * (size_t)kk);
+        }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float v[F];
-        FVec<F>::unpack(v4[q], v);
-#pragma unroll
-        for (int f = 0; f < F; ++f) atomicAdd(&acc[es[q] * F + f], v[f]);
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t ea = e2[r] & 0xFFFFu, eb = e2[r] >> 16;
+          atomicAdd(&acc[2 * ea], q(v4[r].x));
+          atomicAdd(&acc[2 * ea + 1], q(v4[r].y));
+          atomicAdd(&acc[2 * eb], q(v4[r].z));
+          atomicAdd(&acc[2 * eb + 1], q(v4[r].w));
+        }
       }
+      if (i < end) {
+        for (uint32_t kk = i + 2u * (uint32_t)tid; kk + 1u < end; kk += 2048u) {
+          const uint32_t e2 = *reinterpret_cast<const uint32_t*>(pair_idx + kk);
+          const float4 v = *reinterpret_cast<const float4*>(pair_val + 2 * (size_t)kk);
+          atomicAdd(&acc[2 * (e2 & 0xFFFFu)], q(v.x));
+          atomicAdd(&acc[2 * (e2 & 0xFFFFu) + 1], q(v.y));
+          atomicAdd(&acc[2 * (e2 >> 16)], q(v.z));
+          atomicAdd(&acc[2 * (e2 >> 16) + 1], q(v.w));
+        }
+        if (((end - i) & 1u) && tid == 0) add1(end - 1u);
+      }
+    } else {
+      for (uint32_t i = start + tid; i < end; i += 1024) add1(i);
     }
   }
   __syncthreads();
+  const double inv = ldexp(1.0, -k);
   const int64_t base = ((int64_t)c.offset[l] + entry_lo) * F;
   for (int e = tid; e < count * F; e += 1024) {
     const int64_t gi = base + e;
-    const float gsum = acc[e];
+    const float gsum = (float)((double)(long long)acc[e] * inv);
     if (MODE == BIN_GRAD || MODE == BIN_SGD) {
       ap.dst[gi] += gsum;
     } else {
@@ -427,7 +477,8 @@ hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
 
 BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   BinPlan p{};
-  p.log2_be = c.F == 4 ? 12 : 13;
+  // int64 LDS accumulator of one bucket: 2^log2_be * F * 8 bytes = 64 KiB
+  p.log2_be = c.F == 4 ? 11 : (c.F == 2 ? 12 : 13);
   p.chunk = 4096;
   p.nblk = (int)((n + p.chunk - 1) / p.chunk);
   const int64_t per_level_pairs = n * 8;
@@ -482,22 +533,22 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     for (int li = 0; li < grp.n_levels; ++li) max_nbl = grp.nbl[li] > max_nbl ? grp.nbl[li] : max_nbl;
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
     const size_t lds_hist = sizeof(uint32_t) * (size_t)max_nbl;
-    const size_t lds_acc = sizeof(float) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
+    const size_t lds_acc = sizeof(unsigned long long) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
     const size_t lds_emit =
-        sizeof(uint32_t) * ((3 * (size_t)max_nbl + 4 + 3) & ~(size_t)3) + 2048 * (4 + sizeof(float) * (size_t)c.F);
+        sizeof(uint32_t) * ((4 * (size_t)max_nbl + 4 + 3) & ~(size_t)3) + 2048 * (4 + sizeof(float) * (size_t)c.F);
 #define FFN_BIN(FV, MV)                                                                                             \
   do {                                                                                                              \
     hipLaunchKernelGGL((k_bin_count<FV, MV>), grid_bl, dim3(256), lds_hist, st, c, src, n, grp, g, lay, lr,       \
-                       s.cnt);                                                                                      \
+                       s.cnt, s.bmax);                                                                              \
     const int64_t tiles = (n_cnt + 1 + 4095) / 4096;                                                                \
     hipLaunchKernelGGL(k_scan_tiles, dim3((unsigned)tiles), dim3(1024), 0, st, s.cnt, n_cnt, s.off, n_cnt + 1,     \
                        s.sums);                                                                                     \
     hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, st, s.sums, tiles, s.total);                           \
     hipLaunchKernelGGL(k_scan_add, dim3((unsigned)tiles), dim3(1024), 0, st, s.off, n_cnt + 1, s.sums);            \
     hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(256), lds_emit, st, c, src, n, grp, g, lay, lr, s.off, \
-                       s.pair_idx, s.pair_val);                                                                     \
+                       s.pair_idx, s.pair_val, s.bmax);                                                             \
     hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp, s.off, \
-                       s.pair_idx, s.pair_val, ap);                                                                 \
+                       s.pair_idx, s.pair_val, s.bmax, ap);                                                         \
   } while (0)
 #define FFN_BIN_F(MV)                  \
   switch (c.F) {                       \
