@@ -71,25 +71,31 @@ struct Arch {
   static constexpr int lds_floats() { return w_total() + g_total() + 4 * x_per_wave + comp_floats; }
 };
 
-// out tiles (D layout) = act(W . in + b), in given as D-layout tiles
+// out tiles (D layout) = act(W . in + b), in given as D-layout tiles.  The
+// output tiles are interleaved inside each k-step so consecutive MFMAs are
+// independent.
 template <int OT, int IT>
 __device__ __forceinline__ void fwd_tiles(const float* __restrict__ W, const float* __restrict__ B, int P,
                                           const floatx4 (&in)[IT], floatx4 (&out)[OT], int g, int s, bool relu) {
+  floatx4 acc[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = B[16 * t + 4 * g + r];
+  const float* wrow = W + s * P + 4 * g;
+#pragma unroll
+  for (int tp = 0; tp < IT; ++tp)
+#pragma unroll
+    for (int rp = 0; rp < 4; ++rp)
+#pragma unroll
+      for (int t = 0; t < OT; ++t) acc[t] = mfma4(wrow[16 * t * P + 16 * tp + rp], in[tp][rp], acc[t]);
 #pragma unroll
   for (int t = 0; t < OT; ++t) {
-    floatx4 acc;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
-    const float* wrow = W + (16 * t + s) * P + 4 * g;
-#pragma unroll
-    for (int tp = 0; tp < IT; ++tp)
-#pragma unroll
-      for (int rp = 0; rp < 4; ++rp) acc = mfma4(wrow[16 * tp + rp], in[tp][rp], acc);
     if (relu) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
+      for (int r = 0; r < 4; ++r) acc[t][r] = acc[t][r] > 0.0f ? acc[t][r] : 0.0f;
     }
-    out[t] = acc;
+    out[t] = acc[t];
   }
 }
 
@@ -98,14 +104,11 @@ template <int RT, int DT>
 __device__ __forceinline__ void bwd_tiles(const float* __restrict__ W, int P, const floatx4 (&delta)[DT],
                                           floatx4 (&res)[RT], int g, int s) {
 #pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    floatx4 acc = res[t];
+  for (int tp = 0; tp < DT; ++tp)
 #pragma unroll
-    for (int tp = 0; tp < DT; ++tp)
+    for (int rp = 0; rp < 4; ++rp)
 #pragma unroll
-      for (int rp = 0; rp < 4; ++rp) acc = mfma4(W[(16 * tp + 4 * g + rp) * P + 16 * t + s], delta[tp][rp], acc);
-    res[t] = acc;
-  }
+      for (int t = 0; t < RT; ++t) res[t] = mfma4(W[(16 * tp + 4 * g + rp) * P + 16 * t + s], delta[tp][rp], res[t]);
 }
 
 template <int NT>
@@ -161,6 +164,76 @@ __device__ __forceinline__ void accum_dW(float* __restrict__ gW, float* __restri
   }
 }
 
+// Weight-gradient accumulators of one layer held in registers (AGPRs) for all
+// the tiles a wavefront processes: w[T][Tp] is the D-layout 16x16 tile
+// (rows 16T + 4g + r, columns 16Tp + lane%16), b[T] a per-lane partial bias sum.
+template <int OT, int IT>
+struct GradAcc {
+  floatx4 w[OT][IT];
+  float b[OT];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int T = 0; T < OT; ++T) {
+      b[T] = 0.0f;
+#pragma unroll
+      for (int Tp = 0; Tp < IT; ++Tp) w[T][Tp] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  // dW += delta . act^T and db += delta over the wave's 16 samples (operands already transposed)
+  __device__ __forceinline__ void add(const floatx4 (&dop)[OT], const floatx4 (&aop)[IT]) {
+#pragma unroll
+    for (int T = 0; T < OT; ++T) b[T] += (dop[T][0] + dop[T][1]) + (dop[T][2] + dop[T][3]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int T = 0; T < OT; ++T)
+#pragma unroll
+        for (int Tp = 0; Tp < IT; ++Tp) w[T][Tp] = mfma4(dop[T][q], aop[Tp][q], w[T][Tp]);
+  }
+  // add this wavefront's sums into the block's LDS gradient (callers serialise the waves)
+  __device__ __forceinline__ void flush(float* __restrict__ gW, float* __restrict__ gB, int out_dim, int in_dim,
+                                        int g, int s) {
+#pragma unroll
+    for (int T = 0; T < OT; ++T) {
+      float bs = b[T];
+      bs += __shfl_xor(bs, 16);
+      bs += __shfl_xor(bs, 32);
+      if (g == 0 && 16 * T + s < out_dim) gB[16 * T + s] += bs;
+#pragma unroll
+      for (int Tp = 0; Tp < IT; ++Tp) {
+        const int col = 16 * Tp + s;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * T + 4 * g + r;
+          if (row < out_dim && col < in_dim) gW[row * in_dim + col] += w[T][Tp][r];
+        }
+      }
+    }
+  }
+};
+
+template <int OT, int IT>
+__device__ __forceinline__ void transpose_ops(float* __restrict__ sx, const floatx4 (&delta)[OT],
+                                              const floatx4 (&act)[IT], floatx4 (&dop)[OT], floatx4 (&aop)[IT],
+                                              int g, int s) {
+  stash_D(sx, delta, g, s);
+  wave_lds_sync();
+  load_op(sx, dop, g, s);
+  wave_lds_sync();
+  stash_D(sx, act, g, s);
+  wave_lds_sync();
+  load_op(sx, aop, g, s);
+  wave_lds_sync();
+}
+
+template <int OT, int IT>
+__device__ __forceinline__ void layer_grad_reg(float* __restrict__ sx, GradAcc<OT, IT>& acc,
+                                               const floatx4 (&delta)[OT], const floatx4 (&act)[IT], int g, int s) {
+  floatx4 dop[OT], aop[IT];
+  transpose_ops(sx, delta, act, dop, aop, g, s);
+  acc.add(dop, aop);
+}
+
 template <int OT, int IT>
 __device__ __forceinline__ void layer_grad(float* __restrict__ sx, float* __restrict__ gW, float* __restrict__ gB,
                                            int out_dim, int in_dim, const floatx4 (&delta)[OT],
@@ -176,6 +249,38 @@ __device__ __forceinline__ void layer_grad(float* __restrict__ sx, float* __rest
   wave_lds_sync();
   accum_dW(gW, gB, out_dim, in_dim, dop, aop, g, s);
 }
+
+// Register-resident gradient accumulators of every layer (used when they fit:
+// at most 48 16x16 tiles = 192 AGPRs per lane); otherwise the block
+// accumulates in LDS.
+template <int LF, int ND, int NC>
+constexpr int acc_tiles() {
+  return 4 + 16 * (NC - 1) + 8 + 4 + 16 * (ND - 1) + 4 * (LF / 16);
+}
+
+template <int LF, int ND, int NC, bool REG>
+struct AccSet {
+  __device__ __forceinline__ void zero() {}
+};
+template <int LF, int ND, int NC>
+struct AccSet<LF, ND, NC, true> {
+  GradAcc<1, 4> c_out;
+  GradAcc<4, 4> c_h[NC > 1 ? NC - 1 : 1];  // Wc_01, Wc_12, Wc_23
+  GradAcc<4, 2> c_in;
+  GradAcc<1, 4> d_out;
+  GradAcc<4, 4> d_h[ND > 1 ? ND - 1 : 1];  // Wd_01, Wd_12
+  GradAcc<4, LF / 16> d_in;
+  __device__ __forceinline__ void zero() {
+    c_out.zero();
+#pragma unroll
+    for (int i = 0; i < NC - 1; ++i) c_h[i].zero();
+    c_in.zero();
+    d_out.zero();
+#pragma unroll
+    for (int i = 0; i < ND - 1; ++i) d_h[i].zero();
+    d_in.zero();
+  }
+};
 
 template <int LF, int ND, int NC, int FEAT>
 __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
@@ -216,6 +321,10 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     const float dx = c.bmax[0] - c.bmin[0], dy = c.bmax[1] - c.bmin[1], dz = c.bmax[2] - c.bmin[2];
     Dhalf = 0.5f * sqrtf(dx * dx + dy * dy + dz * dz);
   }
+
+  constexpr bool REG_ACC = acc_tiles<LF, ND, NC>() <= 48;
+  AccSet<LF, ND, NC, REG_ACC> ga;
+  ga.zero();
 
   int parity = 0;
   for (int64_t tile = blockIdx.x; tile < a.n_tiles; tile += gridDim.x, parity ^= 1) {
@@ -527,31 +636,36 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     for (int t = 0; t < 4; ++t) dc[NC - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
     bwd_tiles<4, 1>(sW + A::w_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), dco, dc[NC - 1], g, s);
     relu_mask(dc[NC - 1], hc[NC - 1]);
-    layer_grad<1, 4>(sX, sG + A::g_off(FFN_WC_OUT), sG + A::gb_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, dco, hc[NC - 1],
-                     g, s);
+    if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_out, dco, hc[NC - 1], g, s);
+    else layer_grad<1, 4>(sX, sG + A::g_off(FFN_WC_OUT), sG + A::gb_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, dco,
+                          hc[NC - 1], g, s);
     if constexpr (NC >= 4) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) dc[2][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_23), A::pitch(FFN_WC_23), dc[3], dc[2], g, s);
       relu_mask(dc[2], hc[2]);
-      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_23), sG + A::gb_off(FFN_WC_23), FFN_M, FFN_M, dc[3], hc[2], g, s);
+      if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_h[2], dc[3], hc[2], g, s);
+      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_23), sG + A::gb_off(FFN_WC_23), FFN_M, FFN_M, dc[3], hc[2], g, s);
     }
     if constexpr (NC >= 3) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) dc[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_12), A::pitch(FFN_WC_12), dc[2], dc[1], g, s);
       relu_mask(dc[1], hc[1]);
-      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_12), sG + A::gb_off(FFN_WC_12), FFN_M, FFN_M, dc[2], hc[1], g, s);
+      if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_h[1], dc[2], hc[1], g, s);
+      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_12), sG + A::gb_off(FFN_WC_12), FFN_M, FFN_M, dc[2], hc[1], g, s);
     }
     if constexpr (NC >= 2) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) dc[0][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_01), A::pitch(FFN_WC_01), dc[1], dc[0], g, s);
       relu_mask(dc[0], hc[0]);
-      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_01), sG + A::gb_off(FFN_WC_01), FFN_M, FFN_M, dc[1], hc[0], g, s);
+      if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_h[0], dc[1], hc[0], g, s);
+      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_01), sG + A::gb_off(FFN_WC_01), FFN_M, FFN_M, dc[1], hc[0], g, s);
     }
     // color input layer: its gradient, and the dout part of its input delta
-    layer_grad<4, 2>(sX, sG + A::g_off(FFN_WC_IN), sG + A::gb_off(FFN_WC_IN), FFN_M, FFN_C_IN, dc[0], acin, g, s);
+    if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_in, dc[0], acin, g, s);
+    else layer_grad<4, 2>(sX, sG + A::g_off(FFN_WC_IN), sG + A::gb_off(FFN_WC_IN), FFN_M, FFN_C_IN, dc[0], acin, g, s);
     bwd_tiles<1, 4>(sW + A::w_off(FFN_WC_IN), A::pitch(FFN_WC_IN), dc[0], ddo, g, s);
     // density backward
     floatx4 dd[ND][4];
@@ -559,21 +673,24 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     for (int t = 0; t < 4; ++t) dd[ND - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
     bwd_tiles<4, 1>(sW + A::w_off(FFN_WD_OUT), A::pitch(FFN_WD_OUT), ddo, dd[ND - 1], g, s);
     relu_mask(dd[ND - 1], hd[ND - 1]);
-    layer_grad<1, 4>(sX, sG + A::g_off(FFN_WD_OUT), sG + A::gb_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, ddo, hd[ND - 1],
-                     g, s);
+    if constexpr (REG_ACC) layer_grad_reg(sX, ga.d_out, ddo, hd[ND - 1], g, s);
+    else layer_grad<1, 4>(sX, sG + A::g_off(FFN_WD_OUT), sG + A::gb_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, ddo,
+                          hd[ND - 1], g, s);
     if constexpr (ND >= 3) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) dd[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd_tiles<4, 4>(sW + A::w_off(FFN_WD_12), A::pitch(FFN_WD_12), dd[2], dd[1], g, s);
       relu_mask(dd[1], hd[1]);
-      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_12), sG + A::gb_off(FFN_WD_12), FFN_M, FFN_M, dd[2], hd[1], g, s);
+      if constexpr (REG_ACC) layer_grad_reg(sX, ga.d_h[1], dd[2], hd[1], g, s);
+      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_12), sG + A::gb_off(FFN_WD_12), FFN_M, FFN_M, dd[2], hd[1], g, s);
     }
     if constexpr (ND >= 2) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) dd[0][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd_tiles<4, 4>(sW + A::w_off(FFN_WD_01), A::pitch(FFN_WD_01), dd[1], dd[0], g, s);
       relu_mask(dd[0], hd[0]);
-      layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_01), sG + A::gb_off(FFN_WD_01), FFN_M, FFN_M, dd[1], hd[0], g, s);
+      if constexpr (REG_ACC) layer_grad_reg(sX, ga.d_h[0], dd[1], hd[0], g, s);
+      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_01), sG + A::gb_off(FFN_WD_01), FFN_M, FFN_M, dd[1], hd[0], g, s);
     }
     // encoding gradient dL/da0 = Wd_in^T . delta_d1 -> HBM for the hash scatter
     {
@@ -611,11 +728,29 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
       wave_lds_sync();
       load_op(sX, aop, g, s);
       wave_lds_sync();
-      accum_dW(sG + A::g_off(FFN_WD_IN), sG + A::gb_off(FFN_WD_IN), FFN_M, LF, dop, aop, g, s);
+      if constexpr (REG_ACC) ga.d_in.add(dop, aop);
+      else accum_dW(sG + A::g_off(FFN_WD_IN), sG + A::gb_off(FFN_WD_IN), FFN_M, LF, dop, aop, g, s);
     }
   }
 
   if (train) {
+    if constexpr (REG_ACC) {
+      // add the four wavefronts' register sums into the block's LDS gradient, one wave at a time
+      for (int w = 0; w < 4; ++w) {
+        __syncthreads();
+        if (wave == w) {
+          ga.c_out.flush(sG + A::g_off(FFN_WC_OUT), sG + A::gb_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, g, s);
+          if constexpr (NC >= 2) ga.c_h[0].flush(sG + A::g_off(FFN_WC_01), sG + A::gb_off(FFN_WC_01), FFN_M, FFN_M, g, s);
+          if constexpr (NC >= 3) ga.c_h[1].flush(sG + A::g_off(FFN_WC_12), sG + A::gb_off(FFN_WC_12), FFN_M, FFN_M, g, s);
+          if constexpr (NC >= 4) ga.c_h[2].flush(sG + A::g_off(FFN_WC_23), sG + A::gb_off(FFN_WC_23), FFN_M, FFN_M, g, s);
+          ga.c_in.flush(sG + A::g_off(FFN_WC_IN), sG + A::gb_off(FFN_WC_IN), FFN_M, FFN_C_IN, g, s);
+          ga.d_out.flush(sG + A::g_off(FFN_WD_OUT), sG + A::gb_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, g, s);
+          if constexpr (ND >= 2) ga.d_h[0].flush(sG + A::g_off(FFN_WD_01), sG + A::gb_off(FFN_WD_01), FFN_M, FFN_M, g, s);
+          if constexpr (ND >= 3) ga.d_h[1].flush(sG + A::g_off(FFN_WD_12), sG + A::gb_off(FFN_WD_12), FFN_M, FFN_M, g, s);
+          ga.d_in.flush(sG + A::g_off(FFN_WD_IN), sG + A::gb_off(FFN_WD_IN), FFN_M, LF, g, s);
+        }
+      }
+    }
     __syncthreads();
     float* dst = a.partials + (int64_t)blockIdx.x * A::g_total();
     for (int e = tid; e < A::g_total(); e += 256) dst[e] = sG[e];
