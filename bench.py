@@ -97,6 +97,8 @@ def main():
     ap.add_argument("--rays", type=int, default=1 << 18)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run one plain device copy of this size (a known-traffic kernel for PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested); the multi-GPU design is "
@@ -106,6 +108,17 @@ def main():
     import torch
     import ffnerf_tools as ft
     import synthetic_scene as sc
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] calibration copy: {args.copy_calibration_mib} MiB read + {args.copy_calibration_mib} MiB "
+              f"written by one copy kernel", flush=True)
+        del src, dst
 
     spec, occ, S = cfg2_spec(args.mlp)
     n_rays = int(args.rays)
