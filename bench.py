@@ -58,6 +58,36 @@ def algorithmic(spec):
     return fwd_b, bwd_b, mlp_flops, adam_b
 
 
+STAGE_KERNELS = {"mlp": ("void ffn::k_mlp<",), "hash_fwd": ("void ffn::k_hash_fwd<",),
+                 "hash_bwd": ("void ffn::k_bin_count<", "void ffn::k_bin_emit<", "void ffn::k_bin_reduce<")}
+
+
+def recorded_traffic(stage, mlp):
+    """HBM-side bytes of one launch of `stage` from the committed PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs, each scaled by what the counter reads for
+    a plain copy of known size), with the launch duration measured there."""
+    f = ROOT / "profiles" / f"pmc_traffic_cfg2_{mlp}.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    ks = d["kernels"]
+    ref = [v for n, v in ks.items() if n.startswith(STAGE_KERNELS["mlp"][0])]
+    if not ref:
+        return None
+    steps = ref[0]["dispatches"]
+    fetch = write = ns = 0.0
+    for n, v in ks.items():
+        if n.startswith(STAGE_KERNELS[stage]):
+            per_step = v["dispatches"] / steps
+            fetch += v["fetch_bytes"] * per_step
+            write += v["write_bytes"] * per_step
+            ns += v["avg_ns"] * per_step
+    if ns == 0.0:
+        return None
+    return dict(bytes=fetch + write, fetch=fetch, write=write, profiled_ms=ns * 1e-6,
+                source=f"profiles/{f.name}")
+
+
 def cpu_baseline(seconds=12.0):
     """The oracle (single-threaded C restatement of the reference step) on a
     bounded sample: steps of 512 rays x 64 samples at the cfg1 shapes."""
@@ -170,6 +200,7 @@ def main():
     dominant = max(per, key=lambda k: avg[k])
     bound, ach, peak, unit, alg = per[dominant]
     hash_gbs = (fwd_b + bwd_b) * N / ((avg["hash_fwd"] + avg["hash_bwd"]) * 1e-3) / 1e9
+    tr = recorded_traffic(dominant, args.mlp) if n_rays == 1 << 18 else None
     line = {
         "metric": "train samples/sec (fwd+bwd+Adam) per step; hash-grid gather/scatter HBM GB/s",
         "value": value, "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -180,7 +211,9 @@ def main():
                    "global_batch": n_rays, "samples_per_ray": S, "samples_per_step": N, "mlp": args.mlp},
         "hash_grid_gbs": hash_gbs,
         "roofline": {"kernel": dominant, "bound": bound, "achieved": ach, "peak": peak, "unit": unit,
-                     "frac": ach / peak, "algorithmic_per_launch": alg, "traffic": None},
+                     "frac": ach / peak, "algorithmic_per_launch": alg,
+                     "traffic": tr["bytes"] if tr else None,
+                     "traffic_detail": tr},
         "stages_ms_avg": {k: round(v, 4) for k, v in avg.items()},
         "stage_rooflines": {k: {"achieved": v[1], "unit": v[3], "frac": v[1] / v[2]} for k, v in per.items()},
     }
