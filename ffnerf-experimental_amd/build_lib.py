@@ -22,6 +22,9 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
+    # MFMA results in VGPRs: the MLP chains every layer's accumulator into the next layer's operand, and the
+    # AGPR form costs a v_accvgpr_read per value (and spills at the cfg2 shape)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -520,7 +520,10 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
             a.t_dLdc[3 * bj + 2] = dLdc_j[2];
           }
         }
-        // occupancy proposals for run-representative samples (ffnerf_OG.cl:1640-1821)
+      }
+      {
+        // occupancy proposals for run-representative samples (ffnerf_OG.cl:1640-1821); every wavefront
+        // holds the whole ray here and handles the proposals of its own 16 samples
         if (train && a.occ_strength > 0.0f) {
           const float t_j = vj ? a.Ts[bj] : 0.0f;
           uint64_t segmask = 0;
@@ -533,7 +536,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
           const float t_last = __shfl(t_j, base + last), T_last = __shfl(Tr, base + last);
           const float t_nx = __shfl(t_j, base + nsrc), T_nx = __shfl(Tr, base + nsrc);
           const bool is_rep = (segmask >> lid) & 1ull;
-          if (vj && is_rep && dt_j > 0.0f) {
+          if (vj && is_rep && dt_j > 0.0f && (j >> 4) == wave) {
             const float4 ro = a.rays[2 * rj], rdv = a.rays[2 * rj + 1];
             const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
             const int G = c.G;
@@ -592,18 +595,22 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
                 uint32_t q_stoch = ((hseed & 0x00FFFFFFu) < thresh) ? (q0 + 1u) : q0;
                 proposed_q = q_stoch > 16u ? 16u : q_stoch;
               }
-              const float lat = (c.bmax[0] - c.bmin[0]) * (1.0f / (float)G);
-              const float tl = t_j / fmaxf(lat, 1.0e-12f);
-              const float Dl = Dhalf / fmaxf(lat, 1.0e-12f);
-              const float num = tl * tl + tl + (1.0f / 3.0f);
-              const float den = Dl * Dl + Dl + (1.0f / 3.0f);
-              const float keep_p = fminf(num / fmaxf(den, 1.0e-12f), 1.0f);
-              bool keep = keep_p >= 1.0f;
-              if (!keep) {
-                uint32_t rk = hseed;
-                keep = rand01(rk) <= keep_p;
+              // occ_st equals occ_in after every decay and proposals only raise it, so a proposal that does
+              // not exceed the occ_in nibble cannot change occ_st: skip the keep draw and the atomic
+              if (proposed_q > old_q) {
+                const float lat = (c.bmax[0] - c.bmin[0]) * (1.0f / (float)G);
+                const float tl = t_j / fmaxf(lat, 1.0e-12f);
+                const float Dl = Dhalf / fmaxf(lat, 1.0e-12f);
+                const float num = tl * tl + tl + (1.0f / 3.0f);
+                const float den = Dl * Dl + Dl + (1.0f / 3.0f);
+                const float keep_p = fminf(num / fmaxf(den, 1.0e-12f), 1.0f);
+                bool keep = keep_p >= 1.0f;
+                if (!keep) {
+                  uint32_t rk = hseed;
+                  keep = rand01(rk) <= keep_p;
+                }
+                if (keep) occ_nibble_atomic_max(a.occ_st, cell, sub, proposed_q);
               }
-              if (keep) occ_nibble_atomic_max(a.occ_st, cell, sub, proposed_q);
             }
           }
         }
