@@ -72,6 +72,9 @@ struct Handle {
   int n_cu = 0;
   Scratch Ts, DTs, flags, a0, dLda0, partials;
   Scratch bin_cnt, bin_off, bin_sums, bin_total, bin_idx, bin_val, bin_max;
+  // marcher / render
+  Scratch m_state, m_acc, m_counts, m_offsets, m_sums, m_total, m_samples, m_ids, m_a0, m_sigma, m_rgb;
+  uint32_t* host_total = nullptr;  // pinned
 };
 
 size_t bin_budget_bytes() {
@@ -240,6 +243,10 @@ int ffn_destroy(void* handle) {
   h->bin_idx.release();
   h->bin_val.release();
   h->bin_max.release();
+  for (Scratch* sc : {&h->m_state, &h->m_acc, &h->m_counts, &h->m_offsets, &h->m_sums, &h->m_total, &h->m_samples,
+                      &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb})
+    sc->release();
+  if (h->host_total) (void)hipHostFree(h->host_total);
   delete h;
   return 0;
 }
@@ -470,6 +477,147 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     FFN_HIP(ffn::launch_mlp_adam(o, st));
   }
 
+  return 0;
+}
+
+int ffn_occ_bitfield(const uint32_t* occ, int32_t occ_G, uint32_t q_min, uint32_t* bits, void* stream) {
+  if (!occ || !bits) return fail(-1, "NULL buffer");
+  if (occ_G < 1 || occ_G > 512) return fail(-1, "occ_G=%d out of [1,512]", occ_G);
+  FFN_HIP(ffn::launch_occ_bitfield(occ, occ_G, q_min, bits, (hipStream_t)stream));
+  return 0;
+}
+
+namespace {
+
+int check_march(Handle* h, const void* rays, const uint32_t* bits, const ffn_march_params* mp) {
+  if (!h) return fail(-1, "NULL handle");
+  if (!rays || !bits || !mp) return fail(-1, "NULL buffer");
+  if (mp->res < 1 || mp->res > 1024) return fail(-1, "march res=%d out of [1,1024]", mp->res);
+  if (!(mp->dt > 0.0f)) return fail(-1, "march dt must be > 0");
+  if (mp->max_steps == 0 || mp->max_steps > (1u << 20)) return fail(-1, "max_steps=%u out of [1,2^20]", mp->max_steps);
+  return 0;
+}
+
+ffn::MarchArgs march_args(Handle* h, const void* rays, uint32_t num_rays, const uint32_t* bits,
+                          const ffn_march_params* mp) {
+  ffn::MarchArgs a{};
+  for (int i = 0; i < 3; ++i) {
+    a.bmin[i] = h->cfg.box_min[i];
+    a.bmax[i] = h->cfg.box_max[i];
+  }
+  a.t_near = h->cfg.t_near;
+  a.t_far = h->cfg.t_far;
+  a.rays = (const float4*)rays;
+  a.num_rays = num_rays;
+  a.bits = bits;
+  a.res = mp->res;
+  a.dt = mp->dt;
+  a.max_steps = mp->max_steps;
+  a.chunk = mp->max_steps;
+  return a;
+}
+
+}  // namespace
+
+int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits, const ffn_march_params* mp,
+              uint32_t* counts, uint32_t* offsets, float* samples, uint32_t* ray_ids, uint64_t capacity,
+              uint32_t* total, void* stream) {
+  Handle* h = as_handle(handle);
+  int rc = check_march(h, rays, bits, mp);
+  if (rc) return rc;
+  if (!counts || !offsets || !total || (capacity > 0 && (!samples || !ray_ids))) return fail(-1, "NULL buffer");
+  if (num_rays == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
+  a.counts = counts;
+  FFN_HIP(ffn::launch_march(a, false, st));
+  // offsets needs num_rays + 1 slots for the scan's total; use the handle's buffer for it
+  const size_t n1 = (size_t)num_rays + 1;
+  FFN_HIP(h->m_offsets.ensure(sizeof(uint32_t) * n1));
+  FFN_HIP(h->m_sums.ensure(sizeof(uint32_t) * ((n1 + 4095) / 4096 + 1)));
+  uint32_t* off = (uint32_t*)h->m_offsets.p;
+  FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, total, st));
+  FFN_HIP(hipMemcpyAsync(offsets, off, sizeof(uint32_t) * num_rays, hipMemcpyDeviceToDevice, st));
+  a.offsets = off;
+  a.samples = (float4*)samples;
+  a.ray_ids = ray_ids;
+  a.capacity = capacity;
+  FFN_HIP(ffn::launch_march(a, true, st));
+  return 0;
+}
+
+int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits, const ffn_march_params* mp,
+               void* out_rgb, uint32_t* n_samples, void* stream) {
+  Handle* h = as_handle(handle);
+  int rc = check_march(h, rays, bits, mp);
+  if (rc) return rc;
+  if (!out_rgb) return fail(-1, "NULL buffer");
+  if (!h->bound) return fail(-1, "bind params first");
+  if (mp->chunk == 0 || mp->chunk > 1024) return fail(-1, "chunk=%u out of [1,1024]", mp->chunk);
+  if (!(mp->T_stop >= 0.0f && mp->T_stop < 1.0f)) return fail(-1, "T_stop must be in [0,1)");
+  if (num_rays == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  const int LF = h->dc.LF;
+  const size_t n1 = (size_t)num_rays + 1;
+  const size_t cap = (size_t)num_rays * mp->chunk;
+  FFN_HIP(h->m_state.ensure(sizeof(ffn::MarchState) * num_rays));
+  FFN_HIP(h->m_acc.ensure(sizeof(float4) * num_rays));
+  FFN_HIP(h->m_counts.ensure(sizeof(uint32_t) * n1));
+  FFN_HIP(h->m_offsets.ensure(sizeof(uint32_t) * n1));
+  FFN_HIP(h->m_sums.ensure(sizeof(uint32_t) * ((n1 + 4095) / 4096 + 1)));
+  FFN_HIP(h->m_total.ensure(sizeof(uint32_t) * 4));
+  FFN_HIP(h->m_samples.ensure(sizeof(float4) * cap));
+  FFN_HIP(h->m_ids.ensure(sizeof(uint32_t) * cap));
+  FFN_HIP(h->m_a0.ensure(sizeof(float) * cap * LF));
+  FFN_HIP(h->m_sigma.ensure(sizeof(float) * cap));
+  FFN_HIP(h->m_rgb.ensure(sizeof(float) * cap * 3));
+  if (!h->host_total) FFN_HIP(hipHostMalloc((void**)&h->host_total, sizeof(uint32_t) * 4, hipHostMallocDefault));
+  ffn::MarchState* state = (ffn::MarchState*)h->m_state.p;
+  float4* acc = (float4*)h->m_acc.p;
+  uint32_t* counts = (uint32_t*)h->m_counts.p;
+  uint32_t* off = (uint32_t*)h->m_offsets.p;
+  uint32_t* total = (uint32_t*)h->m_total.p;
+  float4* samples = (float4*)h->m_samples.p;
+  uint32_t* ids = (uint32_t*)h->m_ids.p;
+  float* a0 = (float*)h->m_a0.p;
+  float* sigma = (float*)h->m_sigma.p;
+  float* rgb = (float*)h->m_rgb.p;
+  FFN_HIP(ffn::launch_march_init(state, acc, n_samples, num_rays, st));
+  ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
+  a.chunk = mp->chunk;
+  a.state = state;
+  a.counts = counts;
+  a.offsets = off;
+  a.samples = samples;
+  a.ray_ids = ids;
+  a.capacity = cap;
+  ffn::MlpPtrs w{};
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    w.W[k] = h->params.W[k];
+    w.b[k] = h->params.b[k];
+  }
+  int n_blocks = h->n_cu > 0 ? 2 * h->n_cu : 512;
+  const uint32_t rounds = (mp->max_steps + mp->chunk - 1) / mp->chunk;
+  for (uint32_t round = 0; round < rounds; ++round) {
+    FFN_HIP(ffn::launch_march(a, false, st));
+    FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, total, st));
+    FFN_HIP(hipMemcpyAsync(h->host_total, total, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    FFN_HIP(hipStreamSynchronize(st));
+    const int64_t n = *h->host_total;
+    if (n == 0) break;
+    FFN_HIP(ffn::launch_march(a, true, st));
+    ffn::PosSrc src{(const float*)samples, nullptr, nullptr, 0};
+    src.x_stride = 4;
+    const ffn::FeatLayout feat = ffn::level_major(n, h->dc.F);
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, a0, feat, nullptr, st));
+    int nb = (int)((n + 63) / 64);
+    if (nb > n_blocks) nb = n_blocks;
+    FFN_HIP(ffn::launch_mlp_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, mp->sh_multiplier, sigma, rgb, LF,
+                                h->cfg.nd, h->cfg.nc, nb, st));
+    FFN_HIP(ffn::launch_render_composite(off, counts, num_rays, sigma, rgb, mp->dt, mp->T_stop, state, acc,
+                                         n_samples, st));
+  }
+  FFN_HIP(ffn::launch_render_finish(acc, num_rays, (float4*)out_rgb, st));
   return 0;
 }
 

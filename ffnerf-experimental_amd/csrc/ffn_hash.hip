@@ -73,9 +73,10 @@ __device__ __forceinline__ void sample_position(const PosSrc& s, int64_t b, floa
     pos[1] = o.y + t * d.y;
     pos[2] = o.z + t * d.z;
   } else {
-    pos[0] = s.x[3 * b + 0];
-    pos[1] = s.x[3 * b + 1];
-    pos[2] = s.x[3 * b + 2];
+    const float* xb = s.x + (int64_t)s.x_stride * b;
+    pos[0] = xb[0];
+    pos[1] = xb[1];
+    pos[2] = xb[2];
   }
 }
 
@@ -461,6 +462,16 @@ __global__ __launch_bounds__(1024) void k_scan_add(uint32_t* __restrict__ out, i
 
 // ---------------------------------------------------------------------------
 // launchers
+
+// exclusive scan of in[0..n) into out[0..n]; out[n] and *total get the sum; sums has (n + 4096) / 4096 slots
+hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, uint32_t* total,
+                           hipStream_t st) {
+  const int64_t tiles = (n + 1 + 4095) / 4096;
+  hipLaunchKernelGGL(k_scan_tiles, dim3((unsigned)tiles), dim3(1024), 0, st, in, n, out, n + 1, sums);
+  hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, st, sums, tiles, total);
+  hipLaunchKernelGGL(k_scan_add, dim3((unsigned)tiles), dim3(1024), 0, st, out, n + 1, sums);
+  return hipGetLastError();
+}
 
 hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* table, float* a0,
                            const FeatLayout& lay, uint32_t* idx_out, hipStream_t st) {

@@ -46,12 +46,13 @@ inline PackedLayout make_layout(int LF, int nd, int nc) {
   return p;
 }
 
-// where sample positions come from: x[n][3], or o + Ts[b] d of ray b >> log2S
+// where sample positions come from: x[n][x_stride] (first three floats), or o + Ts[b] d of ray b >> log2S
 struct PosSrc {
   const float* x;
   const float4* rays;
   const float* Ts;
   int log2S;
+  int x_stride = 3;
 };
 
 // element (sample b, level l, feature f) of an encoding-shaped array is at
@@ -149,6 +150,48 @@ hipError_t launch_adam(float* p, float* m, float* v, float* g, int64_t n, float 
 hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st);
 hipError_t launch_occ_decay(uint32_t* occ_in, uint32_t* occ_st, uint32_t n_words, uint32_t decay_q24,
                             uint32_t seed, hipStream_t st);
+
+// occupancy bitfield and DDA marcher (no counterpart in the reference; see ffn_march.hip)
+struct MarchState {
+  uint32_t k;      // next lattice index
+  uint32_t cell;   // current cell, 10 bits per axis
+  uint32_t n;      // samples emitted so far
+  uint32_t flags;  // MARCH_FRESH, MARCH_DONE
+};
+enum { MARCH_FRESH = 1u, MARCH_DONE = 2u };
+
+struct MarchArgs {
+  float bmin[3], bmax[3], t_near, t_far;
+  const float4* rays;
+  uint32_t num_rays;
+  const uint32_t* bits;
+  int res;
+  float dt;
+  uint32_t max_steps;        // per ray in total
+  uint32_t chunk;            // per call
+  MarchState* state;         // NULL: every ray starts fresh and no state is kept
+  uint32_t* counts;          // count pass: samples this call per ray
+  const uint32_t* offsets;   // emit pass: first slot of each ray
+  float4* samples;           // emit pass: {x, y, z, t}
+  uint32_t* ray_ids;         // emit pass
+  uint64_t capacity;         // slots of samples / ray_ids
+};
+
+hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint32_t* bits, hipStream_t st);
+hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st);
+hipError_t launch_march_init(MarchState* state, float4* acc, uint32_t* n_used, uint32_t num_rays, hipStream_t st);
+hipError_t launch_render_composite(const uint32_t* offsets, const uint32_t* counts, uint32_t num_rays,
+                                   const float* sigma, const float* rgb, float dt, float T_stop, MarchState* state,
+                                   float4* acc, uint32_t* n_used, hipStream_t st);
+hipError_t launch_render_finish(const float4* acc, uint32_t num_rays, float4* out_rgb, hipStream_t st);
+hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, uint32_t* total,
+                           hipStream_t st);
+
+// forward-only MLP over n samples: encodings a0 (layout feat), view directions from rays[ray_ids[b]];
+// sigma[n], rgb[n][3]
+hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
+                          const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
+                          float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st);
 
 // fused MLP forward + compositing + loss + backward + proposals, per 64-sample tile
 bool mlp_supported(int LF, int nd, int nc);

@@ -1,0 +1,271 @@
+// ffn_march.hip -- occupancy bitfield, DDA marcher with stream compaction, and
+// the early-terminated front-to-back compositing of the forward render.
+//
+// The reference has no marcher: every ray gets S importance-resampled samples
+// (ffnerf_OG.cl:1002-1250).  This path is new; its specification is the CPU
+// definition in the oracle (ora_occ_bitfield, ora_march_ray, ora_render_ray),
+// which these kernels follow operation for operation (no contraction), so the
+// marched sample times are bit-identical.  Nearest reference analogues: the
+// occupancy nibble read (ffnerf_OG.cl:477-483) and the compositing recurrence
+// (ffnerf_OG.cl:1505-1591).
+//
+// MI355X design
+//   * The bitfield holds one bit per cell (x fastest, 32 cells per word):
+//     128^3 cells = 256 KiB, 256^3 = 2 MiB -- resident in each XCD's L2, so the
+//     DDA's bit lookups never reach HBM after the first touch.
+//   * One lane per ray.  Empty cells are skipped in one step: the first lattice
+//     index past the cell's exit is computed directly and corrected to the exact
+//     index the one-by-one walk of the specification reaches.
+//   * Compaction is two passes over the same deterministic walk: count, scan,
+//     emit to the scanned slots.  A chunked variant keeps a 16-byte state per
+//     ray so that the render can march, shade and composite a few samples per
+//     ray per round and retire rays whose transmittance fell below T_stop.
+#include "ffn_device.h"
+#include "ffn_kernels.h"
+
+namespace ffn {
+
+__global__ __launch_bounds__(256) void k_occ_bitfield(const uint32_t* __restrict__ occ, int G, uint32_t q_min,
+                                                      uint32_t* __restrict__ bits, int64_t n_words) {
+  const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= n_words) return;
+  const int R = 2 * G;
+  const int64_t n_cells = (int64_t)R * R * R;
+  uint32_t out = 0;
+  for (int j = 0; j < 32; ++j) {
+    const int64_t i = w * 32 + j;
+    if (i >= n_cells) break;
+    const int x = (int)(i % R), y = (int)((i / R) % R), z = (int)(i / ((int64_t)R * R));
+    const uint32_t word = occ[(x >> 1) + G * ((y >> 1) + G * (z >> 1))];
+    const uint32_t sub = (uint32_t)((x & 1) | ((y & 1) << 1) | ((z & 1) << 2));
+    const uint32_t q = ((word >> (4u * sub)) & 0xFu) + 1u;
+    if (q >= q_min) out |= 1u << j;
+  }
+  bits[w] = out;
+}
+
+__device__ __forceinline__ float lattice_t(float t0, uint32_t k, float dt) { return t0 + ((float)k + 0.5f) * dt; }
+
+// The walk of one ray from its state; returns the samples of this call.  EMIT writes them from slot
+// `base` on and stores the new state; the count pass only reads the state.
+template <bool EMIT>
+__device__ uint32_t march_ray(const MarchArgs& a, uint32_t r, uint64_t base) {
+  MarchState st = a.state ? a.state[r] : MarchState{0u, 0u, 0u, MARCH_FRESH};
+  if (st.flags & MARCH_DONE) return 0;
+  const float4 ro = a.rays[2 * (size_t)r], rd = a.rays[2 * (size_t)r + 1];
+  const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rd.x, rd.y, rd.z};
+  const int R = a.res;
+  uint32_t emitted = 0;
+  bool done = false;
+  float ta, tb;
+  if (!ray_aabb(o, d, a.bmin, a.bmax, ta, tb)) {
+    done = true;
+  } else {
+    const float t0 = fmaxf(ta, a.t_near), t1 = fminf(tb, a.t_far);
+    if (!(t1 > t0)) {
+      done = true;
+    } else {
+      float cell[3], invd[3];
+      int cc[3], step[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const float size = a.bmax[i] - a.bmin[i];
+        cell[i] = size / (float)R;
+        invd[i] = (d[i] != 0.0f) ? (1.0f / d[i]) : __builtin_huge_valf();
+        step[i] = d[i] > 0.0f ? 1 : (d[i] < 0.0f ? -1 : 0);
+      }
+      if (st.flags & MARCH_FRESH) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          const float inv = (float)R / (a.bmax[i] - a.bmin[i]);
+          const float p = o[i] + t0 * d[i];
+          const int ci = (int)floorf((p - a.bmin[i]) * inv);
+          cc[i] = ci < 0 ? 0 : (ci > R - 1 ? R - 1 : ci);
+        }
+        st.k = 0;
+        st.n = 0;
+      } else {
+        cc[0] = (int)(st.cell & 1023u);
+        cc[1] = (int)((st.cell >> 10) & 1023u);
+        cc[2] = (int)((st.cell >> 20) & 1023u);
+      }
+      uint32_t k = st.k;
+      const uint32_t budget = a.chunk;
+      bool paused = false;
+      for (int iter = 0; iter < 3 * R + 3; ++iter) {
+        float t_exit = t1;
+        int axis = -1;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          if (step[i] == 0) continue;
+          const float bound = a.bmin[i] + (float)(cc[i] + (step[i] > 0 ? 1 : 0)) * cell[i];
+          const float te = (bound - o[i]) * invd[i];
+          if (te < t_exit) {
+            t_exit = te;
+            axis = i;
+          }
+        }
+        const int64_t bi = cc[0] + (int64_t)R * (cc[1] + (int64_t)R * cc[2]);
+        const bool occ = (a.bits[bi >> 5] >> (bi & 31)) & 1u;
+        if (occ) {
+          for (;;) {
+            const float tk = lattice_t(t0, k, a.dt);
+            if (!(tk < t_exit)) break;
+            if (st.n + emitted >= a.max_steps) {
+              done = true;
+              break;
+            }
+            if (emitted >= budget) {
+              paused = true;
+              break;
+            }
+            if (EMIT) {
+              const uint64_t slot = base + emitted;
+              if (slot < a.capacity) {
+                a.samples[slot] = make_float4(o[0] + tk * d[0], o[1] + tk * d[1], o[2] + tk * d[2], tk);
+                a.ray_ids[slot] = r;
+              }
+            }
+            ++emitted;
+            ++k;
+          }
+          if (done || paused) break;
+        } else if (lattice_t(t0, k, a.dt) < t_exit) {
+          // skip the empty cell: the first k with t_k >= t_exit, exactly as the one-by-one walk finds it
+          float est = ceilf((t_exit - t0) / a.dt - 0.5f);
+          uint32_t ke = k + 1;
+          if (est > (float)ke) ke = est < 4.0e9f ? (uint32_t)est : 4000000000u;
+          while (ke > k + 1 && !(lattice_t(t0, ke - 1, a.dt) < t_exit)) --ke;
+          while (lattice_t(t0, ke, a.dt) < t_exit) ++ke;
+          k = ke;
+        }
+        if (axis < 0) {
+          done = true;
+          break;
+        }
+        cc[axis] += step[axis];
+        if (cc[axis] < 0 || cc[axis] >= R) {
+          done = true;
+          break;
+        }
+        if (iter == 3 * R + 2) done = true;
+      }
+      if (EMIT) {
+        st.k = k;
+        st.cell = (uint32_t)cc[0] | ((uint32_t)cc[1] << 10) | ((uint32_t)cc[2] << 20);
+      }
+    }
+  }
+  if (EMIT && a.state) {
+    st.n += emitted;
+    st.flags = (st.flags & ~MARCH_FRESH) | (done ? MARCH_DONE : 0u);
+    a.state[r] = st;
+  }
+  return emitted;
+}
+
+template <bool EMIT>
+__global__ __launch_bounds__(256) void k_march(MarchArgs a) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= a.num_rays) return;
+  if (EMIT) {
+    march_ray<true>(a, r, a.offsets[r]);
+  } else {
+    a.counts[r] = march_ray<false>(a, r, 0);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_march_init(MarchState* __restrict__ state, float4* __restrict__ acc,
+                                                    uint32_t* __restrict__ n_used, uint32_t num_rays) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= num_rays) return;
+  state[r] = MarchState{0u, 0u, 0u, MARCH_FRESH};
+  acc[r] = make_float4(0.0f, 0.0f, 0.0f, 1.0f);
+  if (n_used) n_used[r] = 0u;
+}
+
+// front-to-back compositing of this round's samples of each ray (alpha as ffnerf_OG.cl:1505-1520);
+// a ray whose transmittance drops below T_stop is retired
+__global__ __launch_bounds__(256) void k_render_composite(const uint32_t* __restrict__ offsets,
+                                                          const uint32_t* __restrict__ counts, uint32_t num_rays,
+                                                          const float* __restrict__ sigma,
+                                                          const float* __restrict__ rgb, float dt, float T_stop,
+                                                          MarchState* __restrict__ state, float4* __restrict__ acc,
+                                                          uint32_t* __restrict__ n_used) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= num_rays) return;
+  const uint32_t cnt = counts[r];
+  if (cnt == 0) return;
+  const uint32_t off = offsets[r];
+  float4 cv = acc[r];
+  float T = cv.w;
+  if (!(T >= T_stop)) return;  // retired in an earlier round
+  float C0 = cv.x, C1 = cv.y, C2 = cv.z;
+  uint32_t used = 0;
+  for (uint32_t j = 0; j < cnt; ++j) {
+    const uint32_t b = off + j;
+    const float alpha = 1.0f - expf(fminf(fmaxf(-sigma[b] * dt, -5.0f), 18.0f));
+    const float w = T * alpha;
+    C0 = C0 + w * rgb[3 * (size_t)b];
+    C1 = C1 + w * rgb[3 * (size_t)b + 1];
+    C2 = C2 + w * rgb[3 * (size_t)b + 2];
+    T = T * (1.0f - alpha);
+    ++used;
+    if (T < T_stop) {
+      state[r].flags |= MARCH_DONE;
+      break;
+    }
+  }
+  acc[r] = make_float4(C0, C1, C2, T);
+  if (n_used) n_used[r] += used;
+}
+
+__global__ __launch_bounds__(256) void k_render_finish(const float4* __restrict__ acc, uint32_t num_rays,
+                                                       float4* __restrict__ out_rgb) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= num_rays) return;
+  out_rgb[r] = acc[r];  // black background: C + T * 0; w = T_final
+}
+
+// ---------------------------------------------------------------------------
+
+hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint32_t* bits, hipStream_t st) {
+  const int64_t R = 2 * (int64_t)G;
+  const int64_t n_words = (R * R * R + 31) / 32;
+  hipLaunchKernelGGL(k_occ_bitfield, dim3((unsigned)((n_words + 255) / 256)), dim3(256), 0, st, occ, G, q_min,
+                     bits, n_words);
+  return hipGetLastError();
+}
+
+hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st) {
+  if (a.num_rays == 0) return hipSuccess;
+  const dim3 grid((a.num_rays + 255) / 256), block(256);
+  if (emit)
+    hipLaunchKernelGGL(k_march<true>, grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL(k_march<false>, grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_march_init(MarchState* state, float4* acc, uint32_t* n_used, uint32_t num_rays, hipStream_t st) {
+  if (num_rays == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_march_init, dim3((num_rays + 255) / 256), dim3(256), 0, st, state, acc, n_used, num_rays);
+  return hipGetLastError();
+}
+
+hipError_t launch_render_composite(const uint32_t* offsets, const uint32_t* counts, uint32_t num_rays,
+                                   const float* sigma, const float* rgb, float dt, float T_stop, MarchState* state,
+                                   float4* acc, uint32_t* n_used, hipStream_t st) {
+  if (num_rays == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_render_composite, dim3((num_rays + 255) / 256), dim3(256), 0, st, offsets, counts, num_rays,
+                     sigma, rgb, dt, T_stop, state, acc, n_used);
+  return hipGetLastError();
+}
+
+hipError_t launch_render_finish(const float4* acc, uint32_t num_rays, float4* out_rgb, hipStream_t st) {
+  if (num_rays == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_render_finish, dim3((num_rays + 255) / 256), dim3(256), 0, st, acc, num_rays, out_rgb);
+  return hipGetLastError();
+}
+
+}  // namespace ffn

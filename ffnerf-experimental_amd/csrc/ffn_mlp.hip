@@ -282,6 +282,113 @@ struct AccSet<LF, ND, NC, true> {
   }
 };
 
+// stage the weights of every active layer into LDS (zero-padded rows, pitch in+1)
+template <int LF, int ND, int NC>
+__device__ __forceinline__ void stage_weights(float* __restrict__ sW, const MlpPtrs& wp, int tid, int nthreads) {
+  using A = Arch<LF, ND, NC>;
+#pragma unroll
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    if (!layer_active(k, ND, NC)) continue;
+    const int O = layer_out(k), I = layer_in(k, LF), R = A::rows_pad(k), P = A::pitch(k);
+    float* w = sW + A::w_off(k);
+    float* bb = sW + A::b_off(k);
+    const float* gw = wp.W[k];
+    const float* gbias = wp.b[k];
+    for (int e = tid; e < R * P; e += nthreads) {
+      const int r = e / P, col = e - r * P;
+      w[e] = (r < O && col < I) ? gw[r * I + col] : 0.0f;
+    }
+    for (int e = tid; e < R; e += nthreads) bb[e] = e < O ? gbias[e] : 0.0f;
+  }
+}
+
+// a0r[kk] = encoding neuron (LF/4) g + kk (= level n / F, feature n % F) of sample b
+template <int LF, int FEAT>
+__device__ __forceinline__ void load_a0(const float* __restrict__ a0, const FeatLayout& feat, int64_t b, bool valid,
+                                        int g, float (&a0r)[LF / 4]) {
+  constexpr int KA = LF / 4;
+  if (valid) {
+    if constexpr (FEAT >= 2 && KA % 2 == 0) {
+#pragma unroll
+      for (int kk = 0; kk < KA; kk += 2) {
+        const int nn = KA * g + kk;
+        const int l = nn / FEAT, f = nn - l * FEAT;
+        const float2 v = *reinterpret_cast<const float2*>(a0 + l * feat.stride_l + b * feat.stride_b + f);
+        a0r[kk] = v.x;
+        a0r[kk + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KA; ++kk) {
+        const int nn = KA * g + kk;
+        const int l = nn / FEAT, f = nn - l * FEAT;
+        a0r[kk] = a0[l * feat.stride_l + b * feat.stride_b + f];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < KA; ++q) a0r[q] = 0.0f;
+  }
+}
+
+// forward of the wavefront's 16 samples through both MLPs (ffnerf_OG.cl:1373-1466): hidden activations
+// (kept for the backward), the colour-net input [dout | SH * mult] and the sigmoid colours
+template <int LF, int ND, int NC>
+__device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const float (&a0r)[LF / 4],
+                                             const float (&dirv)[3], float sh_mult, int g, int s,
+                                             floatx4 (&hd)[ND][4], floatx4 (&acin)[2], floatx4 (&hc)[NC][4],
+                                             float (&rgb_s)[3]) {
+  using A = Arch<LF, ND, NC>;
+  constexpr int KA = LF / 4;
+  {
+    const float* W = sW + A::w_off(FFN_WD_IN);
+    const float* B = sW + A::b_off(FFN_WD_IN);
+    constexpr int P = A::pitch(FFN_WD_IN);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      floatx4 acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
+      const float* wrow = W + (16 * t + s) * P + KA * g;
+#pragma unroll
+      for (int kk = 0; kk < KA; ++kk) acc = mfma4(wrow[kk], a0r[kk], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
+      hd[0][t] = acc;
+    }
+  }
+  if constexpr (ND >= 2)
+    fwd_tiles<4, 4>(sW + A::w_off(FFN_WD_01), sW + A::b_off(FFN_WD_01), A::pitch(FFN_WD_01), hd[0], hd[1], g, s,
+                    true);
+  if constexpr (ND >= 3)
+    fwd_tiles<4, 4>(sW + A::w_off(FFN_WD_12), sW + A::b_off(FFN_WD_12), A::pitch(FFN_WD_12), hd[1], hd[2], g, s,
+                    true);
+  {
+    floatx4 o1[1];
+    fwd_tiles<1, 4>(sW + A::w_off(FFN_WD_OUT), sW + A::b_off(FFN_WD_OUT), A::pitch(FFN_WD_OUT), hd[ND - 1], o1, g,
+                    s, false);
+    acin[0] = o1[0];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acin[1][r] = sh_component(dirv, 4 * g + r) * sh_mult;
+  }
+  fwd_tiles<4, 2>(sW + A::w_off(FFN_WC_IN), sW + A::b_off(FFN_WC_IN), A::pitch(FFN_WC_IN), acin, hc[0], g, s, true);
+  if constexpr (NC >= 2)
+    fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_01), sW + A::b_off(FFN_WC_01), A::pitch(FFN_WC_01), hc[0], hc[1], g, s,
+                    true);
+  if constexpr (NC >= 3)
+    fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_12), sW + A::b_off(FFN_WC_12), A::pitch(FFN_WC_12), hc[1], hc[2], g, s,
+                    true);
+  if constexpr (NC >= 4)
+    fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_23), sW + A::b_off(FFN_WC_23), A::pitch(FFN_WC_23), hc[2], hc[3], g, s,
+                    true);
+  floatx4 co[1];
+  fwd_tiles<1, 4>(sW + A::w_off(FFN_WC_OUT), sW + A::b_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), hc[NC - 1], co, g, s,
+                  false);
+  rgb_s[0] = sigmoid_soft(co[0][0]);
+  rgb_s[1] = sigmoid_soft(co[0][1]);
+  rgb_s[2] = sigmoid_soft(co[0][2]);
+}
+
 template <int LF, int ND, int NC, int FEAT>
 __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
   using A = Arch<LF, ND, NC>;
@@ -297,21 +404,8 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
   const int S = a.S, log2S = a.log2S;
   const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
 
-  // stage weights (zero-padded rows, pitch in+1) and clear the gradient accumulators
-#pragma unroll
-  for (int k = 0; k < FFN_N_LAYERS; ++k) {
-    if (!layer_active(k, ND, NC)) continue;
-    const int O = layer_out(k), I = layer_in(k, LF), R = A::rows_pad(k), P = A::pitch(k);
-    float* w = sW + A::w_off(k);
-    float* bb = sW + A::b_off(k);
-    const float* gw = a.w.W[k];
-    const float* gbias = a.w.b[k];
-    for (int e = tid; e < R * P; e += 256) {
-      const int r = e / P, col = e - r * P;
-      w[e] = (r < O && col < I) ? gw[r * I + col] : 0.0f;
-    }
-    for (int e = tid; e < R; e += 256) bb[e] = e < O ? gbias[e] : 0.0f;
-  }
+  // stage weights and clear the gradient accumulators
+  stage_weights<LF, ND, NC>(sW, a.w, tid, 256);
   if (train)
     for (int e = tid; e < A::g_total(); e += 256) sG[e] = 0.0f;
   __syncthreads();
@@ -336,29 +430,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     const bool valid = (uint64_t)b < n_samples;
     const int64_t ray = valid ? (b >> log2S) : 0;
     float a0r[KA];
-    if (valid) {
-      // a0r[kk] = encoding neuron KA*g + kk (= level n / F, feature n % F) of sample b
-      if constexpr (FEAT >= 2 && KA % 2 == 0) {
-#pragma unroll
-        for (int kk = 0; kk < KA; kk += 2) {
-          const int nn = KA * g + kk;
-          const int l = nn / FEAT, f = nn - l * FEAT;
-          const float2 v = *reinterpret_cast<const float2*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b + f);
-          a0r[kk] = v.x;
-          a0r[kk + 1] = v.y;
-        }
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < KA; ++kk) {
-          const int nn = KA * g + kk;
-          const int l = nn / FEAT, f = nn - l * FEAT;
-          a0r[kk] = a.a0[l * a.feat.stride_l + b * a.feat.stride_b + f];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < KA; ++q) a0r[q] = 0.0f;
-    }
+    load_a0<LF, FEAT>(a.a0, a.feat, b, valid, g, a0r);
     float dirv[3];
     {
       const float4 rd = a.rays[2 * ray + 1];
@@ -370,59 +442,10 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     const float t_b = valid ? a.Ts[b] : 0.0f;
 
     floatx4 hd[ND][4];
-    {
-      const float* W = sW + A::w_off(FFN_WD_IN);
-      const float* B = sW + A::b_off(FFN_WD_IN);
-      constexpr int P = A::pitch(FFN_WD_IN);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        floatx4 acc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
-        const float* wrow = W + (16 * t + s) * P + KA * g;
-#pragma unroll
-        for (int kk = 0; kk < KA; ++kk) acc = mfma4(wrow[kk], a0r[kk], acc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
-        hd[0][t] = acc;
-      }
-    }
-    if constexpr (ND >= 2)
-      fwd_tiles<4, 4>(sW + A::w_off(FFN_WD_01), sW + A::b_off(FFN_WD_01), A::pitch(FFN_WD_01), hd[0], hd[1], g, s,
-                      true);
-    if constexpr (ND >= 3)
-      fwd_tiles<4, 4>(sW + A::w_off(FFN_WD_12), sW + A::b_off(FFN_WD_12), A::pitch(FFN_WD_12), hd[1], hd[2], g, s,
-                      true);
     floatx4 acin[2];  // [dout(16) | SH*mult(16)] as two D-layout tiles
-    {
-      floatx4 o1[1];
-      fwd_tiles<1, 4>(sW + A::w_off(FFN_WD_OUT), sW + A::b_off(FFN_WD_OUT), A::pitch(FFN_WD_OUT), hd[ND - 1], o1, g,
-                      s, false);
-      acin[0] = o1[0];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acin[1][r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
-    }
     floatx4 hc[NC][4];
-    fwd_tiles<4, 2>(sW + A::w_off(FFN_WC_IN), sW + A::b_off(FFN_WC_IN), A::pitch(FFN_WC_IN), acin, hc[0], g, s,
-                    true);
-    if constexpr (NC >= 2)
-      fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_01), sW + A::b_off(FFN_WC_01), A::pitch(FFN_WC_01), hc[0], hc[1], g, s,
-                      true);
-    if constexpr (NC >= 3)
-      fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_12), sW + A::b_off(FFN_WC_12), A::pitch(FFN_WC_12), hc[1], hc[2], g, s,
-                      true);
-    if constexpr (NC >= 4)
-      fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_23), sW + A::b_off(FFN_WC_23), A::pitch(FFN_WC_23), hc[2], hc[3], g, s,
-                      true);
     float rgb_s[3];
-    {
-      floatx4 co[1];
-      fwd_tiles<1, 4>(sW + A::w_off(FFN_WC_OUT), sW + A::b_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), hc[NC - 1], co, g,
-                      s, false);
-      rgb_s[0] = sigmoid_soft(co[0][0]);
-      rgb_s[1] = sigmoid_soft(co[0][1]);
-      rgb_s[2] = sigmoid_soft(co[0][2]);
-    }
+    mlp_fwd_tile<LF, ND, NC>(sW, a0r, dirv, a.sh_mult, g, s, hd, acin, hc, rgb_s);
     const float dout0 = acin[0][0];
     if (g == 0) {
       float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
@@ -791,6 +814,73 @@ static hipError_t launch_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
   }
 }
 
+// forward only, over a flat list of samples (the render path): 16 samples per wavefront per step
+template <int LF, int ND, int NC, int FEAT>
+__global__ __launch_bounds__(256) void k_mlp_fwd(MlpPtrs wp, const float* __restrict__ a0, FeatLayout feat,
+                                                 const float4* __restrict__ rays, const uint32_t* __restrict__ ray_ids,
+                                                 int64_t n, float sh_mult, float* __restrict__ sigma,
+                                                 float* __restrict__ rgb) {
+  extern __shared__ float smem[];
+  float* sW = smem;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+  stage_weights<LF, ND, NC>(sW, wp, tid, 256);
+  __syncthreads();
+  for (int64_t grp = (int64_t)blockIdx.x * 4 + wave; grp * 16 < n; grp += (int64_t)gridDim.x * 4) {
+    const int64_t b = grp * 16 + s;
+    const bool valid = b < n;
+    float a0r[LF / 4];
+    load_a0<LF, FEAT>(a0, feat, b, valid, g, a0r);
+    float dirv[3] = {0.0f, 0.0f, 1.0f};
+    if (valid) {
+      const float4 rd = rays[2 * (size_t)ray_ids[b] + 1];
+      dirv[0] = rd.x;
+      dirv[1] = rd.y;
+      dirv[2] = rd.z;
+    }
+    floatx4 hd[ND][4];
+    floatx4 acin[2];
+    floatx4 hc[NC][4];
+    float rgb_s[3];
+    mlp_fwd_tile<LF, ND, NC>(sW, a0r, dirv, sh_mult, g, s, hd, acin, hc, rgb_s);
+    if (g == 0 && valid) {
+      sigma[b] = softplus(fminf(fmaxf(acin[0][0], -10.0f), 10.0f));
+      rgb[3 * b] = rgb_s[0];
+      rgb[3 * b + 1] = rgb_s[1];
+      rgb[3 * b + 2] = rgb_s[2];
+    }
+  }
+}
+
+template <int LF, int ND, int NC, int FEAT>
+static hipError_t launch_fwd_f(const MlpPtrs& w, const float* a0, const FeatLayout& feat, const float4* rays,
+                               const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma, float* rgb,
+                               int n_blocks, hipStream_t st) {
+  using A = Arch<LF, ND, NC>;
+  const size_t lds = sizeof(float) * (size_t)A::w_total();
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp_fwd<LF, ND, NC, FEAT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_mlp_fwd<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, w, a0, feat, rays, ray_ids, n,
+                     sh_mult, sigma, rgb);
+  return hipGetLastError();
+}
+
+template <int LF, int ND, int NC>
+static hipError_t launch_fwd_t(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
+                               const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
+                               float* rgb, int n_blocks, hipStream_t st) {
+  switch (c.F) {
+    case 1: return launch_fwd_f<LF, ND, NC, 1>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
+    case 2: return launch_fwd_f<LF, ND, NC, 2>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
+    case 4: return launch_fwd_f<LF, ND, NC, 4>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 #define FFN_MLP_CONFIGS(X) \
   X(16, 1, 2)              \
   X(32, 1, 2)              \
@@ -813,6 +903,18 @@ size_t mlp_lds_bytes(int LF, int nd, int nc) {
   FFN_MLP_CONFIGS(X)
 #undef X
   return 0;
+}
+
+hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
+                          const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
+                          float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+#define X(l, d, nn)                   \
+  if (LF == l && nd == d && nc == nn) \
+    return launch_fwd_t<l, d, nn>(c, w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
+  FFN_MLP_CONFIGS(X)
+#undef X
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {

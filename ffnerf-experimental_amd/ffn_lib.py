@@ -23,7 +23,7 @@ MLP_PRECISION = {"fp32": 0, "fp16": 1}
 EXPORTS = [
     "ffn_version", "ffn_last_error", "ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step",
     "ffn_occ_decay", "ffn_sample", "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam",
-    "ffn_set_profiling", "ffn_stage_times",
+    "ffn_set_profiling", "ffn_stage_times", "ffn_occ_bitfield", "ffn_march", "ffn_render",
 ]
 STAGES = ["sample", "hash_fwd", "mlp", "hash_bwd", "mlp_adam", "table_adam"]
 
@@ -69,6 +69,20 @@ class FfnTaps(C.Structure):
     ]
 
 
+class FfnMarchParams(C.Structure):
+    _fields_ = [
+        ("res", C.c_int32), ("dt", C.c_float), ("max_steps", C.c_uint32), ("T_stop", C.c_float),
+        ("chunk", C.c_uint32), ("sh_multiplier", C.c_float), ("reserved", C.c_int32 * 2),
+    ]
+
+
+def march_params(res, dt, max_steps, T_stop=1e-4, chunk=32, sh_multiplier=1.0) -> FfnMarchParams:
+    m = FfnMarchParams()
+    m.res, m.dt, m.max_steps, m.T_stop, m.chunk, m.sh_multiplier = int(res), float(dt), int(max_steps), \
+        float(T_stop), int(chunk), float(sh_multiplier)
+    return m
+
+
 class FfnError(RuntimeError):
     pass
 
@@ -98,10 +112,15 @@ def load(path: Path | str | None = None) -> C.CDLL:
     lib.ffn_hash_encode_bwd.argtypes = [_vp, _vp, _vp, C.c_int64, _vp, _vp]
     lib.ffn_adam.argtypes = [_vp, _vp, _vp, _vp, C.c_int64, C.c_float, C.c_float, C.c_float, C.c_float, C.c_int32,
                              _vp]
+    lib.ffn_occ_bitfield.argtypes = [_vp, C.c_int32, C.c_uint32, _vp, _vp]
+    lib.ffn_march.argtypes = [_vp, _vp, C.c_uint32, _vp, C.POINTER(FfnMarchParams), _vp, _vp, _vp, _vp, C.c_uint64,
+                              _vp, _vp]
+    lib.ffn_render.argtypes = [_vp, _vp, C.c_uint32, _vp, C.POINTER(FfnMarchParams), _vp, _vp, _vp]
     lib.ffn_set_profiling.argtypes = [_vp, C.c_int32]
     lib.ffn_stage_times.argtypes = [_vp, _fp, C.POINTER(C.c_int32), C.c_int32]
     for name in ("ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step", "ffn_occ_decay", "ffn_sample",
-                 "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam", "ffn_set_profiling", "ffn_stage_times"):
+                 "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam", "ffn_set_profiling", "ffn_stage_times",
+                 "ffn_occ_bitfield", "ffn_march", "ffn_render"):
         getattr(lib, name).restype = C.c_int
     if path is None:
         _LIB = lib

@@ -153,6 +153,45 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
 int ffn_adam(float* p, float* m, float* v, float* g, int64_t n, float lr_t, float beta1, float beta2, float eps,
              int32_t zero_grad, void* stream);
 
+/* ---- occupancy bitfield, DDA marcher, early-terminated render ----------
+ * No counterpart in the reference, which samples every ray with S importance-
+ * resampled points (ffnerf_OG.cl:1002-1250); its nearest analogues are the
+ * occupancy nibble read (ffnerf_OG.cl:477-483) and the compositing recurrence
+ * (ffnerf_OG.cl:1505-1591).  The CPU definitions ora_occ_bitfield,
+ * ora_march_ray and ora_render_ray (oracle/) are the specification. */
+
+/* Bitfield of (2G)^3 cells from the nibble grid occ [G^3]: bit = (q >= q_min)
+ * with q = nibble + 1 of the cell's subcell; bit index x + R (y + R z),
+ * R = 2G, 32 cells per word: bits holds ceil(R^3 / 32) words. */
+int ffn_occ_bitfield(const uint32_t* occ, int32_t occ_G, uint32_t q_min, uint32_t* bits, void* stream);
+
+typedef struct ffn_march_params {
+  int32_t res;            /* cells per axis of the bitfield (<= 1024) */
+  float dt;               /* lattice step: samples at t0 + (k + 1/2) dt, t0 the box entry */
+  uint32_t max_steps;     /* samples per ray at most */
+  float T_stop;           /* render: a ray stops after the sample that leaves T < T_stop */
+  uint32_t chunk;         /* render: samples marched per ray per round */
+  float sh_multiplier;    /* render: SH scale of the colour-net input */
+  int32_t reserved[2];
+} ffn_march_params;
+
+/* March every ray through the bitfield (box and t_near/t_far of the handle's
+ * config) and compact the samples: counts/offsets [num_rays]; samples
+ * [capacity] float4 {x, y, z, t}; ray_ids [capacity]; *total (device) = sum
+ * of counts.  Slots at or beyond capacity are not written: compare *total
+ * with capacity. */
+int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits, const ffn_march_params* mp,
+              uint32_t* counts, uint32_t* offsets, float* samples, uint32_t* ray_ids, uint64_t capacity,
+              uint32_t* total, void* stream);
+
+/* Forward render with the bound parameters: march `chunk` samples per live
+ * ray, encode, run the MLPs, composite front to back, retire rays below
+ * T_stop, repeat.  out_rgb [num_rays] float4 {r, g, b, T_final} (black
+ * background); n_samples [num_rays] (optional) = samples composited.  Waits
+ * on the stream once per round to size the round's launches. */
+int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits, const ffn_march_params* mp,
+               void* out_rgb, uint32_t* n_samples, void* stream);
+
 /* Stage timing (the counterpart of the reference's profiling queue and
  * event_ms, ffnerf_tools.py:11-13,127-138,1521-1530).  When enabled, every
  * ffn_train_step records HIP events around its kernels on the caller's stream;

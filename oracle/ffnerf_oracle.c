@@ -1148,3 +1148,127 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
   free(table_read);
   return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* R4: occupancy bitfield, DDA marcher, early-terminated render.      */
+/* New in this build (the reference samples with R3 only); the        */
+/* definitions below are the specification the HIP kernels follow    */
+/* operation for operation.  Nearest reference analogues: the         */
+/* occupancy nibble read (ffnerf_OG.cl:477-483) and the compositing   */
+/* recurrence (ffnerf_OG.cl:1505-1591).                               */
+
+typedef struct {
+  int32_t res;         /* cells per axis of the bitfield */
+  float dt;            /* lattice step: samples at t0 + (k + 0.5) dt */
+  uint32_t max_steps;  /* emitted samples per ray at most */
+  float T_stop;        /* render: stop once the transmittance drops below */
+  float sh_multiplier;
+} ora_march_cfg;
+
+/* bit (x, y, z) of the (2G)^3 bitfield = (nibble q of that subcell >= q_min); bit index x + R (y + R z),
+ * 32 bits per word.  Subcell (x, y, z) is nibble (x&1) | (y&1)<<1 | (z&1)<<2 of word (x>>1, y>>1, z>>1). */
+void ora_occ_bitfield(const uint32_t* occ, int32_t G, uint32_t q_min, uint32_t* bits) {
+  const int R = 2 * G;
+  const int64_t n = (int64_t)R * R * R;
+  memset(bits, 0, sizeof(uint32_t) * (size_t)((n + 31) / 32));
+  for (int z = 0; z < R; ++z)
+    for (int y = 0; y < R; ++y)
+      for (int x = 0; x < R; ++x) {
+        const uint32_t w = occ[(x >> 1) + G * ((y >> 1) + G * (z >> 1))];
+        const uint32_t sub = (uint32_t)((x & 1) | ((y & 1) << 1) | ((z & 1) << 2));
+        const uint32_t q = ((w >> (4u * sub)) & 0xFu) + 1u;
+        if (q >= q_min) {
+          const int64_t i = x + (int64_t)R * (y + (int64_t)R * z);
+          bits[i >> 5] |= 1u << (i & 31);
+        }
+      }
+}
+
+static int bit_at(const uint32_t* bits, int R, const int c[3]) {
+  const int64_t i = c[0] + (int64_t)R * (c[1] + (int64_t)R * c[2]);
+  return (bits[i >> 5] >> (i & 31)) & 1u;
+}
+
+/* The march of one ray.  The cells come from a DDA that starts at the cell of o + t0 d (clamped into the
+ * grid) and leaves each cell at the nearest face plane crossed, t = (bmin + (c + (d > 0)) cell - o) / d.
+ * A lattice time t_k = t0 + (k + 0.5) dt belongs to the cell whose interval [t_enter, t_exit) holds it;
+ * it is emitted when that cell's bit is set, until t_k >= t1 or max_steps samples.  Here every lattice
+ * point is visited one by one (the brute force of the specification). */
+int ora_march_ray(const ora_cfg* c, const ora_march_cfg* m, const uint32_t* bits, const float* ray, float* t_out) {
+  const float* o = ray;
+  const float* d = ray + 4;
+  float ta, tb;
+  if (!ora_ray_aabb(o, d, c->box_min, c->box_max, &ta, &tb)) return 0;
+  const float t0 = fmaxf(ta, c->t_near), t1 = fminf(tb, c->t_far);
+  if (!(t1 > t0)) return 0;
+  const int R = m->res;
+  float cell[3], inv[3], invd[3];
+  int cc[3], step[3];
+  for (int i = 0; i < 3; ++i) {
+    const float size = c->box_max[i] - c->box_min[i];
+    cell[i] = size / (float)R;
+    inv[i] = (float)R / size;
+    invd[i] = (d[i] != 0.0f) ? (1.0f / d[i]) : INFINITY;
+    step[i] = d[i] > 0.0f ? 1 : (d[i] < 0.0f ? -1 : 0);
+    const float p = o[i] + t0 * d[i];
+    int ci = (int)floorf((p - c->box_min[i]) * inv[i]);
+    cc[i] = ci < 0 ? 0 : (ci > R - 1 ? R - 1 : ci);
+  }
+  uint32_t k = 0, n = 0;
+  for (int iter = 0; iter < 3 * R + 3; ++iter) {
+    float t_exit = t1;
+    int axis = -1;
+    for (int i = 0; i < 3; ++i) {
+      if (step[i] == 0) continue;
+      const float bound = c->box_min[i] + (float)(cc[i] + (step[i] > 0 ? 1 : 0)) * cell[i];
+      const float te = (bound - o[i]) * invd[i];
+      if (te < t_exit) {
+        t_exit = te;
+        axis = i;
+      }
+    }
+    const int occ = bit_at(bits, R, cc);
+    for (;;) {
+      const float tk = t0 + ((float)k + 0.5f) * m->dt;
+      if (!(tk < t_exit)) break;
+      if (occ) {
+        if (n >= m->max_steps) return (int)n;
+        t_out[n++] = tk;
+      }
+      ++k;
+    }
+    if (axis < 0) break;  /* the interval reached t1 */
+    cc[axis] += step[axis];
+    if (cc[axis] < 0 || cc[axis] >= R) break;
+  }
+  return (int)n;
+}
+
+/* Forward render of one ray: the marched samples in order, sigma and rgb from the MLP, front-to-back
+ * compositing (alpha as in ffnerf_OG.cl:1505-1520) stopped after the first sample that leaves
+ * T < T_stop; black background.  out = {r, g, b, T_final}; returns the samples evaluated. */
+int ora_render_ray(const ora_cfg* c, const ora_params* P, const ora_march_cfg* m, const uint32_t* bits,
+                   const float* ray, float* out) {
+  float* ts = (float*)malloc(sizeof(float) * (m->max_steps ? m->max_steps : 1));
+  const int n = ora_march_ray(c, m, bits, ray, ts);
+  float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
+  int used = 0;
+  for (int j = 0; j < n; ++j) {
+    float x[3], a0[ORA_M], sigma, rgb[3];
+    for (int i = 0; i < 3; ++i) x[i] = ray[i] + ts[j] * ray[4 + i];
+    ora_hash_encode(c, P->table, x, 1, a0, NULL, NULL);
+    ora_mlp_forward(c, P, a0, ray + 4, m->sh_multiplier, &sigma, rgb, NULL);
+    const float alpha = 1.0f - expf(fminf(fmaxf(-sigma * m->dt, -5.0f), 18.0f));
+    const float w = T * alpha;
+    for (int i = 0; i < 3; ++i) C[i] = C[i] + w * rgb[i];
+    T = T * (1.0f - alpha);
+    ++used;
+    if (T < m->T_stop) break;
+  }
+  out[0] = C[0];
+  out[1] = C[1];
+  out[2] = C[2];
+  out[3] = T;
+  free(ts);
+  return used;
+}

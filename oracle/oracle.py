@@ -71,6 +71,11 @@ class OraDebug(C.Structure):
     ]
 
 
+class OraMarchCfg(C.Structure):
+    _fields_ = [("res", C.c_int32), ("dt", C.c_float), ("max_steps", C.c_uint32), ("T_stop", C.c_float),
+                ("sh_multiplier", C.c_float)]
+
+
 def _build():
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
 
@@ -112,6 +117,11 @@ def load() -> C.CDLL:
     lib.ora_train_step.restype = C.c_int
     lib.ora_train_step.argtypes = [C.POINTER(OraCfg), C.POINTER(OraParams), _fp, _fp, _fp, C.c_int32, C.c_int32,
                                    C.POINTER(OraScalars), C.POINTER(OraDebug)]
+    lib.ora_occ_bitfield.argtypes = [_up, C.c_int32, C.c_uint32, _up]
+    lib.ora_march_ray.restype = C.c_int
+    lib.ora_march_ray.argtypes = [C.POINTER(OraCfg), C.POINTER(OraMarchCfg), _up, _fp, _fp]
+    lib.ora_render_ray.restype = C.c_int
+    lib.ora_render_ray.argtypes = [C.POINTER(OraCfg), C.POINTER(OraParams), C.POINTER(OraMarchCfg), _up, _fp, _fp]
     return lib
 
 
@@ -255,6 +265,27 @@ def adam(p, m, v, g, lr_t, beta1, beta2, eps):
     lib().ora_adam(fptr(p), fptr(m), fptr(v), fptr(g), p.size, lr_t, beta1, beta2, eps)
 
 
+def march_cfg(res, dt, max_steps, T_stop=0.0, sh_multiplier=1.0) -> OraMarchCfg:
+    m = OraMarchCfg()
+    m.res, m.dt, m.max_steps, m.T_stop, m.sh_multiplier = int(res), float(dt), int(max_steps), float(T_stop), \
+        float(sh_multiplier)
+    return m
+
+
+def occ_bitfield(occ: np.ndarray, G: int, q_min: int) -> np.ndarray:
+    R = 2 * G
+    bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
+    lib().ora_occ_bitfield(uptr(np.ascontiguousarray(occ, np.uint32)), G, q_min, uptr(bits))
+    return bits
+
+
+def march_ray(cfg: OraCfg, m: OraMarchCfg, bits: np.ndarray, ray: np.ndarray) -> np.ndarray:
+    ray = np.ascontiguousarray(ray, np.float32).reshape(8)
+    t = np.zeros(max(1, m.max_steps), np.float32)
+    n = lib().ora_march_ray(C.byref(cfg), C.byref(m), uptr(bits), fptr(ray), fptr(t))
+    return t[:n].copy()
+
+
 class OracleModel:
     """All state of one model on the CPU (float32 arrays), mirroring the device layout."""
 
@@ -279,6 +310,18 @@ class OracleModel:
         P.occ_in = uptr(self.p["occ_in"])
         P.occ_st = uptr(self.p["occ_st"])
         return P
+
+    def render(self, rays, bits, m: OraMarchCfg):
+        """Early-terminated forward render of every ray: (out [N,4] = rgb + T_final, samples used [N])."""
+        rays = np.ascontiguousarray(rays, np.float32).reshape(-1, 8)
+        out = np.zeros((rays.shape[0], 4), np.float32)
+        used = np.zeros(rays.shape[0], np.int32)
+        P = self._params()
+        for r in range(rays.shape[0]):
+            o = out[r]
+            used[r] = lib().ora_render_ray(C.byref(self.cfg), C.byref(P), C.byref(m), uptr(bits),
+                                           fptr(rays[r].copy()), o.ctypes.data_as(_fp))
+        return out, used
 
     def train_step(self, rays, targets, S, scalars: dict, taps=False):
         rays = np.ascontiguousarray(rays, np.float32).reshape(-1, 8)

@@ -119,3 +119,40 @@ class GpuModel:
                                               fl.stream_ptr()), "ffn_hash_encode_bwd")
         torch.cuda.synchronize()
         return to_np(grad)
+
+    def bitfield(self, occ: np.ndarray, G: int, q_min: int) -> np.ndarray:
+        occ_t = to_dev(np.ascontiguousarray(occ, np.uint32))
+        R = 2 * G
+        bits = torch.zeros((R ** 3 + 31) // 32, dtype=torch.int32, device=DEV)
+        fl.check(self.lib.ffn_occ_bitfield(fl.ptr(occ_t), G, q_min, fl.ptr(bits), fl.stream_ptr()),
+                 "ffn_occ_bitfield")
+        torch.cuda.synchronize()
+        return to_np(bits, np.uint32)
+
+    def march(self, rays, bits, mp, capacity=None):
+        rays_t = to_dev(np.ascontiguousarray(rays, np.float32).reshape(-1, 8))
+        bits_t = to_dev(np.ascontiguousarray(bits, np.uint32))
+        N = rays_t.shape[0]
+        cap = N * mp.max_steps if capacity is None else capacity
+        counts = torch.zeros(N, dtype=torch.int32, device=DEV)
+        offsets = torch.zeros(N, dtype=torch.int32, device=DEV)
+        samples = torch.zeros((max(cap, 1), 4), dtype=torch.float32, device=DEV)
+        ids = torch.zeros(max(cap, 1), dtype=torch.int32, device=DEV)
+        total = torch.zeros(4, dtype=torch.int32, device=DEV)
+        fl.check(self.lib.ffn_march(self.h.h, fl.ptr(rays_t), N, fl.ptr(bits_t), C.byref(mp), fl.ptr(counts),
+                                    fl.ptr(offsets), fl.ptr(samples), fl.ptr(ids), cap, fl.ptr(total),
+                                    fl.stream_ptr()), "ffn_march")
+        torch.cuda.synchronize()
+        return (to_np(counts, np.uint32), to_np(offsets, np.uint32), to_np(samples), to_np(ids, np.uint32),
+                int(to_np(total, np.uint32)[0]))
+
+    def render(self, rays, bits, mp):
+        rays_t = to_dev(np.ascontiguousarray(rays, np.float32).reshape(-1, 8))
+        bits_t = to_dev(np.ascontiguousarray(bits, np.uint32))
+        N = rays_t.shape[0]
+        out = torch.zeros((N, 4), dtype=torch.float32, device=DEV)
+        used = torch.zeros(N, dtype=torch.int32, device=DEV)
+        fl.check(self.lib.ffn_render(self.h.h, fl.ptr(rays_t), N, fl.ptr(bits_t), C.byref(mp), fl.ptr(out),
+                                     fl.ptr(used), fl.stream_ptr()), "ffn_render")
+        torch.cuda.synchronize()
+        return to_np(out), to_np(used)

@@ -17,7 +17,8 @@ def declared_functions():
 def test_header_declares_the_boundary():
     names = declared_functions()
     for n in ("ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step", "ffn_occ_decay", "ffn_sample",
-              "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam", "ffn_last_error", "ffn_version"):
+              "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam", "ffn_last_error", "ffn_version",
+              "ffn_occ_bitfield", "ffn_march", "ffn_render"):
         assert n in names
 
 
