@@ -118,6 +118,171 @@ def cpu_baseline(seconds=12.0):
                        f"{dt:.1f} s, 1 thread")
 
 
+def _timed(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def run_cfg3(args):
+    """hash-encoding microbench, 2^24 points, L16 F2 T=2^22 fp32, forward gather and
+    backward scatter-add, uniform and shell point distributions.  One JSON line per distribution."""
+    import ctypes as C
+    import torch
+    import ffn_lib as fl
+    import ffnerf_tools as ft
+    L, n = 16, int(args.points)
+    spec = ft.ModelSpec(n_levels=L, f_per_level=2, log2_T=[22] * L, res=ft.level_resolutions(L, 16.0, finest=2048.0),
+                        nd=1, nc=2, background="black", hash_opt="adam", init="xavier")
+    _, occ, _ = cfg2_spec()
+    h = fl.Handle(ft.spec_dict(spec, occ))
+    rng = np.random.default_rng(1)
+    table = torch.from_numpy(rng.uniform(-1e-4, 1e-4, spec.table_entries() * 2).astype(np.float32)).cuda()
+    occ_t = torch.zeros(64 ** 3, dtype=torch.int32, device="cuda")
+    P = fl.FfnParams()
+    dummies = {}
+    for i, (wn, bn) in enumerate(zip(fl.LAYER_NAMES, fl.BIAS_NAMES)):
+        if wn in spec.layer_shapes():
+            for k in ("W", "b", "mW", "vW", "mb", "vb"):
+                dummies[k + str(i)] = torch.zeros(4096, device="cuda")
+                getattr(P, k)[i] = fl.ptr(dummies[k + str(i)])
+    P.table, P.m_table, P.v_table, P.occ_in, P.occ_st = fl.ptr(table), fl.ptr(table), fl.ptr(table), \
+        fl.ptr(occ_t), fl.ptr(occ_t)
+    h.bind(P, keep=dict(dummies, table=table, occ=occ_t))
+    fwd_b, bwd_b, _, _ = algorithmic(spec)
+    LF = 2 * L
+    lines = []
+    for dist in ("uniform", "shell"):
+        if dist == "uniform":
+            x = rng.random((n, 3), dtype=np.float32)
+        else:
+            k = n // 10
+            v = rng.normal(size=(n - k, 3))
+            v /= np.linalg.norm(v, axis=1, keepdims=True)
+            r = rng.uniform(0.24, 0.26, (n - k, 1))
+            x = np.concatenate([0.5 + v * r, rng.random((k, 3))]).astype(np.float32)
+            x = x[rng.permutation(n)]
+        xt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+        a0 = torch.empty((n, LF), dtype=torch.float32, device="cuda")
+        g = torch.randn((n, LF), dtype=torch.float32, device="cuda", generator=torch.Generator("cuda").manual_seed(1))
+        grad = torch.zeros(spec.table_entries() * 2, dtype=torch.float32, device="cuda")
+        sp = fl.stream_ptr()
+        fwd = lambda: fl.check(h.lib.ffn_hash_encode_fwd(h.h, fl.ptr(xt), n, fl.ptr(a0), None, sp))
+        bwd = lambda: fl.check(h.lib.ffn_hash_encode_bwd(h.h, fl.ptr(xt), fl.ptr(g), n, fl.ptr(grad), sp))
+        t_f = _timed(fwd, args.steps, args.warmup)
+        t_b = _timed(bwd, args.steps, args.warmup)
+        line = {"metric": "hash-grid gather/scatter HBM GB/s (algorithmic bytes)", "workload": f"cfg3-{dist}",
+                "value": (fwd_b + bwd_b) * n / ((t_f + t_b) * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1,
+                "higher_is_better": True, "dtype": "fp32", "data": "synthetic",
+                "config": {"workload": f"BASELINE configs[3] ({dist}): 2^{int(np.log2(n))} points, L16 F2 T2^22 "
+                                       f"fp32 table, res 16->2048", "points": n},
+                "fwd": {"ms": t_f, "points_per_s": n / (t_f * 1e-3), "GBps": fwd_b * n / (t_f * 1e-3) / 1e9,
+                        "frac": fwd_b * n / (t_f * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_point": fwd_b},
+                "bwd": {"ms": t_b, "points_per_s": n / (t_b * 1e-3), "GBps": bwd_b * n / (t_b * 1e-3) / 1e9,
+                        "frac": bwd_b * n / (t_b * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_point": bwd_b},
+                "note": "fp16 tables are not built"}
+        print(json.dumps(line), flush=True)
+        lines.append(line)
+        del xt, a0, g, grad
+    h.close()
+    return lines
+
+
+def shell_bitfield(R, seed=4, radius=0.3, thickness=0.02, noise=0.007):
+    """BASELINE configs[4] bitfield: the cells whose centre lies in a shell around the box centre, plus seeded
+    isolated cells (R^3 bits, x fastest, 32 per word)."""
+    rng = np.random.default_rng(seed)
+    c = (np.arange(R, dtype=np.float32) + 0.5) / R
+    bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
+    set_cells = 0
+    for z in range(R):  # slab by slab to bound host memory
+        yy, xx = np.meshgrid(c, c, indexing="ij")
+        rad = np.sqrt((xx - 0.5) ** 2 + (yy - 0.5) ** 2 + (c[z] - 0.5) ** 2)
+        occ = (np.abs(rad - radius) <= 0.5 * thickness) | (rng.random((R, R)) < noise)
+        idx = np.nonzero(occ.reshape(-1))[0].astype(np.int64) + z * R * R
+        set_cells += idx.size
+        np.bitwise_or.at(bits, idx >> 5, (np.uint32(1) << (idx & 31).astype(np.uint32)))
+    return bits, set_cells / R ** 3
+
+
+def run_cfg4(args):
+    """256^3 bitfield (~3% set, shell), 2^20 rays, <= 1024 steps/ray, early termination at
+    T < 1e-4, cfg1 MLPs (forward render); and Adam over 16 x 2^22 x 2 table params with sparse gradients."""
+    import ctypes as C
+    import tempfile
+    import torch
+    import ffn_lib as fl
+    import ffnerf_tools as ft
+    import synthetic_scene as sc
+    spec, occ, _ = cfg2_spec("fp32")
+    nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_bench4_"), "bench4", spec=spec, occ=occ, rng_seed=0)
+    R, n_rays, max_steps = 256, int(args.rays4), 1024
+    dt = float(np.float32(np.sqrt(3.0) / max_steps))
+    bits_np, frac = shell_bitfield(R)
+    bits = torch.from_numpy(bits_np.view(np.int32)).cuda()
+    rng = np.random.default_rng(5)
+    rays, _ = sc.uniform_batch(sc.cameras_for("cfg1"), n_rays, rng)
+    io = ft.RayBatch.init(n_rays, 1)
+    io.upload_rays(rays)
+    used = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    chunk = int(args.chunk)
+    render = lambda: nerf.render_marched(io, bits, R, dt, max_steps=max_steps, T_stop=1e-4, chunk=chunk,
+                                         n_samples=used)
+    t_r = _timed(render, max(1, args.steps // 3), 1)
+    n_smp = int(used.sum().item())
+    # march + compaction alone (full march, no termination)
+    lib, h = nerf.handle.lib, nerf.handle.h
+    mp = fl.march_params(R, dt, max_steps)
+    counts = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    offs = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    total = torch.zeros(4, dtype=torch.int32, device="cuda")
+    fl.check(lib.ffn_march(h, fl.ptr(io.rays_buf), n_rays, fl.ptr(bits), C.byref(mp), fl.ptr(counts), fl.ptr(offs),
+                           None, None, 0, fl.ptr(total), fl.stream_ptr()))
+    torch.cuda.synchronize()
+    cap = int(total[0].item())
+    smp = torch.empty((max(cap, 1), 4), dtype=torch.float32, device="cuda")
+    ids = torch.empty(max(cap, 1), dtype=torch.int32, device="cuda")
+    march = lambda: fl.check(lib.ffn_march(h, fl.ptr(io.rays_buf), n_rays, fl.ptr(bits), C.byref(mp), fl.ptr(counts),
+                                           fl.ptr(offs), fl.ptr(smp), fl.ptr(ids), cap, fl.ptr(total),
+                                           fl.stream_ptr()))
+    t_m = _timed(march, args.steps, args.warmup)
+    march_bytes = n_rays * (32 + 8) + cap * (16 + 4)
+    # Adam over the cfg4 table with sparse gradients (5% of the rows non-zero, N(0, 1e-3))
+    n_par = 16 * (1 << 22) * 2
+    p = torch.empty(n_par, dtype=torch.float32, device="cuda").uniform_(-1e-4, 1e-4)
+    m = torch.zeros_like(p)
+    v = torch.zeros_like(p)
+    g = torch.zeros(n_par // 2, 2, dtype=torch.float32, device="cuda")
+    rows = torch.rand(n_par // 2, device="cuda") < 0.05
+    g[rows] = torch.randn(int(rows.sum().item()), 2, device="cuda") * 1e-3
+    g = g.reshape(-1)
+    adam = lambda: fl.check(lib.ffn_adam(fl.ptr(p), fl.ptr(m), fl.ptr(v), fl.ptr(g), n_par, 1e-3, 0.9, 0.99, 1e-15, 0,
+                                         fl.stream_ptr()))
+    t_a = _timed(adam, args.steps, args.warmup)
+    line = {"metric": "forward render rays/s with DDA march + early termination (cfg4)", "workload": "cfg4",
+            "value": n_rays / (t_r * 1e-3), "unit": "rays/s", "n_gpus": 1, "higher_is_better": True,
+            "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "BASELINE configs[4]: 256^3 bitfield shell r=0.3 t=0.02 + seeded cells, "
+                                   "2^20 rays, <=1024 steps/ray, T_stop 1e-4, cfg1 MLPs; Adam over 16x2^22x2 params, "
+                                   "5% rows N(0,1e-3)", "rays": n_rays, "bits_set_frac": frac, "chunk": chunk},
+            "render": {"ms": t_r, "samples": n_smp, "samples_per_s": n_smp / (t_r * 1e-3)},
+            "march": {"ms": t_m, "samples": cap, "GBps": march_bytes / (t_m * 1e-3) / 1e9,
+                      "frac": march_bytes / (t_m * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                      "bytes": "40 B/ray (ray + offset, count) + 20 B/sample (xyz t + ray id)"},
+            "adam": {"ms": t_a, "params": n_par, "GBps": 28 * n_par / (t_a * 1e-3) / 1e9,
+                     "frac": 28 * n_par / (t_a * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+    print(json.dumps(line), flush=True)
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -127,6 +292,11 @@ def main():
     ap.add_argument("--rays", type=int, default=1 << 18)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"],
+                    help="cfg2 (default): the training step; cfg3: hash microbench; cfg4: marched render + Adam")
+    ap.add_argument("--points", type=int, default=1 << 24, help="cfg3 points")
+    ap.add_argument("--rays4", type=int, default=1 << 20, help="cfg4 rays")
+    ap.add_argument("--chunk", type=int, default=64, help="cfg4 samples per ray per render round")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this size (a known-traffic kernel for PMC scaling)")
     args = ap.parse_args()
@@ -138,6 +308,13 @@ def main():
     import torch
     import ffnerf_tools as ft
     import synthetic_scene as sc
+
+    if args.workload == "cfg3":
+        run_cfg3(args)
+        return
+    if args.workload == "cfg4":
+        run_cfg4(args)
+        return
 
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4

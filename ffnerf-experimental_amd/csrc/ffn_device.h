@@ -251,27 +251,91 @@ __device__ __forceinline__ bool is_left(int lid, int stride) {
   return ((lid + 1 + stride) & (2 * stride - 1)) == 0;
 }
 
+// Lane movement of the trees.  At stride s the "right" lane of every aligned
+// 2s-lane block reads its partner s lanes below and the "left" lane reads the
+// one s lanes above.  Inside a 16-lane row (s <= 8) that is a DPP row shift;
+// for s = 16 and 32 the lower partner of the served lanes (31, 63 and 63) is
+// what DPP row_bcast:15 / row_bcast:31 deliver; only the upward moves at
+// s = 16 and 32 use ds_bpermute.  Lanes that are not served get unspecified
+// values, exactly as the tree ignores them.
+template <int S_>
+__device__ __forceinline__ float from_lower(float v) {
+  const int x = __float_as_int(v);
+  int r;
+  if constexpr (S_ < 16)
+    r = __builtin_amdgcn_update_dpp(x, x, 0x110 + S_, 0xF, 0xF, false);  // row_shr:S_
+  else if constexpr (S_ == 16)
+    r = __builtin_amdgcn_update_dpp(x, x, 0x142, 0xF, 0xF, false);  // row_bcast:15
+  else
+    r = __builtin_amdgcn_update_dpp(x, x, 0x143, 0xF, 0xF, false);  // row_bcast:31
+  return __int_as_float(r);
+}
+template <int S_>
+__device__ __forceinline__ float from_upper(float v) {
+  if constexpr (S_ < 16) {
+    const int x = __float_as_int(v);
+    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x100 + S_, 0xF, 0xF, false));  // row_shl:S_
+  } else {
+    return __shfl(v, (int)(threadIdx.x & 63) + S_);
+  }
+}
+
+template <int ST>
+__device__ __forceinline__ void scan_add_up(float& v, int lid, int S) {
+  if (ST < S) {
+    const float o = from_lower<ST>(v);
+    if (is_right(lid, ST)) v = v + o;
+  }
+}
+template <int ST>
+__device__ __forceinline__ void scan_add_down(float& v, int lid, int S) {
+  if (ST < S) {
+    const float from_l = from_lower<ST>(v);
+    const float from_r = from_upper<ST>(v);
+    if (is_right(lid, ST)) v = v + from_l;
+    else if (is_left(lid, ST)) v = from_r;
+  }
+}
+
 __device__ __forceinline__ float seg_scan_excl_add(float v, int lid, int S, int base) {
-  for (int stride = 1; stride < S; stride <<= 1) {
-    float o = __shfl(v, base + lid - stride);
-    if (is_right(lid, stride)) v = v + o;
-  }
+  (void)base;
+  scan_add_up<1>(v, lid, S);
+  scan_add_up<2>(v, lid, S);
+  scan_add_up<4>(v, lid, S);
+  scan_add_up<8>(v, lid, S);
+  scan_add_up<16>(v, lid, S);
+  scan_add_up<32>(v, lid, S);
   if (lid == S - 1) v = 0.0f;
-  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
-    float from_l = __shfl(v, base + lid - stride);
-    float from_r = __shfl(v, base + lid + stride);
-    if (is_right(lid, stride)) v = v + from_l;
-    else if (is_left(lid, stride)) v = from_r;
-  }
+  scan_add_down<32>(v, lid, S);
+  scan_add_down<16>(v, lid, S);
+  scan_add_down<8>(v, lid, S);
+  scan_add_down<4>(v, lid, S);
+  scan_add_down<2>(v, lid, S);
+  scan_add_down<1>(v, lid, S);
   return v;
 }
 
 // ffnerf_OG.cl:639-646: a[lid] += a[lid + stride] for lid < stride; result a[0] broadcast
-__device__ __forceinline__ float seg_reduce_add(float v, int lid, int S, int base) {
-  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
-    float o = __shfl(v, base + lid + stride);
-    if (lid < stride) v = v + o;
+template <int ST>
+__device__ __forceinline__ void reduce_add_step(float& v, int lid, int S) {
+  if (ST < S) {
+    float o;
+    if constexpr (ST < 16) {
+      const int x = __float_as_int(v);
+      o = __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x100 + ST, 0xF, 0xF, false));  // row_shl:ST
+    } else {
+      o = __shfl_xor(v, ST);
+    }
+    if (lid < ST) v = v + o;
   }
+}
+__device__ __forceinline__ float seg_reduce_add(float v, int lid, int S, int base) {
+  reduce_add_step<32>(v, lid, S);
+  reduce_add_step<16>(v, lid, S);
+  reduce_add_step<8>(v, lid, S);
+  reduce_add_step<4>(v, lid, S);
+  reduce_add_step<2>(v, lid, S);
+  reduce_add_step<1>(v, lid, S);
   return __shfl(v, base);
 }
 
@@ -294,24 +358,50 @@ __device__ __forceinline__ Seg shfl_seg(const Seg& s, int src) {
   o.v2 = __shfl(s.v2, src);
   return o;
 }
+template <int ST>
+__device__ __forceinline__ Seg seg_lower(const Seg& s) {
+  return Seg{from_lower<ST>(s.a), from_lower<ST>(s.v0), from_lower<ST>(s.v1), from_lower<ST>(s.v2)};
+}
+template <int ST>
+__device__ __forceinline__ Seg seg_upper(const Seg& s) {
+  return Seg{from_upper<ST>(s.a), from_upper<ST>(s.v0), from_upper<ST>(s.v1), from_upper<ST>(s.v2)};
+}
+template <int ST>
+__device__ __forceinline__ void seg_up(Seg& v, int lid, int S) {
+  if (ST < S) {
+    const Seg o = seg_lower<ST>(v);
+    if (is_right(lid, ST)) v = seg_combine(o, v);
+  }
+}
+template <int ST>
+__device__ __forceinline__ void seg_down(Seg& v, int lid, int S) {
+  if (ST < S) {
+    const Seg from_l = seg_lower<ST>(v);
+    const Seg from_r = seg_upper<ST>(v);
+    if (is_right(lid, ST)) v = seg_combine(from_l, v);
+    else if (is_left(lid, ST)) v = from_r;
+  }
+}
 
 // exclusive Seg scan; returns the lane's prefix, total of the segment in *total
 __device__ __forceinline__ Seg seg_scan_excl_seg(Seg v, int lid, int S, int base, Seg* total) {
-  for (int stride = 1; stride < S; stride <<= 1) {
-    Seg o = shfl_seg(v, base + lid - stride);
-    if (is_right(lid, stride)) v = seg_combine(o, v);
-  }
+  seg_up<1>(v, lid, S);
+  seg_up<2>(v, lid, S);
+  seg_up<4>(v, lid, S);
+  seg_up<8>(v, lid, S);
+  seg_up<16>(v, lid, S);
+  seg_up<32>(v, lid, S);
   *total = shfl_seg(v, base + S - 1);
   if (lid == S - 1) {
     v.a = 1.0f;
     v.v0 = v.v1 = v.v2 = 0.0f;
   }
-  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
-    Seg from_l = shfl_seg(v, base + lid - stride);
-    Seg from_r = shfl_seg(v, base + lid + stride);
-    if (is_right(lid, stride)) v = seg_combine(from_l, v);
-    else if (is_left(lid, stride)) v = from_r;
-  }
+  seg_down<32>(v, lid, S);
+  seg_down<16>(v, lid, S);
+  seg_down<8>(v, lid, S);
+  seg_down<4>(v, lid, S);
+  seg_down<2>(v, lid, S);
+  seg_down<1>(v, lid, S);
   return v;
 }
 
@@ -330,22 +420,41 @@ __device__ __forceinline__ Aff shfl_aff(const Aff& s, int src) {
   o.b = __shfl(s.b, src);
   return o;
 }
+template <int ST>
+__device__ __forceinline__ void aff_up(Aff& v, int lid, int S) {
+  if (ST < S) {
+    const Aff o{from_lower<ST>(v.a), from_lower<ST>(v.b)};
+    if (is_right(lid, ST)) v = aff_combine_rev(o, v);
+  }
+}
+template <int ST>
+__device__ __forceinline__ void aff_down(Aff& v, int lid, int S) {
+  if (ST < S) {
+    const Aff from_l{from_lower<ST>(v.a), from_lower<ST>(v.b)};
+    const Aff from_r{from_upper<ST>(v.a), from_upper<ST>(v.b)};
+    if (is_right(lid, ST)) v = aff_combine_rev(from_l, v);
+    else if (is_left(lid, ST)) v = from_r;
+  }
+}
 // exclusive scan with aff_combine_rev over the segment's lanes in lane order
 __device__ __forceinline__ Aff seg_scan_excl_aff_rev(Aff v, int lid, int S, int base) {
-  for (int stride = 1; stride < S; stride <<= 1) {
-    Aff o = shfl_aff(v, base + lid - stride);
-    if (is_right(lid, stride)) v = aff_combine_rev(o, v);
-  }
+  (void)base;
+  aff_up<1>(v, lid, S);
+  aff_up<2>(v, lid, S);
+  aff_up<4>(v, lid, S);
+  aff_up<8>(v, lid, S);
+  aff_up<16>(v, lid, S);
+  aff_up<32>(v, lid, S);
   if (lid == S - 1) {
     v.a = 1.0f;
     v.b = 0.0f;
   }
-  for (int stride = S >> 1; stride >= 1; stride >>= 1) {
-    Aff from_l = shfl_aff(v, base + lid - stride);
-    Aff from_r = shfl_aff(v, base + lid + stride);
-    if (is_right(lid, stride)) v = aff_combine_rev(from_l, v);
-    else if (is_left(lid, stride)) v = from_r;
-  }
+  aff_down<32>(v, lid, S);
+  aff_down<16>(v, lid, S);
+  aff_down<8>(v, lid, S);
+  aff_down<4>(v, lid, S);
+  aff_down<2>(v, lid, S);
+  aff_down<1>(v, lid, S);
   return v;
 }
 

@@ -440,6 +440,21 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     }
     const float dt_b = valid ? a.DTs[b] : 0.0f;
     const float t_b = valid ? a.Ts[b] : 0.0f;
+    // per-sample inputs of the compositing (lane j = sample j of the tile), loaded before the forward so
+    // that their latency hides behind it
+    const int64_t bj = tile * 64 + lane;
+    const bool vj = (uint64_t)bj < n_samples;
+    const int64_t rj = vj ? (bj >> log2S) : 0;
+    const float dt_j = vj ? a.DTs[bj] : 0.0f;
+    float4 tg = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (vj && a.targets) tg = a.targets[rj];
+    const bool proposals = train && a.occ_strength > 0.0f;
+    float t_j = 0.0f;
+    uint64_t segmask = 0;
+    if (proposals && vj) {
+      t_j = a.Ts[bj];
+      segmask = (uint64_t)a.flags[2 * rj] | ((uint64_t)a.flags[2 * rj + 1] << 32);
+    }
 
     floatx4 hd[ND][4];
     floatx4 acin[2];  // [dout(16) | SH*mult(16)] as two D-layout tiles
@@ -462,14 +477,10 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     float dLds_j, dLdc_j[3];
     {
       const int j = lane;
-      const int64_t bj = tile * 64 + j;
-      const bool vj = (uint64_t)bj < n_samples;
       const int lid = j & (S - 1);
       const int base = j - lid;
-      const int64_t rj = vj ? (bj >> log2S) : 0;
       const float sig_j = sSig[j];
       const float c0 = sRgb[3 * j], c1 = sRgb[3 * j + 1], c2 = sRgb[3 * j + 2];
-      const float dt_j = vj ? a.DTs[bj] : 0.0f;
       float alpha = 0.0f;
       if (dt_j > 0.0f) alpha = 1.0f - expf(fminf(fmaxf(-sig_j * dt_j, -5.0f), 18.0f));
       const float oma = 1.0f - alpha;
@@ -492,8 +503,6 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
           bg[2] = rand01(rb);
         }
       }
-      float4 tg = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (vj && a.targets) tg = a.targets[rj];
       const float Cf0 = tot.v0 + T_final * bg[0];
       const float Cf1 = tot.v1 + T_final * bg[1];
       const float Cf2 = tot.v2 + T_final * bg[2];
@@ -547,10 +556,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
       {
         // occupancy proposals for run-representative samples (ffnerf_OG.cl:1640-1821); every wavefront
         // holds the whole ray here and handles the proposals of its own 16 samples
-        if (train && a.occ_strength > 0.0f) {
-          const float t_j = vj ? a.Ts[bj] : 0.0f;
-          uint64_t segmask = 0;
-          if (vj) segmask = (uint64_t)a.flags[2 * rj] | ((uint64_t)a.flags[2 * rj + 1] << 32);
+        if (proposals) {
           const int nxt = find_next_flag(segmask, lid, S);
           const int prev_end = lid > 0 ? lid - 1 : 0;
           const int last = nxt < S ? nxt - 1 : S - 1;

@@ -505,6 +505,34 @@ class Nerf:
             ev.synchronize()
         return None, ev
 
+    # -- forward render with the DDA marcher (no counterpart in the reference) --
+    def occupancy_bitfield(self, q_min: int = 4, out=None):
+        """Bitfield of the (2G)^3 occupancy subcells with q >= q_min (q = nibble + 1).  The default keeps
+        the subcells the reference's inference sampler gives non-zero weight (q_infer > 0, i.e. nibble >= 3,
+        ffnerf_OG.cl:1116)."""
+        torch = _torch()
+        G = int(self.occ.G_occ)
+        R = 2 * G
+        if out is None:
+            out = torch.zeros((R ** 3 + 31) // 32, dtype=torch.int32, device=self.device)
+        fl.check(self.handle.lib.ffn_occ_bitfield(fl.ptr(self.t["occ_in"]), G, int(q_min), fl.ptr(out),
+                                                  fl.stream_ptr()), "ffn_occ_bitfield")
+        return out
+
+    def render_marched(self, io: RayBatch, bits, res: int, dt: float, max_steps: int = 1024, T_stop: float = 1e-4,
+                       chunk: int = 32, sh_multiplier: float = 1.0, n_samples=None, stream=None):
+        """Forward-only render of io's rays: bitfield DDA march, MLPs, front-to-back compositing stopped at
+        T < T_stop.  io.out_buf gets {r, g, b, T_final} per ray (black background)."""
+        mp = fl.march_params(res, dt, max_steps, T_stop=T_stop, chunk=chunk, sh_multiplier=sh_multiplier)
+        fl.check(self.handle.lib.ffn_render(self.handle.h, fl.ptr(io.rays_buf), io.num_rays, fl.ptr(bits),
+                                            C.byref(mp), fl.ptr(io.out_buf), fl.ptr(n_samples),
+                                            fl.stream_ptr(stream)), "ffn_render")
+        torch = _torch()
+        ev = torch.cuda.Event()
+        ev.record()
+        io.ev_last = ev
+        return ev
+
     # -- checkpoints (npz layout of ffnerf_tools.py:989-1189) --------------
     def _model_paths(self, save_id: str):
         td = self.training_dir
