@@ -291,6 +291,7 @@ def main():
     ap.add_argument("--mlp", default="fp32", choices=["fp32", "fp16"])
     ap.add_argument("--rays", type=int, default=1 << 18)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fp16-line", action="store_true", help="skip the fp16-MLP path measurement")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"],
                     help="cfg2 (default): the training step; cfg3: hash microbench; cfg4: marched render + Adam")
@@ -394,6 +395,29 @@ def main():
         "stages_ms_avg": {k: round(v, 4) for k, v in avg.items()},
         "stage_rooflines": {k: {"achieved": v[1], "unit": v[3], "frac": v[1] / v[2]} for k, v in per.items()},
     }
+    if args.mlp == "fp32" and not args.no_fp16_line:
+        # the same step with the fp16/bf16-MFMA MLP (BASELINE reports both paths), same resident batches
+        spec16, _, _ = cfg2_spec("fp16")
+        nerf16 = ft.Nerf(tempfile.mkdtemp(prefix="ffn_bench16_"), "bench16", spec=spec16, occ=occ, rng_seed=0)
+        for i in range(args.warmup):
+            nerf16.step(pool[i % len(pool)], lr_f=1e-2, do_train=True, occ_update_strength=1.0)
+        torch.cuda.synchronize()
+        nerf16.handle.set_profiling(True)
+        nerf16.handle.stage_times(reset=True)
+        t2 = time.perf_counter()
+        for i in range(args.steps):
+            nerf16.step(pool[(args.warmup + i) % len(pool)], lr_f=1e-2, do_train=True, occ_update_strength=1.0)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        st16 = nerf16.handle.stage_times(reset=True)
+        avg16 = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in st16.items()}
+        line["fp16_mlp_path"] = {
+            "value": N * args.steps / (t3 - t2), "unit": "samples/s", "ms_per_step": (t3 - t2) * 1e3 / args.steps,
+            "dtype": "fp16/bf16-mfma, fp32 accumulate", "stages_ms_avg": {k: round(v, 4) for k, v in avg16.items()},
+            "mlp_tflops": mlp_flops * N / (avg16["mlp"] * 1e-3) / 1e12,
+            "mlp_frac_of_fp16_peak": mlp_flops * N / (avg16["mlp"] * 1e-3) / 1e12 / FP16_PEAK_TFLOPS}
+        print(f"[bench] fp16-MLP path: {(t3 - t2) * 1e3 / args.steps:.2f} ms/step", flush=True)
+        del nerf16
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:
         print("[bench] timing the CPU oracle on a bounded sample", flush=True)
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -127,7 +127,8 @@ int validate_config(const ffn_config* c, int64_t* table_entries) {
     if (!(c->box_max[i] > c->box_min[i])) return fail(-1, "box_max must exceed box_min on every axis");
   if (c->background < 0 || c->background > 2) return fail(-1, "background=%d unknown", c->background);
   if (c->hash_opt != FFN_HASH_SGD && c->hash_opt != FFN_HASH_ADAM) return fail(-1, "hash_opt=%d unknown", c->hash_opt);
-  if (c->mlp_precision != FFN_MLP_FP32) return fail(-1, "mlp_precision=%d not built (fp32 only)", c->mlp_precision);
+  if (c->mlp_precision != FFN_MLP_FP32 && c->mlp_precision != FFN_MLP_FP16)
+    return fail(-1, "mlp_precision=%d unknown", c->mlp_precision);
   return 0;
 }
 
@@ -339,7 +340,8 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   if (train && !targets) return fail(-1, "training needs targets");
   if (train && sc->occ_strength > 0.0f && !h->params.occ_st) return fail(-1, "proposals need occ_st");
   const int LF = h->dc.LF;
-  if (!ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
+  const bool mlp16 = h->cfg.mlp_precision == FFN_MLP_FP16;
+  if (mlp16 ? !ffn::mlp16_supported(LF, h->cfg.nd, h->cfg.nc) : !ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
     return fail(-2, "MLP shape LF=%d nd=%d nc=%d is not built", LF, h->cfg.nd, h->cfg.nc);
   hipStream_t st = (hipStream_t)stream;
   int log2S = 0;
@@ -416,7 +418,10 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   }
   {
     StageTimer tm(h, 2, st);
-    FFN_HIP(ffn::launch_mlp(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+    if (mlp16)
+      FFN_HIP(ffn::launch_mlp16(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+    else
+      FFN_HIP(ffn::launch_mlp(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
   }
 
   if (taps) {

@@ -197,6 +197,9 @@ hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, co
 bool mlp_supported(int LF, int nd, int nc);
 size_t mlp_lds_bytes(int LF, int nd, int nc);
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+// the same step on fp16 (forward) / bf16 (backward, weight gradients) MFMAs with fp32 accumulation
+bool mlp16_supported(int LF, int nd, int nc);
+hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
 
 // sum the per-block gradient partials and apply Adam to the MLP parameters
 struct MlpOptArgs {

@@ -27,19 +27,12 @@
 //     reference's ~1.8 KB/sample SoA traffic).
 #include "ffn_device.h"
 #include "ffn_kernels.h"
+#include "ffn_mlp_common.h"
 
 namespace ffn {
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// Make LDS writes of this wavefront visible to its own later LDS reads and
-// keep the compiler from moving LDS accesses across this point.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <int LF_, int ND_, int NC_>
@@ -410,11 +403,8 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     for (int e = tid; e < A::g_total(); e += 256) sG[e] = 0.0f;
   __syncthreads();
 
-  float Dhalf;
-  {
-    const float dx = c.bmax[0] - c.bmin[0], dy = c.bmax[1] - c.bmin[1], dz = c.bmax[2] - c.bmin[2];
-    Dhalf = 0.5f * sqrtf(dx * dx + dy * dy + dz * dz);
-  }
+  const float Dhalf = half_box_diagonal(c);
+  const bool proposals = train && a.occ_strength > 0.0f;
 
   constexpr bool REG_ACC = acc_tiles<LF, ND, NC>() <= 48;
   AccSet<LF, ND, NC, REG_ACC> ga;
@@ -442,19 +432,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     const float t_b = valid ? a.Ts[b] : 0.0f;
     // per-sample inputs of the compositing (lane j = sample j of the tile), loaded before the forward so
     // that their latency hides behind it
-    const int64_t bj = tile * 64 + lane;
-    const bool vj = (uint64_t)bj < n_samples;
-    const int64_t rj = vj ? (bj >> log2S) : 0;
-    const float dt_j = vj ? a.DTs[bj] : 0.0f;
-    float4 tg = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (vj && a.targets) tg = a.targets[rj];
-    const bool proposals = train && a.occ_strength > 0.0f;
-    float t_j = 0.0f;
-    uint64_t segmask = 0;
-    if (proposals && vj) {
-      t_j = a.Ts[bj];
-      segmask = (uint64_t)a.flags[2 * rj] | ((uint64_t)a.flags[2 * rj + 1] << 32);
-    }
+    const CompLane CL = load_comp_lane(a, tile, lane, n_samples, log2S, proposals);
 
     floatx4 hd[ND][4];
     floatx4 acin[2];  // [dout(16) | SH*mult(16)] as two D-layout tiles
@@ -475,176 +453,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     // ------------------------------------------------------------------
     // compositing on 64 lanes: lane j = sample j of the tile (every wave)
     float dLds_j, dLdc_j[3];
-    {
-      const int j = lane;
-      const int lid = j & (S - 1);
-      const int base = j - lid;
-      const float sig_j = sSig[j];
-      const float c0 = sRgb[3 * j], c1 = sRgb[3 * j + 1], c2 = sRgb[3 * j + 2];
-      float alpha = 0.0f;
-      if (dt_j > 0.0f) alpha = 1.0f - expf(fminf(fmaxf(-sig_j * dt_j, -5.0f), 18.0f));
-      const float oma = 1.0f - alpha;
-      Seg my;
-      my.a = oma;
-      my.v0 = alpha * c0;
-      my.v1 = alpha * c1;
-      my.v2 = alpha * c2;
-      Seg tot;
-      const Seg pre = seg_scan_excl_seg(my, lid, S, base, &tot);
-      const float Tr = pre.a, T_final = tot.a;
-      float bg[3] = {0.0f, 0.0f, 0.0f};
-      if (train) {
-        if (c.background == FFN_BG_WHITE) {
-          bg[0] = bg[1] = bg[2] = 1.0f;
-        } else if (c.background == FFN_BG_RANDOM) {
-          uint32_t rb = hash_u32(a.seed ^ (uint32_t)rj * 747796405u ^ 0xA511E9B3u);
-          bg[0] = rand01(rb);
-          bg[1] = rand01(rb);
-          bg[2] = rand01(rb);
-        }
-      }
-      const float Cf0 = tot.v0 + T_final * bg[0];
-      const float Cf1 = tot.v1 + T_final * bg[1];
-      const float Cf2 = tot.v2 + T_final * bg[2];
-      const float gr0 = charbonnier_prime(Cf0 - tg.x);
-      const float gr1 = charbonnier_prime(Cf1 - tg.y);
-      const float gr2 = charbonnier_prime(Cf2 - tg.z);
-      const float gT_end = gr0 * bg[0] + gr1 * bg[1] + gr2 * bg[2];
-      if (wave == 0 && lid == 0 && vj)
-        a.out_rgb[rj] = make_float4(fminf(fmaxf(Cf0, 0.0f), 1.0f), fminf(fmaxf(Cf1, 0.0f), 1.0f),
-                                    fminf(fmaxf(Cf2, 0.0f), 1.0f), train ? 4.0f : 0.0f);
-      const float ws = Tr * alpha;
-      dLdc_j[0] = ws * gr0;
-      dLdc_j[1] = ws * gr1;
-      dLdc_j[2] = ws * gr2;
-      Aff f;
-      f.a = oma;
-      f.b = gr0 * (alpha * c0) + gr1 * (alpha * c1) + gr2 * (alpha * c2);
-      const Aff f_rev = shfl_aff(f, base + (S - 1 - lid));  // lane k holds the element of sample S-1-k
-      const Aff scn = seg_scan_excl_aff_rev(f_rev, lid, S, base);
-      const int m = (lid <= S - 2) ? (S - 2 - lid) : 0;
-      const Aff sm = shfl_aff(scn, base + m);
-      const Aff em = shfl_aff(f_rev, base + m);
-      float gT_next = gT_end;
-      if (lid <= S - 2) {
-        const Aff incl = aff_combine_rev(sm, em);
-        gT_next = incl.a * gT_end + incl.b;
-      }
-      const float gA = gr0 * (Tr * c0) + gr1 * (Tr * c1) + gr2 * (Tr * c2);
-      const float gAlpha = gA - gT_next * Tr;
-      const float dads = (dt_j > 0.0f) ? (dt_j * oma) : 0.0f;
-      const float regu = (dt_j > 0.0f) ? (5e-3f * dt_j / (float)(uint32_t)S) : 0.0f;
-      dLds_j = gAlpha * dads + regu;
-
-      if (wave == 0) {
-        if (vj) {
-          if (a.t_sigma) a.t_sigma[bj] = sig_j;
-          if (a.t_rgb) {
-            a.t_rgb[3 * bj] = c0;
-            a.t_rgb[3 * bj + 1] = c1;
-            a.t_rgb[3 * bj + 2] = c2;
-          }
-          if (a.t_Tr) a.t_Tr[bj] = Tr;
-          if (a.t_dLds) a.t_dLds[bj] = dLds_j;
-          if (a.t_dLdc) {
-            a.t_dLdc[3 * bj] = dLdc_j[0];
-            a.t_dLdc[3 * bj + 1] = dLdc_j[1];
-            a.t_dLdc[3 * bj + 2] = dLdc_j[2];
-          }
-        }
-      }
-      {
-        // occupancy proposals for run-representative samples (ffnerf_OG.cl:1640-1821); every wavefront
-        // holds the whole ray here and handles the proposals of its own 16 samples
-        if (proposals) {
-          const int nxt = find_next_flag(segmask, lid, S);
-          const int prev_end = lid > 0 ? lid - 1 : 0;
-          const int last = nxt < S ? nxt - 1 : S - 1;
-          const int nsrc = nxt < S ? nxt : lid;
-          const float t_prev = __shfl(t_j, base + prev_end), T_prev = __shfl(Tr, base + prev_end);
-          const float t_last = __shfl(t_j, base + last), T_last = __shfl(Tr, base + last);
-          const float t_nx = __shfl(t_j, base + nsrc), T_nx = __shfl(Tr, base + nsrc);
-          const bool is_rep = (segmask >> lid) & 1ull;
-          if (vj && is_rep && dt_j > 0.0f && (j >> 4) == wave) {
-            const float4 ro = a.rays[2 * rj], rdv = a.rays[2 * rj + 1];
-            const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
-            const int G = c.G;
-            float gpos[3], cell_size[3];
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-              const float bs = c.bmax[i] - c.bmin[i];
-              const float xi = o[i] + t_j * d[i];
-              gpos[i] = (xi - c.bmin[i]) * (1.0f / bs) * (float)G;
-              cell_size[i] = bs * (1.0f / (float)G);
-            }
-            const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
-            if ((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G) {
-              uint32_t sub = 0;
-#pragma unroll
-              for (int i = 0; i < 3; ++i) sub += ((gpos[i] - floorf(gpos[i])) >= 0.5f ? 1u : 0u) << i;
-              const int cell = ix + G * (iy + G * iz);
-              float pred = 0.0f;
-              {
-                const int ii[3] = {ix, iy, iz};
-                float cmin[3], cmax[3];
-#pragma unroll
-                for (int i = 0; i < 3; ++i) {
-                  cmin[i] = c.bmin[i] + (float)ii[i] * cell_size[i];
-                  cmax[i] = cmin[i] + cell_size[i];
-                }
-                float t_enter, t_exit;
-                if (ray_aabb(o, d, cmin, cmax, t_enter, t_exit)) {
-                  t_enter = fmaxf(t_enter, c.t_near);
-                  t_exit = fminf(t_exit, c.t_far);
-                  if (t_exit > t_enter) {
-                    const float denom0 = t_j - t_prev;
-                    float u0 = (fabsf(denom0) > 1.0e-8f) ? (t_enter - t_prev) / denom0 : 0.0f;
-                    u0 = fminf(fmaxf(u0, 0.0f), 1.0f);
-                    const float T_enter = T_prev + (Tr - T_prev) * u0;
-                    const float t_next = (nxt < S) ? t_nx : t_exit;
-                    const float T_next = (nxt < S) ? T_nx : T_final;
-                    const float denom1 = t_next - t_last;
-                    float u1 = (fabsf(denom1) > 1.0e-8f) ? (t_exit - t_last) / denom1 : 1.0f;
-                    u1 = fminf(fmaxf(u1, 0.0f), 1.0f);
-                    const float T_exit = T_last + (T_next - T_last) * u1;
-                    pred = fminf(1.0f, fmaxf(0.0f, (T_enter - T_exit) / fmaxf(T_enter, 1.0e-12f)));
-                  }
-                }
-              }
-              const uint32_t old_q = ((a.occ_in[cell] >> (4u * sub)) & 0xFu) + 1u;
-              uint32_t proposed_q = old_q;
-              const float pred16 = pred * 16.0f;
-              const uint32_t hseed = hash_u32(a.seed ^ (uint32_t)rj * 747796405u ^ (uint32_t)lid * 2891336453u ^
-                                              (uint32_t)cell * 9781u ^ sub * 6271u);
-              if (pred16 > (float)old_q && old_q < 16u) {
-                const float f0 = floorf(pred16);
-                const float frac = pred16 - f0;
-                const uint32_t q0 = (uint32_t)f0;
-                const uint32_t thresh = (uint32_t)(frac * 16777216.0f);
-                uint32_t q_stoch = ((hseed & 0x00FFFFFFu) < thresh) ? (q0 + 1u) : q0;
-                proposed_q = q_stoch > 16u ? 16u : q_stoch;
-              }
-              // occ_st equals occ_in after every decay and proposals only raise it, so a proposal that does
-              // not exceed the occ_in nibble cannot change occ_st: skip the keep draw and the atomic
-              if (proposed_q > old_q) {
-                const float lat = (c.bmax[0] - c.bmin[0]) * (1.0f / (float)G);
-                const float tl = t_j / fmaxf(lat, 1.0e-12f);
-                const float Dl = Dhalf / fmaxf(lat, 1.0e-12f);
-                const float num = tl * tl + tl + (1.0f / 3.0f);
-                const float den = Dl * Dl + Dl + (1.0f / 3.0f);
-                const float keep_p = fminf(num / fmaxf(den, 1.0e-12f), 1.0f);
-                bool keep = keep_p >= 1.0f;
-                if (!keep) {
-                  uint32_t rk = hseed;
-                  keep = rand01(rk) <= keep_p;
-                }
-                if (keep) occ_nibble_atomic_max(a.occ_st, cell, sub, proposed_q);
-              }
-            }
-          }
-        }
-      }
-    }
+    composite_tile(a, sSig, sRgb, CL, lane, wave, train, proposals, Dhalf, dLds_j, dLdc_j);
     if (!train) continue;
 
     // ------------------------------------------------------------------
@@ -655,16 +464,12 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
     floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
     if (g == 0 && valid) {
-      const float num = t_b * t_b + t_b * dt_b + (dt_b * dt_b / 3.0f);
-      const float den = Dhalf * Dhalf + Dhalf * dt_b + (dt_b * dt_b / 3.0f);
-      const float xg = t_b / fmaxf(Dhalf, 1.0e-12f);
-      const float sg = (xg >= 1.0f) ? 0.0f : 1.0f;
-      const float gate = (1.0f - sg) * 1.0f + sg * powf(fmaxf(xg, 1.0e-12f), 0.2f);
-      const float f_vol = gate * num / fmaxf(den, 1.0e-12f);
-      dco[0][0] = (f_vol * dLdc0) * ((rgb_s[0] * (1.0f - rgb_s[0])) * 0.5f);
-      dco[0][1] = (f_vol * dLdc1) * ((rgb_s[1] * (1.0f - rgb_s[1])) * 0.5f);
-      dco[0][2] = (f_vol * dLdc2) * ((rgb_s[2] * (1.0f - rgb_s[2])) * 0.5f);
-      ddo[0][0] = 1.0f * (f_vol * dLds) * softplus_prime_from_pre(fminf(fmaxf(dout0, -18.0f), 18.0f));
+      float d3[3], dd0;
+      output_deltas(t_b, dt_b, Dhalf, dLds, dLdc0, dLdc1, dLdc2, rgb_s, dout0, d3, dd0);
+      dco[0][0] = d3[0];
+      dco[0][1] = d3[1];
+      dco[0][2] = d3[2];
+      ddo[0][0] = dd0;
     }
     // color backward
     floatx4 dc[NC][4];

@@ -1,0 +1,658 @@
+// ffn_mlp16.hip -- the fused MLP step on 16-bit MFMAs with fp32 accumulation:
+// forward and backward chains in fp16 (v_mfma_f32_16x16x16_f16; each layer's
+// deltas are scaled by a per-wavefront power of two that puts their largest
+// magnitude just below 2^14, so small deltas neither underflow nor lose bits),
+// weight gradients in bf16 (v_mfma_f32_16x16x16_bf16, whose fp32-sized
+// exponent takes the unscaled deltas of all four wavefronts).  Same semantics as the fp32
+// kernel (ffnerf_OG.cl:1373-2082, weight_update.cl:210-341): compositing, loss
+// gradient, proposals and output deltas are the shared fp32 code.
+//
+// MI355X design
+//   * A 256-thread block (4 wavefronts) walks 64-sample tiles; each wavefront
+//     runs the layers for its 16 samples.  With K = 16 per MFMA a layer's
+//     output tile (lane (g, s) holds neurons 16t + 4g + r of sample s) is, once
+//     converted to four 16-bit values, exactly the B operand of k-block t of
+//     the next layer: activations never move between lanes.
+//   * Weights live in LDS twice, fp16 row-major for the forward (A = W) and
+//     fp16 transposed for the backward (A = W^T); every A operand is one
+//     8-byte LDS read.
+//   * Weight gradients dW = delta . act^T need the samples as K.  Every
+//     wavefront writes its deltas and activations, transposed, into a
+//     block-shared bf16 stash (rows = neurons, 64 samples per row); after one
+//     barrier the 16x16 gradient tiles of all layers are split round-robin
+//     over the four wavefronts, each of which accumulates its tiles over all
+//     64 samples of the tile (4 MFMAs per tile) in registers for the whole
+//     kernel.  A wavefront so holds about a quarter of the gradient instead of
+//     all of it, which keeps the kernel free of register spills.
+#include <utility>
+
+#include "ffn_device.h"
+#include "ffn_kernels.h"
+#include "ffn_mlp_common.h"
+
+namespace ffn {
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma_f16(const half4& a, const half4& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma_bf16(const bf16x4& a, const bf16x4& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ half4 to_half4(const floatx4& v) {
+  half4 h;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) h[r] = (_Float16)v[r];
+  return h;
+}
+__device__ __forceinline__ bf16x4 to_bf16x4(const floatx4& v) {
+  bf16x4 h;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) h[r] = (__bf16)v[r];
+  return h;
+}
+
+// largest value over the wavefront (v >= 0): row-wise prefix maxima with DPP row shifts, then the rows
+// combined with row_bcast:15/31; lane 63 ends with the maximum
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  auto step = [](float x, int ctrl) {
+    const int xi = __float_as_int(x);
+    int r;
+    switch (ctrl) {
+      case 1: r = __builtin_amdgcn_update_dpp(xi, xi, 0x111, 0xF, 0xF, false); break;
+      case 2: r = __builtin_amdgcn_update_dpp(xi, xi, 0x112, 0xF, 0xF, false); break;
+      case 4: r = __builtin_amdgcn_update_dpp(xi, xi, 0x114, 0xF, 0xF, false); break;
+      case 8: r = __builtin_amdgcn_update_dpp(xi, xi, 0x118, 0xF, 0xF, false); break;
+      case 15: r = __builtin_amdgcn_update_dpp(xi, xi, 0x142, 0xF, 0xF, false); break;
+      default: r = __builtin_amdgcn_update_dpp(xi, xi, 0x143, 0xF, 0xF, false); break;
+    }
+    return fmaxf(x, __int_as_float(r));
+  };
+  v = step(v, 1);
+  v = step(v, 2);
+  v = step(v, 4);
+  v = step(v, 8);
+  v = step(v, 15);
+  v = step(v, 31);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// power of two that maps the largest |d| of the wavefront's tiles into [2^13, 2^14) (1 if all zero)
+template <int NT>
+__device__ __forceinline__ float delta_scale(const floatx4 (&d)[NT]) {
+  float m = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(d[t][r]));
+  m = wave_max_nonneg(m);
+  if (!(m > 0.0f) || !(m < 3.0e38f)) return 1.0f;
+  int e;
+  frexpf(m, &e);  // m < 2^e
+  e = 14 - e;
+  e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  return ldexpf(1.0f, e);
+}
+
+template <int NT>
+__device__ __forceinline__ void scaled_half(const floatx4 (&d)[NT], float sc, half4 (&op)[NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) op[t][r] = (_Float16)(d[t][r] * sc);
+}
+
+template <int LF_, int ND_, int NC_>
+struct Arch16 {
+  static constexpr int LF = LF_, ND = ND_, NC = NC_;
+  static constexpr int rows_pad(int k) { return k == FFN_WC_OUT ? 16 : layer_out(k); }
+  static constexpr int pf(int k) { return layer_in(k, LF) + 4; }  // fp16 forward row pitch (halves)
+  static constexpr int pt(int k) { return rows_pad(k) + 4; }      // fp16 transposed row pitch
+  static constexpr int wf_sz(int k) { return layer_active(k, ND, NC) ? rows_pad(k) * pf(k) : 0; }
+  static constexpr int wt_sz(int k) { return layer_active(k, ND, NC) ? layer_in(k, LF) * pt(k) : 0; }
+  static constexpr int wf_off(int k) {  // in halves
+    int o = 0;
+    for (int j = 0; j < k; ++j) o += wf_sz(j);
+    return o;
+  }
+  static constexpr int wt_off(int k) {
+    int o = wf_off(FFN_N_LAYERS);
+    for (int j = 0; j < k; ++j) o += wt_sz(j);
+    return o;
+  }
+  static constexpr int w_halves() { return wt_off(FFN_N_LAYERS); }
+  static constexpr int b_off(int k) {  // in floats, after the 16-bit weights
+    int o = 0;
+    for (int j = 0; j < k; ++j) o += layer_active(j, ND, NC) ? rows_pad(j) : 0;
+    return o;
+  }
+  static constexpr int b_floats() { return b_off(FFN_N_LAYERS); }
+  // stash rows (bf16, PS per row)
+  static constexpr int PS = 64 + 4;
+  static constexpr int a_a0() { return 0; }
+  static constexpr int a_hd(int i) { return LF + 64 * i; }
+  static constexpr int a_acin() { return LF + 64 * ND; }
+  static constexpr int a_hc(int i) { return LF + 64 * ND + 32 + 64 * i; }
+  static constexpr int a_rows() { return LF + 64 * ND + 32 + 64 * NC; }
+  static constexpr int d_hd(int i) { return 64 * i; }
+  static constexpr int d_dout() { return 64 * ND; }
+  static constexpr int d_hc(int i) { return 64 * ND + 16 + 64 * i; }
+  static constexpr int d_cout() { return 64 * ND + 16 + 64 * NC; }
+  static constexpr int d_rows() { return 64 * ND + 16 + 64 * NC + 16; }
+  static constexpr int stash_halves() { return (a_rows() + d_rows()) * PS; }
+  // packed gradient (same layout as make_layout)
+  static constexpr int gsz(int k) {
+    return layer_active(k, ND, NC) ? layer_out(k) * layer_in(k, LF) + layer_out(k) : 0;
+  }
+  static constexpr int g_off(int k) {
+    int o = 0;
+    for (int j = 0; j < k; ++j) o += gsz(j);
+    return o;
+  }
+  static constexpr int g_total() { return g_off(FFN_N_LAYERS); }
+  static constexpr int comp_floats = 2 * 256;
+  static constexpr size_t lds_bytes() {
+    return (size_t)w_halves() * 2 + (size_t)b_floats() * 4 + (size_t)stash_halves() * 2 + comp_floats * 4;
+  }
+  static_assert((size_t)g_total() * 4 <= (size_t)stash_halves() * 2, "gradient flush reuses the stash");
+
+  // weight-gradient tiles: layer k, output tile T (16 rows), input tile Tp (16 columns)
+  static constexpr int ot(int k) { return (k == FFN_WD_OUT || k == FFN_WC_OUT) ? 1 : 4; }
+  static constexpr int it(int k) { return layer_in(k, LF) / 16; }
+  static constexpr int dstash(int k) {
+    return k == FFN_WD_IN ? d_hd(0) : k == FFN_WD_01 ? d_hd(1) : k == FFN_WD_12 ? d_hd(2) : k == FFN_WD_OUT ? d_dout()
+         : k == FFN_WC_IN ? d_hc(0) : k == FFN_WC_01 ? d_hc(1) : k == FFN_WC_12 ? d_hc(2) : k == FFN_WC_23 ? d_hc(3)
+         : d_cout();
+  }
+  static constexpr int astash(int k) {
+    return k == FFN_WD_IN ? a_a0() : k == FFN_WD_01 ? a_hd(0) : k == FFN_WD_12 ? a_hd(1) : k == FFN_WD_OUT ? a_hd(ND - 1)
+         : k == FFN_WC_IN ? a_acin() : k == FFN_WC_01 ? a_hc(0) : k == FFN_WC_12 ? a_hc(1) : k == FFN_WC_23 ? a_hc(2)
+         : a_hc(NC - 1);
+  }
+  static constexpr int n_tiles() {
+    int n = 0;
+    for (int k = 0; k < FFN_N_LAYERS; ++k)
+      if (layer_active(k, ND, NC)) n += ot(k) * it(k);
+    return n;
+  }
+  struct TileRef {
+    int k, T, Tp;
+  };
+  static constexpr TileRef tile(int i) {
+    for (int k = 0; k < FFN_N_LAYERS; ++k) {
+      if (!layer_active(k, ND, NC)) continue;
+      const int n = ot(k) * it(k);
+      if (i < n) return TileRef{k, i / it(k), i % it(k)};
+      i -= n;
+    }
+    return TileRef{-1, 0, 0};
+  }
+  static constexpr int per_wave() { return (n_tiles() + 3) / 4; }
+};
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// forward layer: out tiles = act(W . in + b); in[kb] is the fp16 B operand of k-block kb
+template <int OT, int KB>
+__device__ __forceinline__ void fwd16(const _Float16* __restrict__ W, int P, const float* __restrict__ B,
+                                      const half4 (&in)[KB], floatx4 (&out)[OT], int g, int s, bool relu) {
+  floatx4 acc[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = B[16 * t + 4 * g + r];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int t = 0; t < OT; ++t) {
+      const half4 a = *reinterpret_cast<const half4*>(W + (16 * t + s) * P + 16 * kb + 4 * g);
+      acc[t] = mfma_f16(a, in[kb], acc[t]);
+    }
+#pragma unroll
+  for (int t = 0; t < OT; ++t) {
+    if (relu) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] = acc[t][r] > 0.0f ? acc[t][r] : 0.0f;
+    }
+    out[t] = acc[t];
+  }
+}
+
+// backward layer: res tiles over input neurons += (W^T . (delta * sc)) / sc; Wt is [in][out_pad] fp16 and
+// op the scaled fp16 deltas
+template <int RT, int KB>
+__device__ __forceinline__ void bwd16(const _Float16* __restrict__ Wt, int P, const half4 (&op)[KB], float sc,
+                                      floatx4 (&res)[RT], int g, int s) {
+  floatx4 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const half4 a = *reinterpret_cast<const half4*>(Wt + (16 * t + s) * P + 16 * kb + 4 * g);
+      acc[t] = mfma_f16(a, op[kb], acc[t]);
+    }
+  const float inv = 1.0f / sc;  // a power of two: exact
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) res[t][r] = res[t][r] + acc[t][r] * inv;
+}
+
+// zero the deltas of inactive ReLUs (mask from the forward activations)
+template <int NT>
+__device__ __forceinline__ void relu_mask16(floatx4 (&d)[NT], const half4 (&act)[NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d[t][r] = (float)act[t][r] > 0.0f ? d[t][r] : 0.0f;
+}
+
+// the next layer's operands: scale and fp16 deltas
+template <int NT>
+__device__ __forceinline__ float make_op(const floatx4 (&d)[NT], half4 (&op)[NT]) {
+  const float sc = delta_scale<NT>(d);
+  scaled_half<NT>(d, sc, op);
+  return sc;
+}
+
+// write NT D-layout tiles of this wavefront's samples into stash rows row0 + 16t + 4g + r, column 16w + s
+template <int NT, typename V>
+__device__ __forceinline__ void stash_tiles(__bf16* __restrict__ st, int row0, const V (&v)[NT], int g, int col) {
+  constexpr int PS = 64 + 4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) st[(row0 + 16 * t + 4 * g + r) * PS + col] = (__bf16)(float)v[t][r];
+}
+
+template <int LF, int ND, int NC, int FEAT>
+__global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
+  using A = Arch16<LF, ND, NC>;
+  constexpr int KB0 = LF / 16;  // k-blocks of the first layer
+  extern __shared__ __align__(16) unsigned char smem16[];
+  _Float16* sWf = reinterpret_cast<_Float16*>(smem16);
+  _Float16* sWt = sWf;  // the transposed copies follow the forward weights (offsets in 16-bit units)
+  float* sB = reinterpret_cast<float*>(smem16 + (size_t)A::w_halves() * 2);
+  __bf16* sAct = reinterpret_cast<__bf16*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4);
+  __bf16* sDel = sAct + A::a_rows() * A::PS;
+  float* sC = reinterpret_cast<float*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4 +
+                                       (size_t)A::stash_halves() * 2);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+  const bool train = a.do_train != 0;
+  const DevCfg& c = a.c;
+  const int S = a.S, log2S = a.log2S;
+  const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
+
+  // weights: fp16 [out_pad][in] and bf16 [in][out_pad] (zero padding), fp32 biases
+#pragma unroll
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    if (!layer_active(k, ND, NC)) continue;
+    const int O = layer_out(k), I = layer_in(k, LF), R = A::rows_pad(k);
+    const int PF = A::pf(k), PT = A::pt(k);
+    const float* gw = a.w.W[k];
+    for (int e = tid; e < R * PF; e += 256) {
+      const int r = e / PF, col = e - r * PF;
+      sWf[A::wf_off(k) + e] = (_Float16)((r < O && col < I) ? gw[r * I + col] : 0.0f);
+    }
+    for (int e = tid; e < I * PT; e += 256) {
+      const int i = e / PT, o = e - i * PT;
+      sWt[A::wt_off(k) + e] = (_Float16)((o < O) ? gw[o * I + i] : 0.0f);
+    }
+    for (int e = tid; e < R; e += 256) sB[A::b_off(k) + e] = e < O ? a.w.b[k][e] : 0.0f;
+  }
+  __syncthreads();
+
+  const float Dhalf = half_box_diagonal(c);
+  const bool proposals = train && a.occ_strength > 0.0f;
+  constexpr int NW = A::per_wave();
+  floatx4 gacc[NW];
+  float gbias[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    gacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    gbias[i] = 0.0f;
+  }
+
+  int parity = 0;
+  for (int64_t tile = blockIdx.x; tile < a.n_tiles; tile += gridDim.x, parity ^= 1) {
+    float* sSig = sC + parity * 256;
+    float* sRgb = sSig + 64;
+    const int64_t b = tile * 64 + wave * 16 + s;
+    const bool valid = (uint64_t)b < n_samples;
+    const int64_t ray = valid ? (b >> log2S) : 0;
+    // a0v[4 kb + j] = encoding neuron 16 kb + 4 g + j of sample b
+    float a0v[LF / 4];
+    if (valid) {
+#pragma unroll
+      for (int kb = 0; kb < KB0; ++kb) {
+        if constexpr (FEAT == 4) {
+          const int l = 4 * kb + g;
+          const float4 v = *reinterpret_cast<const float4*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
+          a0v[4 * kb] = v.x;
+          a0v[4 * kb + 1] = v.y;
+          a0v[4 * kb + 2] = v.z;
+          a0v[4 * kb + 3] = v.w;
+        } else if constexpr (FEAT == 2) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int l = 8 * kb + 2 * g + h;
+            const float2 v = *reinterpret_cast<const float2*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
+            a0v[4 * kb + 2 * h] = v.x;
+            a0v[4 * kb + 2 * h + 1] = v.y;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a0v[4 * kb + j] = a.a0[(16 * kb + 4 * g + j) * a.feat.stride_l + b * a.feat.stride_b];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LF / 4; ++q) a0v[q] = 0.0f;
+    }
+    float dirv[3];
+    {
+      const float4 rd = a.rays[2 * ray + 1];
+      dirv[0] = rd.x;
+      dirv[1] = rd.y;
+      dirv[2] = rd.z;
+    }
+    const float dt_b = valid ? a.DTs[b] : 0.0f;
+    const float t_b = valid ? a.Ts[b] : 0.0f;
+    const CompLane CL = load_comp_lane(a, tile, lane, n_samples, log2S, proposals);
+
+    // ---- forward (fp16 operands, fp32 accumulation)
+    half4 a0h[KB0];
+#pragma unroll
+    for (int kb = 0; kb < KB0; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a0h[kb][j] = (_Float16)a0v[4 * kb + j];
+    half4 hdh[ND][4];
+    {
+      floatx4 o[4];
+      fwd16<4, KB0>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), a0h, o, g, s, true);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hdh[0][t] = to_half4(o[t]);
+    }
+    if constexpr (ND >= 2) {
+      floatx4 o[4];
+      fwd16<4, 4>(sWf + A::wf_off(FFN_WD_01), A::pf(FFN_WD_01), sB + A::b_off(FFN_WD_01), hdh[0], o, g, s, true);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hdh[1][t] = to_half4(o[t]);
+    }
+    if constexpr (ND >= 3) {
+      floatx4 o[4];
+      fwd16<4, 4>(sWf + A::wf_off(FFN_WD_12), A::pf(FFN_WD_12), sB + A::b_off(FFN_WD_12), hdh[1], o, g, s, true);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hdh[2][t] = to_half4(o[t]);
+    }
+    floatx4 dout[1];
+    fwd16<1, 4>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), hdh[ND - 1], dout, g, s,
+                false);
+    half4 acinh[2];
+    acinh[0] = to_half4(dout[0]);
+    floatx4 sh;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
+    acinh[1] = to_half4(sh);
+    half4 hch[NC][4];
+    {
+      floatx4 o[4];
+      fwd16<4, 2>(sWf + A::wf_off(FFN_WC_IN), A::pf(FFN_WC_IN), sB + A::b_off(FFN_WC_IN), acinh, o, g, s, true);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hch[0][t] = to_half4(o[t]);
+    }
+#pragma unroll
+    for (int i = 1; i < NC; ++i) {
+      const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
+      floatx4 o[4];
+      fwd16<4, 4>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), hch[i - 1], o, g, s, true);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hch[i][t] = to_half4(o[t]);
+    }
+    float rgb_s[3];
+    {
+      floatx4 co[1];
+      fwd16<1, 4>(sWf + A::wf_off(FFN_WC_OUT), A::pf(FFN_WC_OUT), sB + A::b_off(FFN_WC_OUT), hch[NC - 1], co, g, s,
+                  false);
+      rgb_s[0] = sigmoid_soft(co[0][0]);
+      rgb_s[1] = sigmoid_soft(co[0][1]);
+      rgb_s[2] = sigmoid_soft(co[0][2]);
+    }
+    const float dout0 = dout[0][0];
+    if (g == 0) {
+      float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
+      if (dt_b <= 0.0f) sig = 0.0f;
+      sSig[wave * 16 + s] = sig;
+      sRgb[(wave * 16 + s) * 3 + 0] = rgb_s[0];
+      sRgb[(wave * 16 + s) * 3 + 1] = rgb_s[1];
+      sRgb[(wave * 16 + s) * 3 + 2] = rgb_s[2];
+    }
+    __syncthreads();
+
+    float dLds_j, dLdc_j[3];
+    composite_tile(a, sSig, sRgb, CL, lane, wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+    if (!train) continue;
+
+    // ---- activations into the stash (every wavefront has left the previous tile's gradient phase)
+    const int col = wave * 16 + s;
+    {
+      floatx4 av[KB0];
+#pragma unroll
+      for (int kb = 0; kb < KB0; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) av[kb][j] = a0v[4 * kb + j];
+      stash_tiles<KB0>(sAct, A::a_a0(), av, g, col);
+    }
+#pragma unroll
+    for (int i = 0; i < ND; ++i) stash_tiles<4>(sAct, A::a_hd(i), hdh[i], g, col);
+    {
+      floatx4 ac[2] = {dout[0], sh};
+      stash_tiles<2>(sAct, A::a_acin(), ac, g, col);
+    }
+#pragma unroll
+    for (int i = 0; i < NC; ++i) stash_tiles<4>(sAct, A::a_hc(i), hch[i], g, col);
+
+    // ---- backward (bf16 operands, fp32 accumulation)
+    const int src = wave * 16 + s;
+    const float dLds = __shfl(dLds_j, src);
+    const float dLdc0 = __shfl(dLdc_j[0], src), dLdc1 = __shfl(dLdc_j[1], src), dLdc2 = __shfl(dLdc_j[2], src);
+    floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
+    floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
+    if (g == 0 && valid) {
+      float d3[3], dd0;
+      output_deltas(t_b, dt_b, Dhalf, dLds, dLdc0, dLdc1, dLdc2, rgb_s, dout0, d3, dd0);
+      dco[0][0] = d3[0];
+      dco[0][1] = d3[1];
+      dco[0][2] = d3[2];
+      ddo[0][0] = dd0;
+    }
+    stash_tiles<1>(sDel, A::d_cout(), dco, g, col);
+    half4 dop[4];
+    float dsc;
+    {
+      half4 cop[1];
+      const float csc = make_op<1>(dco, cop);
+      floatx4 dc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd16<4, 1>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
+      relu_mask16<4>(dc, hch[NC - 1]);
+      stash_tiles<4>(sDel, A::d_hc(NC - 1), dc, g, col);
+      dsc = make_op<4>(dc, dop);
+    }
+#pragma unroll
+    for (int i = NC - 1; i >= 1; --i) {
+      const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
+      floatx4 dc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd16<4, 4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
+      relu_mask16<4>(dc, hch[i - 1]);
+      stash_tiles<4>(sDel, A::d_hc(i - 1), dc, g, col);
+      dsc = make_op<4>(dc, dop);
+    }
+    // colour input layer: the dout part of its input delta joins the density head's delta
+    bwd16<1, 4>(sWt + A::wt_off(FFN_WC_IN), A::pt(FFN_WC_IN), dop, dsc, ddo, g, s);
+    stash_tiles<1>(sDel, A::d_dout(), ddo, g, col);
+    {
+      half4 dd_op[1];
+      const float ssc = make_op<1>(ddo, dd_op);
+      floatx4 dd[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd16<4, 1>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
+      relu_mask16<4>(dd, hdh[ND - 1]);
+      stash_tiles<4>(sDel, A::d_hd(ND - 1), dd, g, col);
+      dsc = make_op<4>(dd, dop);
+    }
+#pragma unroll
+    for (int i = ND - 1; i >= 1; --i) {
+      const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
+      floatx4 dd[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd16<4, 4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
+      relu_mask16<4>(dd, hdh[i - 1]);
+      stash_tiles<4>(sDel, A::d_hd(i - 1), dd, g, col);
+      dsc = make_op<4>(dd, dop);
+    }
+    // encoding gradient dL/da0 = Wd_in^T . delta_d1 -> HBM for the hash scatter
+    {
+      floatx4 ga0[KB0];
+#pragma unroll
+      for (int t = 0; t < KB0; ++t) ga0[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd16<KB0, 4>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
+      if (valid) {
+#pragma unroll
+        for (int t = 0; t < KB0; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; r += 2) {
+            const int nn = 16 * t + 4 * g + r;
+            const int l = nn / FEAT, f = nn - l * FEAT;
+            float* dst = a.dL_da0 + l * a.feat.stride_l + b * a.feat.stride_b + f;
+            if constexpr (FEAT >= 2) {
+              *reinterpret_cast<float2*>(dst) = make_float2(ga0[t][r], ga0[t][r + 1]);
+            } else {
+              dst[0] = ga0[t][r];
+              a.dL_da0[(l + 1) * a.feat.stride_l + b * a.feat.stride_b] = ga0[t][r + 1];
+            }
+          }
+      }
+    }
+    __syncthreads();
+
+    // ---- weight gradients: this wavefront's share of the 16x16 tiles, K = the tile's 64 samples
+    static_for<A::n_tiles()>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if ((i & 3) == wave) {
+        constexpr typename A::TileRef tr = A::tile(i);
+        const __bf16* drow = sDel + (A::dstash(tr.k) + 16 * tr.T + s) * A::PS + 4 * g;
+        const __bf16* arow = sAct + (A::astash(tr.k) + 16 * tr.Tp + s) * A::PS + 4 * g;
+        floatx4 acc = gacc[i >> 2];
+        float bs = gbias[i >> 2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const bf16x4 dv = *reinterpret_cast<const bf16x4*>(drow + 16 * q);
+          const bf16x4 av = *reinterpret_cast<const bf16x4*>(arow + 16 * q);
+          acc = mfma_bf16(dv, av, acc);
+          if (tr.Tp == 0) bs += ((float)dv[0] + (float)dv[1]) + ((float)dv[2] + (float)dv[3]);
+        }
+        gacc[i >> 2] = acc;
+        gbias[i >> 2] = bs;
+      }
+    });
+  }
+
+  if (train) {
+    // every wavefront stores its tiles into the block's gradient (reusing the stash), one partial per block
+    __syncthreads();
+    float* sG = reinterpret_cast<float*>(sAct);
+    static_for<A::n_tiles()>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if ((i & 3) == wave) {
+        constexpr typename A::TileRef tr = A::tile(i);
+        constexpr int O = layer_out(tr.k), In = layer_in(tr.k, LF);
+        float* gW = sG + A::g_off(tr.k);
+        const int colw = 16 * tr.Tp + s;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * tr.T + 4 * g + r;
+          if (row < O) gW[row * In + colw] = gacc[i >> 2][r];
+        }
+        if (tr.Tp == 0) {
+          float bs = gbias[i >> 2];
+          bs += __shfl_xor(bs, 16);
+          bs += __shfl_xor(bs, 32);
+          if (g == 0 && 16 * tr.T + s < O) gW[O * In + 16 * tr.T + s] = bs;
+        }
+      }
+    });
+    __syncthreads();
+    float* dst = a.partials + (int64_t)blockIdx.x * A::g_total();
+    for (int e = tid; e < A::g_total(); e += 256) dst[e] = sG[e];
+  }
+}
+
+// ---------------------------------------------------------------------------
+
+template <int LF, int ND, int NC, int FEAT>
+static hipError_t launch16_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
+  using A = Arch16<LF, ND, NC>;
+  const size_t lds = A::lds_bytes();
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int LF, int ND, int NC>
+static hipError_t launch16_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
+  switch (a.c.F) {
+    case 1: return launch16_f<LF, ND, NC, 1>(a, n_blocks, st);
+    case 2: return launch16_f<LF, ND, NC, 2>(a, n_blocks, st);
+    case 4: return launch16_f<LF, ND, NC, 4>(a, n_blocks, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+#define FFN_MLP16_CONFIGS(X) \
+  X(16, 1, 2)                \
+  X(32, 1, 2)                \
+  X(64, 1, 2)                \
+  X(16, 2, 2)                \
+  X(32, 2, 2)                \
+  X(64, 2, 2)
+
+bool mlp16_supported(int LF, int nd, int nc) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return true;
+  FFN_MLP16_CONFIGS(X)
+#undef X
+  return false;
+}
+
+hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return launch16_t<l, d, n>(a, n_blocks, st);
+  FFN_MLP16_CONFIGS(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ffn
