@@ -94,14 +94,14 @@ hipError_t ensure_bins(Handle* h, int64_t n, ffn::BinPlan* plan, ffn::BinScratch
   if ((e = h->bin_total.ensure(sizeof(uint32_t) * 4)) != hipSuccess) return e;
   if ((e = h->bin_idx.ensure(sizeof(uint16_t) * (size_t)plan->max_pairs)) != hipSuccess) return e;
   if ((e = h->bin_val.ensure(sizeof(float) * (size_t)plan->max_pairs * h->dc.F)) != hipSuccess) return e;
-  if ((e = h->bin_max.ensure(sizeof(uint32_t) * (size_t)plan->max_buckets)) != hipSuccess) return e;
+  if ((e = h->bin_max.ensure(sizeof(float) * (size_t)plan->levels_per_group * plan->nblk)) != hipSuccess) return e;
   s->cnt = (uint32_t*)h->bin_cnt.p;
   s->off = (uint32_t*)h->bin_off.p;
   s->sums = (uint32_t*)h->bin_sums.p;
   s->total = (uint32_t*)h->bin_total.p;
   s->pair_idx = (uint16_t*)h->bin_idx.p;
   s->pair_val = (float*)h->bin_val.p;
-  s->bmax = (uint32_t*)h->bin_max.p;
+  s->cmax = (float*)h->bin_max.p;
   return hipSuccess;
 }
 

@@ -458,6 +458,31 @@ __device__ __forceinline__ Aff seg_scan_excl_aff_rev(Aff v, int lid, int S, int 
   return v;
 }
 
+// largest value over the wavefront (v >= 0): row-wise prefix maxima with DPP row shifts, then the rows
+// combined with row_bcast:15/31; lane 63 ends with the maximum
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  auto step = [](float x, int ctrl) {
+    const int xi = __float_as_int(x);
+    int r;
+    switch (ctrl) {
+      case 1: r = __builtin_amdgcn_update_dpp(xi, xi, 0x111, 0xF, 0xF, false); break;
+      case 2: r = __builtin_amdgcn_update_dpp(xi, xi, 0x112, 0xF, 0xF, false); break;
+      case 4: r = __builtin_amdgcn_update_dpp(xi, xi, 0x114, 0xF, 0xF, false); break;
+      case 8: r = __builtin_amdgcn_update_dpp(xi, xi, 0x118, 0xF, 0xF, false); break;
+      case 15: r = __builtin_amdgcn_update_dpp(xi, xi, 0x142, 0xF, 0xF, false); break;
+      default: r = __builtin_amdgcn_update_dpp(xi, xi, 0x143, 0xF, 0xF, false); break;
+    }
+    return fmaxf(x, __int_as_float(r));
+  };
+  v = step(v, 1);
+  v = step(v, 2);
+  v = step(v, 4);
+  v = step(v, 8);
+  v = step(v, 15);
+  v = step(v, 31);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // next set bit strictly after lid inside the segment's 64-bit run mask, or S
 __device__ __forceinline__ int find_next_flag(uint64_t segmask, int lid, int S) {
   if (lid + 1 >= S) return S;

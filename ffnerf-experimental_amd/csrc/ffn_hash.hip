@@ -18,17 +18,22 @@
 //     2. scan   -- exclusive prefix over the (bucket, block) counts, so every
 //                  block owns a contiguous slot range inside every bucket;
 //     3. emit   -- recompute the corners and write (entry-in-bucket, value)
-//                  pairs to the slots (LDS cursors, streaming writes);
+//                  pairs to the slots (LDS counting sort, aligned writes);
 //     4. reduce -- one block per bucket sums its pairs into an LDS copy of
 //                  the bucket and applies the update to its own slice of the
 //                  table: gradient add, the reference SGD, or Adam.  No
 //                  gradient table is materialised for Adam.
 //   LDS float atomics (ds_add_f32) sustain only ~0.33 lanes/clk/CU here while
 //   ds_add_u64 sustains ~4.9 (both measured), so the reduce accumulates in
-//   64-bit fixed point: the emit pass records each bucket's largest |value|
-//   (integer max on the float bits), and the reduce scales by the power of two
-//   that keeps the bucket's total below 2^62 -- an exact scaling, one
-//   round-to-nearest per pair, ~2^-34 of the bucket's largest value per entry.
+//   64-bit fixed point: the count pass records a bound on every |value| of a
+//   chunk (max |g| times max corner weight), the reduce takes the largest over
+//   the level's chunks and scales by the power of two that keeps a bucket's total below
+//   2^62 -- an exact scaling, one round-to-nearest per pair, ~2^-40 of the
+//   level's largest value per entry at the benchmark shape.
+//   Pair stores went through the L2 as 2-byte and 8-byte scattered writes and
+//   stalled the address/data path (measured: write data stalled by the cache),
+//   so every bucket run of an emit round is padded with zero pairs to a
+//   multiple of 4 and each lane stores 4 pairs with aligned 8/16-byte writes.
 //   Levels are processed in groups so the pair buffer stays bounded.
 #include "ffn_device.h"
 #include "ffn_kernels.h"
@@ -144,42 +149,25 @@ __device__ __forceinline__ bool level_grad(const DevCfg& c, const float* __restr
   return any;
 }
 
-template <int F, int MODE>
-__global__ __launch_bounds__(256) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
-                                                   const float* __restrict__ g, FeatLayout lay, float lr,
-                                                   uint32_t* __restrict__ cnt, uint32_t* __restrict__ bmax) {
-  extern __shared__ uint32_t hist[];
-  const int l = grp.level0 + (int)blockIdx.y;
-  const int nbl = grp.nbl[l - grp.level0];
-  const int chunk = blockIdx.x;
-  if (chunk == 0)
-    for (int j = threadIdx.x; j < nbl; j += blockDim.x) bmax[grp.bucket_rel[l - grp.level0] + j] = 0u;
-  for (int j = threadIdx.x; j < nbl; j += blockDim.x) hist[j] = 0u;
-  __syncthreads();
-  const int64_t b0 = (int64_t)chunk * grp.chunk;
-  const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
-  for (int64_t b = b0 + threadIdx.x; b < b1; b += blockDim.x) {
-    float gf[F];
-    if (!level_grad<F, MODE>(c, g, lay, b, l, lr, gf)) continue;
-    float pos[3], p[3];
-    sample_position(src, b, pos);
-    normalize_pos(c, pos, p);
-    const LevelCell lc = level_cell(c.res[l], p);
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) atomicAdd(&hist[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
-  }
-  __syncthreads();
-  const int rel0 = grp.bucket_rel[l - grp.level0];
-  for (int j = threadIdx.x; j < nbl; j += blockDim.x) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
+// Samples per emit round (one per thread) and the run padding: every bucket's run of a round is padded
+// with zero pairs to a multiple of PAD_RUN, so the copy-out moves PAD_RUN pairs per lane with aligned
+// 8/16-byte stores.
+template <int F>
+constexpr int emit_threads() {
+  return F == 4 ? 256 : 512;
 }
+constexpr int PAD_RUN = 4;
+__device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
 
-// Block-wide exclusive scan of cnt[0..n) into off[0..n) (256 threads; n may exceed 256).
+// Block-wide exclusive scan of cnt[0..n) into off[0..n) (NT threads; n may exceed NT); returns the total.
+template <int NT, bool PAD>
 __device__ __forceinline__ uint32_t block_scan_excl(const uint32_t* cnt, uint32_t* off, int n, uint32_t* wsum) {
+  constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int per = (n + 255) / 256;
+  const int per = (n + NT - 1) / NT;
   const int j0 = tid * per;
   uint32_t s = 0;
-  for (int j = j0; j < j0 + per && j < n; ++j) s += cnt[j];
+  for (int j = j0; j < j0 + per && j < n; ++j) s += PAD ? pad_run(cnt[j]) : cnt[j];
   uint32_t incl = s;
   for (int d = 1; d < 64; d <<= 1) {
     uint32_t o = __shfl_up(incl, d);
@@ -187,54 +175,110 @@ __device__ __forceinline__ uint32_t block_scan_excl(const uint32_t* cnt, uint32_
   }
   if (lane == 63) wsum[wv] = incl;
   __syncthreads();
-  uint32_t run = incl - s;
-  for (int k = 0; k < wv; ++k) run += wsum[k];
-  const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  uint32_t run = incl - s, total = 0;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) {
+    if (k < wv) run += wsum[k];
+    total += wsum[k];
+  }
   for (int j = j0; j < j0 + per && j < n; ++j) {
     off[j] = run;
-    run += cnt[j];
+    run += PAD ? pad_run(cnt[j]) : cnt[j];
   }
   return total;
 }
 
-// Emit the (entry, value) pairs of 256 samples at a time: rank them by bucket
-// in LDS (a local counting sort), then copy each bucket's run to its slots
-// with consecutive lanes on consecutive addresses.
+// Pairs per (bucket, chunk), counted round by round exactly as the emit pass lays them out (padded runs),
+// and in cmax[level in group][chunk] a bound on every |value| of the chunk's pairs: the largest
+// max_f |g_f| * max_c |w_c| over its samples.
 template <int F, int MODE>
-__global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
-                                                  const float* __restrict__ g, FeatLayout lay, float lr,
-                                                  const uint32_t* __restrict__ off, uint16_t* __restrict__ pair_idx,
-                                                  float* __restrict__ pair_val, uint32_t* __restrict__ bmax) {
+__global__ __launch_bounds__(emit_threads<F>()) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
+                                                                 const float* __restrict__ g, FeatLayout lay,
+                                                                 float lr, uint32_t* __restrict__ cnt,
+                                                                 float* __restrict__ cmax) {
+  constexpr int NT = emit_threads<F>();
+  extern __shared__ uint32_t hist[];
+  const int l = grp.level0 + (int)blockIdx.y;
+  const int nbl = grp.nbl[l - grp.level0];
+  const int chunk = blockIdx.x;
+  uint32_t* rcnt = hist + nbl;  // [nbl] this round
+  float* wmax = reinterpret_cast<float*>(rcnt + nbl);  // [NT / 64]
+  const int tid = threadIdx.x;
+  for (int j = tid; j < nbl; j += NT) hist[j] = 0u;
+  const int64_t b0 = (int64_t)chunk * grp.chunk;
+  const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
+  float bound = 0.0f;
+  for (int64_t rb = b0; rb < b1; rb += NT) {
+    for (int j = tid; j < nbl; j += NT) rcnt[j] = 0u;
+    __syncthreads();
+    const int64_t b = rb + tid;
+    float gf[F];
+    if (b < b1 && level_grad<F, MODE>(c, g, lay, b, l, lr, gf)) {
+      float pos[3], p[3];
+      sample_position(src, b, pos);
+      normalize_pos(c, pos, p);
+      const LevelCell lc = level_cell(c.res[l], p);
+      float gm = 0.0f, wm = 0.0f;
+#pragma unroll
+      for (int f = 0; f < F; ++f) gm = fmaxf(gm, fabsf(gf[f]));
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {
+        wm = fmaxf(wm, fabsf(corner_weight(lc, cc)));
+        atomicAdd(&rcnt[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
+      }
+      bound = fmaxf(bound, gm * wm);
+    }
+    __syncthreads();
+    for (int j = tid; j < nbl; j += NT) hist[j] += pad_run(rcnt[j]);
+  }
+  bound = wave_max_nonneg(bound);
+  if ((tid & 63) == 0) wmax[tid >> 6] = bound;
+  __syncthreads();
+  if (tid == 0) {
+    float m = 0.0f;
+    for (int w = 0; w < NT / 64; ++w) m = fmaxf(m, wmax[w]);
+    cmax[(int64_t)(l - grp.level0) * grp.nblk + chunk] = m;
+  }
+  const int rel0 = grp.bucket_rel[l - grp.level0];
+  for (int j = tid; j < nbl; j += NT) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
+}
+
+// Emit the (entry, value) pairs of NT samples at a time: rank them by bucket in LDS (a local counting
+// sort into runs padded to PAD_RUN with zero pairs), then copy PAD_RUN pairs per lane to the bucket's
+// slots: one 8-byte store of their entries and F aligned 8-byte-per-pair stores of their values.
+template <int F, int MODE>
+__global__ __launch_bounds__(emit_threads<F>()) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
+                                                                const float* __restrict__ g, FeatLayout lay,
+                                                                float lr, const uint32_t* __restrict__ off,
+                                                                uint16_t* __restrict__ pair_idx,
+                                                                float* __restrict__ pair_val) {
+  constexpr int NT = emit_threads<F>();
   typedef typename FVec<F>::T V;
   extern __shared__ uint32_t sm[];
   const int l = grp.level0 + (int)blockIdx.y;
   const int nbl = grp.nbl[l - grp.level0];
   const int chunk = blockIdx.x;
   const int rel0 = grp.bucket_rel[l - grp.level0];
-  uint32_t* gcur = sm;             // [nbl] next global slot of each bucket
-  uint32_t* lcnt = gcur + nbl;     // [nbl] pairs of the round per bucket
-  uint32_t* loff = lcnt + nbl;     // [nbl] their offsets in the stage
-  uint32_t* lmax = loff + nbl;     // [nbl] float bits of the largest |value| per bucket
-  uint32_t* wsum = lmax + nbl;     // [4]
-  // the stage starts 16-byte aligned: (4 nbl + 4) header words rounded up to a multiple of 4
-  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + ((4 * nbl + 4 + 3) & ~3));  // [2048]
-  uint16_t* st_bkt = st_idx + 2048;                          // [2048]
-  V* st_val = reinterpret_cast<V*>(st_bkt + 2048);           // [2048]
+  // stage capacity: the round's pairs and their padding (at most 8 NT buckets receive pairs)
+  const int np = 8 * NT + (PAD_RUN - 1) * (nbl < 8 * NT ? nbl : 8 * NT);
+  uint32_t* gcur = sm;          // [nbl] next global slot of each bucket
+  uint32_t* lcnt = gcur + nbl;  // [nbl] pairs of the round per bucket
+  uint32_t* loff = lcnt + nbl;  // [nbl] their offsets in the stage
+  uint32_t* wsum = loff + nbl;  // [NT / 64]
+  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + ((3 * nbl + NT / 64 + 3) & ~3));  // [np] entry in bucket
+  uint16_t* st_bkt = st_idx + ((np + 7) & ~7);                                          // [np] bucket
+  V* st_val = reinterpret_cast<V*>(st_bkt + ((np + 7) & ~7));                           // [np]
   const int tid = threadIdx.x;
-  for (int j = tid; j < nbl; j += 256) {
-    gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
-    lmax[j] = 0u;
-  }
+  for (int j = tid; j < nbl; j += NT) gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
-  V* vals = reinterpret_cast<V*>(pair_val);
   const int64_t b_begin = (int64_t)chunk * grp.chunk;
   const int64_t b_end = b_begin + grp.chunk < n ? b_begin + grp.chunk : n;
-  for (int64_t rb = b_begin; rb < b_end; rb += 256) {
-    for (int j = tid; j < nbl; j += 256) lcnt[j] = 0u;
+  for (int64_t rb = b_begin; rb < b_end; rb += NT) {
+    for (int j = tid; j < nbl; j += NT) lcnt[j] = 0u;
     __syncthreads();
     const int64_t b = rb + tid;
     float gf[F];
-    bool act = b < b_end && level_grad<F, MODE>(c, g, lay, b, l, lr, gf);
+    const bool act = b < b_end && level_grad<F, MODE>(c, g, lay, b, l, lr, gf);
     uint32_t ent[8], rank[8];
     LevelCell lc;
     if (act) {
@@ -249,49 +293,58 @@ __global__ __launch_bounds__(256) void k_bin_emit(DevCfg c, PosSrc src, int64_t 
       }
     }
     __syncthreads();
-    const uint32_t total = block_scan_excl(lcnt, loff, nbl, wsum);
+    const uint32_t total = block_scan_excl<NT, true>(lcnt, loff, nbl, wsum);
     __syncthreads();
     if (act) {
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
         const uint32_t bk = ent[cc] >> grp.log2_be;
-        const uint32_t pos = loff[bk] + rank[cc];
+        const uint32_t q = loff[bk] + rank[cc];
         const float w = corner_weight(lc, cc);
         float v[F];
-        float amax = 0.0f;
 #pragma unroll
-        for (int f = 0; f < F; ++f) {
-          v[f] = gf[f] * w;
-          amax = fmaxf(amax, fabsf(v[f]));
-        }
-        st_idx[pos] = (uint16_t)(ent[cc] & be_mask);
-        st_bkt[pos] = (uint16_t)bk;
-        st_val[pos] = FVec<F>::pack(v);
-        atomicMax(&lmax[bk], __float_as_uint(amax));
+        for (int f = 0; f < F; ++f) v[f] = gf[f] * w;
+        st_idx[q] = (uint16_t)(ent[cc] & be_mask);
+        st_bkt[q] = (uint16_t)bk;
+        st_val[q] = FVec<F>::pack(v);
+      }
+    }
+    // zero pairs pad every run to a multiple of PAD_RUN
+    for (int j = tid; j < nbl; j += NT) {
+      const uint32_t c0 = lcnt[j], c1 = pad_run(c0), o = loff[j];
+      for (uint32_t k = c0; k < c1; ++k) {
+        float z[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) z[f] = 0.0f;
+        st_idx[o + k] = 0;
+        st_bkt[o + k] = (uint16_t)j;
+        st_val[o + k] = FVec<F>::pack(z);
       }
     }
     __syncthreads();
-    for (uint32_t i = tid; i < total; i += 256) {
+    for (uint32_t i = (uint32_t)tid * PAD_RUN; i < total; i += NT * PAD_RUN) {
       const uint32_t bk = st_bkt[i];
-      const uint32_t dst = gcur[bk] + (i - loff[bk]);
-      pair_idx[dst] = st_idx[i];
-      vals[dst] = st_val[i];
+      const uint32_t dst = gcur[bk] + (i - loff[bk]);  // a multiple of PAD_RUN
+      *reinterpret_cast<uint2*>(pair_idx + dst) = *reinterpret_cast<const uint2*>(st_idx + i);
+      const float4* sv = reinterpret_cast<const float4*>(st_val + i);
+      float4* gv = reinterpret_cast<float4*>(pair_val + (size_t)dst * F);
+#pragma unroll
+      for (int k = 0; k < F; ++k) gv[k] = sv[k];
     }
     __syncthreads();
-    for (int j = tid; j < nbl; j += 256) gcur[j] += lcnt[j];
+    for (int j = tid; j < nbl; j += NT) gcur[j] += pad_run(lcnt[j]);
   }
-  __syncthreads();
-  for (int j = tid; j < nbl; j += 256)
-    if (lmax[j]) atomicMax(&bmax[rel0 + j], lmax[j]);
 }
 
+// One block per bucket: sum its pairs in 64-bit fixed point in LDS, then apply the mode's update to the
+// bucket's slice of the table.  Zero pairs (the run padding) are skipped.
 template <int F, int MODE>
 __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ off,
                                                      const uint16_t* __restrict__ pair_idx,
                                                      const float* __restrict__ pair_val,
-                                                     const uint32_t* __restrict__ bmax, BinApply ap) {
-  typedef typename FVec<F>::T V;
+                                                     const float* __restrict__ cmax, BinApply ap) {
   extern __shared__ unsigned long long acc[];
+  __shared__ float wmax[16];
   const int j = blockIdx.x;  // bucket, relative to the group
   int li = 0;
   while (li + 1 < grp.n_levels && j >= grp.bucket_rel[li + 1]) ++li;
@@ -302,11 +355,18 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   const int count = (int)((level_T - entry_lo) < (uint32_t)be ? (level_T - entry_lo) : (uint32_t)be);
   const int tid = threadIdx.x;
   for (int e = tid; e < count * F; e += 1024) acc[e] = 0ull;
+  // bound on every |value| of the level: the largest of its chunks' bounds
+  float mxl = 0.0f;
+  for (int ch = tid; ch < grp.nblk; ch += 1024) mxl = fmaxf(mxl, cmax[(int64_t)li * grp.nblk + ch]);
+  mxl = wave_max_nonneg(mxl);
+  if ((tid & 63) == 0) wmax[tid >> 6] = mxl;
   __syncthreads();
+  float mx = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) mx = fmaxf(mx, wmax[w]);
   const uint32_t start = off[(int64_t)j * grp.nblk];
-  const uint32_t end = off[(int64_t)(j + 1) * grp.nblk];
-  // fixed-point scale 2^k with (pairs + 1) * max|v| * 2^k < 2^62: no partial sum can overflow
-  const float mx = __uint_as_float(bmax[j]);
+  const uint32_t end = off[(int64_t)(j + 1) * grp.nblk];  // both multiples of PAD_RUN
+  // fixed-point scale 2^k with (pairs + 1) * bound * 2^k < 2^62: no partial sum can overflow
   int k = 0;
   if (mx > 0.0f) {
     int e_mx, e_n;
@@ -315,53 +375,27 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
     k = 62 - e_mx - e_n;
   }
   const double scale = ldexp(1.0, k);
-  const V* vals = reinterpret_cast<const V*>(pair_val);
-  auto q = [&](float v) -> unsigned long long { return (unsigned long long)__double2ll_rn((double)v * scale); };
-  auto add1 = [&](uint32_t i) {
-    const uint32_t e = pair_idx[i];
-    float v[F];
-    FVec<F>::unpack(vals[i], v);
-#pragma unroll
-    for (int f = 0; f < F; ++f) atomicAdd(&acc[e * F + f], q(v[f]));
+  auto add = [&](uint32_t e, float v, int f) {
+    if (v != 0.0f) atomicAdd(&acc[e * F + f], (unsigned long long)__double2ll_rn((double)v * scale));
   };
   if (mx > 0.0f) {
-    if constexpr (F == 2) {
-      // two pairs per 16-byte load; a block step covers 4 rows of 2048 pairs and every thread issues its
-      // 8 loads before its 16 LDS adds (each wave load reads 1 KiB / 256 B of contiguous memory)
-      const uint32_t even0 = (start + 1u) & ~1u;
-      if (start < even0 && start < end && tid == 0) add1(start);
-      uint32_t i = even0;
-      for (; i + 8192u <= end; i += 8192u) {
-        uint32_t e2[4];
-        float4 v4[4];
+    // PAD_RUN pairs per thread and step: one 8-byte load of entries, F 16-byte loads of values
+    for (uint32_t i = start + (uint32_t)tid * PAD_RUN; i < end; i += 1024u * PAD_RUN) {
+      const uint2 e4 = *reinterpret_cast<const uint2*>(pair_idx + i);
+      float v[PAD_RUN * F];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t kk = i + (uint32_t)r * 2048u + 2u * (uint32_t)tid;
-          e2[r] = *reinterpret_cast<const uint32_t*>(pair_idx + kk);
-          v4[r] = *reinterpret_cast<const float4*>(pair_val + 2 * (size_t)kk);
-        }
+      for (int q = 0; q < F; ++q) {
+        const float4 t = *reinterpret_cast<const float4*>(pair_val + (size_t)i * F + 4 * q);
+        v[4 * q] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+      }
+      const uint32_t ev[PAD_RUN] = {e4.x & 0xFFFFu, e4.x >> 16, e4.y & 0xFFFFu, e4.y >> 16};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t ea = e2[r] & 0xFFFFu, eb = e2[r] >> 16;
-          atomicAdd(&acc[2 * ea], q(v4[r].x));
-          atomicAdd(&acc[2 * ea + 1], q(v4[r].y));
-          atomicAdd(&acc[2 * eb], q(v4[r].z));
-          atomicAdd(&acc[2 * eb + 1], q(v4[r].w));
-        }
-      }
-      if (i < end) {
-        for (uint32_t kk = i + 2u * (uint32_t)tid; kk + 1u < end; kk += 2048u) {
-          const uint32_t e2 = *reinterpret_cast<const uint32_t*>(pair_idx + kk);
-          const float4 v = *reinterpret_cast<const float4*>(pair_val + 2 * (size_t)kk);
-          atomicAdd(&acc[2 * (e2 & 0xFFFFu)], q(v.x));
-          atomicAdd(&acc[2 * (e2 & 0xFFFFu) + 1], q(v.y));
-          atomicAdd(&acc[2 * (e2 >> 16)], q(v.z));
-          atomicAdd(&acc[2 * (e2 >> 16) + 1], q(v.w));
-        }
-        if (((end - i) & 1u) && tid == 0) add1(end - 1u);
-      }
-    } else {
-      for (uint32_t i = start + tid; i < end; i += 1024) add1(i);
+      for (int p = 0; p < PAD_RUN; ++p)
+#pragma unroll
+        for (int f = 0; f < F; ++f) add(ev[p], v[p * F + f], f);
     }
   }
   __syncthreads();
@@ -492,7 +526,16 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   p.log2_be = c.F == 4 ? 11 : (c.F == 2 ? 12 : 13);
   p.chunk = 4096;
   p.nblk = (int)((n + p.chunk - 1) / p.chunk);
-  const int64_t per_level_pairs = n * 8;
+  int max_nbl = 0;
+  for (int l = 0; l < c.L; ++l) {
+    const int nbl = (int)(((int64_t)c.mask[l] + 1 + (1 << p.log2_be) - 1) >> p.log2_be);
+    if (nbl > max_nbl) max_nbl = nbl;
+  }
+  // pairs of one level: 8 per sample plus at most PAD_RUN - 1 padding pairs per bucket and emit round
+  const int nt = c.F == 4 ? 256 : 512;
+  const int64_t rounds = (p.chunk + nt - 1) / nt;
+  const int64_t pad_buckets = max_nbl < 8 * nt ? max_nbl : 8 * nt;
+  const int64_t per_level_pairs = n * 8 + (int64_t)p.nblk * rounds * pad_buckets * (PAD_RUN - 1);
   const int64_t pair_bytes = 2 + 4 * (int64_t)c.F;
   int lg = (int)(pair_budget_bytes / (size_t)(per_level_pairs * pair_bytes));
   // slot offsets are 32-bit: keep a group's pair count below 2^32
@@ -501,14 +544,11 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   if (lg < 1) lg = 1;
   if (lg > c.L) lg = c.L;
   p.levels_per_group = lg;
-  int max_buckets = 0, max_nbl = 0;
+  int max_buckets = 0;
   for (int g0 = 0; g0 < c.L; g0 += lg) {
     int nb = 0;
-    for (int l = g0; l < g0 + lg && l < c.L; ++l) {
-      const int nbl = (int)(((int64_t)c.mask[l] + 1 + (1 << p.log2_be) - 1) >> p.log2_be);
-      nb += nbl;
-      if (nbl > max_nbl) max_nbl = nbl;
-    }
+    for (int l = g0; l < g0 + lg && l < c.L; ++l)
+      nb += (int)(((int64_t)c.mask[l] + 1 + (1 << p.log2_be) - 1) >> p.log2_be);
     if (nb > max_buckets) max_buckets = nb;
   }
   p.max_buckets = max_buckets;
@@ -523,6 +563,7 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                            int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
                            hipStream_t st) {
   if (n <= 0) return hipSuccess;
+  const int nt = c.F == 4 ? 256 : 512;
   for (int g0 = 0; g0 < c.L; g0 += plan.levels_per_group) {
     BinGroup grp{};
     grp.level0 = g0;
@@ -531,41 +572,41 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     grp.chunk = plan.chunk;
     grp.nblk = plan.nblk;
     int rel = 0;
+    int max_nbl = 0;
     for (int li = 0; li < grp.n_levels; ++li) {
       const int l = g0 + li;
       grp.nbl[li] = (int)(((int64_t)c.mask[l] + 1 + (1 << plan.log2_be) - 1) >> plan.log2_be);
       grp.bucket_rel[li] = rel;
       rel += grp.nbl[li];
+      if (grp.nbl[li] > max_nbl) max_nbl = grp.nbl[li];
     }
     grp.bucket_rel[grp.n_levels] = rel;
     const int n_buckets = rel;
     const int64_t n_cnt = (int64_t)n_buckets * plan.nblk;
-    int max_nbl = 0;
-    for (int li = 0; li < grp.n_levels; ++li) max_nbl = grp.nbl[li] > max_nbl ? grp.nbl[li] : max_nbl;
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
-    const size_t lds_hist = sizeof(uint32_t) * (size_t)max_nbl;
+    const size_t lds_count = sizeof(uint32_t) * (2 * (size_t)max_nbl + nt / 64);
     const size_t lds_acc = sizeof(unsigned long long) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
-    const size_t lds_emit =
-        sizeof(uint32_t) * ((4 * (size_t)max_nbl + 4 + 3) & ~(size_t)3) + 2048 * (4 + sizeof(float) * (size_t)c.F);
-#define FFN_BIN(FV, MV)                                                                                             \
-  do {                                                                                                              \
-    hipLaunchKernelGGL((k_bin_count<FV, MV>), grid_bl, dim3(256), lds_hist, st, c, src, n, grp, g, lay, lr,       \
-                       s.cnt, s.bmax);                                                                              \
-    const int64_t tiles = (n_cnt + 1 + 4095) / 4096;                                                                \
-    hipLaunchKernelGGL(k_scan_tiles, dim3((unsigned)tiles), dim3(1024), 0, st, s.cnt, n_cnt, s.off, n_cnt + 1,     \
-                       s.sums);                                                                                     \
-    hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, st, s.sums, tiles, s.total);                           \
-    hipLaunchKernelGGL(k_scan_add, dim3((unsigned)tiles), dim3(1024), 0, st, s.off, n_cnt + 1, s.sums);            \
-    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(256), lds_emit, st, c, src, n, grp, g, lay, lr, s.off, \
-                       s.pair_idx, s.pair_val, s.bmax);                                                             \
+    const size_t np = (size_t)8 * nt + (size_t)(PAD_RUN - 1) * (max_nbl < 8 * nt ? max_nbl : 8 * nt);
+    const size_t np8 = (np + 7) & ~(size_t)7;
+    const size_t lds_emit = sizeof(uint32_t) * ((3 * (size_t)max_nbl + nt / 64 + 3) & ~(size_t)3) + np8 * 4 +
+                            np * sizeof(float) * (size_t)c.F;
+    if (lds_emit > 160 * 1024 || lds_count > 160 * 1024) return hipErrorInvalidConfiguration;  // table too large
+#define FFN_BIN(FV, MV)                                                                                            \
+  do {                                                                                                             \
+    hipLaunchKernelGGL((k_bin_count<FV, MV>), grid_bl, dim3(nt), lds_count, st, c, src, n, grp, g, lay, lr, s.cnt, \
+                       s.cmax);                                                                                    \
+    hipError_t e_ = launch_scan_u32(s.cnt, n_cnt, s.off, s.sums, s.total, st);                                     \
+    if (e_ != hipSuccess) return e_;                                                                               \
+    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(nt), lds_emit, st, c, src, n, grp, g, lay, lr, s.off,  \
+                       s.pair_idx, s.pair_val);                                                                    \
     hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp, s.off, \
-                       s.pair_idx, s.pair_val, s.bmax, ap);                                                         \
+                       s.pair_idx, s.pair_val, s.cmax, ap);                                                        \
   } while (0)
-#define FFN_BIN_F(MV)                  \
-  switch (c.F) {                       \
-    case 1: FFN_BIN(1, MV); break;     \
-    case 2: FFN_BIN(2, MV); break;     \
-    case 4: FFN_BIN(4, MV); break;     \
+#define FFN_BIN_F(MV)                     \
+  switch (c.F) {                          \
+    case 1: FFN_BIN(1, MV); break;        \
+    case 2: FFN_BIN(2, MV); break;        \
+    case 4: FFN_BIN(4, MV); break;        \
     default: return hipErrorInvalidValue; \
   }
     // the scan writes n_cnt + 1 offsets: the last one is the group's pair total

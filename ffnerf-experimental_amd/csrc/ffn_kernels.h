@@ -116,7 +116,7 @@ struct BinScratch {
   uint32_t* off;       // [cnt_elems]
   uint32_t* sums;      // [tiles]
   uint32_t* total;     // [1]
-  uint32_t* bmax;      // [max_buckets] float bits of the largest |value| per bucket
+  float* cmax;         // [levels_per_group][chunks] bound on every |value| of the chunk's pairs
   uint16_t* pair_idx;  // [max_pairs]
   float* pair_val;     // [max_pairs * F]
 };
