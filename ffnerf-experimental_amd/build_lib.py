@@ -16,7 +16,7 @@ CSRC = HERE / "csrc"
 LIB = HERE / "libffnerf_hip.so"
 ARCH = os.environ.get("FFN_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["ffn_capi.hip", "ffn_sample.hip", "ffn_hash.hip", "ffn_mlp.hip", "ffn_optim.hip", "ffn_march.hip", "ffn_mlp16.hip"]
+SOURCES = ["ffn_capi.hip", "ffn_sample.hip", "ffn_hash.hip", "ffn_mlp.hip", "ffn_optim.hip", "ffn_march.hip", "ffn_mlp16.hip", "ffn_batch.hip"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

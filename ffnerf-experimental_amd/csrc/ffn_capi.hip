@@ -626,6 +626,17 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   return 0;
 }
 
+int ffn_make_batch(const float* images, uint32_t n_images, uint32_t width, uint32_t height, const float* c2w,
+                   const float* K, uint32_t num_rays, uint32_t seed, void* rays, void* targets, uint32_t* pixel_ids,
+                   void* stream) {
+  if (!images || !c2w || !K || !rays || !targets) return fail(-1, "NULL buffer");
+  if (n_images == 0 || width == 0 || height == 0) return fail(-1, "empty image set");
+  if ((uint64_t)n_images * width * height >= ((uint64_t)1 << 32)) return fail(-1, "more than 2^32 - 1 pixels");
+  FFN_HIP(ffn::launch_make_batch(images, n_images, width, height, c2w, K, num_rays, seed, (float4*)rays,
+                                 (float4*)targets, pixel_ids, (hipStream_t)stream));
+  return 0;
+}
+
 int ffn_set_profiling(void* handle, int32_t enable) {
   Handle* h = as_handle(handle);
   if (!h) return fail(-1, "NULL handle");

@@ -187,6 +187,11 @@ hipError_t launch_render_finish(const float4* acc, uint32_t num_rays, float4* ou
 hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, uint32_t* total,
                            hipStream_t st);
 
+// training batch on the GPU: uniform pixels of the resident images, their rays and targets
+hipError_t launch_make_batch(const float* images, uint32_t n_images, uint32_t W, uint32_t H, const float* c2w,
+                             const float* K, uint32_t num_rays, uint32_t seed, float4* rays, float4* targets,
+                             uint32_t* pixel_ids, hipStream_t st);
+
 // forward-only MLP over n samples: encodings a0 (layout feat), view directions from rays[ray_ids[b]];
 // sigma[n], rgb[n][3]
 hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,

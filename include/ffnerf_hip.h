@@ -192,6 +192,17 @@ int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t*
 int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits, const ffn_march_params* mp,
                void* out_rgb, uint32_t* n_samples, void* stream);
 
+/* A training batch made on the GPU (replaces the host producer and ray builder,
+ * run_ffnerf_OG.py:585-686 and ffnerf_tools.py:175-234): ray r is pixel
+ * floor(h P / 2^32) of the P = n W H pixels of the resident images, with
+ * h = lowbias32(seed ^ r * 2654435769).  images [n][H][W][3] float32 RGB,
+ * c2w [n][4][4] row-major, K [3][3] shared intrinsics (OpenCV axes).
+ * rays [num_rays] {o, 1, d, 0}; targets [num_rays] {rgb, 0}; pixel_ids
+ * (optional) [num_rays] the drawn pixel index. */
+int ffn_make_batch(const float* images, uint32_t n_images, uint32_t width, uint32_t height, const float* c2w,
+                   const float* K, uint32_t num_rays, uint32_t seed, void* rays, void* targets, uint32_t* pixel_ids,
+                   void* stream);
+
 /* Stage timing (the counterpart of the reference's profiling queue and
  * event_ms, ffnerf_tools.py:11-13,127-138,1521-1530).  When enabled, every
  * ffn_train_step records HIP events around its kernels on the caller's stream;

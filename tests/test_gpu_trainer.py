@@ -1,0 +1,175 @@
+"""GPU checks of the host workflow: the on-device batch generator against the
+reference ray builder, a short training run through the trainer and the
+command line (loss falls, checkpoint, resume, snapshot), the checkpoint round
+trip, and the PSNR of a GPU-trained model against the oracle trained on the
+same batches (north star: within 0.3 dB after N steps)."""
+import json
+
+import numpy as np
+import pytest
+
+from common import default_scalars
+from oracle import oracle as ora
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("a GPU test ran without a visible GPU")
+    return torch
+
+
+def _draw(seed, n, total):
+    """The batch generator's pixel draw, restated with the oracle's lowbias32."""
+    r = np.arange(n, dtype=np.uint64)
+    keys = (np.uint64(seed) ^ ((r * np.uint64(2654435769)) & np.uint64(0xFFFFFFFF))).astype(np.uint32)
+    h = np.array([ora.hash_u32(int(k)) for k in keys], np.uint64)
+    return ((h * np.uint64(total)) >> np.uint64(32)).astype(np.int64)
+
+
+def test_make_batch_matches_host_rays(torch):
+    import ffnerf_tools as ft
+    import synthetic_scene as sc
+    import trainer
+    cams = sc.cameras_for("cfg0")
+    rng = np.random.default_rng(0)
+    images = rng.random((cams.c2w.shape[0], cams.H, cams.W, 3)).astype(np.float32)
+    dev = trainer.DeviceImages(images, cams.c2w, cams.K)
+    io = ft.RayBatch.init(5000, 64)
+    ids = torch.zeros(5000, dtype=torch.int32, device="cuda")
+    import ffn_lib as fl
+    fl.check(dev.lib.ffn_make_batch(fl.ptr(dev.images), dev.n, dev.W, dev.H, fl.ptr(dev.c2w), fl.ptr(dev.K), 5000,
+                                    1234, fl.ptr(io.rays_buf), fl.ptr(io.targets_buf), fl.ptr(ids),
+                                    fl.stream_ptr()))
+    torch.cuda.synchronize()
+    p = ids.cpu().numpy().view(np.uint32).astype(np.int64)
+    np.testing.assert_array_equal(p, _draw(1234, 5000, images[..., 0].size))
+    im, rem = p // (cams.W * cams.H), p % (cams.W * cams.H)
+    v, u = rem // cams.W, rem % cams.W
+    rays, tg = ft.rays_targets_from_indices(im, u, v, images, cams.c2w, cams.W, cams.H, K=cams.K)
+    got = io.rays_buf.cpu().numpy()
+    np.testing.assert_allclose(got, ft.rays_as_array(rays), atol=2e-6)
+    np.testing.assert_array_equal(io.targets_buf.cpu().numpy(), tg)
+    assert len(np.unique(im)) == cams.c2w.shape[0]
+
+
+def _config(tmp_path, steps=40, rays=256):
+    import synthetic_scene as sc
+    npz = sc.write_archive(tmp_path / "scene", "cfg0")
+    cfg = {"data": {"reconstruction": str(npz), "sfm_max_side": 0, "max_side": 0},
+           "scene": {"box_min": [0, 0, 0], "box_max": [1, 1, 1]},
+           "training": {"directory": str(tmp_path / "run"), "model_id": "ball", "steps": steps, "period": 10,
+                        "batch_rays": rays, "lr": 0.01, "lmd": 0.0, "seed": 3},
+           "viewer": {"samples_per_ray": 64, "width": 64, "height": 64, "block_size": 8},
+           "model": {"n_levels": 8, "f_per_level": 2, "log2_T": [14] * 8, "base_res": 16.0,
+                     "finest_res": 16.0 * 1.5 ** 7, "nd": 1, "nc": 2, "hash_opt": "adam", "init": "xavier",
+                     "beta1": 0.9, "beta2": 0.99, "eps": 1e-15, "background": "black", "schedule": "constant",
+                     "occ_G": 32, "occ_decay": 0.95, "occ_period": 16}}
+    path = tmp_path / "scene.json"
+    path.write_text(json.dumps(cfg))
+    return path
+
+
+def test_cli_train_resume_snapshot(torch, tmp_path):
+    import ffnerf_cli
+    import png_io
+    path = _config(tmp_path, steps=60)
+    print("[case] cli train 60 steps", flush=True)
+    assert ffnerf_cli.main(["train", "--config", str(path), "--no-web"]) == 0
+    run = tmp_path / "run"
+    logs = sorted(run.glob("ball_loss_*.csv"))
+    rows = [l.split(",") for l in logs[0].read_text().splitlines()[1:]]
+    mse = [float(r[3]) for r in rows]
+    # per-batch losses of 256 rays are noisy and most pixels are black: check the run is finite and stable
+    # (learning itself is checked on held-out rays by the PSNR test)
+    assert len(mse) >= 6 and np.all(np.isfinite(mse)) and max(mse[-3:]) < 0.1, mse
+    assert (run / "ball_weights_latest.npz").exists()
+    print("[case] cli resume", flush=True)
+    assert ffnerf_cli.main(["train", "--config", str(path), "--resume", "ball", "--steps", "10"]) == 0
+    data = np.load(run / "ball_weights_latest.npz")
+    assert int(data["steps_trained"]) == 70
+    out = tmp_path / "snap.png"
+    print("[case] cli snapshot", flush=True)
+    assert ffnerf_cli.main(["snapshot", "--config", str(path), "--output", str(out), "--view", "2"]) == 0
+    img = png_io.read_png(out)
+    assert img.shape == (64, 64, 3)  # after 70 steps the view is mostly the black background
+
+
+def test_checkpoint_round_trip_bit_exact(torch, tmp_path):
+    import ffnerf_tools as ft
+    import synthetic_scene as sc
+    from common import spec_cfg0
+    spec = ft.ModelSpec(n_levels=8, f_per_level=2, log2_T=[14] * 8, res=ft.level_resolutions(8, 16.0, growth=1.5),
+                        nd=1, nc=2, background="black", hash_opt="adam", init="xavier", beta1=0.9, beta2=0.99,
+                        eps=1e-15)
+    occ = ft.OccParams(G_occ=32, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32))
+    a = ft.Nerf(tmp_path, "rt", spec=spec, occ=occ, rng_seed=5)
+    rays, tg = sc.uniform_batch(sc.cameras_for("cfg0"), 256, np.random.default_rng(1))
+    io = ft.RayBatch.init(256, 64)
+    io.upload_rays(rays)
+    io.upload_targets(tg)
+    for _ in range(3):
+        a.step(io, lr_f=1e-2, do_train=True)
+    a.save(min_new_file_seconds=0)
+    b = ft.Nerf(tmp_path, "rt2", spec=spec, occ=occ, load_id="rt")
+    sa, sb = a.host_state(), b.host_state()
+    assert b.steps_trained == 3 and set(sa) == set(sb)
+    for k in sa:
+        assert np.array_equal(sa[k].view(np.uint32), sb[k].view(np.uint32)), k
+    # one more identical step on both: still identical
+    a.step(io, lr_f=1e-2, do_train=True, rng_u32=np.uint32(77))
+    b.step(io, lr_f=1e-2, do_train=True, rng_u32=np.uint32(77))
+    sa, sb = a.host_state(), b.host_state()
+    for k in sa:
+        assert np.array_equal(sa[k].view(np.uint32), sb[k].view(np.uint32)), k
+
+
+def test_psnr_matches_oracle_after_training(torch):
+    """Train the GPU path and the oracle on the same 60 batches (256 rays x 64 samples aimed at the ball,
+    cfg0 shapes, Adam 1e-2, decay every 16 steps), then render 2048 held-out rays of the same kind with
+    both: the model must have learned the ball (well above the black background) and the two PSNRs must
+    agree within 0.3 dB."""
+    import ffnerf_tools as ft
+    import trainer
+    from common import look_at_rays, spec_cfg0, sphere_targets
+    spec = ft.ModelSpec(n_levels=8, f_per_level=2, log2_T=[14] * 8, res=ft.level_resolutions(8, 16.0, growth=1.5),
+                        nd=1, nc=2, background="black", hash_opt="adam", init="xavier", beta1=0.9, beta2=0.99,
+                        eps=1e-15)
+    occ = ft.OccParams(G_occ=32, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32), decay=0.95,
+                       maintenance_period=16)
+    box = spec_cfg0()
+    import tempfile
+    g = ft.Nerf(tempfile.mkdtemp(), "p", spec=spec, occ=occ, rng_seed=9)
+    host = g.host_state()
+    o = ora.OracleModel(ft.spec_dict(spec, occ), {k: v.reshape(spec.layer_shapes()[k]) if k in spec.layer_shapes()
+                                                 else v for k, v in host.items()})
+    rng = np.random.default_rng(4)
+    io = ft.RayBatch.init(256, 64)
+    for step in range(1, 61):
+        rays = look_at_rays(256, box, seed=1000 + step, miss_frac=0.0)
+        tg = sphere_targets(rays, box)
+        io.upload_rays(rays)
+        io.upload_targets(tg)
+        seed = np.uint32(rng.integers(0, 2 ** 32))
+        g.step(io, lr_f=1e-2, do_train=True, rng_u32=seed)
+        sc_ = default_scalars(lr=1e-2, lr_t=float(g.adam_lr_t(1e-2, step)), rng_seed=int(seed))
+        o.train_step(rays, tg, 64, sc_)
+        if step % 16 == 0:
+            q24 = int(round((1 - 1.0 * (1 - 0.95)) * (1 << 24)))
+            ora.occ_decay(o.p["occ_in"], o.p["occ_st"], q24, int(seed))
+    rays = look_at_rays(2048, box, seed=7, miss_frac=0.0)
+    tg = sphere_targets(rays, box)
+    ev = ft.RayBatch.init(2048, 64)
+    ev.upload_rays(rays)
+    ev.upload_targets(tg)
+    out_g, _ = g.step(ev, lr_f=0.0, do_train=False, occ_update_strength=0.0, return_output=True,
+                      rng_u32=np.uint32(1))
+    out_o, _ = o.train_step(rays, tg, 64, default_scalars(do_train=0, occ_strength=0.0, rng_seed=1))
+    p_g, p_o = trainer.psnr(out_g, tg), trainer.psnr(out_o, tg)
+    p_black = trainer.psnr(np.zeros_like(out_g), tg)
+    print(f"[psnr] gpu {p_g:.3f} dB  oracle {p_o:.3f} dB  black {p_black:.3f} dB", flush=True)
+    assert p_g > p_black + 3.0  # the ball has been learned
+    assert abs(p_g - p_o) < 0.3

@@ -1,0 +1,188 @@
+"""CPU checks of the host workflow: the scene config, the BA-archive reader and
+image geometry (the reference's tests/test_scene_workflow.py:1-80 restated on
+this package, with PNGs written by the package's own codec), the schedules,
+the loss log and the command line's checks.  No GPU needed."""
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import ffnerf_cli
+import ffnerf_tools as ft
+import png_io
+import synthetic_scene as sc
+import trainer
+from scene_config import load_config
+from sfm_data import area_resize, load_images, read_scene, scaled_intrinsics, scene_bounds
+
+
+@pytest.fixture
+def scene(tmp_path):
+    for i in range(2):
+        png_io.write_png(tmp_path / f"{i}.png", np.full((80, 40, 3), 80 + i, np.uint8))
+    K = np.array([[40, 0, 10], [0, 40, 20], [0, 0, 1]], np.float32)
+    poses = np.tile(np.eye(4), (2, 1, 1))
+    poses[1, :3, 3] = [1, 2, 3]
+    data = {"reconstruction": str(tmp_path / "scene.npz"), "images_dir": str(tmp_path), "sfm_max_side": 40,
+            "max_side": 20}
+
+    def save(**kw):
+        np.savez(data["reconstruction"], K=K, img_paths=np.array(["old/place/0.png", "old/place/1.png"]), **kw)
+
+    return dict(root=tmp_path, K=K, poses=poses, data=data, save=save)
+
+
+def test_ba_w2c_and_relocated_images(scene):
+    scene["save"](RT=np.linalg.inv(scene["poses"]), rt_dir=np.array(["w2c"]), active_cam_global=[8, 12])
+    paths, poses, K, ids, points = read_scene(scene["data"])
+    np.testing.assert_allclose(poses, scene["poses"], atol=1e-6)
+    assert ids.tolist() == [8, 12]
+    images, K2, wh = load_images(scene["data"], paths, K)
+    assert images.shape == (2, 20, 10, 3)
+    np.testing.assert_allclose(K2[:2], scene["K"][:2] / 2)
+    np.testing.assert_allclose(images[1], (81 / 255.0), rtol=1e-6)
+
+
+def test_stage2_filters_before_loading_images(scene):
+    scene["save"](c2w=scene["poses"], posed=[True, True], keep_mask=[False, True],
+                  X_track=[[1, 2, 3], [9, 9, 9]], has_X=[True, False])
+    sel = scene["root"] / "selected"
+    sel.mkdir()
+    png_io.write_png(sel / "1.png", np.zeros((80, 40, 3), np.uint8))
+    scene["data"]["images_dir"] = str(sel)
+    paths, poses, K, ids, points = read_scene(scene["data"])
+    assert ids.tolist() == [1]
+    np.testing.assert_allclose(points, [[1, 2, 3]])
+    assert len(paths) == 1
+
+
+def test_object_arrays_are_refused_not_unpickled(scene):
+    np.savez(scene["data"]["reconstruction"], K=scene["K"], c2w=scene["poses"],
+             img_paths=np.array(["0.png", "1.png"], dtype=object))
+    with pytest.raises(ValueError, match="unpickling"):
+        read_scene(scene["data"])
+
+
+def test_geometry_and_bounds(scene):
+    K = scene["K"]
+    np.testing.assert_allclose(scaled_intrinsics(K, (40, 80), (20, 40), 40), K)
+    with pytest.raises(ValueError):
+        scene_bounds({"box_min": [1, 0, 0], "box_max": [0, 1, 1]}, np.empty((0, 3)))
+    lo, hi = scene_bounds({"box_min": None, "box_max": None}, np.array([[1, 2, 3]]))
+    assert np.all(hi > lo)
+    points = np.array([[0, 0, 0], [2, 4, 6], [1, 2, 3]], np.float32)
+    q_lo, q_hi = np.percentile(points, [1, 99], axis=0)
+    center = 0.5 * (q_lo + q_hi)
+    radius = max(0.5 * np.linalg.norm(q_hi - q_lo), 0.01) * 1.5
+    lo, hi = scene_bounds({"box_min": None, "box_max": None}, points)
+    np.testing.assert_allclose((lo + hi) * 0.5, center, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose((hi - lo) * 0.5, np.full(3, radius), rtol=1e-6, atol=1e-6)
+
+
+def test_review_rays_match_training_intrinsics(scene):
+    images = np.zeros((2, 80, 40, 3), np.float32)
+    u, v = np.array([0, 19, 39]), np.array([0, 29, 79])
+    training, _ = ft.rays_targets_from_indices(np.ones(3, np.int32), u, v, images, scene["poses"], 40, 80,
+                                               K=scene["K"])
+    review = ft.rays_from_rt_indices(scene["poses"][1], u, v, 40, 80, K=scene["K"])
+    np.testing.assert_allclose(training["o"], review["o"])
+    np.testing.assert_allclose(training["d"], review["d"], atol=1e-7)
+
+
+def test_config_paths_and_unknown_keys(tmp_path):
+    path = tmp_path / "scene.json"
+    path.write_text(json.dumps({"data": {"reconstruction": "scene.npz"}}))
+    assert load_config(path)["data"]["reconstruction"] == str(tmp_path / "scene.npz")
+    for bad in ({"training": {"stepz": 10}}, {"trainin": {}}, {"data": {"reconstruction": "x", "max_side": -1}},
+                {"data": {"reconstruction": "x"}, "training": {"samples_per_ray": 128}},
+                {"data": {"reconstruction": "x"}, "training": {"model_id": "a b"}},
+                {"data": {"reconstruction": "x"}, "model": {"hash_opt": "rmsprop"}}):
+        path.write_text(json.dumps(bad))
+        with pytest.raises(ValueError):
+            load_config(path)
+
+
+def test_area_resize_is_a_box_filter():
+    rng = np.random.default_rng(0)
+    img = rng.random((12, 18, 3)).astype(np.float32)
+    half = area_resize(img, (9, 6))
+    np.testing.assert_allclose(half, img.reshape(6, 2, 9, 2, 3).mean(axis=(1, 3)), rtol=1e-6)
+    odd = area_resize(img, (7, 5))  # non-integer factors: a convex combination, so constants stay constant
+    np.testing.assert_allclose(area_resize(np.full((12, 18, 3), 0.3, np.float32), (7, 5)), 0.3, rtol=1e-6)
+    assert odd.shape == (5, 7, 3) and np.all(odd >= img.min()) and np.all(odd <= img.max())
+    np.testing.assert_allclose(odd.mean(axis=(0, 1)), img.mean(axis=(0, 1)), rtol=1e-5)
+
+
+def test_schedules_closed_form():
+    B, S, lr, lmd = 512, 64, 1e-4, 1e-4
+    n = B * S
+    for step in (0, 1, 1000, 50000):
+        want = max(lr * np.sqrt(65536 / n) * np.exp(-lmd * np.sqrt(n / 65536) * step), 5e-6)
+        assert trainer.lr_schedule(step, lr, lmd, B, S) == np.float32(want)
+    assert trainer.lr_schedule(10 ** 9, lr, lmd, B, S) == np.float32(5e-6)
+    assert [trainer.sh_multiplier(s) for s in (0, 3000, 3750, 4500, 9000)] == [0.0, 0.0, 0.5, 1.0, 1.0]
+    assert [trainer.occ_multiplier(s) for s in (1500, 1501)] == [0.0, 1.0]
+    assert [trainer.color_rel_lr(s) for s in (0, 1500, 2250, 3000)] == [0.15, 0.15, 0.15 + 0.85 * 0.5, 1.0]
+
+
+def test_loss_log_format(tmp_path):
+    path, f = trainer.open_loss_log(tmp_path, "m1")
+    trainer.write_loss_row(f, 1.5, 10, 1e-3, 0.25, 0.5, 0.75, [2], 3)
+    f.close()
+    lines = path.read_text().splitlines()
+    assert path.name.startswith("m1_loss_") and path.suffix == ".csv"
+    assert lines[0] == "wall_s,step,lr_f,mse,rmse_rgb,l2mean,inflight,batch_q"
+    assert lines[1].split(",")[:3] == ["1.500000", "10", "1.000e-03"]
+    out = np.array([[0.5, 0.5, 0.5, 0]], np.float32)
+    tg = np.array([[0.0, 0.5, 1.0, 0]], np.float32)
+    mse, rmse, l2 = trainer.batch_loss(out, tg)
+    assert mse == pytest.approx(0.5 / 3) and l2 == pytest.approx(np.sqrt(0.5))
+    assert trainer.psnr(out, tg) == pytest.approx(-10 * np.log10(0.5 / 3))
+
+
+def _synthetic_config(tmp_path, **training):
+    npz = sc.write_archive(tmp_path / "scene", "cfg0")
+    cfg = {"data": {"reconstruction": str(npz), "sfm_max_side": 0, "max_side": 0},
+           "scene": {"box_min": [0, 0, 0], "box_max": [1, 1, 1]},
+           "training": dict({"directory": str(tmp_path / "run"), "model_id": "ball", "steps": 5, "period": 5,
+                             "batch_rays": 256, "lr": 0.01, "lmd": 0.0}, **training),
+           "model": {"n_levels": 8, "f_per_level": 2, "log2_T": [14] * 8, "base_res": 16.0,
+                     "finest_res": 16.0 * 1.5 ** 7, "nd": 1, "nc": 2, "hash_opt": "adam", "init": "xavier",
+                     "beta1": 0.9, "beta2": 0.99, "eps": 1e-15, "background": "black", "schedule": "constant"}}
+    path = tmp_path / "scene.json"
+    path.write_text(json.dumps(cfg))
+    return path
+
+
+def test_synthetic_archive_reads_back(tmp_path, capsys):
+    path = _synthetic_config(tmp_path)
+    cfg = load_config(path)
+    paths, poses, K, ids, points = read_scene(cfg["data"])
+    assert len(paths) == 8 and ids.tolist() == list(range(8))
+    images, K2, (W, H) = load_images(cfg["data"], paths, K)
+    assert (W, H) == (64, 64)
+    cams = sc.cameras_for("cfg0")
+    np.testing.assert_allclose(poses, cams.c2w)
+    np.testing.assert_allclose(images[3], np.round(np.clip(sc.render_image(cams, 3), 0, 1) * 255) / 255,
+                               atol=1e-6)
+    assert ffnerf_cli.main(["inspect", "--config", str(path)]) == 0
+    assert "Registered cameras: 8" in capsys.readouterr().out
+
+
+def test_cli_checks(tmp_path):
+    path = _synthetic_config(tmp_path)
+    for argv in (["train", "--config", str(path), "--steps", "0"],
+                 ["train", "--config", str(path), "--model-id", "bad id"]):
+        with pytest.raises(SystemExit):
+            ffnerf_cli.main(argv)
+    run = tmp_path / "run"
+    run.mkdir()
+    (run / "ball_weights_20260101.npz").write_bytes(b"")
+    with pytest.raises(SystemExit):  # would overwrite checkpoints without --resume
+        ffnerf_cli.main(["train", "--config", str(path)])
+    out = tmp_path / "exists.png"
+    out.write_bytes(b"")
+    with pytest.raises(SystemExit):
+        ffnerf_cli.main(["snapshot", "--config", str(path), "--output", str(out)])
