@@ -255,9 +255,11 @@ __device__ __forceinline__ bool is_left(int lid, int stride) {
 // 2s-lane block reads its partner s lanes below and the "left" lane reads the
 // one s lanes above.  Inside a 16-lane row (s <= 8) that is a DPP row shift;
 // for s = 16 and 32 the lower partner of the served lanes (31, 63 and 63) is
-// what DPP row_bcast:15 / row_bcast:31 deliver; only the upward moves at
-// s = 16 and 32 use ds_bpermute.  Lanes that are not served get unspecified
-// values, exactly as the tree ignores them.
+// what DPP row_bcast:15 / row_bcast:31 deliver, and the upper partner of the
+// served lanes (15, 47 and 31) what v_permlane16_swap / v_permlane32_swap
+// deliver (the odd row of each row pair, the upper half of the wave: checked
+// on the device).  All of them are VALU operations: no LDS round trip.  Lanes
+// that are not served get unspecified values, exactly as the tree ignores them.
 template <int S_>
 __device__ __forceinline__ float from_lower(float v) {
   const int x = __float_as_int(v);
@@ -272,11 +274,13 @@ __device__ __forceinline__ float from_lower(float v) {
 }
 template <int S_>
 __device__ __forceinline__ float from_upper(float v) {
+  const int x = __float_as_int(v);
   if constexpr (S_ < 16) {
-    const int x = __float_as_int(v);
     return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x100 + S_, 0xF, 0xF, false));  // row_shl:S_
+  } else if constexpr (S_ == 16) {
+    return __int_as_float((int)__builtin_amdgcn_permlane16_swap(x, x, false, false)[1]);  // lane i <- odd row
   } else {
-    return __shfl(v, (int)(threadIdx.x & 63) + S_);
+    return __int_as_float((int)__builtin_amdgcn_permlane32_swap(x, x, false, false)[1]);  // lanes 0-31 <- 32-63
   }
 }
 
@@ -320,12 +324,7 @@ template <int ST>
 __device__ __forceinline__ void reduce_add_step(float& v, int lid, int S) {
   if (ST < S) {
     float o;
-    if constexpr (ST < 16) {
-      const int x = __float_as_int(v);
-      o = __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x100 + ST, 0xF, 0xF, false));  // row_shl:ST
-    } else {
-      o = __shfl_xor(v, ST);
-    }
+    o = from_upper<ST>(v);  // lanes below ST read lid + ST
     if (lid < ST) v = v + o;
   }
 }

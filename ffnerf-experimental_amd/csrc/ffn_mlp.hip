@@ -432,7 +432,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     const float t_b = valid ? a.Ts[b] : 0.0f;
     // per-sample inputs of the compositing (lane j = sample j of the tile), loaded before the forward so
     // that their latency hides behind it
-    const CompLane CL = load_comp_lane(a, tile, lane, n_samples, log2S, proposals);
+    const CompLane CL = load_comp_lane(a, tile, lane, wave, n_samples, log2S, proposals);
 
     floatx4 hd[ND][4];
     floatx4 acin[2];  // [dout(16) | SH*mult(16)] as two D-layout tiles

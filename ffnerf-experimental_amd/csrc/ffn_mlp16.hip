@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
     }
     const float dt_b = valid ? a.DTs[b] : 0.0f;
     const float t_b = valid ? a.Ts[b] : 0.0f;
-    const CompLane CL = load_comp_lane(a, tile, lane, n_samples, log2S, proposals);
+    const CompLane CL = load_comp_lane(a, tile, lane, wave, n_samples, log2S, proposals);
 
     // ---- forward (fp16 operands, fp32 accumulation)
     half4 a0h[KB0];

@@ -23,10 +23,23 @@ struct CompLane {
   float dt_j, t_j;
   float4 tg;
   uint64_t segmask;
+  uint32_t occ_word;  // occ_in word of the sample's cell (proposal lanes), loaded early for its latency
 };
 
-__device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t tile, int lane, uint64_t n_samples,
-                                                   int log2S, bool proposals) {
+// grid coordinates of a point for the occupancy proposals (ffnerf_OG.cl:1660-1690); the same operations
+// serve the early load of the cell's occupancy word and the proposal itself
+__device__ __forceinline__ void occ_grid_pos(const DevCfg& c, const float (&o)[3], const float (&d)[3], float t,
+                                             float (&gpos)[3]) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float bs = c.bmax[i] - c.bmin[i];
+    const float xi = o[i] + t * d[i];
+    gpos[i] = (xi - c.bmin[i]) * (1.0f / bs) * (float)c.G;
+  }
+}
+
+__device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t tile, int lane, int wave,
+                                                   uint64_t n_samples, int log2S, bool proposals) {
   CompLane L;
   L.bj = tile * 64 + lane;
   L.vj = (uint64_t)L.bj < n_samples;
@@ -36,9 +49,21 @@ __device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t til
   if (L.vj && a.targets) L.tg = a.targets[L.rj];
   L.t_j = 0.0f;
   L.segmask = 0;
+  L.occ_word = 0;
   if (proposals && L.vj) {
     L.t_j = a.Ts[L.bj];
     L.segmask = (uint64_t)a.flags[2 * L.rj] | ((uint64_t)a.flags[2 * L.rj + 1] << 32);
+    const int lid = lane & (a.S - 1);
+    if (((L.segmask >> lid) & 1ull) && L.dt_j > 0.0f && (lane >> 4) == wave) {
+      const float4 ro = a.rays[2 * L.rj], rdv = a.rays[2 * L.rj + 1];
+      const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
+      float gpos[3];
+      occ_grid_pos(a.c, o, d, L.t_j, gpos);
+      const int G = a.c.G;
+      const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
+      if ((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G)
+        L.occ_word = a.occ_in[ix + G * (iy + G * iz)];
+    }
   }
   return L;
 }
@@ -152,11 +177,10 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
           const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
           const int G = c.G;
           float gpos[3], cell_size[3];
+          occ_grid_pos(c, o, d, t_j, gpos);
 #pragma unroll
           for (int i = 0; i < 3; ++i) {
             const float bs = c.bmax[i] - c.bmin[i];
-            const float xi = o[i] + t_j * d[i];
-            gpos[i] = (xi - c.bmin[i]) * (1.0f / bs) * (float)G;
             cell_size[i] = bs * (1.0f / (float)G);
           }
           const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
@@ -193,7 +217,7 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
                 }
               }
             }
-            const uint32_t old_q = ((a.occ_in[cell] >> (4u * sub)) & 0xFu) + 1u;
+            const uint32_t old_q = ((L.occ_word >> (4u * sub)) & 0xFu) + 1u;
             uint32_t proposed_q = old_q;
             const float pred16 = pred * 16.0f;
             const uint32_t hseed = hash_u32(a.seed ^ (uint32_t)rj * 747796405u ^ (uint32_t)lid * 2891336453u ^
