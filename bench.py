@@ -71,13 +71,14 @@ def recorded_traffic(stage, mlp):
         return None
     d = json.loads(f.read_text())
     ks = d["kernels"]
-    ref = [v for n, v in ks.items() if n.startswith(STAGE_KERNELS["mlp"][0])]
+    kernels = dict(STAGE_KERNELS, mlp=("void ffn::k_mlp16<",) if mlp == "fp16" else STAGE_KERNELS["mlp"])
+    ref = [v for n, v in ks.items() if n.startswith(kernels["mlp"][0])]
     if not ref:
         return None
     steps = ref[0]["dispatches"]
     fetch = write = ns = 0.0
     for n, v in ks.items():
-        if n.startswith(STAGE_KERNELS[stage]):
+        if n.startswith(kernels[stage]):
             per_step = v["dispatches"] / steps
             fetch += v["fetch_bytes"] * per_step
             write += v["write_bytes"] * per_step
