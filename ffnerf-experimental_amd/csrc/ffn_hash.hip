@@ -129,14 +129,49 @@ __global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t 
 // ---------------------------------------------------------------------------
 // backward: bucketed scatter
 
+// The raw inputs of one (sample, level) of the scatter: its upstream gradient and what its position is
+// made of.  Loaded one emit/count round ahead of their use, so the loads' latency overlaps the round.
+template <int F>
+struct RawSample {
+  float g[F];
+  float4 o, d;  // ray origin / direction, or the stored position in o.xyz
+  float t;
+};
+
+template <int F>
+__device__ __forceinline__ void load_raw(const PosSrc& s, const float* __restrict__ g, const FeatLayout& lay,
+                                         int64_t b, int l, RawSample<F>& r) {
+  typedef typename FVec<F>::T V;
+  FVec<F>::unpack(*reinterpret_cast<const V*>(g + l * lay.stride_l + b * lay.stride_b), r.g);
+  if (s.rays) {
+    const int64_t ray = b >> s.log2S;
+    r.o = s.rays[2 * ray];
+    r.d = s.rays[2 * ray + 1];
+    r.t = s.Ts[b];
+  } else {
+    const float* xb = s.x + (int64_t)s.x_stride * b;
+    r.o = make_float4(xb[0], xb[1], xb[2], 0.0f);
+  }
+}
+
+// the sample position, computed exactly as sample_position does
+template <int F>
+__device__ __forceinline__ void raw_position(const PosSrc& s, const RawSample<F>& r, float pos[3]) {
+  if (s.rays) {
+    pos[0] = r.o.x + r.t * r.d.x;
+    pos[1] = r.o.y + r.t * r.d.y;
+    pos[2] = r.o.z + r.t * r.d.z;
+  } else {
+    pos[0] = r.o.x;
+    pos[1] = r.o.y;
+    pos[2] = r.o.z;
+  }
+}
+
 // The gradient of one (sample, level): scaled as the mode needs, non-finite
 // components dropped (ffnerf_OG.cl:2162).  Returns false when it is all zero.
 template <int F, int MODE>
-__device__ __forceinline__ bool level_grad(const DevCfg& c, const float* __restrict__ g, const FeatLayout& lay,
-                                           int64_t b, int l, float lr, float gf[F]) {
-  typedef typename FVec<F>::T V;
-  float v[F];
-  FVec<F>::unpack(*reinterpret_cast<const V*>(g + l * lay.stride_l + b * lay.stride_b), v);
+__device__ __forceinline__ bool level_grad(const DevCfg& c, const float (&v)[F], int l, float lr, float gf[F]) {
   bool any = false;
 #pragma unroll
   for (int f = 0; f < F; ++f) {
@@ -152,45 +187,19 @@ __device__ __forceinline__ bool level_grad(const DevCfg& c, const float* __restr
 // Samples per emit round (one per thread) and the run padding: every bucket's run of a round is padded
 // with zero pairs to a multiple of PAD_RUN, so the copy-out moves PAD_RUN pairs per lane with aligned
 // 8/16-byte stores.
+__host__ __device__ constexpr int emit_nt(int F) { return F == 4 ? 256 : (F == 2 ? 1024 : 512); }
 template <int F>
 constexpr int emit_threads() {
-  return F == 4 ? 256 : 512;
+  return emit_nt(F);
 }
 constexpr int PAD_RUN = 4;
 __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
 
-// Block-wide exclusive scan of cnt[0..n) into off[0..n) (NT threads; n may exceed NT); returns the total.
-template <int NT, bool PAD>
-__device__ __forceinline__ uint32_t block_scan_excl(const uint32_t* cnt, uint32_t* off, int n, uint32_t* wsum) {
-  constexpr int NW = NT / 64;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int per = (n + NT - 1) / NT;
-  const int j0 = tid * per;
-  uint32_t s = 0;
-  for (int j = j0; j < j0 + per && j < n; ++j) s += PAD ? pad_run(cnt[j]) : cnt[j];
-  uint32_t incl = s;
-  for (int d = 1; d < 64; d <<= 1) {
-    uint32_t o = __shfl_up(incl, d);
-    if (lane >= d) incl += o;
-  }
-  if (lane == 63) wsum[wv] = incl;
-  __syncthreads();
-  uint32_t run = incl - s, total = 0;
-#pragma unroll
-  for (int k = 0; k < NW; ++k) {
-    if (k < wv) run += wsum[k];
-    total += wsum[k];
-  }
-  for (int j = j0; j < j0 + per && j < n; ++j) {
-    off[j] = run;
-    run += PAD ? pad_run(cnt[j]) : cnt[j];
-  }
-  return total;
-}
-
 // Pairs per (bucket, chunk), counted round by round exactly as the emit pass lays them out (padded runs),
 // and in cmax[level in group][chunk] a bound on every |value| of the chunk's pairs: the largest
-// max_f |g_f| * max_c |w_c| over its samples.
+// max_f |g_f| * max_c |w_c| over its samples.  The round counters are double-buffered: the thread that
+// folds a bucket's counter into the histogram after the round's barrier zeroes it again one round later,
+// so a round needs one barrier.
 template <int F, int MODE>
 __global__ __launch_bounds__(emit_threads<F>()) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                                  const float* __restrict__ g, FeatLayout lay,
@@ -201,21 +210,30 @@ __global__ __launch_bounds__(emit_threads<F>()) void k_bin_count(DevCfg c, PosSr
   const int l = grp.level0 + (int)blockIdx.y;
   const int nbl = grp.nbl[l - grp.level0];
   const int chunk = blockIdx.x;
-  uint32_t* rcnt = hist + nbl;  // [nbl] this round
-  float* wmax = reinterpret_cast<float*>(rcnt + nbl);  // [NT / 64]
+  uint32_t* rcnt = hist + nbl;                              // [2][nbl] per-round counters
+  float* wmax = reinterpret_cast<float*>(rcnt + 2 * nbl);  // [NT / 64]
   const int tid = threadIdx.x;
-  for (int j = tid; j < nbl; j += NT) hist[j] = 0u;
+  for (int j = tid; j < nbl; j += NT) {
+    hist[j] = 0u;
+    rcnt[j] = 0u;
+    rcnt[nbl + j] = 0u;
+  }
   const int64_t b0 = (int64_t)chunk * grp.chunk;
   const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
+  RawSample<F> in;
+  if (b0 + tid < b1) load_raw<F>(src, g, lay, b0 + tid, l, in);
+  __syncthreads();
   float bound = 0.0f;
-  for (int64_t rb = b0; rb < b1; rb += NT) {
-    for (int j = tid; j < nbl; j += NT) rcnt[j] = 0u;
-    __syncthreads();
+  int r = 0;
+  for (int64_t rb = b0; rb < b1; rb += NT, r ^= 1) {
+    uint32_t* cur = rcnt + r * nbl;
+    uint32_t* nxt = rcnt + (r ^ 1) * nbl;
+    for (int j = tid; j < nbl; j += NT) nxt[j] = 0u;  // folded by this thread in the previous round
     const int64_t b = rb + tid;
     float gf[F];
-    if (b < b1 && level_grad<F, MODE>(c, g, lay, b, l, lr, gf)) {
+    if (b < b1 && level_grad<F, MODE>(c, in.g, l, lr, gf)) {
       float pos[3], p[3];
-      sample_position(src, b, pos);
+      raw_position<F>(src, in, pos);
       normalize_pos(c, pos, p);
       const LevelCell lc = level_cell(c.res[l], p);
       float gm = 0.0f, wm = 0.0f;
@@ -224,12 +242,13 @@ __global__ __launch_bounds__(emit_threads<F>()) void k_bin_count(DevCfg c, PosSr
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
         wm = fmaxf(wm, fabsf(corner_weight(lc, cc)));
-        atomicAdd(&rcnt[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
+        atomicAdd(&cur[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
       }
       bound = fmaxf(bound, gm * wm);
     }
+    if (b + NT < b1) load_raw<F>(src, g, lay, b + NT, l, in);
     __syncthreads();
-    for (int j = tid; j < nbl; j += NT) hist[j] += pad_run(rcnt[j]);
+    for (int j = tid; j < nbl; j += NT) hist[j] += pad_run(cur[j]);
   }
   bound = wave_max_nonneg(bound);
   if ((tid & 63) == 0) wmax[tid >> 6] = bound;
@@ -243,9 +262,26 @@ __global__ __launch_bounds__(emit_threads<F>()) void k_bin_count(DevCfg c, PosSr
   for (int j = tid; j < nbl; j += NT) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
 }
 
+// LDS of k_bin_emit, in 32-bit words before the stage and in bytes in total
+__host__ __device__ constexpr int emit_words(int nbl) { return (5 * nbl + 4 + 3) & ~3; }
+__host__ __device__ constexpr int emit_stage_pairs(int nt, int nbl) {
+  return 8 * nt + (PAD_RUN - 1) * (nbl < 8 * nt ? nbl : 8 * nt);
+}
+__host__ __device__ constexpr int round8(int x) { return (x + 7) & ~7; }
+__host__ __device__ constexpr size_t emit_lds_bytes(int nt, int nbl, int F) {
+  return (size_t)emit_words(nbl) * 4 + (size_t)round8(emit_stage_pairs(nt, nbl)) * 2 +
+         (size_t)round8((emit_stage_pairs(nt, nbl) + PAD_RUN - 1) / PAD_RUN) * 2 +
+         (size_t)emit_stage_pairs(nt, nbl) * 4 * (size_t)F;
+}
+
 // Emit the (entry, value) pairs of NT samples at a time: rank them by bucket in LDS (a local counting
 // sort into runs padded to PAD_RUN with zero pairs), then copy PAD_RUN pairs per lane to the bucket's
 // slots: one 8-byte store of their entries and F aligned 8-byte-per-pair stores of their values.
+// A round has three barriers: after the ranking, after wavefront 0 has scanned the round's counts
+// (offsets in the stage, global destinations, next cursors, and the other counter buffer cleared for
+// the next round), and after the stage is written.  The next round's inputs are loaded during the round.
+// Every quad of the stage starts with a real pair (padding only fills a run's last quad), so the lane
+// holding a pair of rank 0 mod 4 records the quad's bucket for the copy-out.
 template <int F, int MODE>
 __global__ __launch_bounds__(emit_threads<F>()) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                                 const float* __restrict__ g, FeatLayout lay,
@@ -259,41 +295,71 @@ __global__ __launch_bounds__(emit_threads<F>()) void k_bin_emit(DevCfg c, PosSrc
   const int nbl = grp.nbl[l - grp.level0];
   const int chunk = blockIdx.x;
   const int rel0 = grp.bucket_rel[l - grp.level0];
-  // stage capacity: the round's pairs and their padding (at most 8 NT buckets receive pairs)
-  const int np = 8 * NT + (PAD_RUN - 1) * (nbl < 8 * NT ? nbl : 8 * NT);
-  uint32_t* gcur = sm;          // [nbl] next global slot of each bucket
-  uint32_t* lcnt = gcur + nbl;  // [nbl] pairs of the round per bucket
-  uint32_t* loff = lcnt + nbl;  // [nbl] their offsets in the stage
-  uint32_t* wsum = loff + nbl;  // [NT / 64]
-  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + ((3 * nbl + NT / 64 + 3) & ~3));  // [np] entry in bucket
-  uint16_t* st_bkt = st_idx + ((np + 7) & ~7);                                          // [np] bucket
-  V* st_val = reinterpret_cast<V*>(st_bkt + ((np + 7) & ~7));                           // [np]
-  const int tid = threadIdx.x;
-  for (int j = tid; j < nbl; j += NT) gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
+  const int np = emit_stage_pairs(NT, nbl);
+  uint32_t* gcur = sm;              // [nbl] next global slot of each bucket
+  uint32_t* gdst = gcur + nbl;      // [nbl] global slot of the round's run minus its stage offset (mod 2^32)
+  uint32_t* lcnt = gdst + nbl;      // [2][nbl] pairs of the round per bucket
+  uint32_t* loff = lcnt + 2 * nbl;  // [nbl] run offsets in the stage
+  uint32_t* total_s = loff + nbl;   // [1] padded pairs of the round
+  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + emit_words(nbl));  // [np] entry in bucket
+  uint16_t* st_bkt = st_idx + round8(np);                                // [np / 4] bucket of each quad
+  V* st_val = reinterpret_cast<V*>(st_bkt + round8((np + PAD_RUN - 1) / PAD_RUN));  // [np]
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int j = tid; j < nbl; j += NT) {
+    gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
+    lcnt[j] = 0u;
+  }
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
   const int64_t b_begin = (int64_t)chunk * grp.chunk;
   const int64_t b_end = b_begin + grp.chunk < n ? b_begin + grp.chunk : n;
-  for (int64_t rb = b_begin; rb < b_end; rb += NT) {
-    for (int j = tid; j < nbl; j += NT) lcnt[j] = 0u;
-    __syncthreads();
+  RawSample<F> in;
+  if (b_begin + tid < b_end) load_raw<F>(src, g, lay, b_begin + tid, l, in);
+  __syncthreads();
+  int r = 0;
+  for (int64_t rb = b_begin; rb < b_end; rb += NT, r ^= 1) {
+    uint32_t* cur = lcnt + r * nbl;
+    uint32_t* nxt = lcnt + (r ^ 1) * nbl;
     const int64_t b = rb + tid;
     float gf[F];
-    const bool act = b < b_end && level_grad<F, MODE>(c, g, lay, b, l, lr, gf);
+    const bool act = b < b_end && level_grad<F, MODE>(c, in.g, l, lr, gf);
     uint32_t ent[8], rank[8];
     LevelCell lc;
     if (act) {
       float pos[3], p[3];
-      sample_position(src, b, pos);
+      raw_position<F>(src, in, pos);
       normalize_pos(c, pos, p);
       lc = level_cell(c.res[l], p);
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
         ent[cc] = corner_entry(lc, cc, l, c.mask[l]);
-        rank[cc] = atomicAdd(&lcnt[ent[cc] >> grp.log2_be], 1u);
+        rank[cc] = atomicAdd(&cur[ent[cc] >> grp.log2_be], 1u);
       }
     }
+    if (b + NT < b_end) load_raw<F>(src, g, lay, b + NT, l, in);
     __syncthreads();
-    const uint32_t total = block_scan_excl<NT, true>(lcnt, loff, nbl, wsum);
+    if (tid < 64) {
+      uint32_t carry = 0;
+      for (int j0 = 0; j0 < nbl; j0 += 64) {
+        const int j = j0 + lane;
+        const uint32_t cn = j < nbl ? pad_run(cur[j]) : 0u;
+        uint32_t incl = cn;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const uint32_t o = __shfl_up(incl, d);
+          if (lane >= d) incl += o;
+        }
+        if (j < nbl) {
+          const uint32_t o = carry + incl - cn;
+          const uint32_t gc = gcur[j];
+          loff[j] = o;
+          gdst[j] = gc - o;
+          gcur[j] = gc + cn;
+          nxt[j] = 0u;
+        }
+        carry += __shfl(incl, 63);
+      }
+      if (lane == 0) total_s[0] = carry;
+    }
     __syncthreads();
     if (act) {
 #pragma unroll
@@ -305,34 +371,32 @@ __global__ __launch_bounds__(emit_threads<F>()) void k_bin_emit(DevCfg c, PosSrc
 #pragma unroll
         for (int f = 0; f < F; ++f) v[f] = gf[f] * w;
         st_idx[q] = (uint16_t)(ent[cc] & be_mask);
-        st_bkt[q] = (uint16_t)bk;
         st_val[q] = FVec<F>::pack(v);
+        if ((rank[cc] & (PAD_RUN - 1)) == 0) st_bkt[q / PAD_RUN] = (uint16_t)bk;
       }
     }
     // zero pairs pad every run to a multiple of PAD_RUN
     for (int j = tid; j < nbl; j += NT) {
-      const uint32_t c0 = lcnt[j], c1 = pad_run(c0), o = loff[j];
+      const uint32_t c0 = cur[j], c1 = pad_run(c0), o = loff[j];
       for (uint32_t k = c0; k < c1; ++k) {
         float z[F];
 #pragma unroll
         for (int f = 0; f < F; ++f) z[f] = 0.0f;
         st_idx[o + k] = 0;
-        st_bkt[o + k] = (uint16_t)j;
         st_val[o + k] = FVec<F>::pack(z);
       }
     }
     __syncthreads();
-    for (uint32_t i = (uint32_t)tid * PAD_RUN; i < total; i += NT * PAD_RUN) {
-      const uint32_t bk = st_bkt[i];
-      const uint32_t dst = gcur[bk] + (i - loff[bk]);  // a multiple of PAD_RUN
+    const uint32_t nq = total_s[0] / PAD_RUN;
+    for (uint32_t qd = (uint32_t)tid; qd < nq; qd += NT) {
+      const uint32_t i = qd * PAD_RUN;
+      const uint32_t dst = gdst[st_bkt[qd]] + i;  // a multiple of PAD_RUN
       *reinterpret_cast<uint2*>(pair_idx + dst) = *reinterpret_cast<const uint2*>(st_idx + i);
       const float4* sv = reinterpret_cast<const float4*>(st_val + i);
       float4* gv = reinterpret_cast<float4*>(pair_val + (size_t)dst * F);
 #pragma unroll
       for (int k = 0; k < F; ++k) gv[k] = sv[k];
     }
-    __syncthreads();
-    for (int j = tid; j < nbl; j += NT) gcur[j] += pad_run(lcnt[j]);
   }
 }
 
@@ -532,7 +596,7 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
     if (nbl > max_nbl) max_nbl = nbl;
   }
   // pairs of one level: 8 per sample plus at most PAD_RUN - 1 padding pairs per bucket and emit round
-  const int nt = c.F == 4 ? 256 : 512;
+  const int nt = emit_nt(c.F);
   const int64_t rounds = (p.chunk + nt - 1) / nt;
   const int64_t pad_buckets = max_nbl < 8 * nt ? max_nbl : 8 * nt;
   const int64_t per_level_pairs = n * 8 + (int64_t)p.nblk * rounds * pad_buckets * (PAD_RUN - 1);
@@ -563,7 +627,7 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                            int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
                            hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  const int nt = c.F == 4 ? 256 : 512;
+  const int nt = emit_nt(c.F);
   for (int g0 = 0; g0 < c.L; g0 += plan.levels_per_group) {
     BinGroup grp{};
     grp.level0 = g0;
@@ -584,12 +648,9 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     const int n_buckets = rel;
     const int64_t n_cnt = (int64_t)n_buckets * plan.nblk;
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
-    const size_t lds_count = sizeof(uint32_t) * (2 * (size_t)max_nbl + nt / 64);
+    const size_t lds_count = sizeof(uint32_t) * (3 * (size_t)max_nbl + nt / 64);
     const size_t lds_acc = sizeof(unsigned long long) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
-    const size_t np = (size_t)8 * nt + (size_t)(PAD_RUN - 1) * (max_nbl < 8 * nt ? max_nbl : 8 * nt);
-    const size_t np8 = (np + 7) & ~(size_t)7;
-    const size_t lds_emit = sizeof(uint32_t) * ((3 * (size_t)max_nbl + nt / 64 + 3) & ~(size_t)3) + np8 * 4 +
-                            np * sizeof(float) * (size_t)c.F;
+    const size_t lds_emit = emit_lds_bytes(nt, max_nbl, c.F);
     if (lds_emit > 160 * 1024 || lds_count > 160 * 1024) return hipErrorInvalidConfiguration;  // table too large
 #define FFN_BIN(FV, MV)                                                                                            \
   do {                                                                                                             \
