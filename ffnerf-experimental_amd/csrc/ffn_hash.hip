@@ -184,15 +184,17 @@ __device__ __forceinline__ bool level_grad(const DevCfg& c, const float (&v)[F],
   return any;
 }
 
-// Samples per emit round (one per thread) and the run padding: every bucket's run of a round is padded
-// with zero pairs to a multiple of PAD_RUN, so the copy-out moves PAD_RUN pairs per lane with aligned
-// 8/16-byte stores.
-__host__ __device__ constexpr int emit_nt(int F) { return F == 4 ? 256 : (F == 2 ? 1024 : 512); }
-template <int F>
-constexpr int emit_threads() {
-  return emit_nt(F);
-}
+// Emit rounds: EMIT_NT threads take EMIT_SPT samples each (EMIT_RS samples per round), and every bucket's
+// run of a round is padded with zero pairs to a multiple of PAD_RUN, so the copy-out moves PAD_RUN pairs
+// per lane with aligned 8/16-byte stores.  The larger the round, the longer the runs that land in each
+// bucket's slots, and short scattered runs are what limits the pass (HBM writes of a few hundred bytes
+// at scattered places).
+constexpr int EMIT_NT = 1024;
+constexpr int EMIT_SPT = 2;
+constexpr int EMIT_RS = EMIT_NT * EMIT_SPT;
 constexpr int PAD_RUN = 4;
+constexpr uint16_t REF_PAD = 0xFFFFu;  // stage reference of a padding pair
+static_assert(EMIT_RS * 8 <= REF_PAD, "stage references are 16-bit");
 __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
 
 // Pairs per (bucket, chunk), counted round by round exactly as the emit pass lays them out (padded runs),
@@ -201,141 +203,154 @@ __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN -
 // folds a bucket's counter into the histogram after the round's barrier zeroes it again one round later,
 // so a round needs one barrier.
 template <int F, int MODE>
-__global__ __launch_bounds__(emit_threads<F>()) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
-                                                                 const float* __restrict__ g, FeatLayout lay,
-                                                                 float lr, uint32_t* __restrict__ cnt,
-                                                                 float* __restrict__ cmax) {
-  constexpr int NT = emit_threads<F>();
+__global__ __launch_bounds__(EMIT_NT) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
+                                                       const float* __restrict__ g, FeatLayout lay, float lr,
+                                                       uint32_t* __restrict__ cnt, float* __restrict__ cmax) {
   extern __shared__ uint32_t hist[];
   const int l = grp.level0 + (int)blockIdx.y;
   const int nbl = grp.nbl[l - grp.level0];
   const int chunk = blockIdx.x;
   uint32_t* rcnt = hist + nbl;                              // [2][nbl] per-round counters
-  float* wmax = reinterpret_cast<float*>(rcnt + 2 * nbl);  // [NT / 64]
+  float* wmax = reinterpret_cast<float*>(rcnt + 2 * nbl);  // [EMIT_NT / 64]
   const int tid = threadIdx.x;
-  for (int j = tid; j < nbl; j += NT) {
+  for (int j = tid; j < nbl; j += EMIT_NT) {
     hist[j] = 0u;
     rcnt[j] = 0u;
     rcnt[nbl + j] = 0u;
   }
   const int64_t b0 = (int64_t)chunk * grp.chunk;
   const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
-  RawSample<F> in;
-  if (b0 + tid < b1) load_raw<F>(src, g, lay, b0 + tid, l, in);
+  RawSample<F> in[EMIT_SPT];
+#pragma unroll
+  for (int q = 0; q < EMIT_SPT; ++q)
+    if (b0 + tid + q * EMIT_NT < b1) load_raw<F>(src, g, lay, b0 + tid + q * EMIT_NT, l, in[q]);
   __syncthreads();
   float bound = 0.0f;
   int r = 0;
-  for (int64_t rb = b0; rb < b1; rb += NT, r ^= 1) {
+  for (int64_t rb = b0; rb < b1; rb += EMIT_RS, r ^= 1) {
     uint32_t* cur = rcnt + r * nbl;
     uint32_t* nxt = rcnt + (r ^ 1) * nbl;
-    for (int j = tid; j < nbl; j += NT) nxt[j] = 0u;  // folded by this thread in the previous round
-    const int64_t b = rb + tid;
-    float gf[F];
-    if (b < b1 && level_grad<F, MODE>(c, in.g, l, lr, gf)) {
-      float pos[3], p[3];
-      raw_position<F>(src, in, pos);
-      normalize_pos(c, pos, p);
-      const LevelCell lc = level_cell(c.res[l], p);
-      float gm = 0.0f, wm = 0.0f;
+    for (int j = tid; j < nbl; j += EMIT_NT) nxt[j] = 0u;  // folded by this thread in the previous round
 #pragma unroll
-      for (int f = 0; f < F; ++f) gm = fmaxf(gm, fabsf(gf[f]));
+    for (int q = 0; q < EMIT_SPT; ++q) {
+      const int64_t b = rb + tid + q * EMIT_NT;
+      float gf[F];
+      if (b < b1 && level_grad<F, MODE>(c, in[q].g, l, lr, gf)) {
+        float pos[3], p[3];
+        raw_position<F>(src, in[q], pos);
+        normalize_pos(c, pos, p);
+        const LevelCell lc = level_cell(c.res[l], p);
+        float gm = 0.0f, wm = 0.0f;
 #pragma unroll
-      for (int cc = 0; cc < 8; ++cc) {
-        wm = fmaxf(wm, fabsf(corner_weight(lc, cc)));
-        atomicAdd(&cur[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
+        for (int f = 0; f < F; ++f) gm = fmaxf(gm, fabsf(gf[f]));
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) {
+          wm = fmaxf(wm, fabsf(corner_weight(lc, cc)));
+          atomicAdd(&cur[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
+        }
+        bound = fmaxf(bound, gm * wm);
       }
-      bound = fmaxf(bound, gm * wm);
+      if (b + EMIT_RS < b1) load_raw<F>(src, g, lay, b + EMIT_RS, l, in[q]);
     }
-    if (b + NT < b1) load_raw<F>(src, g, lay, b + NT, l, in);
     __syncthreads();
-    for (int j = tid; j < nbl; j += NT) hist[j] += pad_run(cur[j]);
+    for (int j = tid; j < nbl; j += EMIT_NT) hist[j] += pad_run(cur[j]);
   }
   bound = wave_max_nonneg(bound);
   if ((tid & 63) == 0) wmax[tid >> 6] = bound;
   __syncthreads();
   if (tid == 0) {
     float m = 0.0f;
-    for (int w = 0; w < NT / 64; ++w) m = fmaxf(m, wmax[w]);
+    for (int w = 0; w < EMIT_NT / 64; ++w) m = fmaxf(m, wmax[w]);
     cmax[(int64_t)(l - grp.level0) * grp.nblk + chunk] = m;
   }
   const int rel0 = grp.bucket_rel[l - grp.level0];
-  for (int j = tid; j < nbl; j += NT) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
+  for (int j = tid; j < nbl; j += EMIT_NT) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
 }
 
-// LDS of k_bin_emit, in 32-bit words before the stage and in bytes in total
+// LDS of k_bin_emit: counters (32-bit words), per-sample corner fractions and gradients, then the stage
 __host__ __device__ constexpr int emit_words(int nbl) { return (5 * nbl + 4 + 3) & ~3; }
-__host__ __device__ constexpr int emit_stage_pairs(int nt, int nbl) {
-  return 8 * nt + (PAD_RUN - 1) * (nbl < 8 * nt ? nbl : 8 * nt);
+__host__ __device__ constexpr int emit_stage_pairs(int nbl) {
+  return 8 * EMIT_RS + (PAD_RUN - 1) * (nbl < 8 * EMIT_RS ? nbl : 8 * EMIT_RS);
 }
 __host__ __device__ constexpr int round8(int x) { return (x + 7) & ~7; }
-__host__ __device__ constexpr size_t emit_lds_bytes(int nt, int nbl, int F) {
-  return (size_t)emit_words(nbl) * 4 + (size_t)round8(emit_stage_pairs(nt, nbl)) * 2 +
-         (size_t)round8((emit_stage_pairs(nt, nbl) + PAD_RUN - 1) / PAD_RUN) * 2 +
-         (size_t)emit_stage_pairs(nt, nbl) * 4 * (size_t)F;
+__host__ __device__ constexpr size_t emit_lds_bytes(int nbl, int F) {
+  return (size_t)emit_words(nbl) * 4 + (size_t)EMIT_RS * (16 + 4 * (size_t)F) +
+         (size_t)round8(emit_stage_pairs(nbl)) * 4 + (size_t)round8((emit_stage_pairs(nbl) + PAD_RUN - 1) / PAD_RUN) * 2;
 }
 
-// Emit the (entry, value) pairs of NT samples at a time: rank them by bucket in LDS (a local counting
+// Emit the (entry, value) pairs of EMIT_RS samples at a time: rank them by bucket in LDS (a local counting
 // sort into runs padded to PAD_RUN with zero pairs), then copy PAD_RUN pairs per lane to the bucket's
-// slots: one 8-byte store of their entries and F aligned 8-byte-per-pair stores of their values.
-// A round has three barriers: after the ranking, after wavefront 0 has scanned the round's counts
-// (offsets in the stage, global destinations, next cursors, and the other counter buffer cleared for
-// the next round), and after the stage is written.  The next round's inputs are loaded during the round.
-// Every quad of the stage starts with a real pair (padding only fills a run's last quad), so the lane
-// holding a pair of rank 0 mod 4 records the quad's bucket for the copy-out.
+// slots: one 8-byte store of their entries and F aligned 8-byte-per-pair stores of their values.  The
+// stage holds, per pair, its entry and a 16-bit reference (sample of the round, corner); the copy-out
+// forms the value g_f * w_corner from the sample's fractions and gradient kept in LDS (the same products
+// as at ranking time).  A round has three barriers: after the ranking, after wavefront 0 has scanned the
+// round's counts (stage offsets, global destinations, next cursors, and the other counter buffer cleared
+// for the next round), and after the stage is written.  The next round's inputs are loaded during the
+// round.  Every quad of the stage starts with a real pair (padding only fills a run's last quad), so the
+// lane holding a pair of rank 0 mod 4 records the quad's bucket for the copy-out.
 template <int F, int MODE>
-__global__ __launch_bounds__(emit_threads<F>()) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
-                                                                const float* __restrict__ g, FeatLayout lay,
-                                                                float lr, const uint32_t* __restrict__ off,
-                                                                uint16_t* __restrict__ pair_idx,
-                                                                float* __restrict__ pair_val) {
-  constexpr int NT = emit_threads<F>();
+__global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
+                                                      const float* __restrict__ g, FeatLayout lay, float lr,
+                                                      const uint32_t* __restrict__ off,
+                                                      uint16_t* __restrict__ pair_idx,
+                                                      float* __restrict__ pair_val) {
   typedef typename FVec<F>::T V;
   extern __shared__ uint32_t sm[];
   const int l = grp.level0 + (int)blockIdx.y;
   const int nbl = grp.nbl[l - grp.level0];
   const int chunk = blockIdx.x;
   const int rel0 = grp.bucket_rel[l - grp.level0];
-  const int np = emit_stage_pairs(NT, nbl);
+  const int np = emit_stage_pairs(nbl);
   uint32_t* gcur = sm;              // [nbl] next global slot of each bucket
   uint32_t* gdst = gcur + nbl;      // [nbl] global slot of the round's run minus its stage offset (mod 2^32)
   uint32_t* lcnt = gdst + nbl;      // [2][nbl] pairs of the round per bucket
   uint32_t* loff = lcnt + 2 * nbl;  // [nbl] run offsets in the stage
   uint32_t* total_s = loff + nbl;   // [1] padded pairs of the round
-  uint16_t* st_idx = reinterpret_cast<uint16_t*>(sm + emit_words(nbl));  // [np] entry in bucket
-  uint16_t* st_bkt = st_idx + round8(np);                                // [np / 4] bucket of each quad
-  V* st_val = reinterpret_cast<V*>(st_bkt + round8((np + PAD_RUN - 1) / PAD_RUN));  // [np]
+  float4* s_frac = reinterpret_cast<float4*>(sm + emit_words(nbl));    // [EMIT_RS] corner fractions
+  V* s_grad = reinterpret_cast<V*>(s_frac + EMIT_RS);                  // [EMIT_RS] gradient
+  uint16_t* st_idx = reinterpret_cast<uint16_t*>(s_grad + EMIT_RS);    // [np] entry in bucket
+  uint16_t* st_ref = st_idx + round8(np);                              // [np] sample * 8 + corner
+  uint16_t* st_bkt = st_ref + round8(np);                              // [np / 4] bucket of each quad
   const int tid = threadIdx.x, lane = tid & 63;
-  for (int j = tid; j < nbl; j += NT) {
+  for (int j = tid; j < nbl; j += EMIT_NT) {
     gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
     lcnt[j] = 0u;
   }
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
   const int64_t b_begin = (int64_t)chunk * grp.chunk;
   const int64_t b_end = b_begin + grp.chunk < n ? b_begin + grp.chunk : n;
-  RawSample<F> in;
-  if (b_begin + tid < b_end) load_raw<F>(src, g, lay, b_begin + tid, l, in);
+  RawSample<F> in[EMIT_SPT];
+#pragma unroll
+  for (int q = 0; q < EMIT_SPT; ++q)
+    if (b_begin + tid + q * EMIT_NT < b_end) load_raw<F>(src, g, lay, b_begin + tid + q * EMIT_NT, l, in[q]);
   __syncthreads();
   int r = 0;
-  for (int64_t rb = b_begin; rb < b_end; rb += NT, r ^= 1) {
+  for (int64_t rb = b_begin; rb < b_end; rb += EMIT_RS, r ^= 1) {
     uint32_t* cur = lcnt + r * nbl;
     uint32_t* nxt = lcnt + (r ^ 1) * nbl;
-    const int64_t b = rb + tid;
-    float gf[F];
-    const bool act = b < b_end && level_grad<F, MODE>(c, in.g, l, lr, gf);
-    uint32_t ent[8], rank[8];
-    LevelCell lc;
-    if (act) {
-      float pos[3], p[3];
-      raw_position<F>(src, in, pos);
-      normalize_pos(c, pos, p);
-      lc = level_cell(c.res[l], p);
+    bool act[EMIT_SPT];
+    float gf[EMIT_SPT][F], fr[EMIT_SPT][3];
+    uint32_t ent[EMIT_SPT][8], rank[EMIT_SPT][8];
 #pragma unroll
-      for (int cc = 0; cc < 8; ++cc) {
-        ent[cc] = corner_entry(lc, cc, l, c.mask[l]);
-        rank[cc] = atomicAdd(&cur[ent[cc] >> grp.log2_be], 1u);
+    for (int q = 0; q < EMIT_SPT; ++q) {
+      const int64_t b = rb + tid + q * EMIT_NT;
+      act[q] = b < b_end && level_grad<F, MODE>(c, in[q].g, l, lr, gf[q]);
+      if (act[q]) {
+        float pos[3], p[3];
+        raw_position<F>(src, in[q], pos);
+        normalize_pos(c, pos, p);
+        const LevelCell lc = level_cell(c.res[l], p);
+        fr[q][0] = lc.f[0];
+        fr[q][1] = lc.f[1];
+        fr[q][2] = lc.f[2];
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) {
+          ent[q][cc] = corner_entry(lc, cc, l, c.mask[l]);
+          rank[q][cc] = atomicAdd(&cur[ent[q][cc] >> grp.log2_be], 1u);
+        }
       }
+      if (b + EMIT_RS < b_end) load_raw<F>(src, g, lay, b + EMIT_RS, l, in[q]);
     }
-    if (b + NT < b_end) load_raw<F>(src, g, lay, b + NT, l, in);
     __syncthreads();
     if (tid < 64) {
       uint32_t carry = 0;
@@ -361,41 +376,59 @@ __global__ __launch_bounds__(emit_threads<F>()) void k_bin_emit(DevCfg c, PosSrc
       if (lane == 0) total_s[0] = carry;
     }
     __syncthreads();
-    if (act) {
+#pragma unroll
+    for (int q = 0; q < EMIT_SPT; ++q) {
+      if (!act[q]) continue;
+      const int ls = tid + q * EMIT_NT;
+      s_frac[ls] = make_float4(fr[q][0], fr[q][1], fr[q][2], 0.0f);
+      s_grad[ls] = FVec<F>::pack(gf[q]);
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
-        const uint32_t bk = ent[cc] >> grp.log2_be;
-        const uint32_t q = loff[bk] + rank[cc];
-        const float w = corner_weight(lc, cc);
-        float v[F];
-#pragma unroll
-        for (int f = 0; f < F; ++f) v[f] = gf[f] * w;
-        st_idx[q] = (uint16_t)(ent[cc] & be_mask);
-        st_val[q] = FVec<F>::pack(v);
-        if ((rank[cc] & (PAD_RUN - 1)) == 0) st_bkt[q / PAD_RUN] = (uint16_t)bk;
+        const uint32_t bk = ent[q][cc] >> grp.log2_be;
+        const uint32_t slot = loff[bk] + rank[q][cc];
+        st_idx[slot] = (uint16_t)(ent[q][cc] & be_mask);
+        st_ref[slot] = (uint16_t)(ls * 8 + cc);
+        if ((rank[q][cc] & (PAD_RUN - 1)) == 0) st_bkt[slot / PAD_RUN] = (uint16_t)bk;
       }
     }
     // zero pairs pad every run to a multiple of PAD_RUN
-    for (int j = tid; j < nbl; j += NT) {
+    for (int j = tid; j < nbl; j += EMIT_NT) {
       const uint32_t c0 = cur[j], c1 = pad_run(c0), o = loff[j];
       for (uint32_t k = c0; k < c1; ++k) {
-        float z[F];
-#pragma unroll
-        for (int f = 0; f < F; ++f) z[f] = 0.0f;
         st_idx[o + k] = 0;
-        st_val[o + k] = FVec<F>::pack(z);
+        st_ref[o + k] = REF_PAD;
       }
     }
     __syncthreads();
     const uint32_t nq = total_s[0] / PAD_RUN;
-    for (uint32_t qd = (uint32_t)tid; qd < nq; qd += NT) {
+    for (uint32_t qd = (uint32_t)tid; qd < nq; qd += EMIT_NT) {
       const uint32_t i = qd * PAD_RUN;
       const uint32_t dst = gdst[st_bkt[qd]] + i;  // a multiple of PAD_RUN
+      const uint2 refs = *reinterpret_cast<const uint2*>(st_ref + i);
+      const uint32_t rf[PAD_RUN] = {refs.x & 0xFFFFu, refs.x >> 16, refs.y & 0xFFFFu, refs.y >> 16};
+      float v[PAD_RUN * F];
+#pragma unroll
+      for (int k = 0; k < PAD_RUN; ++k) {
+        if (rf[k] == REF_PAD) {
+#pragma unroll
+          for (int f = 0; f < F; ++f) v[k * F + f] = 0.0f;
+        } else {
+          const float4 fq = s_frac[rf[k] >> 3];
+          LevelCell lc;
+          lc.f[0] = fq.x;
+          lc.f[1] = fq.y;
+          lc.f[2] = fq.z;
+          const float w = corner_weight(lc, (int)(rf[k] & 7u));
+          float gq[F];
+          FVec<F>::unpack(s_grad[rf[k] >> 3], gq);
+#pragma unroll
+          for (int f = 0; f < F; ++f) v[k * F + f] = gq[f] * w;
+        }
+      }
       *reinterpret_cast<uint2*>(pair_idx + dst) = *reinterpret_cast<const uint2*>(st_idx + i);
-      const float4* sv = reinterpret_cast<const float4*>(st_val + i);
       float4* gv = reinterpret_cast<float4*>(pair_val + (size_t)dst * F);
 #pragma unroll
-      for (int k = 0; k < F; ++k) gv[k] = sv[k];
+      for (int k = 0; k < F; ++k) gv[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
     }
   }
 }
@@ -588,7 +621,7 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   BinPlan p{};
   // int64 LDS accumulator of one bucket: 2^log2_be * F * 8 bytes = 64 KiB
   p.log2_be = c.F == 4 ? 11 : (c.F == 2 ? 12 : 13);
-  p.chunk = 4096;
+  p.chunk = 4 * EMIT_RS;
   p.nblk = (int)((n + p.chunk - 1) / p.chunk);
   int max_nbl = 0;
   for (int l = 0; l < c.L; ++l) {
@@ -596,9 +629,8 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
     if (nbl > max_nbl) max_nbl = nbl;
   }
   // pairs of one level: 8 per sample plus at most PAD_RUN - 1 padding pairs per bucket and emit round
-  const int nt = emit_nt(c.F);
-  const int64_t rounds = (p.chunk + nt - 1) / nt;
-  const int64_t pad_buckets = max_nbl < 8 * nt ? max_nbl : 8 * nt;
+  const int64_t rounds = (p.chunk + EMIT_RS - 1) / EMIT_RS;
+  const int64_t pad_buckets = max_nbl < 8 * EMIT_RS ? max_nbl : 8 * EMIT_RS;
   const int64_t per_level_pairs = n * 8 + (int64_t)p.nblk * rounds * pad_buckets * (PAD_RUN - 1);
   const int64_t pair_bytes = 2 + 4 * (int64_t)c.F;
   int lg = (int)(pair_budget_bytes / (size_t)(per_level_pairs * pair_bytes));
@@ -627,7 +659,7 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                            int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
                            hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  const int nt = emit_nt(c.F);
+  const int nt = EMIT_NT;
   for (int g0 = 0; g0 < c.L; g0 += plan.levels_per_group) {
     BinGroup grp{};
     grp.level0 = g0;
@@ -650,7 +682,7 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
     const size_t lds_count = sizeof(uint32_t) * (3 * (size_t)max_nbl + nt / 64);
     const size_t lds_acc = sizeof(unsigned long long) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
-    const size_t lds_emit = emit_lds_bytes(nt, max_nbl, c.F);
+    const size_t lds_emit = emit_lds_bytes(max_nbl, c.F);
     if (lds_emit > 160 * 1024 || lds_count > 160 * 1024) return hipErrorInvalidConfiguration;  // table too large
 #define FFN_BIN(FV, MV)                                                                                            \
   do {                                                                                                             \
