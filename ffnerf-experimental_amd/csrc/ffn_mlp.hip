@@ -19,12 +19,18 @@
 //   * Compositing needs the whole ray: sigma/rgb go to LDS, one barrier, and
 //     every wavefront runs the reference's scan trees on 64 lanes (one lane
 //     per sample, S lanes per ray) and picks its own samples' gradients.
-//   * Weight gradients dW = sum_s delta[o][s] act[i][s] are MFMAs with the
-//     samples as K: each 16x16 tile is transposed through a per-wave LDS
-//     scratch (4 ds_write_b32 + 1 ds_read_b128) and accumulated with
-//     ds_add_f32 into a per-block LDS copy of the gradient; each block writes
-//     one partial at the end (no staging buffers in HBM, unlike the
-//     reference's ~1.8 KB/sample SoA traffic).
+//   * Weight gradients dW = sum_s delta[o][s] act[i][s] need the samples as
+//     K.  Layer by layer in the backward, every wavefront writes its 16
+//     samples' deltas and input activations into a block-shared fp32 stash
+//     (rows = neurons, 64 sample columns); after a barrier the layer's 16x16
+//     gradient tiles are dealt round-robin over the four wavefronts, each
+//     accumulating its tiles over the 64 samples (16 MFMAs per tile) in
+//     registers for the whole kernel.  A wavefront so holds a quarter of the
+//     gradient (40 registers at the cfg2 shape), the weights are kept once
+//     (the backward reads them transposed), and two blocks fit on a CU.  At
+//     the end every wavefront stores its tiles into the block's partial
+//     (no staging buffers in HBM, unlike the reference's ~1.8 KB/sample SoA
+//     traffic).
 #include "ffn_device.h"
 #include "ffn_kernels.h"
 #include "ffn_mlp_common.h"
@@ -58,10 +64,12 @@ struct Arch {
   }
   static constexpr int gb_off(int k) { return g_off(k) + layer_out(k) * layer_in(k, LF); }
   static constexpr int g_total() { return g_off(FFN_N_LAYERS); }
-  static constexpr int XP = 20;  // transpose scratch pitch: 16 samples + 4 pad
-  static constexpr int x_per_wave = 64 * XP;
+  static constexpr int PSF = 64 + 4;       // stash pitch: 64 sample columns + 4 pad (conflict-free b128 reads)
+  static constexpr int stash_rows = 128;   // one layer's delta rows (<= 64) + input activation rows (<= 64)
   static constexpr int comp_floats = 2 * 256;  // double-buffered sigma[64] + rgb[64][3]
-  static constexpr int lds_floats() { return w_total() + g_total() + 4 * x_per_wave + comp_floats; }
+  static constexpr int lds_floats() { return w_total() + stash_rows * PSF + comp_floats; }
+  // two blocks per CU when the LDS allows it (160 KiB per CU)
+  static constexpr int blocks_per_cu() { return lds_floats() * 4 <= 80 * 1024 ? 2 : 1; }
 };
 
 // out tiles (D layout) = act(W . in + b), in given as D-layout tiles.  The
@@ -112,168 +120,90 @@ __device__ __forceinline__ void relu_mask(floatx4 (&d)[NT], const floatx4 (&act)
     for (int r = 0; r < 4; ++r) d[t][r] = act[t][r] > 0.0f ? d[t][r] : 0.0f;
 }
 
-template <int NT>
-__device__ __forceinline__ void stash_D(float* __restrict__ sx, const floatx4 (&v)[NT], int g, int s) {
-  constexpr int XP = 20;
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sx[(16 * t + 4 * g + r) * XP + s] = v[t][r];
-}
-
-template <int NT>
-__device__ __forceinline__ void load_op(const float* __restrict__ sx, floatx4 (&op)[NT], int g, int m) {
-  constexpr int XP = 20;
-#pragma unroll
-  for (int t = 0; t < NT; ++t) op[t] = *reinterpret_cast<const floatx4*>(sx + (16 * t + m) * XP + 4 * g);
-}
-
-// dW[o][i] += sum_s delta[o][s] act[i][s] and db[o] += sum_s delta[o][s] over the wave's 16 samples.
-// dop: delta operands (OT tiles), aop: activation operands (IT tiles), already transposed.
+// Weight-gradient tiles of one layer held by one wavefront.  The layer's 16x16 tiles i = T * IT + Tp
+// (rows 16T.., columns 16Tp..) are dealt round-robin: wavefront w holds i = 4m + w in w[m] (D layout) and
+// in b[m] a per-lane partial of the bias gradient when Tp = 0.
 template <int OT, int IT>
-__device__ __forceinline__ void accum_dW(float* __restrict__ gW, float* __restrict__ gB, int out_dim, int in_dim,
-                                         const floatx4 (&dop)[OT], const floatx4 (&aop)[IT], int g, int s) {
-#pragma unroll
-  for (int T = 0; T < OT; ++T) {
-    float bs = (dop[T][0] + dop[T][1]) + (dop[T][2] + dop[T][3]);
-    bs += __shfl_xor(bs, 16);
-    bs += __shfl_xor(bs, 32);
-    if (g == 0 && 16 * T + s < out_dim) atomicAdd(gB + 16 * T + s, bs);
-  }
-#pragma unroll
-  for (int T = 0; T < OT; ++T) {
-#pragma unroll
-    for (int Tp = 0; Tp < IT; ++Tp) {
-      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc = mfma4(dop[T][q], aop[Tp][q], acc);
-      const int col = 16 * Tp + s;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * T + 4 * g + r;
-        if (row < out_dim && col < in_dim) atomicAdd(gW + row * in_dim + col, acc[r]);
-      }
-    }
-  }
-}
-
-// Weight-gradient accumulators of one layer held in registers (AGPRs) for all
-// the tiles a wavefront processes: w[T][Tp] is the D-layout 16x16 tile
-// (rows 16T + 4g + r, columns 16Tp + lane%16), b[T] a per-lane partial bias sum.
-template <int OT, int IT>
-struct GradAcc {
-  floatx4 w[OT][IT];
-  float b[OT];
+struct WaveGrad {
+  static constexpr int N = OT * IT / 4;
+  static_assert(OT * IT % 4 == 0, "a layer's gradient tiles split evenly over four wavefronts");
+  floatx4 w[N];
+  float b[N];
   __device__ __forceinline__ void zero() {
 #pragma unroll
-    for (int T = 0; T < OT; ++T) {
-      b[T] = 0.0f;
-#pragma unroll
-      for (int Tp = 0; Tp < IT; ++Tp) w[T][Tp] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < N; ++m) {
+      w[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+      b[m] = 0.0f;
     }
   }
-  // dW += delta . act^T and db += delta over the wave's 16 samples (operands already transposed)
-  __device__ __forceinline__ void add(const floatx4 (&dop)[OT], const floatx4 (&aop)[IT]) {
+};
+
+// this wavefront's samples (stash column col) of a layer: delta rows [0, 16 OT), activation rows
+// [16 OT, 16 (OT + IT)); both given as D-layout tiles (lane (g, s) holds neurons 16t + 4g + r)
+template <int OT, int IT, int PSF>
+__device__ __forceinline__ void stash_layer(float* __restrict__ st, const floatx4 (&d)[OT], const floatx4 (&act)[IT],
+                                            int g, int col) {
 #pragma unroll
-    for (int T = 0; T < OT; ++T) b[T] += (dop[T][0] + dop[T][1]) + (dop[T][2] + dop[T][3]);
+  for (int t = 0; t < OT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) st[(16 * t + 4 * g + r) * PSF + col] = d[t][r];
+#pragma unroll
+  for (int t = 0; t < IT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) st[(16 * (OT + t) + 4 * g + r) * PSF + col] = act[t][r];
+}
+
+// dW tiles of this wavefront over the 64 stashed samples: 16 k-steps of 4, lane group g taking sample
+// 16g + kk at k-step kk (the same permutation for both operands)
+template <int OT, int IT, int PSF>
+__device__ __forceinline__ void layer_dw(const float* __restrict__ st, WaveGrad<OT, IT>& acc, int wave, int g, int s) {
+#pragma unroll
+  for (int m = 0; m < WaveGrad<OT, IT>::N; ++m) {
+    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    const float* drow = st + (16 * T + s) * PSF + 16 * g;
+    const float* arow = st + (16 * (OT + Tp) + s) * PSF + 16 * g;
+    floatx4 dv[4], av[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      dv[q] = *reinterpret_cast<const floatx4*>(drow + 4 * q);
+      av[q] = *reinterpret_cast<const floatx4*>(arow + 4 * q);
+    }
+    floatx4 c = acc.w[m];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int T = 0; T < OT; ++T)
+      for (int e = 0; e < 4; ++e) c = mfma4(dv[q][e], av[q][e], c);
+    acc.w[m] = c;
+    if (Tp == 0) {
+      float bs = 0.0f;
 #pragma unroll
-        for (int Tp = 0; Tp < IT; ++Tp) w[T][Tp] = mfma4(dop[T][q], aop[Tp][q], w[T][Tp]);
-  }
-  // add this wavefront's sums into the block's LDS gradient (callers serialise the waves)
-  __device__ __forceinline__ void flush(float* __restrict__ gW, float* __restrict__ gB, int out_dim, int in_dim,
-                                        int g, int s) {
-#pragma unroll
-    for (int T = 0; T < OT; ++T) {
-      float bs = b[T];
-      bs += __shfl_xor(bs, 16);
-      bs += __shfl_xor(bs, 32);
-      if (g == 0 && 16 * T + s < out_dim) gB[16 * T + s] += bs;
-#pragma unroll
-      for (int Tp = 0; Tp < IT; ++Tp) {
-        const int col = 16 * Tp + s;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = 16 * T + 4 * g + r;
-          if (row < out_dim && col < in_dim) gW[row * in_dim + col] += w[T][Tp][r];
-        }
-      }
+      for (int q = 0; q < 4; ++q) bs += (dv[q][0] + dv[q][1]) + (dv[q][2] + dv[q][3]);
+      acc.b[m] += bs;
     }
   }
-};
+}
 
+// store this wavefront's tiles of a layer into the block's partial gradient (packed [O][In] + [O])
 template <int OT, int IT>
-__device__ __forceinline__ void transpose_ops(float* __restrict__ sx, const floatx4 (&delta)[OT],
-                                              const floatx4 (&act)[IT], floatx4 (&dop)[OT], floatx4 (&aop)[IT],
-                                              int g, int s) {
-  stash_D(sx, delta, g, s);
-  wave_lds_sync();
-  load_op(sx, dop, g, s);
-  wave_lds_sync();
-  stash_D(sx, act, g, s);
-  wave_lds_sync();
-  load_op(sx, aop, g, s);
-  wave_lds_sync();
-}
-
-template <int OT, int IT>
-__device__ __forceinline__ void layer_grad_reg(float* __restrict__ sx, GradAcc<OT, IT>& acc,
-                                               const floatx4 (&delta)[OT], const floatx4 (&act)[IT], int g, int s) {
-  floatx4 dop[OT], aop[IT];
-  transpose_ops(sx, delta, act, dop, aop, g, s);
-  acc.add(dop, aop);
-}
-
-template <int OT, int IT>
-__device__ __forceinline__ void layer_grad(float* __restrict__ sx, float* __restrict__ gW, float* __restrict__ gB,
-                                           int out_dim, int in_dim, const floatx4 (&delta)[OT],
-                                           const floatx4 (&act)[IT], int g, int s) {
-  floatx4 dop[OT], aop[IT];
-  stash_D(sx, delta, g, s);
-  wave_lds_sync();
-  load_op(sx, dop, g, s);
-  wave_lds_sync();
-  stash_D(sx, act, g, s);
-  wave_lds_sync();
-  load_op(sx, aop, g, s);
-  wave_lds_sync();
-  accum_dW(gW, gB, out_dim, in_dim, dop, aop, g, s);
-}
-
-// Register-resident gradient accumulators of every layer (used when they fit:
-// at most 48 16x16 tiles = 192 AGPRs per lane); otherwise the block
-// accumulates in LDS.
-template <int LF, int ND, int NC>
-constexpr int acc_tiles() {
-  return 4 + 16 * (NC - 1) + 8 + 4 + 16 * (ND - 1) + 4 * (LF / 16);
-}
-
-template <int LF, int ND, int NC, bool REG>
-struct AccSet {
-  __device__ __forceinline__ void zero() {}
-};
-template <int LF, int ND, int NC>
-struct AccSet<LF, ND, NC, true> {
-  GradAcc<1, 4> c_out;
-  GradAcc<4, 4> c_h[NC > 1 ? NC - 1 : 1];  // Wc_01, Wc_12, Wc_23
-  GradAcc<4, 2> c_in;
-  GradAcc<1, 4> d_out;
-  GradAcc<4, 4> d_h[ND > 1 ? ND - 1 : 1];  // Wd_01, Wd_12
-  GradAcc<4, LF / 16> d_in;
-  __device__ __forceinline__ void zero() {
-    c_out.zero();
+__device__ __forceinline__ void flush_layer(float* __restrict__ dst, int O, int In, const WaveGrad<OT, IT>& acc,
+                                            int wave, int g, int s) {
 #pragma unroll
-    for (int i = 0; i < NC - 1; ++i) c_h[i].zero();
-    c_in.zero();
-    d_out.zero();
+  for (int m = 0; m < WaveGrad<OT, IT>::N; ++m) {
+    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    const int col = 16 * Tp + s;
 #pragma unroll
-    for (int i = 0; i < ND - 1; ++i) d_h[i].zero();
-    d_in.zero();
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * T + 4 * g + r;
+      if (row < O && col < In) dst[row * In + col] = acc.w[m][r];
+    }
+    if (Tp == 0) {
+      float bs = acc.b[m];
+      bs += __shfl_xor(bs, 16);
+      bs += __shfl_xor(bs, 32);
+      if (g == 0 && 16 * T + s < O) dst[O * In + 16 * T + s] = bs;
+    }
   }
-};
+}
 
 // stage the weights of every active layer into LDS (zero-padded rows, pitch in+1)
 template <int LF, int ND, int NC>
@@ -383,32 +313,41 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
 }
 
 template <int LF, int ND, int NC, int FEAT>
-__global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
+__global__ __launch_bounds__(256, 2) void k_mlp(MlpArgs a) {
   using A = Arch<LF, ND, NC>;
   constexpr int KA = LF / 4;  // a0 values per lane (k-steps of the first layer)
+  constexpr int PSF = A::PSF;
   extern __shared__ float smem[];
   float* sW = smem;
-  float* sG = smem + A::w_total();
+  float* sS = smem + A::w_total();            // per-layer stash of deltas and activations
+  float* sC = sS + A::stash_rows * A::PSF;    // compositing inputs (double-buffered)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
-  float* sX = sG + A::g_total() + wave * A::x_per_wave;
-  float* sC = smem + A::w_total() + A::g_total() + 4 * A::x_per_wave;
+  const int col = wave * 16 + s;              // this lane's stash column
   const bool train = a.do_train != 0;
   const DevCfg& c = a.c;
   const int S = a.S, log2S = a.log2S;
   const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
 
-  // stage weights and clear the gradient accumulators
   stage_weights<LF, ND, NC>(sW, a.w, tid, 256);
-  if (train)
-    for (int e = tid; e < A::g_total(); e += 256) sG[e] = 0.0f;
   __syncthreads();
 
   const float Dhalf = half_box_diagonal(c);
   const bool proposals = train && a.occ_strength > 0.0f;
 
-  constexpr bool REG_ACC = acc_tiles<LF, ND, NC>() <= 48;
-  AccSet<LF, ND, NC, REG_ACC> ga;
-  ga.zero();
+  WaveGrad<1, 4> gc_out;
+  WaveGrad<4, 4> gc_h[NC > 1 ? NC - 1 : 1];  // Wc_01, Wc_12, Wc_23
+  WaveGrad<4, 2> gc_in;
+  WaveGrad<1, 4> gd_out;
+  WaveGrad<4, 4> gd_h[ND > 1 ? ND - 1 : 1];  // Wd_01, Wd_12
+  WaveGrad<4, LF / 16> gd_in;
+  gc_out.zero();
+#pragma unroll
+  for (int i = 0; i < (NC > 1 ? NC - 1 : 1); ++i) gc_h[i].zero();
+  gc_in.zero();
+  gd_out.zero();
+#pragma unroll
+  for (int i = 0; i < (ND > 1 ? ND - 1 : 1); ++i) gd_h[i].zero();
+  gd_in.zero();
 
   int parity = 0;
   for (int64_t tile = blockIdx.x; tile < a.n_tiles; tile += gridDim.x, parity ^= 1) {
@@ -416,7 +355,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     float* sRgb = sSig + 64;
     // ------------------------------------------------------------------
     // forward: this lane's sample in the MLP layout
-    const int64_t b = tile * 64 + wave * 16 + s;
+    const int64_t b = tile * 64 + col;
     const bool valid = (uint64_t)b < n_samples;
     const int64_t ray = valid ? (b >> log2S) : 0;
     float a0r[KA];
@@ -443,10 +382,10 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     if (g == 0) {
       float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
       if (dt_b <= 0.0f) sig = 0.0f;
-      sSig[wave * 16 + s] = sig;
-      sRgb[(wave * 16 + s) * 3 + 0] = rgb_s[0];
-      sRgb[(wave * 16 + s) * 3 + 1] = rgb_s[1];
-      sRgb[(wave * 16 + s) * 3 + 2] = rgb_s[2];
+      sSig[col] = sig;
+      sRgb[col * 3 + 0] = rgb_s[0];
+      sRgb[col * 3 + 1] = rgb_s[1];
+      sRgb[col * 3 + 2] = rgb_s[2];
     }
     __syncthreads();
 
@@ -457,10 +396,10 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
     if (!train) continue;
 
     // ------------------------------------------------------------------
-    // backward of this wave's 16 samples
-    const int src = wave * 16 + s;
-    const float dLds = __shfl(dLds_j, src);
-    const float dLdc0 = __shfl(dLdc_j[0], src), dLdc1 = __shfl(dLdc_j[1], src), dLdc2 = __shfl(dLdc_j[2], src);
+    // backward of this wave's 16 samples; every layer's deltas and inputs go through the stash for the
+    // block's weight-gradient tiles (barrier, this wave's tiles, barrier before the stash is reused)
+    const float dLds = __shfl(dLds_j, col);
+    const float dLdc0 = __shfl(dLdc_j[0], col), dLdc1 = __shfl(dLdc_j[1], col), dLdc2 = __shfl(dLdc_j[2], col);
     floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
     floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
     if (g == 0 && valid) {
@@ -471,68 +410,65 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
       dco[0][2] = d3[2];
       ddo[0][0] = dd0;
     }
-    // color backward
+    // colour output layer
     floatx4 dc[NC][4];
+    stash_layer<1, 4, PSF>(sS, dco, hc[NC - 1], g, col);
 #pragma unroll
     for (int t = 0; t < 4; ++t) dc[NC - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
     bwd_tiles<4, 1>(sW + A::w_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), dco, dc[NC - 1], g, s);
     relu_mask(dc[NC - 1], hc[NC - 1]);
-    if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_out, dco, hc[NC - 1], g, s);
-    else layer_grad<1, 4>(sX, sG + A::g_off(FFN_WC_OUT), sG + A::gb_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, dco,
-                          hc[NC - 1], g, s);
-    if constexpr (NC >= 4) {
+    __syncthreads();
+    layer_dw<1, 4, PSF>(sS, gc_out, wave, g, s);
+    __syncthreads();
+    // hidden colour layers (Wc_23, Wc_12, Wc_01)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dc[2][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_23), A::pitch(FFN_WC_23), dc[3], dc[2], g, s);
-      relu_mask(dc[2], hc[2]);
-      if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_h[2], dc[3], hc[2], g, s);
-      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_23), sG + A::gb_off(FFN_WC_23), FFN_M, FFN_M, dc[3], hc[2], g, s);
-    }
-    if constexpr (NC >= 3) {
+    for (int i = NC - 1; i >= 1; --i) {
+      const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
+      stash_layer<4, 4, PSF>(sS, dc[i], hc[i - 1], g, col);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dc[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_12), A::pitch(FFN_WC_12), dc[2], dc[1], g, s);
-      relu_mask(dc[1], hc[1]);
-      if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_h[1], dc[2], hc[1], g, s);
-      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_12), sG + A::gb_off(FFN_WC_12), FFN_M, FFN_M, dc[2], hc[1], g, s);
+      for (int t = 0; t < 4; ++t) dc[i - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<4, 4>(sW + A::w_off(k), A::pitch(k), dc[i], dc[i - 1], g, s);
+      relu_mask(dc[i - 1], hc[i - 1]);
+      __syncthreads();
+      layer_dw<4, 4, PSF>(sS, gc_h[i - 1], wave, g, s);
+      __syncthreads();
     }
-    if constexpr (NC >= 2) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) dc[0][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd_tiles<4, 4>(sW + A::w_off(FFN_WC_01), A::pitch(FFN_WC_01), dc[1], dc[0], g, s);
-      relu_mask(dc[0], hc[0]);
-      if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_h[0], dc[1], hc[0], g, s);
-      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WC_01), sG + A::gb_off(FFN_WC_01), FFN_M, FFN_M, dc[1], hc[0], g, s);
-    }
-    // color input layer: its gradient, and the dout part of its input delta
-    if constexpr (REG_ACC) layer_grad_reg(sX, ga.c_in, dc[0], acin, g, s);
-    else layer_grad<4, 2>(sX, sG + A::g_off(FFN_WC_IN), sG + A::gb_off(FFN_WC_IN), FFN_M, FFN_C_IN, dc[0], acin, g, s);
+    // colour input layer: its gradient, and the dout part of its input delta
+    stash_layer<4, 2, PSF>(sS, dc[0], acin, g, col);
     bwd_tiles<1, 4>(sW + A::w_off(FFN_WC_IN), A::pitch(FFN_WC_IN), dc[0], ddo, g, s);
-    // density backward
+    __syncthreads();
+    layer_dw<4, 2, PSF>(sS, gc_in, wave, g, s);
+    __syncthreads();
+    // density output layer
     floatx4 dd[ND][4];
+    stash_layer<1, 4, PSF>(sS, ddo, hd[ND - 1], g, col);
 #pragma unroll
     for (int t = 0; t < 4; ++t) dd[ND - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
     bwd_tiles<4, 1>(sW + A::w_off(FFN_WD_OUT), A::pitch(FFN_WD_OUT), ddo, dd[ND - 1], g, s);
     relu_mask(dd[ND - 1], hd[ND - 1]);
-    if constexpr (REG_ACC) layer_grad_reg(sX, ga.d_out, ddo, hd[ND - 1], g, s);
-    else layer_grad<1, 4>(sX, sG + A::g_off(FFN_WD_OUT), sG + A::gb_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, ddo,
-                          hd[ND - 1], g, s);
-    if constexpr (ND >= 3) {
+    __syncthreads();
+    layer_dw<1, 4, PSF>(sS, gd_out, wave, g, s);
+    __syncthreads();
+    // hidden density layers (Wd_12, Wd_01)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dd[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd_tiles<4, 4>(sW + A::w_off(FFN_WD_12), A::pitch(FFN_WD_12), dd[2], dd[1], g, s);
-      relu_mask(dd[1], hd[1]);
-      if constexpr (REG_ACC) layer_grad_reg(sX, ga.d_h[1], dd[2], hd[1], g, s);
-      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_12), sG + A::gb_off(FFN_WD_12), FFN_M, FFN_M, dd[2], hd[1], g, s);
-    }
-    if constexpr (ND >= 2) {
+    for (int i = ND - 1; i >= 1; --i) {
+      const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
+      stash_layer<4, 4, PSF>(sS, dd[i], hd[i - 1], g, col);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dd[0][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd_tiles<4, 4>(sW + A::w_off(FFN_WD_01), A::pitch(FFN_WD_01), dd[1], dd[0], g, s);
-      relu_mask(dd[0], hd[0]);
-      if constexpr (REG_ACC) layer_grad_reg(sX, ga.d_h[0], dd[1], hd[0], g, s);
-      else layer_grad<4, 4>(sX, sG + A::g_off(FFN_WD_01), sG + A::gb_off(FFN_WD_01), FFN_M, FFN_M, dd[1], hd[0], g, s);
+      for (int t = 0; t < 4; ++t) dd[i - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      bwd_tiles<4, 4>(sW + A::w_off(k), A::pitch(k), dd[i], dd[i - 1], g, s);
+      relu_mask(dd[i - 1], hd[i - 1]);
+      __syncthreads();
+      layer_dw<4, 4, PSF>(sS, gd_h[i - 1], wave, g, s);
+      __syncthreads();
     }
+    // density input layer: deltas in rows [0, 64), the encoding (neuron KA g + kk in a0r[kk]) in rows 64..
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sS[(16 * t + 4 * g + r) * PSF + col] = dd[0][t][r];
+#pragma unroll
+    for (int kk = 0; kk < KA; ++kk) sS[(64 + KA * g + kk) * PSF + col] = a0r[kk];
     // encoding gradient dL/da0 = Wd_in^T . delta_d1 -> HBM for the hash scatter
     {
       floatx4 ga[LF / 16];
@@ -557,44 +493,23 @@ __global__ __launch_bounds__(256, 1) void k_mlp(MlpArgs a) {
         }
       }
     }
-    // first-layer weight gradient: a0 is held with the permuted neuron order
-    {
-      floatx4 dop[4], aop[LF / 16];
-      stash_D(sX, dd[0], g, s);
-      wave_lds_sync();
-      load_op(sX, dop, g, s);
-      wave_lds_sync();
-#pragma unroll
-      for (int kk = 0; kk < KA; ++kk) sX[(KA * g + kk) * A::XP + s] = a0r[kk];
-      wave_lds_sync();
-      load_op(sX, aop, g, s);
-      wave_lds_sync();
-      if constexpr (REG_ACC) ga.d_in.add(dop, aop);
-      else accum_dW(sG + A::g_off(FFN_WD_IN), sG + A::gb_off(FFN_WD_IN), FFN_M, LF, dop, aop, g, s);
-    }
+    __syncthreads();
+    layer_dw<4, LF / 16, PSF>(sS, gd_in, wave, g, s);
+    // no barrier: the stash is next written after the next tile's compositing barrier
   }
 
   if (train) {
-    if constexpr (REG_ACC) {
-      // add the four wavefronts' register sums into the block's LDS gradient, one wave at a time
-      for (int w = 0; w < 4; ++w) {
-        __syncthreads();
-        if (wave == w) {
-          ga.c_out.flush(sG + A::g_off(FFN_WC_OUT), sG + A::gb_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, g, s);
-          if constexpr (NC >= 2) ga.c_h[0].flush(sG + A::g_off(FFN_WC_01), sG + A::gb_off(FFN_WC_01), FFN_M, FFN_M, g, s);
-          if constexpr (NC >= 3) ga.c_h[1].flush(sG + A::g_off(FFN_WC_12), sG + A::gb_off(FFN_WC_12), FFN_M, FFN_M, g, s);
-          if constexpr (NC >= 4) ga.c_h[2].flush(sG + A::g_off(FFN_WC_23), sG + A::gb_off(FFN_WC_23), FFN_M, FFN_M, g, s);
-          ga.c_in.flush(sG + A::g_off(FFN_WC_IN), sG + A::gb_off(FFN_WC_IN), FFN_M, FFN_C_IN, g, s);
-          ga.d_out.flush(sG + A::g_off(FFN_WD_OUT), sG + A::gb_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, g, s);
-          if constexpr (ND >= 2) ga.d_h[0].flush(sG + A::g_off(FFN_WD_01), sG + A::gb_off(FFN_WD_01), FFN_M, FFN_M, g, s);
-          if constexpr (ND >= 3) ga.d_h[1].flush(sG + A::g_off(FFN_WD_12), sG + A::gb_off(FFN_WD_12), FFN_M, FFN_M, g, s);
-          ga.d_in.flush(sG + A::g_off(FFN_WD_IN), sG + A::gb_off(FFN_WD_IN), FFN_M, LF, g, s);
-        }
-      }
-    }
-    __syncthreads();
+    // every wavefront stores its tiles into the block's partial gradient
     float* dst = a.partials + (int64_t)blockIdx.x * A::g_total();
-    for (int e = tid; e < A::g_total(); e += 256) dst[e] = sG[e];
+    flush_layer(dst + A::g_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, gc_out, wave, g, s);
+    if constexpr (NC >= 2) flush_layer(dst + A::g_off(FFN_WC_01), FFN_M, FFN_M, gc_h[0], wave, g, s);
+    if constexpr (NC >= 3) flush_layer(dst + A::g_off(FFN_WC_12), FFN_M, FFN_M, gc_h[1], wave, g, s);
+    if constexpr (NC >= 4) flush_layer(dst + A::g_off(FFN_WC_23), FFN_M, FFN_M, gc_h[2], wave, g, s);
+    flush_layer(dst + A::g_off(FFN_WC_IN), FFN_M, FFN_C_IN, gc_in, wave, g, s);
+    flush_layer(dst + A::g_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, gd_out, wave, g, s);
+    if constexpr (ND >= 2) flush_layer(dst + A::g_off(FFN_WD_01), FFN_M, FFN_M, gd_h[0], wave, g, s);
+    if constexpr (ND >= 3) flush_layer(dst + A::g_off(FFN_WD_12), FFN_M, FFN_M, gd_h[1], wave, g, s);
+    flush_layer(dst + A::g_off(FFN_WD_IN), FFN_M, LF, gd_in, wave, g, s);
   }
 }
 
@@ -708,12 +623,12 @@ bool mlp_supported(int LF, int nd, int nc) {
   return false;
 }
 
-size_t mlp_lds_bytes(int LF, int nd, int nc) {
+int mlp_blocks_per_cu(int LF, int nd, int nc) {
 #define X(l, d, n) \
-  if (LF == l && nd == d && nc == n) return sizeof(float) * (size_t)Arch<l, d, n>::lds_floats();
+  if (LF == l && nd == d && nc == n) return Arch<l, d, n>::blocks_per_cu();
   FFN_MLP_CONFIGS(X)
 #undef X
-  return 0;
+  return 1;
 }
 
 hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
