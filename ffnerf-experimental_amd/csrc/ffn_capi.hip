@@ -348,7 +348,8 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   while ((1u << log2S) < spr) ++log2S;
   const int64_t N = (int64_t)num_rays * spr;
   const int64_t n_tiles = (N + 63) / 64;
-  int n_blocks = (h->n_cu > 0 ? h->n_cu : 256) * (mlp16 ? 1 : ffn::mlp_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc));
+  int n_blocks = (h->n_cu > 0 ? h->n_cu : 256) * (mlp16 ? ffn::mlp16_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc)
+                                                          : ffn::mlp_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc));
   if (n_blocks > n_tiles) n_blocks = (int)n_tiles;
 
   FFN_HIP(h->Ts.ensure(sizeof(float) * N));

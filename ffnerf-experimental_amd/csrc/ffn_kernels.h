@@ -201,6 +201,7 @@ hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, co
 // fused MLP forward + compositing + loss + backward + proposals, per 64-sample tile
 bool mlp_supported(int LF, int nd, int nc);
 int mlp_blocks_per_cu(int LF, int nd, int nc);  // blocks of launch_mlp that fit on one CU
+int mlp16_blocks_per_cu(int LF, int nd, int nc);  // blocks of launch_mlp16 that fit on one CU
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
 // the same step on fp16 (forward) / bf16 (backward, weight gradients) MFMAs with fp32 accumulation
 bool mlp16_supported(int LF, int nd, int nc);

@@ -16,16 +16,15 @@
 //   * Weights live in LDS twice, fp16 row-major for the forward (A = W) and
 //     fp16 transposed for the backward (A = W^T); every A operand is one
 //     8-byte LDS read.
-//   * Weight gradients dW = delta . act^T need the samples as K.  Every
-//     wavefront writes its deltas and activations, transposed, into a
-//     block-shared bf16 stash (rows = neurons, 64 samples per row); after one
-//     barrier the 16x16 gradient tiles of all layers are split round-robin
-//     over the four wavefronts, each of which accumulates its tiles over all
-//     64 samples of the tile (4 MFMAs per tile) in registers for the whole
-//     kernel.  A wavefront so holds about a quarter of the gradient instead of
-//     all of it, which keeps the kernel free of register spills.
-#include <utility>
-
+//   * Weight gradients dW = delta . act^T need the samples as K.  Layer by
+//     layer in the backward, every wavefront writes its deltas and the layer's
+//     input activations, transposed, into a block-shared bf16 stash (rows =
+//     neurons, 64 samples per row); after a barrier the layer's 16x16 gradient
+//     tiles are dealt round-robin over the four wavefronts, each of which
+//     accumulates its tiles over the tile's 64 samples (4 MFMAs per tile) in
+//     registers for the whole kernel and stores them into the block's partial
+//     at the end.  A wavefront so holds about a quarter of the gradient, and
+//     the one-layer stash lets two blocks share a CU.
 #include "ffn_device.h"
 #include "ffn_kernels.h"
 #include "ffn_mlp_common.h"
@@ -104,19 +103,10 @@ struct Arch16 {
     return o;
   }
   static constexpr int b_floats() { return b_off(FFN_N_LAYERS); }
-  // stash rows (bf16, PS per row)
+  // one layer's stash (bf16, PS per row): delta rows, then the layer's input activation rows
   static constexpr int PS = 64 + 4;
-  static constexpr int a_a0() { return 0; }
-  static constexpr int a_hd(int i) { return LF + 64 * i; }
-  static constexpr int a_acin() { return LF + 64 * ND; }
-  static constexpr int a_hc(int i) { return LF + 64 * ND + 32 + 64 * i; }
-  static constexpr int a_rows() { return LF + 64 * ND + 32 + 64 * NC; }
-  static constexpr int d_hd(int i) { return 64 * i; }
-  static constexpr int d_dout() { return 64 * ND; }
-  static constexpr int d_hc(int i) { return 64 * ND + 16 + 64 * i; }
-  static constexpr int d_cout() { return 64 * ND + 16 + 64 * NC; }
-  static constexpr int d_rows() { return 64 * ND + 16 + 64 * NC + 16; }
-  static constexpr int stash_halves() { return (a_rows() + d_rows()) * PS; }
+  static constexpr int stash_rows = 128;
+  static constexpr int stash_halves() { return stash_rows * PS; }
   // packed gradient (same layout as make_layout)
   static constexpr int gsz(int k) {
     return layer_active(k, ND, NC) ? layer_out(k) * layer_in(k, LF) + layer_out(k) : 0;
@@ -131,50 +121,8 @@ struct Arch16 {
   static constexpr size_t lds_bytes() {
     return (size_t)w_halves() * 2 + (size_t)b_floats() * 4 + (size_t)stash_halves() * 2 + comp_floats * 4;
   }
-  static_assert((size_t)g_total() * 4 <= (size_t)stash_halves() * 2, "gradient flush reuses the stash");
-
-  // weight-gradient tiles: layer k, output tile T (16 rows), input tile Tp (16 columns)
-  static constexpr int ot(int k) { return (k == FFN_WD_OUT || k == FFN_WC_OUT) ? 1 : 4; }
-  static constexpr int it(int k) { return layer_in(k, LF) / 16; }
-  static constexpr int dstash(int k) {
-    return k == FFN_WD_IN ? d_hd(0) : k == FFN_WD_01 ? d_hd(1) : k == FFN_WD_12 ? d_hd(2) : k == FFN_WD_OUT ? d_dout()
-         : k == FFN_WC_IN ? d_hc(0) : k == FFN_WC_01 ? d_hc(1) : k == FFN_WC_12 ? d_hc(2) : k == FFN_WC_23 ? d_hc(3)
-         : d_cout();
-  }
-  static constexpr int astash(int k) {
-    return k == FFN_WD_IN ? a_a0() : k == FFN_WD_01 ? a_hd(0) : k == FFN_WD_12 ? a_hd(1) : k == FFN_WD_OUT ? a_hd(ND - 1)
-         : k == FFN_WC_IN ? a_acin() : k == FFN_WC_01 ? a_hc(0) : k == FFN_WC_12 ? a_hc(1) : k == FFN_WC_23 ? a_hc(2)
-         : a_hc(NC - 1);
-  }
-  static constexpr int n_tiles() {
-    int n = 0;
-    for (int k = 0; k < FFN_N_LAYERS; ++k)
-      if (layer_active(k, ND, NC)) n += ot(k) * it(k);
-    return n;
-  }
-  struct TileRef {
-    int k, T, Tp;
-  };
-  static constexpr TileRef tile(int i) {
-    for (int k = 0; k < FFN_N_LAYERS; ++k) {
-      if (!layer_active(k, ND, NC)) continue;
-      const int n = ot(k) * it(k);
-      if (i < n) return TileRef{k, i / it(k), i % it(k)};
-      i -= n;
-    }
-    return TileRef{-1, 0, 0};
-  }
-  static constexpr int per_wave() { return (n_tiles() + 3) / 4; }
+  static constexpr int blocks_per_cu() { return lds_bytes() <= 80 * 1024 ? 2 : 1; }
 };
-
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 // forward layer: out tiles = act(W . in + b); in[kb] is the fp16 B operand of k-block kb
 template <int OT, int KB>
@@ -251,16 +199,77 @@ __device__ __forceinline__ void stash_tiles(__bf16* __restrict__ st, int row0, c
     for (int r = 0; r < 4; ++r) st[(row0 + 16 * t + 4 * g + r) * PS + col] = (__bf16)(float)v[t][r];
 }
 
+// Weight-gradient tiles of one layer held by one wavefront: tiles i = T * IT + Tp dealt round-robin,
+// wavefront w holding i = 4m + w (D layout) and a per-lane partial of the bias gradient when Tp = 0.
+template <int OT, int IT>
+struct WaveGrad16 {
+  static constexpr int N = OT * IT / 4;
+  static_assert(OT * IT % 4 == 0, "a layer's gradient tiles split evenly over four wavefronts");
+  floatx4 w[N];
+  float b[N];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int m = 0; m < N; ++m) {
+      w[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+      b[m] = 0.0f;
+    }
+  }
+};
+
+// this wavefront's dW tiles over the 64 stashed samples (delta rows [0, 16 OT), activation rows after)
+template <int OT, int IT, int PS>
+__device__ __forceinline__ void layer_dw16(const __bf16* __restrict__ st, WaveGrad16<OT, IT>& acc, int wave, int g,
+                                           int s) {
+#pragma unroll
+  for (int m = 0; m < WaveGrad16<OT, IT>::N; ++m) {
+    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    const __bf16* drow = st + (16 * T + s) * PS + 4 * g;
+    const __bf16* arow = st + (16 * (OT + Tp) + s) * PS + 4 * g;
+    floatx4 c = acc.w[m];
+    float bs = acc.b[m];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bf16x4 dv = *reinterpret_cast<const bf16x4*>(drow + 16 * q);
+      const bf16x4 av = *reinterpret_cast<const bf16x4*>(arow + 16 * q);
+      c = mfma_bf16(dv, av, c);
+      if (Tp == 0) bs += ((float)dv[0] + (float)dv[1]) + ((float)dv[2] + (float)dv[3]);
+    }
+    acc.w[m] = c;
+    acc.b[m] = bs;
+  }
+}
+
+// store this wavefront's tiles of a layer into the block's partial gradient (packed [O][In] + [O])
+template <int OT, int IT>
+__device__ __forceinline__ void flush_layer16(float* __restrict__ dst, int O, int In, const WaveGrad16<OT, IT>& acc,
+                                              int wave, int g, int s) {
+#pragma unroll
+  for (int m = 0; m < WaveGrad16<OT, IT>::N; ++m) {
+    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    const int col = 16 * Tp + s;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * T + 4 * g + r;
+      if (row < O && col < In) dst[row * In + col] = acc.w[m][r];
+    }
+    if (Tp == 0) {
+      float bs = acc.b[m];
+      bs += __shfl_xor(bs, 16);
+      bs += __shfl_xor(bs, 32);
+      if (g == 0 && 16 * T + s < O) dst[O * In + 16 * T + s] = bs;
+    }
+  }
+}
+
 template <int LF, int ND, int NC, int FEAT>
-__global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
+__global__ __launch_bounds__(256, 2) void k_mlp16(MlpArgs a) {
   using A = Arch16<LF, ND, NC>;
   constexpr int KB0 = LF / 16;  // k-blocks of the first layer
   extern __shared__ __align__(16) unsigned char smem16[];
   _Float16* sWf = reinterpret_cast<_Float16*>(smem16);
   _Float16* sWt = sWf;  // the transposed copies follow the forward weights (offsets in 16-bit units)
   float* sB = reinterpret_cast<float*>(smem16 + (size_t)A::w_halves() * 2);
-  __bf16* sAct = reinterpret_cast<__bf16*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4);
-  __bf16* sDel = sAct + A::a_rows() * A::PS;
+  __bf16* sS = reinterpret_cast<__bf16*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4);
   float* sC = reinterpret_cast<float*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4 +
                                        (size_t)A::stash_halves() * 2);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
@@ -290,14 +299,21 @@ __global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
 
   const float Dhalf = half_box_diagonal(c);
   const bool proposals = train && a.occ_strength > 0.0f;
-  constexpr int NW = A::per_wave();
-  floatx4 gacc[NW];
-  float gbias[NW];
+  constexpr int PS = A::PS;
+  WaveGrad16<1, 4> gc_out;
+  WaveGrad16<4, 4> gc_h[NC > 1 ? NC - 1 : 1];  // Wc_01, Wc_12, Wc_23
+  WaveGrad16<4, 2> gc_in;
+  WaveGrad16<1, 4> gd_out;
+  WaveGrad16<4, 4> gd_h[ND > 1 ? ND - 1 : 1];  // Wd_01, Wd_12
+  WaveGrad16<4, KB0> gd_in;
+  gc_out.zero();
 #pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    gacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-    gbias[i] = 0.0f;
-  }
+  for (int i = 0; i < (NC > 1 ? NC - 1 : 1); ++i) gc_h[i].zero();
+  gc_in.zero();
+  gd_out.zero();
+#pragma unroll
+  for (int i = 0; i < (ND > 1 ? ND - 1 : 1); ++i) gd_h[i].zero();
+  gd_in.zero();
 
   int parity = 0;
   for (int64_t tile = blockIdx.x; tile < a.n_tiles; tile += gridDim.x, parity ^= 1) {
@@ -352,6 +368,11 @@ __global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
     for (int kb = 0; kb < KB0; ++kb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) a0h[kb][j] = (_Float16)a0v[4 * kb + j];
+    bf16x4 a0b[KB0];  // the encoding as the stash holds it (bf16), kept for the first layer's gradient
+#pragma unroll
+    for (int kb = 0; kb < KB0; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a0b[kb][j] = (__bf16)a0v[4 * kb + j];
     half4 hdh[ND][4];
     {
       floatx4 o[4];
@@ -380,6 +401,7 @@ __global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
     acinh[1] = to_half4(sh);
+    const bf16x4 acb[2] = {to_bf16x4(dout[0]), to_bf16x4(sh)};  // colour-net input for its gradient
     half4 hch[NC][4];
     {
       floatx4 o[4];
@@ -419,29 +441,12 @@ __global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
     composite_tile(a, sSig, sRgb, CL, lane, wave, train, proposals, Dhalf, dLds_j, dLdc_j);
     if (!train) continue;
 
-    // ---- activations into the stash (every wavefront has left the previous tile's gradient phase)
+    // ---- backward (fp16 chain with per-wavefront delta scaling, fp32 accumulation); every layer's deltas
+    // and inputs go through the stash for the block's bf16 weight-gradient tiles (barrier, this wave's
+    // tiles, barrier before the stash is reused)
     const int col = wave * 16 + s;
-    {
-      floatx4 av[KB0];
-#pragma unroll
-      for (int kb = 0; kb < KB0; ++kb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) av[kb][j] = a0v[4 * kb + j];
-      stash_tiles<KB0>(sAct, A::a_a0(), av, g, col);
-    }
-#pragma unroll
-    for (int i = 0; i < ND; ++i) stash_tiles<4>(sAct, A::a_hd(i), hdh[i], g, col);
-    {
-      floatx4 ac[2] = {dout[0], sh};
-      stash_tiles<2>(sAct, A::a_acin(), ac, g, col);
-    }
-#pragma unroll
-    for (int i = 0; i < NC; ++i) stash_tiles<4>(sAct, A::a_hc(i), hch[i], g, col);
-
-    // ---- backward (bf16 operands, fp32 accumulation)
-    const int src = wave * 16 + s;
-    const float dLds = __shfl(dLds_j, src);
-    const float dLdc0 = __shfl(dLdc_j[0], src), dLdc1 = __shfl(dLdc_j[1], src), dLdc2 = __shfl(dLdc_j[2], src);
+    const float dLds = __shfl(dLds_j, col);
+    const float dLdc0 = __shfl(dLdc_j[0], col), dLdc1 = __shfl(dLdc_j[1], col), dLdc2 = __shfl(dLdc_j[2], col);
     floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
     floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
     if (g == 0 && valid) {
@@ -452,57 +457,80 @@ __global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
       dco[0][2] = d3[2];
       ddo[0][0] = dd0;
     }
-    stash_tiles<1>(sDel, A::d_cout(), dco, g, col);
+    // colour output layer
     half4 dop[4];
     float dsc;
+    floatx4 dc[4];
+    stash_tiles<1>(sS, 0, dco, g, col);
+    stash_tiles<4>(sS, 16, hch[NC - 1], g, col);
     {
       half4 cop[1];
       const float csc = make_op<1>(dco, cop);
-      floatx4 dc[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd16<4, 1>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
       relu_mask16<4>(dc, hch[NC - 1]);
-      stash_tiles<4>(sDel, A::d_hc(NC - 1), dc, g, col);
       dsc = make_op<4>(dc, dop);
     }
+    __syncthreads();
+    layer_dw16<1, 4, PS>(sS, gc_out, wave, g, s);
+    __syncthreads();
+    // hidden colour layers (Wc_23, Wc_12, Wc_01): delta dc of layer i's output, input hch[i - 1]
 #pragma unroll
     for (int i = NC - 1; i >= 1; --i) {
       const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
-      floatx4 dc[4];
+      stash_tiles<4>(sS, 0, dc, g, col);
+      stash_tiles<4>(sS, 64, hch[i - 1], g, col);
 #pragma unroll
       for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd16<4, 4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
       relu_mask16<4>(dc, hch[i - 1]);
-      stash_tiles<4>(sDel, A::d_hc(i - 1), dc, g, col);
       dsc = make_op<4>(dc, dop);
+      __syncthreads();
+      layer_dw16<4, 4, PS>(sS, gc_h[i - 1], wave, g, s);
+      __syncthreads();
     }
-    // colour input layer: the dout part of its input delta joins the density head's delta
+    // colour input layer: its gradient, and the dout part of its input delta joins the density head's delta
+    stash_tiles<4>(sS, 0, dc, g, col);
+    stash_tiles<2>(sS, 64, acb, g, col);
     bwd16<1, 4>(sWt + A::wt_off(FFN_WC_IN), A::pt(FFN_WC_IN), dop, dsc, ddo, g, s);
-    stash_tiles<1>(sDel, A::d_dout(), ddo, g, col);
+    __syncthreads();
+    layer_dw16<4, 2, PS>(sS, gc_in, wave, g, s);
+    __syncthreads();
+    // density output layer
+    floatx4 dd[4];
+    stash_tiles<1>(sS, 0, ddo, g, col);
+    stash_tiles<4>(sS, 16, hdh[ND - 1], g, col);
     {
       half4 dd_op[1];
       const float ssc = make_op<1>(ddo, dd_op);
-      floatx4 dd[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd16<4, 1>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
       relu_mask16<4>(dd, hdh[ND - 1]);
-      stash_tiles<4>(sDel, A::d_hd(ND - 1), dd, g, col);
       dsc = make_op<4>(dd, dop);
     }
+    __syncthreads();
+    layer_dw16<1, 4, PS>(sS, gd_out, wave, g, s);
+    __syncthreads();
+    // hidden density layers (Wd_12, Wd_01)
 #pragma unroll
     for (int i = ND - 1; i >= 1; --i) {
       const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
-      floatx4 dd[4];
+      stash_tiles<4>(sS, 0, dd, g, col);
+      stash_tiles<4>(sS, 64, hdh[i - 1], g, col);
 #pragma unroll
       for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd16<4, 4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
       relu_mask16<4>(dd, hdh[i - 1]);
-      stash_tiles<4>(sDel, A::d_hd(i - 1), dd, g, col);
       dsc = make_op<4>(dd, dop);
+      __syncthreads();
+      layer_dw16<4, 4, PS>(sS, gd_h[i - 1], wave, g, s);
+      __syncthreads();
     }
-    // encoding gradient dL/da0 = Wd_in^T . delta_d1 -> HBM for the hash scatter
+    // density input layer: deltas and the encoding; encoding gradient dL/da0 = Wd_in^T . delta -> HBM
+    stash_tiles<4>(sS, 0, dd, g, col);
+    stash_tiles<KB0>(sS, 64, a0b, g, col);
     {
       floatx4 ga0[KB0];
 #pragma unroll
@@ -526,56 +554,22 @@ __global__ __launch_bounds__(256, 1) void k_mlp16(MlpArgs a) {
       }
     }
     __syncthreads();
-
-    // ---- weight gradients: this wavefront's share of the 16x16 tiles, K = the tile's 64 samples
-    static_for<A::n_tiles()>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      if ((i & 3) == wave) {
-        constexpr typename A::TileRef tr = A::tile(i);
-        const __bf16* drow = sDel + (A::dstash(tr.k) + 16 * tr.T + s) * A::PS + 4 * g;
-        const __bf16* arow = sAct + (A::astash(tr.k) + 16 * tr.Tp + s) * A::PS + 4 * g;
-        floatx4 acc = gacc[i >> 2];
-        float bs = gbias[i >> 2];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const bf16x4 dv = *reinterpret_cast<const bf16x4*>(drow + 16 * q);
-          const bf16x4 av = *reinterpret_cast<const bf16x4*>(arow + 16 * q);
-          acc = mfma_bf16(dv, av, acc);
-          if (tr.Tp == 0) bs += ((float)dv[0] + (float)dv[1]) + ((float)dv[2] + (float)dv[3]);
-        }
-        gacc[i >> 2] = acc;
-        gbias[i >> 2] = bs;
-      }
-    });
+    layer_dw16<4, KB0, PS>(sS, gd_in, wave, g, s);
+    // no barrier: the stash is next written after the next tile's compositing barrier
   }
 
   if (train) {
-    // every wavefront stores its tiles into the block's gradient (reusing the stash), one partial per block
-    __syncthreads();
-    float* sG = reinterpret_cast<float*>(sAct);
-    static_for<A::n_tiles()>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      if ((i & 3) == wave) {
-        constexpr typename A::TileRef tr = A::tile(i);
-        constexpr int O = layer_out(tr.k), In = layer_in(tr.k, LF);
-        float* gW = sG + A::g_off(tr.k);
-        const int colw = 16 * tr.Tp + s;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = 16 * tr.T + 4 * g + r;
-          if (row < O) gW[row * In + colw] = gacc[i >> 2][r];
-        }
-        if (tr.Tp == 0) {
-          float bs = gbias[i >> 2];
-          bs += __shfl_xor(bs, 16);
-          bs += __shfl_xor(bs, 32);
-          if (g == 0 && 16 * tr.T + s < O) gW[O * In + 16 * tr.T + s] = bs;
-        }
-      }
-    });
-    __syncthreads();
+    // every wavefront stores its tiles into the block's partial gradient
     float* dst = a.partials + (int64_t)blockIdx.x * A::g_total();
-    for (int e = tid; e < A::g_total(); e += 256) dst[e] = sG[e];
+    flush_layer16(dst + A::g_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, gc_out, wave, g, s);
+    if constexpr (NC >= 2) flush_layer16(dst + A::g_off(FFN_WC_01), FFN_M, FFN_M, gc_h[0], wave, g, s);
+    if constexpr (NC >= 3) flush_layer16(dst + A::g_off(FFN_WC_12), FFN_M, FFN_M, gc_h[1], wave, g, s);
+    if constexpr (NC >= 4) flush_layer16(dst + A::g_off(FFN_WC_23), FFN_M, FFN_M, gc_h[2], wave, g, s);
+    flush_layer16(dst + A::g_off(FFN_WC_IN), FFN_M, FFN_C_IN, gc_in, wave, g, s);
+    flush_layer16(dst + A::g_off(FFN_WD_OUT), FFN_D_OUT, FFN_M, gd_out, wave, g, s);
+    if constexpr (ND >= 2) flush_layer16(dst + A::g_off(FFN_WD_01), FFN_M, FFN_M, gd_h[0], wave, g, s);
+    if constexpr (ND >= 3) flush_layer16(dst + A::g_off(FFN_WD_12), FFN_M, FFN_M, gd_h[1], wave, g, s);
+    flush_layer16(dst + A::g_off(FFN_WD_IN), FFN_M, LF, gd_in, wave, g, s);
   }
 }
 
@@ -613,6 +607,14 @@ static hipError_t launch16_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
   X(16, 2, 2)                \
   X(32, 2, 2)                \
   X(64, 2, 2)
+
+int mlp16_blocks_per_cu(int LF, int nd, int nc) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return Arch16<l, d, n>::blocks_per_cu();
+  FFN_MLP16_CONFIGS(X)
+#undef X
+  return 1;
+}
 
 bool mlp16_supported(int LF, int nd, int nc) {
 #define X(l, d, n) \
