@@ -71,7 +71,7 @@ struct Handle {
   int64_t table_floats = 0;
   int n_cu = 0;
   Scratch Ts, DTs, flags, a0, dLda0, partials;
-  Scratch bin_cnt, bin_off, bin_sums, bin_total, bin_idx, bin_val, bin_max;
+  Scratch bin_meta, bin_idx, bin_val, bin_max;
   // marcher / render
   Scratch m_state, m_acc, m_counts, m_offsets, m_sums, m_total, m_samples, m_ids, m_a0, m_sigma, m_rgb;
   uint32_t* host_total = nullptr;  // pinned
@@ -88,17 +88,11 @@ size_t bin_budget_bytes() {
 hipError_t ensure_bins(Handle* h, int64_t n, ffn::BinPlan* plan, ffn::BinScratch* s) {
   *plan = ffn::plan_bins(h->dc, n, bin_budget_bytes());
   hipError_t e;
-  if ((e = h->bin_cnt.ensure(sizeof(uint32_t) * (size_t)plan->cnt_elems)) != hipSuccess) return e;
-  if ((e = h->bin_off.ensure(sizeof(uint32_t) * (size_t)plan->cnt_elems)) != hipSuccess) return e;
-  if ((e = h->bin_sums.ensure(sizeof(uint32_t) * (size_t)plan->tiles)) != hipSuccess) return e;
-  if ((e = h->bin_total.ensure(sizeof(uint32_t) * 4)) != hipSuccess) return e;
+  if ((e = h->bin_meta.ensure(sizeof(uint32_t) * (size_t)plan->meta_elems)) != hipSuccess) return e;
   if ((e = h->bin_idx.ensure(sizeof(uint16_t) * (size_t)plan->max_pairs)) != hipSuccess) return e;
   if ((e = h->bin_val.ensure(sizeof(float) * (size_t)plan->max_pairs * h->dc.F)) != hipSuccess) return e;
   if ((e = h->bin_max.ensure(sizeof(float) * (size_t)plan->levels_per_group * plan->nblk)) != hipSuccess) return e;
-  s->cnt = (uint32_t*)h->bin_cnt.p;
-  s->off = (uint32_t*)h->bin_off.p;
-  s->sums = (uint32_t*)h->bin_sums.p;
-  s->total = (uint32_t*)h->bin_total.p;
+  s->meta = (uint32_t*)h->bin_meta.p;
   s->pair_idx = (uint16_t*)h->bin_idx.p;
   s->pair_val = (float*)h->bin_val.p;
   s->cmax = (float*)h->bin_max.p;
@@ -237,10 +231,7 @@ int ffn_destroy(void* handle) {
   h->a0.release();
   h->dLda0.release();
   h->partials.release();
-  h->bin_cnt.release();
-  h->bin_off.release();
-  h->bin_sums.release();
-  h->bin_total.release();
+  h->bin_meta.release();
   h->bin_idx.release();
   h->bin_val.release();
   h->bin_max.release();

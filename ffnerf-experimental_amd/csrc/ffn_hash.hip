@@ -197,125 +197,50 @@ constexpr uint16_t REF_PAD = 0xFFFFu;  // stage reference of a padding pair
 static_assert(EMIT_RS * 8 <= REF_PAD, "stage references are 16-bit");
 __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
 
-// Pairs per (bucket, chunk), counted round by round exactly as the emit pass lays them out (padded runs),
-// and in cmax[level in group][chunk] a bound on every |value| of the chunk's pairs: the largest
-// max_f |g_f| * max_c |w_c| over its samples.  The round counters are double-buffered: the thread that
-// folds a bucket's counter into the histogram after the round's barrier zeroes it again one round later,
-// so a round needs one barrier.
-template <int F, int MODE>
-__global__ __launch_bounds__(EMIT_NT) void k_bin_count(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
-                                                       const float* __restrict__ g, FeatLayout lay, float lr,
-                                                       uint32_t* __restrict__ cnt, float* __restrict__ cmax) {
-  extern __shared__ uint32_t hist[];
-  const int l = grp.level0 + (int)blockIdx.y;
-  const int nbl = grp.nbl[l - grp.level0];
-  const int chunk = blockIdx.x;
-  uint32_t* rcnt = hist + nbl;                              // [2][nbl] per-round counters
-  float* wmax = reinterpret_cast<float*>(rcnt + 2 * nbl);  // [EMIT_NT / 64]
-  const int tid = threadIdx.x;
-  for (int j = tid; j < nbl; j += EMIT_NT) {
-    hist[j] = 0u;
-    rcnt[j] = 0u;
-    rcnt[nbl + j] = 0u;
-  }
-  const int64_t b0 = (int64_t)chunk * grp.chunk;
-  const int64_t b1 = b0 + grp.chunk < n ? b0 + grp.chunk : n;
-  RawSample<F> in[EMIT_SPT];
-#pragma unroll
-  for (int q = 0; q < EMIT_SPT; ++q)
-    if (b0 + tid + q * EMIT_NT < b1) load_raw<F>(src, g, lay, b0 + tid + q * EMIT_NT, l, in[q]);
-  __syncthreads();
-  float bound = 0.0f;
-  int r = 0;
-  for (int64_t rb = b0; rb < b1; rb += EMIT_RS, r ^= 1) {
-    uint32_t* cur = rcnt + r * nbl;
-    uint32_t* nxt = rcnt + (r ^ 1) * nbl;
-    for (int j = tid; j < nbl; j += EMIT_NT) nxt[j] = 0u;  // folded by this thread in the previous round
-#pragma unroll
-    for (int q = 0; q < EMIT_SPT; ++q) {
-      const int64_t b = rb + tid + q * EMIT_NT;
-      float gf[F];
-      if (b < b1 && level_grad<F, MODE>(c, in[q].g, l, lr, gf)) {
-        float pos[3], p[3];
-        raw_position<F>(src, in[q], pos);
-        normalize_pos(c, pos, p);
-        const LevelCell lc = level_cell(c.res[l], p);
-        float gm = 0.0f, wm = 0.0f;
-#pragma unroll
-        for (int f = 0; f < F; ++f) gm = fmaxf(gm, fabsf(gf[f]));
-#pragma unroll
-        for (int cc = 0; cc < 8; ++cc) {
-          wm = fmaxf(wm, fabsf(corner_weight(lc, cc)));
-          atomicAdd(&cur[corner_entry(lc, cc, l, c.mask[l]) >> grp.log2_be], 1u);
-        }
-        bound = fmaxf(bound, gm * wm);
-      }
-      if (b + EMIT_RS < b1) load_raw<F>(src, g, lay, b + EMIT_RS, l, in[q]);
-    }
-    __syncthreads();
-    for (int j = tid; j < nbl; j += EMIT_NT) hist[j] += pad_run(cur[j]);
-  }
-  bound = wave_max_nonneg(bound);
-  if ((tid & 63) == 0) wmax[tid >> 6] = bound;
-  __syncthreads();
-  if (tid == 0) {
-    float m = 0.0f;
-    for (int w = 0; w < EMIT_NT / 64; ++w) m = fmaxf(m, wmax[w]);
-    cmax[(int64_t)(l - grp.level0) * grp.nblk + chunk] = m;
-  }
-  const int rel0 = grp.bucket_rel[l - grp.level0];
-  for (int j = tid; j < nbl; j += EMIT_NT) cnt[(int64_t)(rel0 + j) * grp.nblk + chunk] = hist[j];
-}
-
 // LDS of k_bin_emit: counters (32-bit words), per-sample corner fractions and gradients, then the stage
-__host__ __device__ constexpr int emit_words(int nbl) { return (5 * nbl + 4 + 3) & ~3; }
+__host__ __device__ constexpr int emit_words(int nbl) { return (3 * nbl + 4 + EMIT_NT / 64 + 3) & ~3; }
 __host__ __device__ constexpr int emit_stage_pairs(int nbl) {
   return 8 * EMIT_RS + (PAD_RUN - 1) * (nbl < 8 * EMIT_RS ? nbl : 8 * EMIT_RS);
 }
 __host__ __device__ constexpr int round8(int x) { return (x + 7) & ~7; }
 __host__ __device__ constexpr size_t emit_lds_bytes(int nbl, int F) {
   return (size_t)emit_words(nbl) * 4 + (size_t)EMIT_RS * (16 + 4 * (size_t)F) +
-         (size_t)round8(emit_stage_pairs(nbl)) * 4 + (size_t)round8((emit_stage_pairs(nbl) + PAD_RUN - 1) / PAD_RUN) * 2;
+         (size_t)round8(emit_stage_pairs(nbl)) * 4;
 }
 
-// Emit the (entry, value) pairs of EMIT_RS samples at a time: rank them by bucket in LDS (a local counting
-// sort into runs padded to PAD_RUN with zero pairs), then copy PAD_RUN pairs per lane to the bucket's
-// slots: one 8-byte store of their entries and F aligned 8-byte-per-pair stores of their values.  The
-// stage holds, per pair, its entry and a 16-bit reference (sample of the round, corner); the copy-out
+// Emit the (entry, value) pairs of EMIT_RS samples at a time.  A round ranks its pairs by bucket in LDS
+// (a local counting sort into runs padded to PAD_RUN with zero pairs) and writes the sorted stage,
+// contiguously, into the round's own slots (np pairs per round), plus one table entry per bucket (the
+// run's offset and length in the slots).  Every write of the pass is so a sequential stream, and no
+// counting pass or global offsets are needed; the reduction reads each bucket's runs from all rounds.
+// The stage holds, per pair, its entry and a 16-bit reference (sample of the round, corner); the copy-out
 // forms the value g_f * w_corner from the sample's fractions and gradient kept in LDS (the same products
 // as at ranking time).  A round has three barriers: after the ranking, after wavefront 0 has scanned the
-// round's counts (stage offsets, global destinations, next cursors, and the other counter buffer cleared
-// for the next round), and after the stage is written.  The next round's inputs are loaded during the
-// round.  Every quad of the stage starts with a real pair (padding only fills a run's last quad), so the
-// lane holding a pair of rank 0 mod 4 records the quad's bucket for the copy-out.
+// round's counts (stage offsets, table entries, the other counter buffer cleared for the next round), and
+// after the stage is written.  The next round's inputs are loaded during the round.  The block also
+// writes cmax[level in group][chunk], a bound on every |value| of its pairs: the largest
+// max_f |g_f| * max_c |w_c| over its samples.
 template <int F, int MODE>
 __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                       const float* __restrict__ g, FeatLayout lay, float lr,
-                                                      const uint32_t* __restrict__ off,
+                                                      uint32_t* __restrict__ meta, float* __restrict__ cmax,
                                                       uint16_t* __restrict__ pair_idx,
                                                       float* __restrict__ pair_val) {
   typedef typename FVec<F>::T V;
   extern __shared__ uint32_t sm[];
-  const int l = grp.level0 + (int)blockIdx.y;
-  const int nbl = grp.nbl[l - grp.level0];
+  const int li = (int)blockIdx.y, l = grp.level0 + li;
+  const int nbl = grp.nbl[li];
   const int chunk = blockIdx.x;
-  const int rel0 = grp.bucket_rel[l - grp.level0];
-  const int np = emit_stage_pairs(nbl);
-  uint32_t* gcur = sm;              // [nbl] next global slot of each bucket
-  uint32_t* gdst = gcur + nbl;      // [nbl] global slot of the round's run minus its stage offset (mod 2^32)
-  uint32_t* lcnt = gdst + nbl;      // [2][nbl] pairs of the round per bucket
+  uint32_t* lcnt = sm;              // [2][nbl] pairs of the round per bucket
   uint32_t* loff = lcnt + 2 * nbl;  // [nbl] run offsets in the stage
   uint32_t* total_s = loff + nbl;   // [1] padded pairs of the round
+  float* wmax = reinterpret_cast<float*>(total_s + 4);                 // [EMIT_NT / 64]
   float4* s_frac = reinterpret_cast<float4*>(sm + emit_words(nbl));    // [EMIT_RS] corner fractions
   V* s_grad = reinterpret_cast<V*>(s_frac + EMIT_RS);                  // [EMIT_RS] gradient
   uint16_t* st_idx = reinterpret_cast<uint16_t*>(s_grad + EMIT_RS);    // [np] entry in bucket
-  uint16_t* st_ref = st_idx + round8(np);                              // [np] sample * 8 + corner
-  uint16_t* st_bkt = st_ref + round8(np);                              // [np / 4] bucket of each quad
+  uint16_t* st_ref = st_idx + round8(grp.np);                          // [np] sample * 8 + corner
   const int tid = threadIdx.x, lane = tid & 63;
-  for (int j = tid; j < nbl; j += EMIT_NT) {
-    gcur[j] = off[(int64_t)(rel0 + j) * grp.nblk + chunk];
-    lcnt[j] = 0u;
-  }
+  for (int j = tid; j < nbl; j += EMIT_NT) lcnt[j] = 0u;
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
   const int64_t b_begin = (int64_t)chunk * grp.chunk;
   const int64_t b_end = b_begin + grp.chunk < n ? b_begin + grp.chunk : n;
@@ -324,8 +249,10 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
   for (int q = 0; q < EMIT_SPT; ++q)
     if (b_begin + tid + q * EMIT_NT < b_end) load_raw<F>(src, g, lay, b_begin + tid + q * EMIT_NT, l, in[q]);
   __syncthreads();
+  float bound = 0.0f;
   int r = 0;
   for (int64_t rb = b_begin; rb < b_end; rb += EMIT_RS, r ^= 1) {
+    const int64_t round = rb / EMIT_RS;  // the round's index in the level
     uint32_t* cur = lcnt + r * nbl;
     uint32_t* nxt = lcnt + (r ^ 1) * nbl;
     bool act[EMIT_SPT];
@@ -343,16 +270,22 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
         fr[q][0] = lc.f[0];
         fr[q][1] = lc.f[1];
         fr[q][2] = lc.f[2];
+        float gm = 0.0f, wm = 0.0f;
+#pragma unroll
+        for (int f = 0; f < F; ++f) gm = fmaxf(gm, fabsf(gf[q][f]));
 #pragma unroll
         for (int cc = 0; cc < 8; ++cc) {
+          wm = fmaxf(wm, fabsf(corner_weight(lc, cc)));
           ent[q][cc] = corner_entry(lc, cc, l, c.mask[l]);
           rank[q][cc] = atomicAdd(&cur[ent[q][cc] >> grp.log2_be], 1u);
         }
+        bound = fmaxf(bound, gm * wm);
       }
       if (b + EMIT_RS < b_end) load_raw<F>(src, g, lay, b + EMIT_RS, l, in[q]);
     }
     __syncthreads();
     if (tid < 64) {
+      uint32_t* mrow = meta + ((int64_t)li * grp.n_rounds + round) * grp.meta_stride;
       uint32_t carry = 0;
       for (int j0 = 0; j0 < nbl; j0 += 64) {
         const int j = j0 + lane;
@@ -365,10 +298,8 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
         }
         if (j < nbl) {
           const uint32_t o = carry + incl - cn;
-          const uint32_t gc = gcur[j];
           loff[j] = o;
-          gdst[j] = gc - o;
-          gcur[j] = gc + cn;
+          mrow[j] = (o << 16) | cn;
           nxt[j] = 0u;
         }
         carry += __shfl(incl, 63);
@@ -384,11 +315,9 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
       s_grad[ls] = FVec<F>::pack(gf[q]);
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
-        const uint32_t bk = ent[q][cc] >> grp.log2_be;
-        const uint32_t slot = loff[bk] + rank[q][cc];
+        const uint32_t slot = loff[ent[q][cc] >> grp.log2_be] + rank[q][cc];
         st_idx[slot] = (uint16_t)(ent[q][cc] & be_mask);
         st_ref[slot] = (uint16_t)(ls * 8 + cc);
-        if ((rank[q][cc] & (PAD_RUN - 1)) == 0) st_bkt[slot / PAD_RUN] = (uint16_t)bk;
       }
     }
     // zero pairs pad every run to a multiple of PAD_RUN
@@ -401,9 +330,9 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
     }
     __syncthreads();
     const uint32_t nq = total_s[0] / PAD_RUN;
+    const int64_t slot0 = ((int64_t)li * grp.n_rounds + round) * grp.np;
     for (uint32_t qd = (uint32_t)tid; qd < nq; qd += EMIT_NT) {
       const uint32_t i = qd * PAD_RUN;
-      const uint32_t dst = gdst[st_bkt[qd]] + i;  // a multiple of PAD_RUN
       const uint2 refs = *reinterpret_cast<const uint2*>(st_ref + i);
       const uint32_t rf[PAD_RUN] = {refs.x & 0xFFFFu, refs.x >> 16, refs.y & 0xFFFFu, refs.y >> 16};
       float v[PAD_RUN * F];
@@ -425,50 +354,75 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
           for (int f = 0; f < F; ++f) v[k * F + f] = gq[f] * w;
         }
       }
-      *reinterpret_cast<uint2*>(pair_idx + dst) = *reinterpret_cast<const uint2*>(st_idx + i);
-      float4* gv = reinterpret_cast<float4*>(pair_val + (size_t)dst * F);
+      *reinterpret_cast<uint2*>(pair_idx + slot0 + i) = *reinterpret_cast<const uint2*>(st_idx + i);
+      float4* gv = reinterpret_cast<float4*>(pair_val + (slot0 + i) * F);
 #pragma unroll
       for (int k = 0; k < F; ++k) gv[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
     }
   }
+  bound = wave_max_nonneg(bound);
+  if (lane == 0) wmax[tid >> 6] = bound;
+  __syncthreads();
+  if (tid == 0) {
+    float m = 0.0f;
+    for (int w = 0; w < EMIT_NT / 64; ++w) m = fmaxf(m, wmax[w]);
+    cmax[(int64_t)li * grp.nblk + chunk] = m;
+  }
 }
 
 // One block per bucket: sum its pairs in 64-bit fixed point in LDS, then apply the mode's update to the
-// bucket's slice of the table.  Zero pairs (the run padding) are skipped.
+// bucket's slice of the table.  The bucket's pairs are one run in each round's slots (the run table gives
+// offset and length); a first pass over the table counts them (for the fixed-point scale), the second
+// walks 16 rounds per wavefront at a time with every lane on one quad of pairs.  Zero pairs (the run
+// padding) are skipped.
 template <int F, int MODE>
-__global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ off,
+__global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ meta,
                                                      const uint16_t* __restrict__ pair_idx,
                                                      const float* __restrict__ pair_val,
                                                      const float* __restrict__ cmax, BinApply ap) {
   extern __shared__ unsigned long long acc[];
   __shared__ float wmax[16];
+  __shared__ uint32_t wtot[16];
+  constexpr int SEG = 16;  // rounds per wavefront step
   const int j = blockIdx.x;  // bucket, relative to the group
   int li = 0;
   while (li + 1 < grp.n_levels && j >= grp.bucket_rel[li + 1]) ++li;
   const int l = grp.level0 + li;
+  const int jb = j - grp.bucket_rel[li];
   const int be = 1 << grp.log2_be;
-  const uint32_t entry_lo = (uint32_t)(j - grp.bucket_rel[li]) << grp.log2_be;
+  const uint32_t entry_lo = (uint32_t)jb << grp.log2_be;
   const uint32_t level_T = c.mask[l] + 1u;
   const int count = (int)((level_T - entry_lo) < (uint32_t)be ? (level_T - entry_lo) : (uint32_t)be);
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < count * F; e += 1024) acc[e] = 0ull;
-  // bound on every |value| of the level: the largest of its chunks' bounds
+  const int nr = grp.n_rounds;
+  const uint32_t* mcol = meta + (int64_t)li * nr * grp.meta_stride + jb;  // entry of round rr: mcol[rr * stride]
+  // bound on every |value| of the level (the largest of its chunks' bounds) and the bucket's pair count
   float mxl = 0.0f;
   for (int ch = tid; ch < grp.nblk; ch += 1024) mxl = fmaxf(mxl, cmax[(int64_t)li * grp.nblk + ch]);
+  uint32_t cnt = 0;
+  for (int rr = tid; rr < nr; rr += 1024) cnt += mcol[(int64_t)rr * grp.meta_stride] & 0xFFFFu;
   mxl = wave_max_nonneg(mxl);
-  if ((tid & 63) == 0) wmax[tid >> 6] = mxl;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d);
+  if (lane == 0) {
+    wmax[wave] = mxl;
+    wtot[wave] = cnt;
+  }
   __syncthreads();
   float mx = 0.0f;
+  uint32_t pairs = 0;
 #pragma unroll
-  for (int w = 0; w < 16; ++w) mx = fmaxf(mx, wmax[w]);
-  const uint32_t start = off[(int64_t)j * grp.nblk];
-  const uint32_t end = off[(int64_t)(j + 1) * grp.nblk];  // both multiples of PAD_RUN
+  for (int w = 0; w < 16; ++w) {
+    mx = fmaxf(mx, wmax[w]);
+    pairs += wtot[w];
+  }
   // fixed-point scale 2^k with (pairs + 1) * bound * 2^k < 2^62: no partial sum can overflow
   int k = 0;
   if (mx > 0.0f) {
     int e_mx, e_n;
-    frexpf(mx, &e_mx);                       // mx < 2^e_mx
-    frexp((double)(end - start) + 1.0, &e_n);  // pairs + 1 <= 2^e_n
+    frexpf(mx, &e_mx);                   // mx < 2^e_mx
+    frexp((double)pairs + 1.0, &e_n);    // pairs + 1 <= 2^e_n
     k = 62 - e_mx - e_n;
   }
   const double scale = ldexp(1.0, k);
@@ -476,23 +430,52 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
     if (v != 0.0f) atomicAdd(&acc[e * F + f], (unsigned long long)__double2ll_rn((double)v * scale));
   };
   if (mx > 0.0f) {
-    // PAD_RUN pairs per thread and step: one 8-byte load of entries, F 16-byte loads of values
-    for (uint32_t i = start + (uint32_t)tid * PAD_RUN; i < end; i += 1024u * PAD_RUN) {
-      const uint2 e4 = *reinterpret_cast<const uint2*>(pair_idx + i);
-      float v[PAD_RUN * F];
+    const int64_t slot_lvl = (int64_t)li * nr * grp.np;
+    for (int r0 = wave * SEG; r0 < nr; r0 += 16 * SEG) {
+      // lanes 0..SEG-1 hold rounds r0 + lane: run offset and quad count, then the quads' running ends
+      uint32_t m = 0;
+      if (lane < SEG && r0 + lane < nr) m = mcol[(int64_t)(r0 + lane) * grp.meta_stride];
+      uint32_t incl = lane < SEG ? (m & 0xFFFFu) / PAD_RUN : 0u;
 #pragma unroll
-      for (int q = 0; q < F; ++q) {
-        const float4 t = *reinterpret_cast<const float4*>(pair_val + (size_t)i * F + 4 * q);
-        v[4 * q] = t.x;
-        v[4 * q + 1] = t.y;
-        v[4 * q + 2] = t.z;
-        v[4 * q + 3] = t.w;
+      for (int d = 1; d < SEG; d <<= 1) {
+        const uint32_t o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
       }
-      const uint32_t ev[PAD_RUN] = {e4.x & 0xFFFFu, e4.x >> 16, e4.y & 0xFFFFu, e4.y >> 16};
+      uint32_t ends[SEG], offs[SEG];
 #pragma unroll
-      for (int p = 0; p < PAD_RUN; ++p)
+      for (int t = 0; t < SEG; ++t) {
+        ends[t] = __builtin_amdgcn_readlane(incl, t);
+        offs[t] = __builtin_amdgcn_readlane(m >> 16, t);
+      }
+      for (uint32_t q = (uint32_t)lane; q < ends[SEG - 1]; q += 64) {
+        // the run holding quad q: the last round whose running start is <= q
+        uint32_t qb = 0, off = offs[0];
+        int sg = 0;
 #pragma unroll
-        for (int f = 0; f < F; ++f) add(ev[p], v[p * F + f], f);
+        for (int t = 1; t < SEG; ++t) {
+          if (q >= ends[t - 1]) {
+            qb = ends[t - 1];
+            off = offs[t];
+            sg = t;
+          }
+        }
+        const int64_t i = slot_lvl + (int64_t)(r0 + sg) * grp.np + off + (int64_t)PAD_RUN * (q - qb);
+        const uint2 e4 = *reinterpret_cast<const uint2*>(pair_idx + i);
+        float v[PAD_RUN * F];
+#pragma unroll
+        for (int qq = 0; qq < F; ++qq) {
+          const float4 t4 = *reinterpret_cast<const float4*>(pair_val + i * F + 4 * qq);
+          v[4 * qq] = t4.x;
+          v[4 * qq + 1] = t4.y;
+          v[4 * qq + 2] = t4.z;
+          v[4 * qq + 3] = t4.w;
+        }
+        const uint32_t ev[PAD_RUN] = {e4.x & 0xFFFFu, e4.x >> 16, e4.y & 0xFFFFu, e4.y >> 16};
+#pragma unroll
+        for (int p = 0; p < PAD_RUN; ++p)
+#pragma unroll
+          for (int f = 0; f < F; ++f) add(ev[p], v[p * F + f], f);
+      }
     }
   }
   __syncthreads();
@@ -623,20 +606,18 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   p.log2_be = c.F == 4 ? 11 : (c.F == 2 ? 12 : 13);
   p.chunk = 4 * EMIT_RS;
   p.nblk = (int)((n + p.chunk - 1) / p.chunk);
+  p.n_rounds = (int)((n + EMIT_RS - 1) / EMIT_RS);
   int max_nbl = 0;
   for (int l = 0; l < c.L; ++l) {
     const int nbl = (int)(((int64_t)c.mask[l] + 1 + (1 << p.log2_be) - 1) >> p.log2_be);
     if (nbl > max_nbl) max_nbl = nbl;
   }
-  // pairs of one level: 8 per sample plus at most PAD_RUN - 1 padding pairs per bucket and emit round
-  const int64_t rounds = (p.chunk + EMIT_RS - 1) / EMIT_RS;
-  const int64_t pad_buckets = max_nbl < 8 * EMIT_RS ? max_nbl : 8 * EMIT_RS;
-  const int64_t per_level_pairs = n * 8 + (int64_t)p.nblk * rounds * pad_buckets * (PAD_RUN - 1);
+  // every round of a level has its own np pair slots (its pairs and at most PAD_RUN - 1 padding pairs per
+  // bucket that receives any)
+  p.np = round8(emit_stage_pairs(max_nbl));
+  const int64_t per_level_pairs = (int64_t)p.n_rounds * p.np;
   const int64_t pair_bytes = 2 + 4 * (int64_t)c.F;
   int lg = (int)(pair_budget_bytes / (size_t)(per_level_pairs * pair_bytes));
-  // slot offsets are 32-bit: keep a group's pair count below 2^32
-  const int lg32 = (int)((((int64_t)1 << 32) - 1) / per_level_pairs);
-  if (lg > lg32) lg = lg32;
   if (lg < 1) lg = 1;
   if (lg > c.L) lg = c.L;
   p.levels_per_group = lg;
@@ -650,8 +631,7 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   p.max_buckets = max_buckets;
   p.max_nbl = max_nbl;
   p.max_pairs = per_level_pairs * lg;
-  p.cnt_elems = (int64_t)max_buckets * p.nblk + 1;
-  p.tiles = (p.cnt_elems + 4095) / 4096;
+  p.meta_elems = (int64_t)lg * p.n_rounds * max_nbl;
   return p;
 }
 
@@ -659,7 +639,10 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                            int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
                            hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  const int nt = EMIT_NT;
+  // run offsets and lengths are 16-bit, and a round's stage must fit in LDS
+  const size_t lds_emit = emit_lds_bytes(plan.max_nbl, c.F);
+  if (plan.np > 65535 || lds_emit > 160 * 1024) return hipErrorInvalidConfiguration;  // table too large
+  const size_t lds_acc = sizeof(unsigned long long) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
   for (int g0 = 0; g0 < c.L; g0 += plan.levels_per_group) {
     BinGroup grp{};
     grp.level0 = g0;
@@ -667,32 +650,24 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     grp.log2_be = plan.log2_be;
     grp.chunk = plan.chunk;
     grp.nblk = plan.nblk;
+    grp.n_rounds = plan.n_rounds;
+    grp.np = plan.np;
+    grp.meta_stride = plan.max_nbl;
     int rel = 0;
-    int max_nbl = 0;
     for (int li = 0; li < grp.n_levels; ++li) {
       const int l = g0 + li;
       grp.nbl[li] = (int)(((int64_t)c.mask[l] + 1 + (1 << plan.log2_be) - 1) >> plan.log2_be);
       grp.bucket_rel[li] = rel;
       rel += grp.nbl[li];
-      if (grp.nbl[li] > max_nbl) max_nbl = grp.nbl[li];
     }
     grp.bucket_rel[grp.n_levels] = rel;
     const int n_buckets = rel;
-    const int64_t n_cnt = (int64_t)n_buckets * plan.nblk;
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
-    const size_t lds_count = sizeof(uint32_t) * (3 * (size_t)max_nbl + nt / 64);
-    const size_t lds_acc = sizeof(unsigned long long) * ((size_t)1 << plan.log2_be) * (size_t)c.F;
-    const size_t lds_emit = emit_lds_bytes(max_nbl, c.F);
-    if (lds_emit > 160 * 1024 || lds_count > 160 * 1024) return hipErrorInvalidConfiguration;  // table too large
 #define FFN_BIN(FV, MV)                                                                                            \
   do {                                                                                                             \
-    hipLaunchKernelGGL((k_bin_count<FV, MV>), grid_bl, dim3(nt), lds_count, st, c, src, n, grp, g, lay, lr, s.cnt, \
-                       s.cmax);                                                                                    \
-    hipError_t e_ = launch_scan_u32(s.cnt, n_cnt, s.off, s.sums, s.total, st);                                     \
-    if (e_ != hipSuccess) return e_;                                                                               \
-    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(nt), lds_emit, st, c, src, n, grp, g, lay, lr, s.off,  \
-                       s.pair_idx, s.pair_val);                                                                    \
-    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp, s.off, \
+    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(EMIT_NT), lds_emit, st, c, src, n, grp, g, lay, lr,     \
+                       s.meta, s.cmax, s.pair_idx, s.pair_val);                                                    \
+    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp, s.meta, \
                        s.pair_idx, s.pair_val, s.cmax, ap);                                                        \
   } while (0)
 #define FFN_BIN_F(MV)                     \
@@ -702,7 +677,6 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     case 4: FFN_BIN(4, MV); break;        \
     default: return hipErrorInvalidValue; \
   }
-    // the scan writes n_cnt + 1 offsets: the last one is the group's pair total
     if (mode == BIN_GRAD) {
       FFN_BIN_F(BIN_GRAD)
     } else if (mode == BIN_SGD) {

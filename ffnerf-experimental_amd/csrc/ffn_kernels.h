@@ -102,22 +102,22 @@ enum { BIN_GRAD = 0, BIN_SGD = 1, BIN_ADAM = 2 };
 
 struct BinGroup {
   int level0, n_levels, log2_be, chunk, nblk;
+  int n_rounds;     // emit rounds per level (the samples in runs of the emit round size)
+  int np;           // pair slots of one round (the stage size; a multiple of 4)
+  int meta_stride;  // entries per round in the run table (the group's largest bucket count)
   int nbl[FFN_MAX_LEVELS];             // buckets of each level of the group
   int bucket_rel[FFN_MAX_LEVELS + 1];  // first bucket of each level, relative to the group
 };
 
 struct BinPlan {
-  int log2_be, chunk, nblk, levels_per_group, max_buckets, max_nbl;
-  int64_t max_pairs, cnt_elems, tiles;
+  int log2_be, chunk, nblk, levels_per_group, max_buckets, max_nbl, n_rounds, np;
+  int64_t max_pairs, meta_elems;
 };
 
 struct BinScratch {
-  uint32_t* cnt;       // [cnt_elems]
-  uint32_t* off;       // [cnt_elems]
-  uint32_t* sums;      // [tiles]
-  uint32_t* total;     // [1]
+  uint32_t* meta;      // [levels_per_group][n_rounds][max_nbl] each bucket's run in a round's slots: offset << 16 | length
   float* cmax;         // [levels_per_group][chunks] bound on every |value| of the chunk's pairs
-  uint16_t* pair_idx;  // [max_pairs]
+  uint16_t* pair_idx;  // [max_pairs] entry within the bucket
   float* pair_val;     // [max_pairs * F]
 };
 
