@@ -59,7 +59,7 @@ def algorithmic(spec):
 
 
 STAGE_KERNELS = {"mlp": ("void ffn::k_mlp<",), "hash_fwd": ("void ffn::k_hash_fwd<",),
-                 "hash_bwd": ("void ffn::k_bin_count<", "void ffn::k_bin_emit<", "void ffn::k_bin_reduce<")}
+                 "hash_bwd": ("void ffn::k_bin_emit<", "void ffn::k_bin_reduce<")}
 
 
 def recorded_traffic(stage, mlp):
