@@ -83,6 +83,37 @@ def test_hash_backward_matches_oracle(gh, ora, which):
     assert (touched_g == touched_o).mean() > 0.9999
 
 
+@pytest.mark.parametrize("case", ["f1", "one_partial_round", "wide_table"])
+def test_hash_backward_shapes(gh, ora, case):
+    """The scatter's edge shapes: one feature per level (8192-entry buckets), fewer samples than one emit
+    round, and 2^22-entry levels (1024 buckets per level: the widest run table and emit stage)."""
+    print(f"[case] hash bwd shape {case}", flush=True)
+    if case == "f1":
+        spec, n = spec_cfg0(f_per_level=1), 20000
+    elif case == "one_partial_round":
+        spec, n = spec_cfg0(), 1000
+    else:
+        spec, n = spec_cfg0(n_levels=2, log2_T=[22, 22], res=[256.0, 2048.0]), 50000
+    p = random_params(spec, seed=33)
+    m = gh.GpuModel(spec, p)
+    rng = np.random.default_rng(34)
+    lo, hi = np.array(spec["box_min"]), np.array(spec["box_max"])
+    x = (lo + (hi - lo) * rng.uniform(0, 1, (n, 3))).astype(np.float32)
+    LF = spec["n_levels"] * spec["f_per_level"]
+    g = rng.normal(size=(n, LF)).astype(np.float32)
+    grad_g = m.encode_bwd(x, g, table_floats(spec))
+    grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
+    scale = np.abs(grad_o).max()
+    assert np.isfinite(grad_g).all()
+    assert np.abs(grad_g - grad_o).max() <= 1e-5 * scale
+    assert ((grad_g != 0) == (grad_o != 0)).mean() > 0.9999
+    if case == "f1":  # and the forward of the same shape, bit-exact
+        a0_g, idx_g = m.encode(x[:5000], with_idx=True)
+        a0_o, idx_o, _ = ora.hash_encode(ora.make_cfg(spec), p["table"], x[:5000], with_idx=True)
+        assert np.array_equal(idx_g, idx_o)
+        assert np.array_equal(a0_g.view(np.uint32), a0_o.view(np.uint32))
+
+
 def test_occ_decay_bit_exact(gh, ora):
     import ctypes
     import torch
