@@ -45,7 +45,9 @@ template <int LF_, int ND_, int NC_>
 struct Arch {
   static constexpr int LF = LF_, ND = ND_, NC = NC_;
   static constexpr int rows_pad(int k) { return k == FFN_WC_OUT ? 16 : layer_out(k); }
-  static constexpr int pitch(int k) { return layer_in(k, LF) + 1; }
+  // row pitch in+4 (4 mod 32 for in = 16, 32, 64): the forward's 16-byte reads of four k-steps and the
+  // backward's transposed 4-byte reads both fall on distinct banks
+  static constexpr int pitch(int k) { return layer_in(k, LF) + 4; }
   static constexpr int wsz(int k) { return layer_active(k, ND, NC) ? rows_pad(k) * pitch(k) + rows_pad(k) : 0; }
   static constexpr int w_off(int k) {
     int o = 0;
@@ -66,8 +68,10 @@ struct Arch {
   static constexpr int g_total() { return g_off(FFN_N_LAYERS); }
   static constexpr int PSF = 64 + 4;       // stash pitch: 64 sample columns + 4 pad (conflict-free b128 reads)
   static constexpr int stash_rows = 128;   // one layer's delta rows (<= 64) + input activation rows (<= 64)
-  static constexpr int comp_floats = 2 * 256;  // double-buffered sigma[64] + rgb[64][3]
-  static constexpr int lds_floats() { return w_total() + stash_rows * PSF + comp_floats; }
+  // sigma[64] + rgb[64][3] of the tile: one slot when training (the stash barriers separate a tile's
+  // compositing from the next tile's writes), two alternating slots for a forward-only launch
+  static constexpr int comp_floats(bool train) { return train ? 256 : 512; }
+  static constexpr int lds_floats(bool train = true) { return w_total() + stash_rows * PSF + comp_floats(train); }
   // two blocks per CU when the LDS allows it (160 KiB per CU)
   static constexpr int blocks_per_cu() { return lds_floats() * 4 <= 80 * 1024 ? 2 : 1; }
 };
@@ -85,11 +89,15 @@ __device__ __forceinline__ void fwd_tiles(const float* __restrict__ W, const flo
     for (int r = 0; r < 4; ++r) acc[t][r] = B[16 * t + 4 * g + r];
   const float* wrow = W + s * P + 4 * g;
 #pragma unroll
-  for (int tp = 0; tp < IT; ++tp)
+  for (int tp = 0; tp < IT; ++tp) {
+    floatx4 w4[OT];
+#pragma unroll
+    for (int t = 0; t < OT; ++t) w4[t] = *reinterpret_cast<const floatx4*>(wrow + 16 * t * P + 16 * tp);
 #pragma unroll
     for (int rp = 0; rp < 4; ++rp)
 #pragma unroll
-      for (int t = 0; t < OT; ++t) acc[t] = mfma4(wrow[16 * t * P + 16 * tp + rp], in[tp][rp], acc[t]);
+      for (int t = 0; t < OT; ++t) acc[t] = mfma4(w4[t][rp], in[tp][rp], acc[t]);
+  }
 #pragma unroll
   for (int t = 0; t < OT; ++t) {
     if (relu) {
@@ -274,7 +282,11 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
       for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
       const float* wrow = W + (16 * t + s) * P + KA * g;
 #pragma unroll
-      for (int kk = 0; kk < KA; ++kk) acc = mfma4(wrow[kk], a0r[kk], acc);
+      for (int kq = 0; kq < KA; kq += 4) {
+        const floatx4 w4 = *reinterpret_cast<const floatx4*>(wrow + kq);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc = mfma4(w4[kk], a0r[kq + kk], acc);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
       hd[0][t] = acc;
@@ -313,7 +325,7 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
 }
 
 template <int LF, int ND, int NC, int FEAT>
-__global__ __launch_bounds__(256, 2) void k_mlp(MlpArgs a) {
+__global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_mlp(MlpArgs a) {
   using A = Arch<LF, ND, NC>;
   constexpr int KA = LF / 4;  // a0 values per lane (k-steps of the first layer)
   constexpr int PSF = A::PSF;
@@ -351,7 +363,7 @@ __global__ __launch_bounds__(256, 2) void k_mlp(MlpArgs a) {
 
   int parity = 0;
   for (int64_t tile = blockIdx.x; tile < a.n_tiles; tile += gridDim.x, parity ^= 1) {
-    float* sSig = sC + parity * 256;
+    float* sSig = sC + (train ? 0 : parity * 256);
     float* sRgb = sSig + 64;
     // ------------------------------------------------------------------
     // forward: this lane's sample in the MLP layout
@@ -518,11 +530,12 @@ __global__ __launch_bounds__(256, 2) void k_mlp(MlpArgs a) {
 template <int LF, int ND, int NC, int FEAT>
 static hipError_t launch_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch<LF, ND, NC>;
-  const size_t lds = sizeof(float) * (size_t)A::lds_floats();
+  const size_t lds = sizeof(float) * (size_t)A::lds_floats(a.do_train != 0);
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)(sizeof(float) * (size_t)A::lds_floats(false)));
     if (e != hipSuccess) return e;
     attr_set = true;
   }

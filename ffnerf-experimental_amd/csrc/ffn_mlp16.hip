@@ -262,7 +262,7 @@ __device__ __forceinline__ void flush_layer16(float* __restrict__ dst, int O, in
 }
 
 template <int LF, int ND, int NC, int FEAT>
-__global__ __launch_bounds__(256, 2) void k_mlp16(MlpArgs a) {
+__global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_mlp16(MlpArgs a) {
   using A = Arch16<LF, ND, NC>;
   constexpr int KB0 = LF / 16;  // k-blocks of the first layer
   extern __shared__ __align__(16) unsigned char smem16[];
