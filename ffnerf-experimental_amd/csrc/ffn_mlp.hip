@@ -383,7 +383,8 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     const float t_b = valid ? a.Ts[b] : 0.0f;
     // per-sample inputs of the compositing (lane j = sample j of the tile), loaded before the forward so
     // that their latency hides behind it
-    const CompLane CL = load_comp_lane(a, tile, lane, wave, n_samples, log2S, proposals);
+    const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront makes the tile's proposals
+    const CompLane CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
 
     floatx4 hd[ND][4];
     floatx4 acin[2];  // [dout(16) | SH*mult(16)] as two D-layout tiles
@@ -404,7 +405,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     // ------------------------------------------------------------------
     // compositing on 64 lanes: lane j = sample j of the tile (every wave)
     float dLds_j, dLdc_j[3];
-    composite_tile(a, sSig, sRgb, CL, lane, wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+    composite_tile(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
     if (!train) continue;
 
     // ------------------------------------------------------------------

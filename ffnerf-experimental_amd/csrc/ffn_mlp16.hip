@@ -360,7 +360,8 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     }
     const float dt_b = valid ? a.DTs[b] : 0.0f;
     const float t_b = valid ? a.Ts[b] : 0.0f;
-    const CompLane CL = load_comp_lane(a, tile, lane, wave, n_samples, log2S, proposals);
+    const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront makes the tile's proposals
+    const CompLane CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
 
     // ---- forward (fp16 operands, fp32 accumulation)
     half4 a0h[KB0];
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     __syncthreads();
 
     float dLds_j, dLdc_j[3];
-    composite_tile(a, sSig, sRgb, CL, lane, wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+    composite_tile(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
     if (!train) continue;
 
     // ---- backward (fp16 chain with per-wavefront delta scaling, fp32 accumulation); every layer's deltas

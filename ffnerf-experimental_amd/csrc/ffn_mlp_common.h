@@ -38,7 +38,8 @@ __device__ __forceinline__ void occ_grid_pos(const DevCfg& c, const float (&o)[3
   }
 }
 
-__device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t tile, int lane, int wave,
+// prop_wave: this wavefront makes the tile's occupancy proposals (one wavefront per tile, all 64 lanes)
+__device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t tile, int lane, bool prop_wave,
                                                    uint64_t n_samples, int log2S, bool proposals) {
   CompLane L;
   L.bj = tile * 64 + lane;
@@ -54,7 +55,7 @@ __device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t til
     L.t_j = a.Ts[L.bj];
     L.segmask = (uint64_t)a.flags[2 * L.rj] | ((uint64_t)a.flags[2 * L.rj + 1] << 32);
     const int lid = lane & (a.S - 1);
-    if (((L.segmask >> lid) & 1ull) && L.dt_j > 0.0f && (lane >> 4) == wave) {
+    if (((L.segmask >> lid) & 1ull) && L.dt_j > 0.0f && prop_wave) {
       const float4 ro = a.rays[2 * L.rj], rdv = a.rays[2 * L.rj + 1];
       const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
       float gpos[3];
@@ -69,12 +70,13 @@ __device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t til
 }
 
 // Compositing of the tile's rays on the wavefront's 64 lanes (S lanes per ray), the loss gradient, the
-// output colour (wavefront 0), taps (wavefront 0) and the proposals of this wavefront's 16 samples; returns
-// dL/dsigma and dL/dc of lane j's sample.  sSig/sRgb hold sigma[64] and rgb[64][3] of the tile.
+// output colour (wavefront 0), taps (wavefront 0) and, on the tile's proposal wavefront, the occupancy
+// proposals of all its samples; returns dL/dsigma and dL/dc of lane j's sample.  sSig/sRgb hold
+// sigma[64] and rgb[64][3] of the tile.
 __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __restrict__ sSig,
                                                const float* __restrict__ sRgb, const CompLane& L, int lane,
-                                               int wave, bool train, bool proposals, float Dhalf, float& dLds_j,
-                                               float (&dLdc_j)[3]) {
+                                               int wave, bool prop_wave, bool train, bool proposals, float Dhalf,
+                                               float& dLds_j, float (&dLdc_j)[3]) {
   const DevCfg& c = a.c;
   const int S = a.S;
   const int64_t bj = L.bj, rj = L.rj;
@@ -162,8 +164,8 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
     }
     {
       // occupancy proposals for run-representative samples (ffnerf_OG.cl:1640-1821); every wavefront
-      // holds the whole ray here and handles the proposals of its own 16 samples
-      if (proposals) {
+      // holds the whole ray here, and one per tile (rotating) makes the proposals of all 64 samples
+      if (proposals && prop_wave) {
         const int nxt = find_next_flag(segmask, lid, S);
         const int prev_end = lid > 0 ? lid - 1 : 0;
         const int last = nxt < S ? nxt - 1 : S - 1;
@@ -172,7 +174,7 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
         const float t_last = __shfl(t_j, base + last), T_last = __shfl(Tr, base + last);
         const float t_nx = __shfl(t_j, base + nsrc), T_nx = __shfl(Tr, base + nsrc);
         const bool is_rep = (segmask >> lid) & 1ull;
-        if (vj && is_rep && dt_j > 0.0f && (j >> 4) == wave) {
+        if (vj && is_rep && dt_j > 0.0f) {
           const float4 ro = a.rays[2 * rj], rdv = a.rays[2 * rj + 1];
           const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
           const int G = c.G;
