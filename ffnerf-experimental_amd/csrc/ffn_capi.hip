@@ -79,7 +79,7 @@ struct Handle {
 
 size_t bin_budget_bytes() {
   const char* e = getenv("FFN_BIN_BUDGET_MB");
-  size_t mb = e ? (size_t)atoll(e) : (size_t)6144;
+  size_t mb = e ? (size_t)atoll(e) : (size_t)24576;
   if (mb < 64) mb = 64;
   return mb << 20;
 }
