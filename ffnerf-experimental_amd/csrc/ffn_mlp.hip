@@ -344,6 +344,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   __syncthreads();
 
   const float Dhalf = half_box_diagonal(c);
+  const bool taps = taps_requested(a);
   const bool proposals = train && a.occ_strength > 0.0f;
 
   WaveGrad<1, 4> gc_out;
@@ -385,6 +386,10 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     // that their latency hides behind it
     const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront makes the tile's proposals
     const CompLane CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
+    if (!taps && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
+      empty_tile<LF, FEAT>(a, CL, lane, wave, b, valid, train, g);
+      continue;
+    }
 
     floatx4 hd[ND][4];
     floatx4 acin[2];  // [dout(16) | SH*mult(16)] as two D-layout tiles
@@ -488,23 +493,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
 #pragma unroll
       for (int t = 0; t < LF / 16; ++t) ga[t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd_tiles<LF / 16, 4>(sW + A::w_off(FFN_WD_IN), A::pitch(FFN_WD_IN), dd[0], ga, g, s);
-      if (valid) {
-#pragma unroll
-        for (int t = 0; t < LF / 16; ++t) {
-#pragma unroll
-          for (int r = 0; r < 4; r += 2) {  // neurons 16t+4g+r, r+1: one level when F >= 2
-            const int nn = 16 * t + 4 * g + r;
-            const int l = nn / FEAT, f = nn - l * FEAT;
-            float* dst = a.dL_da0 + l * a.feat.stride_l + b * a.feat.stride_b + f;
-            if constexpr (FEAT >= 2) {
-              *reinterpret_cast<float2*>(dst) = make_float2(ga[t][r], ga[t][r + 1]);
-            } else {
-              dst[0] = ga[t][r];
-              a.dL_da0[(l + 1) * a.feat.stride_l + b * a.feat.stride_b] = ga[t][r + 1];
-            }
-          }
-        }
-      }
+      if (valid) store_enc_grad<LF, FEAT>(a, b, g, ga);
     }
     __syncthreads();
     layer_dw<4, LF / 16, PSF>(sS, gd_in, wave, g, s);

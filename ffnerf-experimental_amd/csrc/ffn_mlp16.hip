@@ -298,6 +298,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   __syncthreads();
 
   const float Dhalf = half_box_diagonal(c);
+  const bool taps = taps_requested(a);
   const bool proposals = train && a.occ_strength > 0.0f;
   constexpr int PS = A::PS;
   WaveGrad16<1, 4> gc_out;
@@ -362,6 +363,10 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     const float t_b = valid ? a.Ts[b] : 0.0f;
     const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront makes the tile's proposals
     const CompLane CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
+    if (!taps && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
+      empty_tile<LF, FEAT>(a, CL, lane, wave, b, valid, train, g);
+      continue;
+    }
 
     // ---- forward (fp16 operands, fp32 accumulation)
     half4 a0h[KB0];
@@ -537,22 +542,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
 #pragma unroll
       for (int t = 0; t < KB0; ++t) ga0[t] = floatx4{0.f, 0.f, 0.f, 0.f};
       bwd16<KB0, 4>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
-      if (valid) {
-#pragma unroll
-        for (int t = 0; t < KB0; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; r += 2) {
-            const int nn = 16 * t + 4 * g + r;
-            const int l = nn / FEAT, f = nn - l * FEAT;
-            float* dst = a.dL_da0 + l * a.feat.stride_l + b * a.feat.stride_b + f;
-            if constexpr (FEAT >= 2) {
-              *reinterpret_cast<float2*>(dst) = make_float2(ga0[t][r], ga0[t][r + 1]);
-            } else {
-              dst[0] = ga0[t][r];
-              a.dL_da0[(l + 1) * a.feat.stride_l + b * a.feat.stride_b] = ga0[t][r + 1];
-            }
-          }
-      }
+      if (valid) store_enc_grad<LF, FEAT>(a, b, g, ga0);
     }
     __syncthreads();
     layer_dw16<4, KB0, PS>(sS, gd_in, wave, g, s);

@@ -16,6 +16,22 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// the background colour of ray rj (black, white, or the seeded random colour while training;
+// ffnerf_OG.cl:1534-1541)
+__device__ __forceinline__ void background(const MlpArgs& a, int64_t rj, bool train, float (&bg)[3]) {
+  bg[0] = bg[1] = bg[2] = 0.0f;
+  if (train) {
+    if (a.c.background == FFN_BG_WHITE) {
+      bg[0] = bg[1] = bg[2] = 1.0f;
+    } else if (a.c.background == FFN_BG_RANDOM) {
+      uint32_t rb = hash_u32(a.seed ^ (uint32_t)rj * 747796405u ^ 0xA511E9B3u);
+      bg[0] = rand01(rb);
+      bg[1] = rand01(rb);
+      bg[2] = rand01(rb);
+    }
+  }
+}
+
 // per-sample inputs of the compositing; lane j holds sample j of the 64-sample tile
 struct CompLane {
   int64_t bj, rj;
@@ -101,17 +117,8 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
     Seg tot;
     const Seg pre = seg_scan_excl_seg(my, lid, S, base, &tot);
     const float Tr = pre.a, T_final = tot.a;
-    float bg[3] = {0.0f, 0.0f, 0.0f};
-    if (train) {
-      if (c.background == FFN_BG_WHITE) {
-        bg[0] = bg[1] = bg[2] = 1.0f;
-      } else if (c.background == FFN_BG_RANDOM) {
-        uint32_t rb = hash_u32(a.seed ^ (uint32_t)rj * 747796405u ^ 0xA511E9B3u);
-        bg[0] = rand01(rb);
-        bg[1] = rand01(rb);
-        bg[2] = rand01(rb);
-      }
-    }
+    float bg[3];
+    background(a, rj, train, bg);
     const float Cf0 = tot.v0 + T_final * bg[0];
     const float Cf1 = tot.v1 + T_final * bg[1];
     const float Cf2 = tot.v2 + T_final * bg[2];
@@ -270,6 +277,52 @@ __device__ __forceinline__ void output_deltas(float t_b, float dt_b, float Dhalf
   dco[1] = (f_vol * dLdc1) * ((rgb_s[1] * (1.0f - rgb_s[1])) * 0.5f);
   dco[2] = (f_vol * dLdc2) * ((rgb_s[2] * (1.0f - rgb_s[2])) * 0.5f);
   dd0 = 1.0f * (f_vol * dLds) * softplus_prime_from_pre(fminf(fmaxf(dout0, -18.0f), 18.0f));
+}
+
+// dL/da0 of this lane's sample b: tile t holds encoding neurons 16t + 4g + r (level n / F, feature n % F)
+template <int LF, int FEAT>
+__device__ __forceinline__ void store_enc_grad(const MlpArgs& a, int64_t b, int g, const floatx4 (&ga)[LF / 16]) {
+#pragma unroll
+  for (int t = 0; t < LF / 16; ++t) {
+#pragma unroll
+    for (int r = 0; r < 4; r += 2) {  // neurons 16t+4g+r, r+1: one level when F >= 2
+      const int nn = 16 * t + 4 * g + r;
+      const int l = nn / FEAT, f = nn - l * FEAT;
+      float* dst = a.dL_da0 + l * a.feat.stride_l + b * a.feat.stride_b + f;
+      if constexpr (FEAT >= 2) {
+        *reinterpret_cast<float2*>(dst) = make_float2(ga[t][r], ga[t][r + 1]);
+      } else {
+        dst[0] = ga[t][r];
+        a.dL_da0[(l + 1) * a.feat.stride_l + b * a.feat.stride_b] = ga[t][r + 1];
+      }
+    }
+  }
+}
+
+// A tile whose samples are all inactive (dt <= 0, e.g. a ray that misses the box) composites to exactly
+// the background (every alpha is 0, so T = 1 and the colour sum is 0) and every gradient of its samples is
+// zero; this writes what the full path would write for it -- the rays' colours and zero encoding
+// gradients -- so the MLP can be skipped.  Taps, which expose per-sample MLP outputs, take the full path.
+template <int LF, int FEAT>
+__device__ __forceinline__ void empty_tile(const MlpArgs& a, const CompLane& L, int lane, int wave, int64_t b,
+                                           bool valid, bool train, int g) {
+  const int lid = lane & (a.S - 1);
+  if (wave == 0 && lid == 0 && L.vj) {
+    float bg[3];
+    background(a, L.rj, train, bg);
+    a.out_rgb[L.rj] = make_float4(fminf(fmaxf(bg[0], 0.0f), 1.0f), fminf(fmaxf(bg[1], 0.0f), 1.0f),
+                                  fminf(fmaxf(bg[2], 0.0f), 1.0f), train ? 4.0f : 0.0f);
+  }
+  if (train && valid) {
+    floatx4 z[LF / 16];
+#pragma unroll
+    for (int t = 0; t < LF / 16; ++t) z[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    store_enc_grad<LF, FEAT>(a, b, g, z);
+  }
+}
+
+__device__ __forceinline__ bool taps_requested(const MlpArgs& a) {
+  return a.t_sigma || a.t_rgb || a.t_Tr || a.t_dLds || a.t_dLdc;
 }
 
 __device__ __forceinline__ float half_box_diagonal(const DevCfg& c) {

@@ -232,6 +232,27 @@ def test_train_step_cfg0_adam(gh, ora, S):
     _compare_step(spec, p, rays, tg, S, default_scalars(), gh, ora)
 
 
+@pytest.mark.parametrize("S", [64, 16])
+def test_train_step_empty_tiles_match_full_path(gh, ora, S):
+    """Tiles whose samples are all inactive (rays that miss the box) skip the MLP when no taps are
+    requested; the step must leave exactly the state and colours of the full path (which the other step
+    tests check against the oracle)."""
+    print(f"[case] train step empty tiles S={S}", flush=True)
+    spec = spec_cfg0(hash_opt=1, background=2)
+    p = random_params(spec, seed=81)
+    rays = look_at_rays(96 * 64 // S, spec, seed=82, miss_frac=0.4)
+    tg = sphere_targets(rays, spec)
+    full = gh.GpuModel(spec, p)
+    fast = gh.GpuModel(spec, p)
+    out_full, _ = full.train_step(rays, tg, S, default_scalars(), taps=True)
+    out_fast, _ = fast.train_step(rays, tg, S, default_scalars(), taps=False)
+    assert np.array_equal(out_full.view(np.uint32), out_fast.view(np.uint32))
+    sf, ss = full.state(), fast.state()
+    assert set(sf) == set(ss)
+    for k in sf:
+        assert np.array_equal(sf[k].view(np.uint32), ss[k].view(np.uint32)), k
+
+
 def test_train_step_empty_grid_proposals(gh, ora):
     print("[case] train step proposals", flush=True)
     spec = spec_cfg0(hash_opt=1)
