@@ -324,8 +324,9 @@ def main():
                     help="first run one plain device copy of this size (a known-traffic kernel for PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested); the multi-GPU design is "
-              f"described in DESIGN.md and is not run here.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build runs the step on a "
+              f"single GPU; sharding rays over GPUs with all-reduced table and MLP gradients is not built.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
