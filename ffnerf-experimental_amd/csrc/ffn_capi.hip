@@ -71,7 +71,7 @@ struct Handle {
   int64_t table_floats = 0;
   int n_cu = 0;
   Scratch Ts, DTs, flags, a0, dLda0, partials;
-  Scratch bin_meta, bin_idx, bin_val, bin_max;
+  Scratch bin_meta, bin_meta_t, bin_idx, bin_val, bin_max;
   // marcher / render
   Scratch m_state, m_acc, m_counts, m_offsets, m_sums, m_total, m_samples, m_ids, m_a0, m_sigma, m_rgb;
   uint32_t* host_total = nullptr;  // pinned
@@ -89,10 +89,12 @@ hipError_t ensure_bins(Handle* h, int64_t n, ffn::BinPlan* plan, ffn::BinScratch
   *plan = ffn::plan_bins(h->dc, n, bin_budget_bytes());
   hipError_t e;
   if ((e = h->bin_meta.ensure(sizeof(uint32_t) * (size_t)plan->meta_elems)) != hipSuccess) return e;
+  if ((e = h->bin_meta_t.ensure(sizeof(uint32_t) * (size_t)plan->meta_elems)) != hipSuccess) return e;
   if ((e = h->bin_idx.ensure(sizeof(uint16_t) * (size_t)plan->max_pairs)) != hipSuccess) return e;
   if ((e = h->bin_val.ensure(sizeof(float) * (size_t)plan->max_pairs * h->dc.F)) != hipSuccess) return e;
   if ((e = h->bin_max.ensure(sizeof(float) * (size_t)plan->levels_per_group * plan->nblk)) != hipSuccess) return e;
   s->meta = (uint32_t*)h->bin_meta.p;
+  s->meta_t = (uint32_t*)h->bin_meta_t.p;
   s->pair_idx = (uint16_t*)h->bin_idx.p;
   s->pair_val = (float*)h->bin_val.p;
   s->cmax = (float*)h->bin_max.p;
@@ -232,6 +234,7 @@ int ffn_destroy(void* handle) {
   h->dLda0.release();
   h->partials.release();
   h->bin_meta.release();
+  h->bin_meta_t.release();
   h->bin_idx.release();
   h->bin_val.release();
   h->bin_max.release();

@@ -370,9 +370,32 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
   }
 }
 
+// The run table as emit writes it, [level][round][bucket], turned bucket-major, [level][bucket][round],
+// so that each reduce block reads its bucket's runs as one contiguous row (a strided column read costs a
+// memory sector per round once the table outgrows the caches).  64x64 tiles through LDS.
+__global__ __launch_bounds__(256) void k_bin_meta_transpose(const uint32_t* __restrict__ meta,
+                                                            uint32_t* __restrict__ meta_t, int n_rounds,
+                                                            int stride) {
+  __shared__ uint32_t tile[64][65];
+  const int r0 = blockIdx.x * 64, b0 = blockIdx.y * 64, li = blockIdx.z;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const uint32_t* src = meta + (int64_t)li * n_rounds * stride;
+  uint32_t* dst = meta_t + (int64_t)li * stride * n_rounds;
+  for (int i = ty; i < 64; i += 4) {
+    const int r = r0 + i, bk = b0 + tx;
+    tile[i][tx] = (r < n_rounds && bk < stride) ? src[(int64_t)r * stride + bk] : 0u;
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int bk = b0 + i, r = r0 + tx;
+    if (bk < stride && r < n_rounds) dst[(int64_t)bk * n_rounds + r] = tile[tx][i];
+  }
+}
+
 // One block per bucket: sum its pairs in 64-bit fixed point in LDS, then apply the mode's update to the
-// bucket's slice of the table.  The bucket's pairs are one run in each round's slots (the run table gives
-// offset and length); a first pass over the table counts them (for the fixed-point scale), the second
+// bucket's slice of the table.  The bucket's pairs are one run in each round's slots (its row of the
+// bucket-major run table gives offset and length); a first pass over the row counts them (for the
+// fixed-point scale), the second
 // walks 16 rounds per wavefront at a time with every lane on one quad of pairs.  Zero pairs (the run
 // padding) are skipped.
 template <int F, int MODE>
@@ -396,12 +419,12 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < count * F; e += 1024) acc[e] = 0ull;
   const int nr = grp.n_rounds;
-  const uint32_t* mcol = meta + (int64_t)li * nr * grp.meta_stride + jb;  // entry of round rr: mcol[rr * stride]
+  const uint32_t* mrow = meta + ((int64_t)li * grp.meta_stride + jb) * nr;  // bucket-major: round rr at mrow[rr]
   // bound on every |value| of the level (the largest of its chunks' bounds) and the bucket's pair count
   float mxl = 0.0f;
   for (int ch = tid; ch < grp.nblk; ch += 1024) mxl = fmaxf(mxl, cmax[(int64_t)li * grp.nblk + ch]);
   uint32_t cnt = 0;
-  for (int rr = tid; rr < nr; rr += 1024) cnt += mcol[(int64_t)rr * grp.meta_stride] & 0xFFFFu;
+  for (int rr = tid; rr < nr; rr += 1024) cnt += mrow[rr] & 0xFFFFu;
   mxl = wave_max_nonneg(mxl);
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d);
@@ -434,7 +457,7 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
     for (int r0 = wave * SEG; r0 < nr; r0 += 16 * SEG) {
       // lanes 0..SEG-1 hold rounds r0 + lane: run offset and quad count, then the quads' running ends
       uint32_t m = 0;
-      if (lane < SEG && r0 + lane < nr) m = mcol[(int64_t)(r0 + lane) * grp.meta_stride];
+      if (lane < SEG && r0 + lane < nr) m = mrow[r0 + lane];
       uint32_t incl = lane < SEG ? (m & 0xFFFFu) / PAD_RUN : 0u;
 #pragma unroll
       for (int d = 1; d < SEG; d <<= 1) {
@@ -663,12 +686,16 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     grp.bucket_rel[grp.n_levels] = rel;
     const int n_buckets = rel;
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
+    const dim3 grid_tr((unsigned)((plan.n_rounds + 63) / 64), (unsigned)((plan.max_nbl + 63) / 64),
+                       (unsigned)grp.n_levels);
 #define FFN_BIN(FV, MV)                                                                                            \
   do {                                                                                                             \
     hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(EMIT_NT), lds_emit, st, c, src, n, grp, g, lay, lr,     \
                        s.meta, s.cmax, s.pair_idx, s.pair_val);                                                    \
-    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp, s.meta, \
-                       s.pair_idx, s.pair_val, s.cmax, ap);                                                        \
+    hipLaunchKernelGGL(k_bin_meta_transpose, grid_tr, dim3(256), 0, st, s.meta, s.meta_t, grp.n_rounds,            \
+                       grp.meta_stride);                                                                           \
+    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,         \
+                       s.meta_t, s.pair_idx, s.pair_val, s.cmax, ap);                                              \
   } while (0)
 #define FFN_BIN_F(MV)                     \
   switch (c.F) {                          \

@@ -116,6 +116,7 @@ struct BinPlan {
 
 struct BinScratch {
   uint32_t* meta;      // [levels_per_group][n_rounds][max_nbl] each bucket's run in a round's slots: offset << 16 | length
+  uint32_t* meta_t;    // the same, bucket-major: [levels_per_group][max_nbl][n_rounds]
   float* cmax;         // [levels_per_group][chunks] bound on every |value| of the chunk's pairs
   uint16_t* pair_idx;  // [max_pairs] entry within the bucket
   float* pair_val;     // [max_pairs * F]
