@@ -46,132 +46,205 @@ __global__ __launch_bounds__(256) void k_occ_bitfield(const uint32_t* __restrict
 
 __device__ __forceinline__ float lattice_t(float t0, uint32_t k, float dt) { return t0 + ((float)k + 0.5f) * dt; }
 
-// The walk of one ray from its state; returns the samples of this call.  EMIT writes them from slot
-// `base` on and stores the new state; the count pass only reads the state.
+// Rays per wavefront of k_march.  A lane walks one ray at a time and, when that ray is finished (or paused at
+// the chunk budget), takes the next unclaimed ray of its wavefront's range: walks are 37 % as long as
+// their wavefront's longest on average, so a lane per ray would leave most lanes idle.
+constexpr uint32_t MARCH_RPW = 256;
+constexpr int MARCH_CELLS_PER_CLAIM = 8;
+
+// One lane's walk of one ray, advanced a cell at a time.  The sequence of operations per ray is the
+// specification's (ora_march_ray): the same cells, exit times and lattice indices, so the emitted samples
+// are bit-identical whatever order the lane meets its rays in.
 template <bool EMIT>
-__device__ uint32_t march_ray(const MarchArgs& a, uint32_t r, uint64_t base) {
-  MarchState st = a.state ? a.state[r] : MarchState{0u, 0u, 0u, MARCH_FRESH};
-  if (st.flags & MARCH_DONE) return 0;
-  const float4 ro = a.rays[2 * (size_t)r], rd = a.rays[2 * (size_t)r + 1];
-  const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rd.x, rd.y, rd.z};
-  const int R = a.res;
-  uint32_t emitted = 0;
-  bool done = false;
-  float ta, tb;
-  if (!ray_aabb(o, d, a.bmin, a.bmax, ta, tb)) {
-    done = true;
-  } else {
-    const float t0 = fmaxf(ta, a.t_near), t1 = fminf(tb, a.t_far);
+struct RayWalk {
+  MarchState st;
+  float o[3], d[3], invd[3], t0, t1;
+  int cc[3], step[3];
+  uint32_t r, k, emitted;
+  uint64_t base;
+  int iter;
+  bool done, paused;
+
+  // claim ray rr; returns false when the ray has nothing to walk (it is then already finished)
+  __device__ __forceinline__ bool start(const MarchArgs& a, uint32_t rr, const float (&cell)[3]) {
+    r = rr;
+    emitted = 0;
+    iter = 0;
+    done = false;
+    paused = false;
+    st = a.state ? a.state[r] : MarchState{0u, 0u, 0u, MARCH_FRESH};
+    if (st.flags & MARCH_DONE) return false;  // no state change, no samples
+    const float4 ro = a.rays[2 * (size_t)r], rd = a.rays[2 * (size_t)r + 1];
+    o[0] = ro.x; o[1] = ro.y; o[2] = ro.z;
+    d[0] = rd.x; d[1] = rd.y; d[2] = rd.z;
+    base = EMIT ? (uint64_t)a.offsets[r] : 0;
+    float ta, tb;
+    if (!ray_aabb(o, d, a.bmin, a.bmax, ta, tb)) {
+      done = true;
+      finish_state(a, false);
+      return false;
+    }
+    t0 = fmaxf(ta, a.t_near);
+    t1 = fminf(tb, a.t_far);
     if (!(t1 > t0)) {
       done = true;
-    } else {
-      float cell[3], invd[3];
-      int cc[3], step[3];
+      finish_state(a, false);
+      return false;
+    }
+    const int R = a.res;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      invd[i] = (d[i] != 0.0f) ? (1.0f / d[i]) : __builtin_huge_valf();
+      step[i] = d[i] > 0.0f ? 1 : (d[i] < 0.0f ? -1 : 0);
+    }
+    if (st.flags & MARCH_FRESH) {
 #pragma unroll
       for (int i = 0; i < 3; ++i) {
-        const float size = a.bmax[i] - a.bmin[i];
-        cell[i] = size / (float)R;
-        invd[i] = (d[i] != 0.0f) ? (1.0f / d[i]) : __builtin_huge_valf();
-        step[i] = d[i] > 0.0f ? 1 : (d[i] < 0.0f ? -1 : 0);
+        const float inv = (float)R / (a.bmax[i] - a.bmin[i]);
+        const float p = o[i] + t0 * d[i];
+        const int ci = (int)floorf((p - a.bmin[i]) * inv);
+        cc[i] = ci < 0 ? 0 : (ci > R - 1 ? R - 1 : ci);
       }
-      if (st.flags & MARCH_FRESH) {
+      st.k = 0;
+      st.n = 0;
+    } else {
+      cc[0] = (int)(st.cell & 1023u);
+      cc[1] = (int)((st.cell >> 10) & 1023u);
+      cc[2] = (int)((st.cell >> 20) & 1023u);
+    }
+    k = st.k;
+    return true;
+  }
+
+  // one cell of the walk; returns true when the ray is finished or paused for this call
+  __device__ __forceinline__ bool advance(const MarchArgs& a, const float (&cell)[3]) {
+    const int R = a.res;
+    float t_exit = t1;
+    int axis = -1;
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          const float inv = (float)R / (a.bmax[i] - a.bmin[i]);
-          const float p = o[i] + t0 * d[i];
-          const int ci = (int)floorf((p - a.bmin[i]) * inv);
-          cc[i] = ci < 0 ? 0 : (ci > R - 1 ? R - 1 : ci);
-        }
-        st.k = 0;
-        st.n = 0;
-      } else {
-        cc[0] = (int)(st.cell & 1023u);
-        cc[1] = (int)((st.cell >> 10) & 1023u);
-        cc[2] = (int)((st.cell >> 20) & 1023u);
+    for (int i = 0; i < 3; ++i) {
+      if (step[i] == 0) continue;
+      const float bound = a.bmin[i] + (float)(cc[i] + (step[i] > 0 ? 1 : 0)) * cell[i];
+      const float te = (bound - o[i]) * invd[i];
+      if (te < t_exit) {
+        t_exit = te;
+        axis = i;
       }
-      uint32_t k = st.k;
-      const uint32_t budget = a.chunk;
-      bool paused = false;
-      for (int iter = 0; iter < 3 * R + 3; ++iter) {
-        float t_exit = t1;
-        int axis = -1;
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          if (step[i] == 0) continue;
-          const float bound = a.bmin[i] + (float)(cc[i] + (step[i] > 0 ? 1 : 0)) * cell[i];
-          const float te = (bound - o[i]) * invd[i];
-          if (te < t_exit) {
-            t_exit = te;
-            axis = i;
-          }
-        }
-        const int64_t bi = cc[0] + (int64_t)R * (cc[1] + (int64_t)R * cc[2]);
-        const bool occ = (a.bits[bi >> 5] >> (bi & 31)) & 1u;
-        if (occ) {
-          for (;;) {
-            const float tk = lattice_t(t0, k, a.dt);
-            if (!(tk < t_exit)) break;
-            if (st.n + emitted >= a.max_steps) {
-              done = true;
-              break;
-            }
-            if (emitted >= budget) {
-              paused = true;
-              break;
-            }
-            if (EMIT) {
-              const uint64_t slot = base + emitted;
-              if (slot < a.capacity) {
-                a.samples[slot] = make_float4(o[0] + tk * d[0], o[1] + tk * d[1], o[2] + tk * d[2], tk);
-                a.ray_ids[slot] = r;
-              }
-            }
-            ++emitted;
-            ++k;
-          }
-          if (done || paused) break;
-        } else if (lattice_t(t0, k, a.dt) < t_exit) {
-          // skip the empty cell: the first k with t_k >= t_exit, exactly as the one-by-one walk finds it
-          float est = ceilf((t_exit - t0) / a.dt - 0.5f);
-          uint32_t ke = k + 1;
-          if (est > (float)ke) ke = est < 4.0e9f ? (uint32_t)est : 4000000000u;
-          while (ke > k + 1 && !(lattice_t(t0, ke - 1, a.dt) < t_exit)) --ke;
-          while (lattice_t(t0, ke, a.dt) < t_exit) ++ke;
-          k = ke;
-        }
-        if (axis < 0) {
+    }
+    const int64_t bi = cc[0] + (int64_t)R * (cc[1] + (int64_t)R * cc[2]);
+    const bool occ = (a.bits[bi >> 5] >> (bi & 31)) & 1u;
+    if (occ) {
+      for (;;) {
+        const float tk = lattice_t(t0, k, a.dt);
+        if (!(tk < t_exit)) break;
+        if (st.n + emitted >= a.max_steps) {
           done = true;
           break;
         }
-        cc[axis] += step[axis];
-        if (cc[axis] < 0 || cc[axis] >= R) {
-          done = true;
+        if (emitted >= a.chunk) {
+          paused = true;
           break;
         }
-        if (iter == 3 * R + 2) done = true;
+        if (EMIT) {
+          const uint64_t slot = base + emitted;
+          if (slot < a.capacity) {
+            a.samples[slot] = make_float4(o[0] + tk * d[0], o[1] + tk * d[1], o[2] + tk * d[2], tk);
+            a.ray_ids[slot] = r;
+          }
+        }
+        ++emitted;
+        ++k;
       }
-      if (EMIT) {
+      if (done || paused) return true;
+    } else if (lattice_t(t0, k, a.dt) < t_exit) {
+      // skip the empty cell: the first k with t_k >= t_exit, exactly as the one-by-one walk finds it
+      float est = ceilf((t_exit - t0) / a.dt - 0.5f);
+      uint32_t ke = k + 1;
+      if (est > (float)ke) ke = est < 4.0e9f ? (uint32_t)est : 4000000000u;
+      while (ke > k + 1 && !(lattice_t(t0, ke - 1, a.dt) < t_exit)) --ke;
+      while (lattice_t(t0, ke, a.dt) < t_exit) ++ke;
+      k = ke;
+    }
+    if (axis < 0) {
+      done = true;
+      return true;
+    }
+    // step into the next cell (static indices: the walk state stays in registers)
+    int ncc = 0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (i == axis) {
+        cc[i] += step[i];
+        ncc = cc[i];
+      }
+    }
+    if (ncc < 0 || ncc >= R) {
+      done = true;
+      return true;
+    }
+    if (iter == 3 * R + 2) {
+      done = true;
+      return true;
+    }
+    ++iter;
+    return false;
+  }
+
+  // the state kept for the next call (walked rays only)
+  __device__ __forceinline__ void finish_state(const MarchArgs& a, bool walked) {
+    if (EMIT && a.state) {
+      if (walked) {
         st.k = k;
         st.cell = (uint32_t)cc[0] | ((uint32_t)cc[1] << 10) | ((uint32_t)cc[2] << 20);
       }
+      st.n += emitted;
+      st.flags = (st.flags & ~MARCH_FRESH) | (done ? MARCH_DONE : 0u);
+      a.state[r] = st;
     }
   }
-  if (EMIT && a.state) {
-    st.n += emitted;
-    st.flags = (st.flags & ~MARCH_FRESH) | (done ? MARCH_DONE : 0u);
-    a.state[r] = st;
-  }
-  return emitted;
-}
+};
 
 template <bool EMIT>
 __global__ __launch_bounds__(256) void k_march(MarchArgs a) {
-  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= a.num_rays) return;
-  if (EMIT) {
-    march_ray<true>(a, r, a.offsets[r]);
-  } else {
-    a.counts[r] = march_ray<false>(a, r, 0);
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint64_t r_begin = wave * MARCH_RPW;
+  if (r_begin >= a.num_rays) return;  // the same on every lane of the wavefront
+  const uint32_t r_end = (uint32_t)(r_begin + MARCH_RPW < a.num_rays ? r_begin + MARCH_RPW : a.num_rays);
+  float cell[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) cell[i] = (a.bmax[i] - a.bmin[i]) / (float)a.res;
+  uint32_t next = (uint32_t)r_begin;  // the wavefront's next unclaimed ray
+  RayWalk<EMIT> w;
+  bool have = false;  // this lane walks a ray
+  for (;;) {
+    // lanes without a ray claim the next rays of the range, in lane order
+    const uint64_t need = __ballot(!have);
+    if (!have) {
+      const uint32_t rr = next + (uint32_t)__popcll(need & ((1ull << lane) - 1ull));
+      if (rr < r_end) {
+        if (w.start(a, rr, cell)) {
+          have = true;
+        } else if (!EMIT) {
+          a.counts[rr] = 0u;
+        }
+      }
+    }
+    next = next + (uint32_t)__popcll(need);
+    if (next > r_end) next = r_end;
+    if (__ballot(have) == 0ull) {
+      if (next >= r_end) break;
+      continue;
+    }
+    // a few cells per lane between claims: the claim's wavefront-wide bookkeeping is paid once per batch
+#pragma unroll 1
+    for (int j = 0; j < MARCH_CELLS_PER_CLAIM; ++j) {
+      if (have && w.advance(a, cell)) {
+        w.finish_state(a, true);
+        if (!EMIT) a.counts[w.r] = w.emitted;
+        have = false;
+      }
+    }
   }
 }
 
@@ -239,7 +312,8 @@ hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint3
 
 hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st) {
   if (a.num_rays == 0) return hipSuccess;
-  const dim3 grid((a.num_rays + 255) / 256), block(256);
+  const uint64_t waves = (a.num_rays + MARCH_RPW - 1) / MARCH_RPW;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
   if (emit)
     hipLaunchKernelGGL(k_march<true>, grid, block, 0, st, a);
   else
