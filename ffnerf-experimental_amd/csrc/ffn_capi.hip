@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <cmath>
 #include <string>
 #include <vector>
 
@@ -147,6 +148,10 @@ ffn::DevCfg make_devcfg(const ffn_config* c) {
   for (int i = 0; i < 3; ++i) {
     d.bmin[i] = c->box_min[i];
     d.bmax[i] = c->box_max[i];
+    // the extent as the device computes it; its reciprocal is exact when it is a power of two
+    const float bs = d.bmax[i] - d.bmin[i];
+    int e = 0;
+    d.inv_extent[i] = (std::isfinite(bs) && bs > 0.0f && std::frexp(bs, &e) == 0.5f) ? std::ldexp(1.0f, 1 - e) : 0.0f;
   }
   d.rho_min = c->rho_min;
   d.rho_max = c->rho_max;
@@ -298,9 +303,17 @@ int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint
   if (n < 0) return fail(-1, "negative size");
   if (n > 0 && (!x || !a0)) return fail(-1, "NULL buffer");
   if (!h->params.table) return fail(-1, "bind params (table) first");
+  if (n == 0) return 0;
+  // the gather writes level-major (one contiguous array per level pass) into the handle's scratch, and one
+  // tiled transpose makes the caller's sample-major rows: the passes would otherwise write F floats out
+  // of every L * F
+  const hipStream_t st = (hipStream_t)stream;
+  FFN_HIP(h->a0.ensure(sizeof(float) * (size_t)n * h->dc.LF));
+  const ffn::FeatLayout lm = ffn::level_major(n, h->dc.F);
   ffn::PosSrc src{x, nullptr, nullptr, 0};
-  FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, a0, ffn::sample_major(h->dc.L, h->dc.F), idx_out,
-                               (hipStream_t)stream));
+  FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, (float*)h->a0.p, lm, idx_out, st));
+  FFN_HIP(ffn::launch_feat_relayout((const float*)h->a0.p, lm, a0, ffn::sample_major(h->dc.L, h->dc.F), n, h->dc.L,
+                                    h->dc.F, st));
   return 0;
 }
 
@@ -313,11 +326,17 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
   ffn::BinPlan plan;
   ffn::BinScratch bs;
   FFN_HIP(ensure_bins(h, n, &plan, &bs));
+  // the scatter reads one level per pass: the caller's sample-major rows are transposed to level-major
+  // first (the passes would otherwise fetch every row once per level for F floats of it)
+  const hipStream_t st = (hipStream_t)stream;
+  FFN_HIP(h->dLda0.ensure(sizeof(float) * (size_t)n * h->dc.LF));
+  const ffn::FeatLayout lm = ffn::level_major(n, h->dc.F);
+  FFN_HIP(ffn::launch_feat_relayout(g, ffn::sample_major(h->dc.L, h->dc.F), (float*)h->dLda0.p, lm, n, h->dc.L,
+                                    h->dc.F, st));
   ffn::PosSrc src{x, nullptr, nullptr, 0};
   ffn::BinApply ap{};
   ap.dst = grad;
-  FFN_HIP(ffn::launch_hash_bwd(h->dc, src, n, g, ffn::sample_major(h->dc.L, h->dc.F), ffn::BIN_GRAD, 0.0f, ap, plan,
-                               bs, (hipStream_t)stream));
+  FFN_HIP(ffn::launch_hash_bwd(h->dc, src, n, (const float*)h->dLda0.p, lm, ffn::BIN_GRAD, 0.0f, ap, plan, bs, st));
   return 0;
 }
 

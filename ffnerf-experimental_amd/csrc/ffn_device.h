@@ -30,6 +30,7 @@ struct DevCfg {
   float lvl_lr_scale[FFN_MAX_LEVELS];
   int nd, nc, G;
   float bmin[3], bmax[3];
+  float inv_extent[3];  // 1 / (bmax - bmin) when that extent is a power of two (exact), else 0
   float rho_min, rho_max, dt_min, dt_max, t_near, t_far;
   int background, hash_opt;
 };
@@ -150,11 +151,20 @@ __device__ __forceinline__ bool ray_aabb(const float o[3], const float d[3], con
 // ---------------------------------------------------------------------------
 // hash grid corner math (ffnerf_OG.cl:1286-1364); bit-identical to the oracle
 
+// (x - bmin) / (bmax - bmin), clamped.  For a power-of-two extent the product with its reciprocal is the
+// same correctly rounded value as the quotient (both round d * 2^-k), at a fraction of the cost of a
+// division; the branch is uniform.
 __device__ __forceinline__ void normalize_pos(const DevCfg& c, const float x[3], float p[3]) {
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    float bs = c.bmax[i] - c.bmin[i];
-    float v = (x[i] - c.bmin[i]) / bs;
+    const float d = x[i] - c.bmin[i];
+    float v;
+    if (c.inv_extent[i] != 0.0f) {
+      v = d * c.inv_extent[i];
+    } else {
+      const float bs = c.bmax[i] - c.bmin[i];
+      v = d / bs;
+    }
     p[i] = fminf(fmaxf(v, 0.0f), 1.0f - 1.0e-6f);
   }
 }

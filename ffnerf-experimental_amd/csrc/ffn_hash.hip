@@ -12,22 +12,24 @@
 //   Backward: scattered float atomics run at ~21 G lanes/s on this chip
 //   (measured), far below what the HBM can stream, so the scatter is done
 //   without global atomics, as a bucketed reduction:
-//     1. count  -- per (level, sample chunk), how many corner contributions
-//                  land in each bucket (BE consecutive table entries of one
-//                  level); LDS histogram, one row of counts per block;
-//     2. scan   -- exclusive prefix over the (bucket, block) counts, so every
-//                  block owns a contiguous slot range inside every bucket;
-//     3. emit   -- recompute the corners and write (entry-in-bucket, value)
-//                  pairs to the slots (LDS counting sort, aligned writes);
-//     4. reduce -- one block per bucket sums its pairs into an LDS copy of
-//                  the bucket and applies the update to its own slice of the
-//                  table: gradient add, the reference SGD, or Adam.  No
-//                  gradient table is materialised for Adam.
+//     1. emit      -- per (level, sample chunk), rounds of 1024 samples (512
+//                     at F = 4): each
+//                     round ranks its (entry-in-bucket, value) pairs by bucket
+//                     (BE consecutive table entries of one level) with an LDS
+//                     counting sort and writes them contiguously into its own
+//                     slots, plus a run table (offset, length per bucket);
+//                     consecutive samples in the same cell of the level are
+//                     merged first, one pair per corner for the whole run;
+//     2. transpose -- the run table turned bucket-major;
+//     3. reduce    -- one block per bucket sums its runs from every round into
+//                     an LDS copy of the bucket and applies the update to its
+//                     own slice of the table: gradient add, the reference SGD,
+//                     or Adam.  No gradient table is materialised for Adam.
 //   LDS float atomics (ds_add_f32) sustain only ~0.33 lanes/clk/CU here while
 //   ds_add_u64 sustains ~4.9 (both measured), so the reduce accumulates in
-//   64-bit fixed point: the count pass records a bound on every |value| of a
-//   chunk (max |g| times max corner weight), the reduce takes the largest over
-//   the level's chunks and scales by the power of two that keeps a bucket's total below
+//   64-bit fixed point: the emit records a bound on every |value| of a chunk
+//   (the largest it wrote), the reduce takes the largest over the level's
+//   chunks and scales by the power of two that keeps a bucket's total below
 //   2^62 -- an exact scaling, one round-to-nearest per pair, ~2^-40 of the
 //   level's largest value per entry at the benchmark shape.
 //   Pair stores went through the L2 as 2-byte and 8-byte scattered writes and
@@ -184,180 +186,257 @@ __device__ __forceinline__ bool level_grad(const DevCfg& c, const float (&v)[F],
   return any;
 }
 
-// Emit rounds: EMIT_NT threads take EMIT_SPT samples each (EMIT_RS samples per round), and every bucket's
-// run of a round is padded with zero pairs to a multiple of PAD_RUN, so the copy-out moves PAD_RUN pairs
-// per lane with aligned 8/16-byte stores.  The larger the round, the longer the runs that land in each
-// bucket's slots, and short scattered runs are what limits the pass (HBM writes of a few hundred bytes
-// at scattered places).
-constexpr int EMIT_NT = 1024;
-constexpr int EMIT_SPT = 2;
-constexpr int EMIT_RS = EMIT_NT * EMIT_SPT;
+// One step of the emit's segmented suffix sum: lane i adds lane i + D's values when both are in its run
+// (take).  Runs lie inside aligned groups of at most 8 lanes, so lane i + D is in the same 16-lane row and
+// the DPP row shift reaches it.
+template <int D, int F>
+__device__ __forceinline__ void merge_step(float (&v)[8][F], bool take) {
+  static_assert(D < 16, "a row shift");
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+      // row_shl:D, zero past the row's end: the read folds into the add as a DPP operand
+      const float u = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[cc][f]), 0x100 + D, 0xF, 0xF, true));
+      const float t = v[cc][f] + u;
+      v[cc][f] = take ? t : v[cc][f];
+    }
+}
+
+// Emit rounds: one sample per thread, emit_nt(F) samples per round (the stage of a round's pairs must fit
+// in LDS at 2 + 4F bytes per pair), and every bucket's run of a round is padded with zero pairs to a
+// multiple of PAD_RUN, so the copy-out moves PAD_RUN pairs per lane with aligned 8/16-byte stores.
+// Same-cell samples merge within aligned groups of MERGE_BLK lanes (a run never crosses one), which keeps
+// the merge to log2(MERGE_BLK) register steps; longer groups would merge little more (at the benchmark
+// shape 73 % of the pairs remain with unbounded runs, 76 % with groups of 8).
 constexpr int PAD_RUN = 4;
-constexpr uint16_t REF_PAD = 0xFFFFu;  // stage reference of a padding pair
-static_assert(EMIT_RS * 8 <= REF_PAD, "stage references are 16-bit");
+constexpr int MERGE_BLK = 8;
+__host__ __device__ constexpr int emit_nt(int F) { return F >= 4 ? 512 : 1024; }
 __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
 
-// LDS of k_bin_emit: counters (32-bit words), per-sample corner fractions and gradients, then the stage
-__host__ __device__ constexpr int emit_words(int nbl) { return (3 * nbl + 4 + EMIT_NT / 64 + 3) & ~3; }
-__host__ __device__ constexpr int emit_stage_pairs(int nbl) {
-  return 8 * EMIT_RS + (PAD_RUN - 1) * (nbl < 8 * EMIT_RS ? nbl : 8 * EMIT_RS);
+// LDS of k_bin_emit: counters and the round's run-table row (32-bit words), then the stage: values
+// [np][F] and entries [np]
+__host__ __device__ constexpr int emit_words(int nbl, int F) { return (4 * nbl + 4 + emit_nt(F) / 64 + 3) & ~3; }
+__host__ __device__ constexpr int emit_stage_pairs(int nbl, int F) {
+  return 8 * emit_nt(F) + (PAD_RUN - 1) * (nbl < 8 * emit_nt(F) ? nbl : 8 * emit_nt(F));
 }
 __host__ __device__ constexpr int round8(int x) { return (x + 7) & ~7; }
 __host__ __device__ constexpr size_t emit_lds_bytes(int nbl, int F) {
-  return (size_t)emit_words(nbl) * 4 + (size_t)EMIT_RS * (16 + 4 * (size_t)F) +
-         (size_t)round8(emit_stage_pairs(nbl)) * 4;
+  return (size_t)emit_words(nbl, F) * 4 + (size_t)round8(emit_stage_pairs(nbl, F)) * (2 + 4 * (size_t)F);
 }
 
-// Emit the (entry, value) pairs of EMIT_RS samples at a time.  A round ranks its pairs by bucket in LDS
-// (a local counting sort into runs padded to PAD_RUN with zero pairs) and writes the sorted stage,
-// contiguously, into the round's own slots (np pairs per round), plus one table entry per bucket (the
-// run's offset and length in the slots).  Every write of the pass is so a sequential stream, and no
-// counting pass or global offsets are needed; the reduction reads each bucket's runs from all rounds.
-// The stage holds, per pair, its entry and a 16-bit reference (sample of the round, corner); the copy-out
-// forms the value g_f * w_corner from the sample's fractions and gradient kept in LDS (the same products
-// as at ranking time).  A round has three barriers: after the ranking, after wavefront 0 has scanned the
-// round's counts (stage offsets, table entries, the other counter buffer cleared for the next round), and
-// after the stage is written.  The next round's inputs are loaded during the round.  The block also
-// writes cmax[level in group][chunk], a bound on every |value| of its pairs: the largest
-// max_f |g_f| * max_c |w_c| over its samples.
+// Inclusive sum over the 64 lanes: DPP row shifts within 16-lane rows, then row broadcasts of lanes 15
+// and 31 into the rows above (all VALU).
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
+  int v = (int)x;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2 and 3
+  return (uint32_t)v;
+}
+
+// One sample of an emit round, ready to rank: its cell at the level and, at a run's head, the run's eight
+// corner sums.
+template <int F>
+struct EmitSample {
+  bool head;
+  int i0[3];
+  float v[8][F];
+};
+
+// Form a sample's corner values g_f * w_corner and merge same-cell runs: a sample in the same cell as the
+// previous lane's (within its group of MERGE_BLK lanes) continues that lane's run; a segmented suffix sum
+// over the lanes (DPP row shifts by 1, 2, 4, a step taken only when some run of the wavefront is longer
+// than its stride) leaves each run's first lane, its head, with the run's sums.  The additions follow a
+// fixed tree, so the values are deterministic.
 template <int F, int MODE>
-__global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
-                                                      const float* __restrict__ g, FeatLayout lay, float lr,
-                                                      uint32_t* __restrict__ meta, float* __restrict__ cmax,
-                                                      uint16_t* __restrict__ pair_idx,
-                                                      float* __restrict__ pair_val) {
+__device__ __forceinline__ void emit_prepare(const DevCfg& c, const PosSrc& src, const RawSample<F>& in, bool valid,
+                                             int l, float lr, int lane, EmitSample<F>& es) {
+  float gf[F];
+  const bool act = valid && level_grad<F, MODE>(c, in.g, l, lr, gf);
+  LevelCell lc;
+  lc.i0[0] = lc.i0[1] = lc.i0[2] = -1;
+  if (act) {
+    float pos[3], p[3];
+    raw_position<F>(src, in, pos);
+    normalize_pos(c, pos, p);
+    lc = level_cell(c.res[l], p);
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+      const float w = corner_weight(lc, cc);
+#pragma unroll
+      for (int f = 0; f < F; ++f) es.v[cc][f] = gf[f] * w;
+    }
+  } else {
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+      for (int f = 0; f < F; ++f) es.v[cc][f] = 0.0f;
+  }
+  const int p0 = __shfl_up(lc.i0[0], 1), p1 = __shfl_up(lc.i0[1], 1), p2 = __shfl_up(lc.i0[2], 1);
+  const bool cont = act && (lane & (MERGE_BLK - 1)) != 0 && p0 == lc.i0[0] && p1 == lc.i0[1] && p2 == lc.i0[2];
+  const uint64_t cm = __ballot(cont);
+  if (cm != 0ull) {
+    // lanes from this one to its run's end (the next lane that continues nothing); at most MERGE_BLK
+    const uint64_t starts_above = lane == 63 ? 0ull : (~cm >> (lane + 1));
+    const int len = starts_above == 0ull ? 64 - lane : 1 + (int)__builtin_ctzll(starts_above);
+    merge_step<1, F>(es.v, len > 1);
+    if (__ballot(len > 2) != 0ull) {
+      merge_step<2, F>(es.v, len > 2);
+      if (__ballot(len > 4) != 0ull) merge_step<4, F>(es.v, len > 4);
+    }
+  }
+  es.head = act && !cont;
+  es.i0[0] = lc.i0[0];
+  es.i0[1] = lc.i0[1];
+  es.i0[2] = lc.i0[2];
+}
+
+// Emit the (entry, value) pairs of emit_nt(F) samples at a time.  Only run heads (emit_prepare) rank and
+// stage pairs: along a ray the coarse levels hold many samples per cell (at the benchmark shape the pairs
+// fall to ~76 % over the 16 levels, to ~30 % at the coarsest).  A round ranks the heads' pairs by bucket
+// in LDS (a local counting sort into runs padded to PAD_RUN with zero pairs), stages them (entry in
+// bucket, values), and writes the stage contiguously into the round's own slots (np pairs per round),
+// plus its row of the run table (each bucket's run offset and length in the slots).  Every write of the
+// pass is so a sequential stream, and no counting pass or global offsets are needed; the reduction reads
+// each bucket's runs from all rounds.
+// Order within a round: prepare the round's samples; issue the next round's loads; rank; barrier;
+// wavefront 0 scans the counts (stage offsets, the run-table row, the other counter buffer cleared for
+// the next round); barrier; stage the pairs; barrier; copy out the stage and the run-table row.  The pass
+// is bound by its vector ALU work (hashes, weights, the merge; a wave64 instruction occupies its SIMD four
+// cycles).  Measured slower at the benchmark shape: preparing the next round's samples before the
+// copy-out (6.2 against 5.5 ms), and splitting the wavefronts into loaders that never store and writers
+// that never load (7.3 ms: the loaders' ALU work per wavefront doubles).  The block also writes
+// cmax[level in group][chunk], a bound on every |value| of its pairs: the largest it staged.
+template <int F, int MODE>
+__global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
+                                                         const float* __restrict__ g, FeatLayout lay, float lr,
+                                                         uint32_t* __restrict__ meta, float* __restrict__ cmax,
+                                                         uint16_t* __restrict__ pair_idx,
+                                                         float* __restrict__ pair_val) {
   typedef typename FVec<F>::T V;
+  constexpr int NT = emit_nt(F);
   extern __shared__ uint32_t sm[];
   const int li = (int)blockIdx.y, l = grp.level0 + li;
   const int nbl = grp.nbl[li];
   const int chunk = blockIdx.x;
   uint32_t* lcnt = sm;              // [2][nbl] pairs of the round per bucket
   uint32_t* loff = lcnt + 2 * nbl;  // [nbl] run offsets in the stage
-  uint32_t* total_s = loff + nbl;   // [1] padded pairs of the round
-  float* wmax = reinterpret_cast<float*>(total_s + 4);                 // [EMIT_NT / 64]
-  float4* s_frac = reinterpret_cast<float4*>(sm + emit_words(nbl));    // [EMIT_RS] corner fractions
-  V* s_grad = reinterpret_cast<V*>(s_frac + EMIT_RS);                  // [EMIT_RS] gradient
-  uint16_t* st_idx = reinterpret_cast<uint16_t*>(s_grad + EMIT_RS);    // [np] entry in bucket
-  uint16_t* st_ref = st_idx + round8(grp.np);                          // [np] sample * 8 + corner
+  uint32_t* lrow = loff + nbl;      // [nbl] the round's run-table row
+  uint32_t* total_s = lrow + nbl;   // [1] padded pairs of the round
+  float* wmax = reinterpret_cast<float*>(total_s + 4);                          // [NT / 64]
+  float* st_val = reinterpret_cast<float*>(sm + emit_words(nbl, F));            // [np][F]
+  uint16_t* st_idx = reinterpret_cast<uint16_t*>(st_val + (size_t)grp.np * F);  // [np]
   const int tid = threadIdx.x, lane = tid & 63;
-  for (int j = tid; j < nbl; j += EMIT_NT) lcnt[j] = 0u;
+  for (int j = tid; j < nbl; j += NT) lcnt[j] = 0u;
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
   const int64_t b_begin = (int64_t)chunk * grp.chunk;
   const int64_t b_end = b_begin + grp.chunk < n ? b_begin + grp.chunk : n;
-  RawSample<F> in[EMIT_SPT];
-#pragma unroll
-  for (int q = 0; q < EMIT_SPT; ++q)
-    if (b_begin + tid + q * EMIT_NT < b_end) load_raw<F>(src, g, lay, b_begin + tid + q * EMIT_NT, l, in[q]);
+  const int kb = (nbl + 63) >> 6;  // counters per lane in the scan
+  RawSample<F> in;
+  if (b_begin + tid < b_end) load_raw<F>(src, g, lay, b_begin + tid, l, in);
   __syncthreads();
   float bound = 0.0f;
   int r = 0;
-  for (int64_t rb = b_begin; rb < b_end; rb += EMIT_RS, r ^= 1) {
-    const int64_t round = rb / EMIT_RS;  // the round's index in the level
+  for (int64_t rb = b_begin; rb < b_end; rb += NT, r ^= 1) {
+    const int64_t round = rb / NT;  // the round's index in the level
     uint32_t* cur = lcnt + r * nbl;
     uint32_t* nxt = lcnt + (r ^ 1) * nbl;
-    bool act[EMIT_SPT];
-    float gf[EMIT_SPT][F], fr[EMIT_SPT][3];
-    uint32_t ent[EMIT_SPT][8], rank[EMIT_SPT][8];
+    EmitSample<F> es;
+    emit_prepare<F, MODE>(c, src, in, rb + tid < b_end, l, lr, lane, es);
+    if (rb + NT + tid < b_end) load_raw<F>(src, g, lay, rb + NT + tid, l, in);
+    uint32_t ent[8], rank[8];
+    if (es.head) {
+      LevelCell lc;
+      lc.i0[0] = es.i0[0];
+      lc.i0[1] = es.i0[1];
+      lc.i0[2] = es.i0[2];
 #pragma unroll
-    for (int q = 0; q < EMIT_SPT; ++q) {
-      const int64_t b = rb + tid + q * EMIT_NT;
-      act[q] = b < b_end && level_grad<F, MODE>(c, in[q].g, l, lr, gf[q]);
-      if (act[q]) {
-        float pos[3], p[3];
-        raw_position<F>(src, in[q], pos);
-        normalize_pos(c, pos, p);
-        const LevelCell lc = level_cell(c.res[l], p);
-        fr[q][0] = lc.f[0];
-        fr[q][1] = lc.f[1];
-        fr[q][2] = lc.f[2];
-        float gm = 0.0f, wm = 0.0f;
+      for (int cc = 0; cc < 8; ++cc) {
 #pragma unroll
-        for (int f = 0; f < F; ++f) gm = fmaxf(gm, fabsf(gf[q][f]));
-#pragma unroll
-        for (int cc = 0; cc < 8; ++cc) {
-          wm = fmaxf(wm, fabsf(corner_weight(lc, cc)));
-          ent[q][cc] = corner_entry(lc, cc, l, c.mask[l]);
-          rank[q][cc] = atomicAdd(&cur[ent[q][cc] >> grp.log2_be], 1u);
-        }
-        bound = fmaxf(bound, gm * wm);
+        for (int f = 0; f < F; ++f) bound = fmaxf(bound, fabsf(es.v[cc][f]));
+        ent[cc] = corner_entry(lc, cc, l, c.mask[l]);
+        rank[cc] = atomicAdd(&cur[ent[cc] >> grp.log2_be], 1u);
       }
-      if (b + EMIT_RS < b_end) load_raw<F>(src, g, lay, b + EMIT_RS, l, in[q]);
     }
     __syncthreads();
     if (tid < 64) {
-      uint32_t* mrow = meta + ((int64_t)li * grp.n_rounds + round) * grp.meta_stride;
-      uint32_t carry = 0;
-      for (int j0 = 0; j0 < nbl; j0 += 64) {
-        const int j = j0 + lane;
-        const uint32_t cn = j < nbl ? pad_run(cur[j]) : 0u;
-        uint32_t incl = cn;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const uint32_t o = __shfl_up(incl, d);
-          if (lane >= d) incl += o;
+      // lane t scans counters [t * kb, t * kb + kb); nbl is a power of two, so from 256 buckets on every
+      // lane holds a multiple of 4 of them, read and written 16 bytes at a time
+      const int j0 = lane * kb;
+      uint32_t own = 0;
+      if (j0 < nbl) {
+        if (kb >= 4) {
+          for (int k = 0; k < kb; k += 4) {
+            const uint4 c4 = *reinterpret_cast<const uint4*>(cur + j0 + k);
+            own += pad_run(c4.x) + pad_run(c4.y) + pad_run(c4.z) + pad_run(c4.w);
+          }
+        } else {
+          for (int k = 0; k < kb; ++k) own += pad_run(cur[j0 + k]);
         }
-        if (j < nbl) {
-          const uint32_t o = carry + incl - cn;
-          loff[j] = o;
-          mrow[j] = (o << 16) | cn;
-          nxt[j] = 0u;
-        }
-        carry += __shfl(incl, 63);
       }
-      if (lane == 0) total_s[0] = carry;
+      const uint32_t incl = wave_incl_sum(own);
+      uint32_t o = incl - own;
+      if (j0 < nbl) {
+        if (kb >= 4) {
+          for (int k = 0; k < kb; k += 4) {
+            const uint4 c4 = *reinterpret_cast<const uint4*>(cur + j0 + k);
+            const uint32_t n0 = pad_run(c4.x), n1 = pad_run(c4.y), n2 = pad_run(c4.z), n3 = pad_run(c4.w);
+            const uint4 of = make_uint4(o, o + n0, o + n0 + n1, o + n0 + n1 + n2);
+            *reinterpret_cast<uint4*>(loff + j0 + k) = of;
+            *reinterpret_cast<uint4*>(lrow + j0 + k) =
+                make_uint4((of.x << 16) | n0, (of.y << 16) | n1, (of.z << 16) | n2, (of.w << 16) | n3);
+            *reinterpret_cast<uint4*>(nxt + j0 + k) = make_uint4(0u, 0u, 0u, 0u);
+            o = of.w + n3;
+          }
+        } else {
+          for (int k = 0; k < kb; ++k) {
+            const int j = j0 + k;
+            const uint32_t cn = pad_run(cur[j]);
+            loff[j] = o;
+            lrow[j] = (o << 16) | cn;
+            nxt[j] = 0u;
+            o += cn;
+          }
+        }
+      }
+      if (lane == 63) total_s[0] = incl;
     }
     __syncthreads();
-#pragma unroll
-    for (int q = 0; q < EMIT_SPT; ++q) {
-      if (!act[q]) continue;
-      const int ls = tid + q * EMIT_NT;
-      s_frac[ls] = make_float4(fr[q][0], fr[q][1], fr[q][2], 0.0f);
-      s_grad[ls] = FVec<F>::pack(gf[q]);
+    if (es.head) {
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
-        const uint32_t slot = loff[ent[q][cc] >> grp.log2_be] + rank[q][cc];
-        st_idx[slot] = (uint16_t)(ent[q][cc] & be_mask);
-        st_ref[slot] = (uint16_t)(ls * 8 + cc);
+        const uint32_t slot = loff[ent[cc] >> grp.log2_be] + rank[cc];
+        st_idx[slot] = (uint16_t)(ent[cc] & be_mask);
+        reinterpret_cast<V*>(st_val)[slot] = FVec<F>::pack(es.v[cc]);
       }
     }
     // zero pairs pad every run to a multiple of PAD_RUN
-    for (int j = tid; j < nbl; j += EMIT_NT) {
+    for (int j = tid; j < nbl; j += NT) {
       const uint32_t c0 = cur[j], c1 = pad_run(c0), o = loff[j];
       for (uint32_t k = c0; k < c1; ++k) {
         st_idx[o + k] = 0;
-        st_ref[o + k] = REF_PAD;
+        float z[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) z[f] = 0.0f;
+        reinterpret_cast<V*>(st_val)[o + k] = FVec<F>::pack(z);
       }
     }
     __syncthreads();
-    const uint32_t nq = total_s[0] / PAD_RUN;
+    uint32_t* mrow = meta + ((int64_t)li * grp.n_rounds + round) * grp.meta_stride;
+    for (int j = tid; j < nbl; j += NT) mrow[j] = lrow[j];
+    const uint32_t nq = min(total_s[0], (uint32_t)grp.np) / PAD_RUN;  // the round's slots bound the copy
     const int64_t slot0 = ((int64_t)li * grp.n_rounds + round) * grp.np;
-    for (uint32_t qd = (uint32_t)tid; qd < nq; qd += EMIT_NT) {
+    for (uint32_t qd = (uint32_t)tid; qd < nq; qd += NT) {
       const uint32_t i = qd * PAD_RUN;
-      const uint2 refs = *reinterpret_cast<const uint2*>(st_ref + i);
-      const uint32_t rf[PAD_RUN] = {refs.x & 0xFFFFu, refs.x >> 16, refs.y & 0xFFFFu, refs.y >> 16};
-      float v[PAD_RUN * F];
-#pragma unroll
-      for (int k = 0; k < PAD_RUN; ++k) {
-        if (rf[k] == REF_PAD) {
-#pragma unroll
-          for (int f = 0; f < F; ++f) v[k * F + f] = 0.0f;
-        } else {
-          const float4 fq = s_frac[rf[k] >> 3];
-          LevelCell lc;
-          lc.f[0] = fq.x;
-          lc.f[1] = fq.y;
-          lc.f[2] = fq.z;
-          const float w = corner_weight(lc, (int)(rf[k] & 7u));
-          float gq[F];
-          FVec<F>::unpack(s_grad[rf[k] >> 3], gq);
-#pragma unroll
-          for (int f = 0; f < F; ++f) v[k * F + f] = gq[f] * w;
-        }
-      }
       *reinterpret_cast<uint2*>(pair_idx + slot0 + i) = *reinterpret_cast<const uint2*>(st_idx + i);
+      const float4* sv = reinterpret_cast<const float4*>(st_val + (size_t)i * F);
       float4* gv = reinterpret_cast<float4*>(pair_val + (slot0 + i) * F);
 #pragma unroll
-      for (int k = 0; k < F; ++k) gv[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+      for (int k = 0; k < F; ++k) gv[k] = sv[k];
     }
   }
   bound = wave_max_nonneg(bound);
@@ -365,7 +444,7 @@ __global__ __launch_bounds__(EMIT_NT) void k_bin_emit(DevCfg c, PosSrc src, int6
   __syncthreads();
   if (tid == 0) {
     float m = 0.0f;
-    for (int w = 0; w < EMIT_NT / 64; ++w) m = fmaxf(m, wmax[w]);
+    for (int w = 0; w < NT / 64; ++w) m = fmaxf(m, wmax[w]);
     cmax[(int64_t)li * grp.nblk + chunk] = m;
   }
 }
@@ -625,11 +704,19 @@ hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
 
 BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   BinPlan p{};
-  // int64 LDS accumulator of one bucket: 2^log2_be * F * 8 bytes = 64 KiB
+  // int64 LDS accumulator of one bucket: 2^log2_be * F * 8 bytes = 64 KiB (two reduce blocks per CU), or
+  // 128 KiB when a level would otherwise have more than 256 buckets: an emit round's pairs spread over
+  // the buckets, and runs of a few pairs make the reduction's reads short and the padding large
   p.log2_be = c.F == 4 ? 11 : (c.F == 2 ? 12 : 13);
-  p.chunk = 4 * EMIT_RS;
+  {
+    uint32_t max_T = 0;
+    for (int l = 0; l < c.L; ++l) max_T = c.mask[l] + 1 > max_T ? c.mask[l] + 1 : max_T;
+    if ((max_T >> p.log2_be) > 256u) ++p.log2_be;
+  }
+  const int rs = emit_nt(c.F);  // samples per emit round
+  p.chunk = 8 * rs;
   p.nblk = (int)((n + p.chunk - 1) / p.chunk);
-  p.n_rounds = (int)((n + EMIT_RS - 1) / EMIT_RS);
+  p.n_rounds = (int)((n + rs - 1) / rs);
   int max_nbl = 0;
   for (int l = 0; l < c.L; ++l) {
     const int nbl = (int)(((int64_t)c.mask[l] + 1 + (1 << p.log2_be) - 1) >> p.log2_be);
@@ -637,7 +724,7 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   }
   // every round of a level has its own np pair slots (its pairs and at most PAD_RUN - 1 padding pairs per
   // bucket that receives any)
-  p.np = round8(emit_stage_pairs(max_nbl));
+  p.np = round8(emit_stage_pairs(max_nbl, c.F));
   const int64_t per_level_pairs = (int64_t)p.n_rounds * p.np;
   const int64_t pair_bytes = 2 + 4 * (int64_t)c.F;
   int lg = (int)(pair_budget_bytes / (size_t)(per_level_pairs * pair_bytes));
@@ -690,8 +777,8 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                        (unsigned)grp.n_levels);
 #define FFN_BIN(FV, MV)                                                                                            \
   do {                                                                                                             \
-    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(EMIT_NT), lds_emit, st, c, src, n, grp, g, lay, lr,     \
-                       s.meta, s.cmax, s.pair_idx, s.pair_val);                                                    \
+    hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(emit_nt(FV)), lds_emit, st, c, src, n, grp, g, lay,   \
+                       lr, s.meta, s.cmax, s.pair_idx, s.pair_val);                                                \
     hipLaunchKernelGGL(k_bin_meta_transpose, grid_tr, dim3(256), 0, st, s.meta, s.meta_t, grp.n_rounds,            \
                        grp.meta_stride);                                                                           \
     hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,         \
@@ -719,21 +806,70 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
   return hipSuccess;
 }
 
-// level-major [L][N][F] <-> sample-major [N][L*F] copies (for taps)
-__global__ __launch_bounds__(256) void k_feat_relayout(const float* __restrict__ src, FeatLayout ls,
-                                                       float* __restrict__ dst, FeatLayout ld, int64_t n, int L,
-                                                       int F) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= n) return;
-  for (int l = 0; l < L; ++l)
-    for (int f = 0; f < F; ++f) dst[l * ld.stride_l + b * ld.stride_b + f] = src[l * ls.stride_l + b * ls.stride_b + f];
+// level-major [L][N][F] <-> sample-major [N][L*F] transposes (the encode entry points' sample-major
+// buffers, taps).  A block moves RL_TB samples through an LDS tile [RL_TB][L*F + 1] (odd pitch: the
+// level-major side's column accesses spread over the banks): the sample-major side is one contiguous
+// range, the level-major side one contiguous range per level, so every global access is coalesced.
+constexpr int RL_TB = 128;
+template <bool TO_LEVEL_MAJOR>
+__global__ __launch_bounds__(256) void k_feat_relayout(const float* __restrict__ src, float* __restrict__ dst,
+                                                       int64_t n, int L, int F) {
+  extern __shared__ float tile[];
+  const int LF = L * F, pitch = LF + 1, lgF = F >> 1;  // F is 1, 2 or 4
+  const int64_t b0 = (int64_t)blockIdx.x * RL_TB;
+  const int nb = (int)(n - b0 < RL_TB ? n - b0 : RL_TB);
+  const int tid = threadIdx.x;
+  // sample-major side: element i of the range is (sample i / LF, feature i % LF); the quotient and
+  // remainder advance by a fixed step per iteration
+  const int qs = 256 / LF, rs = 256 % LF;
+  if (TO_LEVEL_MAJOR) {
+    int bq = tid / LF, kr = tid % LF;
+    for (int i = tid; i < nb * LF; i += 256) {
+      tile[bq * pitch + kr] = src[b0 * LF + i];
+      bq += qs;
+      kr += rs;
+      if (kr >= LF) {
+        kr -= LF;
+        ++bq;
+      }
+    }
+    __syncthreads();
+    for (int l = 0; l < L; ++l)
+      for (int j = tid; j < nb * F; j += 256)
+        dst[(int64_t)l * n * F + b0 * F + j] = tile[(j >> lgF) * pitch + l * F + (j & (F - 1))];
+  } else {
+    for (int l = 0; l < L; ++l)
+      for (int j = tid; j < nb * F; j += 256)
+        tile[(j >> lgF) * pitch + l * F + (j & (F - 1))] = src[(int64_t)l * n * F + b0 * F + j];
+    __syncthreads();
+    int bq = tid / LF, kr = tid % LF;
+    for (int i = tid; i < nb * LF; i += 256) {
+      dst[b0 * LF + i] = tile[bq * pitch + kr];
+      bq += qs;
+      kr += rs;
+      if (kr >= LF) {
+        kr -= LF;
+        ++bq;
+      }
+    }
+  }
 }
 
 hipError_t launch_feat_relayout(const float* src, const FeatLayout& ls, float* dst, const FeatLayout& ld, int64_t n,
                                 int L, int F, hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_feat_relayout, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, ls, dst, ld, n, L,
-                     F);
+  const FeatLayout sm = sample_major(L, F), lm = level_major(n, F);
+  const bool s_sm = ls.stride_l == sm.stride_l && ls.stride_b == sm.stride_b;
+  const bool s_lm = ls.stride_l == lm.stride_l && ls.stride_b == lm.stride_b;
+  const bool d_sm = ld.stride_l == sm.stride_l && ld.stride_b == sm.stride_b;
+  const bool d_lm = ld.stride_l == lm.stride_l && ld.stride_b == lm.stride_b;
+  if (!((s_sm && d_lm) || (s_lm && d_sm)) || (F != 1 && F != 2 && F != 4)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((n + RL_TB - 1) / RL_TB));
+  const size_t lds = sizeof(float) * (size_t)RL_TB * (size_t)(L * F + 1);
+  if (s_sm)
+    hipLaunchKernelGGL(k_feat_relayout<true>, grid, dim3(256), lds, st, src, dst, n, L, F);
+  else
+    hipLaunchKernelGGL(k_feat_relayout<false>, grid, dim3(256), lds, st, src, dst, n, L, F);
   return hipGetLastError();
 }
 

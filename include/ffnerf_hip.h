@@ -141,11 +141,15 @@ int ffn_sample(void* handle, const void* rays, uint32_t num_rays, uint32_t sampl
                int32_t do_train, float* Ts, float* DTs, uint32_t* flags, void* stream);
 
 /* Hash-grid encoding of n points x [n][3] (world space) with the bound table:
- * a0 [n][LF].  idx_out (optional) [n][L][8]: feature base index per corner. */
+ * a0 [n][LF].  idx_out (optional) [n][L][8]: feature base index per corner.
+ * Stages the encodings level-major in the handle's scratch (n * LF floats), so
+ * calls on one handle must not overlap. */
 int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint32_t* idx_out, void* stream);
 
 /* Scatter-add of the encoding gradient g [n][LF] of points x into grad
- * (table-shaped, caller-zeroed).  Non-finite gradients are skipped. */
+ * (table-shaped, caller-zeroed).  Non-finite gradients are skipped.  Stages g
+ * level-major in the handle's scratch (n * LF floats), so calls on one handle
+ * must not overlap. */
 int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n, float* grad, void* stream);
 
 /* Adam over n parameters (weight_update.cl:177-201 form).  If zero_grad,

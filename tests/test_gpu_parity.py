@@ -83,24 +83,45 @@ def test_hash_backward_matches_oracle(gh, ora, which):
     assert (touched_g == touched_o).mean() > 0.9999
 
 
-@pytest.mark.parametrize("case", ["f1", "one_partial_round", "wide_table"])
+def _ray_walk_points(rng, lo, hi, n_rays, per_ray):
+    """Points that walk along rays in small steps, so consecutive samples share cells at the coarse levels
+    (runs of every length, longer than one merge group)."""
+    o = lo + (hi - lo) * rng.uniform(0.2, 0.8, (n_rays, 1, 3))
+    d = rng.normal(size=(n_rays, 1, 3))
+    d /= np.linalg.norm(d, axis=2, keepdims=True)
+    t = np.cumsum(rng.uniform(0.0, 0.006, (n_rays, per_ray, 1)), axis=1)
+    return np.clip(o + t * d * (hi - lo), lo, hi).reshape(-1, 3).astype(np.float32)
+
+
+@pytest.mark.parametrize("case", ["f1", "one_partial_round", "wide_table", "runs", "runs_f4"])
 def test_hash_backward_shapes(gh, ora, case):
     """The scatter's edge shapes: one feature per level (8192-entry buckets), fewer samples than one emit
-    round, and 2^22-entry levels (1024 buckets per level: the widest run table and emit stage)."""
+    round, 2^22-entry levels (1024 buckets per level: the widest run table and emit stage), and samples
+    along rays (consecutive samples in one cell are merged before the scatter; zero-gradient samples inside
+    the runs break them), at two and four features per level."""
     print(f"[case] hash bwd shape {case}", flush=True)
+    rng = np.random.default_rng(34)
     if case == "f1":
         spec, n = spec_cfg0(f_per_level=1), 20000
     elif case == "one_partial_round":
         spec, n = spec_cfg0(), 1000
-    else:
+    elif case == "wide_table":
         spec, n = spec_cfg0(n_levels=2, log2_T=[22, 22], res=[256.0, 2048.0]), 50000
+    else:
+        spec = spec_cfg0(f_per_level=4 if case == "runs_f4" else 2)
+        n = 96 * 64 + 37
     p = random_params(spec, seed=33)
     m = gh.GpuModel(spec, p)
-    rng = np.random.default_rng(34)
     lo, hi = np.array(spec["box_min"]), np.array(spec["box_max"])
-    x = (lo + (hi - lo) * rng.uniform(0, 1, (n, 3))).astype(np.float32)
+    if case.startswith("runs"):
+        x = np.concatenate([_ray_walk_points(rng, lo, hi, 96, 64), _ray_walk_points(rng, lo, hi, 1, 37)])
+        x[100:140] = x[100]  # one point repeated over a whole merge group and more
+    else:
+        x = (lo + (hi - lo) * rng.uniform(0, 1, (n, 3))).astype(np.float32)
     LF = spec["n_levels"] * spec["f_per_level"]
     g = rng.normal(size=(n, LF)).astype(np.float32)
+    if case.startswith("runs"):
+        g[::7] = 0.0
     grad_g = m.encode_bwd(x, g, table_floats(spec))
     grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
     scale = np.abs(grad_o).max()
