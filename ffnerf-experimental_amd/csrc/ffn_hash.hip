@@ -705,13 +705,16 @@ hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
 BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   BinPlan p{};
   // int64 LDS accumulator of one bucket: 2^log2_be * F * 8 bytes = 64 KiB (two reduce blocks per CU), or
-  // 128 KiB when a level would otherwise have more than 256 buckets: an emit round's pairs spread over
-  // the buckets, and runs of a few pairs make the reduction's reads short and the padding large
+  // 128 KiB (one) when a level would otherwise have more than 64 buckets.  An emit round's pairs spread
+  // over the buckets, and every run costs its two edge sectors twice (the neighbouring buckets' blocks
+  // read them too) plus its padding: at the benchmark shape 64 buckets per level measured emit 4.95 and
+  // reduce 2.81 ms against 5.12 and 3.19 ms with 128.  Small tables keep the small buckets, so that the
+  // reduction still has blocks for every CU.
   p.log2_be = c.F == 4 ? 11 : (c.F == 2 ? 12 : 13);
   {
     uint32_t max_T = 0;
     for (int l = 0; l < c.L; ++l) max_T = c.mask[l] + 1 > max_T ? c.mask[l] + 1 : max_T;
-    if ((max_T >> p.log2_be) > 256u) ++p.log2_be;
+    if ((max_T >> p.log2_be) > 64u) ++p.log2_be;
   }
   const int rs = emit_nt(c.F);  // samples per emit round
   p.chunk = 8 * rs;
