@@ -72,7 +72,7 @@ struct Handle {
   int64_t table_floats = 0;
   int n_cu = 0;
   Scratch Ts, DTs, flags, a0, dLda0, partials;
-  Scratch bin_meta, bin_meta_t, bin_idx, bin_val, bin_max;
+  Scratch bin_meta, bin_meta_t, bin_pairs, bin_max;
   // marcher / render
   Scratch m_state, m_acc, m_counts, m_offsets, m_sums, m_total, m_samples, m_ids, m_a0, m_sigma, m_rgb;
   uint32_t* host_total = nullptr;  // pinned
@@ -80,7 +80,7 @@ struct Handle {
 
 size_t bin_budget_bytes() {
   const char* e = getenv("FFN_BIN_BUDGET_MB");
-  size_t mb = e ? (size_t)atoll(e) : (size_t)24576;
+  size_t mb = e ? (size_t)atoll(e) : (size_t)32768;
   if (mb < 64) mb = 64;
   return mb << 20;
 }
@@ -91,13 +91,11 @@ hipError_t ensure_bins(Handle* h, int64_t n, ffn::BinPlan* plan, ffn::BinScratch
   hipError_t e;
   if ((e = h->bin_meta.ensure(sizeof(uint32_t) * (size_t)plan->meta_elems)) != hipSuccess) return e;
   if ((e = h->bin_meta_t.ensure(sizeof(uint32_t) * (size_t)plan->meta_elems)) != hipSuccess) return e;
-  if ((e = h->bin_idx.ensure(sizeof(uint16_t) * (size_t)plan->max_pairs)) != hipSuccess) return e;
-  if ((e = h->bin_val.ensure(sizeof(float) * (size_t)plan->max_pairs * h->dc.F)) != hipSuccess) return e;
+  if ((e = h->bin_pairs.ensure((2 + 4 * (size_t)h->dc.F) * (size_t)plan->max_pairs)) != hipSuccess) return e;
   if ((e = h->bin_max.ensure(sizeof(float) * (size_t)plan->levels_per_group * plan->nblk)) != hipSuccess) return e;
   s->meta = (uint32_t*)h->bin_meta.p;
   s->meta_t = (uint32_t*)h->bin_meta_t.p;
-  s->pair_idx = (uint16_t*)h->bin_idx.p;
-  s->pair_val = (float*)h->bin_val.p;
+  s->pairs = (uint4*)h->bin_pairs.p;
   s->cmax = (float*)h->bin_max.p;
   return hipSuccess;
 }
@@ -240,8 +238,7 @@ int ffn_destroy(void* handle) {
   h->partials.release();
   h->bin_meta.release();
   h->bin_meta_t.release();
-  h->bin_idx.release();
-  h->bin_val.release();
+  h->bin_pairs.release();
   h->bin_max.release();
   for (Scratch* sc : {&h->m_state, &h->m_acc, &h->m_counts, &h->m_offsets, &h->m_sums, &h->m_total, &h->m_samples,
                       &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb})

@@ -35,7 +35,8 @@
 //   Pair stores went through the L2 as 2-byte and 8-byte scattered writes and
 //   stalled the address/data path (measured: write data stalled by the cache),
 //   so every bucket run of an emit round is padded with zero pairs to a
-//   multiple of 4 and each lane stores 4 pairs with aligned 8/16-byte writes.
+//   multiple of 8 and the pairs move in 16-byte aligned blocks of 8 (values,
+//   then entries), one block per lane.
 //   Levels are processed in groups so the pair buffer stays bounded.
 #include "ffn_device.h"
 #include "ffn_kernels.h"
@@ -205,11 +206,15 @@ __device__ __forceinline__ void merge_step(float (&v)[8][F], bool take) {
 
 // Emit rounds: one sample per thread, emit_nt(F) samples per round (the stage of a round's pairs must fit
 // in LDS at 2 + 4F bytes per pair), and every bucket's run of a round is padded with zero pairs to a
-// multiple of PAD_RUN, so the copy-out moves PAD_RUN pairs per lane with aligned 8/16-byte stores.
+// multiple of PAD_RUN.  The pair buffer is a sequence of blocks of PAD_RUN pairs, each 16-byte aligned:
+// the block's 8F values, then its 8 entries (pair_block_words(F) 16-byte words), so a run is one
+// contiguous range for the reduction (with entries and values in separate arrays, a run of a few dozen
+// pairs was two short ranges whose edge sectors were fetched twice).
 // Same-cell samples merge within aligned groups of MERGE_BLK lanes (a run never crosses one), which keeps
 // the merge to log2(MERGE_BLK) register steps; longer groups would merge little more (at the benchmark
 // shape 73 % of the pairs remain with unbounded runs, 76 % with groups of 8).
-constexpr int PAD_RUN = 4;
+constexpr int PAD_RUN = 8;
+__host__ __device__ constexpr int pair_block_words(int F) { return 2 * F + 1; }
 constexpr int MERGE_BLK = 8;
 __host__ __device__ constexpr int emit_nt(int F) { return F >= 4 ? 512 : 1024; }
 __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
@@ -315,8 +320,7 @@ template <int F, int MODE>
 __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                          const float* __restrict__ g, FeatLayout lay, float lr,
                                                          uint32_t* __restrict__ meta, float* __restrict__ cmax,
-                                                         uint16_t* __restrict__ pair_idx,
-                                                         float* __restrict__ pair_val) {
+                                                         uint4* __restrict__ pbuf) {
   typedef typename FVec<F>::T V;
   constexpr int NT = emit_nt(F);
   extern __shared__ uint32_t sm[];
@@ -428,15 +432,15 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
     __syncthreads();
     uint32_t* mrow = meta + ((int64_t)li * grp.n_rounds + round) * grp.meta_stride;
     for (int j = tid; j < nbl; j += NT) mrow[j] = lrow[j];
-    const uint32_t nq = min(total_s[0], (uint32_t)grp.np) / PAD_RUN;  // the round's slots bound the copy
-    const int64_t slot0 = ((int64_t)li * grp.n_rounds + round) * grp.np;
-    for (uint32_t qd = (uint32_t)tid; qd < nq; qd += NT) {
-      const uint32_t i = qd * PAD_RUN;
-      *reinterpret_cast<uint2*>(pair_idx + slot0 + i) = *reinterpret_cast<const uint2*>(st_idx + i);
-      const float4* sv = reinterpret_cast<const float4*>(st_val + (size_t)i * F);
-      float4* gv = reinterpret_cast<float4*>(pair_val + (slot0 + i) * F);
-#pragma unroll
-      for (int k = 0; k < F; ++k) gv[k] = sv[k];
+    // the round's blocks as one sequence of 16-byte words, lane t on word t: every store instruction
+    // writes 1 KB contiguously (a lane per block would store at the block stride)
+    constexpr uint32_t W = pair_block_words(F);
+    const uint32_t nw = min(total_s[0], (uint32_t)grp.np) / PAD_RUN * W;  // the round's slots bound the copy
+    uint4* dst = pbuf + ((int64_t)li * grp.n_rounds + round) * (grp.np / PAD_RUN) * W;
+    for (uint32_t w = (uint32_t)tid; w < nw; w += NT) {
+      const uint32_t blk = w / W, k = w - blk * W;
+      dst[w] = k < 2 * F ? reinterpret_cast<const uint4*>(st_val)[blk * 2 * F + k]
+                         : reinterpret_cast<const uint4*>(st_idx)[blk];
     }
   }
   bound = wave_max_nonneg(bound);
@@ -475,12 +479,11 @@ __global__ __launch_bounds__(256) void k_bin_meta_transpose(const uint32_t* __re
 // bucket's slice of the table.  The bucket's pairs are one run in each round's slots (its row of the
 // bucket-major run table gives offset and length); a first pass over the row counts them (for the
 // fixed-point scale), the second
-// walks 16 rounds per wavefront at a time with every lane on one quad of pairs.  Zero pairs (the run
+// walks 16 rounds per wavefront at a time with every lane on one block of 8 pairs.  Zero pairs (the run
 // padding) are skipped.
 template <int F, int MODE>
 __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ meta,
-                                                     const uint16_t* __restrict__ pair_idx,
-                                                     const float* __restrict__ pair_val,
+                                                     const uint4* __restrict__ pbuf,
                                                      const float* __restrict__ cmax, BinApply ap) {
   extern __shared__ unsigned long long acc[];
   __shared__ float wmax[16];
@@ -532,9 +535,10 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
     if (v != 0.0f) atomicAdd(&acc[e * F + f], (unsigned long long)__double2ll_rn((double)v * scale));
   };
   if (mx > 0.0f) {
-    const int64_t slot_lvl = (int64_t)li * nr * grp.np;
+    const int64_t bpr = grp.np / PAD_RUN;  // pair blocks per round
+    const int64_t blk_lvl = (int64_t)li * nr * bpr;
     for (int r0 = wave * SEG; r0 < nr; r0 += 16 * SEG) {
-      // lanes 0..SEG-1 hold rounds r0 + lane: run offset and quad count, then the quads' running ends
+      // lanes 0..SEG-1 hold rounds r0 + lane: run offset and block count, then the blocks' running ends
       uint32_t m = 0;
       if (lane < SEG && r0 + lane < nr) m = mrow[r0 + lane];
       uint32_t incl = lane < SEG ? (m & 0xFFFFu) / PAD_RUN : 0u;
@@ -550,7 +554,7 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
         offs[t] = __builtin_amdgcn_readlane(m >> 16, t);
       }
       for (uint32_t q = (uint32_t)lane; q < ends[SEG - 1]; q += 64) {
-        // the run holding quad q: the last round whose running start is <= q
+        // the run holding block q: the last round whose running start is <= q
         uint32_t qb = 0, off = offs[0];
         int sg = 0;
 #pragma unroll
@@ -561,18 +565,20 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
             sg = t;
           }
         }
-        const int64_t i = slot_lvl + (int64_t)(r0 + sg) * grp.np + off + (int64_t)PAD_RUN * (q - qb);
-        const uint2 e4 = *reinterpret_cast<const uint2*>(pair_idx + i);
+        const uint4* src =
+            pbuf + (blk_lvl + (int64_t)(r0 + sg) * bpr + off / PAD_RUN + (q - qb)) * pair_block_words(F);
         float v[PAD_RUN * F];
 #pragma unroll
-        for (int qq = 0; qq < F; ++qq) {
-          const float4 t4 = *reinterpret_cast<const float4*>(pair_val + i * F + 4 * qq);
+        for (int qq = 0; qq < 2 * F; ++qq) {
+          const float4 t4 = *reinterpret_cast<const float4*>(src + qq);
           v[4 * qq] = t4.x;
           v[4 * qq + 1] = t4.y;
           v[4 * qq + 2] = t4.z;
           v[4 * qq + 3] = t4.w;
         }
-        const uint32_t ev[PAD_RUN] = {e4.x & 0xFFFFu, e4.x >> 16, e4.y & 0xFFFFu, e4.y >> 16};
+        const uint4 e8 = src[2 * F];
+        const uint32_t ev[PAD_RUN] = {e8.x & 0xFFFFu, e8.x >> 16, e8.y & 0xFFFFu, e8.y >> 16,
+                                      e8.z & 0xFFFFu, e8.z >> 16, e8.w & 0xFFFFu, e8.w >> 16};
 #pragma unroll
         for (int p = 0; p < PAD_RUN; ++p)
 #pragma unroll
@@ -781,11 +787,11 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
 #define FFN_BIN(FV, MV)                                                                                            \
   do {                                                                                                             \
     hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(emit_nt(FV)), lds_emit, st, c, src, n, grp, g, lay,   \
-                       lr, s.meta, s.cmax, s.pair_idx, s.pair_val);                                                \
+                       lr, s.meta, s.cmax, s.pairs);                                                               \
     hipLaunchKernelGGL(k_bin_meta_transpose, grid_tr, dim3(256), 0, st, s.meta, s.meta_t, grp.n_rounds,            \
                        grp.meta_stride);                                                                           \
     hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,         \
-                       s.meta_t, s.pair_idx, s.pair_val, s.cmax, ap);                                              \
+                       s.meta_t, s.pairs, s.cmax, ap);                                                             \
   } while (0)
 #define FFN_BIN_F(MV)                     \
   switch (c.F) {                          \

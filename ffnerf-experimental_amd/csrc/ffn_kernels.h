@@ -118,8 +118,7 @@ struct BinScratch {
   uint32_t* meta;      // [levels_per_group][n_rounds][max_nbl] each bucket's run in a round's slots: offset << 16 | length
   uint32_t* meta_t;    // the same, bucket-major: [levels_per_group][max_nbl][n_rounds]
   float* cmax;         // [levels_per_group][chunks] bound on every |value| of the chunk's pairs
-  uint16_t* pair_idx;  // [max_pairs] entry within the bucket
-  float* pair_val;     // [max_pairs * F]
+  uint4* pairs;        // [max_pairs / 8] blocks of 8 pairs: 8 * F fp32 values, then 8 u16 entries (in bucket)
 };
 
 struct BinApply {
