@@ -379,60 +379,68 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     for (int kb = 0; kb < KB0; ++kb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) a0b[kb][j] = (__bf16)a0v[4 * kb + j];
-    half4 hdh[ND][4];
-    {
-      floatx4 o[4];
-      fwd16<4, KB0>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), a0h, o, g, s, true);
+    // the network's activations: computed for the colours, dropped across the compositing (held there,
+    // they spilled to scratch), and computed again, bit-identically, for the backward
+    auto forward = [&](half4(&hdh)[ND][4], half4(&acinh)[2], bf16x4(&acb)[2], half4(&hch)[NC][4], float(&rgb_s)[3],
+                       float& dout0) {
+      {
+        floatx4 o[4];
+        fwd16<4, KB0>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), a0h, o, g, s, true);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) hdh[0][t] = to_half4(o[t]);
-    }
-    if constexpr (ND >= 2) {
-      floatx4 o[4];
-      fwd16<4, 4>(sWf + A::wf_off(FFN_WD_01), A::pf(FFN_WD_01), sB + A::b_off(FFN_WD_01), hdh[0], o, g, s, true);
+        for (int t = 0; t < 4; ++t) hdh[0][t] = to_half4(o[t]);
+      }
+      if constexpr (ND >= 2) {
+        floatx4 o[4];
+        fwd16<4, 4>(sWf + A::wf_off(FFN_WD_01), A::pf(FFN_WD_01), sB + A::b_off(FFN_WD_01), hdh[0], o, g, s, true);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) hdh[1][t] = to_half4(o[t]);
-    }
-    if constexpr (ND >= 3) {
-      floatx4 o[4];
-      fwd16<4, 4>(sWf + A::wf_off(FFN_WD_12), A::pf(FFN_WD_12), sB + A::b_off(FFN_WD_12), hdh[1], o, g, s, true);
+        for (int t = 0; t < 4; ++t) hdh[1][t] = to_half4(o[t]);
+      }
+      if constexpr (ND >= 3) {
+        floatx4 o[4];
+        fwd16<4, 4>(sWf + A::wf_off(FFN_WD_12), A::pf(FFN_WD_12), sB + A::b_off(FFN_WD_12), hdh[1], o, g, s, true);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) hdh[2][t] = to_half4(o[t]);
-    }
-    floatx4 dout[1];
-    fwd16<1, 4>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), hdh[ND - 1], dout, g, s,
-                false);
-    half4 acinh[2];
-    acinh[0] = to_half4(dout[0]);
-    floatx4 sh;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
-    acinh[1] = to_half4(sh);
-    const bf16x4 acb[2] = {to_bf16x4(dout[0]), to_bf16x4(sh)};  // colour-net input for its gradient
-    half4 hch[NC][4];
-    {
-      floatx4 o[4];
-      fwd16<4, 2>(sWf + A::wf_off(FFN_WC_IN), A::pf(FFN_WC_IN), sB + A::b_off(FFN_WC_IN), acinh, o, g, s, true);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) hch[0][t] = to_half4(o[t]);
-    }
-#pragma unroll
-    for (int i = 1; i < NC; ++i) {
-      const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
-      floatx4 o[4];
-      fwd16<4, 4>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), hch[i - 1], o, g, s, true);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) hch[i][t] = to_half4(o[t]);
-    }
-    float rgb_s[3];
-    {
-      floatx4 co[1];
-      fwd16<1, 4>(sWf + A::wf_off(FFN_WC_OUT), A::pf(FFN_WC_OUT), sB + A::b_off(FFN_WC_OUT), hch[NC - 1], co, g, s,
+        for (int t = 0; t < 4; ++t) hdh[2][t] = to_half4(o[t]);
+      }
+      floatx4 dout[1];
+      fwd16<1, 4>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), hdh[ND - 1], dout, g, s,
                   false);
-      rgb_s[0] = sigmoid_soft(co[0][0]);
-      rgb_s[1] = sigmoid_soft(co[0][1]);
-      rgb_s[2] = sigmoid_soft(co[0][2]);
+      acinh[0] = to_half4(dout[0]);
+      floatx4 sh;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
+      acinh[1] = to_half4(sh);
+      acb[0] = to_bf16x4(dout[0]);  // colour-net input, for its gradient
+      acb[1] = to_bf16x4(sh);
+      {
+        floatx4 o[4];
+        fwd16<4, 2>(sWf + A::wf_off(FFN_WC_IN), A::pf(FFN_WC_IN), sB + A::b_off(FFN_WC_IN), acinh, o, g, s, true);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) hch[0][t] = to_half4(o[t]);
+      }
+#pragma unroll
+      for (int i = 1; i < NC; ++i) {
+        const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
+        floatx4 o[4];
+        fwd16<4, 4>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), hch[i - 1], o, g, s, true);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) hch[i][t] = to_half4(o[t]);
+      }
+      {
+        floatx4 co[1];
+        fwd16<1, 4>(sWf + A::wf_off(FFN_WC_OUT), A::pf(FFN_WC_OUT), sB + A::b_off(FFN_WC_OUT), hch[NC - 1], co, g, s,
+                    false);
+        rgb_s[0] = sigmoid_soft(co[0][0]);
+        rgb_s[1] = sigmoid_soft(co[0][1]);
+        rgb_s[2] = sigmoid_soft(co[0][2]);
+      }
+      dout0 = dout[0][0];
+    };
+    float rgb_s[3], dout0;
+    {
+      half4 hdh[ND][4], acinh[2], hch[NC][4];
+      bf16x4 acb[2];
+      forward(hdh, acinh, acb, hch, rgb_s, dout0);
     }
-    const float dout0 = dout[0][0];
     if (g == 0) {
       float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
       if (dt_b <= 0.0f) sig = 0.0f;
@@ -446,6 +454,12 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     float dLds_j, dLdc_j[3];
     composite_tile(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
     if (!train) continue;
+    half4 hdh[ND][4], acinh[2], hch[NC][4];
+    bf16x4 acb[2];
+    {
+      float rgb_r[3], dout_r;
+      forward(hdh, acinh, acb, hch, rgb_r, dout_r);
+    }
 
     // ---- backward (fp16 chain with per-wavefront delta scaling, fp32 accumulation); every layer's deltas
     // and inputs go through the stash for the block's bf16 weight-gradient tiles (barrier, this wave's
