@@ -379,6 +379,9 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     for (int kb = 0; kb < KB0; ++kb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) a0b[kb][j] = (__bf16)a0v[4 * kb + j];
+    floatx4 sh;  // this lane's four SH inputs of the colour net
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
     // the network's activations: computed for the colours, dropped across the compositing (held there,
     // they spilled to scratch), and computed again, bit-identically, for the backward
     auto forward = [&](half4(&hdh)[ND][4], half4(&acinh)[2], bf16x4(&acb)[2], half4(&hch)[NC][4], float(&rgb_s)[3],
@@ -405,9 +408,6 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       fwd16<1, 4>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), hdh[ND - 1], dout, g, s,
                   false);
       acinh[0] = to_half4(dout[0]);
-      floatx4 sh;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
       acinh[1] = to_half4(sh);
       acb[0] = to_bf16x4(dout[0]);  // colour-net input, for its gradient
       acb[1] = to_bf16x4(sh);
