@@ -165,7 +165,9 @@ __device__ __forceinline__ void bwd16(const _Float16* __restrict__ Wt, int P, co
       const half4 a = *reinterpret_cast<const half4*>(Wt + (16 * t + s) * P + 16 * kb + 4 * g);
       acc[t] = mfma_f16(a, op[kb], acc[t]);
     }
-  const float inv = 1.0f / sc;  // a power of two: exact
+  int e;
+  frexpf(sc, &e);  // sc = 2^(e - 1)
+  const float inv = ldexpf(1.0f, 1 - e);  // 1 / sc, exactly
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll

@@ -149,7 +149,7 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
     const float gA = gr0 * (Tr * c0) + gr1 * (Tr * c1) + gr2 * (Tr * c2);
     const float gAlpha = gA - gT_next * Tr;
     const float dads = (dt_j > 0.0f) ? (dt_j * oma) : 0.0f;
-    const float regu = (dt_j > 0.0f) ? (5e-3f * dt_j / (float)(uint32_t)S) : 0.0f;
+    const float regu = (dt_j > 0.0f) ? (5e-3f * dt_j * ldexpf(1.0f, -a.log2S)) : 0.0f;  // / S, exactly
     dLds_j = gAlpha * dads + regu;
 
     if (wave == 0) {
@@ -267,12 +267,14 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
 __device__ __forceinline__ void output_deltas(float t_b, float dt_b, float Dhalf, float dLds, float dLdc0,
                                               float dLdc1, float dLdc2, const float (&rgb_s)[3], float dout0,
                                               float (&dco)[3], float& dd0) {
-  const float num = t_b * t_b + t_b * dt_b + (dt_b * dt_b / 3.0f);
-  const float den = Dhalf * Dhalf + Dhalf * dt_b + (dt_b * dt_b / 3.0f);
-  const float xg = t_b / fmaxf(Dhalf, 1.0e-12f);
+  // hardware reciprocal, exp2 and log2 (about 1 ulp each) in place of division and powf
+  const float num = t_b * t_b + t_b * dt_b + dt_b * dt_b * (1.0f / 3.0f);
+  const float den = Dhalf * Dhalf + Dhalf * dt_b + dt_b * dt_b * (1.0f / 3.0f);
+  const float xg = t_b * fast_rcp(fmaxf(Dhalf, 1.0e-12f));
   const float sg = (xg >= 1.0f) ? 0.0f : 1.0f;
-  const float gate = (1.0f - sg) * 1.0f + sg * powf(fmaxf(xg, 1.0e-12f), 0.2f);
-  const float f_vol = gate * num / fmaxf(den, 1.0e-12f);
+  const float pw = __builtin_amdgcn_exp2f(0.2f * __builtin_amdgcn_logf(fmaxf(xg, 1.0e-12f)));  // xg^0.2
+  const float gate = (1.0f - sg) * 1.0f + sg * pw;
+  const float f_vol = gate * num * fast_rcp(fmaxf(den, 1.0e-12f));
   dco[0] = (f_vol * dLdc0) * ((rgb_s[0] * (1.0f - rgb_s[0])) * 0.5f);
   dco[1] = (f_vol * dLdc1) * ((rgb_s[1] * (1.0f - rgb_s[1])) * 0.5f);
   dco[2] = (f_vol * dLdc2) * ((rgb_s[2] * (1.0f - rgb_s[2])) * 0.5f);
