@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void k_render_composite(const uint32_t* __rest
   uint32_t used = 0;
   for (uint32_t j = 0; j < cnt; ++j) {
     const uint32_t b = off + j;
-    const float alpha = 1.0f - expf(fminf(fmaxf(-sigma[b] * dt, -5.0f), 18.0f));
+    const float alpha = 1.0f - fast_exp(fminf(fmaxf(-sigma[b] * dt, -5.0f), 18.0f));
     const float w = T * alpha;
     C0 = C0 + w * rgb[3 * (size_t)b];
     C1 = C1 + w * rgb[3 * (size_t)b + 1];

@@ -107,7 +107,7 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
     const float sig_j = sSig[j];
     const float c0 = sRgb[3 * j], c1 = sRgb[3 * j + 1], c2 = sRgb[3 * j + 2];
     float alpha = 0.0f;
-    if (dt_j > 0.0f) alpha = 1.0f - expf(fminf(fmaxf(-sig_j * dt_j, -5.0f), 18.0f));
+    if (dt_j > 0.0f) alpha = 1.0f - fast_exp(fminf(fmaxf(-sig_j * dt_j, -5.0f), 18.0f));
     const float oma = 1.0f - alpha;
     Seg my;
     my.a = oma;
