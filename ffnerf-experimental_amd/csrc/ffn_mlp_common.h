@@ -85,6 +85,51 @@ __device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t til
   return L;
 }
 
+// The compositing's transmittance and colour prefix on DPP: Hillis-Steele steps inside 16-lane rows, then
+// across rows.  Segments are S consecutive lanes (one ray), S a power of two <= 64.  The combine order is
+// not the reference's work-group tree (the results agree to fp32 rounding: the prefix multiplies both
+// terms of every gradient alike), and the scan takes about a third of the tree's vector instructions.
+
+// v read from the lane CTRL selects (row masks ROW_MASK), `old` where the source lane is invalid
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_or(float old, float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ Seg seg_dpp(const Seg& v) {  // identity (1, 0) where the source is invalid
+  return Seg{dpp_or<CTRL, ROW_MASK>(1.0f, v.a), dpp_or<CTRL, ROW_MASK>(0.0f, v.v0),
+             dpp_or<CTRL, ROW_MASK>(0.0f, v.v1), dpp_or<CTRL, ROW_MASK>(0.0f, v.v2)};
+}
+
+// exclusive prefix of seg_combine over each segment (identity at its first lane); *total = the segment's
+// combination of all its lanes
+__device__ __forceinline__ Seg comp_seg_prefix(Seg v, int lane, int S, Seg* total) {
+  const int key = lane & 15 & (S - 1);  // position inside the segment's part of the row
+  if (S > 1) {
+    const Seg n = seg_combine(seg_dpp<0x111>(v), v);  // row_shr:1
+    if (key >= 1) v = n;
+  }
+  if (S > 2) {
+    const Seg n = seg_combine(seg_dpp<0x112>(v), v);
+    if (key >= 2) v = n;
+  }
+  if (S > 4) {
+    const Seg n = seg_combine(seg_dpp<0x114>(v), v);
+    if (key >= 4) v = n;
+  }
+  if (S > 8) {
+    const Seg n = seg_combine(seg_dpp<0x118>(v), v);
+    if (key >= 8) v = n;
+  }
+  if (S >= 32) v = seg_combine(seg_dpp<0x142, 0xA>(v), v);  // row_bcast:15 into rows 1 and 3
+  if (S >= 64) v = seg_combine(seg_dpp<0x143, 0xC>(v), v);  // row_bcast:31 into rows 2 and 3
+  *total = shfl_seg(v, (lane & ~(S - 1)) + S - 1);
+  Seg e = seg_dpp<0x138>(v);  // wave_shr:1
+  if ((lane & (S - 1)) == 0) e = Seg{1.0f, 0.0f, 0.0f, 0.0f};
+  return e;
+}
+
 // Compositing of the tile's rays on the wavefront's 64 lanes (S lanes per ray), the loss gradient, the
 // output colour (wavefront 0), taps (wavefront 0) and, on the tile's proposal wavefront, the occupancy
 // proposals of all its samples; returns dL/dsigma and dL/dc of lane j's sample.  sSig/sRgb hold
@@ -115,7 +160,7 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
     my.v1 = alpha * c1;
     my.v2 = alpha * c2;
     Seg tot;
-    const Seg pre = seg_scan_excl_seg(my, lid, S, base, &tot);
+    const Seg pre = comp_seg_prefix(my, lane, S, &tot);
     const float Tr = pre.a, T_final = tot.a;
     float bg[3];
     background(a, rj, train, bg);
@@ -136,6 +181,10 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
     Aff f;
     f.a = oma;
     f.b = gr0 * (alpha * c0) + gr1 * (alpha * c1) + gr2 * (alpha * c2);
+    // gT after sample j, in the reference's tree order: dL/dsigma is Tr (sum g c - gT_next) with the two
+    // terms nearly equal for many samples, so another combine order (rounding differences of 1e-7 in
+    // gT_next) moves it by up to 1e-2 of its range against the CPU restatement; the prefix above has no
+    // such cancellation
     const Aff f_rev = shfl_aff(f, base + (S - 1 - lid));  // lane k holds the element of sample S-1-k
     const Aff scn = seg_scan_excl_aff_rev(f_rev, lid, S, base);
     const int m = (lid <= S - 2) ? (S - 2 - lid) : 0;

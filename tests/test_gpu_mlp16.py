@@ -77,7 +77,7 @@ def _compare16(spec, p, rays, tg, S, sc, gh, ora):
         assert (err <= lim).mean() > 0.99, (k, (err <= lim).mean())
 
 
-@pytest.mark.parametrize("S", [64, 32, 16])
+@pytest.mark.parametrize("S", [64, 32, 16, 8, 1])
 def test_train_step_fp16_cfg0(gh, ora, S):
     print(f"[case] fp16 train step cfg0 S={S}", flush=True)
     spec = spec_cfg0(hash_opt=1, mlp_precision=1)

@@ -243,7 +243,7 @@ def _compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
     return m, o
 
 
-@pytest.mark.parametrize("S", [64, 32, 16])
+@pytest.mark.parametrize("S", [64, 32, 16, 8, 4, 2, 1])
 def test_train_step_cfg0_adam(gh, ora, S):
     print(f"[case] train step cfg0 adam S={S}", flush=True)
     spec = spec_cfg0(hash_opt=1)
