@@ -209,10 +209,15 @@ __device__ __forceinline__ uint32_t corner_entry(const LevelCell& lc, int cc, in
 // result is checked within a relative tolerance
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
+// log(1 + e^x): log1p of y = e^x as log(u) * y / (u - 1), u = 1 + y (exact for the rounded u, so accurate
+// for small y; Goldberg's method), on v_log_f32 and v_rcp_f32
 __device__ __forceinline__ float softplus(float x) {
   if (x > 20.0f) return x;
-  if (x < -20.0f) return fast_exp(x);
-  return log1pf(fast_exp(x));
+  const float y = fast_exp(x);
+  if (x < -20.0f) return y;
+  const float u = 1.0f + y;
+  if (u == 1.0f) return y;
+  return __builtin_amdgcn_logf(u) * 0.69314718055994531f * y * __builtin_amdgcn_rcpf(u - 1.0f);
 }
 // The MLP's per-sample activation and loss derivatives use the hardware reciprocal and reciprocal square
 // root (v_rcp_f32 / v_rsq_f32, about 1 ulp) instead of IEEE division: they feed outputs checked against
