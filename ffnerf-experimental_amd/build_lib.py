@@ -15,6 +15,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libffnerf_hip.so"
 ARCH = os.environ.get("FFN_OFFLOAD_ARCH", "gfx950")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["ffn_capi.hip", "ffn_sample.hip", "ffn_hash.hip", "ffn_mlp.hip", "ffn_optim.hip", "ffn_march.hip", "ffn_mlp16.hip", "ffn_batch.hip"]
 
@@ -29,7 +30,7 @@ FLAGS = [
 
 
 def build(verbose: bool = False, jobs: int = 8) -> Path:
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    hipcc = HIPCC
     objdir = HERE / "_build"
     objdir.mkdir(exist_ok=True)
     procs = []

@@ -103,7 +103,7 @@ enum { BIN_GRAD = 0, BIN_SGD = 1, BIN_ADAM = 2 };
 struct BinGroup {
   int level0, n_levels, log2_be, chunk, nblk;
   int n_rounds;     // emit rounds per level (the samples in runs of the emit round size)
-  int np;           // pair slots of one round (the stage size; a multiple of 4)
+  int np;           // pair slots of one round (the stage size; a multiple of 8)
   int meta_stride;  // entries per round in the run table (the group's largest bucket count)
   int nbl[FFN_MAX_LEVELS];             // buckets of each level of the group
   int bucket_rel[FFN_MAX_LEVELS + 1];  // first bucket of each level, relative to the group

@@ -98,6 +98,12 @@ def load(path: Path | str | None = None) -> C.CDLL:
     p = Path(path) if path else LIB_PATH
     if not p.exists():
         raise FfnError(f"{p} is not built; run __graft_entry__.build() (hipcc, gfx950)")
+    # torch first: its wheel bundles a HIP runtime that its libraries name "libamdhip64.so", while this
+    # library names the system's "libamdhip64.so.7".  Loaded first, this library would map the system runtime
+    # and torch would then map its own as a second one, so that torch's device pointers and streams would
+    # belong to another runtime than this library's launches.  With torch loaded, the soname
+    # "libamdhip64.so.7" resolves to torch's copy and the process has one runtime.
+    import torch  # noqa: F401
     lib = C.CDLL(str(p))
     lib.ffn_version.restype = C.c_int
     lib.ffn_last_error.restype = C.c_char_p

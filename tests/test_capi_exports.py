@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     import ffn_lib
     if not ffn_lib.LIB_PATH.exists():
         pytest.fail("libffnerf_hip.so is not built (run __graft_entry__.build())")
-    lib = ctypes.CDLL(str(ffn_lib.LIB_PATH))
+    lib = ffn_lib.load()
     for n in declared_functions():
         assert hasattr(lib, n), n
     assert sorted(ffn_lib.EXPORTS) == declared_functions()
@@ -44,3 +44,16 @@ def test_invalid_config_is_an_error_not_a_silent_return():
     cfg = fl.make_config(spec_cfg0(f_per_level=3))
     assert lib.ffn_create(ctypes.byref(cfg), ctypes.byref(h)) < 0
     assert b"f_per_level" in lib.ffn_last_error()
+
+
+def test_one_hip_runtime_per_process():
+    """Loading the library must leave one HIP runtime in the process: torch's (ffn_lib.load imports torch
+    before the library, whose own dependency would otherwise map the system runtime beside torch's)."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r); import ffn_lib; ffn_lib.load(); "
+            "print(sorted({l.split()[-1] for l in open('/proc/self/maps') if 'libamdhip64' in l}))")
+    out = subprocess.run([sys.executable, "-c", code % str(ROOT / "ffnerf-experimental_amd")],
+                         capture_output=True, text=True, check=True).stdout
+    maps = eval(out.strip().splitlines()[-1])
+    assert len(maps) == 1, maps
