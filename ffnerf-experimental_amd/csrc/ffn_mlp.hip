@@ -324,7 +324,7 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
   rgb_s[2] = sigmoid_soft(co[0][2]);
 }
 
-template <int LF, int ND, int NC, int FEAT>
+template <int LF, int ND, int NC, int FEAT, bool TAPS>
 __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_mlp(MlpArgs a) {
   using A = Arch<LF, ND, NC>;
   constexpr int KA = LF / 4;  // a0 values per lane (k-steps of the first layer)
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   __syncthreads();
 
   const float Dhalf = half_box_diagonal(c);
-  const bool taps = taps_requested(a);
+  constexpr bool taps = TAPS;
   const bool proposals = train && a.occ_strength > 0.0f;
 
   WaveGrad<1, 4> gc_out;
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     // ------------------------------------------------------------------
     // compositing on 64 lanes: lane j = sample j of the tile (every wave)
     float dLds_j, dLdc_j[3];
-    composite_tile(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+    composite_tile<TAPS>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
     if (!train) continue;
 
     // ------------------------------------------------------------------
@@ -517,28 +517,32 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC, int FEAT>
+template <int LF, int ND, int NC, int FEAT, bool TAPS>
 static hipError_t launch_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch<LF, ND, NC>;
   const size_t lds = sizeof(float) * (size_t)A::lds_floats(a.do_train != 0);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT, TAPS>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)(sizeof(float) * (size_t)A::lds_floats(false)));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp<LF, ND, NC, FEAT, TAPS>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
 template <int LF, int ND, int NC>
 static hipError_t launch_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
+  const bool taps = taps_requested(a);
   switch (a.c.F) {
-    case 1: return launch_f<LF, ND, NC, 1>(a, n_blocks, st);
-    case 2: return launch_f<LF, ND, NC, 2>(a, n_blocks, st);
-    case 4: return launch_f<LF, ND, NC, 4>(a, n_blocks, st);
+    case 1:
+      return taps ? launch_f<LF, ND, NC, 1, true>(a, n_blocks, st) : launch_f<LF, ND, NC, 1, false>(a, n_blocks, st);
+    case 2:
+      return taps ? launch_f<LF, ND, NC, 2, true>(a, n_blocks, st) : launch_f<LF, ND, NC, 2, false>(a, n_blocks, st);
+    case 4:
+      return taps ? launch_f<LF, ND, NC, 4, true>(a, n_blocks, st) : launch_f<LF, ND, NC, 4, false>(a, n_blocks, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -263,7 +263,7 @@ __device__ __forceinline__ void flush_layer16(float* __restrict__ dst, int O, in
   }
 }
 
-template <int LF, int ND, int NC, int FEAT>
+template <int LF, int ND, int NC, int FEAT, bool TAPS>
 __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_mlp16(MlpArgs a) {
   using A = Arch16<LF, ND, NC>;
   constexpr int KB0 = LF / 16;  // k-blocks of the first layer
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   __syncthreads();
 
   const float Dhalf = half_box_diagonal(c);
-  const bool taps = taps_requested(a);
+  constexpr bool taps = TAPS;
   const bool proposals = train && a.occ_strength > 0.0f;
   constexpr int PS = A::PS;
   WaveGrad16<1, 4> gc_out;
@@ -454,7 +454,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     __syncthreads();
 
     float dLds_j, dLdc_j[3];
-    composite_tile(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+    composite_tile<TAPS>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
     if (!train) continue;
     half4 hdh[ND][4], acinh[2], hch[NC][4];
     bf16x4 acb[2];
@@ -582,27 +582,31 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC, int FEAT>
+template <int LF, int ND, int NC, int FEAT, bool TAPS>
 static hipError_t launch16_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch16<LF, ND, NC>;
   const size_t lds = A::lds_bytes();
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT, TAPS>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT, TAPS>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
 template <int LF, int ND, int NC>
 static hipError_t launch16_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
+  const bool taps = taps_requested(a);
   switch (a.c.F) {
-    case 1: return launch16_f<LF, ND, NC, 1>(a, n_blocks, st);
-    case 2: return launch16_f<LF, ND, NC, 2>(a, n_blocks, st);
-    case 4: return launch16_f<LF, ND, NC, 4>(a, n_blocks, st);
+    case 1:
+      return taps ? launch16_f<LF, ND, NC, 1, true>(a, n_blocks, st) : launch16_f<LF, ND, NC, 1, false>(a, n_blocks, st);
+    case 2:
+      return taps ? launch16_f<LF, ND, NC, 2, true>(a, n_blocks, st) : launch16_f<LF, ND, NC, 2, false>(a, n_blocks, st);
+    case 4:
+      return taps ? launch16_f<LF, ND, NC, 4, true>(a, n_blocks, st) : launch16_f<LF, ND, NC, 4, false>(a, n_blocks, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -134,6 +134,7 @@ __device__ __forceinline__ Seg comp_seg_prefix(Seg v, int lane, int S, Seg* tota
 // output colour (wavefront 0), taps (wavefront 0) and, on the tile's proposal wavefront, the occupancy
 // proposals of all its samples; returns dL/dsigma and dL/dc of lane j's sample.  sSig/sRgb hold
 // sigma[64] and rgb[64][3] of the tile.
+template <bool TAPS>
 __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __restrict__ sSig,
                                                const float* __restrict__ sRgb, const CompLane& L, int lane,
                                                int wave, bool prop_wave, bool train, bool proposals, float Dhalf,
@@ -201,7 +202,7 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
     const float regu = (dt_j > 0.0f) ? (5e-3f * dt_j * ldexpf(1.0f, -a.log2S)) : 0.0f;  // / S, exactly
     dLds_j = gAlpha * dads + regu;
 
-    if (wave == 0) {
+    if (TAPS && wave == 0) {
       if (vj) {
         if (a.t_sigma) a.t_sigma[bj] = sig_j;
         if (a.t_rgb) {
@@ -372,7 +373,10 @@ __device__ __forceinline__ void empty_tile(const MlpArgs& a, const CompLane& L, 
   }
 }
 
-__device__ __forceinline__ bool taps_requested(const MlpArgs& a) {
+// Whether any per-sample tap is bound.  The MLP kernels take it as a template parameter (TAPS): without
+// taps the tap pointers and their tests leave the kernel, which keeps its scalar registers within the
+// hardware's limit (the test-only taps otherwise cost spills to vector-register lanes in every tile).
+__host__ __device__ __forceinline__ bool taps_requested(const MlpArgs& a) {
   return a.t_sigma || a.t_rgb || a.t_Tr || a.t_dLds || a.t_dLdc;
 }
 
