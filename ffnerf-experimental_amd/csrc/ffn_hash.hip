@@ -219,9 +219,9 @@ constexpr int MERGE_BLK = 8;
 __host__ __device__ constexpr int emit_nt(int F) { return F >= 4 ? 512 : 1024; }
 __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
 
-// LDS of k_bin_emit: counters and the round's run-table row (32-bit words), then the stage: values
-// [np][F] and entries [np]
-__host__ __device__ constexpr int emit_words(int nbl, int F) { return (4 * nbl + 4 + emit_nt(F) / 64 + 3) & ~3; }
+// LDS of k_bin_emit: counters, run offsets, the round totals and wavefront maxima (32-bit words), then the
+// stage: values [np][F] and entries [np]
+__host__ __device__ constexpr int emit_words(int nbl, int F) { return (3 * nbl + 4 + emit_nt(F) / 64 + 3) & ~3; }
 __host__ __device__ constexpr int emit_stage_pairs(int nbl, int F) {
   return 8 * emit_nt(F) + (PAD_RUN - 1) * (nbl < 8 * emit_nt(F) ? nbl : 8 * emit_nt(F));
 }
@@ -308,14 +308,35 @@ __device__ __forceinline__ void emit_prepare(const DevCfg& c, const PosSrc& src,
 // plus its row of the run table (each bucket's run offset and length in the slots).  Every write of the
 // pass is so a sequential stream, and no counting pass or global offsets are needed; the reduction reads
 // each bucket's runs from all rounds.
-// Order within a round: prepare the round's samples; issue the next round's loads; rank; barrier;
-// wavefront 0 scans the counts (stage offsets, the run-table row, the other counter buffer cleared for
-// the next round); barrier; stage the pairs; barrier; copy out the stage and the run-table row.  The pass
-// is bound by its vector ALU work (hashes, weights, the merge; a wave64 instruction occupies its SIMD four
-// cycles).  Measured slower at the benchmark shape: preparing the next round's samples before the
-// copy-out (6.2 against 5.5 ms), and splitting the wavefronts into loaders that never store and writers
-// that never load (7.3 ms: the loaders' ALU work per wavefront doubles).  The block also writes
+// Order within a round: prepare the round's samples; issue the next round's loads; rank; barrier; copy
+// out the previous round's stage (complete since that barrier) while wavefront 0 scans the counts (stage
+// offsets, the run-table row straight to memory, the other counter buffer cleared for the next round);
+// barrier; stage the pairs.  Two barriers a round: the copy-out fills the time the other wavefronts
+// waited for the scan, and the next round's first barrier orders the stage before its copy-out (with a
+// third barrier before an in-round copy-out the pass took 7.55 instead of 7.28 ms with its reduce).  The
+// wavefronts spend most of their time waiting (barriers, LDS returns); with a 1024-thread block that
+// needs 87 KB of LDS, one block per CU gives four wavefronts per SIMD.  Measured slower at the benchmark
+// shape: preparing the next round's samples before the copy-out (6.2 against 5.5 ms), and splitting the
+// wavefronts into loaders that never store and writers that never load (7.3 ms: the loaders' ALU work
+// per wavefront doubles).  The block also writes
 // cmax[level in group][chunk], a bound on every |value| of its pairs: the largest it staged.
+// Write one round's stage (total padded pairs) as a sequence of 16-byte words, lane t on word t: every
+// store instruction writes 1 KB contiguously (a lane per block would store at the block stride)
+template <int F>
+__device__ __forceinline__ void copy_out_round(uint4* __restrict__ pbuf, const BinGroup& grp, int li, int64_t round,
+                                               const float* st_val, const uint16_t* st_idx, uint32_t total,
+                                               int tid) {
+  constexpr int NT = emit_nt(F);
+  constexpr uint32_t W = pair_block_words(F);
+  const uint32_t nw = min(total, (uint32_t)grp.np) / PAD_RUN * W;  // the round's slots bound the copy
+  uint4* dst = pbuf + ((int64_t)li * grp.n_rounds + round) * (grp.np / PAD_RUN) * W;
+  for (uint32_t w = (uint32_t)tid; w < nw; w += NT) {
+    const uint32_t blk = w / W, k = w - blk * W;
+    dst[w] = k < 2 * F ? reinterpret_cast<const uint4*>(st_val)[blk * 2 * F + k]
+                       : reinterpret_cast<const uint4*>(st_idx)[blk];
+  }
+}
+
 template <int F, int MODE>
 __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                          const float* __restrict__ g, FeatLayout lay, float lr,
@@ -329,8 +350,7 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
   const int chunk = blockIdx.x;
   uint32_t* lcnt = sm;              // [2][nbl] pairs of the round per bucket
   uint32_t* loff = lcnt + 2 * nbl;  // [nbl] run offsets in the stage
-  uint32_t* lrow = loff + nbl;      // [nbl] the round's run-table row
-  uint32_t* total_s = lrow + nbl;   // [1] padded pairs of the round
+  uint32_t* total_s = loff + nbl;   // [2] padded pairs of the round, by round parity
   float* wmax = reinterpret_cast<float*>(total_s + 4);                          // [NT / 64]
   float* st_val = reinterpret_cast<float*>(sm + emit_words(nbl, F));            // [np][F]
   uint16_t* st_idx = reinterpret_cast<uint16_t*>(st_val + (size_t)grp.np * F);  // [np]
@@ -367,6 +387,9 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
       }
     }
     __syncthreads();
+    // the previous round's stage, complete since the barrier above, goes out while wavefront 0 scans
+    if (rb != b_begin) copy_out_round<F>(pbuf, grp, li, round - 1, st_val, st_idx, total_s[r ^ 1], tid);
+    uint32_t* mrow = meta + ((int64_t)li * grp.n_rounds + round) * grp.meta_stride;
     if (tid < 64) {
       // lane t scans counters [t * kb, t * kb + kb); nbl is a power of two, so from 256 buckets on every
       // lane holds a multiple of 4 of them, read and written 16 bytes at a time
@@ -391,7 +414,7 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
             const uint32_t n0 = pad_run(c4.x), n1 = pad_run(c4.y), n2 = pad_run(c4.z), n3 = pad_run(c4.w);
             const uint4 of = make_uint4(o, o + n0, o + n0 + n1, o + n0 + n1 + n2);
             *reinterpret_cast<uint4*>(loff + j0 + k) = of;
-            *reinterpret_cast<uint4*>(lrow + j0 + k) =
+            *reinterpret_cast<uint4*>(mrow + j0 + k) =
                 make_uint4((of.x << 16) | n0, (of.y << 16) | n1, (of.z << 16) | n2, (of.w << 16) | n3);
             *reinterpret_cast<uint4*>(nxt + j0 + k) = make_uint4(0u, 0u, 0u, 0u);
             o = of.w + n3;
@@ -401,13 +424,13 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
             const int j = j0 + k;
             const uint32_t cn = pad_run(cur[j]);
             loff[j] = o;
-            lrow[j] = (o << 16) | cn;
+            mrow[j] = (o << 16) | cn;
             nxt[j] = 0u;
             o += cn;
           }
         }
       }
-      if (lane == 63) total_s[0] = incl;
+      if (lane == 63) total_s[r] = incl;
     }
     __syncthreads();
     if (es.head) {
@@ -429,20 +452,10 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
         reinterpret_cast<V*>(st_val)[o + k] = FVec<F>::pack(z);
       }
     }
-    __syncthreads();
-    uint32_t* mrow = meta + ((int64_t)li * grp.n_rounds + round) * grp.meta_stride;
-    for (int j = tid; j < nbl; j += NT) mrow[j] = lrow[j];
-    // the round's blocks as one sequence of 16-byte words, lane t on word t: every store instruction
-    // writes 1 KB contiguously (a lane per block would store at the block stride)
-    constexpr uint32_t W = pair_block_words(F);
-    const uint32_t nw = min(total_s[0], (uint32_t)grp.np) / PAD_RUN * W;  // the round's slots bound the copy
-    uint4* dst = pbuf + ((int64_t)li * grp.n_rounds + round) * (grp.np / PAD_RUN) * W;
-    for (uint32_t w = (uint32_t)tid; w < nw; w += NT) {
-      const uint32_t blk = w / W, k = w - blk * W;
-      dst[w] = k < 2 * F ? reinterpret_cast<const uint4*>(st_val)[blk * 2 * F + k]
-                         : reinterpret_cast<const uint4*>(st_idx)[blk];
-    }
   }
+  // the last round's stage
+  __syncthreads();
+  if (b_end > b_begin) copy_out_round<F>(pbuf, grp, li, (b_end - 1) / NT, st_val, st_idx, total_s[r ^ 1], tid);
   bound = wave_max_nonneg(bound);
   if (lane == 0) wmax[tid >> 6] = bound;
   __syncthreads();
