@@ -78,11 +78,13 @@ struct Handle {
   uint32_t* host_total = nullptr;  // pinned
 };
 
+// Pair-buffer budget of the scatter: FFN_BIN_BUDGET_MB (MiB, clamped to [64, 2^22]), default 32 GiB
 size_t bin_budget_bytes() {
   const char* e = getenv("FFN_BIN_BUDGET_MB");
-  size_t mb = e ? (size_t)atoll(e) : (size_t)32768;
+  long long mb = e ? atoll(e) : 32768;
   if (mb < 64) mb = 64;
-  return mb << 20;
+  if (mb > (1ll << 22)) mb = 1ll << 22;
+  return (size_t)mb << 20;
 }
 
 // size the bucketed-scatter scratch for n samples and fill the views
