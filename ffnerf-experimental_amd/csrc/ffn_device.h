@@ -202,6 +202,24 @@ __device__ __forceinline__ uint32_t corner_entry(const LevelCell& lc, int cc, in
 }
 
 // ---------------------------------------------------------------------------
+// Streaming stores: the non-temporal hint (`nt`) lets the written lines leave the L2 first, so that data a
+// kernel writes once for a later pass does not evict what the kernel itself still gathers from the caches
+
+__device__ __forceinline__ void store_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void store_stream(float2* p, float2 v) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  __builtin_nontemporal_store(f2{v.x, v.y}, reinterpret_cast<f2*>(p));
+}
+__device__ __forceinline__ void store_stream(float4* p, float4 v) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(f4{v.x, v.y, v.z, v.w}, reinterpret_cast<f4*>(p));
+}
+__device__ __forceinline__ void store_stream(uint4* p, uint4 v) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(u4{v.x, v.y, v.z, v.w}, reinterpret_cast<u4*>(p));
+}
+
+// ---------------------------------------------------------------------------
 // activations (ffnerf_OG.cl:214-253) and SH degree 3 (ffnerf_OG.cl:572-602)
 
 // e^x as 2^(x log2 e) on v_exp_f32 instead of the range-reduced correctly rounded expf: relative error
