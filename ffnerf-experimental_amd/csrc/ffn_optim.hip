@@ -118,12 +118,49 @@ hipError_t launch_occ_decay(uint32_t* occ_in, uint32_t* occ_st, uint32_t n_words
 }
 
 // ---------------------------------------------------------------------------
-// MLP: sum the per-block gradient partials (fixed block order, so the result
-// is deterministic) and apply Adam; color layers step at lr_t * color_rel_lr.
+// MLP: sum the per-block gradient partials and apply Adam; color layers step at lr_t * color_rel_lr.
+// A block takes 64 parameters (one per lane, so every partial row is read coalesced) and its 16
+// wavefronts split the partials: wavefront w sums partials w, w + 16, ... into four accumulators taken in
+// turn, and wavefront 0 adds the 16 wavefront sums as a fixed pairwise tree.  The order of every addition
+// is fixed, so the result is deterministic.  (One thread per parameter walking all partials in sequence
+// was latency bound: 0.21 ms for 20 MB at the benchmark shape.)
+constexpr int ADAM_PB = 64;
+constexpr int ADAM_WAVES = 16;
 
-__global__ __launch_bounds__(256) void k_mlp_adam(MlpOptArgs a) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= a.lay.total) return;
+__global__ __launch_bounds__(64 * ADAM_WAVES) void k_mlp_adam(MlpOptArgs a) {
+  __shared__ float part[ADAM_WAVES][ADAM_PB];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = blockIdx.x * ADAM_PB + lane;
+  const bool in_range = i < a.lay.total;
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+  if (in_range) {
+    const int64_t stride = a.lay.total;
+    const float* p = a.partials + i;
+    int blk = w;
+    for (; blk + 3 * ADAM_WAVES < a.n_partials; blk += 4 * ADAM_WAVES) {
+      s0 += p[(int64_t)blk * stride];
+      s1 += p[(int64_t)(blk + ADAM_WAVES) * stride];
+      s2 += p[(int64_t)(blk + 2 * ADAM_WAVES) * stride];
+      s3 += p[(int64_t)(blk + 3 * ADAM_WAVES) * stride];
+    }
+    for (int q = 0; blk < a.n_partials; blk += ADAM_WAVES, ++q) {
+      const float x = p[(int64_t)blk * stride];
+      if (q == 0) s0 += x;
+      else if (q == 1) s1 += x;
+      else s2 += x;
+    }
+  }
+  part[w][lane] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (w != 0 || !in_range) return;
+  float v[ADAM_WAVES];
+#pragma unroll
+  for (int k = 0; k < ADAM_WAVES; ++k) v[k] = part[k][lane];
+#pragma unroll
+  for (int h = ADAM_WAVES / 2; h >= 1; h >>= 1)
+#pragma unroll
+    for (int k = 0; k < h; ++k) v[k] = v[k] + v[k + h];
+  const float g = v[0];
   int k = -1, j = 0;
   bool is_b = false;
   for (int s = 0; s < FFN_N_LAYERS; ++s) {
@@ -139,9 +176,6 @@ __global__ __launch_bounds__(256) void k_mlp_adam(MlpOptArgs a) {
     }
   }
   if (k < 0) return;
-  float g = 0.0f;
-  const int stride = a.lay.total;
-  for (int blk = 0; blk < a.n_partials; ++blk) g += a.partials[(int64_t)blk * stride + i];
   const float lr = (k >= FFN_WC_IN) ? a.lr_t * a.color_rel_lr : a.lr_t;
   float* P = is_b ? a.b[k] : a.W[k];
   float* Mm = is_b ? a.mb[k] : a.mW[k];
@@ -156,7 +190,8 @@ __global__ __launch_bounds__(256) void k_mlp_adam(MlpOptArgs a) {
 }
 
 hipError_t launch_mlp_adam(const MlpOptArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_mlp_adam, dim3((a.lay.total + 255) / 256), dim3(256), 0, st, a);
+  if (a.lay.total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_mlp_adam, dim3((a.lay.total + ADAM_PB - 1) / ADAM_PB), dim3(64 * ADAM_WAVES), 0, st, a);
   return hipGetLastError();
 }
 
