@@ -317,3 +317,29 @@ def test_render_mode(gh, ora):
     st = m.state()
     for k in ("table", "Wd_in", "Wc_out", "occ_in", "occ_st"):
         assert np.array_equal(st[k], p[k]), k
+
+
+@pytest.mark.parametrize("mlp_precision", [0, 1])
+def test_train_step_deterministic(gh, mlp_precision):
+    """Two runs of the same step from the same state leave bit-identical state and colours: the scatter
+    sums in fixed point (order-free), the MLP weight gradients are summed over the block partials in a
+    fixed order, and the occupancy proposals only take maxima.  The batch (cfg1 shapes, 4096 rays x 64
+    samples) spans many MLP blocks and scatter chunks, so any order-dependent sum would show."""
+    print(f"[case] train step determinism mlp_precision={mlp_precision}", flush=True)
+    spec = spec_cfg1(hash_opt=1, mlp_precision=mlp_precision)
+    p = random_params(spec, seed=101)
+    rays = look_at_rays(4096, spec, seed=102, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    runs = []
+    for _ in range(2):
+        m = gh.GpuModel(spec, p)
+        out, _ = m.train_step(rays, tg, 64, default_scalars(), taps=False)
+        out2, _ = m.train_step(rays, tg, 64, default_scalars(rng_seed=7), taps=False)
+        runs.append((out, out2, m.state()))
+        del m
+    (a1, a2, sa), (b1, b2, sb) = runs
+    assert np.array_equal(a1.view(np.uint32), b1.view(np.uint32))
+    assert np.array_equal(a2.view(np.uint32), b2.view(np.uint32))
+    assert set(sa) == set(sb)
+    for k in sa:
+        assert np.array_equal(sa[k].view(np.uint32), sb[k].view(np.uint32)), k
