@@ -337,7 +337,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   const int col = wave * 16 + s;              // this lane's stash column
   const bool train = a.do_train != 0;
   const DevCfg& c = a.c;
-  const int S = a.S, log2S = a.log2S;
+  const int log2S = a.log2S;
   const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
 
   stage_weights<LF, ND, NC>(sW, a.w, tid, 256);

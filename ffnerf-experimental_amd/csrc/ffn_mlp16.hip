@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
   const bool train = a.do_train != 0;
   const DevCfg& c = a.c;
-  const int S = a.S, log2S = a.log2S;
+  const int log2S = a.log2S;
   const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
 
   // weights: fp16 [out_pad][in] and bf16 [in][out_pad] (zero padding), fp32 biases
