@@ -343,3 +343,46 @@ def test_train_step_deterministic(gh, mlp_precision):
     assert set(sa) == set(sb)
     for k in sa:
         assert np.array_equal(sa[k].view(np.uint32), sb[k].view(np.uint32)), k
+
+
+def test_hash_scatter_full_size_adjoint(gh):
+    """The scatter at the benchmark's full size, 2^24 samples (2^18 rays x 64 points walking along each
+    ray, clamped into the box) on the cfg1/cfg2 table (16 levels of 2^19 entries): 16384 emit rounds per
+    level in one level group, which the oracle comparisons (tens of thousands of points) do not reach.
+    Size-independent properties of the linear map table -> encoding and its adjoint, summed in float64:
+      <encode(x; T), g> = <T, encode_bwd(x, g)>   (adjoint identity),
+      sum(encode_bwd(x, g)) = sum(g)              (the eight trilinear weights sum to one).
+    Positive T and g keep both sums free of cancellation, so fp32 rounding stays near 1e-7."""
+    import torch
+    import ffn_lib as fl
+    print("[case] hash scatter full size adjoint", flush=True)
+    spec = spec_cfg1(hash_opt=1)
+    p = random_params(spec, seed=111)
+    p["table"] = np.random.default_rng(112).uniform(0.5, 1.5, p["table"].shape).astype(np.float32)
+    m = gh.GpuModel(spec, p)
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(113)
+    n_rays, S = 1 << 18, 64
+    lo = torch.tensor(spec["box_min"], dtype=torch.float32, device=dev)
+    hi = torch.tensor(spec["box_max"], dtype=torch.float32, device=dev)
+    o = lo + (hi - lo) * (0.2 + 0.6 * torch.rand((n_rays, 1, 3), generator=gen, device=dev))
+    d = torch.randn((n_rays, 1, 3), generator=gen, device=dev)
+    d = d / d.norm(dim=2, keepdim=True)
+    t = torch.cumsum(0.02 * torch.rand((n_rays, S, 1), generator=gen, device=dev), dim=1)
+    x = torch.minimum(torch.maximum(o + t * d * (hi - lo), lo), hi).reshape(-1, 3).contiguous()
+    n = x.shape[0]
+    LF = spec["n_levels"] * spec["f_per_level"]
+    a0 = torch.empty((n, LF), dtype=torch.float32, device=dev)
+    fl.check(m.lib.ffn_hash_encode_fwd(m.h.h, fl.ptr(x), n, fl.ptr(a0), None, fl.stream_ptr()), "encode fwd")
+    g = 0.5 + torch.rand((n, LF), generator=gen, device=dev)
+    G = torch.zeros(table_floats(spec), dtype=torch.float32, device=dev)
+    fl.check(m.lib.ffn_hash_encode_bwd(m.h.h, fl.ptr(x), fl.ptr(g), n, fl.ptr(G), fl.stream_ptr()), "encode bwd")
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(G).all())
+    lhs = sum(float((a0[i:i + (1 << 22)].double() * g[i:i + (1 << 22)].double()).sum()) for i in range(0, n, 1 << 22))
+    rhs = float((m.t["table"].double() * G.double()).sum())
+    gsum = sum(float(g[i:i + (1 << 22)].double().sum()) for i in range(0, n, 1 << 22))
+    Gsum = float(G.double().sum())
+    print(f"adjoint rel {abs(lhs - rhs) / lhs:.2e}  weight-sum rel {abs(Gsum - gsum) / gsum:.2e}", flush=True)
+    assert abs(lhs - rhs) <= 2e-6 * lhs
+    assert abs(Gsum - gsum) <= 2e-6 * gsum
