@@ -135,6 +135,19 @@ def test_hash_backward_shapes(gh, ora, case):
         assert np.array_equal(a0_g.view(np.uint32), a0_o.view(np.uint32))
 
 
+def test_hash_backward_too_wide_is_an_error(gh):
+    """F = 4 with 2^22-entry levels needs an emit stage larger than a CU's LDS: the scatter refuses the
+    shape before launching its kernels (an error with a message, no silent return)."""
+    import ffn_lib as fl
+    print("[case] hash bwd too wide", flush=True)
+    spec = spec_cfg0(n_levels=2, f_per_level=4, log2_T=[22, 22], res=[256.0, 2048.0])
+    m = gh.GpuModel(spec, random_params(spec, seed=35))
+    x = np.random.default_rng(36).uniform(0.0, 1.0, (1000, 3)).astype(np.float32)
+    g = np.ones((1000, 8), np.float32)
+    with pytest.raises(fl.FfnError, match="ffn_hash_encode_bwd"):
+        m.encode_bwd(x, g, table_floats(spec))
+
+
 def test_occ_decay_bit_exact(gh, ora):
     import ctypes
     import torch
