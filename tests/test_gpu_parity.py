@@ -399,3 +399,26 @@ def test_hash_scatter_full_size_adjoint(gh):
     print(f"adjoint rel {abs(lhs - rhs) / lhs:.2e}  weight-sum rel {abs(Gsum - gsum) / gsum:.2e}", flush=True)
     assert abs(lhs - rhs) <= 2e-6 * lhs
     assert abs(Gsum - gsum) <= 2e-6 * gsum
+
+
+def test_scatter_level_groups_bit_identical(gh, monkeypatch):
+    """A pair budget smaller than one step's pairs splits the levels into groups (one emit and one reduce
+    launch per group, the pair buffer reused).  At FFN_BIN_BUDGET_MB=64, 2^18 points on 16 levels of 2^19
+    entries need 256 rounds x 8640 slots x 10 B = 22 MB per level, so three levels per group and six
+    groups; the per-level fixed-point sums do not depend on the grouping, so the table gradient must equal
+    the single-group one bit for bit."""
+    print("[case] scatter level groups", flush=True)
+    spec = spec_cfg1(hash_opt=1)
+    p = random_params(spec, seed=121)
+    rng = np.random.default_rng(122)
+    lo, hi = np.array(spec["box_min"]), np.array(spec["box_max"])
+    x = _ray_walk_points(rng, lo, hi, 4096, 64)
+    LF = spec["n_levels"] * spec["f_per_level"]
+    g = rng.normal(size=(x.shape[0], LF)).astype(np.float32)
+    m = gh.GpuModel(spec, p)
+    one_group = m.encode_bwd(x, g, table_floats(spec))
+    monkeypatch.setenv("FFN_BIN_BUDGET_MB", "64")
+    grouped = m.encode_bwd(x, g, table_floats(spec))
+    monkeypatch.delenv("FFN_BIN_BUDGET_MB")
+    assert np.abs(one_group).max() > 0
+    assert np.array_equal(one_group.view(np.uint32), grouped.view(np.uint32))
