@@ -422,3 +422,28 @@ def test_scatter_level_groups_bit_identical(gh, monkeypatch):
     monkeypatch.delenv("FFN_BIN_BUDGET_MB")
     assert np.abs(one_group).max() > 0
     assert np.array_equal(one_group.view(np.uint32), grouped.view(np.uint32))
+
+
+def test_stage_times(gh):
+    """ffn_set_profiling / ffn_stage_times (the reference's profiling queue and event_ms,
+    ffnerf_tools.py:11-13,127-138): with profiling on, each stage of a training step is bracketed by
+    events on the caller's stream; two steps give two launches of every stage, positive times, and a reset
+    empties the record."""
+    print("[case] stage times", flush=True)
+    spec = spec_cfg0(hash_opt=1)
+    p = random_params(spec, seed=131)
+    rays = look_at_rays(256, spec, seed=132, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    m = gh.GpuModel(spec, p)
+    m.h.set_profiling(True)
+    m.h.stage_times(reset=True)
+    for _ in range(2):
+        m.train_step(rays, tg, 64, default_scalars(), taps=False)
+    st = m.h.stage_times(reset=True)
+    for s in ("sample", "hash_fwd", "mlp", "hash_bwd", "mlp_adam"):
+        assert st[s][1] == 2 and st[s][0] > 0.0, (s, st[s])
+    assert st["table_adam"][1] == 0  # the table Adam is fused into the scatter's reduce
+    assert all(n == 0 for _, n in m.h.stage_times(reset=True).values())
+    m.h.set_profiling(False)
+    m.train_step(rays, tg, 64, default_scalars(), taps=False)
+    assert all(n == 0 for _, n in m.h.stage_times(reset=True).values())
