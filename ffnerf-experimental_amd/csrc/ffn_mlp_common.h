@@ -231,7 +231,17 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
         const float t_last = __shfl(t_j, base + last), T_last = __shfl(Tr, base + last);
         const float t_nx = __shfl(t_j, base + nsrc), T_nx = __shfl(Tr, base + nsrc);
         const bool is_rep = (segmask >> lid) & 1ull;
-        if (vj && is_rep && dt_j > 0.0f) {
+        // Early out, exact: transmittance never rises along the ray, so the run's predicted absorption
+        // pred = 1 - T_exit / T_enter below is at most (T_prev - T_next) / T_prev.  When 16 times that bound
+        // cannot exceed the smallest level in the cell's occupancy word, no subcell of the cell can take a
+        // proposal, and the lane would neither draw nor write.  The scan's products may exceed monotonicity
+        // by a few ulps (< 1e-6 relative); the 1e-4 margin covers that, so only such lanes are skipped.
+        uint32_t wmin = 15u;  // smallest nibble of the word (its subcells' level - 1)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) wmin = min(wmin, (L.occ_word >> (4 * q)) & 0xFu);
+        const float T_nb = nxt < S ? T_nx : T_final;
+        const bool may_rise = 16.0f * (T_prev - T_nb) > (float)(wmin + 1u) * T_prev * (1.0f - 1.0e-4f);
+        if (vj && is_rep && dt_j > 0.0f && may_rise) {
           const float4 ro = a.rays[2 * rj], rdv = a.rays[2 * rj + 1];
           const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
           const int G = c.G;

@@ -300,6 +300,30 @@ def test_train_step_empty_grid_proposals(gh, ora):
     assert not np.array_equal(o.p["occ_st"], p["occ_st"])
 
 
+def test_train_step_many_proposals(gh, ora):
+    """Occupancy levels 1..8 in every subcell and a dense field (density bias 8), so that many runs absorb
+    enough light to propose: the proposals (including the kernels' exact early out for runs whose
+    transmittance drop cannot exceed the cell's smallest level) must match the oracle, which evaluates
+    every run in full."""
+    print("[case] train step many proposals", flush=True)
+    spec = spec_cfg0(hash_opt=1)
+    p = random_params(spec, seed=151)
+    rng = np.random.default_rng(152)
+    nib = rng.integers(0, 8, (p["occ_in"].size, 8)).astype(np.uint32)
+    occ = np.zeros(p["occ_in"].size, np.uint32)
+    for q in range(8):
+        occ |= nib[:, q] << np.uint32(4 * q)
+    p["occ_in"][:] = occ.reshape(p["occ_in"].shape)
+    p["occ_st"][:] = p["occ_in"]
+    p["bd_out"][0] = 8.0
+    rays = look_at_rays(256, spec, seed=153, miss_frac=0.0)
+    tg = sphere_targets(rays, spec)
+    m, o = _compare_step(spec, p, rays, tg, 64, default_scalars(), gh, ora)
+    changed = int((o.p["occ_st"] != p["occ_st"]).sum())
+    print(f"occupancy words raised by the oracle's proposals: {changed}", flush=True)
+    assert changed > 50
+
+
 @pytest.mark.parametrize("bg", [1, 2])
 def test_train_step_backgrounds_and_sgd(gh, ora, bg):
     print(f"[case] train step sgd bg={bg}", flush=True)
