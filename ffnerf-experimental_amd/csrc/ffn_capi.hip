@@ -426,6 +426,9 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     a.t_sigma = taps->sigma;
     a.t_rgb = taps->rgb;
     a.t_Tr = taps->Tr;
+    a.t_Tfinal = taps->T_final;
+    a.t_relu = taps->relu;
+    a.t_color = (float4*)taps->color;
     a.t_dLds = taps->dL_dsigma;
     a.t_dLdc = taps->dL_dc;
   }

@@ -68,6 +68,8 @@ struct MlpPtrs {
   const float* b[FFN_N_LAYERS];
 };
 
+constexpr int RELU_WORDS = 14;  // ReLU-branch tap words per sample: two per hidden layer slot (3 density, 4 colour)
+
 struct MlpArgs {
   DevCfg c;
   MlpPtrs w;
@@ -93,6 +95,9 @@ struct MlpArgs {
   float* t_sigma;
   float* t_rgb;
   float* t_Tr;
+  float* t_Tfinal;
+  uint32_t* t_relu;  // [N][RELU_WORDS]
+  float4* t_color;   // [num_rays] colour before clamping
   float* t_dLds;
   float* t_dLdc;
 };

@@ -396,6 +396,15 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     floatx4 hc[NC][4];
     float rgb_s[3];
     mlp_fwd_tile<LF, ND, NC>(sW, a0r, dirv, a.sh_mult, g, s, hd, acin, hc, rgb_s);
+    if constexpr (TAPS) {
+      if (a.t_relu) {
+        uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
+#pragma unroll
+        for (int i = 0; i < ND; ++i) tap_relu(rec, i, hd[i], g);
+#pragma unroll
+        for (int i = 0; i < NC; ++i) tap_relu(rec, 3 + i, hc[i], g);
+      }
+    }
     const float dout0 = acin[0][0];
     if (g == 0) {
       float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));

@@ -442,6 +442,15 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       half4 hdh[ND][4], acinh[2], hch[NC][4];
       bf16x4 acb[2];
       forward(hdh, acinh, acb, hch, rgb_s, dout0);
+      if constexpr (TAPS) {
+        if (a.t_relu) {
+          uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
+#pragma unroll
+          for (int i = 0; i < ND; ++i) tap_relu(rec, i, hdh[i], g);
+#pragma unroll
+          for (int i = 0; i < NC; ++i) tap_relu(rec, 3 + i, hch[i], g);
+        }
+      }
     }
     if (g == 0) {
       float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));

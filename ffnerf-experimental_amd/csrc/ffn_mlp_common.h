@@ -211,6 +211,8 @@ __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __
           a.t_rgb[3 * bj + 2] = c2;
         }
         if (a.t_Tr) a.t_Tr[bj] = Tr;
+        if (a.t_Tfinal && lid == 0) a.t_Tfinal[rj] = T_final;
+        if (a.t_color && lid == 0) a.t_color[rj] = make_float4(Cf0, Cf1, Cf2, 0.0f);
         if (a.t_dLds) a.t_dLds[bj] = dLds_j;
         if (a.t_dLdc) {
           a.t_dLdc[3 * bj] = dLdc_j[0];
@@ -387,7 +389,33 @@ __device__ __forceinline__ void empty_tile(const MlpArgs& a, const CompLane& L, 
 // taps the tap pointers and their tests leave the kernel, which keeps its scalar registers within the
 // hardware's limit (the test-only taps otherwise cost spills to vector-register lanes in every tile).
 __host__ __device__ __forceinline__ bool taps_requested(const MlpArgs& a) {
-  return a.t_sigma || a.t_rgb || a.t_Tr || a.t_dLds || a.t_dLdc;
+  return a.t_sigma || a.t_rgb || a.t_Tr || a.t_Tfinal || a.t_dLds || a.t_dLdc || a.t_relu || a.t_color;
+}
+
+// ReLU-branch tap of hidden layer slot h (0..2 density, 3..6 colour) for this lane's sample: bit n of the
+// record's words 2h, 2h + 1 is set when unit n's activation (as the backward reads it) is positive.  Lane
+// (g, s) holds units 16t + 4g + r; the four lane groups of a sample combine their bits.  Every lane of the
+// wavefront must call this (rec may be NULL for lanes without a sample).
+template <typename V>
+__device__ __forceinline__ void tap_relu(uint32_t* rec, int h, const V (&act)[4], int g) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t on = (float)act[t][r] > 0.0f ? 1u : 0u;
+      const int n = 16 * t + 4 * g + r;
+      if (t < 2) lo |= on << (n & 31);
+      else hi |= on << (n & 31);
+    }
+  lo |= __shfl_xor(lo, 16);
+  lo |= __shfl_xor(lo, 32);
+  hi |= __shfl_xor(hi, 16);
+  hi |= __shfl_xor(hi, 32);
+  if (rec && g == 0) {
+    rec[2 * h] = lo;
+    rec[2 * h + 1] = hi;
+  }
 }
 
 __device__ __forceinline__ float half_box_diagonal(const DevCfg& c) {

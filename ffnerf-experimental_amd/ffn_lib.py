@@ -25,6 +25,7 @@ EXPORTS = [
     "ffn_occ_decay", "ffn_sample", "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam",
     "ffn_set_profiling", "ffn_stage_times", "ffn_occ_bitfield", "ffn_march", "ffn_render", "ffn_make_batch",
 ]
+RELU_WORDS = 14  # ReLU-branch tap words per sample
 STAGES = ["sample", "hash_fwd", "mlp", "hash_bwd", "mlp_adam", "table_adam"]
 
 _vp = C.c_void_p
@@ -65,7 +66,7 @@ class FfnTaps(C.Structure):
     _fields_ = [
         ("Ts", _vp), ("DTs", _vp), ("flags", _vp), ("a0", _vp), ("sigma", _vp), ("rgb", _vp), ("Tr", _vp),
         ("dL_dsigma", _vp), ("dL_dc", _vp), ("dL_da0", _vp), ("gW", _vp * N_LAYERS), ("gb", _vp * N_LAYERS),
-        ("g_table", _vp),
+        ("g_table", _vp), ("T_final", _vp), ("relu", _vp), ("color", _vp),
     ]
 
 

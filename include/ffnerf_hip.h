@@ -116,6 +116,11 @@ typedef struct ffn_taps {
   float* gW[FFN_N_LAYERS];  /* summed weight gradients (before Adam) */
   float* gb[FFN_N_LAYERS];
   float* g_table;       /* table gradient (FFN_HASH_ADAM), before Adam */
+  float* T_final;       /* [num_rays] transmittance after each ray's last sample */
+  uint32_t* relu;       /* [N][14] ReLU branches: words 2h, 2h+1 hold bit n set when hidden unit n of hidden
+                           layer h (h = 0..2 density, 3..6 colour) has a positive activation */
+  float* color;         /* [num_rays][4] composited colour before clamping, background included (the
+                           photometric loss's input), 0 */
 } ffn_taps;
 
 int ffn_version(void);

@@ -45,6 +45,7 @@
 #define ORA_C_OUT 3
 #define ORA_S_MAX 64
 #define ORA_MAX_LEVELS 32
+#define ORA_RELU_WORDS 14
 
 /* layer slots, in the reference's kernel-argument order (ffnerf_tools.py:1210-1232) */
 enum { L_WD_IN = 0, L_WD_01, L_WD_12, L_WD_OUT, L_WC_IN, L_WC_01, L_WC_12, L_WC_23, L_WC_OUT, L_COUNT };
@@ -105,6 +106,14 @@ typedef struct {
   float* gW[L_COUNT]; /* weight gradients (sum over samples), sized like W */
   float* gb[L_COUNT];
   float* g_table;     /* table gradient (hash_opt == 1), sized like table */
+  /* ReLU branches, ORA_RELU_WORDS words per sample: words 2h, 2h+1 hold bit n of hidden unit n of hidden
+   * layer h (h = 0..2 density, 3..6 colour) */
+  const uint32_t* relu_in; /* [N*S][14] input: the branch each unit takes (another implementation's) */
+  uint32_t* relu_out;      /* [N*S][14] output: pre-activation > 0 as this restatement computes it */
+  float* preact;           /* [N*S][7][64] output: hidden pre-activations */
+  /* the composited colour before clamping, background included: the photometric loss's input */
+  const float* C_in;       /* [N][4] input: evaluate the loss gradient at this colour (another implementation's) */
+  float* C_out;            /* [N][4] output: the colour as composited here */
 } ora_debug;
 
 /* ------------------------------------------------------------------ */
@@ -663,25 +672,49 @@ typedef struct {
   float hd[3][ORA_M];       /* density hidden activations */
   float acin[ORA_C_IN];     /* [dout(16), SH*mult(16)] */
   float hc[4][ORA_M];       /* color hidden activations */
+  uint64_t on[7];           /* ReLU branch of every hidden unit (h = 0..2 density, 3..6 colour) */
+  uint64_t own[7];          /* pre-activation > 0, as computed here */
+  float pre[7][ORA_M];      /* hidden pre-activations */
   float sigma;
   float rgb[3];
 } mlp_state;
 
-static void mlp_forward(const ora_cfg* c, const ora_params* P, const float* dir, float sh_mult, mlp_state* st) {
+/* hidden layer h: pre-activations from fc, then the ReLU.  Unit n passes its pre-activation when its
+ * branch is on: the branch is pre > 0 (ffnerf_OG.cl:754-791), or, when `force` is given, bit n of the
+ * layer's words there (another implementation's decision; that unit's value is then passed unclamped). */
+static void hidden(mlp_state* st, int h, float* out, const float* in, int in_dim, const float* W, const float* b,
+                   const uint32_t* force) {
+  fc(st->pre[h], in, in_dim, ORA_M, W, b, 0);
+  uint64_t own = 0, on;
+  for (int n = 0; n < ORA_M; ++n)
+    if (st->pre[h][n] > 0.0f) own |= 1ull << n;
+  on = force ? ((uint64_t)force[2 * h] | ((uint64_t)force[2 * h + 1] << 32)) : own;
+  for (int n = 0; n < ORA_M; ++n) out[n] = ((on >> n) & 1ull) ? st->pre[h][n] : 0.0f;
+  st->own[h] = own;
+  st->on[h] = on;
+}
+
+static int unit_on(const mlp_state* st, int h, int n) { return (int)((st->on[h] >> n) & 1ull); }
+
+static void mlp_forward(const ora_cfg* c, const ora_params* P, const float* dir, float sh_mult, mlp_state* st,
+                        const uint32_t* force) {
   const int LF = c->n_levels * c->f_per_level;
   const int nd = c->nd, nc = c->nc;
-  fc(st->hd[0], st->a0, LF, ORA_M, P->W[L_WD_IN], P->b[L_WD_IN], 1);
-  if (nd >= 2) fc(st->hd[1], st->hd[0], ORA_M, ORA_M, P->W[L_WD_01], P->b[L_WD_01], 1);
-  if (nd >= 3) fc(st->hd[2], st->hd[1], ORA_M, ORA_M, P->W[L_WD_12], P->b[L_WD_12], 1);
+  memset(st->on, 0, sizeof(st->on));
+  memset(st->own, 0, sizeof(st->own));
+  memset(st->pre, 0, sizeof(st->pre));
+  hidden(st, 0, st->hd[0], st->a0, LF, P->W[L_WD_IN], P->b[L_WD_IN], force);
+  if (nd >= 2) hidden(st, 1, st->hd[1], st->hd[0], ORA_M, P->W[L_WD_01], P->b[L_WD_01], force);
+  if (nd >= 3) hidden(st, 2, st->hd[2], st->hd[1], ORA_M, P->W[L_WD_12], P->b[L_WD_12], force);
   float dout[ORA_D_OUT];
   fc(dout, st->hd[nd - 1], ORA_M, ORA_D_OUT, P->W[L_WD_OUT], P->b[L_WD_OUT], 0);
   for (int i = 0; i < ORA_D_OUT; ++i) st->acin[i] = dout[i];
   st->sigma = softplus(fminf(fmaxf(dout[0], -10.0f), 10.0f));
   ora_sh_encode(dir, st->acin + ORA_D_OUT);
   for (int i = 0; i < ORA_L_DIR; ++i) st->acin[ORA_D_OUT + i] *= sh_mult;
-  fc(st->hc[0], st->acin, ORA_C_IN, ORA_M, P->W[L_WC_IN], P->b[L_WC_IN], 1);
+  hidden(st, 3, st->hc[0], st->acin, ORA_C_IN, P->W[L_WC_IN], P->b[L_WC_IN], force);
   static const int slot[4] = {0, L_WC_01, L_WC_12, L_WC_23};
-  for (int k = 1; k < nc; ++k) fc(st->hc[k], st->hc[k - 1], ORA_M, ORA_M, P->W[slot[k]], P->b[slot[k]], 1);
+  for (int k = 1; k < nc; ++k) hidden(st, 3 + k, st->hc[k], st->hc[k - 1], ORA_M, P->W[slot[k]], P->b[slot[k]], force);
   float cout[ORA_C_OUT];
   fc(cout, st->hc[nc - 1], ORA_M, ORA_C_OUT, P->W[L_WC_OUT], P->b[L_WC_OUT], 0);
   for (int i = 0; i < 3; ++i) st->rgb[i] = sigmoid_soft(cout[i]);
@@ -693,7 +726,7 @@ void ora_mlp_forward(const ora_cfg* c, const ora_params* P, const float* a0, con
   mlp_state st;
   const int LF = c->n_levels * c->f_per_level;
   memcpy(st.a0, a0, sizeof(float) * LF);
-  mlp_forward(c, P, dir, sh_mult, &st);
+  mlp_forward(c, P, dir, sh_mult, &st, NULL);
   *sigma = st.sigma;
   for (int i = 0; i < 3; ++i) rgb[i] = st.rgb[i];
   if (dout) memcpy(dout, st.acin, sizeof(float) * ORA_D_OUT);
@@ -829,12 +862,29 @@ void ora_occ_propose_ray(const ora_cfg* c, const float* ray, uint32_t ray_id, in
   }
 }
 
+/* the proposals of a batch of rays (rays in order) from given per-sample times, transmittances and run
+ * flags: the step's proposal pass (ffnerf_OG.cl:1640-1821) fed with another implementation's compositing
+ * results, so that the integer outcome can be compared word for word */
+void ora_occ_propose_batch(const ora_cfg* c, const float* rays, int32_t num_rays, int S, uint32_t seed,
+                           const float* Ts, const float* DTs, const float* Tr, const float* T_final,
+                           const uint32_t* flags, const uint32_t* occ_in, uint32_t* occ_st) {
+  for (int32_t r = 0; r < num_rays; ++r) {
+    const int64_t b0 = (int64_t)r * S;
+    ora_occ_propose_ray(c, rays + 8 * (int64_t)r, (uint32_t)r, S, seed, Ts + b0, DTs + b0, Tr + b0, T_final[r],
+                        flags + 2 * (int64_t)r, occ_in, occ_st);
+  }
+}
+
 /* ------------------------------------------------------------------ */
 /* compositing, loss gradient and its backward of one ray (ffnerf_OG.cl:1505-1634) */
 
-void ora_composite_ray(const ora_cfg* c, uint32_t ray_id, int S, uint32_t seed, int do_train,
-                       const float* sigma, const float* rgb, const float* DTs, const float* target, float* out4,
-                       float* Tr, float* T_final_out, float* dL_dc, float* dL_dsigma) {
+/* C_force (optional): the loss gradient is evaluated at this colour instead of the composited one (the
+ * Charbonnier derivative has slope up to 1/eps = 1000 near a zero residual, so comparisons with another
+ * implementation feed it that implementation's colour); C_own (optional) receives the composited colour */
+static void composite_ray(const ora_cfg* c, uint32_t ray_id, int S, uint32_t seed, int do_train,
+                          const float* sigma, const float* rgb, const float* DTs, const float* target, float* out4,
+                          float* Tr, float* T_final_out, float* dL_dc, float* dL_dsigma, const float* C_force,
+                          float* C_own) {
   const uint32_t WG = (uint32_t)S;
   Seg segs[ORA_S_MAX], total;
   float alpha[ORA_S_MAX];
@@ -869,8 +919,10 @@ void ora_composite_ray(const ora_cfg* c, uint32_t ray_id, int S, uint32_t seed, 
   for (int k = 0; k < 3; ++k) {
     float Cf = total.v[k] + T_final * bg[k];
     out4[k] = fminf(fmaxf(Cf, 0.0f), 1.0f);
-    gr[k] = charbonnier_prime(Cf - target[k]);
+    if (C_own) C_own[k] = Cf;
+    gr[k] = charbonnier_prime((C_force ? C_force[k] : Cf) - target[k]);
   }
+  if (C_own) C_own[3] = 0.0f;
   out4[3] = 0.0f;
   float gT_end = gr[0] * bg[0] + gr[1] * bg[1] + gr[2] * bg[2];
 
@@ -905,6 +957,13 @@ void ora_composite_ray(const ora_cfg* c, uint32_t ray_id, int S, uint32_t seed, 
     float regu = (dt_s > 0.0f) ? (5e-3f * dt_s / (float)(uint32_t)S) : 0.0f;
     dL_dsigma[lid] = gAlpha * dads + regu;
   }
+}
+
+void ora_composite_ray(const ora_cfg* c, uint32_t ray_id, int S, uint32_t seed, int do_train,
+                       const float* sigma, const float* rgb, const float* DTs, const float* target, float* out4,
+                       float* Tr, float* T_final_out, float* dL_dc, float* dL_dsigma) {
+  composite_ray(c, ray_id, S, seed, do_train, sigma, rgb, DTs, target, out4, Tr, T_final_out, dL_dc, dL_dsigma, NULL,
+                NULL);
 }
 
 /* ------------------------------------------------------------------ */
@@ -1006,13 +1065,22 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
       float x[3];
       for (int i = 0; i < 3; ++i) x[i] = ray[i] + Ts[s] * ray[4 + i];
       ora_hash_encode(c, table_read, x, 1, st[s].a0, NULL, NULL);
-      mlp_forward(c, &PR, ray + 4, sc->sh_multiplier, &st[s]);
+      const int64_t bs_ = (int64_t)r * S + s;
+      mlp_forward(c, &PR, ray + 4, sc->sh_multiplier, &st[s],
+                  (dbg && dbg->relu_in) ? dbg->relu_in + ORA_RELU_WORDS * bs_ : NULL);
+      if (dbg && dbg->relu_out)
+        for (int h = 0; h < 7; ++h) {
+          dbg->relu_out[ORA_RELU_WORDS * bs_ + 2 * h] = (uint32_t)st[s].own[h];
+          dbg->relu_out[ORA_RELU_WORDS * bs_ + 2 * h + 1] = (uint32_t)(st[s].own[h] >> 32);
+        }
+      if (dbg && dbg->preact) memcpy(dbg->preact + 7 * ORA_M * bs_, st[s].pre, sizeof(float) * 7 * ORA_M);
       sig[s] = (DTs[s] <= 0.0f) ? 0.0f : st[s].sigma;
       for (int k = 0; k < 3; ++k) rgb[3 * s + k] = st[s].rgb[k];
     }
     float* o4 = out_rgb + 4 * (int64_t)r;
-    ora_composite_ray(c, (uint32_t)r, S, sc->rng_seed, do_train, sig, rgb, DTs, targets + 4 * (int64_t)r, o4, Tr,
-                      &T_final, dLdc, dLds);
+    composite_ray(c, (uint32_t)r, S, sc->rng_seed, do_train, sig, rgb, DTs, targets + 4 * (int64_t)r, o4, Tr,
+                  &T_final, dLdc, dLds, (dbg && dbg->C_in) ? dbg->C_in + 4 * (int64_t)r : NULL,
+                  (dbg && dbg->C_out) ? dbg->C_out + 4 * (int64_t)r : NULL);
     if (sc->occ_strength > 0.0f && do_train)
       ora_occ_propose_ray(c, ray, (uint32_t)r, S, sc->rng_seed, Ts, DTs, Tr, T_final, flags, P->occ_in, P->occ_st);
 
@@ -1055,10 +1123,10 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
       /* color backward */
       float dc[4][ORA_M];
       fc_bwd(dc[nc - 1], dcout, ORA_C_OUT, ORA_M, P->W[L_WC_OUT]);
-      for (int j = 0; j < ORA_M; ++j) dc[nc - 1][j] = m->hc[nc - 1][j] > 0.0f ? dc[nc - 1][j] : 0.0f;
+      for (int j = 0; j < ORA_M; ++j) dc[nc - 1][j] = unit_on(m, 3 + nc - 1, j) ? dc[nc - 1][j] : 0.0f;
       for (int k = nc - 1; k >= 1; --k) {
         fc_bwd(dc[k - 1], dc[k], ORA_M, ORA_M, P->W[cslot[k]]);
-        for (int j = 0; j < ORA_M; ++j) dc[k - 1][j] = m->hc[k - 1][j] > 0.0f ? dc[k - 1][j] : 0.0f;
+        for (int j = 0; j < ORA_M; ++j) dc[k - 1][j] = unit_on(m, 3 + k - 1, j) ? dc[k - 1][j] : 0.0f;
       }
       for (int i = 0; i < ORA_D_OUT; ++i) {
         float sacc = 0.0f;
@@ -1068,10 +1136,10 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
       /* density backward */
       float dd[3][ORA_M];
       fc_bwd(dd[nd - 1], ddout, ORA_D_OUT, ORA_M, P->W[L_WD_OUT]);
-      for (int j = 0; j < ORA_M; ++j) dd[nd - 1][j] = m->hd[nd - 1][j] > 0.0f ? dd[nd - 1][j] : 0.0f;
+      for (int j = 0; j < ORA_M; ++j) dd[nd - 1][j] = unit_on(m, nd - 1, j) ? dd[nd - 1][j] : 0.0f;
       for (int k = nd - 1; k >= 1; --k) {
         fc_bwd(dd[k - 1], dd[k], ORA_M, ORA_M, P->W[dslot[k]]);
-        for (int j = 0; j < ORA_M; ++j) dd[k - 1][j] = m->hd[k - 1][j] > 0.0f ? dd[k - 1][j] : 0.0f;
+        for (int j = 0; j < ORA_M; ++j) dd[k - 1][j] = unit_on(m, k - 1, j) ? dd[k - 1][j] : 0.0f;
       }
       /* weight gradients: dW[o][i] += delta[o] * act_in[i] (weight_update.cl:260-314) */
 #define ACC(slot, delta, act, od, id)                                                         \

@@ -67,8 +67,11 @@ class OraDebug(C.Structure):
     _fields_ = [
         ("Ts", _fp), ("DTs", _fp), ("flags", _up), ("a0", _fp), ("sigma", _fp), ("rgb", _fp), ("Tr", _fp),
         ("T_final", _fp), ("dL_dsigma", _fp), ("dL_dc", _fp), ("dL_da0", _fp), ("gW", _fp * 9), ("gb", _fp * 9),
-        ("g_table", _fp),
+        ("g_table", _fp), ("relu_in", _up), ("relu_out", _up), ("preact", _fp), ("C_in", _fp), ("C_out", _fp),
     ]
+
+
+RELU_WORDS = 14  # ReLU-branch words per sample: two per hidden layer (3 density, 4 colour)
 
 
 class OraMarchCfg(C.Structure):
@@ -110,6 +113,8 @@ def load() -> C.CDLL:
     lib.ora_mlp_forward.argtypes = [C.POINTER(OraCfg), C.POINTER(OraParams), _fp, _fp, C.c_float, _fp, _fp, _fp]
     lib.ora_occ_propose_ray.argtypes = [C.POINTER(OraCfg), _fp, C.c_uint32, C.c_int, C.c_uint32, _fp, _fp, _fp,
                                         C.c_float, _up, _up, _up]
+    lib.ora_occ_propose_batch.argtypes = [C.POINTER(OraCfg), _fp, C.c_int32, C.c_int, C.c_uint32, _fp, _fp, _fp,
+                                          _fp, _up, _up, _up]
     lib.ora_composite_ray.argtypes = [C.POINTER(OraCfg), C.c_uint32, C.c_int, C.c_uint32, C.c_int, _fp, _fp, _fp,
                                       _fp, _fp, _fp, _fp, _fp, _fp]
     lib.ora_adam.argtypes = [_fp, _fp, _fp, _fp, C.c_int64, C.c_float, C.c_float, C.c_float, C.c_float]
@@ -257,6 +262,17 @@ def hash_backward(cfg: OraCfg, x: np.ndarray, g: np.ndarray, table_n: int) -> np
     return grad
 
 
+def occ_propose(cfg: OraCfg, rays, S: int, seed: int, Ts, DTs, Tr, T_final, flags, occ_in, occ_st):
+    """The proposal pass over a batch from given compositing results; raises occ_st in place."""
+    rays = np.ascontiguousarray(rays, np.float32).reshape(-1, 8)
+    n = rays.shape[0]
+    arrs = [np.ascontiguousarray(a, np.float32).reshape(-1) for a in (Ts, DTs, Tr, T_final)]
+    fl = np.ascontiguousarray(flags, np.uint32).reshape(-1)
+    assert arrs[0].size == n * S and arrs[3].size == n and fl.size == 2 * n
+    lib().ora_occ_propose_batch(C.byref(cfg), fptr(rays), n, S, seed & 0xFFFFFFFF, *[fptr(a) for a in arrs],
+                                uptr(fl), uptr(np.ascontiguousarray(occ_in, np.uint32).reshape(-1)), uptr(occ_st))
+
+
 def occ_decay(occ_in: np.ndarray, occ_st: np.ndarray, decay_q24: int, seed: int):
     lib().ora_occ_decay(uptr(occ_in), uptr(occ_st), occ_in.size, decay_q24, seed & 0xFFFFFFFF)
 
@@ -323,7 +339,12 @@ class OracleModel:
                                            fptr(rays[r].copy()), o.ctypes.data_as(_fp))
         return out, used
 
-    def train_step(self, rays, targets, S, scalars: dict, taps=False):
+    def train_step(self, rays, targets, S, scalars: dict, taps=False, relu_in=None, C_in=None):
+        """One step of the restatement.  relu_in ([N*S][14] u32, optional): take every hidden unit's ReLU
+        branch from these words (another implementation's decisions) instead of the sign of its
+        pre-activation; the taps then also hold the restatement's own signs (relu_out) and the
+        pre-activations (preact [N*S][7][64]).  C_in ([N][4], optional): evaluate the photometric loss
+        gradient at these composited colours; the taps hold the restatement's own colours (C)."""
         rays = np.ascontiguousarray(rays, np.float32).reshape(-1, 8)
         targets = np.ascontiguousarray(targets, np.float32).reshape(-1, 4)
         N = rays.shape[0]
@@ -354,6 +375,20 @@ class OracleModel:
             if self.cfg.hash_opt == 1:
                 t["g_table"] = np.zeros_like(self.p["table"])
                 dbg.g_table = fptr(t["g_table"])
+            t["C"] = np.zeros((N, 4), np.float32)
+            dbg.C_out = fptr(t["C"])
+            t["relu_out"] = np.zeros((N * S, RELU_WORDS), np.uint32)
+            t["preact"] = np.zeros((N * S, 7, M), np.float32)
+            dbg.relu_out = uptr(t["relu_out"])
+            dbg.preact = fptr(t["preact"])
+        if relu_in is not None:
+            assert taps, "relu_in needs taps=True"
+            relu_in = np.ascontiguousarray(relu_in, np.uint32).reshape(N * S, RELU_WORDS)
+            dbg.relu_in = uptr(relu_in)
+        if C_in is not None:
+            assert taps, "C_in needs taps=True"
+            C_in = np.ascontiguousarray(C_in, np.float32).reshape(N, 4)
+            dbg.C_in = fptr(C_in)
         P = self._params()
         rc = lib().ora_train_step(C.byref(self.cfg), C.byref(P), fptr(rays), fptr(targets), fptr(out), N, S,
                                   C.byref(sc), C.byref(dbg) if taps else None)

@@ -65,11 +65,12 @@ class GpuModel:
             LF = self.spec["n_levels"] * self.spec["f_per_level"]
             z = lambda *s: torch.zeros(s, dtype=torch.float32, device=DEV)
             td = dict(Ts=z(N * S), DTs=z(N * S), flags=torch.zeros(N * 2, dtype=torch.int32, device=DEV),
-                      a0=z(N * S, LF), sigma=z(N * S), rgb=z(N * S, 3), Tr=z(N * S), dL_dsigma=z(N * S),
-                      dL_dc=z(N * S, 3), dL_da0=z(N * S, LF))
+                      a0=z(N * S, LF), sigma=z(N * S), rgb=z(N * S, 3), Tr=z(N * S), T_final=z(N), dL_dsigma=z(N * S),
+                      dL_dc=z(N * S, 3), dL_da0=z(N * S, LF),
+                      relu=torch.zeros((N * S, fl.RELU_WORDS), dtype=torch.int32, device=DEV), C=z(N, 4))
             tp = fl.FfnTaps()
             for k, v in td.items():
-                setattr(tp, k, fl.ptr(v))
+                setattr(tp, "color" if k == "C" else k, fl.ptr(v))
             for i, wn in enumerate(fl.LAYER_NAMES):
                 if wn in self.t:
                     bn = fl.BIAS_NAMES[i]
@@ -87,6 +88,7 @@ class GpuModel:
         if taps:
             res = {k: to_np(v) for k, v in td.items()}
             res["flags"] = res["flags"].view(np.uint32)
+            res["relu"] = res["relu"].view(np.uint32)
         return to_np(out), res
 
     def sample(self, rays, S, seed, do_train=1):
