@@ -14,6 +14,7 @@ scatter + Adam (MLP and table) [+ occupancy decay].  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -89,13 +90,14 @@ def recorded_traffic(stage, mlp):
                 source=f"profiles/{f.name}")
 
 
-def active_tile_fraction(nerf, pool, S):
-    """Fraction of 64-sample tiles of the resident batches holding at least one active sample (dt > 0),
-    from the library's own sampler on the same rays."""
+def active_fractions(nerf, pool, S):
+    """(fraction of 64-sample tiles holding at least one active sample, fraction of active samples) of the
+    resident batches: active = dt > 0 (the ray meets the box), from the library's own sampler on the same
+    rays."""
     import torch
     import ffn_lib as fl
     lib = nerf.handle.lib
-    tot = act = 0
+    tot = act = n_smp = n_act = 0
     for i, io in enumerate(pool):
         n = io.num_rays
         Ts = torch.zeros(n * S, dtype=torch.float32, device="cuda")
@@ -104,40 +106,119 @@ def active_tile_fraction(nerf, pool, S):
         fl.check(lib.ffn_sample(nerf.handle.h, fl.ptr(io.rays_buf), n, S, 1234 + i, 1, fl.ptr(Ts), fl.ptr(DTs),
                                 fl.ptr(flags), fl.stream_ptr()), "ffn_sample")
         d = DTs.cpu().numpy()
+        n_smp += d.size
+        n_act += int(np.count_nonzero(d > 0))
         d = np.pad(d, (0, (-d.size) % 64)).reshape(-1, 64)
         tot += d.shape[0]
         act += int(np.count_nonzero((d > 0).any(axis=1)))
-    return act / max(tot, 1)
+    return act / max(tot, 1), n_act / max(n_smp, 1)
 
 
-def cpu_baseline(seconds=12.0):
-    """The oracle (single-threaded C restatement of the reference step) on a
-    bounded sample: steps of 512 rays x 64 samples at the cfg1 shapes."""
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, warmup=3, reps=10):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baseline(points=1 << 18, points_one_core=1 << 16):
+    """The C restatement of the reference step (oracle/, its OpenMP build) on the host: whole training steps of
+    512 rays x 64 samples at the cfg0 and cfg1 model shapes (3 warm-ups, then the median of 10), and the cfg3
+    hash encode/scatter on uniform points (2^18 on all cores, 2^16 on one; 1 warm-up, the median of 5), each on
+    all available cores and on one."""
     sys.path.insert(0, str(ROOT / "tests"))
     from oracle import oracle as ora
     import ffnerf_tools as ft
     import synthetic_scene as sc
-    spec, occ, S = cfg2_spec()
-    sd = ft.spec_dict(spec, occ)
-    rng = np.random.default_rng(0)
-    p = ft.init_params(spec, occ, rng)
-    model = ora.OracleModel(sd, {k: v.reshape(spec.layer_shapes()[k]) if k in spec.layer_shapes() else v
-                                 for k, v in p.items()})
-    cams = sc.cameras_for("cfg1")
-    scal = dict(lr=1e-2, lr_t=1e-2, color_rel_lr=1.0, sh_multiplier=1.0, occ_strength=1.0, beta1=0.9, beta2=0.99,
-                eps=1e-15, rng_seed=1, do_train=1)
-    rays, tg = sc.uniform_batch(cams, 512, rng)
-    model.train_step(rays, tg, S, scal)  # warm-up
-    n_steps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds or n_steps < 2:
-        rays, tg = sc.uniform_batch(cams, 512, rng)
-        scal["rng_seed"] = n_steps + 2
-        model.train_step(rays, tg, S, scal)
-        n_steps += 1
-    dt = time.perf_counter() - t0
-    return dict(value=n_steps * 512 * S / dt, unit="samples/s", cores=1, kind="port",
-                sample=f"{n_steps} oracle steps of 512 rays x {S} samples (cfg1 shapes: L16 F2 T2^19, Adam), "
-                       f"{dt:.1f} s, 1 thread")
+    lib = ora.load(ora.OMP_LIB_PATH)
+    ora.use_library(lib)
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    S, n_rays = 64, 512
+    res = {}
+    for name, cams_for, L, log2T, finest, G in (("cfg0", "cfg0", 8, 14, None, 32), ("cfg1", "cfg1", 16, 19, 2048.0, 64)):
+        res_l = ft.level_resolutions(L, 16.0, growth=1.5) if finest is None else \
+            ft.level_resolutions(L, 16.0, finest=finest)
+        spec = ft.ModelSpec(n_levels=L, f_per_level=2, log2_T=[log2T] * L, res=res_l, nd=1, nc=2,
+                            background="black", hash_opt="adam", init="xavier", beta1=0.9, beta2=0.99, eps=1e-15)
+        occ = ft.OccParams(G_occ=G, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32), rho_min=1.0,
+                           rho_max=16.0, dt_min=np.float32(1.0 / 8192), dt_max=np.float32(12.8 / S / 6),
+                           t_near_clip=0.3, t_far_clip=1e9, occ_update_strength0=1.0, decay=0.95,
+                           maintenance_period=16)
+        rng = np.random.default_rng(0)
+        p = ft.init_params(spec, occ, rng)
+        model = ora.OracleModel(ft.spec_dict(spec, occ), {k: v.reshape(spec.layer_shapes()[k])
+                                                         if k in spec.layer_shapes() else v for k, v in p.items()})
+        rays, tg = sc.uniform_batch(sc.cameras_for(cams_for), n_rays, rng)
+        scal = dict(lr=1e-2, lr_t=1e-2, color_rel_lr=1.0, sh_multiplier=1.0, occ_strength=1.0, beta1=0.9,
+                    beta2=0.99, eps=1e-15, rng_seed=1, do_train=1)
+        for n in (cores, 1):
+            lib.ora_set_threads(n)
+            t = _median_time(lambda: model.train_step(rays, tg, S, scal))
+            res[(name, n)] = dict(samples_per_s=n_rays * S / t, ms_per_step=t * 1e3, threads=n)
+    # cfg3 subset: L16 F2 T2^22 fp32 table, uniform points
+    L = 16
+    spec3 = dict(n_levels=L, f_per_level=2, log2_T=[22] * L, res=ft.level_resolutions(L, 16.0, finest=2048.0), nd=1,
+                 nc=2, occ_G=64, box_min=[0.0] * 3, box_max=[1.0] * 3, rho_min=1.0, rho_max=16.0, dt_min=1e-4,
+                 dt_max=0.03, t_near=0.3, t_far=1e9)
+    cfg3 = ora.make_cfg(spec3)
+    rng = np.random.default_rng(1)
+    tab = rng.uniform(-1e-4, 1e-4, L * (1 << 22) * 2).astype(np.float32)
+    x_all = rng.random((points, 3), dtype=np.float32)
+    g_all = rng.standard_normal((points, 2 * L), dtype=np.float32)
+    fwd_b, bwd_b = L * 8 * 2 * 4 + 12 + 2 * L * 4, 2 * L * 8 * 2 * 4 + 12 + 2 * L * 4
+    grad = np.zeros(tab.size, np.float64)
+    for n, npts in ((cores, points), (1, points_one_core)):
+        lib.ora_set_threads(n)
+        x, g = x_all[:npts], g_all[:npts]
+        tf = _median_time(lambda: ora.hash_encode(cfg3, tab, x), warmup=1, reps=5)
+        bwd = lambda: lib.ora_hash_backward(C.byref(cfg3), ora.fptr(x), ora.fptr(g), npts,
+                                            grad.ctypes.data_as(ora._dp))  # accumulates: the rate is the same
+        tb = _median_time(bwd, warmup=1, reps=5)
+        res[("cfg3", n)] = dict(points=npts, fwd_points_per_s=npts / tf, bwd_points_per_s=npts / tb,
+                                fwd_GBps=fwd_b * npts / tf / 1e9, bwd_GBps=bwd_b * npts / tb / 1e9, threads=n)
+    lib.ora_set_threads(cores)
+    head = res[("cfg1", cores)]
+    return dict(value=head["samples_per_s"], unit="samples/s", cores=cores, kind="port",
+                label=f"C restatement of ffnerf_OG.cl semantics (oracle/, OpenMP), {cores} cores",
+                cpu_model=_cpu_model(), nproc=os.cpu_count(),
+                sample=f"training steps of {n_rays} rays x {S} samples at the cfg1 model shape (L16 F2 T2^19, Adam "
+                       f"on table and MLPs), 3 warm-ups then the median of 10, {cores} threads",
+                one_core=res[("cfg1", 1)], cfg0={"all_cores": res[("cfg0", cores)], "one_core": res[("cfg0", 1)]},
+                cfg3_subset={"table": "L16 F2 T2^22 fp32, uniform points",
+                             "all_cores": res[("cfg3", cores)], "one_core": res[("cfg3", 1)]})
+
+
+def profiled_pass(nerf, one, first, steps):
+    """Run `steps` more steps with the library's stage events on; returns (per-stage (total ms, launches),
+    ms per step of this pass)."""
+    import torch
+    nerf.handle.set_profiling(True)
+    nerf.handle.stage_times(reset=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        one(first + i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    stages = nerf.handle.stage_times(reset=True)
+    nerf.handle.set_profiling(False)
+    return stages, (t1 - t0) * 1e3 / steps
 
 
 def _timed(fn, steps, warmup):
@@ -314,7 +395,6 @@ def main():
     ap.add_argument("--rays", type=int, default=1 << 18)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp16-line", action="store_true", help="skip the fp16-MLP path measurement")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"],
                     help="cfg2 (default): the training step; cfg3: hash microbench; cfg4: marched render + Adam")
     ap.add_argument("--points", type=int, default=1 << 24, help="cfg3 points")
@@ -374,18 +454,18 @@ def main():
 
     for i in range(args.warmup):
         one(i)
-    torch.cuda.synchronize()
-    nerf.handle.set_profiling(True)
-    nerf.handle.stage_times(reset=True)
+    # the timed region: K steps, nothing else on the stream (stage timing off)
+    nerf.handle.set_profiling(False)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         one(args.warmup + i)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    stages = nerf.handle.stage_times(reset=True)
-    nerf.handle.set_profiling(False)
     print(f"[bench] timed {args.steps} steps in {t1 - t0:.3f} s", flush=True)
+    # a second pass of the same steps with the library's stage events on the step's stream: the per-kernel
+    # durations the rooflines use
+    stages, ms_prof = profiled_pass(nerf, one, args.warmup + args.steps, args.steps)
 
     N = n_rays * S
     ms_step = (t1 - t0) * 1e3 / args.steps
@@ -400,7 +480,7 @@ def main():
     }
     # the MLP kernels skip 64-sample tiles whose samples are all inactive (rays that miss the box); count
     # the tiles with an active sample on the resident batches to state the rate over the computed tiles
-    act = active_tile_fraction(nerf, pool, S)
+    act, act_smp = active_fractions(nerf, pool, S)
     dominant = max(per, key=lambda k: avg[k])
     bound, ach, peak, unit, alg = per[dominant]
     hash_gbs = (fwd_b + bwd_b) * N / ((avg["hash_fwd"] + avg["hash_bwd"]) * 1e-3) / 1e9
@@ -420,6 +500,12 @@ def main():
                      "traffic_detail": tr},
         "stages_ms_avg": {k: round(v, 4) for k, v in avg.items()},
         "stage_rooflines": {k: {"achieved": v[1], "unit": v[3], "frac": v[1] / v[2]} for k, v in per.items()},
+        "active_samples": {"frac": act_smp, "value": value * act_smp, "unit": "samples/s",
+                           "note": "samples whose ray meets the box (dt > 0); value counts every sample of the "
+                                   "batch, as the reference's fixed S samples per ray do"},
+        "profiled_pass": {"ms_per_step": ms_prof, "steps": args.steps,
+                          "note": "stage durations come from this second pass, with HIP events recorded around "
+                                  "each stage on the step's stream; ms_per_step above is timed without them"},
         "mlp_active_tiles": {"frac": act, "achieved_over_computed_tiles": per["mlp"][1] * act,
                              "frac_of_peak_over_computed_tiles": per["mlp"][1] * act / per["mlp"][2],
                              "note": "the MLP kernels skip 64-sample tiles whose samples are all inactive "
@@ -430,17 +516,19 @@ def main():
         # the same step with the fp16/bf16-MFMA MLP (BASELINE reports both paths), same resident batches
         spec16, _, _ = cfg2_spec("fp16")
         nerf16 = ft.Nerf(tempfile.mkdtemp(prefix="ffn_bench16_"), "bench16", spec=spec16, occ=occ, rng_seed=0)
-        for i in range(args.warmup):
+        def one16(i):
             nerf16.step(pool[i % len(pool)], lr_f=1e-2, do_train=True, occ_update_strength=1.0)
+
+        for i in range(args.warmup):
+            one16(i)
+        nerf16.handle.set_profiling(False)
         torch.cuda.synchronize()
-        nerf16.handle.set_profiling(True)
-        nerf16.handle.stage_times(reset=True)
         t2 = time.perf_counter()
         for i in range(args.steps):
-            nerf16.step(pool[(args.warmup + i) % len(pool)], lr_f=1e-2, do_train=True, occ_update_strength=1.0)
+            one16(args.warmup + i)
         torch.cuda.synchronize()
         t3 = time.perf_counter()
-        st16 = nerf16.handle.stage_times(reset=True)
+        st16, _ = profiled_pass(nerf16, one16, args.warmup + args.steps, args.steps)
         avg16 = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in st16.items()}
         line["fp16_mlp_path"] = {
             "value": N * args.steps / (t3 - t2), "unit": "samples/s", "ms_per_step": (t3 - t2) * 1e3 / args.steps,
@@ -451,7 +539,7 @@ def main():
         del nerf16
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:
         print("[bench] timing the CPU oracle on a bounded sample", flush=True)
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline()
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line))

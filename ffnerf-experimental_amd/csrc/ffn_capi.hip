@@ -63,7 +63,10 @@ struct StageEvent {
 
 struct Handle {
   bool prof = false;
-  std::vector<StageEvent> events;
+  std::vector<StageEvent> events;    // recorded, not yet folded into the totals
+  std::vector<hipEvent_t> event_pool;  // created events free for reuse
+  double stage_ms[FFN_N_STAGES] = {};
+  int32_t stage_n[FFN_N_STAGES] = {};
   ffn_config cfg;
   ffn::DevCfg dc;
   ffn::PackedLayout lay;
@@ -103,6 +106,12 @@ hipError_t ensure_bins(Handle* h, int64_t n, ffn::BinPlan* plan, ffn::BinScratch
 }
 
 bool is_pow2(uint32_t v) { return v && !(v & (v - 1)); }
+
+uint32_t max_level_entries(const ffn::DevCfg& c) {
+  uint32_t m = 0;
+  for (int l = 0; l < c.L; ++l) m = c.mask[l] + 1 > m ? c.mask[l] + 1 : m;
+  return m;
+}
 
 int validate_config(const ffn_config* c, int64_t* table_entries) {
   if (!c) return fail(-1, "config is NULL");
@@ -166,8 +175,42 @@ ffn::DevCfg make_devcfg(const ffn_config* c) {
 
 Handle* as_handle(void* h) { return static_cast<Handle*>(h); }
 
-// Brackets one stage of a step with HIP events when profiling is on.
+hipError_t take_event(Handle* h, hipEvent_t* e) {
+  if (!h->event_pool.empty()) {
+    *e = h->event_pool.back();
+    h->event_pool.pop_back();
+    return hipSuccess;
+  }
+  return hipEventCreate(e);
+}
+
+// Fold the oldest `count` recorded stages into the per-stage totals (waiting for each) and return their
+// events to the pool.
+hipError_t fold_events(Handle* h, size_t count) {
+  if (count > h->events.size()) count = h->events.size();
+  hipError_t err = hipSuccess;
+  for (size_t i = 0; i < count; ++i) {
+    StageEvent& e = h->events[i];
+    float ms = 0.0f;
+    hipError_t r = hipEventSynchronize(e.stop);
+    if (r == hipSuccess) r = hipEventElapsedTime(&ms, e.start, e.stop);
+    if (r == hipSuccess) {
+      h->stage_ms[e.stage] += ms;
+      h->stage_n[e.stage] += 1;
+    } else if (err == hipSuccess) {
+      err = r;
+    }
+    h->event_pool.push_back(e.start);
+    h->event_pool.push_back(e.stop);
+  }
+  h->events.erase(h->events.begin(), h->events.begin() + (std::ptrdiff_t)count);
+  return err;
+}
+
+// Brackets one stage of a step with HIP events when profiling is on.  At most kMaxPending stages wait
+// unfolded, so a long profiled run holds a bounded number of events.
 struct StageTimer {
+  static constexpr size_t kMaxPending = 64;
   Handle* h;
   hipStream_t st;
   StageEvent ev{};
@@ -175,7 +218,12 @@ struct StageTimer {
   StageTimer(Handle* h_, int stage, hipStream_t s) : h(h_), st(s), on(h_->prof) {
     if (!on) return;
     ev.stage = stage;
-    if (hipEventCreate(&ev.start) != hipSuccess || hipEventCreate(&ev.stop) != hipSuccess) {
+    if (take_event(h, &ev.start) != hipSuccess) {
+      on = false;
+      return;
+    }
+    if (take_event(h, &ev.stop) != hipSuccess) {
+      h->event_pool.push_back(ev.start);
       on = false;
       return;
     }
@@ -185,15 +233,18 @@ struct StageTimer {
     if (!on) return;
     (void)hipEventRecord(ev.stop, st);
     h->events.push_back(ev);
+    if (h->events.size() > kMaxPending) (void)fold_events(h, h->events.size() - kMaxPending / 2);
   }
 };
 
-void clear_events(Handle* h) {
+void destroy_events(Handle* h) {
   for (auto& e : h->events) {
     (void)hipEventDestroy(e.start);
     (void)hipEventDestroy(e.stop);
   }
   h->events.clear();
+  for (hipEvent_t e : h->event_pool) (void)hipEventDestroy(e);
+  h->event_pool.clear();
 }
 
 }  // namespace
@@ -231,7 +282,7 @@ int ffn_destroy(void* handle) {
   Handle* h = as_handle(handle);
   if (!h) return 0;
   (void)hipDeviceSynchronize();
-  clear_events(h);
+  destroy_events(h);
   h->Ts.release();
   h->DTs.release();
   h->flags.release();
@@ -322,6 +373,9 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
   if (n < 0) return fail(-1, "negative size");
   if (n > 0 && (!x || !g || !grad)) return fail(-1, "NULL buffer");
   if (n == 0) return 0;
+  if (!ffn::scatter_supported(h->dc))
+    return fail(-2, "ffn_hash_encode_bwd: the scatter is not built for this table shape (F=%d with %u-entry levels)",
+                h->dc.F, max_level_entries(h->dc));
   ffn::BinPlan plan;
   ffn::BinScratch bs;
   FFN_HIP(ensure_bins(h, n, &plan, &bs));
@@ -355,6 +409,10 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   const bool mlp16 = h->cfg.mlp_precision == FFN_MLP_FP16;
   if (mlp16 ? !ffn::mlp16_supported(LF, h->cfg.nd, h->cfg.nc) : !ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
     return fail(-2, "MLP shape LF=%d nd=%d nc=%d is not built", LF, h->cfg.nd, h->cfg.nc);
+  // refused before any launch, so that a step is applied whole or not at all
+  if (train && !ffn::scatter_supported(h->dc))
+    return fail(-2, "ffn_train_step: the scatter is not built for this table shape (F=%d with %u-entry levels)",
+                h->dc.F, max_level_entries(h->dc));
   hipStream_t st = (hipStream_t)stream;
   int log2S = 0;
   while ((1u << log2S) < spr) ++log2S;
@@ -663,18 +721,15 @@ int ffn_set_profiling(void* handle, int32_t enable) {
 int ffn_stage_times(void* handle, float* total_ms, int32_t* launches, int32_t reset) {
   Handle* h = as_handle(handle);
   if (!h || !total_ms || !launches) return fail(-1, "NULL argument");
+  FFN_HIP(fold_events(h, h->events.size()));
   for (int i = 0; i < FFN_N_STAGES; ++i) {
-    total_ms[i] = 0.0f;
-    launches[i] = 0;
+    total_ms[i] = (float)h->stage_ms[i];
+    launches[i] = h->stage_n[i];
+    if (reset) {
+      h->stage_ms[i] = 0.0;
+      h->stage_n[i] = 0;
+    }
   }
-  for (auto& e : h->events) {
-    FFN_HIP(hipEventSynchronize(e.stop));
-    float ms = 0.0f;
-    FFN_HIP(hipEventElapsedTime(&ms, e.start, e.stop));
-    total_ms[e.stage] += ms;
-    launches[e.stage] += 1;
-  }
-  if (reset) clear_events(h);
   return 0;
 }
 

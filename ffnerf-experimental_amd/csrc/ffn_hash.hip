@@ -769,6 +769,11 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {
   return p;
 }
 
+bool scatter_supported(const DevCfg& c) {
+  const BinPlan p = plan_bins(c, 1, (size_t)1 << 30);  // the stage size depends on the table, not on n
+  return p.np <= 65535 && emit_lds_bytes(p.max_nbl, c.F) <= 160 * 1024;
+}
+
 hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* g, const FeatLayout& lay,
                            int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
                            hipStream_t st) {

@@ -135,6 +135,9 @@ struct BinApply {
 };
 
 BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes);
+// whether the scatter is built for this table shape: a round's stage must fit in a CU's LDS and its run
+// offsets in 16 bits (F = 4 with 2^22-entry levels does not)
+bool scatter_supported(const DevCfg& c);
 
 hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays, int S, uint32_t seed,
                          const uint32_t* occ_in, int do_train, float* Ts, float* DTs, uint32_t* flags,

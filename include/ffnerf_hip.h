@@ -216,7 +216,10 @@ int ffn_make_batch(const float* images, uint32_t n_images, uint32_t width, uint3
  * event_ms, ffnerf_tools.py:11-13,127-138,1521-1530).  When enabled, every
  * ffn_train_step records HIP events around its kernels on the caller's stream;
  * ffn_stage_times waits for the last step and returns the accumulated
- * milliseconds and launch counts per stage since the last reset.  Stages:
+ * milliseconds and launch counts per stage since the last reset.  The events
+ * of at most 64 stages wait unread; past that the oldest are waited for and
+ * added to the totals, so a long profiled run holds a bounded number of
+ * events (and may wait on the GPU from inside ffn_train_step).  Stages:
  * 0 sample, 1 hash_fwd, 2 mlp, 3 hash_bwd, 4 mlp_adam, 5 table_adam.  No
  * counterpart in the reference's kernel ABI: it replaces the host-side event
  * reads above. */

@@ -28,6 +28,12 @@
  *     Taylor series), identical to the device implementation;
  *   - other transcendentals use the C library (single precision).
  *
+ * Built without OpenMP (liboracle.so, the checker) everything runs on one
+ * thread in a fixed order.  The same source built with -fopenmp
+ * (liboracle_omp.so) is the multi-core CPU baseline only: rays, points and
+ * parameters are spread over threads, and the sums into shared arrays (table
+ * gradient, reference SGD, proposals) become atomic, so their order varies.
+ *
  * Where the reference's result depends on work-item interleaving (the Hogwild
  * CAS scatter into the hash table, ffnerf_OG.cl:2090-2173), the oracle uses
  * the synchronous interleaving: every forward read sees the table as it was
@@ -37,6 +43,12 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#define ORA_ATOMIC _Pragma("omp atomic")
+#else
+#define ORA_ATOMIC
+#endif
 
 #define ORA_M 64
 #define ORA_D_OUT 16
@@ -118,6 +130,22 @@ typedef struct {
 
 /* ------------------------------------------------------------------ */
 /* integer helpers (ffnerf_OG.cl:293-311, decay_occ_grid_in-st.cl:2-10) */
+
+/* thread count of the OpenMP build (the checker build has one) */
+void ora_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+int ora_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
 
 uint32_t ora_hash_u32(uint32_t x) {
   x ^= x >> 16;
@@ -371,10 +399,20 @@ static uint32_t chg_find_next(const uint32_t* f, uint32_t idx, uint32_t WG) {
 
 static void occ_nibble_max(uint32_t* grid, int cell, uint32_t sub, uint32_t proposed_q) {
   uint32_t shift = 4u * sub;
+#ifdef _OPENMP
+  uint32_t old_u = __atomic_load_n(&grid[cell], __ATOMIC_RELAXED);
+  for (;;) {
+    uint32_t old_q = ((old_u >> shift) & 0xFu) + 1u;
+    if (proposed_q <= old_q) return;
+    uint32_t nu = (old_u & ~(0xFu << shift)) | (((proposed_q - 1u) & 0xFu) << shift);
+    if (__atomic_compare_exchange_n(&grid[cell], &old_u, nu, 0, __ATOMIC_RELAXED, __ATOMIC_RELAXED)) return;
+  }
+#else
   uint32_t old_u = grid[cell];
   uint32_t old_q = ((old_u >> shift) & 0xFu) + 1u;
   if (proposed_q <= old_q) return;
   grid[cell] = (old_u & ~(0xFu << shift)) | (((proposed_q - 1u) & 0xFu) << shift);
+#endif
 }
 
 /* ------------------------------------------------------------------ */
@@ -562,33 +600,42 @@ static void level_corners(const ora_cfg* c, int lvl, const float p[3], uint32_t 
   }
 }
 
+/* encoding of one point x[3] -> a0[LF]; optionally its feature base indices [L*8] and weights [L*8] */
+static void encode_point(const ora_cfg* c, const float* table, const float* x, float* a0, uint32_t* idx_out,
+                         float* w_out) {
+  const int L = c->n_levels, F = c->f_per_level;
+  float p[3];
+  normalize_pos(c, x, p);
+  for (int l = 0; l < L; ++l) {
+    uint32_t feat[8];
+    float w[8];
+    level_corners(c, l, p, feat, w);
+    for (int f = 0; f < F; ++f) {
+      float acc = 0.0f;
+      for (int cc = 0; cc < 8; ++cc) acc += w[cc] * table[feat[cc] + (uint32_t)f];
+      a0[l * F + f] = acc;
+    }
+    if (idx_out)
+      for (int cc = 0; cc < 8; ++cc) idx_out[l * 8 + cc] = feat[cc];
+    if (w_out)
+      for (int cc = 0; cc < 8; ++cc) w_out[l * 8 + cc] = w[cc];
+  }
+}
+
 /* encode n points x[n*3] -> a0[n*LF]; optionally the feature base index [n*L*8] and weights [n*L*8] */
 void ora_hash_encode(const ora_cfg* c, const float* table, const float* x, int64_t n, float* a0,
                      uint32_t* idx_out, float* w_out) {
-  const int L = c->n_levels, F = c->f_per_level, LF = L * F;
-  for (int64_t s = 0; s < n; ++s) {
-    float p[3];
-    normalize_pos(c, x + 3 * s, p);
-    for (int l = 0; l < L; ++l) {
-      uint32_t feat[8];
-      float w[8];
-      level_corners(c, l, p, feat, w);
-      for (int f = 0; f < F; ++f) {
-        float acc = 0.0f;
-        for (int cc = 0; cc < 8; ++cc) acc += w[cc] * table[feat[cc] + (uint32_t)f];
-        a0[s * LF + l * F + f] = acc;
-      }
-      if (idx_out)
-        for (int cc = 0; cc < 8; ++cc) idx_out[(s * L + l) * 8 + cc] = feat[cc];
-      if (w_out)
-        for (int cc = 0; cc < 8; ++cc) w_out[(s * L + l) * 8 + cc] = w[cc];
-    }
-  }
+  const int L = c->n_levels, LF = L * c->f_per_level;
+#pragma omp parallel for schedule(static)
+  for (int64_t s = 0; s < n; ++s)
+    encode_point(c, table, x + 3 * s, a0 + s * LF, idx_out ? idx_out + s * L * 8 : NULL,
+                 w_out ? w_out + s * L * 8 : NULL);
 }
 
 /* scatter the encoding gradient g[n*LF] of points x into grad (plain sum, double accumulators) */
 void ora_hash_backward(const ora_cfg* c, const float* x, const float* g, int64_t n, double* grad) {
   const int L = c->n_levels, F = c->f_per_level, LF = L * F;
+#pragma omp parallel for schedule(static)
   for (int64_t s = 0; s < n; ++s) {
     float p[3];
     normalize_pos(c, x + 3 * s, p);
@@ -599,7 +646,10 @@ void ora_hash_backward(const ora_cfg* c, const float* x, const float* g, int64_t
       for (int f = 0; f < F; ++f) {
         float gf = g[s * LF + l * F + f];
         if (!isfinite(gf)) continue;
-        for (int cc = 0; cc < 8; ++cc) grad[feat[cc] + (uint32_t)f] += (double)(gf * w[cc]);
+        for (int cc = 0; cc < 8; ++cc) {
+          ORA_ATOMIC
+          grad[feat[cc] + (uint32_t)f] += (double)(gf * w[cc]);
+        }
       }
     }
   }
@@ -971,6 +1021,7 @@ void ora_composite_ray(const ora_cfg* c, uint32_t ray_id, int S, uint32_t seed, 
 
 void ora_adam(float* p, float* m, float* v, const float* g, int64_t n, float lr_t, float beta1, float beta2,
               float eps) {
+#pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < n; ++i) {
     float mi = fmaf(1.0f - beta1, g[i], beta1 * m[i]);
     float vi = fmaf(1.0f - beta2, g[i] * g[i], beta2 * v[i]);
@@ -1031,7 +1082,8 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
   /* forward reads use the table as of the step start */
   float* table_read = (float*)malloc(sizeof(float) * (size_t)table_n);
   if (!table_read) return -3;
-  memcpy(table_read, P->table, sizeof(float) * (size_t)table_n);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < table_n; ++i) table_read[i] = P->table[i];
 
   double* gW[L_COUNT];
   double* gb[L_COUNT];
@@ -1043,18 +1095,38 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
     gW[k] = (double*)calloc((size_t)odim[k] * idim[k], sizeof(double));
     gb[k] = (double*)calloc((size_t)odim[k], sizeof(double));
   }
-  double* gtab = (c->hash_opt == 1 && do_train) ? (double*)calloc((size_t)table_n, sizeof(double)) : NULL;
+  double* gtab = (c->hash_opt == 1 && do_train) ? (double*)malloc(sizeof(double) * (size_t)table_n) : NULL;
+  if (gtab) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < table_n; ++i) gtab[i] = 0.0;
+  }
 
   ora_params PR = *P;
   PR.table = table_read;
 
-  mlp_state* st = (mlp_state*)malloc(sizeof(mlp_state) * (size_t)S);
   const float D = 0.5f * sqrtf((c->box_max[0] - c->box_min[0]) * (c->box_max[0] - c->box_min[0]) +
                                (c->box_max[1] - c->box_min[1]) * (c->box_max[1] - c->box_min[1]) +
                                (c->box_max[2] - c->box_min[2]) * (c->box_max[2] - c->box_min[2]));
   static const int cslot[4] = {L_WC_IN, L_WC_01, L_WC_12, L_WC_23};
   static const int dslot[3] = {L_WD_IN, L_WD_01, L_WD_12};
 
+#pragma omp parallel
+  {
+  mlp_state* st = (mlp_state*)malloc(sizeof(mlp_state) * (size_t)S);
+  /* weight-gradient sums: the shared ones, or per thread in the OpenMP build (added together at the end) */
+  double* lgW[L_COUNT];
+  double* lgb[L_COUNT];
+  for (int k = 0; k < L_COUNT; ++k) {
+    lgW[k] = gW[k];
+    lgb[k] = gb[k];
+#ifdef _OPENMP
+    if (gW[k]) {
+      lgW[k] = (double*)calloc((size_t)odim[k] * idim[k], sizeof(double));
+      lgb[k] = (double*)calloc((size_t)odim[k], sizeof(double));
+    }
+#endif
+  }
+#pragma omp for schedule(dynamic, 4)
   for (int32_t r = 0; r < num_rays; ++r) {
     const float* ray = rays + 8 * (int64_t)r;
     float Ts[ORA_S_MAX], DTs[ORA_S_MAX], Tr[ORA_S_MAX], sig[ORA_S_MAX], rgb[3 * ORA_S_MAX];
@@ -1064,7 +1136,7 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
     for (int s = 0; s < S; ++s) {
       float x[3];
       for (int i = 0; i < 3; ++i) x[i] = ray[i] + Ts[s] * ray[4 + i];
-      ora_hash_encode(c, table_read, x, 1, st[s].a0, NULL, NULL);
+      encode_point(c, table_read, x, st[s].a0, NULL, NULL);
       const int64_t bs_ = (int64_t)r * S + s;
       mlp_forward(c, &PR, ray + 4, sc->sh_multiplier, &st[s],
                   (dbg && dbg->relu_in) ? dbg->relu_in + ORA_RELU_WORDS * bs_ : NULL);
@@ -1146,8 +1218,8 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
   do {                                                                                        \
     for (int o_ = 0; o_ < (od); ++o_) {                                                       \
       double dv = (double)(delta)[o_];                                                        \
-      gb[slot][o_] += dv;                                                                     \
-      for (int i_ = 0; i_ < (id); ++i_) gW[slot][o_ * (id) + i_] += dv * (double)(act)[i_]; \
+      lgb[slot][o_] += dv;                                                                    \
+      for (int i_ = 0; i_ < (id); ++i_) lgW[slot][o_ * (id) + i_] += dv * (double)(act)[i_]; \
     }                                                                                         \
   } while (0)
       ACC(L_WC_OUT, dcout, m->hc[nc - 1], ORA_C_OUT, ORA_M);
@@ -1177,12 +1249,29 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
           float g = gf[l * F + f];
           if (!isfinite(g)) continue;
           for (int cc = 0; cc < 8; ++cc) {
-            if (c->hash_opt == 1) gtab[feat[cc] + (uint32_t)f] += (double)(g * w[cc]);
-            else P->table[feat[cc] + (uint32_t)f] += -lr_lvl * 0.5f * g * w[cc];
+            if (c->hash_opt == 1) {
+              ORA_ATOMIC
+              gtab[feat[cc] + (uint32_t)f] += (double)(g * w[cc]);
+            } else {
+              ORA_ATOMIC
+              P->table[feat[cc] + (uint32_t)f] += -lr_lvl * 0.5f * g * w[cc];
+            }
           }
         }
       }
     }
+  }
+#ifdef _OPENMP
+#pragma omp critical
+  for (int k = 0; k < L_COUNT; ++k) {
+    if (!gW[k]) continue;
+    for (int i = 0; i < odim[k] * idim[k]; ++i) gW[k][i] += lgW[k][i];
+    for (int i = 0; i < odim[k]; ++i) gb[k][i] += lgb[k][i];
+    free(lgW[k]);
+    free(lgb[k]);
+  }
+#endif
+  free(st);
   }
 
   if (do_train) {
@@ -1204,6 +1293,7 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
     }
     if (gtab) {
       float* gtf = (float*)malloc(sizeof(float) * (size_t)table_n);
+#pragma omp parallel for schedule(static)
       for (int64_t i = 0; i < table_n; ++i) gtf[i] = (float)gtab[i];
       if (dbg && dbg->g_table) memcpy(dbg->g_table, gtf, sizeof(float) * (size_t)table_n);
       ora_adam(P->table, P->m_table, P->v_table, gtf, table_n, sc->lr_t, sc->beta1, sc->beta2, sc->eps);
@@ -1212,7 +1302,6 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
   }
   for (int k = 0; k < L_COUNT; ++k) { free(gW[k]); free(gb[k]); }
   free(gtab);
-  free(st);
   free(table_read);
   return 0;
 }

@@ -83,10 +83,18 @@ def _build():
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
 
 
-def load() -> C.CDLL:
-    if not LIB_PATH.exists():
+OMP_LIB_PATH = HERE / "liboracle_omp.so"
+
+
+def load(path: Path = None) -> C.CDLL:
+    """The checker build (one thread, fixed order), or with path=OMP_LIB_PATH the same restatement on every
+    host core (the CPU baseline only)."""
+    path = LIB_PATH if path is None else path
+    if not path.exists():
         _build()
-    lib = C.CDLL(str(LIB_PATH))
+    lib = C.CDLL(str(path))
+    lib.ora_set_threads.argtypes = [C.c_int]
+    lib.ora_max_threads.restype = C.c_int
     lib.ora_hash_u32.restype = C.c_uint32
     lib.ora_hash_u32.argtypes = [C.c_uint32]
     lib.ora_xorshift32.restype = C.c_uint32
@@ -138,6 +146,12 @@ def lib() -> C.CDLL:
     if _LIB is None:
         _LIB = load()
     return _LIB
+
+
+def use_library(cdll: C.CDLL) -> None:
+    """Route the wrappers below to another build of the restatement (the OpenMP baseline build)."""
+    global _LIB
+    _LIB = cdll
 
 
 def fptr(a):

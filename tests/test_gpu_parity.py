@@ -151,6 +151,22 @@ def test_hash_backward_too_wide_is_an_error(gh):
         m.encode_bwd(x, g, table_floats(spec))
 
 
+def test_train_step_with_unbuilt_scatter_changes_nothing(gh):
+    """A training step whose table shape the scatter does not support is refused before its first launch:
+    no colour, occupancy proposal, table or MLP update is written (a step is applied whole or not at all)."""
+    import ffn_lib as fl
+    print("[case] train step refused for an unbuilt scatter shape", flush=True)
+    spec = spec_cfg0(n_levels=4, f_per_level=4, log2_T=[22, 14, 14, 14], res=[32.0, 64.0, 128.0, 256.0])
+    m = gh.GpuModel(spec, random_params(spec, seed=37))
+    before = m.state()
+    rays = look_at_rays(64, spec, seed=38)
+    with pytest.raises(fl.FfnError, match="scatter is not built"):
+        m.train_step(rays, sphere_targets(rays, spec), 64, default_scalars(), taps=False)
+    after = m.state()
+    for k in before:
+        assert np.array_equal(before[k].view(np.uint32), after[k].view(np.uint32)), k
+
+
 def test_occ_decay_bit_exact(gh, ora):
     import ctypes
     import torch
