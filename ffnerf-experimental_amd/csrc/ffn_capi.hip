@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -175,6 +176,45 @@ ffn::DevCfg make_devcfg(const ffn_config* c) {
 
 Handle* as_handle(void* h) { return static_cast<Handle*>(h); }
 
+// ---- the march's scratch for callers that cannot allocate (ffn_march_noalloc) ------------------------
+// The march's exclusive scan needs num_rays + 1 offsets and one partial sum per 4096 of them.  This array
+// holds them for up to FFN_MARCH_NOALLOC_MAX_RAYS rays, once per GPU for the life of the process (4 MiB).
+// Host code never uses the array's name as an address: the per-device address comes from
+// hipGetSymbolAddress, taken once per device with that device current (at ffn_create, or at the first
+// ffn_march_noalloc call on a device that has no handle).
+constexpr uint64_t kNoallocScanWords = (uint64_t)FFN_MARCH_NOALLOC_MAX_RAYS + 1;
+constexpr uint64_t kNoallocSumWords = (kNoallocScanWords + 4095) / 4096 + 1;
+static __device__ __align__(256) uint32_t scratch[kNoallocScanWords + kNoallocSumWords];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// the current device's address of `scratch` (looked up once per device); NULL with an error message
+uint32_t* noalloc_scratch() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(-3, "hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(-3, "device %d beyond the %d devices this library tracks", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      fail(-3, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<uint32_t*>(ptr);
+  }
+  return g_scratch_ptr[dev];
+}
+
 hipError_t take_event(Handle* h, hipEvent_t* e) {
   if (!h->event_pool.empty()) {
     *e = h->event_pool.back();
@@ -272,6 +312,12 @@ int ffn_create(const ffn_config* cfg, void** handle) {
   if (e != hipSuccess) {
     delete h;
     return fail(-3, "no HIP device: %s", hipGetErrorString(e));
+  }
+  // the address of this device's ffn_march_noalloc scratch, taken here rather than inside a caller's
+  // no-allocation region
+  if (!noalloc_scratch()) {
+    delete h;
+    return -3;
   }
   *handle = h;
   g_err.clear();
@@ -616,6 +662,35 @@ int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t*
   FFN_HIP(h->m_sums.ensure(sizeof(uint32_t) * ((n1 + 4095) / 4096 + 1)));
   uint32_t* off = (uint32_t*)h->m_offsets.p;
   FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, total, st));
+  FFN_HIP(hipMemcpyAsync(offsets, off, sizeof(uint32_t) * num_rays, hipMemcpyDeviceToDevice, st));
+  a.offsets = off;
+  a.samples = (float4*)samples;
+  a.ray_ids = ray_ids;
+  a.capacity = capacity;
+  FFN_HIP(ffn::launch_march(a, true, st));
+  return 0;
+}
+
+int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits,
+                      const ffn_march_params* mp, uint32_t* counts, uint32_t* offsets, float* samples,
+                      uint32_t* ray_ids, uint64_t capacity, uint32_t* total, void* stream) {
+  Handle* h = as_handle(handle);
+  int rc = check_march(h, rays, bits, mp);
+  if (rc) return rc;
+  if (!counts || !offsets || !total || (capacity > 0 && (!samples || !ray_ids))) return fail(-1, "NULL buffer");
+  if (num_rays > FFN_MARCH_NOALLOC_MAX_RAYS)
+    return fail(-1, "ffn_march_noalloc: num_rays=%u exceeds its scratch of %u rays (use ffn_march)", num_rays,
+                (uint32_t)FFN_MARCH_NOALLOC_MAX_RAYS);
+  if (num_rays == 0) return 0;
+  uint32_t* off = noalloc_scratch();  // [num_rays + 1] offsets, then the scan's tile sums
+  if (!off) return -3;
+  uint32_t* sums = off + kNoallocScanWords;
+  hipStream_t st = (hipStream_t)stream;
+  ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
+  a.counts = counts;
+  FFN_HIP(ffn::launch_march(a, false, st));
+  // every word the scan reads is written by it first (offsets, tile sums, total): nothing to clear
+  FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, sums, total, st));
   FFN_HIP(hipMemcpyAsync(offsets, off, sizeof(uint32_t) * num_rays, hipMemcpyDeviceToDevice, st));
   a.offsets = off;
   a.samples = (float4*)samples;

@@ -193,6 +193,19 @@ int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t*
               uint32_t* counts, uint32_t* offsets, float* samples, uint32_t* ray_ids, uint64_t capacity,
               uint32_t* total, void* stream);
 
+/* ffn_march without any allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as ffn_march; the scan's offsets and partial sums live
+ * in a fixed device array of the library (4 MiB, held on every GPU the
+ * library runs on until the process ends), so num_rays may not exceed
+ * FFN_MARCH_NOALLOC_MAX_RAYS (an error otherwise), and calls that overlap on
+ * one GPU (other streams, other threads) race on that array. */
+#define FFN_MARCH_NOALLOC_MAX_RAYS (1u << 20)
+int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits,
+                      const ffn_march_params* mp, uint32_t* counts, uint32_t* offsets, float* samples,
+                      uint32_t* ray_ids, uint64_t capacity, uint32_t* total, void* stream);
+
 /* Forward render with the bound parameters: march `chunk` samples per live
  * ray, encode, run the MLPs, composite front to back, retire rays below
  * T_stop, repeat.  out_rgb [num_rays] float4 {r, g, b, T_final} (black
