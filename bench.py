@@ -51,8 +51,9 @@ def cfg2_spec(mlp="fp32"):
 def algorithmic(spec):
     L, F = spec.n_levels, spec.f_per_level
     LF = L * F
-    fwd_b = L * 8 * F * 4 + 12 + LF * 4            # corner gathers + xyz + features out
-    bwd_b = 2 * L * 8 * F * 4 + 12 + LF * 4        # atomic read-modify-write + xyz + upstream grad
+    s_tab = 2 if spec.table_dtype == "fp16" else 4  # bytes per table (and table-gradient) value
+    fwd_b = L * 8 * F * s_tab + 12 + LF * 4        # corner gathers + xyz + features out
+    bwd_b = 2 * L * 8 * F * s_tab + 12 + LF * 4    # atomic read-modify-write + xyz + upstream grad
     macs = LF * 64 + 64 * 16 + 32 * 64 + (spec.nc - 1) * 64 * 64 + 64 * 3 + (spec.nd - 1) * 64 * 64
     mlp_flops = 6 * macs                           # fwd + dX + dW
     adam_b = 28                                    # per parameter: r p,g,m,v; w p,m,v
@@ -236,66 +237,71 @@ def _timed(fn, steps, warmup):
 
 
 def run_cfg3(args):
-    """hash-encoding microbench, 2^24 points, L16 F2 T=2^22 fp32, forward gather and
-    backward scatter-add, uniform and shell point distributions.  One JSON line per distribution."""
-    import ctypes as C
+    """hash-encoding microbench, 2^24 points, L16 F2 T=2^22, forward gather and backward
+    scatter-add, fp32 and fp16 tables (the gradient table in the table's type), uniform and shell point
+    distributions.  One JSON line per (table type, distribution)."""
     import torch
     import ffn_lib as fl
     import ffnerf_tools as ft
     L, n = 16, int(args.points)
-    spec = ft.ModelSpec(n_levels=L, f_per_level=2, log2_T=[22] * L, res=ft.level_resolutions(L, 16.0, finest=2048.0),
-                        nd=1, nc=2, background="black", hash_opt="adam", init="xavier")
-    _, occ, _ = cfg2_spec()
-    h = fl.Handle(ft.spec_dict(spec, occ))
-    rng = np.random.default_rng(1)
-    table = torch.from_numpy(rng.uniform(-1e-4, 1e-4, spec.table_entries() * 2).astype(np.float32)).cuda()
-    occ_t = torch.zeros(64 ** 3, dtype=torch.int32, device="cuda")
-    P = fl.FfnParams()
-    dummies = {}
-    for i, (wn, bn) in enumerate(zip(fl.LAYER_NAMES, fl.BIAS_NAMES)):
-        if wn in spec.layer_shapes():
-            for k in ("W", "b", "mW", "vW", "mb", "vb"):
-                dummies[k + str(i)] = torch.zeros(4096, device="cuda")
-                getattr(P, k)[i] = fl.ptr(dummies[k + str(i)])
-    P.table, P.m_table, P.v_table, P.occ_in, P.occ_st = fl.ptr(table), fl.ptr(table), fl.ptr(table), \
-        fl.ptr(occ_t), fl.ptr(occ_t)
-    h.bind(P, keep=dict(dummies, table=table, occ=occ_t))
-    fwd_b, bwd_b, _, _ = algorithmic(spec)
     LF = 2 * L
+    _, occ, _ = cfg2_spec()
+    rng = np.random.default_rng(1)
+    pts = {}
+    pts["uniform"] = rng.random((n, 3), dtype=np.float32)
+    k = n // 10
+    v = rng.normal(size=(n - k, 3))
+    v /= np.linalg.norm(v, axis=1, keepdims=True)
+    r = rng.uniform(0.24, 0.26, (n - k, 1))
+    x = np.concatenate([0.5 + v * r, rng.random((k, 3))]).astype(np.float32)
+    pts["shell"] = x[rng.permutation(n)]
+    tab_np = rng.uniform(-1e-4, 1e-4, L * (1 << 22) * 2).astype(np.float32)
     lines = []
-    for dist in ("uniform", "shell"):
-        if dist == "uniform":
-            x = rng.random((n, 3), dtype=np.float32)
-        else:
-            k = n // 10
-            v = rng.normal(size=(n - k, 3))
-            v /= np.linalg.norm(v, axis=1, keepdims=True)
-            r = rng.uniform(0.24, 0.26, (n - k, 1))
-            x = np.concatenate([0.5 + v * r, rng.random((k, 3))]).astype(np.float32)
-            x = x[rng.permutation(n)]
-        xt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
-        a0 = torch.empty((n, LF), dtype=torch.float32, device="cuda")
-        g = torch.randn((n, LF), dtype=torch.float32, device="cuda", generator=torch.Generator("cuda").manual_seed(1))
-        grad = torch.zeros(spec.table_entries() * 2, dtype=torch.float32, device="cuda")
-        sp = fl.stream_ptr()
-        fwd = lambda: fl.check(h.lib.ffn_hash_encode_fwd(h.h, fl.ptr(xt), n, fl.ptr(a0), None, sp))
-        bwd = lambda: fl.check(h.lib.ffn_hash_encode_bwd(h.h, fl.ptr(xt), fl.ptr(g), n, fl.ptr(grad), sp))
-        t_f = _timed(fwd, args.steps, args.warmup)
-        t_b = _timed(bwd, args.steps, args.warmup)
-        line = {"metric": "hash-grid gather/scatter HBM GB/s (algorithmic bytes)", "workload": f"cfg3-{dist}",
-                "value": (fwd_b + bwd_b) * n / ((t_f + t_b) * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1,
-                "higher_is_better": True, "dtype": "fp32", "data": "synthetic",
-                "config": {"workload": f"BASELINE configs[3] ({dist}): 2^{int(np.log2(n))} points, L16 F2 T2^22 "
-                                       f"fp32 table, res 16->2048", "points": n},
-                "fwd": {"ms": t_f, "points_per_s": n / (t_f * 1e-3), "GBps": fwd_b * n / (t_f * 1e-3) / 1e9,
-                        "frac": fwd_b * n / (t_f * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_point": fwd_b},
-                "bwd": {"ms": t_b, "points_per_s": n / (t_b * 1e-3), "GBps": bwd_b * n / (t_b * 1e-3) / 1e9,
-                        "frac": bwd_b * n / (t_b * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_point": bwd_b},
-                "note": "fp16 tables are not built"}
-        print(json.dumps(line), flush=True)
-        lines.append(line)
-        del xt, a0, g, grad
-    h.close()
+    for dtype in args.table_dtypes.split(","):
+        tdt = torch.float16 if dtype == "fp16" else torch.float32
+        spec = ft.ModelSpec(n_levels=L, f_per_level=2, log2_T=[22] * L,
+                            res=ft.level_resolutions(L, 16.0, finest=2048.0), nd=1, nc=2, background="black",
+                            hash_opt="adam", init="xavier", table_dtype=dtype)
+        h = fl.Handle(ft.spec_dict(spec, occ))
+        table = torch.from_numpy(tab_np).cuda().to(tdt)
+        occ_t = torch.zeros(64 ** 3, dtype=torch.int32, device="cuda")
+        P = fl.FfnParams()
+        dummies = {}
+        for i, (wn, bn) in enumerate(zip(fl.LAYER_NAMES, fl.BIAS_NAMES)):
+            if wn in spec.layer_shapes():
+                for kk in ("W", "b", "mW", "vW", "mb", "vb"):
+                    dummies[kk + str(i)] = torch.zeros(4096, device="cuda")
+                    getattr(P, kk)[i] = fl.ptr(dummies[kk + str(i)])
+        mv = torch.zeros(tab_np.size, dtype=torch.float32, device="cuda")
+        P.table, P.m_table, P.v_table, P.occ_in, P.occ_st = fl.ptr(table), fl.ptr(mv), fl.ptr(mv), \
+            fl.ptr(occ_t), fl.ptr(occ_t)
+        h.bind(P, keep=dict(dummies, table=table, occ=occ_t, mv=mv))
+        fwd_b, bwd_b, _, _ = algorithmic(spec)
+        for dist in ("uniform", "shell"):
+            xt = torch.from_numpy(np.ascontiguousarray(pts[dist])).cuda()
+            a0 = torch.empty((n, LF), dtype=torch.float32, device="cuda")
+            g = torch.randn((n, LF), dtype=torch.float32, device="cuda",
+                            generator=torch.Generator("cuda").manual_seed(1))
+            grad = torch.zeros(tab_np.size, dtype=tdt, device="cuda")
+            sp = fl.stream_ptr()
+            fwd = lambda: fl.check(h.lib.ffn_hash_encode_fwd(h.h, fl.ptr(xt), n, fl.ptr(a0), None, sp))
+            bwd = lambda: fl.check(h.lib.ffn_hash_encode_bwd(h.h, fl.ptr(xt), fl.ptr(g), n, fl.ptr(grad), sp))
+            t_f = _timed(fwd, args.steps, args.warmup)
+            t_b = _timed(bwd, args.steps, args.warmup)
+            line = {"metric": "hash-grid gather/scatter HBM GB/s (algorithmic bytes)", "workload": f"cfg3-{dist}-{dtype}",
+                    "value": (fwd_b + bwd_b) * n / ((t_f + t_b) * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1,
+                    "higher_is_better": True, "dtype": dtype, "data": "synthetic",
+                    "config": {"workload": f"BASELINE configs[3] ({dist}): 2^{int(np.log2(n))} points, L16 F2 "
+                                           f"T2^22 {dtype} table (and gradient table), res 16->2048", "points": n},
+                    "fwd": {"ms": t_f, "points_per_s": n / (t_f * 1e-3), "GBps": fwd_b * n / (t_f * 1e-3) / 1e9,
+                            "frac": fwd_b * n / (t_f * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_point": fwd_b},
+                    "bwd": {"ms": t_b, "points_per_s": n / (t_b * 1e-3), "GBps": bwd_b * n / (t_b * 1e-3) / 1e9,
+                            "frac": bwd_b * n / (t_b * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_point": bwd_b}}
+            print(json.dumps(line), flush=True)
+            lines.append(line)
+            del xt, a0, g, grad
+        h.close()
+        del table, mv
     return lines
 
 
@@ -398,6 +404,7 @@ def main():
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"],
                     help="cfg2 (default): the training step; cfg3: hash microbench; cfg4: marched render + Adam")
     ap.add_argument("--points", type=int, default=1 << 24, help="cfg3 points")
+    ap.add_argument("--table-dtypes", default="fp32,fp16", help="cfg3 table types")
     ap.add_argument("--rays4", type=int, default=1 << 20, help="cfg4 rays")
     ap.add_argument("--chunk", type=int, default=64, help="cfg4 samples per ray per render round")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,

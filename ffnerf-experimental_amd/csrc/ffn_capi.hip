@@ -136,6 +136,8 @@ int validate_config(const ffn_config* c, int64_t* table_entries) {
   if (c->hash_opt != FFN_HASH_SGD && c->hash_opt != FFN_HASH_ADAM) return fail(-1, "hash_opt=%d unknown", c->hash_opt);
   if (c->mlp_precision != FFN_MLP_FP32 && c->mlp_precision != FFN_MLP_FP16)
     return fail(-1, "mlp_precision=%d unknown", c->mlp_precision);
+  if (c->table_dtype != FFN_TABLE_FP32 && c->table_dtype != FFN_TABLE_FP16)
+    return fail(-1, "table_dtype=%d unknown", c->table_dtype);
   return 0;
 }
 
@@ -171,6 +173,7 @@ ffn::DevCfg make_devcfg(const ffn_config* c) {
   d.t_far = c->t_far;
   d.background = c->background;
   d.hash_opt = c->hash_opt;
+  d.table_f16 = c->table_dtype == FFN_TABLE_FP16 ? 1 : 0;
   return d;
 }
 
@@ -413,7 +416,7 @@ int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint
   return 0;
 }
 
-int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n, float* grad, void* stream) {
+int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n, void* grad, void* stream) {
   Handle* h = as_handle(handle);
   if (!h) return fail(-1, "NULL handle");
   if (n < 0) return fail(-1, "negative size");
@@ -435,6 +438,7 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
   ffn::PosSrc src{x, nullptr, nullptr, 0};
   ffn::BinApply ap{};
   ap.dst = grad;
+  ap.dst_f16 = h->dc.table_f16;
   FFN_HIP(ffn::launch_hash_bwd(h->dc, src, n, (const float*)h->dLda0.p, lm, ffn::BIN_GRAD, 0.0f, ap, plan, bs, st));
   return 0;
 }
@@ -562,6 +566,7 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     s2.Ts = Ts;
     ffn::BinApply ap{};
     ap.dst = P.table;
+    ap.dst_f16 = h->dc.table_f16;
     int mode = ffn::BIN_SGD;
     if (h->cfg.hash_opt == FFN_HASH_ADAM) {
       mode = ffn::BIN_ADAM;

@@ -33,6 +33,7 @@ struct DevCfg {
   float inv_extent[3];  // 1 / (bmax - bmin) when that extent is a power of two (exact), else 0
   float rho_min, rho_max, dt_min, dt_max, t_near, t_far;
   int background, hash_opt;
+  int table_f16;  // the table is IEEE binary16 (FFN_TABLE_FP16)
 };
 
 // ---------------------------------------------------------------------------

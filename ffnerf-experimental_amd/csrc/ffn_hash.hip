@@ -72,6 +72,41 @@ struct FVec<4> {
   static __device__ __forceinline__ T pack(const float* o) { return make_float4(o[0], o[1], o[2], o[3]); }
 };
 
+// F features of a binary16 table entry: one 2-, 4- or 8-byte load, widened exactly to fp32
+template <int F>
+struct HVec;
+template <>
+struct HVec<1> {
+  typedef _Float16 T;
+  static __device__ __forceinline__ void unpack(const T& v, float* o) { o[0] = (float)v; }
+};
+template <>
+struct HVec<2> {
+  typedef _Float16 T __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ void unpack(const T& v, float* o) {
+    o[0] = (float)v.x;
+    o[1] = (float)v.y;
+  }
+};
+template <>
+struct HVec<4> {
+  typedef _Float16 T __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ void unpack(const T& v, float* o) {
+    o[0] = (float)v.x;
+    o[1] = (float)v.y;
+    o[2] = (float)v.z;
+    o[3] = (float)v.w;
+  }
+};
+template <int F, typename TT>
+struct TabVec {
+  typedef FVec<F> V;
+};
+template <int F>
+struct TabVec<F, _Float16> {
+  typedef HVec<F> V;
+};
+
 __device__ __forceinline__ void sample_position(const PosSrc& s, int64_t b, float pos[3]) {
   if (s.rays) {
     const int64_t r = b >> s.log2S;
@@ -91,11 +126,12 @@ __device__ __forceinline__ void sample_position(const PosSrc& s, int64_t b, floa
 // ---------------------------------------------------------------------------
 // forward
 
-template <int F>
+template <int F, typename TT>
 __global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t n, int level0,
-                                                  const float* __restrict__ table, float* __restrict__ a0,
+                                                  const TT* __restrict__ table, float* __restrict__ a0,
                                                   FeatLayout lay, uint32_t* __restrict__ idx_out) {
-  typedef typename FVec<F>::T V;
+  typedef typename TabVec<F, TT>::V TV;
+  typedef typename TV::T V;
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= n) return;
   const int l = level0 + (int)blockIdx.y;
@@ -118,13 +154,14 @@ __global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t 
   for (int cc = 0; cc < 8; ++cc) {
     const float w = corner_weight(lc, cc);
     float t[F];
-    FVec<F>::unpack(val[cc], t);
+    TV::unpack(val[cc], t);
 #pragma unroll
     for (int f = 0; f < F; ++f) acc[f] += w * t[f];
   }
   // a streaming store: the encodings are read by the next pass, while this one gathers from the level's
   // table in the L2 (3 % faster than a plain store at the benchmark shape)
-  store_stream(reinterpret_cast<V*>(a0 + l * lay.stride_l + b * lay.stride_b), FVec<F>::pack(acc));
+  store_stream(reinterpret_cast<typename FVec<F>::T*>(a0 + l * lay.stride_l + b * lay.stride_b),
+               FVec<F>::pack(acc));
   if (idx_out) {
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) idx_out[(b * c.L + l) * 8 + cc] = fb[cc];
@@ -604,21 +641,27 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   __syncthreads();
   const double inv = ldexp(1.0, -k);
   const int64_t base = ((int64_t)c.offset[l] + entry_lo) * F;
+  float* dst32 = static_cast<float*>(ap.dst);
+  _Float16* dst16 = static_cast<_Float16*>(ap.dst);
   for (int e = tid; e < count * F; e += 1024) {
     const int64_t gi = base + e;
     const float gsum = (float)((double)(long long)acc[e] * inv);
+    float pp = ap.dst_f16 ? (float)dst16[gi] : dst32[gi];
     if (MODE == BIN_GRAD || MODE == BIN_SGD) {
-      ap.dst[gi] += gsum;
+      pp = pp + gsum;
     } else {
       if (ap.g_tap) ap.g_tap[gi] = gsum;
-      float pp = ap.dst[gi], mm = ap.m[gi], vv = ap.v[gi];
+      float mm = ap.m[gi], vv = ap.v[gi];
       float mi = fmaf(1.0f - ap.beta1, gsum, ap.beta1 * mm);
       float vi = fmaf(1.0f - ap.beta2, gsum * gsum, ap.beta2 * vv);
       pp = pp - ap.lr_t * (mi / (sqrtf(vi) + ap.eps));
-      ap.dst[gi] = pp;
       ap.m[gi] = mi;
       ap.v[gi] = vi;
     }
+    if (ap.dst_f16)
+      dst16[gi] = (_Float16)pp;  // round to nearest even, once per entry and step
+    else
+      dst32[gi] = pp;
   }
 }
 
@@ -710,17 +753,25 @@ hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_
   return hipGetLastError();
 }
 
-hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* table, float* a0,
-                           const FeatLayout& lay, uint32_t* idx_out, hipStream_t st) {
-  if (n <= 0) return hipSuccess;
+template <typename TT>
+static hipError_t launch_hash_fwd_t(const DevCfg& c, const PosSrc& src, int64_t n, const TT* table, float* a0,
+                                    const FeatLayout& lay, uint32_t* idx_out, hipStream_t st) {
   const dim3 grid((unsigned)((n + 255) / 256), (unsigned)c.L), block(256);
   switch (c.F) {
-    case 1: hipLaunchKernelGGL(k_hash_fwd<1>, grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
-    case 2: hipLaunchKernelGGL(k_hash_fwd<2>, grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
-    case 4: hipLaunchKernelGGL(k_hash_fwd<4>, grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
+    case 1: hipLaunchKernelGGL((k_hash_fwd<1, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
+    case 2: hipLaunchKernelGGL((k_hash_fwd<2, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
+    case 4: hipLaunchKernelGGL((k_hash_fwd<4, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const void* table, float* a0,
+                           const FeatLayout& lay, uint32_t* idx_out, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  if (c.table_f16)
+    return launch_hash_fwd_t(c, src, n, static_cast<const _Float16*>(table), a0, lay, idx_out, st);
+  return launch_hash_fwd_t(c, src, n, static_cast<const float*>(table), a0, lay, idx_out, st);
 }
 
 BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {

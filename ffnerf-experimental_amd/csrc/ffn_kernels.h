@@ -127,7 +127,8 @@ struct BinScratch {
 };
 
 struct BinApply {
-  float* dst;  // grad (BIN_GRAD), table (BIN_SGD, BIN_ADAM)
+  void* dst;   // grad (BIN_GRAD), table (BIN_SGD, BIN_ADAM): float, or binary16 when dst_f16
+  int dst_f16;
   float* m;
   float* v;
   float* g_tap;  // optional: the summed table gradient (BIN_ADAM)
@@ -143,7 +144,8 @@ hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays,
                          const uint32_t* occ_in, int do_train, float* Ts, float* DTs, uint32_t* flags,
                          hipStream_t st);
 
-hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* table, float* a0,
+// table: float, or binary16 when c.table_f16 (widened exactly; the sums are the same fp32 operations)
+hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const void* table, float* a0,
                            const FeatLayout& lay, uint32_t* idx_out, hipStream_t st);
 // BIN_GRAD: dst += scatter(g); BIN_SGD: table += scatter(-lr 2^(-0.1 l) 0.5 g) (reference SGD);
 // BIN_ADAM: Adam on the table with the scattered gradient

@@ -19,6 +19,7 @@ BIAS_NAMES = ["bd_0", "bd_1", "bd_2", "bd_out", "bc_0", "bc_1", "bc_2", "bc_3", 
 BG = {"black": 0, "white": 1, "random": 2}
 HASH_OPT = {"sgd": 0, "adam": 1}
 MLP_PRECISION = {"fp32": 0, "fp16": 1}
+TABLE_DTYPE = {"fp32": 0, "fp16": 1}
 
 EXPORTS = [
     "ffn_version", "ffn_last_error", "ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step",
@@ -44,7 +45,7 @@ class FfnConfig(C.Structure):
         ("rho_min", C.c_float), ("rho_max", C.c_float), ("dt_min", C.c_float), ("dt_max", C.c_float),
         ("t_near", C.c_float), ("t_far", C.c_float),
         ("background", C.c_int32), ("hash_opt", C.c_int32), ("mlp_precision", C.c_int32),
-        ("reserved", C.c_int32 * 8),
+        ("table_dtype", C.c_int32), ("reserved", C.c_int32 * 7),
     ]
 
 
@@ -192,6 +193,8 @@ def make_config(spec: dict) -> FfnConfig:
     c.hash_opt = HASH_OPT[ho] if isinstance(ho, str) else int(ho)
     mp = spec.get("mlp_precision", 0)
     c.mlp_precision = MLP_PRECISION[mp] if isinstance(mp, str) else int(mp)
+    td = spec.get("table_dtype", 0)
+    c.table_dtype = TABLE_DTYPE[td] if isinstance(td, str) else int(td)
     return c
 
 

@@ -177,6 +177,7 @@ class ModelSpec:
     background: str = "black"   # training background: black | white | random
     hash_opt: str = "sgd"       # sgd (reference, in-step) | adam
     mlp_precision: str = "fp32"
+    table_dtype: str = "fp32"   # fp32 (reference) | fp16: the table's storage; its Adam state stays fp32
     init: str = "he"            # he (reference) | xavier
     beta1: float = 0.9
     beta2: float = 0.999
@@ -246,7 +247,7 @@ def spec_dict(spec: ModelSpec, occ: OccParams) -> dict:
         rho_min=float(occ.rho_min), rho_max=float(occ.rho_max), dt_min=float(occ.dt_min),
         dt_max=float(occ.dt_max), t_near=float(occ.t_near_clip), t_far=float(occ.t_far_clip),
         background=fl.BG[spec.background], hash_opt=fl.HASH_OPT[spec.hash_opt],
-        mlp_precision=fl.MLP_PRECISION[spec.mlp_precision],
+        mlp_precision=fl.MLP_PRECISION[spec.mlp_precision], table_dtype=fl.TABLE_DTYPE[spec.table_dtype],
     )
 
 
@@ -257,6 +258,8 @@ def init_params(spec: ModelSpec, occ: OccParams, rng: np.random.Generator) -> di
     p = {}
     n_tab = spec.table_entries() * spec.f_per_level
     p["table"] = rng.uniform(-1e-4, 1e-4, size=n_tab).astype(np.float32)
+    if spec.table_dtype == "fp16":  # the values a binary16 table holds (round to nearest even)
+        p["table"] = p["table"].astype(np.float16).astype(np.float32)
     for wn in fl.LAYER_NAMES:
         if wn not in shapes:
             continue
@@ -413,7 +416,9 @@ class Nerf:
         return self.spec.nc
 
     def _upload(self, host: dict):
-        self.t = {k: _dev_tensor(v, self.device) for k, v in host.items()}
+        f16 = self.spec.table_dtype == "fp16"
+        self.t = {k: _dev_tensor(v.astype(np.float16) if (k == "table" and f16) else v, self.device)
+                  for k, v in host.items()}
         self._rebind()
 
     def _rebind(self):
@@ -441,6 +446,7 @@ class Nerf:
         out = {}
         for k, v in self.t.items():
             out[k] = _to_numpy(v, np.uint32 if k.startswith("occ_") else None).copy()
+        out["table"] = out["table"].astype(np.float32)  # a binary16 table widens exactly
         return out
 
     def setup_buffers(self, num_rays: int, samples_per_ray: int, do_train=None):
@@ -568,6 +574,7 @@ class Nerf:
             level_log2_T=np.asarray(self.spec.log2_T[: self.spec.n_levels], np.int32),
             level_res=np.asarray(self.spec.res[: self.spec.n_levels], np.int32),
             n_levels=np.int32(self.spec.n_levels), hash_opt=np.array(self.spec.hash_opt),
+            table_dtype=np.array(self.spec.table_dtype),
             background=np.array(self.spec.background), init=np.array(self.spec.init),
             adam_beta1=np.float32(self.spec.beta1), adam_beta2=np.float32(self.spec.beta2),
             adam_eps=np.float32(self.spec.eps),
@@ -606,6 +613,7 @@ class Nerf:
             background=str(data["background"]) if "background" in data.files else self.spec.background,
             hash_opt=str(data["hash_opt"]) if "hash_opt" in data.files else "sgd",
             mlp_precision=self.spec.mlp_precision,
+            table_dtype=str(data["table_dtype"]) if "table_dtype" in data.files else "fp32",
             init=str(data["init"]) if "init" in data.files else "he",
             beta1=float(data["adam_beta1"]) if "adam_beta1" in data.files else self.spec.beta1,
             beta2=float(data["adam_beta2"]) if "adam_beta2" in data.files else self.spec.beta2,

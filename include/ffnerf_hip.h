@@ -52,6 +52,7 @@ enum {
 enum { FFN_BG_BLACK = 0, FFN_BG_WHITE = 1, FFN_BG_RANDOM = 2 };     /* -DBACKGROUND_COLOR */
 enum { FFN_HASH_SGD = 0, FFN_HASH_ADAM = 1 };                       /* table optimizer */
 enum { FFN_MLP_FP32 = 0, FFN_MLP_FP16 = 1 };                        /* MLP arithmetic */
+enum { FFN_TABLE_FP32 = 0, FFN_TABLE_FP16 = 1 };                    /* hash-table storage */
 
 /* Build-time constants of the reference (ffnerf_OG.cl:16-81,161-200;
  * ffnerf_tools.py:23-69; run_ffnerf_OG.py:1044-1057) as runtime values. */
@@ -68,7 +69,8 @@ typedef struct ffn_config {
   int32_t background;                   /* FFN_BG_* (training only; render is black) */
   int32_t hash_opt;                     /* FFN_HASH_* */
   int32_t mlp_precision;                /* FFN_MLP_* */
-  int32_t reserved[8];
+  int32_t table_dtype;                  /* FFN_TABLE_*: the table's storage (its Adam state stays fp32) */
+  int32_t reserved[7];
 } ffn_config;
 
 /* Caller-owned device buffers of one model.  Weights are row-major
@@ -81,7 +83,8 @@ typedef struct ffn_params {
   float* vW[FFN_N_LAYERS];
   float* mb[FFN_N_LAYERS];
   float* vb[FFN_N_LAYERS];
-  float* table;                         /* [sum_l 2^log2_T[l]][F] */
+  void* table;                          /* [sum_l 2^log2_T[l]][F]: float32, or IEEE binary16 when
+                                           table_dtype is FFN_TABLE_FP16 (updates round to nearest even) */
   float* m_table;                       /* Adam state, required for FFN_HASH_ADAM */
   float* v_table;
   uint32_t* occ_in;                     /* [G^3] 8 nibbles per word */
@@ -152,10 +155,12 @@ int ffn_sample(void* handle, const void* rays, uint32_t num_rays, uint32_t sampl
 int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint32_t* idx_out, void* stream);
 
 /* Scatter-add of the encoding gradient g [n][LF] of points x into grad
- * (table-shaped, caller-zeroed).  Non-finite gradients are skipped.  Stages g
+ * (table-shaped, caller-zeroed; of the table's storage type: with
+ * FFN_TABLE_FP16 each entry takes its exactly summed gradient in one
+ * round-to-nearest-even addition).  Non-finite gradients are skipped.  Stages g
  * level-major in the handle's scratch (n * LF floats), so calls on one handle
  * must not overlap. */
-int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n, float* grad, void* stream);
+int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n, void* grad, void* stream);
 
 /* Adam over n parameters (weight_update.cl:177-201 form).  If zero_grad,
  * g is cleared after it is read. */

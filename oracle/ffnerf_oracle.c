@@ -75,6 +75,9 @@ typedef struct {
   float rho_min, rho_max, dt_min, dt_max, t_near, t_far;
   int32_t background;                /* 0 black, 1 white, 2 random (train only) */
   int32_t hash_opt;                  /* 0 reference SGD in the step, 1 Adam */
+  int32_t table_f16;                 /* the table is stored as IEEE binary16 (values here are its exact
+                                        float32 widenings; every update rounds to nearest even, once per
+                                        entry and step) */
 } ora_cfg;
 
 typedef struct {
@@ -130,6 +133,54 @@ typedef struct {
 
 /* ------------------------------------------------------------------ */
 /* integer helpers (ffnerf_OG.cl:293-311, decay_occ_grid_in-st.cl:2-10) */
+
+/* ------------------------------------------------------------------ */
+/* IEEE 754 binary16 rounding (round to nearest, ties to even), from   */
+/* the format's definition: 1 sign, 5 exponent (bias 15), 10 fraction  */
+/* bits; subnormals in units of 2^-24; overflow at 65520 to infinity.  */
+
+uint16_t ora_f32_to_f16_bits(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x7F800000u) /* infinity, NaN (quiet, payload kept where it fits) */
+    return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? (0x200u | ((ax >> 13) & 0x3FFu)) : 0u));
+  if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* >= 65520: rounds to infinity */
+  if (ax < 0x38800000u) {                                  /* below 2^-14: subnormal (or zero) */
+    float a;
+    memcpy(&a, &ax, 4);
+    const float units = a * 16777216.0f; /* |f| / 2^-24, exact */
+    float m = floorf(units);
+    const float rem = units - m;
+    if (rem > 0.5f || (rem == 0.5f && fmodf(m, 2.0f) != 0.0f)) m += 1.0f;
+    return (uint16_t)(sign | (uint32_t)m); /* m = 1024 is the smallest normal, 0x0400 */
+  }
+  uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7FFFFFu) >> 13);
+  const uint32_t rem = ax & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u; /* a carry moves into the exponent */
+  return (uint16_t)(sign | h);
+}
+
+float ora_f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  uint32_t x;
+  if (e == 0) {
+    float v = (float)m * (1.0f / 16777216.0f);
+    memcpy(&x, &v, 4);
+  } else if (e == 31) {
+    x = 0x7F800000u | (m << 13);
+  } else {
+    x = ((e + 112u) << 23) | (m << 13);
+  }
+  x |= sign;
+  float r;
+  memcpy(&r, &x, 4);
+  return r;
+}
+
+float ora_f16_round(float f) { return ora_f16_bits_to_f32(ora_f32_to_f16_bits(f)); }
 
 /* thread count of the OpenMP build (the checker build has one) */
 void ora_set_threads(int n) {
@@ -1095,7 +1146,9 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
     gW[k] = (double*)calloc((size_t)odim[k] * idim[k], sizeof(double));
     gb[k] = (double*)calloc((size_t)odim[k], sizeof(double));
   }
-  double* gtab = (c->hash_opt == 1 && do_train) ? (double*)malloc(sizeof(double) * (size_t)table_n) : NULL;
+  /* the summed table gradient (Adam), or for a binary16 table the summed SGD update of each entry, added once */
+  const int sum_table = do_train && (c->hash_opt == 1 || c->table_f16);
+  double* gtab = sum_table ? (double*)malloc(sizeof(double) * (size_t)table_n) : NULL;
   if (gtab) {
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < table_n; ++i) gtab[i] = 0.0;
@@ -1252,6 +1305,9 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
             if (c->hash_opt == 1) {
               ORA_ATOMIC
               gtab[feat[cc] + (uint32_t)f] += (double)(g * w[cc]);
+            } else if (c->table_f16) {
+              ORA_ATOMIC
+              gtab[feat[cc] + (uint32_t)f] += (double)(-lr_lvl * 0.5f * g * w[cc]);
             } else {
               ORA_ATOMIC
               P->table[feat[cc] + (uint32_t)f] += -lr_lvl * 0.5f * g * w[cc];
@@ -1291,13 +1347,20 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
       free(gwf);
       free(gbf);
     }
-    if (gtab) {
+    if (gtab && c->hash_opt == 1) {
       float* gtf = (float*)malloc(sizeof(float) * (size_t)table_n);
 #pragma omp parallel for schedule(static)
       for (int64_t i = 0; i < table_n; ++i) gtf[i] = (float)gtab[i];
       if (dbg && dbg->g_table) memcpy(dbg->g_table, gtf, sizeof(float) * (size_t)table_n);
       ora_adam(P->table, P->m_table, P->v_table, gtf, table_n, sc->lr_t, sc->beta1, sc->beta2, sc->eps);
       free(gtf);
+      if (c->table_f16) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < table_n; ++i) P->table[i] = ora_f16_round(P->table[i]);
+      }
+    } else if (gtab) { /* binary16 table, reference SGD: each entry's summed update in one rounding */
+#pragma omp parallel for schedule(static)
+      for (int64_t i = 0; i < table_n; ++i) P->table[i] = ora_f16_round(P->table[i] + (float)gtab[i]);
     }
   }
   for (int k = 0; k < L_COUNT; ++k) { free(gW[k]); free(gb[k]); }

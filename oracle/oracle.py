@@ -44,7 +44,7 @@ class OraCfg(C.Structure):
         ("box_min", C.c_float * 3), ("box_max", C.c_float * 3),
         ("rho_min", C.c_float), ("rho_max", C.c_float), ("dt_min", C.c_float), ("dt_max", C.c_float),
         ("t_near", C.c_float), ("t_far", C.c_float),
-        ("background", C.c_int32), ("hash_opt", C.c_int32),
+        ("background", C.c_int32), ("hash_opt", C.c_int32), ("table_f16", C.c_int32),
     ]
 
 
@@ -94,6 +94,12 @@ def load(path: Path = None) -> C.CDLL:
         _build()
     lib = C.CDLL(str(path))
     lib.ora_set_threads.argtypes = [C.c_int]
+    lib.ora_f32_to_f16_bits.restype = C.c_uint16
+    lib.ora_f32_to_f16_bits.argtypes = [C.c_float]
+    lib.ora_f16_bits_to_f32.restype = C.c_float
+    lib.ora_f16_bits_to_f32.argtypes = [C.c_uint16]
+    lib.ora_f16_round.restype = C.c_float
+    lib.ora_f16_round.argtypes = [C.c_float]
     lib.ora_max_threads.restype = C.c_int
     lib.ora_hash_u32.restype = C.c_uint32
     lib.ora_hash_u32.argtypes = [C.c_uint32]
@@ -210,6 +216,8 @@ def make_cfg(spec: dict) -> OraCfg:
         setattr(c, k, float(spec[k]))
     c.background = int(spec.get("background", 0))
     c.hash_opt = int(spec.get("hash_opt", 0))
+    td = spec.get("table_dtype", 0)
+    c.table_f16 = 1 if td in (1, "fp16") else 0
     return c
 
 

@@ -23,11 +23,19 @@ def to_np(t, dtype=None):
     return a.view(dtype) if dtype is not None else a
 
 
+def table_f16(spec) -> bool:
+    return spec.get("table_dtype", 0) in (1, "fp16")
+
+
 class GpuModel:
+    """With an fp16 table (spec table_dtype), params["table"] holds binary16 values as float32: it is uploaded
+    as float16 (exactly) and state() widens it back."""
+
     def __init__(self, spec: dict, params: dict):
         self.spec = dict(spec)
         self.h = fl.Handle(spec)
-        self.t = {k: to_dev(v) for k, v in params.items()}
+        self.f16 = table_f16(spec)
+        self.t = {k: to_dev(v.astype(np.float16) if (k == "table" and self.f16) else v) for k, v in params.items()}
         P = fl.FfnParams()
         for i, (wn, bn) in enumerate(zip(fl.LAYER_NAMES, fl.BIAS_NAMES)):
             if wn in self.t:
@@ -47,7 +55,9 @@ class GpuModel:
 
     def state(self) -> dict:
         torch.cuda.synchronize()
-        return {k: to_np(v, np.uint32 if k.startswith("occ_") else None).copy() for k, v in self.t.items()}
+        out = {k: to_np(v, np.uint32 if k.startswith("occ_") else None).copy() for k, v in self.t.items()}
+        out["table"] = out["table"].astype(np.float32)
+        return out
 
     def train_step(self, rays, targets, S, scalars: dict, taps=False):
         rays_t = to_dev(np.ascontiguousarray(rays, np.float32).reshape(-1, 8))
@@ -79,7 +89,7 @@ class GpuModel:
                     tp.gW[i] = fl.ptr(td["g" + wn])
                     tp.gb[i] = fl.ptr(td["g" + bn])
             if self.spec.get("hash_opt", 0) == 1:
-                td["g_table"] = torch.zeros_like(self.t["table"])
+                td["g_table"] = torch.zeros(self.t["table"].shape, dtype=torch.float32, device=DEV)
                 tp.g_table = fl.ptr(td["g_table"])
         fl.check(self.lib.ffn_train_step(self.h.h, fl.ptr(rays_t), fl.ptr(tg_t), fl.ptr(out), N, S, C.byref(sc),
                                          C.byref(tp) if tp is not None else None, fl.stream_ptr()), "ffn_train_step")
@@ -116,11 +126,11 @@ class GpuModel:
     def encode_bwd(self, x, g, table_n):
         x_t = to_dev(np.ascontiguousarray(x, np.float32).reshape(-1, 3))
         g_t = to_dev(np.ascontiguousarray(g, np.float32))
-        grad = torch.zeros(table_n, dtype=torch.float32, device=DEV)
+        grad = torch.zeros(table_n, dtype=torch.float16 if self.f16 else torch.float32, device=DEV)
         fl.check(self.lib.ffn_hash_encode_bwd(self.h.h, fl.ptr(x_t), fl.ptr(g_t), x_t.shape[0], fl.ptr(grad),
                                               fl.stream_ptr()), "ffn_hash_encode_bwd")
         torch.cuda.synchronize()
-        return to_np(grad)
+        return to_np(grad).astype(np.float32)
 
     def bitfield(self, occ: np.ndarray, G: int, q_min: int) -> np.ndarray:
         occ_t = to_dev(np.ascontiguousarray(occ, np.uint32))

@@ -24,7 +24,11 @@ What is compared, and how every difference is accounted for:
   first moment);
 - reference SGD on the table: every entry within the tolerance of the largest
   update, plus the rounding of the restatement's one-at-a-time adds (n/2 + 1
-  ulps for n contributions).
+  ulps for n contributions);
+- binary16 tables (table_dtype fp16): both sides widen the stored values
+  exactly, so the encodings stay bit-exact; each entry's update is rounded to
+  nearest even once per step on both sides (Adam of the GPU's own gradient
+  bit for bit after that rounding; SGD within one binary16 ulp).
 """
 from __future__ import annotations
 
@@ -80,11 +84,13 @@ def _check_relu(spec, G, O, tol, stats):
     assert zrel <= tol["flip_z"], zrel
 
 
-def _check_adam(name, p0, m0, v0, g_gpu, g_ora, st_g, st_o, lr, sc, tol, frac, ora, stats):
+def _check_adam(name, p0, m0, v0, g_gpu, g_ora, st_g, st_o, lr, sc, tol, frac, ora, stats, f16=False):
     """p, m, v of the GPU = Adam(p0, m0, v0, g_gpu) exactly; against the restatement by count and size."""
     mk, vk = ("m_" + name, "v_" + name) if name == "table" else ("m" + name, "v" + name)
     pe, me, ve = p0.copy(), m0.copy(), v0.copy()
     ora.adam(pe, me, ve, np.ascontiguousarray(g_gpu, np.float32), lr, sc["beta1"], sc["beta2"], sc["eps"])
+    if f16:  # a binary16 table takes the update rounded to nearest even
+        pe = pe.astype(np.float16).astype(np.float32)
     assert np.array_equal(st_g[name].view(np.uint32), pe.view(np.uint32)), name
     assert np.array_equal(st_g[mk].view(np.uint32), me.view(np.uint32)), name
     assert np.array_equal(st_g[vk].view(np.uint32), ve.view(np.uint32)), name
@@ -92,7 +98,7 @@ def _check_adam(name, p0, m0, v0, g_gpu, g_ora, st_g, st_o, lr, sc, tol, frac, o
     g_ora = np.asarray(g_ora, np.float64).ravel()
     d_g = (st_g[name].astype(np.float64) - p0).ravel()
     d_o = (st_o[name].astype(np.float64) - p0).ravel()
-    ulp = np.spacing(np.abs(st_o[name]).astype(np.float32)).astype(np.float64).ravel()
+    ulp = np.spacing(np.abs(st_o[name]).astype(np.float16 if f16 else np.float32)).astype(np.float64).ravel()
     err = np.abs(d_g - d_o)
     out = err > tol * np.abs(d_o) + 4.0 * ulp  # updates that differ by more than the path's tolerance
     n_out = int(out.sum())
@@ -112,6 +118,9 @@ def compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
     docstring.  Returns (gpu model, oracle model, stats)."""
     prec = int(spec.get("mlp_precision", 0))
     tol = TOL[prec]
+    f16 = spec.get("table_dtype", 0) in (1, "fp16")
+    if f16:
+        assert np.array_equal(p["table"], p["table"].astype(np.float16).astype(np.float32)), "table not binary16"
     m = gh.GpuModel(spec, p)
     o = ora.OracleModel(spec, {k: v.copy() for k, v in p.items()})
     out_g, G = m.train_step(rays, tg, S, sc, taps=True)
@@ -173,7 +182,7 @@ def compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
                         tol["undet_frac"], ora, stats)
     if hash_adam:
         _check_adam("table", p["table"], p["m_table"], p["v_table"], G["g_table"], O["g_table"], st_g, st_o,
-                    float(lr_t), sc, tol["table"], tol["undet_frac"], ora, stats)
+                    float(lr_t), sc, tol["table"], tol["undet_frac"], ora, stats, f16=f16)
     else:
         # reference SGD: the update is linear in the gradient.  The restatement adds every (sample, corner)
         # contribution to the float table one at a time, as the reference's atomics do, rounding each time at
@@ -183,6 +192,12 @@ def compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
         d_o = st_o["table"].astype(np.float64) - p["table"]
         big = np.maximum(np.abs(p["table"]), np.abs(st_o["table"])).astype(np.float32)
         ulp = np.spacing(big).astype(np.float64)
+        if f16:  # both add each entry's summed update once, rounding to binary16: one ulp of binary16 apart
+            err = np.abs(d_g - d_o)
+            lim = tol["table"] * np.abs(d_o).max() + np.spacing(big.astype(np.float16)).astype(np.float64)
+            stats["table_sgd"] = float(err.max() / (np.abs(d_o).max() + 1e-30))
+            assert (err <= lim).all(), stats["table_sgd"]
+            return m, o, stats
         x = (rays[:, None, :3] + G["Ts"].reshape(-1, S)[:, :, None] * rays[:, None, 4:7]).astype(np.float32)
         _, idx, _ = ora.hash_encode(o.cfg, p["table"], x.reshape(-1, 3), with_idx=True)
         F = int(spec["f_per_level"])

@@ -472,3 +472,59 @@ def test_headline_shape_sixteen_steps(gh, ora, mlp_precision):
     assert (state["occ_in"] != state["occ_st"]).sum() > 100  # the merge path of the decay
     assert np.array_equal(gh.to_np(gi, np.uint32), oi)
     assert np.array_equal(gh.to_np(gs, np.uint32), os_)
+
+
+def _f16_params(spec, seed, **kw):
+    p = random_params(spec, seed=seed, **kw)
+    p["table"] = p["table"].astype(np.float16).astype(np.float32)  # binary16 values (stored exactly as fp16)
+    return p
+
+
+@pytest.mark.parametrize("which", ["cfg0", "cfg3"])
+def test_hash_fp16_table_forward_bit_exact(gh, ora, which):
+    """A binary16 table widens exactly: the encodings and indices are bit-identical to
+    the oracle's over the same values."""
+    print(f"[case] hash fwd fp16 table {which}", flush=True)
+    spec = spec_cfg0(table_dtype=1) if which == "cfg0" else spec_cfg1(table_dtype=1, log2_T=[22] * 16)
+    p = _f16_params(spec, seed=211)
+    m = gh.GpuModel(spec, p)
+    rng = np.random.default_rng(212)
+    x = rng.uniform(-0.05, 1.05, (20000, 3)).astype(np.float32)
+    x[:16] = 1.0
+    a0_g, idx_g = m.encode(x, with_idx=True)
+    a0_o, idx_o, _ = ora.hash_encode(ora.make_cfg(spec), p["table"], x, with_idx=True)
+    assert np.array_equal(idx_g, idx_o)
+    assert np.array_equal(a0_g.view(np.uint32), a0_o.view(np.uint32))
+
+
+@pytest.mark.parametrize("which", ["cfg0", "cfg3"])
+def test_hash_fp16_table_backward(gh, ora, which):
+    """The scatter into a binary16 gradient table: every entry is its exact sum rounded once to nearest even,
+    so it is within one binary16 ulp of the oracle's float64 sum (and the touched entries agree)."""
+    print(f"[case] hash bwd fp16 table {which}", flush=True)
+    spec = spec_cfg0(table_dtype=1) if which == "cfg0" else spec_cfg1(table_dtype=1, log2_T=[22] * 16)
+    m = gh.GpuModel(spec, _f16_params(spec, seed=221))
+    rng = np.random.default_rng(222)
+    n = 30000
+    x = rng.uniform(0, 1, (n, 3)).astype(np.float32)
+    LF = spec["n_levels"] * spec["f_per_level"]
+    g = rng.normal(size=(n, LF)).astype(np.float32)
+    grad_g = m.encode_bwd(x, g, table_floats(spec)).astype(np.float64)
+    grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
+    with np.errstate(over="ignore"):
+        ulp16 = np.spacing(np.abs(grad_o).astype(np.float16)).astype(np.float64)
+    err = np.abs(grad_g - grad_o)
+    assert (err <= ulp16 + 1e-6 * np.abs(grad_o).max()).all(), float((err - ulp16).max())
+    assert ((grad_g != 0) == (grad_o != 0)).mean() > 0.9999
+
+
+@pytest.mark.parametrize("hash_opt,mlp_precision", [(1, 0), (0, 0), (1, 1)])
+def test_train_step_fp16_table(gh, ora, hash_opt, mlp_precision):
+    """Training steps on a binary16 table (Adam with fp32 moments, or the reference SGD), fp32 and fp16 MLPs,
+    against the oracle's binary16 table semantics (tests/parity.py)."""
+    print(f"[case] train step fp16 table hash_opt={hash_opt} mlp={mlp_precision}", flush=True)
+    spec = spec_cfg0(hash_opt=hash_opt, mlp_precision=mlp_precision, table_dtype=1)
+    p = _f16_params(spec, seed=231)
+    rays = look_at_rays(96, spec, seed=232, miss_frac=0.1)
+    m, o = _compare_step(spec, p, rays, sphere_targets(rays, spec), 64, default_scalars(lr=0.05), gh, ora)
+    assert not np.array_equal(m.state()["table"], p["table"])

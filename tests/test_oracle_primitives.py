@@ -206,3 +206,26 @@ def test_adam_step_one_closed_form(ora):
     exp = p0 - lr * (1 - b1) * g / (np.sqrt((1 - b2) * g.astype(np.float64) ** 2) + eps)
     assert np.allclose(p, exp, rtol=1e-6, atol=1e-7)
     assert np.allclose(m, (1 - b1) * g, rtol=1e-6)
+
+
+def test_binary16_rounding_matches_numpy(ora):
+    """The oracle's float32 -> binary16 rounding (fp16 tables) against numpy's astype(float16), which rounds
+    to nearest even: every finite half round-trips, the midpoints between neighbours (ties) go to the even
+    one, and random floats over the whole range (subnormals, overflow to infinity) agree."""
+    lib = ora.lib()
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    h = bits.view(np.float16)
+    finite = np.isfinite(h)
+    f32 = h.astype(np.float32)
+    for b, v in zip(bits[finite], f32[finite]):
+        assert lib.ora_f32_to_f16_bits(float(v)) == int(b)
+        assert np.float32(lib.ora_f16_bits_to_f32(int(b))).view(np.uint32) == v.view(np.uint32)
+    pos = np.sort(f32[finite & (f32 >= 0)]).astype(np.float64)
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)          # exact in float32
+    rng = np.random.default_rng(7)
+    rand = np.concatenate([rng.uniform(-7e4, 7e4, 20000), rng.standard_normal(20000) * 1e-5,
+                           rng.standard_normal(20000) * 1e-7, [65519.99, 65520.0, -65520.0, 1e-8, 5.96e-8, 2.98e-8]])
+    for v in np.concatenate([mids, -mids[:2000], rand.astype(np.float32)]):
+        with np.errstate(over="ignore"):  # values past 65520 become infinity, as intended
+            want = np.float32(v).astype(np.float16).view(np.uint16)
+        assert lib.ora_f32_to_f16_bits(float(v)) == int(want), v
