@@ -4,9 +4,10 @@ Counterpart of the reference's ffnerf_cli.py (ffnerf_cli.py:1-86): the same
 commands, flags and checks -- --config, --steps (positive), --model-id
 (restricted characters), --resume, --no-web, --output (must not exist); train
 refuses to overwrite existing checkpoints of a model id unless --resume is
-given and writes the resolved config next to them.  `snapshot` renders one
-training view with the trained model (forward-only step) to a PNG; the
-interactive `review` viewer is not part of this build.
+given and writes the resolved config next to them.  Here each command is a
+handler in a table; `inspect` prints a report of the scene as aligned rows;
+`snapshot` renders one training view with the trained model (forward-only
+step) to a PNG.  The interactive `review` viewer is not part of this build.
 """
 from __future__ import annotations
 
@@ -23,28 +24,44 @@ if str(HERE) not in sys.path:
 import numpy as np
 
 from scene_config import MODEL_ID_CHARS, load_config
-from sfm_data import image_geometry, read_scene, scaled_intrinsics, scene_bounds
+from sfm_data import image_geometry, open_reconstruction, read_scene, scaled_intrinsics, scene_bounds
+
+
+def scene_report(cfg) -> list:
+    """(label, value) rows describing the configured scene: cameras, image sizes, the training images'
+    memory, the intrinsics at the training size, the scene box and how much of the sparse cloud it holds,
+    and the range of camera positions.  Every image must decode to one common size."""
+    rec = open_reconstruction(cfg["data"])
+    sizes = {}
+    for path in rec.image_paths:
+        img, train_wh = image_geometry(path, cfg["data"])
+        sizes.setdefault(img.shape[:2], path)
+        if len(sizes) > 1:
+            raise ValueError(f"Inconsistent image dimensions: {path}")
+    (h, w), = sizes.keys()
+    lo, hi = scene_bounds(cfg["scene"], rec.points)
+    centres = rec.c2w[:, :3, 3]
+    rows = [
+        ("registered cameras", len(rec.image_paths)),
+        ("finite sparse points", len(rec.points)),
+        ("camera ids", rec.camera_ids.tolist()),
+        ("original image size", f"{w}x{h}"),
+        ("training image size", f"{train_wh[0]}x{train_wh[1]}"),
+        ("training RGB memory", f"{len(rec.image_paths) * train_wh[0] * train_wh[1] * 12 / 2 ** 30:.2f} GiB"),
+        ("training K", scaled_intrinsics(rec.K, (w, h), train_wh, cfg["data"]["sfm_max_side"]).tolist()),
+        ("scene box", json.dumps({"box_min": lo.tolist(), "box_max": hi.tolist()})),
+    ]
+    if len(rec.points):
+        rows.append(("sparse points inside box", f"{np.all((rec.points >= lo) & (rec.points <= hi), axis=1).mean():.1%}"))
+    rows.append(("camera positions", f"{centres.min(axis=0).tolist()} .. {centres.max(axis=0).tolist()}"))
+    return rows
 
 
 def inspect(cfg) -> None:
-    paths, poses, K, indices, points = read_scene(cfg["data"])
-    lo, hi = scene_bounds(cfg["scene"], points)
-    first, wh = image_geometry(paths[0], cfg["data"])
-    h, w = first.shape[:2]
-    for path in paths[1:]:
-        image, _ = image_geometry(path, cfg["data"])
-        if image.shape[:2] != (h, w):
-            raise ValueError(f"Inconsistent image dimensions: {path}")
-    print(f"Registered cameras: {len(paths)}; finite sparse points: {len(points)}")
-    print(f"Original images: {w}x{h}; training images: {wh[0]}x{wh[1]}")
-    print(f"Training RGB memory: {len(paths) * wh[0] * wh[1] * 12 / 1024 ** 3:.2f} GiB")
-    print("Camera IDs:", indices.tolist())
-    print("Training K:\n", scaled_intrinsics(K, (w, h), wh, cfg["data"]["sfm_max_side"]))
-    print("Scene bounds:", json.dumps({"box_min": lo.tolist(), "box_max": hi.tolist()}))
-    if len(points):
-        inside = np.all((points >= lo) & (points <= hi), axis=1).mean()
-        print(f"Sparse points inside box: {inside:.1%}")
-    print("Camera position range:", poses[:, :3, 3].min(axis=0), poses[:, :3, 3].max(axis=0))
+    rows = scene_report(cfg)
+    width = max(len(k) for k, _ in rows)
+    for k, v in rows:
+        print(f"{k:<{width}}  {v}")
 
 
 def snapshot(cfg, output: Path, view: int = 0) -> Path:
@@ -79,53 +96,83 @@ def snapshot(cfg, output: Path, view: int = 0) -> Path:
     return output
 
 
-def main(argv=None) -> int:
-    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("command", choices=["inspect", "train", "snapshot"])
-    parser.add_argument("--config", required=True, type=Path)
-    parser.add_argument("--steps", type=int, help="Override the number of additional training steps")
-    parser.add_argument("--model-id", help="Override output/review model ID")
-    parser.add_argument("--resume", metavar="MODEL_ID", help="Continue weights and optimizer state from this ID")
-    parser.add_argument("--no-web", action="store_true", help="Accepted for compatibility (no preview server)")
-    parser.add_argument("--output", type=Path, help="Snapshot PNG path (must not already exist)")
-    parser.add_argument("--view", type=int, default=0, help="Snapshot: registered camera index")
-    args = parser.parse_args(argv)
-    cfg = load_config(args.config)
+def _parser() -> argparse.ArgumentParser:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("command", choices=sorted(COMMANDS))
+    p.add_argument("--config", required=True, type=Path)
+    p.add_argument("--steps", type=int, help="Override the number of additional training steps")
+    p.add_argument("--model-id", help="Override output/review model ID")
+    p.add_argument("--resume", metavar="MODEL_ID", help="Continue weights and optimizer state from this ID")
+    p.add_argument("--no-web", action="store_true", help="Accepted for compatibility (no preview server)")
+    p.add_argument("--output", type=Path, help="Snapshot PNG path (must not already exist)")
+    p.add_argument("--view", type=int, default=0, help="Snapshot: registered camera index")
+    return p
+
+
+class UsageError(Exception):
+    pass
+
+
+def _overrides(cfg, args) -> None:
+    """Command-line values over the config file (validated like the file's own)."""
     if args.steps is not None:
         if args.steps <= 0:
-            parser.error("--steps must be positive")
+            raise UsageError("--steps must be positive")
         cfg["training"]["steps"] = args.steps
     if args.model_id:
-        if any(ch not in MODEL_ID_CHARS for ch in args.model_id):
-            parser.error("Invalid --model-id")
+        if not set(args.model_id) <= set(MODEL_ID_CHARS):
+            raise UsageError("Invalid --model-id")
         cfg["training"]["model_id"] = args.model_id
     if args.no_web:
         cfg["preview"]["enabled"] = False
-    if args.command == "inspect":
-        inspect(cfg)
-        return 0
+
+
+def _stamp() -> str:
+    return datetime.now().strftime("%Y%m%d-%H%M%S-%f")
+
+
+def cmd_inspect(cfg, args) -> None:
+    inspect(cfg)
+
+
+def cmd_snapshot(cfg, args) -> None:
     t = cfg["training"]
-    directory = Path(t["directory"])
-    if args.command == "snapshot":
-        output = args.output or directory / (
-            t["model_id"] + "_snapshot_" + datetime.now().strftime("%Y%m%d-%H%M%S-%f") + ".png")
-        if output.exists():
-            parser.error(f"Snapshot already exists: {output}")
-        print(f"Snapshot -> {snapshot(cfg, output, args.view)}")
-        return 0
-    if not args.resume and list(directory.glob(f"{t['model_id']}_weights_*.npz")):
-        parser.error("Checkpoints already exist for this model ID. Use --resume or choose a new --model-id.")
-    _, _, _, _, points = read_scene(cfg["data"])
-    lo, hi = scene_bounds(cfg["scene"], points)
-    cfg["scene"].update(box_min=lo.tolist(), box_max=hi.tolist())
-    directory.mkdir(parents=True, exist_ok=True)
-    stamp = datetime.now().strftime("%Y%m%d-%H%M%S-%f")
-    manifest = directory / f"{t['model_id']}_config_{stamp}.json"
+    out = args.output or Path(t["directory"]) / f"{t['model_id']}_snapshot_{_stamp()}.png"
+    if out.exists():
+        raise UsageError(f"Snapshot already exists: {out}")
+    print(f"Snapshot -> {snapshot(cfg, out, args.view)}")
+
+
+def cmd_train(cfg, args) -> None:
+    """A new model id must not have checkpoints yet (unless resuming); the scene box is resolved once and
+    the resolved config is written beside the checkpoints before training starts."""
+    t = cfg["training"]
+    run_dir = Path(t["directory"])
+    if args.resume is None and any(run_dir.glob(f"{t['model_id']}_weights_*.npz")):
+        raise UsageError("Checkpoints already exist for this model ID. Use --resume or choose a new --model-id.")
+    lo, hi = scene_bounds(cfg["scene"], open_reconstruction(cfg["data"]).points)
+    cfg["scene"]["box_min"], cfg["scene"]["box_max"] = lo.tolist(), hi.tolist()
+    run_dir.mkdir(parents=True, exist_ok=True)
+    manifest = run_dir / f"{t['model_id']}_config_{_stamp()}.json"
     manifest.write_text(json.dumps(cfg, indent=2) + "\n", encoding="utf-8")
     print(f"Resolved run config: {manifest}")
     import trainer
     res = trainer.train(cfg, load_id=args.resume)
     print(f"steps_trained={res['steps_trained']} loss log {res['loss_log']}")
+
+
+COMMANDS = {"inspect": cmd_inspect, "train": cmd_train, "snapshot": cmd_snapshot}
+
+
+def main(argv=None) -> int:
+    parser = _parser()
+    args = parser.parse_args(argv)
+    cfg = load_config(args.config)
+    try:
+        _overrides(cfg, args)
+        COMMANDS[args.command](cfg, args)
+    except UsageError as e:
+        parser.error(str(e))
     return 0
 
 

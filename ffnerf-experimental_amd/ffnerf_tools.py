@@ -14,6 +14,7 @@ Reference interface mirrored here (file:line in /root/reference):
 from __future__ import annotations
 
 import ctypes as C
+import shutil
 import time
 from dataclasses import dataclass, field
 from datetime import datetime
@@ -61,77 +62,61 @@ def default_ray_dtype() -> np.dtype:
 # rays
 
 
-def rays_targets_from_indices(im_idx, u_idx, v_idx, Ims, c2w_all, W, H, K=None):
-    """Pinhole rays (OpenCV camera: x right, y down, z forward) and targets
-    for pixels (u, v) of images im_idx; same semantics as the reference."""
-    im_idx = np.asarray(im_idx, dtype=np.int32)
-    u_idx = np.asarray(u_idx, dtype=np.int32)
-    v_idx = np.asarray(v_idx, dtype=np.int32)
-    n = im_idx.size
-    assert Ims.ndim == 4 and Ims.shape[1] == H and Ims.shape[2] == W, (Ims.shape, H, W)
-    assert c2w_all.shape[0] == Ims.shape[0]
-    if K is not None:
-        if K.ndim == 2:
-            fx, fy = float(K[0, 0]), float(K[1, 1])
-            cx, cy = float(K[0, 2]), float(K[1, 2])
-        else:
-            Ki = K[im_idx].astype(np.float32)
-            fx, fy, cx, cy = Ki[:, 0, 0], Ki[:, 1, 1], Ki[:, 0, 2], Ki[:, 1, 2]
-        x = (u_idx.astype(np.float32) + 0.5 - cx) / fx
-        y = (v_idx.astype(np.float32) + 0.5 - cy) / fy
-        z = np.ones((n,), dtype=np.float32)
-        rays_cam = np.stack([x, y, z], axis=1)
-    else:
-        px = u_idx.astype(np.float32) - (W / 2.0) + 0.5
-        py = v_idx.astype(np.float32) - (H / 2.0) + 0.5
-        pz = np.full((n,), np.sqrt(H * W), dtype=np.float32)
-        rays_cam = np.stack([px, py, pz], axis=1)
-    R = c2w_all[im_idx, :3, :3].astype(np.float32)
-    t = c2w_all[im_idx, :3, 3].astype(np.float32)
-    dirs = np.einsum("nij,nj->ni", R, rays_cam)
-    dirs /= (np.linalg.norm(dirs, axis=1, keepdims=True) + 1e-12).astype(np.float32)
-    rays = np.zeros((n,), dtype=ray_dtype)
+def camera_directions(u, v, W, H, K=None) -> np.ndarray:
+    """Camera-frame directions [n, 3] float32 through the centres of pixels (u, v), OpenCV axes (x right,
+    y down, z forward).  K: shared [3, 3], per-pixel [n, 3, 3], or None for the reference's focal-free
+    fallback, (u + 1/2 - W/2, v + 1/2 - H/2, sqrt(W H))."""
+    uc = np.asarray(u, np.float32).reshape(-1) + np.float32(0.5)
+    vc = np.asarray(v, np.float32).reshape(-1) + np.float32(0.5)
+    if K is None:
+        return np.stack([uc - W / 2.0, vc - H / 2.0, np.full(uc.shape, np.sqrt(H * W), np.float32)], axis=1)
+    K = np.asarray(K, np.float32)
+    fx, fy, cx, cy = K[..., 0, 0], K[..., 1, 1], K[..., 0, 2], K[..., 1, 2]
+    return np.stack([(uc - cx) / fx, (vc - cy) / fy, np.ones(uc.shape, np.float32)], axis=1)
+
+
+def world_rays(c2w, dirs_cam: np.ndarray) -> np.ndarray:
+    """Rays (ray_dtype) from camera-to-world transforms ([4, 4] shared or [n, 4, 4]) and camera-frame
+    directions: origin = the camera centre (w = 1), direction = R d normalised with +1e-12 (w = 0)."""
+    c2w = np.asarray(c2w, np.float32)
+    R, t = c2w[..., :3, :3], c2w[..., :3, 3]
+    d = np.einsum("...ij,...j->...i", R, dirs_cam, dtype=np.float32)
+    d /= np.linalg.norm(d, axis=1, keepdims=True) + np.float32(1e-12)
+    rays = np.zeros(dirs_cam.shape[0], dtype=ray_dtype)
     rays["o"][:, :3] = t
     rays["o"][:, 3] = 1.0
-    rays["d"][:, :3] = dirs
-    rays["d"][:, 3] = 0.0
-    rgb = Ims[im_idx, v_idx, u_idx, :3]
-    if rgb.dtype != np.float32:
-        rgb = rgb.astype(np.float32) / 255.0
-    targets = np.zeros((n, 4), dtype=np.float32)
-    targets[:, :3] = rgb
+    rays["d"][:, :3] = d
+    return rays
+
+
+def rays_targets_from_indices(im_idx, u_idx, v_idx, Ims, c2w_all, W, H, K=None):
+    """Training rays and targets for pixels (u, v) of images im_idx (ffnerf_tools.py:175-234 of the
+    reference): Ims [N, H, W, 3] (float in [0, 1], or 8-bit), c2w_all [N, 4, 4], K [3, 3], [N, 3, 3] or
+    None.  Targets are {rgb, 0}."""
+    im = np.asarray(im_idx, np.int32).reshape(-1)
+    u = np.asarray(u_idx, np.int32).reshape(-1)
+    v = np.asarray(v_idx, np.int32).reshape(-1)
+    assert Ims.ndim == 4 and Ims.shape[1:3] == (H, W), (Ims.shape, H, W)
+    assert len(c2w_all) == len(Ims)
+    K_pix = None if K is None else (K if np.ndim(K) == 2 else np.asarray(K)[im])
+    rays = world_rays(np.asarray(c2w_all)[im], camera_directions(u, v, W, H, K_pix))
+    targets = np.zeros((im.size, 4), np.float32)
+    rgb = Ims[im, v, u, :3]
+    targets[:, :3] = rgb if rgb.dtype == np.float32 else rgb.astype(np.float32) / 255.0
     return rays, targets
 
 
 def rays_from_rt_indices(RT, idx, idy, W, H, K=None):
-    RT = np.asarray(RT, dtype=np.float32)
+    """Rays of pixels (idx, idy) of one camera RT [4, 4] (camera-to-world), as the training rays are made
+    (ffnerf_tools.py:237-272 of the reference)."""
+    RT = np.asarray(RT, np.float32)
     if RT.shape != (4, 4):
         raise ValueError(f"RT must be shape (4,4), got {RT.shape}")
-    idx = np.asarray(idx, dtype=np.int32).reshape(-1)
-    idy = np.asarray(idy, dtype=np.int32).reshape(-1)
-    if idx.size != idy.size:
+    u = np.asarray(idx, np.int32).reshape(-1)
+    v = np.asarray(idy, np.int32).reshape(-1)
+    if u.size != v.size:
         raise ValueError("idx and idy must have the same length.")
-    n = idx.size
-    if K is None:
-        px = idx.astype(np.float32) - W / 2.0 + 0.5
-        py = idy.astype(np.float32) - H / 2.0 + 0.5
-        pz = np.full(n, np.sqrt(H * W), dtype=np.float32)
-    else:
-        px = (idx.astype(np.float32) + 0.5 - K[0, 2]) / K[0, 0]
-        py = (idy.astype(np.float32) + 0.5 - K[1, 2]) / K[1, 1]
-        pz = np.ones(n, dtype=np.float32)
-    rays_cam = np.stack([px, py, pz], axis=1)
-    R = RT[:3, :3].astype(np.float32)
-    t = RT[:3, 3].astype(np.float32)
-    dirs = rays_cam @ R.T
-    norms = np.linalg.norm(dirs, axis=1, keepdims=True).astype(np.float32)
-    dirs = dirs / (norms + 1e-12)
-    rays = np.zeros((n,), dtype=ray_dtype)
-    rays["o"][:, :3] = np.broadcast_to(t[None, :], (n, 3))
-    rays["o"][:, 3] = 1.0
-    rays["d"][:, :3] = dirs
-    rays["d"][:, 3] = 0.0
-    return rays
+    return world_rays(RT, camera_directions(u, v, W, H, K))
 
 
 def rays_as_array(rays) -> np.ndarray:
@@ -540,57 +525,58 @@ class Nerf:
         return ev
 
     # -- checkpoints (npz layout of ffnerf_tools.py:989-1189) --------------
-    def _model_paths(self, save_id: str):
-        td = self.training_dir
-        td.mkdir(parents=True, exist_ok=True)
-        pats = sorted(td.glob(f"{save_id}_weights_*.npz"))
-        return td / f"{save_id}_weights_latest.npz", pats
+    def _checkpoint_payload(self) -> dict:
+        """The npz contents: the reference's keys and int32 bit-pattern storage (ffnerf_tools.py:989-1086),
+        plus this build's per-level layout, options and the table's Adam state."""
+        st = self.host_state()
+        bits = lambda a: np.ascontiguousarray(a, np.float32).view(np.int32).reshape(-1)
+        sp, oc = self.spec, self.occ
+        payload = dict(
+            timestamp=datetime.now().strftime("%Y%m%d-%H%M%S"), model_id=self.model_id,
+            steps_trained=np.int32(self.steps_trained), transfer_fmt=np.array(self.transfer_fmt),
+            ND=np.int32(sp.nd), NC=np.int32(sp.nc), table_i=bits(st["table"]),
+            table_size_entries=np.int32(sp.table_entries()), table_f_per_level=np.int32(sp.f_per_level),
+            occ_grid_in_u32=st["occ_in"].astype(np.uint32), occ_grid_st_u32=st["occ_st"].astype(np.uint32),
+            G_occ=np.int32(oc.G_occ), box_min=np.asarray(oc.box_min, np.float32),
+            box_max=np.asarray(oc.box_max, np.float32),
+            level_log2_T=np.asarray(sp.log2_T[: sp.n_levels], np.int32),
+            level_res=np.asarray(sp.res[: sp.n_levels], np.int32), n_levels=np.int32(sp.n_levels),
+            hash_opt=np.array(sp.hash_opt), table_dtype=np.array(sp.table_dtype), background=np.array(sp.background),
+            init=np.array(sp.init), adam_beta1=np.float32(sp.beta1), adam_beta2=np.float32(sp.beta2),
+            adam_eps=np.float32(sp.eps), m_table_i=bits(st["m_table"]), v_table_i=bits(st["v_table"]),
+        )
+        for k in ("rho_min", "rho_max", "dt_min", "dt_max", "t_near_clip", "t_far_clip"):
+            payload[k] = np.float32(getattr(oc, k))
+        shapes = sp.layer_shapes()
+        names = sorted(list(shapes) + [fl.BIAS_NAMES[fl.LAYER_NAMES.index(wn)] for wn in shapes])
+        payload["active_params"] = np.array(names, dtype="U32")
+        for name in names:
+            for pre in ("", "m", "v"):
+                payload[f"{pre}{name}_i"] = bits(st[pre + name])
+        return payload
+
+    def _checkpoint_targets(self, min_new_file_seconds: float) -> list:
+        """Files one save writes.  `<id>_weights_latest.npz` always; a new `<id>_weights_<timestamp>.npz`
+        besides it unless the latest file is younger than min_new_file_seconds (so frequent saves refresh
+        one file while a history of snapshots accumulates at that spacing)."""
+        d = self.training_dir
+        d.mkdir(parents=True, exist_ok=True)
+        latest = d / f"{self.model_id}_weights_latest.npz"
+        try:
+            age = time.time() - latest.stat().st_mtime
+        except OSError:  # no latest file yet (or unreadable): start a new snapshot
+            age = float("inf")
+        if age < float(min_new_file_seconds):
+            return [latest]
+        return [d / f"{self.model_id}_weights_{datetime.now().strftime('%Y%m%d-%H%M%S')}.npz", latest]
 
     def save(self, min_new_file_seconds: int = 300) -> Path:
-        st = self.host_state()
-        latest_path, _ = self._model_paths(self.model_id)
-        now = time.time()
-        make_new = True
-        if latest_path.exists():
-            try:
-                make_new = (now - latest_path.stat().st_mtime) >= float(min_new_file_seconds)
-            except OSError:
-                make_new = True
-        ts = datetime.now().strftime("%Y%m%d-%H%M%S")
-        fname = (self.training_dir / f"{self.model_id}_weights_{ts}.npz") if make_new else latest_path
-        f2i = lambda a: np.ascontiguousarray(a, np.float32).view(np.int32).reshape(-1)
-        payload = dict(
-            timestamp=ts, model_id=self.model_id, steps_trained=np.int32(self.steps_trained),
-            transfer_fmt=np.array(self.transfer_fmt), ND=np.int32(self.spec.nd), NC=np.int32(self.spec.nc),
-            table_i=f2i(st["table"]), table_size_entries=np.int32(self.spec.table_entries()),
-            table_f_per_level=np.int32(self.spec.f_per_level),
-            occ_grid_in_u32=st["occ_in"].astype(np.uint32), occ_grid_st_u32=st["occ_st"].astype(np.uint32),
-            G_occ=np.int32(self.occ.G_occ), box_min=np.asarray(self.occ.box_min, np.float32),
-            box_max=np.asarray(self.occ.box_max, np.float32), rho_min=np.float32(self.occ.rho_min),
-            rho_max=np.float32(self.occ.rho_max), dt_min=np.float32(self.occ.dt_min),
-            dt_max=np.float32(self.occ.dt_max), t_near_clip=np.float32(self.occ.t_near_clip),
-            t_far_clip=np.float32(self.occ.t_far_clip),
-            # additions of this build: per-level layout and the table's Adam state
-            level_log2_T=np.asarray(self.spec.log2_T[: self.spec.n_levels], np.int32),
-            level_res=np.asarray(self.spec.res[: self.spec.n_levels], np.int32),
-            n_levels=np.int32(self.spec.n_levels), hash_opt=np.array(self.spec.hash_opt),
-            table_dtype=np.array(self.spec.table_dtype),
-            background=np.array(self.spec.background), init=np.array(self.spec.init),
-            adam_beta1=np.float32(self.spec.beta1), adam_beta2=np.float32(self.spec.beta2),
-            adam_eps=np.float32(self.spec.eps),
-            m_table_i=f2i(st["m_table"]), v_table_i=f2i(st["v_table"]),
-        )
-        shapes = self.spec.layer_shapes()
-        active = sorted([wn for wn in shapes] + [fl.BIAS_NAMES[fl.LAYER_NAMES.index(wn)] for wn in shapes])
-        payload["active_params"] = np.array(active, dtype="U32")
-        for name in active:
-            payload[name + "_i"] = f2i(st[name])
-            payload["m" + name + "_i"] = f2i(st["m" + name])
-            payload["v" + name + "_i"] = f2i(st["v" + name])
-        np.savez_compressed(fname, **payload)
-        if make_new:
-            np.savez_compressed(latest_path, **payload)
-        return fname
+        """Write a checkpoint; returns the file named for this save (the new snapshot, or the latest file)."""
+        targets = self._checkpoint_targets(min_new_file_seconds)
+        np.savez_compressed(targets[0], **self._checkpoint_payload())
+        for extra in targets[1:]:
+            shutil.copyfile(targets[0], extra)
+        return targets[0]
 
     def load_latest(self, load_id: str, push: bool = True) -> dict:
         td = self.training_dir

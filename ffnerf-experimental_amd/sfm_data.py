@@ -1,8 +1,9 @@
 """Reading the BA / SfM-stage-2 reconstruction archives and their images.
 
 Counterpart of the reference's sfm_data.py (read_scene, scene_bounds,
-image_geometry, scaled_intrinsics, load_images; sfm_data.py:1-110), with the
-same archive keys and validation:
+image_geometry, scaled_intrinsics, load_images; sfm_data.py:1-110): the same
+archive keys, filters and validation rules, organised here as one validator
+per archive part feeding a Reconstruction record.  Keys:
   img_paths, K (shared 3x3), c2w or RT + rt_dir ('c2w' / 'w2c'), optional
   posed / keep_mask filters, X or X_track + has_X sparse points,
   active_cam_global camera ids.
@@ -14,6 +15,7 @@ OpenCV (8-bit PNG only).
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
 from pathlib import Path, PureWindowsPath
 
 import numpy as np
@@ -30,79 +32,143 @@ def _load_archive(path: Path) -> dict:
                          f"store img_paths as a string array ({e})") from None
 
 
-def read_scene(data: dict):
-    """-> (image paths, c2w poses [n,4,4] float32, K [3,3], camera ids, finite sparse points [m,3])."""
-    path = Path(data["reconstruction"])
-    d = _load_archive(path)
-    paths = d["img_paths"]
-    n = len(paths)
-    keep = np.ones(n, dtype=bool)
+@dataclass
+class Reconstruction:
+    """The registered cameras of a BA / SfM-stage-2 archive."""
+    image_paths: list          # resolved image files, registered cameras only
+    c2w: np.ndarray            # [n, 4, 4] float32 camera-to-world (OpenCV camera axes)
+    K: np.ndarray              # [3, 3] float32 intrinsics shared by all cameras
+    camera_ids: np.ndarray     # [n] int32 global camera ids
+    points: np.ndarray         # [m, 3] float32 finite sparse points
+
+    def as_tuple(self):
+        return self.image_paths, self.c2w, self.K, self.camera_ids, self.points
+
+
+def _registered(d: dict, n: int) -> np.ndarray:
+    """Cameras kept by every filter the archive carries (posed, keep_mask)."""
+    masks = []
     for key in ("posed", "keep_mask"):
-        if key in d:
-            mask = np.asarray(d[key], dtype=bool)
-            if mask.shape != (n,):
-                raise ValueError(f"{key} must align with img_paths")
-            keep &= mask
+        if key not in d:
+            continue
+        m = np.asarray(d[key], dtype=bool)
+        if m.shape != (n,):
+            raise ValueError(f"{key} must align with img_paths")
+        masks.append(m)
+    keep = np.logical_and.reduce(masks) if masks else np.ones(n, dtype=bool)
     if not keep.any():
         raise ValueError("No registered cameras in reconstruction")
+    return keep
+
+
+# RT arrays are stored in either direction; rt_dir names it
+_TO_C2W = {"c2w": lambda m: m, "w2c": np.linalg.inv}
+
+
+def _camera_to_world(d: dict, n: int) -> np.ndarray:
     if "c2w" in d:
         poses = d["c2w"]
     else:
-        poses = d["RT"]
         direction = str(np.asarray(d["rt_dir"]).reshape(-1)[0]).lower()
-        if direction == "w2c":
-            poses = np.linalg.inv(poses)
-        elif direction != "c2w":
+        if direction not in _TO_C2W:
             raise ValueError(f"Unknown rt_dir: {direction}")
-    if poses.shape != (n, 4, 4):
+        poses = _TO_C2W[direction](d["RT"])
+    if np.shape(poses) != (n, 4, 4):
         raise ValueError("Camera transforms must align with img_paths and have shape (N,4,4)")
-    poses = np.asarray(poses[keep], dtype=np.float32)
-    if not np.isfinite(poses).all():
-        raise ValueError("Non-finite camera transforms")
+    return np.asarray(poses)
+
+
+def _shared_intrinsics(d: dict) -> np.ndarray:
     K = np.asarray(d["K"], dtype=np.float32)
-    if K.shape != (3, 3) or not np.isfinite(K).all() or K[0, 0] <= 0 or K[1, 1] <= 0:
+    ok = K.shape == (3, 3) and bool(np.isfinite(K).all()) and K[0, 0] > 0 and K[1, 1] > 0
+    if not ok:
         raise ValueError("Expected finite shared 3x3 intrinsics with positive focal lengths")
-    resolved = []
-    for stored in paths[keep]:
-        if data.get("images_dir"):
-            p = Path(data["images_dir"]) / PureWindowsPath(str(stored)).name
-        else:
-            p = Path(str(stored))
-            if not p.is_absolute():
-                p = path.parent / p
-        if not p.is_file():
-            raise FileNotFoundError(f"Image missing: {p}. Set data.images_dir to relocate images.")
-        resolved.append(p)
-    if "X" in d:
-        points = np.asarray(d["X"], dtype=np.float32).reshape(-1, 3)
-    elif "X_track" in d:
-        points = np.asarray(d["X_track"], dtype=np.float32).reshape(-1, 3)
-        if "has_X" in d:
-            points = points[np.asarray(d["has_X"], dtype=bool)]
+    return K
+
+
+def _locate_image(stored, archive_dir: Path, images_dir) -> Path:
+    """An image named in the archive: relocated by file name into data.images_dir when that is set (stored
+    Windows paths included), else taken as stored, relative to the archive."""
+    if images_dir:
+        found = Path(images_dir) / PureWindowsPath(str(stored)).name
     else:
-        points = np.empty((0, 3), np.float32)
-    points = points[np.isfinite(points).all(axis=1)]
+        found = Path(str(stored))
+        found = found if found.is_absolute() else archive_dir / found
+    if not found.is_file():
+        raise FileNotFoundError(f"Image missing: {found}. Set data.images_dir to relocate images.")
+    return found
+
+
+def _sparse_points(d: dict) -> np.ndarray:
+    """X, or X_track filtered by has_X; rows with a non-finite coordinate dropped."""
+    if "X" in d:
+        pts = np.asarray(d["X"], dtype=np.float32).reshape(-1, 3)
+    elif "X_track" in d:
+        pts = np.asarray(d["X_track"], dtype=np.float32).reshape(-1, 3)
+        if "has_X" in d:
+            pts = pts[np.asarray(d["has_X"], dtype=bool)]
+    else:
+        pts = np.empty((0, 3), np.float32)
+    return pts[np.isfinite(pts).all(axis=1)]
+
+
+def open_reconstruction(data: dict) -> Reconstruction:
+    archive = Path(data["reconstruction"])
+    d = _load_archive(archive)
+    stored = d["img_paths"]
+    n = len(stored)
+    keep = _registered(d, n)
+    c2w = np.asarray(_camera_to_world(d, n)[keep], dtype=np.float32)
+    if not np.isfinite(c2w).all():
+        raise ValueError("Non-finite camera transforms")
+    K = _shared_intrinsics(d)
+    paths = [_locate_image(p, archive.parent, data.get("images_dir")) for p in stored[keep]]
     ids = np.asarray(d.get("active_cam_global", np.arange(n)), dtype=np.int32)[keep]
-    return resolved, poses, K, ids, points
+    return Reconstruction(paths, c2w, K, ids, _sparse_points(d))
+
+
+def read_scene(data: dict):
+    """-> (image paths, c2w poses [n,4,4] float32, K [3,3], camera ids, finite sparse points [m,3])."""
+    return open_reconstruction(data).as_tuple()
+
+
+def _check_box(lo, hi):
+    lo, hi = np.asarray(lo, dtype=np.float32), np.asarray(hi, dtype=np.float32)
+    valid = lo.shape == (3,) and hi.shape == (3,) and bool(np.isfinite(lo).all() and np.isfinite(hi).all())
+    if not valid or not (hi > lo).all():
+        raise ValueError("Scene bounds must be finite xyz vectors with box_max > box_min")
+    return lo, hi
+
+
+def _cube_around(points: np.ndarray):
+    """A cube centred on the sparse points' 1 %/99 % percentile box, half-side 3/2 of the radius of the sphere
+    through that box's corners (at least 0.015): room around the reconstruction without chasing outliers."""
+    if not len(points):
+        raise ValueError("No finite sparse points: set scene.box_min and scene.box_max")
+    q = np.percentile(points, [1, 99], axis=0)
+    half = 1.5 * max(0.5 * float(np.linalg.norm(q[1] - q[0])), 0.01)
+    mid = q.mean(axis=0)
+    return mid - half, mid + half
 
 
 def scene_bounds(scene: dict, points: np.ndarray):
-    """Explicit box, or a cube around the sparse points: the sphere circumscribing their 1%/99%
-    percentile box, radius enlarged by 3/2 (the reference's rule, sfm_data.py:66-84)."""
+    """The scene box: scene.box_min/box_max when both are set, the cube around the sparse points when both
+    are null (sfm_data.py:58-76 of the reference gives the same rule)."""
     lo, hi = scene["box_min"], scene["box_max"]
-    if lo is None and hi is None:
-        if not len(points):
-            raise ValueError("No finite sparse points: set scene.box_min and scene.box_max")
-        q_lo, q_hi = np.percentile(points, [1, 99], axis=0)
-        center = 0.5 * (q_lo + q_hi)
-        radius = 1.5 * max(0.5 * float(np.linalg.norm(q_hi - q_lo)), 0.01)
-        lo, hi = center - radius, center + radius
-    elif lo is None or hi is None:
+    given = (lo is not None, hi is not None)
+    if given == (False, False):
+        lo, hi = _cube_around(points)
+    elif given != (True, True):
         raise ValueError("Set both scene.box_min and scene.box_max, or leave both null")
-    lo, hi = np.asarray(lo, dtype=np.float32), np.asarray(hi, dtype=np.float32)
-    if lo.shape != (3,) or hi.shape != (3,) or not np.isfinite([lo, hi]).all() or not (hi > lo).all():
-        raise ValueError("Scene bounds must be finite xyz vectors with box_max > box_min")
-    return lo, hi
+    return _check_box(lo, hi)
+
+
+def fit_within(w: int, h: int, max_side) -> tuple:
+    """Integer (w, h) with the longer side limited to max_side (0 = unlimited), never upscaled."""
+    if max_side <= 0:
+        return w, h
+    s = min(1.0, max_side / max(w, h))
+    return max(1, int(w * s)), max(1, int(h * s))
 
 
 def read_rgb(path) -> np.ndarray:
@@ -114,26 +180,20 @@ def read_rgb(path) -> np.ndarray:
 
 
 def image_geometry(path, data: dict):
-    """(image, training size (w, h)): the longer side is limited to data.max_side (0 = unlimited)."""
+    """(image, training size (w, h)): the image's size fit within data.max_side."""
     try:
         im = read_rgb(path)
     except (ValueError, OSError) as e:
         raise ValueError(f"Cannot decode image: {path} ({e})") from None
-    h, w = im.shape[:2]
-    max_side = data["max_side"]
-    scale = min(1.0, max_side / max(h, w)) if max_side > 0 else 1.0
-    return im, (max(1, int(w * scale)), max(1, int(h * scale)))
+    return im, fit_within(im.shape[1], im.shape[0], data["max_side"])
 
 
 def scaled_intrinsics(K, original_wh, target_wh, sfm_max_side):
-    """K of the SfM images (their longer side limited to sfm_max_side with integer sizes) mapped to target."""
-    w, h = original_wh
-    s = min(1.0, sfm_max_side / max(w, h)) if sfm_max_side > 0 else 1.0
-    sw, sh = max(1, int(w * s)), max(1, int(h * s))
-    out = np.asarray(K, np.float32).copy()
-    out[0] *= target_wh[0] / sw
-    out[1] *= target_wh[1] / sh
-    return out
+    """The archive's K belongs to the images SfM saw: the originals fit within sfm_max_side (the same integer
+    rule).  Rescale its focal and principal rows to the target size."""
+    sfm_w, sfm_h = fit_within(original_wh[0], original_wh[1], sfm_max_side)
+    return np.asarray(K, np.float32) * np.array([[target_wh[0] / sfm_w], [target_wh[1] / sfm_h], [1.0]],
+                                                np.float32)
 
 
 def _area_matrix(n_in: int, n_out: int) -> np.ndarray:

@@ -219,3 +219,36 @@ def test_full_batch_training_learns(torch, mlp):
     assert p > black + 10.0
     del nerf, pool
     torch.cuda.empty_cache()
+
+
+def test_reference_layout_checkpoint_loads_and_steps(torch, tmp_path):
+    """A checkpoint written in the reference's own npz layout (tests/golden/reference_checkpoint.py: its
+    compiled-in hash layout with F = 4, ND = NC = 2, no keys of this build) is loaded by Nerf.load_latest
+    and trained one step: the step matches the oracle from the same loaded state (tests/parity.py), and the
+    trainer's own step moves the parameters and keeps them finite."""
+    import sys
+    from pathlib import Path
+    import ffnerf_tools as ft
+    import gpu_helpers as gh
+    from common import look_at_rays, sphere_targets
+    from parity import compare_step
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import reference_checkpoint as rc
+    print("[case] reference-layout checkpoint", flush=True)
+    rc.write(tmp_path, "refckpt", seed=5)
+    nerf = ft.Nerf(tmp_path, "refckpt", load_id="refckpt")
+    assert nerf.spec.log2_T == rc.LEVEL_LOG2 and nerf.spec.f_per_level == 4 and nerf.steps_trained == 1234
+    before = nerf.host_state()
+    spec = ft.spec_dict(nerf.spec, nerf.occ)
+    rays = look_at_rays(64, spec, seed=6, miss_frac=0.1, radius=1.2)
+    tg = np.random.default_rng(7).uniform(0, 1, (64, 4)).astype(np.float32)
+    sc = default_scalars(lr=1e-3, lr_t=1e-3, beta2=0.999, eps=1e-6, occ_strength=0.0)
+    compare_step(spec, {k: v.copy() for k, v in before.items()}, rays, tg, 64, sc, gh, ora)
+    io = ft.RayBatch.init(64, 64)
+    io.upload_rays(rays)
+    io.upload_targets(tg)
+    nerf.step(io, lr_f=1e-3, do_train=True, occ_update_strength=0.0, sh_multiplier=1.0, color_MLP_rel_lr=1.0)
+    after = nerf.host_state()
+    assert nerf.steps_trained == 1235
+    for k in ("table", "Wd_in", "Wc_out", "bd_out"):
+        assert np.isfinite(after[k]).all() and not np.array_equal(after[k], before[k]), k

@@ -168,7 +168,11 @@ def test_synthetic_archive_reads_back(tmp_path, capsys):
     np.testing.assert_allclose(images[3], np.round(np.clip(sc.render_image(cams, 3), 0, 1) * 255) / 255,
                                atol=1e-6)
     assert ffnerf_cli.main(["inspect", "--config", str(path)]) == 0
-    assert "Registered cameras: 8" in capsys.readouterr().out
+    out = capsys.readouterr().out
+    rows = dict(ffnerf_cli.scene_report(cfg))
+    assert rows["registered cameras"] == 8 and rows["training image size"] == "64x64"
+    assert rows["sparse points inside box"] == "100.0%"
+    assert any(line.split() == ["registered", "cameras", "8"] for line in out.splitlines())
 
 
 def test_cli_checks(tmp_path):
@@ -186,3 +190,26 @@ def test_cli_checks(tmp_path):
     out.write_bytes(b"")
     with pytest.raises(SystemExit):
         ffnerf_cli.main(["snapshot", "--config", str(path), "--output", str(out)])
+
+
+def test_reference_checkpoint_layout_loads(tmp_path):
+    """A checkpoint in the reference's own layout (no keys of this build: reference hash layout, F = 4,
+    ND = NC = 2, int32 bit patterns) is read by Nerf.load_latest's parser into the reference shape, every
+    value bit for bit (the GPU test steps it)."""
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import reference_checkpoint as rc
+    path = rc.write(tmp_path, "refckpt", seed=3)
+    data = np.load(path, allow_pickle=False)
+    assert "level_log2_T" not in data.files and "m_table_i" not in data.files
+    nerf = ft.Nerf.__new__(ft.Nerf)  # the parser alone: no device
+    nerf.training_dir, nerf.spec, nerf.occ = tmp_path, ft.ModelSpec(), ft.OccParams()
+    host = nerf.load_latest("refckpt", push=False)
+    assert nerf.spec.log2_T == rc.LEVEL_LOG2 and nerf.spec.f_per_level == 4
+    assert (nerf.spec.nd, nerf.spec.nc, nerf.spec.hash_opt) == (2, 2, "sgd")
+    assert nerf.steps_trained == 1234 and nerf.occ.G_occ == rc.G_OCC
+    assert np.array_equal(host["table"].view(np.int32), data["table_i"])
+    for name in [str(x) for x in data["active_params"]]:
+        for pre in ("", "m", "v"):
+            assert np.array_equal(host[pre + name].reshape(-1).view(np.int32), data[pre + name + "_i"]), pre + name
+    assert not host["m_table"].any() and not host["v_table"].any()
+    assert np.array_equal(host["occ_in"], data["occ_grid_in_u32"])
