@@ -322,6 +322,83 @@ def shell_bitfield(R, seed=4, radius=0.3, thickness=0.02, noise=0.007):
     return bits, set_cells / R ** 3
 
 
+def ball_bitfield(R, radius=0.25):
+    """The synthetic scene's ball as an R^3 bitfield: the cells whose centre lies within radius plus one cell
+    diagonal of the box centre."""
+    c = (np.arange(R, dtype=np.float32) + 0.5) / R
+    bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
+    lim = radius + np.sqrt(3.0) / R
+    for z in range(R):
+        yy, xx = np.meshgrid(c, c, indexing="ij")
+        occ = (xx - 0.5) ** 2 + (yy - 0.5) ** 2 + (c[z] - 0.5) ** 2 <= lim * lim
+        idx = np.nonzero(occ.reshape(-1))[0].astype(np.int64) + z * R * R
+        np.bitwise_or.at(bits, idx >> 5, (np.uint32(1) << (idx & 31).astype(np.uint32)))
+    return bits
+
+
+def run_marched_train(args, pool_rays, pool_tg):
+    """The training step fed by the march (ffn_train_step_marched): the cfg2 model and batches (2^18 rays of
+    the ball scene per step), a 256^3 bitfield of the ball's cells, dt = sqrt(3)/1024, at most 1024 samples
+    per ray, compositing stopped at T < 1e-4.  Returns the measurement as a dict."""
+    import tempfile
+    import torch
+    import ffnerf_tools as ft
+    spec, occ, _ = cfg2_spec("fp32")
+    nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_benchm_"), "benchm", spec=spec, occ=occ, rng_seed=0)
+    R, max_steps = 256, 1024
+    dt = float(np.float32(np.sqrt(3.0) / max_steps))
+    bits = torch.from_numpy(ball_bitfield(R).view(np.int32)).cuda()
+    n_rays = pool_rays[0].shape[0]
+    pool = []
+    for rays, tg in zip(pool_rays, pool_tg):
+        io = ft.RayBatch.init(n_rays, 1)
+        io.upload_rays(rays)
+        io.upload_targets(tg)
+        pool.append(io)
+    used = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    one = lambda i: nerf.step_marched(pool[i % len(pool)], 1e-2, bits, R, dt, max_steps=max_steps, T_stop=1e-4,
+                                      n_samples=used)
+    steps = max(1, args.steps // 2)
+    for i in range(args.warmup):
+        one(i)
+    nerf.handle.set_profiling(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        one(args.warmup + i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    composited = int(used.sum().item())  # of the last step
+    stages, ms_prof = profiled_pass(nerf, one, args.warmup + steps, steps)
+    avg = {("march" if k == "sample" else k): (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
+    # samples marched per step (the MLP's work): one march of the same batches
+    import ctypes as C
+    import ffn_lib as fl
+    mp = fl.march_params(R, dt, max_steps)
+    counts = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    offs = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    total = torch.zeros(4, dtype=torch.int32, device="cuda")
+    marched = []
+    for io in pool:
+        fl.check(nerf.handle.lib.ffn_march(nerf.handle.h, fl.ptr(io.rays_buf), n_rays, fl.ptr(bits), C.byref(mp),
+                                           fl.ptr(counts), fl.ptr(offs), None, None, 0, fl.ptr(total),
+                                           fl.stream_ptr()))
+        torch.cuda.synchronize()
+        marched.append(int(total[0].item()))
+    ms = (t1 - t0) * 1e3 / steps
+    n_avg = float(np.mean(marched))
+    fwd_b, bwd_b, mlp_flops, _ = algorithmic(spec)
+    del nerf
+    return {"ms_per_step": ms, "rays": n_rays, "samples_marched_avg": n_avg, "samples_composited_last": composited,
+            "value": n_avg / (ms * 1e-3), "unit": "marched samples/s",
+            "rays_per_s": n_rays / (ms * 1e-3), "steps": steps, "profiled_ms_per_step": ms_prof,
+            "stages_ms_avg": {k: round(v, 4) for k, v in avg.items()},
+            "hash_grid_gbs": (fwd_b + bwd_b) * n_avg / ((avg["hash_fwd"] + avg["hash_bwd"]) * 1e-3) / 1e9,
+            "config": "cfg2 model and ray batches (ball scene), 256^3 bitfield of the ball (r 0.25 + one cell "
+                      "diagonal), dt sqrt(3)/1024, <= 1024 samples/ray, T_stop 1e-4; stage 'march' = march count, "
+                      "scan, host wait, emit; 'mlp' = forward, compositing, backward"}
+
+
 def run_cfg4(args):
     """256^3 bitfield (~3% set, shell), 2^20 rays, <= 1024 steps/ray, early termination at
     T < 1e-4, cfg1 MLPs (forward render); and Adam over 16 x 2^22 x 2 table params with sparse gradients."""
@@ -388,6 +465,17 @@ def run_cfg4(args):
                       "bytes": "40 B/ray (ray + offset, count) + 20 B/sample (xyz t + ray id)"},
             "adam": {"ms": t_a, "params": n_par, "GBps": 28 * n_par / (t_a * 1e-3) / 1e9,
                      "frac": 28 * n_par / (t_a * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+    if not args.no_marched_train:
+        del nerf, io
+        cams = sc.cameras_for("cfg2")
+        rng2 = np.random.default_rng(123)
+        pr, pt = [], []
+        for _ in range(4):
+            r_, t_ = sc.uniform_batch(cams, 1 << 18, rng2)
+            pr.append(r_)
+            pt.append(t_)
+        print("[bench] marched training step", flush=True)
+        line["train_marched"] = run_marched_train(args, pr, pt)
     print(json.dumps(line), flush=True)
     return line
 
@@ -407,6 +495,7 @@ def main():
     ap.add_argument("--table-dtypes", default="fp32,fp16", help="cfg3 table types")
     ap.add_argument("--rays4", type=int, default=1 << 20, help="cfg4 rays")
     ap.add_argument("--chunk", type=int, default=64, help="cfg4 samples per ray per render round")
+    ap.add_argument("--no-marched-train", action="store_true", help="cfg4: skip the marched training step")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this size (a known-traffic kernel for PMC scaling)")
     args = ap.parse_args()

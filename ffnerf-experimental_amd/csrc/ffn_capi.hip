@@ -79,6 +79,8 @@ struct Handle {
   Scratch bin_meta, bin_meta_t, bin_pairs, bin_max;
   // marcher / render
   Scratch m_state, m_acc, m_counts, m_offsets, m_sums, m_total, m_samples, m_ids, m_a0, m_sigma, m_rgb;
+  // marched training
+  Scratch m_Tr, m_dLds, m_dLdc;
   uint32_t* host_total = nullptr;  // pinned
 };
 
@@ -343,7 +345,7 @@ int ffn_destroy(void* handle) {
   h->bin_pairs.release();
   h->bin_max.release();
   for (Scratch* sc : {&h->m_state, &h->m_acc, &h->m_counts, &h->m_offsets, &h->m_sums, &h->m_total, &h->m_samples,
-                      &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb})
+                      &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb, &h->m_Tr, &h->m_dLds, &h->m_dLdc})
     sc->release();
   if (h->host_total) (void)hipHostFree(h->host_total);
   delete h;
@@ -702,6 +704,203 @@ int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const u
   a.ray_ids = ray_ids;
   a.capacity = capacity;
   FFN_HIP(ffn::launch_march(a, true, st));
+  return 0;
+}
+
+int ffn_train_step_marched(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
+                           const uint32_t* bits, const ffn_march_params* mp, const ffn_step_scalars* sc,
+                           const ffn_taps* taps, uint32_t* n_samples, void* stream) {
+  Handle* h = as_handle(handle);
+  int rc = check_march(h, rays, bits, mp);
+  if (rc) return rc;
+  if (!h->bound) return fail(-1, "ffn_bind_params must be called before ffn_train_step_marched");
+  if (!sc || !targets || !out_rgb) return fail(-1, "NULL scalars/targets/out_rgb");
+  if (num_rays == 0) return fail(-1, "num_rays must be > 0");
+  if (!sc->do_train) return fail(-1, "ffn_train_step_marched trains; ffn_render is the marched forward render");
+  if (!(mp->T_stop >= 0.0f && mp->T_stop < 1.0f)) return fail(-1, "T_stop must be in [0,1)");
+  if ((uint64_t)num_rays * mp->max_steps >= ((uint64_t)1 << 32))
+    return fail(-1, "num_rays * max_steps must stay below 2^32 samples");
+  const int LF = h->dc.LF;
+  if (h->cfg.mlp_precision != FFN_MLP_FP32)
+    return fail(-2, "ffn_train_step_marched: only the fp32 MLP path is built for marched training");
+  if (!ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
+    return fail(-2, "MLP shape LF=%d nd=%d nc=%d is not built", LF, h->cfg.nd, h->cfg.nc);
+  if (!ffn::scatter_supported(h->dc))
+    return fail(-2, "ffn_train_step_marched: the scatter is not built for this table shape (F=%d with %u-entry "
+                    "levels)", h->dc.F, max_level_entries(h->dc));
+  hipStream_t st = (hipStream_t)stream;
+  const ffn_params& P = h->params;
+
+  // 1. march: count, scan (the step's sample count comes back to size the launches), emit
+  const size_t n1 = (size_t)num_rays + 1;
+  FFN_HIP(h->m_counts.ensure(sizeof(uint32_t) * n1));
+  FFN_HIP(h->m_offsets.ensure(sizeof(uint32_t) * n1));
+  FFN_HIP(h->m_sums.ensure(sizeof(uint32_t) * ((n1 + 4095) / 4096 + 1)));
+  FFN_HIP(h->m_total.ensure(sizeof(uint32_t) * 4));
+  if (!h->host_total) FFN_HIP(hipHostMalloc((void**)&h->host_total, sizeof(uint32_t) * 4, hipHostMallocDefault));
+  uint32_t* counts = (uint32_t*)h->m_counts.p;
+  uint32_t* off = (uint32_t*)h->m_offsets.p;
+  ffn::MarchArgs ma = march_args(h, rays, num_rays, bits, mp);
+  ma.counts = counts;
+  int64_t n = 0;
+  {
+    StageTimer tm(h, 0, st);
+    FFN_HIP(ffn::launch_march(ma, false, st));
+    FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, (uint32_t*)h->m_total.p, st));
+    FFN_HIP(hipMemcpyAsync(h->host_total, h->m_total.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    FFN_HIP(hipStreamSynchronize(st));
+    n = *h->host_total;
+    FFN_HIP(h->m_samples.ensure(sizeof(float4) * (size_t)(n > 0 ? n : 1)));
+    FFN_HIP(h->m_ids.ensure(sizeof(uint32_t) * (size_t)(n > 0 ? n : 1)));
+    ma.offsets = off;
+    ma.samples = (float4*)h->m_samples.p;
+    ma.ray_ids = (uint32_t*)h->m_ids.p;
+    ma.capacity = (uint64_t)n;
+    FFN_HIP(ffn::launch_march(ma, true, st));
+  }
+  const float4* smp = (const float4*)h->m_samples.p;
+  const uint32_t* ids = (const uint32_t*)h->m_ids.p;
+  const size_t nz = (size_t)(n > 0 ? n : 1);
+  FFN_HIP(h->a0.ensure(sizeof(float) * nz * LF));
+  FFN_HIP(h->dLda0.ensure(sizeof(float) * nz * LF));
+  FFN_HIP(h->m_sigma.ensure(sizeof(float) * nz));
+  FFN_HIP(h->m_rgb.ensure(sizeof(float) * nz * 3));
+  FFN_HIP(h->m_Tr.ensure(sizeof(float) * nz));
+  FFN_HIP(h->m_dLds.ensure(sizeof(float) * nz));
+  FFN_HIP(h->m_dLdc.ensure(sizeof(float) * nz * 3));
+  float* a0 = (float*)h->a0.p;
+  float* dLda0 = (float*)h->dLda0.p;
+  float* sigma = (float*)h->m_sigma.p;
+  float* rgb = (float*)h->m_rgb.p;
+  const ffn::FeatLayout feat = ffn::level_major(n, h->dc.F);
+  ffn::PosSrc src{(const float*)smp, nullptr, nullptr, 0};
+  src.x_stride = 4;
+
+  // 2. encode the samples
+  {
+    StageTimer tm(h, 1, st);
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, P.table, a0, feat, nullptr, st));
+  }
+  // 3-5. forward MLP, compositing with early termination and the loss, MLP backward
+  const int64_t n_tiles = (n + 63) / 64;
+  int n_blocks = (h->n_cu > 0 ? h->n_cu : 256) * ffn::mlp_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc);
+  if (n_blocks > n_tiles) n_blocks = (int)(n_tiles > 0 ? n_tiles : 1);
+  FFN_HIP(h->partials.ensure(sizeof(float) * (size_t)n_blocks * h->lay.total));
+  ffn::MlpPtrs w{};
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    w.W[k] = P.W[k];
+    w.b[k] = P.b[k];
+  }
+  {
+    StageTimer tm(h, 2, st);
+    FFN_HIP(ffn::launch_mlp_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, sc->sh_multiplier, sigma, rgb, LF,
+                                h->cfg.nd, h->cfg.nc, n_blocks, st));
+    ffn::CompMarchArgs ca{};
+    ca.offsets = off;
+    ca.counts = counts;
+    ca.num_rays = num_rays;
+    ca.sigma = sigma;
+    ca.rgb = rgb;
+    ca.targets = (const float4*)targets;
+    ca.dt = mp->dt;
+    ca.T_stop = mp->T_stop;
+    ca.regu = 5e-3f * mp->dt / (float)mp->max_steps;
+    ca.background = h->cfg.background;
+    ca.seed = sc->rng_seed;
+    ca.out_rgb = (float4*)out_rgb;
+    ca.Tr = (float*)h->m_Tr.p;
+    ca.dLds = (float*)h->m_dLds.p;
+    ca.dLdc = (float*)h->m_dLdc.p;
+    ca.n_used = n_samples;
+    ca.T_final = taps ? taps->T_final : nullptr;
+    ca.color = taps ? (float4*)taps->color : nullptr;
+    FFN_HIP(ffn::launch_composite_marched(ca, st));
+    ffn::MlpArgs a{};
+    a.c = h->dc;
+    a.w = w;
+    a.rays = (const float4*)rays;
+    a.a0 = a0;
+    a.dL_da0 = dLda0;
+    a.feat = feat;
+    a.partials = (float*)h->partials.p;
+    a.num_rays = (uint32_t)n;  // one "ray" per sample: the kernel walks n samples in tiles of 64
+    a.S = 1;
+    a.log2S = 0;
+    a.n_tiles = n_tiles;
+    a.sh_mult = sc->sh_multiplier;
+    a.occ_strength = 0.0f;
+    a.seed = sc->rng_seed;
+    a.do_train = 1;
+    a.smp = smp;
+    a.ray_ids = ids;
+    a.in_dLds = ca.dLds;
+    a.in_dLdc = ca.dLdc;
+    a.march_dt = mp->dt;
+    if (taps) a.t_relu = taps->relu;
+    if (n > 0) FFN_HIP(ffn::launch_mlp_marched(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+    else FFN_HIP(ffn::launch_fill((float*)h->partials.p, h->lay.total, 0.0f, st));
+  }
+  if (taps) {
+    if (taps->sigma) FFN_HIP(hipMemcpyAsync(taps->sigma, sigma, sizeof(float) * n, hipMemcpyDeviceToDevice, st));
+    if (taps->rgb) FFN_HIP(hipMemcpyAsync(taps->rgb, rgb, sizeof(float) * 3 * n, hipMemcpyDeviceToDevice, st));
+    if (taps->Tr) FFN_HIP(hipMemcpyAsync(taps->Tr, h->m_Tr.p, sizeof(float) * n, hipMemcpyDeviceToDevice, st));
+    if (taps->dL_dsigma)
+      FFN_HIP(hipMemcpyAsync(taps->dL_dsigma, h->m_dLds.p, sizeof(float) * n, hipMemcpyDeviceToDevice, st));
+    if (taps->dL_dc)
+      FFN_HIP(hipMemcpyAsync(taps->dL_dc, h->m_dLdc.p, sizeof(float) * 3 * n, hipMemcpyDeviceToDevice, st));
+    const ffn::FeatLayout sm = ffn::sample_major(h->dc.L, h->dc.F);
+    if (taps->a0) FFN_HIP(ffn::launch_feat_relayout(a0, feat, taps->a0, sm, n, h->dc.L, h->dc.F, st));
+    if (taps->dL_da0) FFN_HIP(ffn::launch_feat_relayout(dLda0, feat, taps->dL_da0, sm, n, h->dc.L, h->dc.F, st));
+  }
+  // 6. the table update from the samples' encoding gradients
+  {
+    StageTimer tm(h, 3, st);
+    ffn::BinPlan plan{};
+    ffn::BinScratch bs{};
+    FFN_HIP(ensure_bins(h, n > 0 ? n : 1, &plan, &bs));
+    ffn::BinApply ap{};
+    ap.dst = P.table;
+    ap.dst_f16 = h->dc.table_f16;
+    int mode = ffn::BIN_SGD;
+    if (h->cfg.hash_opt == FFN_HASH_ADAM) {
+      mode = ffn::BIN_ADAM;
+      ap.m = P.m_table;
+      ap.v = P.v_table;
+      ap.g_tap = taps ? taps->g_table : nullptr;
+      ap.lr_t = sc->lr_t;
+      ap.beta1 = sc->beta1;
+      ap.beta2 = sc->beta2;
+      ap.eps = sc->eps;
+    }
+    // with no samples nothing runs: the table and its moments stay as they are
+    FFN_HIP(ffn::launch_hash_bwd(h->dc, src, n, dLda0, feat, mode, sc->lr, ap, plan, bs, st));
+  }
+  // 7. MLP Adam
+  ffn::MlpOptArgs o{};
+  o.lay = h->lay;
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    o.W[k] = P.W[k];
+    o.b[k] = P.b[k];
+    o.mW[k] = P.mW[k];
+    o.vW[k] = P.vW[k];
+    o.mb[k] = P.mb[k];
+    o.vb[k] = P.vb[k];
+    if (taps) {
+      o.gW[k] = taps->gW[k];
+      o.gb[k] = taps->gb[k];
+    }
+  }
+  o.partials = (const float*)h->partials.p;
+  o.n_partials = n_blocks;
+  o.lr_t = sc->lr_t;
+  o.color_rel_lr = sc->color_rel_lr;
+  o.beta1 = sc->beta1;
+  o.beta2 = sc->beta2;
+  o.eps = sc->eps;
+  {
+    StageTimer tm(h, 4, st);
+    FFN_HIP(ffn::launch_mlp_adam(o, st));
+  }
   return 0;
 }
 

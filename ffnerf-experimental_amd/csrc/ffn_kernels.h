@@ -100,6 +100,13 @@ struct MlpArgs {
   float4* t_color;   // [num_rays] colour before clamping
   float* t_dLds;
   float* t_dLdc;
+  // marched training (the backward over compacted samples): sample b is smp[b] = {x, y, z, t} of ray
+  // ray_ids[b], lattice step march_dt; its loss gradients come from the compositing kernel
+  const float4* smp;
+  const uint32_t* ray_ids;
+  const float* in_dLds;
+  const float* in_dLdc;
+  float march_dt;
 };
 
 // bucketed backward scatter
@@ -197,6 +204,28 @@ hipError_t launch_render_finish(const float4* acc, uint32_t num_rays, float4* ou
 hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, uint32_t* total,
                            hipStream_t st);
 
+// compositing of a marched training batch (one lane per ray, front to back, stopping after the sample that
+// leaves T < T_stop), the photometric loss gradient and the compositing backward of every sample
+struct CompMarchArgs {
+  const uint32_t* offsets;
+  const uint32_t* counts;
+  uint32_t num_rays;
+  const float* sigma;
+  const float* rgb;
+  const float4* targets;
+  float dt, T_stop, regu;  // regu = 5e-3 dt / max_steps, the density penalty of every composited sample
+  int background;          // FFN_BG_*
+  uint32_t seed;
+  float4* out_rgb;         // {clamped rgb, 4}
+  float* Tr;               // [n] transmittance before each sample
+  float* dLds;             // [n]
+  float* dLdc;             // [n][3]
+  uint32_t* n_used;        // [num_rays] samples composited (optional)
+  float* T_final;          // [num_rays] (optional)
+  float4* color;           // [num_rays] colour before clamping (optional)
+};
+hipError_t launch_composite_marched(const CompMarchArgs& a, hipStream_t st);
+
 // training batch on the GPU: uniform pixels of the resident images, their rays and targets
 hipError_t launch_make_batch(const float* images, uint32_t n_images, uint32_t W, uint32_t H, const float* c2w,
                              const float* K, uint32_t num_rays, uint32_t seed, float4* rays, float4* targets,
@@ -213,6 +242,9 @@ bool mlp_supported(int LF, int nd, int nc);
 int mlp_blocks_per_cu(int LF, int nd, int nc);  // blocks of launch_mlp that fit on one CU
 int mlp16_blocks_per_cu(int LF, int nd, int nc);  // blocks of launch_mlp16 that fit on one CU
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+// the same kernel's backward over marched samples (a.smp, a.ray_ids, a.in_dLds, a.in_dLdc; a.num_rays = the
+// sample count, log2S = 0): no compositing, no proposals
+hipError_t launch_mlp_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
 // the same step on fp16 (forward) / bf16 (backward, weight gradients) MFMAs with fp32 accumulation
 bool mlp16_supported(int LF, int nd, int nc);
 hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);

@@ -300,6 +300,75 @@ __global__ __launch_bounds__(256) void k_render_finish(const float4* __restrict_
   out_rgb[r] = acc[r];  // black background: C + T * 0; w = T_final
 }
 
+// Compositing of marched training rays: one lane per ray walks its samples front to back (the order of the
+// specification, ora_train_step_marched), keeping the transmittance before every sample for the backward
+// sweep, which walks them back to front with dL/dT of the next sample (ffnerf_OG.cl:1593-1634 restated as a
+// sequential recurrence: gT_i = g . (alpha_i c_i) + (1 - alpha_i) gT_(i+1), gT_end = g . bg).
+__global__ __launch_bounds__(256) void k_composite_marched(CompMarchArgs a) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= a.num_rays) return;
+  const uint32_t cnt = a.counts[r], off = a.offsets[r];
+  float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
+  uint32_t used = 0;
+  for (uint32_t j = 0; j < cnt; ++j) {
+    const uint32_t b = off + j;
+    const float alpha = 1.0f - fast_exp(fminf(fmaxf(-a.sigma[b] * a.dt, -5.0f), 18.0f));
+    a.Tr[b] = T;
+    const float w = T * alpha;
+    C0 = C0 + w * a.rgb[3 * (size_t)b];
+    C1 = C1 + w * a.rgb[3 * (size_t)b + 1];
+    C2 = C2 + w * a.rgb[3 * (size_t)b + 2];
+    T = T * (1.0f - alpha);
+    ++used;
+    if (T < a.T_stop) break;
+  }
+  float bg[3] = {0.0f, 0.0f, 0.0f};
+  if (a.background == FFN_BG_WHITE) {
+    bg[0] = bg[1] = bg[2] = 1.0f;
+  } else if (a.background == FFN_BG_RANDOM) {
+    uint32_t rb = hash_u32(a.seed ^ r * 747796405u ^ 0xA511E9B3u);
+    bg[0] = rand01(rb);
+    bg[1] = rand01(rb);
+    bg[2] = rand01(rb);
+  }
+  const float4 tg = a.targets[r];
+  const float Cf0 = C0 + T * bg[0], Cf1 = C1 + T * bg[1], Cf2 = C2 + T * bg[2];
+  const float gr0 = charbonnier_prime(Cf0 - tg.x), gr1 = charbonnier_prime(Cf1 - tg.y),
+              gr2 = charbonnier_prime(Cf2 - tg.z);
+  a.out_rgb[r] = make_float4(fminf(fmaxf(Cf0, 0.0f), 1.0f), fminf(fmaxf(Cf1, 0.0f), 1.0f),
+                             fminf(fmaxf(Cf2, 0.0f), 1.0f), 4.0f);
+  if (a.n_used) a.n_used[r] = used;
+  if (a.T_final) a.T_final[r] = T;
+  if (a.color) a.color[r] = make_float4(Cf0, Cf1, Cf2, 0.0f);
+  float gT = gr0 * bg[0] + gr1 * bg[1] + gr2 * bg[2];
+  for (uint32_t j = used; j-- > 0;) {
+    const uint32_t b = off + j;
+    const float alpha = 1.0f - fast_exp(fminf(fmaxf(-a.sigma[b] * a.dt, -5.0f), 18.0f));
+    const float Ti = a.Tr[b];
+    const float c0 = a.rgb[3 * (size_t)b], c1 = a.rgb[3 * (size_t)b + 1], c2 = a.rgb[3 * (size_t)b + 2];
+    const float gA = gr0 * (Ti * c0) + gr1 * (Ti * c1) + gr2 * (Ti * c2);
+    const float gAlpha = gA - gT * Ti;
+    a.dLds[b] = gAlpha * (a.dt * (1.0f - alpha)) + a.regu;
+    const float ws = Ti * alpha;
+    a.dLdc[3 * (size_t)b] = ws * gr0;
+    a.dLdc[3 * (size_t)b + 1] = ws * gr1;
+    a.dLdc[3 * (size_t)b + 2] = ws * gr2;
+    gT = (gr0 * (alpha * c0) + gr1 * (alpha * c1) + gr2 * (alpha * c2)) + (1.0f - alpha) * gT;
+  }
+  for (uint32_t j = used; j < cnt; ++j) {  // past the termination: no contribution, no gradient
+    const uint32_t b = off + j;
+    a.Tr[b] = T;
+    a.dLds[b] = 0.0f;
+    a.dLdc[3 * (size_t)b] = a.dLdc[3 * (size_t)b + 1] = a.dLdc[3 * (size_t)b + 2] = 0.0f;
+  }
+}
+
+hipError_t launch_composite_marched(const CompMarchArgs& a, hipStream_t st) {
+  if (a.num_rays == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_composite_marched, dim3((a.num_rays + 255) / 256), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 
 hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint32_t* bits, hipStream_t st) {

@@ -324,7 +324,9 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
   rgb_s[2] = sigmoid_soft(co[0][2]);
 }
 
-template <int LF, int ND, int NC, int FEAT, bool TAPS>
+// MARCHED: the backward over marched samples -- sample b is a.smp[b] of ray a.ray_ids[b], its loss gradients
+// are read (a.in_dLds, a.in_dLdc), and there is no compositing and no proposal
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
 __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_mlp(MlpArgs a) {
   using A = Arch<LF, ND, NC>;
   constexpr int KA = LF / 4;  // a0 values per lane (k-steps of the first layer)
@@ -370,7 +372,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     // forward: this lane's sample in the MLP layout
     const int64_t b = tile * 64 + col;
     const bool valid = (uint64_t)b < n_samples;
-    const int64_t ray = valid ? (b >> log2S) : 0;
+    const int64_t ray = valid ? (MARCHED ? (int64_t)a.ray_ids[b] : (b >> log2S)) : 0;
     float a0r[KA];
     load_a0<LF, FEAT>(a.a0, a.feat, b, valid, g, a0r);
     float dirv[3];
@@ -380,15 +382,18 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
       dirv[1] = rd.y;
       dirv[2] = rd.z;
     }
-    const float dt_b = valid ? a.DTs[b] : 0.0f;
-    const float t_b = valid ? a.Ts[b] : 0.0f;
+    const float dt_b = valid ? (MARCHED ? a.march_dt : a.DTs[b]) : 0.0f;
+    const float t_b = valid ? (MARCHED ? a.smp[b].w : a.Ts[b]) : 0.0f;
     // per-sample inputs of the compositing (lane j = sample j of the tile), loaded before the forward so
     // that their latency hides behind it
     const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront makes the tile's proposals
-    const CompLane CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
-    if (!taps && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
-      empty_tile<LF, FEAT>(a, CL, lane, wave, b, valid, train, g);
-      continue;
+    CompLane CL{};
+    if constexpr (!MARCHED) {
+      CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
+      if (!taps && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
+        empty_tile<LF, FEAT>(a, CL, lane, wave, b, valid, train, g);
+        continue;
+      }
     }
 
     floatx4 hd[ND][4];
@@ -406,27 +411,38 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
       }
     }
     const float dout0 = acin[0][0];
-    if (g == 0) {
-      float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
-      if (dt_b <= 0.0f) sig = 0.0f;
-      sSig[col] = sig;
-      sRgb[col * 3 + 0] = rgb_s[0];
-      sRgb[col * 3 + 1] = rgb_s[1];
-      sRgb[col * 3 + 2] = rgb_s[2];
-    }
-    __syncthreads();
+    float dLds, dLdc0, dLdc1, dLdc2;
+    if constexpr (MARCHED) {
+      __syncthreads();  // the previous tile's last weight-gradient tiles have read the stash
+      dLds = valid ? a.in_dLds[b] : 0.0f;
+      dLdc0 = valid ? a.in_dLdc[3 * b] : 0.0f;
+      dLdc1 = valid ? a.in_dLdc[3 * b + 1] : 0.0f;
+      dLdc2 = valid ? a.in_dLdc[3 * b + 2] : 0.0f;
+    } else {
+      if (g == 0) {
+        float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
+        if (dt_b <= 0.0f) sig = 0.0f;
+        sSig[col] = sig;
+        sRgb[col * 3 + 0] = rgb_s[0];
+        sRgb[col * 3 + 1] = rgb_s[1];
+        sRgb[col * 3 + 2] = rgb_s[2];
+      }
+      __syncthreads();
 
-    // ------------------------------------------------------------------
-    // compositing on 64 lanes: lane j = sample j of the tile (every wave)
-    float dLds_j, dLdc_j[3];
-    composite_tile<TAPS>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
-    if (!train) continue;
+      // ------------------------------------------------------------------
+      // compositing on 64 lanes: lane j = sample j of the tile (every wave)
+      float dLds_j, dLdc_j[3];
+      composite_tile<TAPS>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+      if (!train) continue;
+      dLds = __shfl(dLds_j, col);
+      dLdc0 = __shfl(dLdc_j[0], col);
+      dLdc1 = __shfl(dLdc_j[1], col);
+      dLdc2 = __shfl(dLdc_j[2], col);
+    }
 
     // ------------------------------------------------------------------
     // backward of this wave's 16 samples; every layer's deltas and inputs go through the stash for the
     // block's weight-gradient tiles (barrier, this wave's tiles, barrier before the stash is reused)
-    const float dLds = __shfl(dLds_j, col);
-    const float dLdc0 = __shfl(dLdc_j[0], col), dLdc1 = __shfl(dLdc_j[1], col), dLdc2 = __shfl(dLdc_j[2], col);
     floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
     floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
     if (g == 0 && valid) {
@@ -526,32 +542,35 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC, int FEAT, bool TAPS>
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
 static hipError_t launch_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch<LF, ND, NC>;
   const size_t lds = sizeof(float) * (size_t)A::lds_floats(a.do_train != 0);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT, TAPS>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT, TAPS, MARCHED>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)(sizeof(float) * (size_t)A::lds_floats(false)));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp<LF, ND, NC, FEAT, TAPS>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp<LF, ND, NC, FEAT, TAPS, MARCHED>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
-template <int LF, int ND, int NC>
+template <int LF, int ND, int NC, bool MARCHED>
 static hipError_t launch_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
   const bool taps = taps_requested(a);
   switch (a.c.F) {
     case 1:
-      return taps ? launch_f<LF, ND, NC, 1, true>(a, n_blocks, st) : launch_f<LF, ND, NC, 1, false>(a, n_blocks, st);
+      return taps ? launch_f<LF, ND, NC, 1, true, MARCHED>(a, n_blocks, st)
+                  : launch_f<LF, ND, NC, 1, false, MARCHED>(a, n_blocks, st);
     case 2:
-      return taps ? launch_f<LF, ND, NC, 2, true>(a, n_blocks, st) : launch_f<LF, ND, NC, 2, false>(a, n_blocks, st);
+      return taps ? launch_f<LF, ND, NC, 2, true, MARCHED>(a, n_blocks, st)
+                  : launch_f<LF, ND, NC, 2, false, MARCHED>(a, n_blocks, st);
     case 4:
-      return taps ? launch_f<LF, ND, NC, 4, true>(a, n_blocks, st) : launch_f<LF, ND, NC, 4, false>(a, n_blocks, st);
+      return taps ? launch_f<LF, ND, NC, 4, true, MARCHED>(a, n_blocks, st)
+                  : launch_f<LF, ND, NC, 4, false, MARCHED>(a, n_blocks, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -661,7 +680,15 @@ hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, co
 
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
 #define X(l, d, n) \
-  if (LF == l && nd == d && nc == n) return launch_t<l, d, n>(a, n_blocks, st);
+  if (LF == l && nd == d && nc == n) return launch_t<l, d, n, false>(a, n_blocks, st);
+  FFN_MLP_CONFIGS(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_mlp_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return launch_t<l, d, n, true>(a, n_blocks, st);
   FFN_MLP_CONFIGS(X)
 #undef X
   return hipErrorInvalidValue;

@@ -510,6 +510,37 @@ class Nerf:
                                                   fl.stream_ptr()), "ffn_occ_bitfield")
         return out
 
+    def step_marched(self, io: RayBatch, lr_f: float, bits, res: int, dt: float, max_steps: int = 1024,
+                     T_stop: float = 1e-4, sh_multiplier: float = 1.0, color_MLP_rel_lr: float = 1.0,
+                     rng_u32: np.uint32 | None = None, n_samples=None, taps: fl.FfnTaps | None = None, stream=None):
+        """A training step whose samples come from the bitfield march instead of the resampler (the step of
+        ffnerf_tools.py:1446-1530 with ffn_train_step_marched): io's rays and targets, the same learning-rate
+        schedule and Adam counter as step().  The occupancy grid is not updated (the bitfield is an input);
+        n_samples (optional, device [num_rays]) gets the samples composited per ray.  Waits on the stream once
+        inside, after the march's count."""
+        if rng_u32 is None:
+            rng_u32 = self._get_rng_u32()
+        self.steps_trained = int(self.steps_trained) + 1
+        sc = fl.FfnStepScalars()
+        sc.lr = float(np.float32(lr_f))
+        sc.lr_t = float(self.adam_lr_t(lr_f, self.steps_trained))
+        sc.color_rel_lr = float(color_MLP_rel_lr)
+        sc.sh_multiplier = float(sh_multiplier)
+        sc.occ_strength = 0.0
+        sc.beta1, sc.beta2, sc.eps = float(self.spec.beta1), float(self.spec.beta2), float(self.spec.eps)
+        sc.rng_seed = int(rng_u32) & 0xFFFFFFFF
+        sc.do_train = 1
+        mp = fl.march_params(res, dt, max_steps, T_stop=T_stop, sh_multiplier=sh_multiplier)
+        fl.check(self.handle.lib.ffn_train_step_marched(
+            self.handle.h, fl.ptr(io.rays_buf), fl.ptr(io.targets_buf), fl.ptr(io.out_buf), io.num_rays,
+            fl.ptr(bits), C.byref(mp), C.byref(sc), C.byref(taps) if taps is not None else None, fl.ptr(n_samples),
+            fl.stream_ptr(stream)), "ffn_train_step_marched")
+        torch = _torch()
+        ev = torch.cuda.Event()
+        ev.record()
+        io.ev_last = ev
+        return ev
+
     def render_marched(self, io: RayBatch, bits, res: int, dt: float, max_steps: int = 1024, T_stop: float = 1e-4,
                        chunk: int = 32, sh_multiplier: float = 1.0, n_samples=None, stream=None):
         """Forward-only render of io's rays: bitfield DDA march, MLPs, front-to-back compositing stopped at

@@ -211,6 +211,30 @@ int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const u
                       const ffn_march_params* mp, uint32_t* counts, uint32_t* offsets, float* samples,
                       uint32_t* ray_ids, uint64_t capacity, uint32_t* total, void* stream);
 
+/* A training step over marched samples (the DDA march replaces the reference's
+ * S importance-resampled samples per ray, ffnerf_OG.cl:1002-1250): march every
+ * ray through the bitfield (as ffn_march: lattice samples of occupied cells,
+ * at most mp->max_steps), encode, run the MLPs, composite front to back
+ * stopping after the sample that leaves T < mp->T_stop (the later samples
+ * contribute nothing and get no gradient), the photometric loss and its
+ * gradient (ffnerf_OG.cl:1505-1634, as a sequential recurrence), the MLP
+ * backward, the table update (reference SGD or Adam) and the MLP Adam.  The
+ * density penalty of a composited sample is 5e-3 dt / max_steps (the
+ * reference's 5e-3 dt / S).  No occupancy proposals: the bitfield is an input
+ * (ffn_occ_bitfield).  Specification: ora_train_step_marched (oracle/).
+ * rays, targets, out_rgb as ffn_train_step (out_rgb.w = 4); n_samples
+ * (optional) [num_rays] = samples composited per ray.  taps (optional) index
+ * the step's samples in march order (ray by ray, front to back; at most
+ * num_rays * max_steps): sigma, rgb, Tr, dL_dsigma, dL_dc, a0, dL_da0, relu,
+ * the per-ray T_final and color, and the summed gradients.  A step whose
+ * march finds no samples returns the background, leaves the table and its
+ * moments as they are and runs the MLP's Adam on zero gradients.  fp32 MLP
+ * path only.  Waits on the stream once, after the march's count, to size the
+ * step's launches. */
+int ffn_train_step_marched(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
+                           const uint32_t* bits, const ffn_march_params* mp, const ffn_step_scalars* scalars,
+                           const ffn_taps* taps, uint32_t* n_samples, void* stream);
+
 /* Forward render with the bound parameters: march `chunk` samples per live
  * ray, encode, run the MLPs, composite front to back, retire rays below
  * T_stop, repeat.  out_rgb [num_rays] float4 {r, g, b, T_final} (black

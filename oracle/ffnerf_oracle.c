@@ -1116,12 +1116,149 @@ void ora_occ_decay(uint32_t* occ_in, uint32_t* occ_st, uint32_t n_words, uint32_
 /* the full step: sampler -> encode -> MLPs -> composite -> proposals  */
 /* -> deltas -> MLP backward -> table update -> weight grads -> Adam   */
 
+/* backward of one sample from its loss gradients (ffnerf_OG.cl:1863-2173): output deltas with the distance
+ * gate f_vol, the colour and density MLP backward through the sample's ReLU branches, the weight gradients
+ * added to gW/gb (weight_update.cl:260-314), the encoding gradient (written to gf_out when given) and the
+ * table update -- summed into gtab (Adam, or a binary16 table's SGD) or added to the table one
+ * contribution at a time (the reference SGD).  x is the sample's position, t/dtl its time and dt. */
+/* the step's parameter updates: MLP Adam with colour layers at lr_t * color_rel_lr
+ * (weight_update.cl:487-573) from the summed weight gradients, then the table -- Adam on its summed gradient,
+ * or a binary16 table's summed SGD update added once (rounded to nearest even); the reference SGD on a float
+ * table was applied during the backward.  gtab may be NULL (no table update). */
+static void apply_updates(const ora_cfg* c, ora_params* P, const ora_scalars* sc, double** gW, double** gb,
+                          const int* odim, const int* idim, double* gtab, int64_t table_n, ora_debug* dbg) {
+  /* MLP Adam; color layers at lr_t * color_rel_lr (weight_update.cl:487-573) */
+  for (int k = 0; k < L_COUNT; ++k) {
+    if (!gW[k]) continue;
+    int n = odim[k] * idim[k];
+    float* gwf = (float*)malloc(sizeof(float) * n);
+    float* gbf = (float*)malloc(sizeof(float) * odim[k]);
+    for (int i = 0; i < n; ++i) gwf[i] = (float)gW[k][i];
+    for (int i = 0; i < odim[k]; ++i) gbf[i] = (float)gb[k][i];
+    float lrk = (k >= L_WC_IN) ? sc->lr_t * sc->color_rel_lr : sc->lr_t;
+    if (dbg && dbg->gW[k]) memcpy(dbg->gW[k], gwf, sizeof(float) * n);
+    if (dbg && dbg->gb[k]) memcpy(dbg->gb[k], gbf, sizeof(float) * odim[k]);
+    ora_adam(P->W[k], P->mW[k], P->vW[k], gwf, n, lrk, sc->beta1, sc->beta2, sc->eps);
+    ora_adam(P->b[k], P->mb[k], P->vb[k], gbf, odim[k], lrk, sc->beta1, sc->beta2, sc->eps);
+    free(gwf);
+    free(gbf);
+  }
+  if (gtab && c->hash_opt == 1) {
+    float* gtf = (float*)malloc(sizeof(float) * (size_t)table_n);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < table_n; ++i) gtf[i] = (float)gtab[i];
+    if (dbg && dbg->g_table) memcpy(dbg->g_table, gtf, sizeof(float) * (size_t)table_n);
+    ora_adam(P->table, P->m_table, P->v_table, gtf, table_n, sc->lr_t, sc->beta1, sc->beta2, sc->eps);
+    free(gtf);
+    if (c->table_f16) {
+#pragma omp parallel for schedule(static)
+      for (int64_t i = 0; i < table_n; ++i) P->table[i] = ora_f16_round(P->table[i]);
+    }
+  } else if (gtab) { /* binary16 table, reference SGD: each entry's summed update in one rounding */
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < table_n; ++i) P->table[i] = ora_f16_round(P->table[i] + (float)gtab[i]);
+  }
+}
+
+static void sample_backward(const ora_cfg* c, ora_params* P, const ora_scalars* sc, const mlp_state* m,
+                            const float x[3], float t, float dtl, float D, float dLds, const float* dLdc,
+                            double** lgW, double** lgb, double* gtab, float* gf_out) {
+  static const int cslot[4] = {L_WC_IN, L_WC_01, L_WC_12, L_WC_23};
+  static const int dslot[3] = {L_WD_IN, L_WD_01, L_WD_12};
+  const int L = c->n_levels, F = c->f_per_level, LF = L * F;
+  const int nd = c->nd, nc = c->nc;
+  /* output deltas with the distance gate f_vol (ffnerf_OG.cl:1863-1891) */
+  float num = t * t + t * dtl + (dtl * dtl / 3.0f);
+  float den = D * D + D * dtl + (dtl * dtl / 3.0f);
+  float xg = t / fmaxf(D, 1.0e-12f);
+  float sg = (xg >= 1.0f) ? 0.0f : 1.0f;
+  float gate = (1.0f - sg) * 1.0f + sg * powf(fmaxf(xg, 1.0e-12f), 0.2f);
+  float f_vol = gate * num / fmaxf(den, 1.0e-12f);
+  float d_sigma = f_vol * dLds;
+  float dcout[ORA_C_OUT], ddout[ORA_D_OUT];
+  for (int k = 0; k < 3; ++k) {
+    float sk = m->rgb[k];
+    dcout[k] = (f_vol * dLdc[k]) * ((sk * (1.0f - sk)) * 0.5f);
+  }
+  ddout[0] = 1.0f * d_sigma * softplus_prime_from_pre(fminf(fmaxf(m->acin[0], -18.0f), 18.0f));
+  for (int i = 1; i < ORA_D_OUT; ++i) ddout[i] = 0.0f;
+
+  /* color backward */
+  float dc[4][ORA_M];
+  fc_bwd(dc[nc - 1], dcout, ORA_C_OUT, ORA_M, P->W[L_WC_OUT]);
+  for (int j = 0; j < ORA_M; ++j) dc[nc - 1][j] = unit_on(m, 3 + nc - 1, j) ? dc[nc - 1][j] : 0.0f;
+  for (int k = nc - 1; k >= 1; --k) {
+    fc_bwd(dc[k - 1], dc[k], ORA_M, ORA_M, P->W[cslot[k]]);
+    for (int j = 0; j < ORA_M; ++j) dc[k - 1][j] = unit_on(m, 3 + k - 1, j) ? dc[k - 1][j] : 0.0f;
+  }
+  for (int i = 0; i < ORA_D_OUT; ++i) {
+    float sacc = 0.0f;
+    for (int j = 0; j < ORA_M; ++j) sacc += P->W[L_WC_IN][j * ORA_C_IN + i] * dc[0][j];
+    ddout[i] += sacc;
+  }
+  /* density backward */
+  float dd[3][ORA_M];
+  fc_bwd(dd[nd - 1], ddout, ORA_D_OUT, ORA_M, P->W[L_WD_OUT]);
+  for (int j = 0; j < ORA_M; ++j) dd[nd - 1][j] = unit_on(m, nd - 1, j) ? dd[nd - 1][j] : 0.0f;
+  for (int k = nd - 1; k >= 1; --k) {
+    fc_bwd(dd[k - 1], dd[k], ORA_M, ORA_M, P->W[dslot[k]]);
+    for (int j = 0; j < ORA_M; ++j) dd[k - 1][j] = unit_on(m, k - 1, j) ? dd[k - 1][j] : 0.0f;
+  }
+  /* weight gradients: dW[o][i] += delta[o] * act_in[i] (weight_update.cl:260-314) */
+#define ACC(slot, delta, act, od, id)                                                         \
+  do {                                                                                        \
+    for (int o_ = 0; o_ < (od); ++o_) {                                                       \
+      double dv = (double)(delta)[o_];                                                        \
+      lgb[slot][o_] += dv;                                                                    \
+      for (int i_ = 0; i_ < (id); ++i_) lgW[slot][o_ * (id) + i_] += dv * (double)(act)[i_]; \
+    }                                                                                         \
+  } while (0)
+  ACC(L_WC_OUT, dcout, m->hc[nc - 1], ORA_C_OUT, ORA_M);
+  for (int k = nc - 1; k >= 1; --k) ACC(cslot[k], dc[k], m->hc[k - 1], ORA_M, ORA_M);
+  ACC(L_WC_IN, dc[0], m->acin, ORA_M, ORA_C_IN);
+  ACC(L_WD_OUT, ddout, m->hd[nd - 1], ORA_D_OUT, ORA_M);
+  for (int k = nd - 1; k >= 1; --k) ACC(dslot[k], dd[k], m->hd[k - 1], ORA_M, ORA_M);
+  ACC(L_WD_IN, dd[0], m->a0, ORA_M, LF);
+#undef ACC
+  /* encoding gradient and table update (ffnerf_OG.cl:2090-2173) */
+  float gf[ORA_M];
+  for (int k = 0; k < LF; ++k) {
+    float sacc = 0.0f;
+    for (int j = 0; j < ORA_M; ++j) sacc += P->W[L_WD_IN][j * LF + k] * dd[0][j];
+    gf[k] = sacc;
+  }
+  if (gf_out) memcpy(gf_out, gf, sizeof(float) * LF);
+  float p[3];
+  normalize_pos(c, x, p);
+  for (int l = 0; l < L; ++l) {
+    uint32_t feat[8];
+    float w[8];
+    level_corners(c, l, p, feat, w);
+    float lr_lvl = sc->lr * c->lvl_lr_scale[l];
+    for (int f = 0; f < F; ++f) {
+      float g = gf[l * F + f];
+      if (!isfinite(g)) continue;
+      for (int cc = 0; cc < 8; ++cc) {
+        if (c->hash_opt == 1) {
+          ORA_ATOMIC
+          gtab[feat[cc] + (uint32_t)f] += (double)(g * w[cc]);
+        } else if (c->table_f16) {
+          ORA_ATOMIC
+          gtab[feat[cc] + (uint32_t)f] += (double)(-lr_lvl * 0.5f * g * w[cc]);
+        } else {
+          ORA_ATOMIC
+          P->table[feat[cc] + (uint32_t)f] += -lr_lvl * 0.5f * g * w[cc];
+        }
+      }
+    }
+  }
+}
+
 int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const float* targets, float* out_rgb,
                    int32_t num_rays, int32_t S, const ora_scalars* sc, ora_debug* dbg) {
   if (S <= 0 || S > ORA_S_MAX || (S & (S - 1)) != 0) return -1;
   const int L = c->n_levels, F = c->f_per_level, LF = L * F;
   if (LF > ORA_M || c->nd < 1 || c->nd > 3 || c->nc < 1 || c->nc > 4) return -2;
-  const int nd = c->nd, nc = c->nc;
   const int do_train = sc->do_train != 0;
   int64_t table_entries = 0;
   for (int l = 0; l < L; ++l) {
@@ -1160,9 +1297,6 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
   const float D = 0.5f * sqrtf((c->box_max[0] - c->box_min[0]) * (c->box_max[0] - c->box_min[0]) +
                                (c->box_max[1] - c->box_min[1]) * (c->box_max[1] - c->box_min[1]) +
                                (c->box_max[2] - c->box_min[2]) * (c->box_max[2] - c->box_min[2]));
-  static const int cslot[4] = {L_WC_IN, L_WC_01, L_WC_12, L_WC_23};
-  static const int dslot[3] = {L_WD_IN, L_WD_01, L_WD_12};
-
 #pragma omp parallel
   {
   mlp_state* st = (mlp_state*)malloc(sizeof(mlp_state) * (size_t)S);
@@ -1227,94 +1361,10 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
     o4[3] += 4.0f; /* ffnerf_OG.cl:2091 */
 
     for (int s = 0; s < S; ++s) {
-      mlp_state* m = &st[s];
-      const float t = Ts[s], dtl = DTs[s];
-      /* output deltas with the distance gate f_vol (ffnerf_OG.cl:1863-1891) */
-      float num = t * t + t * dtl + (dtl * dtl / 3.0f);
-      float den = D * D + D * dtl + (dtl * dtl / 3.0f);
-      float xg = t / fmaxf(D, 1.0e-12f);
-      float sg = (xg >= 1.0f) ? 0.0f : 1.0f;
-      float gate = (1.0f - sg) * 1.0f + sg * powf(fmaxf(xg, 1.0e-12f), 0.2f);
-      float f_vol = gate * num / fmaxf(den, 1.0e-12f);
-      float d_sigma = f_vol * dLds[s];
-      float dcout[ORA_C_OUT], ddout[ORA_D_OUT];
-      for (int k = 0; k < 3; ++k) {
-        float sk = m->rgb[k];
-        dcout[k] = (f_vol * dLdc[3 * s + k]) * ((sk * (1.0f - sk)) * 0.5f);
-      }
-      ddout[0] = 1.0f * d_sigma * softplus_prime_from_pre(fminf(fmaxf(m->acin[0], -18.0f), 18.0f));
-      for (int i = 1; i < ORA_D_OUT; ++i) ddout[i] = 0.0f;
-
-      /* color backward */
-      float dc[4][ORA_M];
-      fc_bwd(dc[nc - 1], dcout, ORA_C_OUT, ORA_M, P->W[L_WC_OUT]);
-      for (int j = 0; j < ORA_M; ++j) dc[nc - 1][j] = unit_on(m, 3 + nc - 1, j) ? dc[nc - 1][j] : 0.0f;
-      for (int k = nc - 1; k >= 1; --k) {
-        fc_bwd(dc[k - 1], dc[k], ORA_M, ORA_M, P->W[cslot[k]]);
-        for (int j = 0; j < ORA_M; ++j) dc[k - 1][j] = unit_on(m, 3 + k - 1, j) ? dc[k - 1][j] : 0.0f;
-      }
-      for (int i = 0; i < ORA_D_OUT; ++i) {
-        float sacc = 0.0f;
-        for (int j = 0; j < ORA_M; ++j) sacc += P->W[L_WC_IN][j * ORA_C_IN + i] * dc[0][j];
-        ddout[i] += sacc;
-      }
-      /* density backward */
-      float dd[3][ORA_M];
-      fc_bwd(dd[nd - 1], ddout, ORA_D_OUT, ORA_M, P->W[L_WD_OUT]);
-      for (int j = 0; j < ORA_M; ++j) dd[nd - 1][j] = unit_on(m, nd - 1, j) ? dd[nd - 1][j] : 0.0f;
-      for (int k = nd - 1; k >= 1; --k) {
-        fc_bwd(dd[k - 1], dd[k], ORA_M, ORA_M, P->W[dslot[k]]);
-        for (int j = 0; j < ORA_M; ++j) dd[k - 1][j] = unit_on(m, k - 1, j) ? dd[k - 1][j] : 0.0f;
-      }
-      /* weight gradients: dW[o][i] += delta[o] * act_in[i] (weight_update.cl:260-314) */
-#define ACC(slot, delta, act, od, id)                                                         \
-  do {                                                                                        \
-    for (int o_ = 0; o_ < (od); ++o_) {                                                       \
-      double dv = (double)(delta)[o_];                                                        \
-      lgb[slot][o_] += dv;                                                                    \
-      for (int i_ = 0; i_ < (id); ++i_) lgW[slot][o_ * (id) + i_] += dv * (double)(act)[i_]; \
-    }                                                                                         \
-  } while (0)
-      ACC(L_WC_OUT, dcout, m->hc[nc - 1], ORA_C_OUT, ORA_M);
-      for (int k = nc - 1; k >= 1; --k) ACC(cslot[k], dc[k], m->hc[k - 1], ORA_M, ORA_M);
-      ACC(L_WC_IN, dc[0], m->acin, ORA_M, ORA_C_IN);
-      ACC(L_WD_OUT, ddout, m->hd[nd - 1], ORA_D_OUT, ORA_M);
-      for (int k = nd - 1; k >= 1; --k) ACC(dslot[k], dd[k], m->hd[k - 1], ORA_M, ORA_M);
-      ACC(L_WD_IN, dd[0], m->a0, ORA_M, LF);
-#undef ACC
-      /* encoding gradient and table update (ffnerf_OG.cl:2090-2173) */
-      float gf[ORA_M];
-      for (int k = 0; k < LF; ++k) {
-        float sacc = 0.0f;
-        for (int j = 0; j < ORA_M; ++j) sacc += P->W[L_WD_IN][j * LF + k] * dd[0][j];
-        gf[k] = sacc;
-      }
-      if (dbg && dbg->dL_da0) memcpy(dbg->dL_da0 + ((int64_t)r * S + s) * LF, gf, sizeof(float) * LF);
-      float x[3], p[3];
+      float x[3];
       for (int i = 0; i < 3; ++i) x[i] = ray[i] + Ts[s] * ray[4 + i];
-      normalize_pos(c, x, p);
-      for (int l = 0; l < L; ++l) {
-        uint32_t feat[8];
-        float w[8];
-        level_corners(c, l, p, feat, w);
-        float lr_lvl = sc->lr * c->lvl_lr_scale[l];
-        for (int f = 0; f < F; ++f) {
-          float g = gf[l * F + f];
-          if (!isfinite(g)) continue;
-          for (int cc = 0; cc < 8; ++cc) {
-            if (c->hash_opt == 1) {
-              ORA_ATOMIC
-              gtab[feat[cc] + (uint32_t)f] += (double)(g * w[cc]);
-            } else if (c->table_f16) {
-              ORA_ATOMIC
-              gtab[feat[cc] + (uint32_t)f] += (double)(-lr_lvl * 0.5f * g * w[cc]);
-            } else {
-              ORA_ATOMIC
-              P->table[feat[cc] + (uint32_t)f] += -lr_lvl * 0.5f * g * w[cc];
-            }
-          }
-        }
-      }
+      sample_backward(c, P, sc, &st[s], x, Ts[s], DTs[s], D, dLds[s], dLdc + 3 * s, lgW, lgb, gtab,
+                      (dbg && dbg->dL_da0) ? dbg->dL_da0 + ((int64_t)r * S + s) * LF : NULL);
     }
   }
 #ifdef _OPENMP
@@ -1330,39 +1380,7 @@ int ora_train_step(const ora_cfg* c, ora_params* P, const float* rays, const flo
   free(st);
   }
 
-  if (do_train) {
-    /* MLP Adam; color layers at lr_t * color_rel_lr (weight_update.cl:487-573) */
-    for (int k = 0; k < L_COUNT; ++k) {
-      if (!gW[k]) continue;
-      int n = odim[k] * idim[k];
-      float* gwf = (float*)malloc(sizeof(float) * n);
-      float* gbf = (float*)malloc(sizeof(float) * odim[k]);
-      for (int i = 0; i < n; ++i) gwf[i] = (float)gW[k][i];
-      for (int i = 0; i < odim[k]; ++i) gbf[i] = (float)gb[k][i];
-      float lrk = (k >= L_WC_IN) ? sc->lr_t * sc->color_rel_lr : sc->lr_t;
-      if (dbg && dbg->gW[k]) memcpy(dbg->gW[k], gwf, sizeof(float) * n);
-      if (dbg && dbg->gb[k]) memcpy(dbg->gb[k], gbf, sizeof(float) * odim[k]);
-      ora_adam(P->W[k], P->mW[k], P->vW[k], gwf, n, lrk, sc->beta1, sc->beta2, sc->eps);
-      ora_adam(P->b[k], P->mb[k], P->vb[k], gbf, odim[k], lrk, sc->beta1, sc->beta2, sc->eps);
-      free(gwf);
-      free(gbf);
-    }
-    if (gtab && c->hash_opt == 1) {
-      float* gtf = (float*)malloc(sizeof(float) * (size_t)table_n);
-#pragma omp parallel for schedule(static)
-      for (int64_t i = 0; i < table_n; ++i) gtf[i] = (float)gtab[i];
-      if (dbg && dbg->g_table) memcpy(dbg->g_table, gtf, sizeof(float) * (size_t)table_n);
-      ora_adam(P->table, P->m_table, P->v_table, gtf, table_n, sc->lr_t, sc->beta1, sc->beta2, sc->eps);
-      free(gtf);
-      if (c->table_f16) {
-#pragma omp parallel for schedule(static)
-        for (int64_t i = 0; i < table_n; ++i) P->table[i] = ora_f16_round(P->table[i]);
-      }
-    } else if (gtab) { /* binary16 table, reference SGD: each entry's summed update in one rounding */
-#pragma omp parallel for schedule(static)
-      for (int64_t i = 0; i < table_n; ++i) P->table[i] = ora_f16_round(P->table[i] + (float)gtab[i]);
-    }
-  }
+  if (do_train) apply_updates(c, P, sc, gW, gb, odim, idim, gtab, table_n, dbg);
   for (int k = 0; k < L_COUNT; ++k) { free(gW[k]); free(gb[k]); }
   free(gtab);
   free(table_read);
@@ -1491,4 +1509,178 @@ int ora_render_ray(const ora_cfg* c, const ora_params* P, const ora_march_cfg* m
   out[3] = T;
   free(ts);
   return used;
+}
+
+/* ------------------------------------------------------------------ */
+/* training over marched samples: the specification of                */
+/* ffn_train_step_marched (no counterpart in the reference, whose     */
+/* training samples every ray with S resampled points)                */
+
+/* Compositing of one marched ray of n samples and its backward.  Front to back with
+ * alpha_i = 1 - exp(clamp(-sigma_i dt, -5, 18)) (ffnerf_OG.cl:1505-1520), stopping after the sample that leaves
+ * T < T_stop (or after exactly used_force samples when that is >= 0: another implementation's termination);
+ * Cf = sum T_i alpha_i c_i + T_end bg; the Charbonnier gradient g at Cf (or at C_force); then back to front
+ * gT_end = g.bg, dL/dsigma_i = (g.(T_i c_i) - gT_(i+1) T_i) dt (1 - alpha_i) + regu, dL/dc_i = T_i alpha_i g,
+ * gT_i = g.(alpha_i c_i) + (1 - alpha_i) gT_(i+1) (ffnerf_OG.cl:1593-1634 as a sequential recurrence).  Samples
+ * after the stop get no gradient and Tr = T_end.  Returns the samples composited. */
+int ora_composite_marched(const float* sig, const float* rgb, int n, float dt, float T_stop, const float* bg,
+                          const float* target, const float* C_force, int used_force, float regu, float* Tr,
+                          float* dLds, float* dLdc, float* Cf, float* T_end) {
+  float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
+  int used = 0;
+  for (int j = 0; j < n; ++j) {
+    if (used_force >= 0 && j >= used_force) break;
+    const float alpha = 1.0f - expf(fminf(fmaxf(-sig[j] * dt, -5.0f), 18.0f));
+    Tr[j] = T;
+    const float w = T * alpha;
+    for (int k = 0; k < 3; ++k) C[k] = C[k] + w * rgb[3 * j + k];
+    T = T * (1.0f - alpha);
+    ++used;
+    if (used_force < 0 && T < T_stop) break;
+  }
+  for (int j = used; j < n; ++j) Tr[j] = T;
+  float gr[3];
+  for (int k = 0; k < 3; ++k) {
+    Cf[k] = C[k] + T * bg[k];
+    gr[k] = charbonnier_prime((C_force ? C_force[k] : Cf[k]) - target[k]);
+  }
+  *T_end = T;
+  float gT = gr[0] * bg[0] + gr[1] * bg[1] + gr[2] * bg[2];
+  for (int j = n - 1; j >= 0; --j) {
+    if (j >= used) {
+      dLds[j] = 0.0f;
+      dLdc[3 * j] = dLdc[3 * j + 1] = dLdc[3 * j + 2] = 0.0f;
+      continue;
+    }
+    const float alpha = 1.0f - expf(fminf(fmaxf(-sig[j] * dt, -5.0f), 18.0f));
+    const float Ti = Tr[j];
+    const float* cs = rgb + 3 * j;
+    const float gA = gr[0] * (Ti * cs[0]) + gr[1] * (Ti * cs[1]) + gr[2] * (Ti * cs[2]);
+    const float gAlpha = gA - gT * Ti;
+    dLds[j] = gAlpha * (dt * (1.0f - alpha)) + regu;
+    const float ws = Ti * alpha;
+    for (int k = 0; k < 3; ++k) dLdc[3 * j + k] = ws * gr[k];
+    gT = (gr[0] * (alpha * cs[0]) + gr[1] * (alpha * cs[1]) + gr[2] * (alpha * cs[2])) + (1.0f - alpha) * gT;
+  }
+  return used;
+}
+
+/* Per ray: the march's samples (ora_march_ray), their encodings and MLP outputs, front-to-back compositing
+ * with alpha = 1 - exp(clamp(-sigma dt, -5, 18)) (ffnerf_OG.cl:1505-1520) that stops after the sample leaving
+ * T < T_stop, the Charbonnier loss gradient at the composited colour plus background
+ * (ffnerf_OG.cl:1534-1562), and its backward as a back-to-front recurrence of dL/dT
+ * (gT_i = g.(alpha_i c_i) + (1 - alpha_i) gT_(i+1), gT_end = g.bg; dL/dsigma_i = (g.(T_i c_i) - gT_(i+1) T_i)
+ * dt (1 - alpha_i) + 5e-3 dt / max_steps, dL/dc_i = T_i alpha_i g: ffnerf_OG.cl:1593-1634 sequentially);
+ * samples past the termination get no gradient.  Then every sample's backward (sample_backward) and the
+ * parameter updates.  A step without samples leaves the table and its moments as they are (no table update
+ * runs) while the MLP's Adam runs on zero gradients.  Taps index samples in march order.
+ * n_used (optional) [num_rays] = samples composited; used_in (optional) [num_rays]: composite exactly that
+ * many samples per ray (another implementation's termination).  No occupancy proposals. */
+int ora_train_step_marched(const ora_cfg* c, ora_params* P, const ora_march_cfg* m, const uint32_t* bits,
+                           const float* rays, const float* targets, float* out_rgb, int32_t num_rays,
+                           const ora_scalars* sc, ora_debug* dbg, const uint32_t* used_in, uint32_t* n_used) {
+  const int L = c->n_levels, F = c->f_per_level, LF = L * F;
+  if (LF > ORA_M || c->nd < 1 || c->nd > 3 || c->nc < 1 || c->nc > 4 || m->max_steps == 0) return -2;
+  int64_t table_entries = 0;
+  for (int l = 0; l < L; ++l) {
+    int64_t e = (int64_t)c->offset[l] + ((int64_t)1 << c->log2_T[l]);
+    if (e > table_entries) table_entries = e;
+  }
+  const int64_t table_n = table_entries * F;
+  float* table_read = (float*)malloc(sizeof(float) * (size_t)table_n);
+  if (!table_read) return -3;
+  memcpy(table_read, P->table, sizeof(float) * (size_t)table_n);
+  double* gW[L_COUNT];
+  double* gb[L_COUNT];
+  int odim[L_COUNT], idim[L_COUNT];
+  for (int k = 0; k < L_COUNT; ++k) {
+    gW[k] = NULL;
+    gb[k] = NULL;
+    if (!ora_layer_shape(c, k, &odim[k], &idim[k])) continue;
+    gW[k] = (double*)calloc((size_t)odim[k] * idim[k], sizeof(double));
+    gb[k] = (double*)calloc((size_t)odim[k], sizeof(double));
+  }
+  double* gtab = (c->hash_opt == 1 || c->table_f16) ? (double*)calloc((size_t)table_n, sizeof(double)) : NULL;
+  ora_params PR = *P;
+  PR.table = table_read;
+  const float D = 0.5f * sqrtf((c->box_max[0] - c->box_min[0]) * (c->box_max[0] - c->box_min[0]) +
+                               (c->box_max[1] - c->box_min[1]) * (c->box_max[1] - c->box_min[1]) +
+                               (c->box_max[2] - c->box_min[2]) * (c->box_max[2] - c->box_min[2]));
+  const float dt = m->dt;
+  const float regu = 5e-3f * dt / (float)m->max_steps;
+  float* ts = (float*)malloc(sizeof(float) * m->max_steps);
+  mlp_state* st = (mlp_state*)malloc(sizeof(mlp_state) * m->max_steps);
+  float* sig = (float*)malloc(sizeof(float) * m->max_steps);
+  float* rgb = (float*)malloc(sizeof(float) * 3 * m->max_steps);
+  float* Tr = (float*)malloc(sizeof(float) * m->max_steps);
+  float* dLds = (float*)malloc(sizeof(float) * m->max_steps);
+  float* dLdc = (float*)malloc(sizeof(float) * 3 * m->max_steps);
+  int64_t base = 0;
+  for (int32_t r = 0; r < num_rays; ++r) {
+    const float* ray = rays + 8 * (int64_t)r;
+    const int n = ora_march_ray(c, m, bits, ray, ts);
+    for (int j = 0; j < n; ++j) {
+      float x[3];
+      for (int i = 0; i < 3; ++i) x[i] = ray[i] + ts[j] * ray[4 + i];
+      encode_point(c, table_read, x, st[j].a0, NULL, NULL);
+      const int64_t b = base + j;
+      mlp_forward(c, &PR, ray + 4, sc->sh_multiplier, &st[j],
+                  (dbg && dbg->relu_in) ? dbg->relu_in + ORA_RELU_WORDS * b : NULL);
+      if (dbg && dbg->relu_out)
+        for (int h = 0; h < 7; ++h) {
+          dbg->relu_out[ORA_RELU_WORDS * b + 2 * h] = (uint32_t)st[j].own[h];
+          dbg->relu_out[ORA_RELU_WORDS * b + 2 * h + 1] = (uint32_t)(st[j].own[h] >> 32);
+        }
+      if (dbg && dbg->preact) memcpy(dbg->preact + 7 * ORA_M * b, st[j].pre, sizeof(float) * 7 * ORA_M);
+      if (dbg && dbg->a0) memcpy(dbg->a0 + b * LF, st[j].a0, sizeof(float) * LF);
+      sig[j] = st[j].sigma;
+      for (int k = 0; k < 3; ++k) rgb[3 * j + k] = st[j].rgb[k];
+    }
+    float bg[3] = {0.0f, 0.0f, 0.0f};
+    if (c->background == 1) {
+      bg[0] = bg[1] = bg[2] = 1.0f;
+    } else if (c->background == 2) {
+      uint32_t rr = ora_hash_u32(sc->rng_seed ^ (uint32_t)r * 747796405u ^ 0xA511E9B3u);
+      bg[0] = rand01(&rr);
+      bg[1] = rand01(&rr);
+      bg[2] = rand01(&rr);
+    }
+    float Cf[3], T;
+    const int used = ora_composite_marched(sig, rgb, n, dt, m->T_stop, bg, targets + 4 * (int64_t)r,
+                                           (dbg && dbg->C_in) ? dbg->C_in + 4 * (int64_t)r : NULL,
+                                           used_in ? (int)used_in[r] : -1, regu, Tr, dLds, dLdc, Cf, &T);
+    for (int k = 0; k < 3; ++k) out_rgb[4 * (int64_t)r + k] = fminf(fmaxf(Cf[k], 0.0f), 1.0f);
+    out_rgb[4 * (int64_t)r + 3] = 4.0f; /* the training output's marker (ffnerf_OG.cl:2091) */
+    if (n_used) n_used[r] = (uint32_t)used;
+    if (dbg) {
+      if (dbg->Ts) memcpy(dbg->Ts + base, ts, sizeof(float) * n);
+      if (dbg->sigma) memcpy(dbg->sigma + base, sig, sizeof(float) * n);
+      if (dbg->rgb) memcpy(dbg->rgb + 3 * base, rgb, sizeof(float) * 3 * n);
+      if (dbg->Tr) memcpy(dbg->Tr + base, Tr, sizeof(float) * n);
+      if (dbg->T_final) dbg->T_final[r] = T;
+      if (dbg->C_out)
+        for (int k = 0; k < 4; ++k) dbg->C_out[4 * (int64_t)r + k] = k < 3 ? Cf[k] : 0.0f;
+      if (dbg->dL_dsigma) memcpy(dbg->dL_dsigma + base, dLds, sizeof(float) * n);
+      if (dbg->dL_dc) memcpy(dbg->dL_dc + 3 * base, dLdc, sizeof(float) * 3 * n);
+    }
+    for (int j = 0; j < n; ++j) {
+      float x[3];
+      for (int i = 0; i < 3; ++i) x[i] = ray[i] + ts[j] * ray[4 + i];
+      sample_backward(c, P, sc, &st[j], x, ts[j], dt, D, dLds[j], dLdc + 3 * j, gW, gb, gtab,
+                      (dbg && dbg->dL_da0) ? dbg->dL_da0 + (base + j) * LF : NULL);
+    }
+    base += n;
+  }
+  apply_updates(c, P, sc, gW, gb, odim, idim, base > 0 ? gtab : NULL, table_n, dbg);
+  for (int k = 0; k < L_COUNT; ++k) { free(gW[k]); free(gb[k]); }
+  free(gtab);
+  free(table_read);
+  free(ts);
+  free(st);
+  free(sig);
+  free(rgb);
+  free(Tr);
+  free(dLds);
+  free(dLdc);
+  return 0;
 }

@@ -137,6 +137,12 @@ def load(path: Path = None) -> C.CDLL:
     lib.ora_train_step.argtypes = [C.POINTER(OraCfg), C.POINTER(OraParams), _fp, _fp, _fp, C.c_int32, C.c_int32,
                                    C.POINTER(OraScalars), C.POINTER(OraDebug)]
     lib.ora_occ_bitfield.argtypes = [_up, C.c_int32, C.c_uint32, _up]
+    lib.ora_train_step_marched.restype = C.c_int
+    lib.ora_train_step_marched.argtypes = [C.POINTER(OraCfg), C.POINTER(OraParams), C.POINTER(OraMarchCfg), _up, _fp,
+                                           _fp, _fp, C.c_int32, C.POINTER(OraScalars), C.POINTER(OraDebug), _up, _up]
+    lib.ora_composite_marched.restype = C.c_int
+    lib.ora_composite_marched.argtypes = [_fp, _fp, C.c_int, C.c_float, C.c_float, _fp, _fp, _fp, C.c_int, C.c_float,
+                                          _fp, _fp, _fp, _fp, _fp]
     lib.ora_march_ray.restype = C.c_int
     lib.ora_march_ray.argtypes = [C.POINTER(OraCfg), C.POINTER(OraMarchCfg), _up, _fp, _fp]
     lib.ora_render_ray.restype = C.c_int
@@ -317,6 +323,20 @@ def occ_bitfield(occ: np.ndarray, G: int, q_min: int) -> np.ndarray:
     return bits
 
 
+def composite_marched(sigma, rgb, dt, T_stop, bg, target, regu, C_force=None, used_force=-1):
+    """One marched ray's compositing and backward: (used, Tr, dL/dsigma, dL/dc, Cf, T_end)."""
+    sigma = np.ascontiguousarray(sigma, np.float32)
+    rgb = np.ascontiguousarray(rgb, np.float32).reshape(-1, 3)
+    n = sigma.size
+    Tr, dLds = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    dLdc, Cf, T = np.zeros((n, 3), np.float32), np.zeros(3, np.float32), np.zeros(1, np.float32)
+    cf = None if C_force is None else np.ascontiguousarray(C_force, np.float32)
+    used = lib().ora_composite_marched(fptr(sigma), fptr(rgb), n, dt, T_stop, fptr(np.asarray(bg, np.float32)),
+                                       fptr(np.asarray(target, np.float32)), fptr(cf), used_force, regu, fptr(Tr),
+                                       fptr(dLds), fptr(dLdc), fptr(Cf), fptr(T))
+    return used, Tr, dLds, dLdc, Cf, float(T[0])
+
+
 def march_ray(cfg: OraCfg, m: OraMarchCfg, bits: np.ndarray, ray: np.ndarray) -> np.ndarray:
     ray = np.ascontiguousarray(ray, np.float32).reshape(8)
     t = np.zeros(max(1, m.max_steps), np.float32)
@@ -360,6 +380,58 @@ class OracleModel:
             used[r] = lib().ora_render_ray(C.byref(self.cfg), C.byref(P), C.byref(m), uptr(bits),
                                            fptr(rays[r].copy()), o.ctypes.data_as(_fp))
         return out, used
+
+    def train_step_marched(self, rays, targets, bits, m: OraMarchCfg, scalars: dict, relu_in=None, C_in=None,
+                           used_in=None):
+        """One training step over marched samples (ora_train_step_marched).  Returns (out [N,4], n_used [N],
+        taps) with the taps indexed by sample in march order.  relu_in / C_in / used_in (optional): another
+        implementation's ReLU branches [n][14], loss colours [N][4] and samples composited per ray [N]."""
+        rays = np.ascontiguousarray(rays, np.float32).reshape(-1, 8)
+        targets = np.ascontiguousarray(targets, np.float32).reshape(-1, 4)
+        bits = np.ascontiguousarray(bits, np.uint32)
+        N = rays.shape[0]
+        n = int(sum(march_ray(self.cfg, m, bits, r).size for r in rays))
+        LF = self.cfg.n_levels * self.cfg.f_per_level
+        t = dict(Ts=np.zeros(n, np.float32), a0=np.zeros((n, LF), np.float32), sigma=np.zeros(n, np.float32),
+                 rgb=np.zeros((n, 3), np.float32), Tr=np.zeros(n, np.float32), T_final=np.zeros(N, np.float32),
+                 dL_dsigma=np.zeros(n, np.float32), dL_dc=np.zeros((n, 3), np.float32),
+                 dL_da0=np.zeros((n, LF), np.float32), relu_out=np.zeros((n, RELU_WORDS), np.uint32),
+                 preact=np.zeros((n, 7, M), np.float32), C=np.zeros((N, 4), np.float32))
+        dbg = OraDebug()
+        for k, v in t.items():
+            key = {"relu_out": "relu_out", "C": "C_out"}.get(k, k)
+            setattr(dbg, key, uptr(v) if v.dtype == np.uint32 else fptr(v))
+        for i, wn in enumerate(LAYER_NAMES):
+            if wn in self.p:
+                t["g" + wn] = np.zeros_like(self.p[wn])
+                t["g" + BIAS_NAMES[i]] = np.zeros_like(self.p[BIAS_NAMES[i]])
+                dbg.gW[i] = fptr(t["g" + wn])
+                dbg.gb[i] = fptr(t["g" + BIAS_NAMES[i]])
+        if self.cfg.hash_opt == 1:
+            t["g_table"] = np.zeros_like(self.p["table"])
+            dbg.g_table = fptr(t["g_table"])
+        keep = []
+        if relu_in is not None:
+            keep.append(np.ascontiguousarray(relu_in, np.uint32).reshape(n, RELU_WORDS))
+            dbg.relu_in = uptr(keep[-1])
+        if C_in is not None:
+            keep.append(np.ascontiguousarray(C_in, np.float32).reshape(N, 4))
+            dbg.C_in = fptr(keep[-1])
+        ui = None if used_in is None else np.ascontiguousarray(used_in, np.uint32).reshape(N)
+        sc = OraScalars()
+        for k in ("lr", "lr_t", "color_rel_lr", "sh_multiplier", "occ_strength", "beta1", "beta2", "eps"):
+            setattr(sc, k, float(scalars[k]))
+        sc.rng_seed = int(scalars["rng_seed"]) & 0xFFFFFFFF
+        sc.do_train = 1
+        out = np.zeros((N, 4), np.float32)
+        used = np.zeros(N, np.uint32)
+        P = self._params()
+        rc = lib().ora_train_step_marched(C.byref(self.cfg), C.byref(P), C.byref(m), uptr(bits), fptr(rays),
+                                          fptr(targets), fptr(out), N, C.byref(sc), C.byref(dbg), uptr(ui),
+                                          uptr(used))
+        if rc != 0:
+            raise RuntimeError(f"ora_train_step_marched failed: {rc}")
+        return out, used, t
 
     def train_step(self, rays, targets, S, scalars: dict, taps=False, relu_in=None, C_in=None):
         """One step of the restatement.  relu_in ([N*S][14] u32, optional): take every hidden unit's ReLU

@@ -168,3 +168,50 @@ class GpuModel:
                                      fl.ptr(used), fl.stream_ptr()), "ffn_render")
         torch.cuda.synchronize()
         return to_np(out), to_np(used)
+
+    def train_step_marched(self, rays, targets, bits, mp, scalars: dict):
+        """ffn_train_step_marched with every tap.  The step's samples (and so the taps' length) come from an
+        ffn_march of the same rays first, which also gives the sample times (Ts), positions (x) and samples
+        marched per ray (n_march).  Returns (out [N,4], n_used [N], taps)."""
+        counts, _, smp, _, n = self.march(rays, bits, mp)
+        rays_t = to_dev(np.ascontiguousarray(rays, np.float32).reshape(-1, 8))
+        tg_t = to_dev(np.ascontiguousarray(targets, np.float32).reshape(-1, 4))
+        bits_t = to_dev(np.ascontiguousarray(bits, np.uint32))
+        N = rays_t.shape[0]
+        out = torch.zeros((N, 4), dtype=torch.float32, device=DEV)
+        used = torch.zeros(N, dtype=torch.int32, device=DEV)
+        sc = fl.FfnStepScalars()
+        for k in ("lr", "lr_t", "color_rel_lr", "sh_multiplier", "occ_strength", "beta1", "beta2", "eps"):
+            setattr(sc, k, float(scalars[k]))
+        sc.rng_seed = int(scalars["rng_seed"]) & 0xFFFFFFFF
+        sc.do_train = 1
+        LF = self.spec["n_levels"] * self.spec["f_per_level"]
+        nz = max(n, 1)
+        z = lambda *s: torch.zeros(s, dtype=torch.float32, device=DEV)
+        td = dict(a0=z(nz, LF), sigma=z(nz), rgb=z(nz, 3), Tr=z(nz), T_final=z(N), dL_dsigma=z(nz), dL_dc=z(nz, 3),
+                  dL_da0=z(nz, LF), relu=torch.zeros((nz, fl.RELU_WORDS), dtype=torch.int32, device=DEV), C=z(N, 4))
+        tp = fl.FfnTaps()
+        for k, v in td.items():
+            setattr(tp, "color" if k == "C" else k, fl.ptr(v))
+        for i, wn in enumerate(fl.LAYER_NAMES):
+            if wn in self.t:
+                bn = fl.BIAS_NAMES[i]
+                td["g" + wn] = torch.zeros_like(self.t[wn])
+                td["g" + bn] = torch.zeros_like(self.t[bn])
+                tp.gW[i] = fl.ptr(td["g" + wn])
+                tp.gb[i] = fl.ptr(td["g" + bn])
+        if self.spec.get("hash_opt", 0) == 1:
+            td["g_table"] = torch.zeros(self.t["table"].shape, dtype=torch.float32, device=DEV)
+            tp.g_table = fl.ptr(td["g_table"])
+        fl.check(self.lib.ffn_train_step_marched(self.h.h, fl.ptr(rays_t), fl.ptr(tg_t), fl.ptr(out), N,
+                                                 fl.ptr(bits_t), C.byref(mp), C.byref(sc), C.byref(tp), fl.ptr(used),
+                                                 fl.stream_ptr()), "ffn_train_step_marched")
+        torch.cuda.synchronize()
+        res = {k: to_np(v) for k, v in td.items()}
+        res["relu"] = res["relu"].view(np.uint32)
+        for k in ("a0", "sigma", "rgb", "Tr", "dL_dsigma", "dL_dc", "dL_da0", "relu"):
+            res[k] = res[k][:n]
+        res["Ts"] = smp[:n, 3].copy()
+        res["x"] = smp[:n, :3].copy()
+        res["n_march"] = counts.astype(np.int64)
+        return to_np(out), to_np(used, np.uint32), res

@@ -143,21 +143,7 @@ def compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
     train = bool(sc.get("do_train", 1))
     if not train:
         return m, o, stats
-    # loss gradients and the encoding gradient, every sample
-    for k in ("dL_dsigma", "dL_dc", "dL_da0"):
-        stats[k] = _maxrel(G[k], O[k])
-        assert stats[k] <= tol["loss"], (k, stats[k])
-    # summed weight gradients
-    shapes = layer_shapes(spec)
-    for wn in shapes:
-        bn = BIASES[LAYERS.index(wn)]
-        for k in (wn, bn):
-            stats["g" + k] = _normrel(G["g" + k], O["g" + k])
-            assert stats["g" + k] <= tol["grad"], (k, stats["g" + k])
-    hash_adam = int(spec.get("hash_opt", 0)) == 1
-    if hash_adam:
-        stats["g_table"] = _maxrel(G["g_table"], O["g_table"])
-        assert stats["g_table"] <= tol["table"], stats["g_table"]
+    _check_grads(spec, G, O, tol, stats)
     st_g, st_o = m.state(), o.p
     # occupancy: proposals from the GPU's own compositing reproduce its grid word for word
     assert np.array_equal(st_g["occ_in"], p["occ_in"])
@@ -172,39 +158,102 @@ def compare_step(spec, p, rays, tg, S, sc, gh, ora, check_params=True):
         assert np.array_equal(st_g["occ_st"], p["occ_st"])
     if not check_params:
         return m, o, stats
-    # Adam on the MLP parameters (colour layers at lr_t * color_rel_lr, as float32)
+    x = (rays[:, None, :3] + G["Ts"].reshape(-1, S)[:, :, None] * rays[:, None, 4:7]).astype(np.float32)
+    _check_params(spec, p, G, O, st_g, st_o, sc, tol, ora, o.cfg, x.reshape(-1, 3), stats)
+    return m, o, stats
+
+
+def _check_grads(spec, G, O, tol, stats):
+    """Loss and encoding gradients of every sample; the summed weight and table gradients."""
+    for k in ("dL_dsigma", "dL_dc", "dL_da0"):
+        stats[k] = _maxrel(G[k], O[k])
+        assert stats[k] <= tol["loss"], (k, stats[k])
+    for wn in layer_shapes(spec):
+        bn = BIASES[LAYERS.index(wn)]
+        for k in (wn, bn):
+            stats["g" + k] = _normrel(G["g" + k], O["g" + k])
+            assert stats["g" + k] <= tol["grad"], (k, stats["g" + k])
+    if int(spec.get("hash_opt", 0)) == 1:
+        stats["g_table"] = _maxrel(G["g_table"], O["g_table"])
+        assert stats["g_table"] <= tol["table"], stats["g_table"]
+
+
+def _check_params(spec, p, G, O, st_g, st_o, sc, tol, ora, cfg, x, stats):
+    """The updated parameters from state p: Adam on the MLP (colour layers at lr_t * color_rel_lr, as
+    float32) and on the table, or the reference SGD on the table.  x [n, 3]: the step's sample positions."""
+    f16 = spec.get("table_dtype", 0) in (1, "fp16")
     lr_t = np.float32(sc["lr_t"])
-    for wn in shapes:
+    for wn in layer_shapes(spec):
         bn = BIASES[LAYERS.index(wn)]
         lr = float(lr_t * np.float32(sc["color_rel_lr"])) if LAYERS.index(wn) >= 4 else float(lr_t)
         for k in (wn, bn):
             _check_adam(k, p[k], p["m" + k], p["v" + k], G["g" + k], O["g" + k], st_g, st_o, lr, sc, tol["grad"],
                         tol["undet_frac"], ora, stats)
-    if hash_adam:
+    if int(spec.get("hash_opt", 0)) == 1:
         _check_adam("table", p["table"], p["m_table"], p["v_table"], G["g_table"], O["g_table"], st_g, st_o,
                     float(lr_t), sc, tol["table"], tol["undet_frac"], ora, stats, f16=f16)
+        return
+    # reference SGD: the update is linear in the gradient.  The restatement adds every (sample, corner)
+    # contribution to the float table one at a time, as the reference's atomics do, rounding each time at the
+    # entry's magnitude; the GPU adds each entry's exact sum once.  An entry with n contributions may so differ
+    # by n/2 + 1 ulps beyond the gradient tolerance.
+    d_g = st_g["table"].astype(np.float64) - p["table"]
+    d_o = st_o["table"].astype(np.float64) - p["table"]
+    big = np.maximum(np.abs(p["table"]), np.abs(st_o["table"])).astype(np.float32)
+    ulp = np.spacing(big).astype(np.float64)
+    err = np.abs(d_g - d_o)
+    stats["table_sgd"] = float(err.max() / (np.abs(d_o).max() + 1e-30))
+    if f16:  # both add each entry's summed update once, rounding to binary16: one ulp of binary16 apart
+        lim = tol["table"] * np.abs(d_o).max() + np.spacing(big.astype(np.float16)).astype(np.float64)
     else:
-        # reference SGD: the update is linear in the gradient.  The restatement adds every (sample, corner)
-        # contribution to the float table one at a time, as the reference's atomics do, rounding each time at
-        # the entry's magnitude; the GPU adds each entry's exact sum once.  An entry with n contributions may
-        # so differ by n/2 + 1 ulps beyond the gradient tolerance.
-        d_g = st_g["table"].astype(np.float64) - p["table"]
-        d_o = st_o["table"].astype(np.float64) - p["table"]
-        big = np.maximum(np.abs(p["table"]), np.abs(st_o["table"])).astype(np.float32)
-        ulp = np.spacing(big).astype(np.float64)
-        if f16:  # both add each entry's summed update once, rounding to binary16: one ulp of binary16 apart
-            err = np.abs(d_g - d_o)
-            lim = tol["table"] * np.abs(d_o).max() + np.spacing(big.astype(np.float16)).astype(np.float64)
-            stats["table_sgd"] = float(err.max() / (np.abs(d_o).max() + 1e-30))
-            assert (err <= lim).all(), stats["table_sgd"]
-            return m, o, stats
-        x = (rays[:, None, :3] + G["Ts"].reshape(-1, S)[:, :, None] * rays[:, None, 4:7]).astype(np.float32)
-        _, idx, _ = ora.hash_encode(o.cfg, p["table"], x.reshape(-1, 3), with_idx=True)
+        _, idx, _ = ora.hash_encode(cfg, p["table"], x, with_idx=True)
         F = int(spec["f_per_level"])
         n_per_entry = np.bincount((idx.ravel() // F).astype(np.int64), minlength=p["table"].size // F)
         n_contrib = np.repeat(n_per_entry, F).astype(np.float64)
-        err = np.abs(d_g - d_o)
         lim = tol["table"] * np.abs(d_o).max() + (0.5 * n_contrib + 2.0) * ulp
-        stats["table_sgd"] = float(err.max() / (np.abs(d_o).max() + 1e-30))
-        assert (err <= lim).all(), stats["table_sgd"]
+    assert (err <= lim).all(), stats["table_sgd"]
+
+
+def compare_marched_step(spec, p, rays, tg, bits, mp, sc, gh, ora):
+    """One marched training step (ffn_train_step_marched against ora_train_step_marched) from state p, checked
+    as compare_step checks the resampled step.  The march is bit-exact (sample times, samples per ray), and so
+    are the encodings; the restatement takes the GPU's ReLU branches, loss colours and samples composited per
+    ray.  Rays whose termination differs from the restatement's own run are counted, and each stops where T
+    lies within rounding of T_stop.  The step makes no occupancy proposals: both grids stay as they were."""
+    prec = int(spec.get("mlp_precision", 0))
+    tol = TOL[prec]
+    m = gh.GpuModel(spec, p)
+    out_g, used_g, G = m.train_step_marched(rays, tg, bits, mp, sc)
+    mcfg = ora.march_cfg(mp.res, mp.dt, mp.max_steps, T_stop=mp.T_stop, sh_multiplier=mp.sh_multiplier)
+    free = ora.OracleModel(spec, {k: v.copy() for k, v in p.items()})
+    _, used_free, F = free.train_step_marched(rays, tg, bits, mcfg, sc)
+    o = ora.OracleModel(spec, {k: v.copy() for k, v in p.items()})
+    out_o, used_o, O = o.train_step_marched(rays, tg, bits, mcfg, sc, relu_in=G["relu"], C_in=G["C"],
+                                            used_in=used_g)
+    stats = {"samples": int(G["Ts"].size), "composited": int(used_g.sum())}
+    assert np.array_equal(G["Ts"], O["Ts"])
+    assert np.array_equal(used_o, used_g)
+    assert np.array_equal(G["a0"].view(np.uint32), O["a0"].view(np.uint32))
+    flips = np.flatnonzero(used_g != used_free)
+    stats["termination_flips"] = int(flips.size)
+    assert flips.size <= max(2, 0.01 * rays.shape[0]), flips.size
+    assert mp.T_stop > 0.0 or flips.size == 0
+    off = np.concatenate([[0], np.cumsum(G["n_march"])]).astype(np.int64)
+    for r in flips:
+        k = int(min(used_g[r], used_free[r]))  # the earlier stop: T after its last sample straddles T_stop
+        T_after = F["Tr"][off[r] + k] if k < G["n_march"][r] else F["T_final"][r]
+        # T is a product of up to max_steps factors, each carrying the forward tolerance of sigma
+        assert abs(T_after / mp.T_stop - 1.0) <= 50.0 * tol["fwd"], (r, T_after)
+    _check_relu(spec, G, O, tol, stats)
+    for k in ("sigma", "rgb", "Tr", "T_final"):
+        stats[k] = _maxrel(G[k], O[k])
+        assert stats[k] <= tol["fwd"], (k, stats[k])
+    stats["out"] = float(np.abs(out_g - out_o).max())
+    assert stats["out"] <= tol["out"], stats["out"]
+    stats["C"] = float(np.abs(G["C"] - O["C"]).max())
+    assert stats["C"] <= tol["out"], stats["C"]
+    _check_grads(spec, G, O, tol, stats)
+    st_g, st_o = m.state(), o.p
+    assert np.array_equal(st_g["occ_in"], p["occ_in"]) and np.array_equal(st_g["occ_st"], p["occ_st"])
+    _check_params(spec, p, G, O, st_g, st_o, sc, tol, ora, o.cfg, G["x"], stats)
     return m, o, stats

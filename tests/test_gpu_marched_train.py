@@ -1,0 +1,99 @@
+"""GPU parity of the marched training step (ffn_train_step_marched) against the restatement
+(ora_train_step_marched): samples from the DDA march through an occupancy bitfield instead of the resampler,
+compositing that stops once T < T_stop, the Charbonnier loss, the MLP backward, the table update and the MLP
+Adam.  How each difference is accounted for is described in parity.compare_marched_step."""
+import numpy as np
+import pytest
+
+from common import look_at_rays, random_params, spec_cfg0, sphere_targets, default_scalars
+from parity import compare_marched_step
+
+pytestmark = pytest.mark.gpu
+
+R = 32
+DT = np.float32(np.sqrt(3.0) / 128)
+
+
+@pytest.fixture(scope="module")
+def gh():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("a GPU test ran without a visible GPU")
+    import gpu_helpers
+    return gpu_helpers
+
+
+def shell_bits(R, seed=0, frac=0.02):
+    """A spherical shell of occupied cells plus scattered ones, as an R^3 bitfield."""
+    rng = np.random.default_rng(seed)
+    c = (np.arange(R) + 0.5) / R
+    z, y, x = np.meshgrid(c, c, c, indexing="ij")
+    rad = np.sqrt((x - 0.5) ** 2 + (y - 0.5) ** 2 + (z - 0.5) ** 2)
+    occ = (np.abs(rad - 0.3) <= 0.08) | (rng.random((R, R, R)) < frac)
+    idx = np.nonzero(occ.reshape(-1))[0]
+    bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
+    np.bitwise_or.at(bits, idx >> 5, (np.uint32(1) << (idx & 31).astype(np.uint32)))
+    return bits
+
+
+@pytest.mark.parametrize("T_stop,hash_opt,table", [(1e-2, 1, "fp32"), (0.0, 1, "fp32"), (1e-2, 0, "fp32"),
+                                                   (1e-2, 1, "fp16"), (1e-2, 0, "fp16")])
+def test_marched_steps_match_oracle(gh, ora, T_stop, hash_opt, table):
+    print(f"[case] marched train T_stop={T_stop} hash_opt={hash_opt} table={table}", flush=True)
+    import ffn_lib as fl
+    spec = spec_cfg0(occ_G=R // 2, hash_opt=hash_opt, table_dtype=table)
+    p = random_params(spec, seed=41)
+    if table == "fp16":
+        p["table"] = p["table"].astype(np.float16).astype(np.float32)
+    p["bd_out"][0] = 8.0  # dense enough that about a third of the rays terminate inside their marched samples
+    rays = look_at_rays(384, spec, seed=42, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    bits = shell_bits(R, seed=43, frac=0.2)
+    mp = fl.march_params(R, DT, 128, T_stop=T_stop)
+    for step in range(3):
+        sc = default_scalars(rng_seed=1000 + step, occ_strength=0.0)
+        m, _, stats = compare_marched_step(spec, p, rays, tg, bits, mp, sc, gh, ora)
+        print(f"[step {step}] {stats}", flush=True)
+        assert stats["samples"] > 2000
+        if T_stop > 0.0:
+            assert stats["composited"] < stats["samples"]  # some rays terminate early
+        else:
+            assert stats["composited"] == stats["samples"]
+        p = m.state()  # the next step starts from the GPU's state, as training does
+
+
+def test_marched_step_without_samples(gh, ora):
+    """An empty bitfield: no samples and the background colour; the table and its moments stay as they are
+    while the MLP's Adam runs on zero gradients (moving by its moments), as in the restatement."""
+    print("[case] marched train, no samples", flush=True)
+    import ffn_lib as fl
+    spec = spec_cfg0(occ_G=R // 2, hash_opt=1, background=1)
+    p = random_params(spec, seed=51)
+    rng = np.random.default_rng(52)
+    for k in list(p):  # nonzero Adam moments
+        if k.startswith("v"):
+            p[k] = rng.uniform(1e-6, 1e-4, p[k].shape).astype(np.float32)
+        elif k.startswith("m"):
+            p[k] = rng.normal(0, 1e-3, p[k].shape).astype(np.float32)
+    rays = look_at_rays(64, spec, seed=53)
+    tg = sphere_targets(rays, spec)
+    bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
+    mp = fl.march_params(R, DT, 128, T_stop=1e-3)
+    sc = default_scalars(rng_seed=7, occ_strength=0.0)
+    m = gh.GpuModel(spec, p)
+    out, used, G = m.train_step_marched(rays, tg, bits, mp, sc)
+    assert not used.any() and G["n_march"].sum() == 0
+    np.testing.assert_array_equal(out[:, :3], np.ones((64, 3), np.float32))
+    np.testing.assert_array_equal(out[:, 3], np.full(64, 4.0, np.float32))
+    o = ora.OracleModel(spec, {k: v.copy() for k, v in p.items()})
+    out_o, used_o, _ = o.train_step_marched(rays, tg, bits, ora.march_cfg(R, DT, 128, T_stop=1e-3), sc)
+    np.testing.assert_array_equal(out, out_o)
+    st = m.state()
+    for k, v in o.p.items():
+        if k.startswith("occ_"):
+            np.testing.assert_array_equal(st[k], v)
+        else:
+            np.testing.assert_allclose(st[k], v, rtol=2e-6, atol=1e-12, err_msg=k)
+    for k in ("table", "m_table", "v_table"):
+        np.testing.assert_array_equal(st[k], p[k])
+    assert not np.array_equal(st["Wd_in"], p["Wd_in"])  # the MLP's Adam moved by its moments

@@ -193,3 +193,47 @@ def test_render_constant_field_closed_form():
             Tn = (1.0 - float(alpha)) ** n
             np.testing.assert_allclose(out[r, 3], Tn, rtol=1e-5)
             np.testing.assert_allclose(out[r, :3], rgb * (1.0 - Tn), rtol=1e-5, atol=1e-7)
+
+
+def test_marched_compositing_matches_autograd(ora):
+    """ora_composite_marched (the marched training step's compositing, loss gradient and backward) against
+    float64 autograd of the same function: alpha = 1 - exp(-sigma dt), front-to-back weights, the
+    Charbonnier loss sqrt(r^2 + 1e-6) at the composited colour plus background, stopping after the sample
+    that leaves T < T_stop; dL/dsigma adds the density penalty regu on every composited sample, and the
+    samples after the stop get no gradient."""
+    import torch
+    rng = np.random.default_rng(9)
+    for case in range(40):
+        n = int(rng.integers(1, 90))
+        dt = np.float32(rng.uniform(0.005, 0.03))
+        sig = rng.uniform(0.0, 4.5 / dt, n).astype(np.float32) * (rng.random(n) < 0.5)  # sigma dt < 5: no clamp
+        rgb = rng.uniform(0.05, 0.95, (n, 3)).astype(np.float32)
+        bg = rng.uniform(0, 1, 3).astype(np.float32) * (case % 2)
+        tg = rng.uniform(0, 1, 3).astype(np.float32)
+        T_stop = np.float32([0.0, 1e-4, 1e-2][case % 3])
+        regu = np.float32(5e-3) * dt / np.float32(128)
+        used, Tr, dLds, dLdc, Cf, T_end = ora.composite_marched(sig, rgb, dt, T_stop, bg, tg, regu)
+        s = torch.tensor(sig.astype(np.float64), requires_grad=True)
+        c = torch.tensor(rgb.astype(np.float64), requires_grad=True)
+        alpha = 1.0 - torch.exp(-s * float(dt))
+        T = torch.cumprod(torch.cat([torch.ones(1, dtype=torch.float64), 1.0 - alpha]), 0)
+        stop = n
+        Td = T.detach().numpy()
+        for j in range(n):  # the same rule in float64
+            if Td[j + 1] < float(T_stop):
+                stop = j + 1
+                break
+        if abs(Td[stop] - float(T_stop)) < 1e-5 and stop < n:
+            continue  # within rounding of the threshold: either stop is right
+        assert used == stop, (case, used, stop)
+        C = (T[:stop, None] * alpha[:stop, None] * c[:stop]).sum(0) + T[stop] * torch.tensor(bg, dtype=torch.float64)
+        loss = torch.sqrt((C - torch.tensor(tg, dtype=torch.float64)) ** 2 + 1e-6).sum()
+        loss.backward()
+        g_s = s.grad.numpy().copy()
+        g_s[:stop] += float(regu)
+        g_c = c.grad.numpy()
+        scale = max(np.abs(g_s).max(), 1e-12)
+        assert np.abs(dLds - g_s).max() <= 2e-4 * scale + 1e-9, (case, np.abs(dLds - g_s).max(), scale)
+        assert np.abs(dLdc - g_c).max() <= 2e-4 * max(np.abs(g_c).max(), 1e-12) + 1e-9, case
+        assert np.allclose(Cf, C.detach().numpy(), rtol=1e-5, atol=1e-6)
+        assert np.all(dLds[stop:] == 0) and np.all(dLdc[stop:] == 0)
