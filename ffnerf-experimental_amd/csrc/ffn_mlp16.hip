@@ -1,30 +1,40 @@
 // ffn_mlp16.hip -- the fused MLP step on 16-bit MFMAs with fp32 accumulation:
-// forward and backward chains in fp16 (v_mfma_f32_16x16x16_f16; each layer's
-// deltas are scaled by a per-wavefront power of two that puts their largest
-// magnitude just below 2^14, so small deltas neither underflow nor lose bits),
-// weight gradients in bf16 (v_mfma_f32_16x16x16_bf16, whose fp32-sized
-// exponent takes the unscaled deltas of all four wavefronts).  Same semantics as the fp32
-// kernel (ffnerf_OG.cl:1373-2082, weight_update.cl:210-341): compositing, loss
-// gradient, proposals and output deltas are the shared fp32 code.
+// forward and backward chains in fp16, weight gradients in bf16 (whose
+// fp32-sized exponent takes the unscaled deltas of all four wavefronts); each
+// layer's fp16 deltas are scaled by a per-wavefront power of two that puts
+// their largest magnitude just below 2^14, so small deltas neither underflow
+// nor lose bits.  Same semantics as the fp32 kernel (ffnerf_OG.cl:1373-2082,
+// weight_update.cl:210-341): compositing, loss gradient, proposals and output
+// deltas are the shared fp32 code.
 //
 // MI355X design
-//   * A 256-thread block (4 wavefronts) walks 64-sample tiles; each wavefront
-//     runs the layers for its 16 samples.  With K = 16 per MFMA a layer's
-//     output tile (lane (g, s) holds neurons 16t + 4g + r of sample s) is, once
-//     converted to four 16-bit values, exactly the B operand of k-block t of
-//     the next layer: activations never move between lanes.
-//   * Weights live in LDS twice, fp16 row-major for the forward (A = W) and
-//     fp16 transposed for the backward (A = W^T); every A operand is one
-//     8-byte LDS read.
+//   * A 256-thread block (4 wavefronts) walks groups of four 64-sample tiles.
+//     Each wavefront runs the layers for its 16 samples of every tile; a
+//     layer's output tile (lane (g, s) holds neurons 16t + 4g + r of sample s)
+//     is exactly one half of the next layer's B operand.
+//   * gfx950's K = 32 MFMAs (v_mfma_f32_16x16x32_f16 / _bf16): lane group g
+//     supplies eight K values per operand.  Slot j of group g in K block kb
+//     stands for neuron 32 kb + 16 (j / 4) + 4 g + j % 4, i.e. the four values
+//     of output tile 2 kb and the four of tile 2 kb + 1 that the lane already
+//     holds -- activations never move between lanes; the weights in LDS are
+//     stored with their K columns in that order, so every A operand is one
+//     16-byte LDS read.  Layers with K = 16 (the output layers' backward, a
+//     16-wide encoding) keep v_mfma_f32_16x16x16.
+//   * Per group: (0) wavefront w loads the compositing inputs of the group's
+//     tile w; (A) every wavefront runs the forward of its samples of the four
+//     tiles and leaves sigma and rgb in LDS; (B) wavefront w composites tile
+//     w alone (64 lanes, its proposals too) and leaves dL/dsigma, dL/dc in LDS
+//     -- one compositing per tile, not one per wavefront; (C) per tile, the
+//     forward again (the activations are not held across the compositing:
+//     registers) and the backward.
 //   * Weight gradients dW = delta . act^T need the samples as K.  Layer by
 //     layer in the backward, every wavefront writes its deltas and the layer's
 //     input activations, transposed, into a block-shared bf16 stash (rows =
 //     neurons, 64 samples per row); after a barrier the layer's 16x16 gradient
 //     tiles are dealt round-robin over the four wavefronts, each of which
-//     accumulates its tiles over the tile's 64 samples (4 MFMAs per tile) in
-//     registers for the whole kernel and stores them into the block's partial
-//     at the end.  A wavefront so holds about a quarter of the gradient, and
-//     the one-layer stash lets two blocks share a CU.
+//     accumulates its tiles over the tile's 64 samples (two K = 32 MFMAs per
+//     tile) in registers for the whole kernel and stores them into the
+//     block's partial at the end.
 #include "ffn_device.h"
 #include "ffn_kernels.h"
 #include "ffn_mlp_common.h"
@@ -32,19 +42,45 @@
 namespace ffn {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ floatx4 mfma_f16(const half4& a, const half4& b, const floatx4& c) {
+__device__ __forceinline__ floatx4 mfma_k16(const half4& a, const half4& b, const floatx4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ floatx4 mfma_bf16(const bf16x4& a, const bf16x4& b, const floatx4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+__device__ __forceinline__ floatx4 mfma_k32(const half8& a, const half8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ floatx4 mfma_k32b(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// neuron of K slot j of lane group g in K block kb (see the file comment)
+__host__ __device__ constexpr int kslot_neuron(int kb, int g, int j) {
+  return 32 * kb + 16 * (j >> 2) + 4 * g + (j & 3);
+}
+// the same for the position p = 32 kb + 8 g + j of a K-ordered row
+__host__ __device__ constexpr int kpos_neuron(int p) { return kslot_neuron(p >> 5, (p >> 3) & 3, p & 7); }
+
 __device__ __forceinline__ half4 to_half4(const floatx4& v) {
   half4 h;
 #pragma unroll
   for (int r = 0; r < 4; ++r) h[r] = (_Float16)v[r];
   return h;
+}
+// K block of two D-layout tiles: slots 0-3 = tile lo, slots 4-7 = tile hi
+__device__ __forceinline__ half8 to_half8(const floatx4& lo, const floatx4& hi) {
+  half8 h;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    h[r] = (_Float16)lo[r];
+    h[4 + r] = (_Float16)hi[r];
+  }
+  return h;
+}
+__device__ __forceinline__ half8 join8(const half4& lo, const half4& hi) {
+  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 __device__ __forceinline__ bf16x4 to_bf16x4(const floatx4& v) {
   bf16x4 h;
@@ -69,21 +105,22 @@ __device__ __forceinline__ float delta_scale(const floatx4 (&d)[NT]) {
   e = e > 100 ? 100 : (e < -100 ? -100 : e);
   return ldexpf(1.0f, e);
 }
-
-template <int NT>
-__device__ __forceinline__ void scaled_half(const floatx4 (&d)[NT], float sc, half4 (&op)[NT]) {
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) op[t][r] = (_Float16)(d[t][r] * sc);
+// 1 / sc exactly (sc a power of two)
+__device__ __forceinline__ float inv_pow2(float sc) {
+  int e;
+  frexpf(sc, &e);  // sc = 2^(e - 1)
+  return ldexpf(1.0f, 1 - e);
 }
 
 template <int LF_, int ND_, int NC_>
 struct Arch16 {
   static constexpr int LF = LF_, ND = ND_, NC = NC_;
   static constexpr int rows_pad(int k) { return k == FFN_WC_OUT ? 16 : layer_out(k); }
-  static constexpr int pf(int k) { return layer_in(k, LF) + 4; }  // fp16 forward row pitch (halves)
-  static constexpr int pt(int k) { return rows_pad(k) + 4; }      // fp16 transposed row pitch
+  // forward copy [rows_pad][in + 8] (columns in K-slot order when in is a multiple of 32); transposed copy
+  // for the backward [in][rows_pad + 8] (columns in K-slot order when rows_pad is a multiple of 32).  The
+  // 8-half pad keeps the 16-byte reads aligned and spreads a tile's 16 rows over distinct banks.
+  static constexpr int pf(int k) { return layer_in(k, LF) + 8; }
+  static constexpr int pt(int k) { return rows_pad(k) + 8; }
   static constexpr int wf_sz(int k) { return layer_active(k, ND, NC) ? rows_pad(k) * pf(k) : 0; }
   static constexpr int wt_sz(int k) { return layer_active(k, ND, NC) ? layer_in(k, LF) * pt(k) : 0; }
   static constexpr int wf_off(int k) {  // in halves
@@ -104,7 +141,7 @@ struct Arch16 {
   }
   static constexpr int b_floats() { return b_off(FFN_N_LAYERS); }
   // one layer's stash (bf16, PS per row): delta rows, then the layer's input activation rows
-  static constexpr int PS = 64 + 4;
+  static constexpr int PS = 64 + 8;
   static constexpr int stash_rows = 128;
   static constexpr int stash_halves() { return stash_rows * PS; }
   // packed gradient (same layout as make_layout)
@@ -117,17 +154,19 @@ struct Arch16 {
     return o;
   }
   static constexpr int g_total() { return g_off(FFN_N_LAYERS); }
-  static constexpr int comp_floats = 2 * 256;
+  // per tile of the group: sigma[64] + rgb[64][3] (the compositing overwrites them with dL/dsigma, dL/dc);
+  // then the group's four busy flags
+  static constexpr int comp_floats = 4 * 256 + 4;
   static constexpr size_t lds_bytes() {
     return (size_t)w_halves() * 2 + (size_t)b_floats() * 4 + (size_t)stash_halves() * 2 + comp_floats * 4;
   }
   static constexpr int blocks_per_cu() { return lds_bytes() <= 80 * 1024 ? 2 : 1; }
 };
 
-// forward layer: out tiles = act(W . in + b); in[kb] is the fp16 B operand of k-block kb
+// forward layer, K = 32 blocks: out tiles = act(W . in + b); W is the K-ordered forward copy
 template <int OT, int KB>
-__device__ __forceinline__ void fwd16(const _Float16* __restrict__ W, int P, const float* __restrict__ B,
-                                      const half4 (&in)[KB], floatx4 (&out)[OT], int g, int s, bool relu) {
+__device__ __forceinline__ void fwd_k32(const _Float16* __restrict__ W, int P, const float* __restrict__ B,
+                                        const half8 (&in)[KB], floatx4 (&out)[OT], int g, int s, bool relu) {
   floatx4 acc[OT];
 #pragma unroll
   for (int t = 0; t < OT; ++t)
@@ -137,8 +176,8 @@ __device__ __forceinline__ void fwd16(const _Float16* __restrict__ W, int P, con
   for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
     for (int t = 0; t < OT; ++t) {
-      const half4 a = *reinterpret_cast<const half4*>(W + (16 * t + s) * P + 16 * kb + 4 * g);
-      acc[t] = mfma_f16(a, in[kb], acc[t]);
+      const half8 w = *reinterpret_cast<const half8*>(W + (16 * t + s) * P + 32 * kb + 8 * g);
+      acc[t] = mfma_k32(w, in[kb], acc[t]);
     }
 #pragma unroll
   for (int t = 0; t < OT; ++t) {
@@ -150,55 +189,96 @@ __device__ __forceinline__ void fwd16(const _Float16* __restrict__ W, int P, con
   }
 }
 
-// backward layer: res tiles over input neurons += (W^T . (delta * sc)) / sc; Wt is [in][out_pad] fp16 and
-// op the scaled fp16 deltas
-template <int RT, int KB>
-__device__ __forceinline__ void bwd16(const _Float16* __restrict__ Wt, int P, const half4 (&op)[KB], float sc,
-                                      floatx4 (&res)[RT], int g, int s) {
+// forward layer with K = 16 (a 16-wide encoding): natural column order
+template <int OT>
+__device__ __forceinline__ void fwd_k16(const _Float16* __restrict__ W, int P, const float* __restrict__ B,
+                                        const half4& in, floatx4 (&out)[OT], int g, int s, bool relu) {
+#pragma unroll
+  for (int t = 0; t < OT; ++t) {
+    floatx4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
+    const half4 w = *reinterpret_cast<const half4*>(W + (16 * t + s) * P + 4 * g);
+    acc = mfma_k16(w, in, acc);
+    if (relu) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
+    }
+    out[t] = acc;
+  }
+}
+
+// backward layer over a 64-wide output (K = 32 blocks): res tiles over input neurons += (W^T . op) / sc, with
+// Wt the K-ordered transposed copy and op the scaled fp16 deltas
+template <int RT>
+__device__ __forceinline__ void bwd_k32(const _Float16* __restrict__ Wt, int P, const half8 (&op)[2], float sc,
+                                        floatx4 (&res)[RT], int g, int s) {
   floatx4 acc[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb)
+  for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      const half4 a = *reinterpret_cast<const half4*>(Wt + (16 * t + s) * P + 16 * kb + 4 * g);
-      acc[t] = mfma_f16(a, op[kb], acc[t]);
+      const half8 w = *reinterpret_cast<const half8*>(Wt + (16 * t + s) * P + 32 * kb + 8 * g);
+      acc[t] = mfma_k32(w, op[kb], acc[t]);
     }
-  int e;
-  frexpf(sc, &e);  // sc = 2^(e - 1)
-  const float inv = ldexpf(1.0f, 1 - e);  // 1 / sc, exactly
+  const float inv = inv_pow2(sc);
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) res[t][r] = res[t][r] + acc[t][r] * inv;
 }
 
-// zero the deltas of inactive ReLUs (mask from the forward activations)
-template <int NT>
-__device__ __forceinline__ void relu_mask16(floatx4 (&d)[NT], const half4 (&act)[NT]) {
+// backward layer over a 16-wide output (K = 16): natural column order
+template <int RT>
+__device__ __forceinline__ void bwd_k16(const _Float16* __restrict__ Wt, int P, const half4& op, float sc,
+                                        floatx4 (&res)[RT], int g, int s) {
+  const float inv = inv_pow2(sc);
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < RT; ++t) {
+    const half4 w = *reinterpret_cast<const half4*>(Wt + (16 * t + s) * P + 4 * g);
+    const floatx4 acc = mfma_k16(w, op, floatx4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-    for (int r = 0; r < 4; ++r) d[t][r] = (float)act[t][r] > 0.0f ? d[t][r] : 0.0f;
+    for (int r = 0; r < 4; ++r) res[t][r] = res[t][r] + acc[r] * inv;
+  }
 }
 
-// the next layer's operands: scale and fp16 deltas
-template <int NT>
-__device__ __forceinline__ float make_op(const floatx4 (&d)[NT], half4 (&op)[NT]) {
-  const float sc = delta_scale<NT>(d);
-  scaled_half<NT>(d, sc, op);
+// zero the deltas of inactive ReLUs (act: the forward's fp16 activations, two tiles per K block)
+__device__ __forceinline__ void relu_mask(floatx4 (&d)[4], const half8 (&act)[2]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d[t][r] = act[t >> 1][4 * (t & 1) + r] > (_Float16)0.0f ? d[t][r] : 0.0f;
+}
+
+// the next layer's operands from four delta tiles: scale and fp16 K blocks
+__device__ __forceinline__ float make_op4(const floatx4 (&d)[4], half8 (&op)[2]) {
+  const float sc = delta_scale<4>(d);
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      op[kb][r] = (_Float16)(d[2 * kb][r] * sc);
+      op[kb][4 + r] = (_Float16)(d[2 * kb + 1][r] * sc);
+    }
+  return sc;
+}
+__device__ __forceinline__ float make_op1(const floatx4 (&d)[1], half4& op) {
+  const float sc = delta_scale<1>(d);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) op[r] = (_Float16)(d[0][r] * sc);
   return sc;
 }
 
-// write NT D-layout tiles of this wavefront's samples into stash rows row0 + 16t + 4g + r, column 16w + s
-template <int NT, typename V>
-__device__ __forceinline__ void stash_tiles(__bf16* __restrict__ st, int row0, const V (&v)[NT], int g, int col) {
-  constexpr int PS = 64 + 4;
+// stash rows row0 + 16 t + 4 g + r, column `col`, of NT D-layout tiles (value(t, r))
+template <int NT, typename F>
+__device__ __forceinline__ void stash_rows(__bf16* __restrict__ st, int row0, int g, int col, F value) {
+  constexpr int PS = 64 + 8;
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) st[(row0 + 16 * t + 4 * g + r) * PS + col] = (__bf16)(float)v[t][r];
+    for (int r = 0; r < 4; ++r) st[(row0 + 16 * t + 4 * g + r) * PS + col] = (__bf16)value(t, r);
 }
 
 // Weight-gradient tiles of one layer held by one wavefront: tiles i = T * IT + Tp dealt round-robin,
@@ -218,23 +298,26 @@ struct WaveGrad16 {
   }
 };
 
-// this wavefront's dW tiles over the 64 stashed samples (delta rows [0, 16 OT), activation rows after)
+// this wavefront's dW tiles over the 64 stashed samples (delta rows [0, 16 OT), activation rows after): two
+// K = 32 blocks of samples, lane group g reading samples 32 q + 8 g .. + 7 of both operands
 template <int OT, int IT, int PS>
-__device__ __forceinline__ void layer_dw16(const __bf16* __restrict__ st, WaveGrad16<OT, IT>& acc, int wave, int g,
-                                           int s) {
+__device__ __forceinline__ void layer_dw(const __bf16* __restrict__ st, WaveGrad16<OT, IT>& acc, int wave, int g,
+                                         int s) {
 #pragma unroll
   for (int m = 0; m < WaveGrad16<OT, IT>::N; ++m) {
     const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
-    const __bf16* drow = st + (16 * T + s) * PS + 4 * g;
-    const __bf16* arow = st + (16 * (OT + Tp) + s) * PS + 4 * g;
+    const __bf16* drow = st + (16 * T + s) * PS + 8 * g;
+    const __bf16* arow = st + (16 * (OT + Tp) + s) * PS + 8 * g;
     floatx4 c = acc.w[m];
     float bs = acc.b[m];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const bf16x4 dv = *reinterpret_cast<const bf16x4*>(drow + 16 * q);
-      const bf16x4 av = *reinterpret_cast<const bf16x4*>(arow + 16 * q);
-      c = mfma_bf16(dv, av, c);
-      if (Tp == 0) bs += ((float)dv[0] + (float)dv[1]) + ((float)dv[2] + (float)dv[3]);
+    for (int q = 0; q < 2; ++q) {
+      const bf16x8 dv = *reinterpret_cast<const bf16x8*>(drow + 32 * q);
+      const bf16x8 av = *reinterpret_cast<const bf16x8*>(arow + 32 * q);
+      c = mfma_k32b(dv, av, c);
+      if (Tp == 0)
+        bs += (((float)dv[0] + (float)dv[1]) + ((float)dv[2] + (float)dv[3])) +
+              (((float)dv[4] + (float)dv[5]) + ((float)dv[6] + (float)dv[7]));
     }
     acc.w[m] = c;
     acc.b[m] = bs;
@@ -263,10 +346,141 @@ __device__ __forceinline__ void flush_layer16(float* __restrict__ dst, int O, in
   }
 }
 
+// this lane's encoding values: a0v[4 kb + j] = neuron 16 kb + 4 g + j of sample b (0 when !valid)
+template <int LF, int FEAT>
+__device__ __forceinline__ void load_a0(const MlpArgs& a, int64_t b, bool valid, int g, float (&a0v)[LF / 4]) {
+  if (!valid) {
+#pragma unroll
+    for (int q = 0; q < LF / 4; ++q) a0v[q] = 0.0f;
+    return;
+  }
+#pragma unroll
+  for (int kb = 0; kb < LF / 16; ++kb) {
+    if constexpr (FEAT == 4) {
+      const int l = 4 * kb + g;
+      const float4 v = *reinterpret_cast<const float4*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
+      a0v[4 * kb] = v.x;
+      a0v[4 * kb + 1] = v.y;
+      a0v[4 * kb + 2] = v.z;
+      a0v[4 * kb + 3] = v.w;
+    } else if constexpr (FEAT == 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int l = 8 * kb + 2 * g + h;
+        const float2 v = *reinterpret_cast<const float2*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
+        a0v[4 * kb + 2 * h] = v.x;
+        a0v[4 * kb + 2 * h + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a0v[4 * kb + j] = a.a0[(16 * kb + 4 * g + j) * a.feat.stride_l + b * a.feat.stride_b];
+    }
+  }
+}
+
+// The network's forward for this wavefront's 16 samples: a0 (fp16 K blocks, or one K = 16 operand when
+// LF = 16) through the density net, [dout | SH] through the colour net.  Activations in fp16 K blocks
+// (hd, hc), the colour net's input as K block cin; rgb and the density head's first output for the lane.
+template <int LF, int ND, int NC>
+struct Fwd16 {
+  static constexpr int KA = LF >= 32 ? LF / 32 : 1;  // K blocks of the encoding
+  half8 a0k[KA];                                     // LF >= 32
+  half4 a0q;                                         // LF == 16
+  half8 hd[ND][2];
+  half8 cin;
+  half8 hc[NC][2];
+  float rgb[3];
+  float dout0;
+};
+
+template <int LF, int ND, int NC, typename A>
+__device__ __forceinline__ void forward16(const _Float16* __restrict__ sWf, const float* __restrict__ sB,
+                                          const float (&a0v)[LF / 4], const floatx4& sh, int g, int s,
+                                          Fwd16<LF, ND, NC>& f) {
+  floatx4 o[4];
+  if constexpr (LF >= 32) {
+#pragma unroll
+    for (int kb = 0; kb < LF / 32; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f.a0k[kb][j] = (_Float16)a0v[8 * kb + j];          // neuron 32 kb + 4 g + j
+        f.a0k[kb][4 + j] = (_Float16)a0v[8 * kb + 4 + j];  // neuron 32 kb + 16 + 4 g + j
+      }
+    fwd_k32<4, LF / 32>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), f.a0k, o, g, s, true);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.a0q[j] = (_Float16)a0v[j];
+    fwd_k16<4>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), f.a0q, o, g, s, true);
+  }
+  f.hd[0][0] = to_half8(o[0], o[1]);
+  f.hd[0][1] = to_half8(o[2], o[3]);
+#pragma unroll
+  for (int i = 1; i < ND; ++i) {
+    const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
+    fwd_k32<4, 2>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), f.hd[i - 1], o, g, s, true);
+    f.hd[i][0] = to_half8(o[0], o[1]);
+    f.hd[i][1] = to_half8(o[2], o[3]);
+  }
+  floatx4 dout[1];
+  fwd_k32<1, 2>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), f.hd[ND - 1], dout, g, s,
+                false);
+  f.cin = to_half8(dout[0], sh);
+  {
+    const half8 cin[1] = {f.cin};
+    fwd_k32<4, 1>(sWf + A::wf_off(FFN_WC_IN), A::pf(FFN_WC_IN), sB + A::b_off(FFN_WC_IN), cin, o, g, s, true);
+  }
+  f.hc[0][0] = to_half8(o[0], o[1]);
+  f.hc[0][1] = to_half8(o[2], o[3]);
+#pragma unroll
+  for (int i = 1; i < NC; ++i) {
+    const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
+    fwd_k32<4, 2>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), f.hc[i - 1], o, g, s, true);
+    f.hc[i][0] = to_half8(o[0], o[1]);
+    f.hc[i][1] = to_half8(o[2], o[3]);
+  }
+  floatx4 co[1];
+  fwd_k32<1, 2>(sWf + A::wf_off(FFN_WC_OUT), A::pf(FFN_WC_OUT), sB + A::b_off(FFN_WC_OUT), f.hc[NC - 1], co, g, s,
+                false);
+  f.rgb[0] = sigmoid_soft(co[0][0]);
+  f.rgb[1] = sigmoid_soft(co[0][1]);
+  f.rgb[2] = sigmoid_soft(co[0][2]);
+  f.dout0 = dout[0][0];
+}
+
+// ReLU taps from fp16 K blocks (two tiles each)
+__device__ __forceinline__ void tap_relu8(uint32_t* rec, int h, const half8 (&act)[2], int g) {
+  half4 t4[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) t4[t] = half4{act[t >> 1][4 * (t & 1)], act[t >> 1][4 * (t & 1) + 1],
+                                            act[t >> 1][4 * (t & 1) + 2], act[t >> 1][4 * (t & 1) + 3]};
+  tap_relu(rec, h, t4, g);
+}
+
+// what a wavefront reads from HBM for its 16 samples of a tile; loaded one tile ahead of its use
+template <int LF>
+struct TileIn {
+  float a0v[LF / 4];
+  float4 rd;  // the ray direction
+  float dt, t;
+};
+template <int LF, int FEAT>
+__device__ __forceinline__ void load_tile_in(const MlpArgs& a, int64_t b, bool valid, int g, int log2S,
+                                             TileIn<LF>& in) {
+  load_a0<LF, FEAT>(a, b, valid, g, in.a0v);
+  in.rd = a.rays[2 * (valid ? (b >> log2S) : 0) + 1];
+  in.dt = valid ? a.DTs[b] : 0.0f;
+  in.t = valid ? a.Ts[b] : 0.0f;
+}
+// the first busy tile of the group at or after tt (4 if none)
+__device__ __forceinline__ int next_busy(const int* flags, int tt) {
+  while (tt < 4 && !flags[tt]) ++tt;
+  return tt;
+}
+
 template <int LF, int ND, int NC, int FEAT, bool TAPS>
 __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_mlp16(MlpArgs a) {
   using A = Arch16<LF, ND, NC>;
-  constexpr int KB0 = LF / 16;  // k-blocks of the first layer
+  constexpr int KB0 = LF / 16;  // D-layout tiles of the encoding
   extern __shared__ __align__(16) unsigned char smem16[];
   _Float16* sWf = reinterpret_cast<_Float16*>(smem16);
   _Float16* sWt = sWf;  // the transposed copies follow the forward weights (offsets in 16-bit units)
@@ -274,25 +488,31 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   __bf16* sS = reinterpret_cast<__bf16*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4);
   float* sC = reinterpret_cast<float*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4 +
                                        (size_t)A::stash_halves() * 2);
+  int* sFlag = reinterpret_cast<int*>(sC + 4 * 256);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+  const int col = wave * 16 + s;  // this lane's sample column in a tile
   const bool train = a.do_train != 0;
   const DevCfg& c = a.c;
   const int log2S = a.log2S;
   const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
 
-  // weights: fp16 [out_pad][in] and bf16 [in][out_pad] (zero padding), fp32 biases
+  // weights: fp16 [out_pad][in] and [in][out_pad] (K-ordered columns where K blocks are 32 wide, zero
+  // padding), fp32 biases
 #pragma unroll
   for (int k = 0; k < FFN_N_LAYERS; ++k) {
     if (!layer_active(k, ND, NC)) continue;
     const int O = layer_out(k), I = layer_in(k, LF), R = A::rows_pad(k);
     const int PF = A::pf(k), PT = A::pt(k);
+    const bool kf = I % 32 == 0, kt = R % 32 == 0;
     const float* gw = a.w.W[k];
     for (int e = tid; e < R * PF; e += 256) {
-      const int r = e / PF, col = e - r * PF;
-      sWf[A::wf_off(k) + e] = (_Float16)((r < O && col < I) ? gw[r * I + col] : 0.0f);
+      const int r = e / PF, p = e - r * PF;
+      const int i = p < I ? (kf ? kpos_neuron(p) : p) : I;
+      sWf[A::wf_off(k) + e] = (_Float16)((r < O && i < I) ? gw[r * I + i] : 0.0f);
     }
     for (int e = tid; e < I * PT; e += 256) {
-      const int i = e / PT, o = e - i * PT;
+      const int i = e / PT, p = e - i * PT;
+      const int o = p < R ? (kt ? kpos_neuron(p) : p) : R;
       sWt[A::wt_off(k) + e] = (_Float16)((o < O) ? gw[o * I + i] : 0.0f);
     }
     for (int e = tid; e < R; e += 256) sB[A::b_off(k) + e] = e < O ? a.w.b[k][e] : 0.0f;
@@ -300,7 +520,6 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   __syncthreads();
 
   const float Dhalf = half_box_diagonal(c);
-  constexpr bool taps = TAPS;
   const bool proposals = train && a.occ_strength > 0.0f;
   constexpr int PS = A::PS;
   WaveGrad16<1, 4> gc_out;
@@ -318,260 +537,222 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   for (int i = 0; i < (ND > 1 ? ND - 1 : 1); ++i) gd_h[i].zero();
   gd_in.zero();
 
-  int parity = 0;
-  for (int64_t tile = blockIdx.x; tile < a.n_tiles; tile += gridDim.x, parity ^= 1) {
-    float* sSig = sC + parity * 256;
-    float* sRgb = sSig + 64;
-    const int64_t b = tile * 64 + wave * 16 + s;
-    const bool valid = (uint64_t)b < n_samples;
-    const int64_t ray = valid ? (b >> log2S) : 0;
-    // a0v[4 kb + j] = encoding neuron 16 kb + 4 g + j of sample b
-    float a0v[LF / 4];
-    if (valid) {
-#pragma unroll
-      for (int kb = 0; kb < KB0; ++kb) {
-        if constexpr (FEAT == 4) {
-          const int l = 4 * kb + g;
-          const float4 v = *reinterpret_cast<const float4*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
-          a0v[4 * kb] = v.x;
-          a0v[4 * kb + 1] = v.y;
-          a0v[4 * kb + 2] = v.z;
-          a0v[4 * kb + 3] = v.w;
-        } else if constexpr (FEAT == 2) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int l = 8 * kb + 2 * g + h;
-            const float2 v = *reinterpret_cast<const float2*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
-            a0v[4 * kb + 2 * h] = v.x;
-            a0v[4 * kb + 2 * h + 1] = v.y;
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) a0v[4 * kb + j] = a.a0[(16 * kb + 4 * g + j) * a.feat.stride_l + b * a.feat.stride_b];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < LF / 4; ++q) a0v[q] = 0.0f;
-    }
-    float dirv[3];
-    {
-      const float4 rd = a.rays[2 * ray + 1];
-      dirv[0] = rd.x;
-      dirv[1] = rd.y;
-      dirv[2] = rd.z;
-    }
-    const float dt_b = valid ? a.DTs[b] : 0.0f;
-    const float t_b = valid ? a.Ts[b] : 0.0f;
-    const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront makes the tile's proposals
-    const CompLane CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
-    if (!taps && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
-      empty_tile<LF, FEAT>(a, CL, lane, wave, b, valid, train, g);
-      continue;
-    }
+  const int64_t n_groups = (a.n_tiles + 3) / 4;
+  for (int64_t grp = blockIdx.x; grp < n_groups; grp += gridDim.x) {
+    const int64_t tile0 = grp * 4;
+    // (0) the compositing inputs of tile tile0 + wave (past the last tile: no valid lane)
+    const CompLane CL = load_comp_lane(a, tile0 + wave, lane, true, n_samples, log2S, proposals);
+    const bool busy = TAPS ? __ballot(CL.vj) != 0ull : __ballot(CL.vj && CL.dt_j > 0.0f) != 0ull;
+    __syncthreads();  // the previous group is done with sC and the flags
+    if (lane == 0) sFlag[wave] = busy ? 1 : 0;
+    __syncthreads();
 
-    // ---- forward (fp16 operands, fp32 accumulation)
-    half4 a0h[KB0];
-#pragma unroll
-    for (int kb = 0; kb < KB0; ++kb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a0h[kb][j] = (_Float16)a0v[4 * kb + j];
-    bf16x4 a0b[KB0];  // the encoding as the stash holds it (bf16), kept for the first layer's gradient
-#pragma unroll
-    for (int kb = 0; kb < KB0; ++kb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a0b[kb][j] = (__bf16)a0v[4 * kb + j];
-    floatx4 sh;  // this lane's four SH inputs of the colour net
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
-    // the network's activations: computed for the colours, dropped across the compositing (held there,
-    // they spilled to scratch), and computed again, bit-identically, for the backward
-    auto forward = [&](half4(&hdh)[ND][4], half4(&acinh)[2], bf16x4(&acb)[2], half4(&hch)[NC][4], float(&rgb_s)[3],
-                       float& dout0) {
-      {
-        floatx4 o[4];
-        fwd16<4, KB0>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), a0h, o, g, s, true);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) hdh[0][t] = to_half4(o[t]);
+    // (A) forward of this wavefront's samples of every busy tile: sigma and rgb into sC; each tile's inputs
+    // are loaded while the previous tile's forward runs
+    TileIn<LF> cur;
+    int tt = next_busy(sFlag, 0);
+    if (tt < 4) {
+      const int64_t b = (tile0 + tt) * 64 + col;
+      load_tile_in<LF, FEAT>(a, b, (uint64_t)b < n_samples, g, log2S, cur);
+    }
+#pragma unroll 1
+    while (tt < 4) {
+      const int64_t b = (tile0 + tt) * 64 + col;
+      const bool valid = (uint64_t)b < n_samples;
+      const int tn = next_busy(sFlag, tt + 1);
+      TileIn<LF> nxt;
+      if (tn < 4) {
+        const int64_t bn = (tile0 + tn) * 64 + col;
+        load_tile_in<LF, FEAT>(a, bn, (uint64_t)bn < n_samples, g, log2S, nxt);
       }
-      if constexpr (ND >= 2) {
-        floatx4 o[4];
-        fwd16<4, 4>(sWf + A::wf_off(FFN_WD_01), A::pf(FFN_WD_01), sB + A::b_off(FFN_WD_01), hdh[0], o, g, s, true);
+      const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
+      floatx4 sh;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) hdh[1][t] = to_half4(o[t]);
-      }
-      if constexpr (ND >= 3) {
-        floatx4 o[4];
-        fwd16<4, 4>(sWf + A::wf_off(FFN_WD_12), A::pf(FFN_WD_12), sB + A::b_off(FFN_WD_12), hdh[1], o, g, s, true);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) hdh[2][t] = to_half4(o[t]);
-      }
-      floatx4 dout[1];
-      fwd16<1, 4>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), hdh[ND - 1], dout, g, s,
-                  false);
-      acinh[0] = to_half4(dout[0]);
-      acinh[1] = to_half4(sh);
-      acb[0] = to_bf16x4(dout[0]);  // colour-net input, for its gradient
-      acb[1] = to_bf16x4(sh);
-      {
-        floatx4 o[4];
-        fwd16<4, 2>(sWf + A::wf_off(FFN_WC_IN), A::pf(FFN_WC_IN), sB + A::b_off(FFN_WC_IN), acinh, o, g, s, true);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) hch[0][t] = to_half4(o[t]);
-      }
-#pragma unroll
-      for (int i = 1; i < NC; ++i) {
-        const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
-        floatx4 o[4];
-        fwd16<4, 4>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), hch[i - 1], o, g, s, true);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) hch[i][t] = to_half4(o[t]);
-      }
-      {
-        floatx4 co[1];
-        fwd16<1, 4>(sWf + A::wf_off(FFN_WC_OUT), A::pf(FFN_WC_OUT), sB + A::b_off(FFN_WC_OUT), hch[NC - 1], co, g, s,
-                    false);
-        rgb_s[0] = sigmoid_soft(co[0][0]);
-        rgb_s[1] = sigmoid_soft(co[0][1]);
-        rgb_s[2] = sigmoid_soft(co[0][2]);
-      }
-      dout0 = dout[0][0];
-    };
-    float rgb_s[3], dout0;
-    {
-      half4 hdh[ND][4], acinh[2], hch[NC][4];
-      bf16x4 acb[2];
-      forward(hdh, acinh, acb, hch, rgb_s, dout0);
+      for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
+      Fwd16<LF, ND, NC> f;
+      forward16<LF, ND, NC, A>(sWf, sB, cur.a0v, sh, g, s, f);
       if constexpr (TAPS) {
         if (a.t_relu) {
           uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
 #pragma unroll
-          for (int i = 0; i < ND; ++i) tap_relu(rec, i, hdh[i], g);
+          for (int i = 0; i < ND; ++i) tap_relu8(rec, i, f.hd[i], g);
 #pragma unroll
-          for (int i = 0; i < NC; ++i) tap_relu(rec, 3 + i, hch[i], g);
+          for (int i = 0; i < NC; ++i) tap_relu8(rec, 3 + i, f.hc[i], g);
         }
       }
-    }
-    if (g == 0) {
-      float sig = softplus(fminf(fmaxf(dout0, -10.0f), 10.0f));
-      if (dt_b <= 0.0f) sig = 0.0f;
-      sSig[wave * 16 + s] = sig;
-      sRgb[(wave * 16 + s) * 3 + 0] = rgb_s[0];
-      sRgb[(wave * 16 + s) * 3 + 1] = rgb_s[1];
-      sRgb[(wave * 16 + s) * 3 + 2] = rgb_s[2];
+      if (g == 0) {
+        float sig = softplus(fminf(fmaxf(f.dout0, -10.0f), 10.0f));
+        if (cur.dt <= 0.0f) sig = 0.0f;
+        float* sSig = sC + tt * 256;
+        sSig[col] = sig;
+        sSig[64 + col * 3 + 0] = f.rgb[0];
+        sSig[64 + col * 3 + 1] = f.rgb[1];
+        sSig[64 + col * 3 + 2] = f.rgb[2];
+      }
+      cur = nxt;
+      tt = tn;
     }
     __syncthreads();
 
-    float dLds_j, dLdc_j[3];
-    composite_tile<TAPS>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+    // (B) this wavefront composites tile tile0 + wave (all its 64 samples, proposals included); lane j's
+    // loss gradients replace its sigma and rgb
+    {
+      float* sSig = sC + wave * 256;
+      if (busy) {
+        float dLds_j, dLdc_j[3];
+        composite_tile<TAPS>(a, sSig, sSig + 64, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
+        sSig[lane] = dLds_j;
+        sSig[64 + 3 * lane] = dLdc_j[0];
+        sSig[64 + 3 * lane + 1] = dLdc_j[1];
+        sSig[64 + 3 * lane + 2] = dLdc_j[2];
+      } else if ((lane & (a.S - 1)) == 0 && CL.vj) {
+        // every alpha is 0: T = 1 and the colour is the background
+        float bg[3];
+        background(a, CL.rj, train, bg);
+        a.out_rgb[CL.rj] = make_float4(fminf(fmaxf(bg[0], 0.0f), 1.0f), fminf(fmaxf(bg[1], 0.0f), 1.0f),
+                                       fminf(fmaxf(bg[2], 0.0f), 1.0f), train ? 4.0f : 0.0f);
+      }
+    }
     if (!train) continue;
-    half4 hdh[ND][4], acinh[2], hch[NC][4];
-    bf16x4 acb[2];
-    {
-      float rgb_r[3], dout_r;
-      forward(hdh, acinh, acb, hch, rgb_r, dout_r);
-    }
+    __syncthreads();
 
-    // ---- backward (fp16 chain with per-wavefront delta scaling, fp32 accumulation); every layer's deltas
-    // and inputs go through the stash for the block's bf16 weight-gradient tiles (barrier, this wave's
-    // tiles, barrier before the stash is reused)
-    const int col = wave * 16 + s;
-    const float dLds = __shfl(dLds_j, col);
-    const float dLdc0 = __shfl(dLdc_j[0], col), dLdc1 = __shfl(dLdc_j[1], col), dLdc2 = __shfl(dLdc_j[2], col);
-    floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
-    floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
-    if (g == 0 && valid) {
-      float d3[3], dd0;
-      output_deltas(t_b, dt_b, Dhalf, dLds, dLdc0, dLdc1, dLdc2, rgb_s, dout0, d3, dd0);
-      dco[0][0] = d3[0];
-      dco[0][1] = d3[1];
-      dco[0][2] = d3[2];
-      ddo[0][0] = dd0;
+    // (C) per busy tile: the forward again, then the backward (fp16 chain with per-wavefront delta scaling,
+    // fp32 accumulation); every layer's deltas and inputs go through the stash for the block's bf16
+    // weight-gradient tiles (barrier, this wave's tiles, barrier before the stash is reused).  First the
+    // zero encoding gradients of the idle tiles' samples.
+#pragma unroll 1
+    for (int ti = 0; ti < 4; ++ti) {
+      const int64_t b = (tile0 + ti) * 64 + col;
+      if (sFlag[ti] || (uint64_t)b >= n_samples) continue;
+      floatx4 z[KB0];
+#pragma unroll
+      for (int t = 0; t < KB0; ++t) z[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      store_enc_grad<LF, FEAT>(a, b, g, z);
     }
-    // colour output layer
-    half4 dop[4];
-    float dsc;
-    floatx4 dc[4];
-    stash_tiles<1>(sS, 0, dco, g, col);
-    stash_tiles<4>(sS, 16, hch[NC - 1], g, col);
-    {
-      half4 cop[1];
-      const float csc = make_op<1>(dco, cop);
+    // (the inputs load at the start of each tile: loaded a tile ahead, they stayed live through the backward
+    // and cost more in spills than the latency they hid)
+    tt = next_busy(sFlag, 0);
+#pragma unroll 1
+    while (tt < 4) {
+      const int64_t b = (tile0 + tt) * 64 + col;
+      const bool valid = (uint64_t)b < n_samples;
+      const int tn = next_busy(sFlag, tt + 1);
+      load_tile_in<LF, FEAT>(a, b, valid, g, log2S, cur);
+      const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
+      floatx4 sh;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd16<4, 1>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
-      relu_mask16<4>(dc, hch[NC - 1]);
-      dsc = make_op<4>(dc, dop);
-    }
-    __syncthreads();
-    layer_dw16<1, 4, PS>(sS, gc_out, wave, g, s);
-    __syncthreads();
-    // hidden colour layers (Wc_23, Wc_12, Wc_01): delta dc of layer i's output, input hch[i - 1]
+      for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
+      const float dt_b = cur.dt, t_b = cur.t;
+      float a0v[LF / 4];
 #pragma unroll
-    for (int i = NC - 1; i >= 1; --i) {
-      const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
-      stash_tiles<4>(sS, 0, dc, g, col);
-      stash_tiles<4>(sS, 64, hch[i - 1], g, col);
+      for (int q = 0; q < LF / 4; ++q) a0v[q] = cur.a0v[q];
+      Fwd16<LF, ND, NC> f;
+      forward16<LF, ND, NC, A>(sWf, sB, a0v, sh, g, s, f);
+      bf16x4 a0b[KB0];  // the encoding as the stash holds it (bf16 of the fp32 values)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd16<4, 4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
-      relu_mask16<4>(dc, hch[i - 1]);
-      dsc = make_op<4>(dc, dop);
+      for (int t = 0; t < KB0; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a0b[t][r] = (__bf16)a0v[4 * t + r];
+      const float* sD = sC + tt * 256;
+      const float dLds = sD[col], dLdc0 = sD[64 + 3 * col], dLdc1 = sD[64 + 3 * col + 1],
+                  dLdc2 = sD[64 + 3 * col + 2];
+      floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
+      floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
+      if (g == 0 && valid) {
+        float d3[3], dd0;
+        output_deltas(t_b, dt_b, Dhalf, dLds, dLdc0, dLdc1, dLdc2, f.rgb, f.dout0, d3, dd0);
+        dco[0][0] = d3[0];
+        dco[0][1] = d3[1];
+        dco[0][2] = d3[2];
+        ddo[0][0] = dd0;
+      }
+      __syncthreads();  // the previous tile's last gradient tiles have read the stash
+      // colour output layer
+      half8 dop[2];
+      float dsc;
+      floatx4 dc[4];
+      stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return dco[t][r]; });
+      stash_rows<4>(sS, 16, g, col, [&](int t, int r) { return (float)f.hc[NC - 1][t >> 1][4 * (t & 1) + r]; });
+      {
+        half4 cop;
+        const float csc = make_op1(dco, cop);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        bwd_k16<4>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
+        relu_mask(dc, f.hc[NC - 1]);
+        dsc = make_op4(dc, dop);
+      }
       __syncthreads();
-      layer_dw16<4, 4, PS>(sS, gc_h[i - 1], wave, g, s);
+      layer_dw<1, 4, PS>(sS, gc_out, wave, g, s);
       __syncthreads();
-    }
-    // colour input layer: its gradient, and the dout part of its input delta joins the density head's delta
-    stash_tiles<4>(sS, 0, dc, g, col);
-    stash_tiles<2>(sS, 64, acb, g, col);
-    bwd16<1, 4>(sWt + A::wt_off(FFN_WC_IN), A::pt(FFN_WC_IN), dop, dsc, ddo, g, s);
-    __syncthreads();
-    layer_dw16<4, 2, PS>(sS, gc_in, wave, g, s);
-    __syncthreads();
-    // density output layer
-    floatx4 dd[4];
-    stash_tiles<1>(sS, 0, ddo, g, col);
-    stash_tiles<4>(sS, 16, hdh[ND - 1], g, col);
-    {
-      half4 dd_op[1];
-      const float ssc = make_op<1>(ddo, dd_op);
+      // hidden colour layers (Wc_23, Wc_12, Wc_01): delta dc of layer i's output, input hc[i - 1]
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd16<4, 1>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
-      relu_mask16<4>(dd, hdh[ND - 1]);
-      dsc = make_op<4>(dd, dop);
-    }
-    __syncthreads();
-    layer_dw16<1, 4, PS>(sS, gd_out, wave, g, s);
-    __syncthreads();
-    // hidden density layers (Wd_12, Wd_01)
+      for (int i = NC - 1; i >= 1; --i) {
+        const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
+        stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dc[t][r]; });
+        stash_rows<4>(sS, 64, g, col, [&](int t, int r) { return (float)f.hc[i - 1][t >> 1][4 * (t & 1) + r]; });
 #pragma unroll
-    for (int i = ND - 1; i >= 1; --i) {
-      const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
-      stash_tiles<4>(sS, 0, dd, g, col);
-      stash_tiles<4>(sS, 64, hdh[i - 1], g, col);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd16<4, 4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
-      relu_mask16<4>(dd, hdh[i - 1]);
-      dsc = make_op<4>(dd, dop);
+        for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        bwd_k32<4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
+        relu_mask(dc, f.hc[i - 1]);
+        dsc = make_op4(dc, dop);
+        __syncthreads();
+        layer_dw<4, 4, PS>(sS, gc_h[i - 1], wave, g, s);
+        __syncthreads();
+      }
+      // colour input layer: its gradient, and the dout part of its input delta joins the density head's delta
+      stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dc[t][r]; });
+      stash_rows<2>(sS, 64, g, col, [&](int t, int r) { return (float)f.cin[4 * t + r]; });
+      bwd_k32<1>(sWt + A::wt_off(FFN_WC_IN), A::pt(FFN_WC_IN), dop, dsc, ddo, g, s);
       __syncthreads();
-      layer_dw16<4, 4, PS>(sS, gd_h[i - 1], wave, g, s);
+      layer_dw<4, 2, PS>(sS, gc_in, wave, g, s);
       __syncthreads();
-    }
-    // density input layer: deltas and the encoding; encoding gradient dL/da0 = Wd_in^T . delta -> HBM
-    stash_tiles<4>(sS, 0, dd, g, col);
-    stash_tiles<KB0>(sS, 64, a0b, g, col);
-    {
-      floatx4 ga0[KB0];
+      // density output layer
+      floatx4 dd[4];
+      stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return ddo[t][r]; });
+      stash_rows<4>(sS, 16, g, col, [&](int t, int r) { return (float)f.hd[ND - 1][t >> 1][4 * (t & 1) + r]; });
+      {
+        half4 dd_op;
+        const float ssc = make_op1(ddo, dd_op);
 #pragma unroll
-      for (int t = 0; t < KB0; ++t) ga0[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bwd16<KB0, 4>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
-      if (valid) store_enc_grad<LF, FEAT>(a, b, g, ga0);
+        for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        bwd_k16<4>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
+        relu_mask(dd, f.hd[ND - 1]);
+        dsc = make_op4(dd, dop);
+      }
+      __syncthreads();
+      layer_dw<1, 4, PS>(sS, gd_out, wave, g, s);
+      __syncthreads();
+      // hidden density layers (Wd_12, Wd_01)
+#pragma unroll
+      for (int i = ND - 1; i >= 1; --i) {
+        const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
+        stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
+        stash_rows<4>(sS, 64, g, col, [&](int t, int r) { return (float)f.hd[i - 1][t >> 1][4 * (t & 1) + r]; });
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        bwd_k32<4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
+        relu_mask(dd, f.hd[i - 1]);
+        dsc = make_op4(dd, dop);
+        __syncthreads();
+        layer_dw<4, 4, PS>(sS, gd_h[i - 1], wave, g, s);
+        __syncthreads();
+      }
+      // density input layer: deltas and the encoding (bf16 of the fp32 values); dL/da0 = Wd_in^T . delta
+      stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
+      stash_rows<KB0>(sS, 64, g, col, [&](int t, int r) { return (float)a0b[t][r]; });
+      {
+        floatx4 ga0[KB0];
+#pragma unroll
+        for (int t = 0; t < KB0; ++t) ga0[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        bwd_k32<KB0>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
+        if (valid) store_enc_grad<LF, FEAT>(a, b, g, ga0);
+      }
+      __syncthreads();
+      layer_dw<4, KB0, PS>(sS, gd_in, wave, g, s);
+      // no barrier: the stash is next written after the next tile's barrier
+      tt = tn;
     }
-    __syncthreads();
-    layer_dw16<4, KB0, PS>(sS, gd_in, wave, g, s);
-    // no barrier: the stash is next written after the next tile's compositing barrier
   }
 
   if (train) {
