@@ -509,13 +509,6 @@ def main():
     import ffnerf_tools as ft
     import synthetic_scene as sc
 
-    if args.workload == "cfg3":
-        run_cfg3(args)
-        return
-    if args.workload == "cfg4":
-        run_cfg4(args)
-        return
-
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -526,6 +519,13 @@ def main():
         print(f"[bench] calibration copy: {args.copy_calibration_mib} MiB read + {args.copy_calibration_mib} MiB "
               f"written by one copy kernel", flush=True)
         del src, dst
+
+    if args.workload == "cfg3":
+        run_cfg3(args)
+        return
+    if args.workload == "cfg4":
+        run_cfg4(args)
+        return
 
     spec, occ, S = cfg2_spec(args.mlp)
     n_rays = int(args.rays)

@@ -229,3 +229,88 @@ def test_render_mode_changes_nothing(ora):
     assert np.all(out[:, 3] == 0.0)
     out_t, _ = model.train_step(rays, np.zeros((16, 4), np.float32), 64, default_scalars(do_train=1))
     assert np.all(out_t[:, 3] == 4.0)
+
+
+def _shell_bits(R, seed=0, frac=0.2):
+    rng = np.random.default_rng(seed)
+    c = (np.arange(R) + 0.5) / R
+    z, y, x = np.meshgrid(c, c, c, indexing="ij")
+    rad = np.sqrt((x - 0.5) ** 2 + (y - 0.5) ** 2 + (z - 0.5) ** 2)
+    occ = (np.abs(rad - 0.3) <= 0.08) | (rng.random((R, R, R)) < frac)
+    idx = np.nonzero(occ.reshape(-1))[0]
+    bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
+    np.bitwise_or.at(bits, idx >> 5, (np.uint32(1) << (idx & 31).astype(np.uint32)))
+    return bits
+
+
+@pytest.mark.parametrize("T_stop", [0.0, 1e-2])
+def test_marched_step_is_the_composition_of_pinned_parts(ora, T_stop):
+    """ora_train_step_marched is the march (ora_march_ray), the encoding at the marched positions
+    (ora_hash_encode), the reference MLP (torch float64), the marched compositing and its backward
+    (ora_composite_marched, pinned against autograd in test_oracle_march) and the reference backward from the
+    output deltas with dt = the march step and t = the sample time (autograd of the surrogate, as for the
+    resampled step), then the scatter of dL/da0 (ora_hash_backward)."""
+    spec = spec_cfg0(hash_opt=1, occ_G=16)
+    p = random_params(spec, seed=21)
+    p["bd_out"][0] = 8.0
+    model = ora.OracleModel(spec, {k: v.copy() for k, v in p.items()})
+    rays = look_at_rays(40, spec, seed=22, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    R = 32
+    bits = _shell_bits(R, seed=23)
+    dt = np.float32(np.sqrt(3.0) / 128)
+    m = ora.march_cfg(R, dt, 128, T_stop=T_stop)
+    sc = default_scalars(occ_strength=0.0)
+    out, used, taps = model.train_step_marched(rays, tg, bits, m, sc)
+    # the march and the encodings
+    ts = [ora.march_ray(model.cfg, m, bits, r) for r in rays]
+    counts = np.array([t.size for t in ts])
+    assert counts.sum() == taps["Ts"].size and counts.sum() > 500
+    np.testing.assert_array_equal(taps["Ts"], np.concatenate(ts))
+    x = np.concatenate([(r[None, :3] + t[:, None] * r[None, 4:7]).astype(np.float32) for r, t in zip(rays, ts)])
+    a0 = ora.hash_encode(model.cfg, p["table"], x)
+    np.testing.assert_array_equal(taps["a0"].view(np.uint32), a0.view(np.uint32))
+    # the MLP outputs
+    dirs = np.repeat(rays[:, 4:7], counts, axis=0)
+    t, xa, dout, cout = _torch_mlp(spec, p, a0, dirs, sc["sh_multiplier"])
+    sig_ref = np.log1p(np.exp(np.clip(dout[:, 0].detach().numpy(), -10, 10)))
+    rgb_ref = 1 / (1 + np.exp(-np.clip(0.5 * cout.detach().numpy(), -18, 18)))
+    assert np.allclose(taps["sigma"], sig_ref, rtol=1e-5, atol=1e-6)
+    assert np.allclose(taps["rgb"], rgb_ref, rtol=1e-5, atol=1e-6)
+    # per ray: compositing and its backward are ora_composite_marched on those outputs
+    regu = np.float32(5e-3) * dt / np.float32(128)
+    off = np.concatenate([[0], np.cumsum(counts)])
+    for r in range(rays.shape[0]):
+        sl = slice(off[r], off[r + 1])
+        u, Tr, dLds, dLdc, Cf, T_end = ora.composite_marched(taps["sigma"][sl], taps["rgb"][sl], dt, m.T_stop,
+                                                             np.zeros(3, np.float32), tg[r, :3], regu)
+        assert u == used[r]
+        np.testing.assert_array_equal(taps["dL_dsigma"][sl], dLds)
+        np.testing.assert_array_equal(taps["dL_dc"][sl], dLdc)
+        np.testing.assert_array_equal(out[r, :3], np.clip(Cf, 0, 1))
+        assert out[r, 3] == 4.0
+    if T_stop > 0:
+        assert (used < counts).sum() >= 3  # some rays stop early
+    else:
+        np.testing.assert_array_equal(used, counts)
+    # the backward from the output deltas (dt = the march step, t = the sample time)
+    Ts = taps["Ts"].astype(np.float64)
+    DT = float(dt)
+    D = 0.5 * np.sqrt(3.0)
+    num = Ts * Ts + Ts * DT + DT * DT / 3
+    den = D * D + D * DT + DT * DT / 3
+    xg = Ts / D
+    fvol = np.where(xg >= 1, 1.0, np.power(np.maximum(xg, 1e-12), 0.2)) * num / den
+    d_cout = fvol[:, None] * taps["dL_dc"] * rgb_ref * (1 - rgb_ref) * 0.5
+    z = np.clip(dout[:, 0].detach().numpy(), -18, 18)
+    d_dout0 = fvol * taps["dL_dsigma"] / (1 + np.exp(-z))
+    ((torch.tensor(d_cout) * cout).sum() + (torch.tensor(d_dout0) * dout[:, 0]).sum()).backward()
+    for wn in layer_shapes(spec):
+        bn = BIASES[LAYERS.index(wn)]
+        gw, gb = t[wn].grad.numpy(), t[bn].grad.numpy()
+        assert np.abs(taps["g" + wn] - gw).max() <= 2e-4 * (np.abs(gw).max() + 1e-30), wn
+        assert np.abs(taps["g" + bn] - gb).max() <= 2e-4 * (np.abs(gb).max() + 1e-30), bn
+    gx = xa.grad.numpy()
+    assert np.abs(taps["dL_da0"] - gx).max() <= 2e-4 * (np.abs(gx).max() + 1e-30)
+    g_scatter = ora.hash_backward(model.cfg, x, taps["dL_da0"], table_floats(spec))
+    assert np.allclose(taps["g_table"], g_scatter, rtol=1e-5, atol=1e-9 * np.abs(g_scatter).max())
