@@ -314,3 +314,47 @@ def test_marched_step_is_the_composition_of_pinned_parts(ora, T_stop):
     assert np.abs(taps["dL_da0"] - gx).max() <= 2e-4 * (np.abs(gx).max() + 1e-30)
     g_scatter = ora.hash_backward(model.cfg, x, taps["dL_da0"], table_floats(spec))
     assert np.allclose(taps["g_table"], g_scatter, rtol=1e-5, atol=1e-9 * np.abs(g_scatter).max())
+
+
+@pytest.mark.parametrize("hash_opt", [1, 0])
+def test_fp16_table_step_reduces_to_the_fp32_step(ora, hash_opt):
+    """A binary16 table holds values that float32 represents exactly, so the fp16-table step computes every
+    encoding, MLP output and gradient exactly as the fp32 step does on the same values; only the table's
+    update differs: Adam (fp32 moments) rounds the fp32 step's result to binary16 once, and the reference SGD
+    rounds the table plus the entry's summed update once (the fp32 step adds the contributions one by
+    one).  The binary16 rounding itself is pinned against numpy (test_binary16_rounding_matches_numpy)."""
+    spec32 = spec_cfg0(hash_opt=hash_opt)
+    spec16 = spec_cfg0(hash_opt=hash_opt, table_dtype="fp16")
+    p = random_params(spec32, seed=31)
+    p["table"] = p["table"].astype(np.float16).astype(np.float32)
+    rays = look_at_rays(24, spec32, seed=32, miss_frac=0.15)
+    tg = sphere_targets(rays, spec32)
+    sc = default_scalars(occ_strength=0.0)
+    m32 = ora.OracleModel(spec32, {k: v.copy() for k, v in p.items()})
+    m16 = ora.OracleModel(spec16, {k: v.copy() for k, v in p.items()})
+    out32, t32 = m32.train_step(rays, tg, 16, sc, taps=True)
+    out16, t16 = m16.train_step(rays, tg, 16, sc, taps=True)
+    np.testing.assert_array_equal(out32, out16)
+    for k in ("a0", "sigma", "rgb", "dL_dsigma", "dL_dc", "dL_da0"):
+        np.testing.assert_array_equal(t32[k], t16[k], err_msg=k)
+    for k in p:
+        if k in ("table", "m_table", "v_table"):
+            continue
+        np.testing.assert_array_equal(m32.p[k], m16.p[k], err_msg=k)
+    if hash_opt == 1:
+        np.testing.assert_array_equal(m16.p["m_table"], m32.p["m_table"])
+        np.testing.assert_array_equal(m16.p["v_table"], m32.p["v_table"])
+        np.testing.assert_array_equal(m16.p["table"], m32.p["table"].astype(np.float16).astype(np.float32))
+    else:
+        L, F = spec32["n_levels"], spec32["f_per_level"]
+        scale = np.array(ora.lvl_lr_scale(L), np.float32)
+        g = t32["dL_da0"].reshape(-1, L, F) * (-np.float32(sc["lr"]) * scale[None, :, None] * 0.5)
+        Ts = t32["Ts"].reshape(-1, 16)
+        x_s = (rays[:, None, :3] + Ts[..., None] * rays[:, None, 4:7]).reshape(-1, 3).astype(np.float32)
+        upd = ora.hash_backward(m32.cfg, x_s, g.reshape(-1, L * F).astype(np.float32), table_floats(spec32))
+        exp = (p["table"].astype(np.float64) + upd).astype(np.float32)
+        # float64 sum, one rounding to float32, then to binary16: within one binary16 ulp of the exact rounding
+        got, ref = m16.p["table"], exp.astype(np.float16).astype(np.float32)
+        ulp16 = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+        assert np.all(np.abs(got - ref) <= ulp16), np.abs(got - ref).max()
+        assert np.mean(got == ref) > 0.999
