@@ -120,12 +120,20 @@ __device__ __forceinline__ void bwd_tiles(const float* __restrict__ W, int P, co
       for (int t = 0; t < RT; ++t) res[t] = mfma4(W[(16 * tp + 4 * g + rp) * P + 16 * t + s], delta[tp][rp], res[t]);
 }
 
+// The activation passes through an empty asm first: otherwise the compiler proves act > 0 equal to the
+// forward ReLU's own comparison and keeps that lane mask (two SGPRs per value, 48 values) live from the
+// forward to the backward, which spilled SGPRs to VGPR lanes by the hundred per tile.  Here the test is
+// made where it is used, on the value the backward holds anyway.
 template <int NT>
 __device__ __forceinline__ void relu_mask(floatx4 (&d)[NT], const floatx4 (&act)[NT]) {
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) d[t][r] = act[t][r] > 0.0f ? d[t][r] : 0.0f;
+    for (int r = 0; r < 4; ++r) {
+      float v = act[t][r];
+      __asm__("" : "+v"(v));
+      d[t][r] = v > 0.0f ? d[t][r] : 0.0f;
+    }
 }
 
 // Weight-gradient tiles of one layer held by one wavefront.  The layer's 16x16 tiles i = T * IT + Tp
