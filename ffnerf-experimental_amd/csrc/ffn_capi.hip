@@ -721,9 +721,8 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   if ((uint64_t)num_rays * mp->max_steps >= ((uint64_t)1 << 32))
     return fail(-1, "num_rays * max_steps must stay below 2^32 samples");
   const int LF = h->dc.LF;
-  if (h->cfg.mlp_precision != FFN_MLP_FP32)
-    return fail(-2, "ffn_train_step_marched: only the fp32 MLP path is built for marched training");
-  if (!ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
+  const bool mlp16 = h->cfg.mlp_precision == FFN_MLP_FP16;
+  if (mlp16 ? !ffn::mlp16_supported(LF, h->cfg.nd, h->cfg.nc) : !ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
     return fail(-2, "MLP shape LF=%d nd=%d nc=%d is not built", LF, h->cfg.nd, h->cfg.nc);
   if (!ffn::scatter_supported(h->dc))
     return fail(-2, "ffn_train_step_marched: the scatter is not built for this table shape (F=%d with %u-entry "
@@ -783,8 +782,11 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   }
   // 3-5. forward MLP, compositing with early termination and the loss, MLP backward
   const int64_t n_tiles = (n + 63) / 64;
-  int n_blocks = (h->n_cu > 0 ? h->n_cu : 256) * ffn::mlp_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc);
-  if (n_blocks > n_tiles) n_blocks = (int)(n_tiles > 0 ? n_tiles : 1);
+  // the fp16 kernel walks groups of four tiles
+  const int64_t n_work = mlp16 ? (n_tiles + 3) / 4 : n_tiles;
+  int n_blocks = (h->n_cu > 0 ? h->n_cu : 256) * (mlp16 ? ffn::mlp16_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc)
+                                                         : ffn::mlp_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc));
+  if (n_blocks > n_work) n_blocks = (int)(n_work > 0 ? n_work : 1);
   FFN_HIP(h->partials.ensure(sizeof(float) * (size_t)n_blocks * h->lay.total));
   ffn::MlpPtrs w{};
   for (int k = 0; k < FFN_N_LAYERS; ++k) {
@@ -793,8 +795,12 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   }
   {
     StageTimer tm(h, 2, st);
-    FFN_HIP(ffn::launch_mlp_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, sc->sh_multiplier, sigma, rgb, LF,
-                                h->cfg.nd, h->cfg.nc, n_blocks, st));
+    if (mlp16)
+      FFN_HIP(ffn::launch_mlp16_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, sc->sh_multiplier, sigma, rgb,
+                                    LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+    else
+      FFN_HIP(ffn::launch_mlp_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, sc->sh_multiplier, sigma, rgb,
+                                  LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
     ffn::CompMarchArgs ca{};
     ca.offsets = off;
     ca.counts = counts;
@@ -837,7 +843,8 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
     a.in_dLdc = ca.dLdc;
     a.march_dt = mp->dt;
     if (taps) a.t_relu = taps->relu;
-    if (n > 0) FFN_HIP(ffn::launch_mlp_marched(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+    if (n > 0 && mlp16) FFN_HIP(ffn::launch_mlp16_marched(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+    else if (n > 0) FFN_HIP(ffn::launch_mlp_marched(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
     else FFN_HIP(ffn::launch_fill((float*)h->partials.p, h->lay.total, 0.0f, st));
   }
   if (taps) {

@@ -248,6 +248,11 @@ hipError_t launch_mlp_marched(const MlpArgs& a, int LF, int nd, int nc, int n_bl
 // the same step on fp16 (forward) / bf16 (backward, weight gradients) MFMAs with fp32 accumulation
 bool mlp16_supported(int LF, int nd, int nc);
 hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+// the fp16 path of the marched training step: forward only over indexed samples, and the backward
+hipError_t launch_mlp16_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
+                            const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
+                            float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+hipError_t launch_mlp16_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
 
 // sum the per-block gradient partials and apply Adam to the MLP parameters
 struct MlpOptArgs {

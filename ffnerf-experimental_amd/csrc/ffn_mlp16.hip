@@ -348,7 +348,8 @@ __device__ __forceinline__ void flush_layer16(float* __restrict__ dst, int O, in
 
 // this lane's encoding values: a0v[4 kb + j] = neuron 16 kb + 4 g + j of sample b (0 when !valid)
 template <int LF, int FEAT>
-__device__ __forceinline__ void load_a0(const MlpArgs& a, int64_t b, bool valid, int g, float (&a0v)[LF / 4]) {
+__device__ __forceinline__ void load_a0(const float* __restrict__ a0, const FeatLayout& feat, int64_t b, bool valid,
+                                        int g, float (&a0v)[LF / 4]) {
   if (!valid) {
 #pragma unroll
     for (int q = 0; q < LF / 4; ++q) a0v[q] = 0.0f;
@@ -358,7 +359,7 @@ __device__ __forceinline__ void load_a0(const MlpArgs& a, int64_t b, bool valid,
   for (int kb = 0; kb < LF / 16; ++kb) {
     if constexpr (FEAT == 4) {
       const int l = 4 * kb + g;
-      const float4 v = *reinterpret_cast<const float4*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
+      const float4 v = *reinterpret_cast<const float4*>(a0 + l * feat.stride_l + b * feat.stride_b);
       a0v[4 * kb] = v.x;
       a0v[4 * kb + 1] = v.y;
       a0v[4 * kb + 2] = v.z;
@@ -367,13 +368,13 @@ __device__ __forceinline__ void load_a0(const MlpArgs& a, int64_t b, bool valid,
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int l = 8 * kb + 2 * g + h;
-        const float2 v = *reinterpret_cast<const float2*>(a.a0 + l * a.feat.stride_l + b * a.feat.stride_b);
+        const float2 v = *reinterpret_cast<const float2*>(a0 + l * feat.stride_l + b * feat.stride_b);
         a0v[4 * kb + 2 * h] = v.x;
         a0v[4 * kb + 2 * h + 1] = v.y;
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) a0v[4 * kb + j] = a.a0[(16 * kb + 4 * g + j) * a.feat.stride_l + b * a.feat.stride_b];
+      for (int j = 0; j < 4; ++j) a0v[4 * kb + j] = a0[(16 * kb + 4 * g + j) * feat.stride_l + b * feat.stride_b];
     }
   }
 }
@@ -463,13 +464,20 @@ struct TileIn {
   float4 rd;  // the ray direction
   float dt, t;
 };
-template <int LF, int FEAT>
+// MARCHED: sample b is a.smp[b] of ray a.ray_ids[b], lattice step a.march_dt
+template <int LF, int FEAT, bool MARCHED>
 __device__ __forceinline__ void load_tile_in(const MlpArgs& a, int64_t b, bool valid, int g, int log2S,
                                              TileIn<LF>& in) {
-  load_a0<LF, FEAT>(a, b, valid, g, in.a0v);
-  in.rd = a.rays[2 * (valid ? (b >> log2S) : 0) + 1];
-  in.dt = valid ? a.DTs[b] : 0.0f;
-  in.t = valid ? a.Ts[b] : 0.0f;
+  load_a0<LF, FEAT>(a.a0, a.feat, b, valid, g, in.a0v);
+  if constexpr (MARCHED) {
+    in.rd = a.rays[2 * (valid ? (int64_t)a.ray_ids[b] : 0) + 1];
+    in.dt = valid ? a.march_dt : 0.0f;
+    in.t = valid ? a.smp[b].w : 0.0f;
+  } else {
+    in.rd = a.rays[2 * (valid ? (b >> log2S) : 0) + 1];
+    in.dt = valid ? a.DTs[b] : 0.0f;
+    in.t = valid ? a.Ts[b] : 0.0f;
+  }
 }
 // the first busy tile of the group at or after tt (4 if none)
 __device__ __forceinline__ int next_busy(const int* flags, int tt) {
@@ -477,7 +485,9 @@ __device__ __forceinline__ int next_busy(const int* flags, int tt) {
   return tt;
 }
 
-template <int LF, int ND, int NC, int FEAT, bool TAPS>
+// MARCHED: the backward over marched samples (phase C only, every tile busy): the loss gradients are read
+// from a.in_dLds / a.in_dLdc, the samples' rays, times and step from the march; no compositing, no proposals
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
 __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_mlp16(MlpArgs a) {
   using A = Arch16<LF, ND, NC>;
   constexpr int KB0 = LF / 16;  // D-layout tiles of the encoding
@@ -540,104 +550,111 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   const int64_t n_groups = (a.n_tiles + 3) / 4;
   for (int64_t grp = blockIdx.x; grp < n_groups; grp += gridDim.x) {
     const int64_t tile0 = grp * 4;
-    // (0) the compositing inputs of tile tile0 + wave (past the last tile: no valid lane)
-    const CompLane CL = load_comp_lane(a, tile0 + wave, lane, true, n_samples, log2S, proposals);
-    const bool busy = TAPS ? __ballot(CL.vj) != 0ull : __ballot(CL.vj && CL.dt_j > 0.0f) != 0ull;
-    __syncthreads();  // the previous group is done with sC and the flags
-    if (lane == 0) sFlag[wave] = busy ? 1 : 0;
-    __syncthreads();
-
-    // (A) forward of this wavefront's samples of every busy tile: sigma and rgb into sC; each tile's inputs
-    // are loaded while the previous tile's forward runs
     TileIn<LF> cur;
-    int tt = next_busy(sFlag, 0);
-    if (tt < 4) {
-      const int64_t b = (tile0 + tt) * 64 + col;
-      load_tile_in<LF, FEAT>(a, b, (uint64_t)b < n_samples, g, log2S, cur);
-    }
-#pragma unroll 1
-    while (tt < 4) {
-      const int64_t b = (tile0 + tt) * 64 + col;
-      const bool valid = (uint64_t)b < n_samples;
-      const int tn = next_busy(sFlag, tt + 1);
-      TileIn<LF> nxt;
-      if (tn < 4) {
-        const int64_t bn = (tile0 + tn) * 64 + col;
-        load_tile_in<LF, FEAT>(a, bn, (uint64_t)bn < n_samples, g, log2S, nxt);
+    int tt = 0;
+    if constexpr (!MARCHED) {
+      // (0) the compositing inputs of tile tile0 + wave (past the last tile: no valid lane)
+      const CompLane CL = load_comp_lane(a, tile0 + wave, lane, true, n_samples, log2S, proposals);
+      const bool busy = TAPS ? __ballot(CL.vj) != 0ull : __ballot(CL.vj && CL.dt_j > 0.0f) != 0ull;
+      __syncthreads();  // the previous group is done with sC and the flags
+      if (lane == 0) sFlag[wave] = busy ? 1 : 0;
+      __syncthreads();
+
+      // (A) forward of this wavefront's samples of every busy tile: sigma and rgb into sC; each tile's inputs
+      // are loaded while the previous tile's forward runs
+      tt = next_busy(sFlag, 0);
+      if (tt < 4) {
+        const int64_t b = (tile0 + tt) * 64 + col;
+        load_tile_in<LF, FEAT, MARCHED>(a, b, (uint64_t)b < n_samples, g, log2S, cur);
       }
-      const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
-      floatx4 sh;
+#pragma unroll 1
+      while (tt < 4) {
+        const int64_t b = (tile0 + tt) * 64 + col;
+        const bool valid = (uint64_t)b < n_samples;
+        const int tn = next_busy(sFlag, tt + 1);
+        TileIn<LF> nxt;
+        if (tn < 4) {
+          const int64_t bn = (tile0 + tn) * 64 + col;
+          load_tile_in<LF, FEAT, MARCHED>(a, bn, (uint64_t)bn < n_samples, g, log2S, nxt);
+        }
+        const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
+        floatx4 sh;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
-      Fwd16<LF, ND, NC> f;
-      forward16<LF, ND, NC, A>(sWf, sB, cur.a0v, sh, g, s, f);
-      if constexpr (TAPS) {
-        if (a.t_relu) {
-          uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
+        for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
+        Fwd16<LF, ND, NC> f;
+        forward16<LF, ND, NC, A>(sWf, sB, cur.a0v, sh, g, s, f);
+        if constexpr (TAPS) {
+          if (a.t_relu) {
+            uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
 #pragma unroll
-          for (int i = 0; i < ND; ++i) tap_relu8(rec, i, f.hd[i], g);
+            for (int i = 0; i < ND; ++i) tap_relu8(rec, i, f.hd[i], g);
 #pragma unroll
-          for (int i = 0; i < NC; ++i) tap_relu8(rec, 3 + i, f.hc[i], g);
+            for (int i = 0; i < NC; ++i) tap_relu8(rec, 3 + i, f.hc[i], g);
+          }
+        }
+        if (g == 0) {
+          float sig = softplus(fminf(fmaxf(f.dout0, -10.0f), 10.0f));
+          if (cur.dt <= 0.0f) sig = 0.0f;
+          float* sSig = sC + tt * 256;
+          sSig[col] = sig;
+          sSig[64 + col * 3 + 0] = f.rgb[0];
+          sSig[64 + col * 3 + 1] = f.rgb[1];
+          sSig[64 + col * 3 + 2] = f.rgb[2];
+        }
+        cur = nxt;
+        tt = tn;
+      }
+      __syncthreads();
+
+      // (B) this wavefront composites tile tile0 + wave (all its 64 samples, proposals included); lane j's
+      // loss gradients replace its sigma and rgb
+      {
+        float* sSig = sC + wave * 256;
+        if (busy) {
+          float dLds_j, dLdc_j[3];
+          composite_tile<TAPS>(a, sSig, sSig + 64, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
+          sSig[lane] = dLds_j;
+          sSig[64 + 3 * lane] = dLdc_j[0];
+          sSig[64 + 3 * lane + 1] = dLdc_j[1];
+          sSig[64 + 3 * lane + 2] = dLdc_j[2];
+        } else if ((lane & (a.S - 1)) == 0 && CL.vj) {
+          // every alpha is 0: T = 1 and the colour is the background
+          float bg[3];
+          background(a, CL.rj, train, bg);
+          a.out_rgb[CL.rj] = make_float4(fminf(fmaxf(bg[0], 0.0f), 1.0f), fminf(fmaxf(bg[1], 0.0f), 1.0f),
+                                         fminf(fmaxf(bg[2], 0.0f), 1.0f), train ? 4.0f : 0.0f);
         }
       }
-      if (g == 0) {
-        float sig = softplus(fminf(fmaxf(f.dout0, -10.0f), 10.0f));
-        if (cur.dt <= 0.0f) sig = 0.0f;
-        float* sSig = sC + tt * 256;
-        sSig[col] = sig;
-        sSig[64 + col * 3 + 0] = f.rgb[0];
-        sSig[64 + col * 3 + 1] = f.rgb[1];
-        sSig[64 + col * 3 + 2] = f.rgb[2];
-      }
-      cur = nxt;
-      tt = tn;
+      if (!train) continue;
+      __syncthreads();
     }
-    __syncthreads();
-
-    // (B) this wavefront composites tile tile0 + wave (all its 64 samples, proposals included); lane j's
-    // loss gradients replace its sigma and rgb
-    {
-      float* sSig = sC + wave * 256;
-      if (busy) {
-        float dLds_j, dLdc_j[3];
-        composite_tile<TAPS>(a, sSig, sSig + 64, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
-        sSig[lane] = dLds_j;
-        sSig[64 + 3 * lane] = dLdc_j[0];
-        sSig[64 + 3 * lane + 1] = dLdc_j[1];
-        sSig[64 + 3 * lane + 2] = dLdc_j[2];
-      } else if ((lane & (a.S - 1)) == 0 && CL.vj) {
-        // every alpha is 0: T = 1 and the colour is the background
-        float bg[3];
-        background(a, CL.rj, train, bg);
-        a.out_rgb[CL.rj] = make_float4(fminf(fmaxf(bg[0], 0.0f), 1.0f), fminf(fmaxf(bg[1], 0.0f), 1.0f),
-                                       fminf(fmaxf(bg[2], 0.0f), 1.0f), train ? 4.0f : 0.0f);
-      }
-    }
-    if (!train) continue;
-    __syncthreads();
 
     // (C) per busy tile: the forward again, then the backward (fp16 chain with per-wavefront delta scaling,
     // fp32 accumulation); every layer's deltas and inputs go through the stash for the block's bf16
     // weight-gradient tiles (barrier, this wave's tiles, barrier before the stash is reused).  First the
     // zero encoding gradients of the idle tiles' samples.
+    if constexpr (!MARCHED) {
 #pragma unroll 1
-    for (int ti = 0; ti < 4; ++ti) {
-      const int64_t b = (tile0 + ti) * 64 + col;
-      if (sFlag[ti] || (uint64_t)b >= n_samples) continue;
-      floatx4 z[KB0];
+      for (int ti = 0; ti < 4; ++ti) {
+        const int64_t b = (tile0 + ti) * 64 + col;
+        if (sFlag[ti] || (uint64_t)b >= n_samples) continue;
+        floatx4 z[KB0];
 #pragma unroll
-      for (int t = 0; t < KB0; ++t) z[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      store_enc_grad<LF, FEAT>(a, b, g, z);
+        for (int t = 0; t < KB0; ++t) z[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        store_enc_grad<LF, FEAT>(a, b, g, z);
+      }
     }
     // (the inputs load at the start of each tile: loaded a tile ahead, they stayed live through the backward
     // and cost more in spills than the latency they hid)
-    tt = next_busy(sFlag, 0);
+    // marched tiles are all busy up to the last one
+    const int tiles_here = MARCHED ? (int)(a.n_tiles - tile0 < 4 ? a.n_tiles - tile0 : 4) : 4;
+    tt = MARCHED ? 0 : next_busy(sFlag, 0);
 #pragma unroll 1
-    while (tt < 4) {
+    while (tt < tiles_here) {
       const int64_t b = (tile0 + tt) * 64 + col;
       const bool valid = (uint64_t)b < n_samples;
-      const int tn = next_busy(sFlag, tt + 1);
-      load_tile_in<LF, FEAT>(a, b, valid, g, log2S, cur);
+      const int tn = MARCHED ? tt + 1 : next_busy(sFlag, tt + 1);
+      load_tile_in<LF, FEAT, MARCHED>(a, b, valid, g, log2S, cur);
       const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
       floatx4 sh;
 #pragma unroll
@@ -653,9 +670,28 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       for (int t = 0; t < KB0; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) a0b[t][r] = (__bf16)a0v[4 * t + r];
-      const float* sD = sC + tt * 256;
-      const float dLds = sD[col], dLdc0 = sD[64 + 3 * col], dLdc1 = sD[64 + 3 * col + 1],
-                  dLdc2 = sD[64 + 3 * col + 2];
+      float dLds, dLdc0, dLdc1, dLdc2;
+      if constexpr (MARCHED) {
+        dLds = valid ? a.in_dLds[b] : 0.0f;
+        dLdc0 = valid ? a.in_dLdc[3 * b] : 0.0f;
+        dLdc1 = valid ? a.in_dLdc[3 * b + 1] : 0.0f;
+        dLdc2 = valid ? a.in_dLdc[3 * b + 2] : 0.0f;
+        if constexpr (TAPS) {
+          if (a.t_relu) {
+            uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
+#pragma unroll
+            for (int i = 0; i < ND; ++i) tap_relu8(rec, i, f.hd[i], g);
+#pragma unroll
+            for (int i = 0; i < NC; ++i) tap_relu8(rec, 3 + i, f.hc[i], g);
+          }
+        }
+      } else {
+        const float* sD = sC + tt * 256;
+        dLds = sD[col];
+        dLdc0 = sD[64 + 3 * col];
+        dLdc1 = sD[64 + 3 * col + 1];
+        dLdc2 = sD[64 + 3 * col + 2];
+      }
       floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
       floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
       if (g == 0 && valid) {
@@ -772,33 +808,106 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC, int FEAT, bool TAPS>
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
 static hipError_t launch16_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch16<LF, ND, NC>;
   const size_t lds = A::lds_bytes();
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT, TAPS>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT, TAPS>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
-template <int LF, int ND, int NC>
+template <int LF, int ND, int NC, bool MARCHED>
 static hipError_t launch16_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
   const bool taps = taps_requested(a);
   switch (a.c.F) {
     case 1:
-      return taps ? launch16_f<LF, ND, NC, 1, true>(a, n_blocks, st) : launch16_f<LF, ND, NC, 1, false>(a, n_blocks, st);
+      return taps ? launch16_f<LF, ND, NC, 1, true, MARCHED>(a, n_blocks, st)
+                  : launch16_f<LF, ND, NC, 1, false, MARCHED>(a, n_blocks, st);
     case 2:
-      return taps ? launch16_f<LF, ND, NC, 2, true>(a, n_blocks, st) : launch16_f<LF, ND, NC, 2, false>(a, n_blocks, st);
+      return taps ? launch16_f<LF, ND, NC, 2, true, MARCHED>(a, n_blocks, st)
+                  : launch16_f<LF, ND, NC, 2, false, MARCHED>(a, n_blocks, st);
     case 4:
-      return taps ? launch16_f<LF, ND, NC, 4, true>(a, n_blocks, st) : launch16_f<LF, ND, NC, 4, false>(a, n_blocks, st);
+      return taps ? launch16_f<LF, ND, NC, 4, true, MARCHED>(a, n_blocks, st)
+                  : launch16_f<LF, ND, NC, 4, false, MARCHED>(a, n_blocks, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Forward only, for samples given by index (the marched training step's sigma and rgb, which its
+// compositing kernel needs before the backward): the same fp16 forward as k_mlp16's, 16 samples per
+// wavefront at a time; sample b belongs to ray ray_ids[b]
+template <int LF, int ND, int NC, int FEAT>
+__global__ __launch_bounds__(256) void k_mlp16_fwd(MlpPtrs wp, const float* __restrict__ a0, FeatLayout feat,
+                                                   const float4* __restrict__ rays,
+                                                   const uint32_t* __restrict__ ray_ids, int64_t n, float sh_mult,
+                                                   float* __restrict__ sigma, float* __restrict__ rgb) {
+  using A = Arch16<LF, ND, NC>;
+  extern __shared__ __align__(16) unsigned char smem16f[];
+  _Float16* sWf = reinterpret_cast<_Float16*>(smem16f);
+  float* sB = reinterpret_cast<float*>(smem16f + (size_t)A::wf_off(FFN_N_LAYERS) * 2);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+#pragma unroll
+  for (int k = 0; k < FFN_N_LAYERS; ++k) {
+    if (!layer_active(k, ND, NC)) continue;
+    const int O = layer_out(k), I = layer_in(k, LF), R = A::rows_pad(k), PF = A::pf(k);
+    const bool kf = I % 32 == 0;
+    for (int e = tid; e < R * PF; e += 256) {
+      const int r = e / PF, p = e - r * PF;
+      const int i = p < I ? (kf ? kpos_neuron(p) : p) : I;
+      sWf[A::wf_off(k) + e] = (_Float16)((r < O && i < I) ? wp.W[k][r * I + i] : 0.0f);
+    }
+    for (int e = tid; e < R; e += 256) sB[A::b_off(k) + e] = e < O ? wp.b[k][e] : 0.0f;
+  }
+  __syncthreads();
+  for (int64_t grp = (int64_t)blockIdx.x * 4 + wave; grp * 16 < n; grp += (int64_t)gridDim.x * 4) {
+    const int64_t b = grp * 16 + s;
+    const bool valid = b < n;
+    float a0v[LF / 4];
+    load_a0<LF, FEAT>(a0, feat, b, valid, g, a0v);
+    float dirv[3] = {0.0f, 0.0f, 1.0f};
+    if (valid) {
+      const float4 rd = rays[2 * (size_t)ray_ids[b] + 1];
+      dirv[0] = rd.x;
+      dirv[1] = rd.y;
+      dirv[2] = rd.z;
+    }
+    floatx4 sh;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * sh_mult;
+    Fwd16<LF, ND, NC> f;
+    forward16<LF, ND, NC, A>(sWf, sB, a0v, sh, g, s, f);
+    if (g == 0 && valid) {
+      sigma[b] = softplus(fminf(fmaxf(f.dout0, -10.0f), 10.0f));
+      rgb[3 * b] = f.rgb[0];
+      rgb[3 * b + 1] = f.rgb[1];
+      rgb[3 * b + 2] = f.rgb[2];
+    }
+  }
+}
+
+template <int LF, int ND, int NC, int FEAT>
+static hipError_t launch16_fwd_f(const MlpPtrs& w, const float* a0, const FeatLayout& feat, const float4* rays,
+                                 const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma, float* rgb,
+                                 int n_blocks, hipStream_t st) {
+  using A = Arch16<LF, ND, NC>;
+  const size_t lds = (size_t)A::wf_off(FFN_N_LAYERS) * 2 + (size_t)A::b_floats() * 4;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16_fwd<LF, ND, NC, FEAT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_mlp16_fwd<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, w, a0, feat, rays,
+                     ray_ids, n, sh_mult, sigma, rgb);
+  return hipGetLastError();
 }
 
 #define FFN_MLP16_CONFIGS(X) \
@@ -827,7 +936,33 @@ bool mlp16_supported(int LF, int nd, int nc) {
 
 hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
 #define X(l, d, n) \
-  if (LF == l && nd == d && nc == n) return launch16_t<l, d, n>(a, n_blocks, st);
+  if (LF == l && nd == d && nc == n) return launch16_t<l, d, n, false>(a, n_blocks, st);
+  FFN_MLP16_CONFIGS(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_mlp16_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+#define X(l, d, n) \
+  if (LF == l && nd == d && nc == n) return launch16_t<l, d, n, true>(a, n_blocks, st);
+  FFN_MLP16_CONFIGS(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_mlp16_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
+                            const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
+                            float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+#define X(l, d, nn)                                                                                             \
+  if (LF == l && nd == d && nc == nn) {                                                                         \
+    switch (c.F) {                                                                                              \
+      case 1: return launch16_fwd_f<l, d, nn, 1>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st); \
+      case 2: return launch16_fwd_f<l, d, nn, 2>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st); \
+      case 4: return launch16_fwd_f<l, d, nn, 4>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st); \
+      default: return hipErrorInvalidValue;                                                                     \
+    }                                                                                                           \
+  }
   FFN_MLP16_CONFIGS(X)
 #undef X
   return hipErrorInvalidValue;

@@ -228,9 +228,9 @@ int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const u
  * num_rays * max_steps): sigma, rgb, Tr, dL_dsigma, dL_dc, a0, dL_da0, relu,
  * the per-ray T_final and color, and the summed gradients.  A step whose
  * march finds no samples returns the background, leaves the table and its
- * moments as they are and runs the MLP's Adam on zero gradients.  fp32 MLP
- * path only.  Waits on the stream once, after the march's count, to size the
- * step's launches. */
+ * moments as they are and runs the MLP's Adam on zero gradients.  Both MLP
+ * paths (mlp_precision fp32 or fp16).  Waits on the stream once, after the
+ * march's count, to size the step's launches. */
 int ffn_train_step_marched(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
                            const uint32_t* bits, const ffn_march_params* mp, const ffn_step_scalars* scalars,
                            const ffn_taps* taps, uint32_t* n_samples, void* stream);

@@ -36,12 +36,13 @@ def shell_bits(R, seed=0, frac=0.02):
     return bits
 
 
-@pytest.mark.parametrize("T_stop,hash_opt,table", [(1e-2, 1, "fp32"), (0.0, 1, "fp32"), (1e-2, 0, "fp32"),
-                                                   (1e-2, 1, "fp16"), (1e-2, 0, "fp16")])
-def test_marched_steps_match_oracle(gh, ora, T_stop, hash_opt, table):
-    print(f"[case] marched train T_stop={T_stop} hash_opt={hash_opt} table={table}", flush=True)
+@pytest.mark.parametrize("T_stop,hash_opt,table,mlp", [(1e-2, 1, "fp32", 0), (0.0, 1, "fp32", 0), (1e-2, 0, "fp32", 0),
+                                                       (1e-2, 1, "fp16", 0), (1e-2, 0, "fp16", 0),
+                                                       (1e-2, 1, "fp32", 1), (0.0, 0, "fp16", 1)])
+def test_marched_steps_match_oracle(gh, ora, T_stop, hash_opt, table, mlp):
+    print(f"[case] marched train T_stop={T_stop} hash_opt={hash_opt} table={table} mlp_precision={mlp}", flush=True)
     import ffn_lib as fl
-    spec = spec_cfg0(occ_G=R // 2, hash_opt=hash_opt, table_dtype=table)
+    spec = spec_cfg0(occ_G=R // 2, hash_opt=hash_opt, table_dtype=table, mlp_precision=mlp)
     p = random_params(spec, seed=41)
     if table == "fp16":
         p["table"] = p["table"].astype(np.float16).astype(np.float32)
