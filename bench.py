@@ -336,14 +336,14 @@ def ball_bitfield(R, radius=0.25):
     return bits
 
 
-def run_marched_train(args, pool_rays, pool_tg):
+def run_marched_train(args, pool_rays, pool_tg, mlp="fp32"):
     """The training step fed by the march (ffn_train_step_marched): the cfg2 model and batches (2^18 rays of
     the ball scene per step), a 256^3 bitfield of the ball's cells, dt = sqrt(3)/1024, at most 1024 samples
     per ray, compositing stopped at T < 1e-4.  Returns the measurement as a dict."""
     import tempfile
     import torch
     import ffnerf_tools as ft
-    spec, occ, _ = cfg2_spec("fp32")
+    spec, occ, _ = cfg2_spec(mlp)
     nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_benchm_"), "benchm", spec=spec, occ=occ, rng_seed=0)
     R, max_steps = 256, 1024
     dt = float(np.float32(np.sqrt(3.0) / max_steps))
@@ -476,6 +476,10 @@ def run_cfg4(args):
             pt.append(t_)
         print("[bench] marched training step", flush=True)
         line["train_marched"] = run_marched_train(args, pr, pt)
+        print("[bench] marched training step, fp16 MLP", flush=True)
+        m16 = run_marched_train(args, pr, pt, mlp="fp16")
+        line["train_marched"]["fp16_mlp_path"] = {k: m16[k] for k in ("ms_per_step", "value", "unit",
+                                                                       "stages_ms_avg")}
     print(json.dumps(line), flush=True)
     return line
 
