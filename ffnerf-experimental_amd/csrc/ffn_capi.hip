@@ -81,6 +81,7 @@ struct Handle {
   Scratch m_state, m_acc, m_counts, m_offsets, m_sums, m_total, m_samples, m_ids, m_a0, m_sigma, m_rgb;
   // marched training
   Scratch m_Tr, m_dLds, m_dLdc;
+  Scratch m_bits;  // the bitfield of ffn_train_step's march sampler
   uint32_t* host_total = nullptr;  // pinned
 };
 
@@ -140,6 +141,16 @@ int validate_config(const ffn_config* c, int64_t* table_entries) {
     return fail(-1, "mlp_precision=%d unknown", c->mlp_precision);
   if (c->table_dtype != FFN_TABLE_FP32 && c->table_dtype != FFN_TABLE_FP16)
     return fail(-1, "table_dtype=%d unknown", c->table_dtype);
+  if (c->sampler != FFN_SAMPLER_RESAMPLE && c->sampler != FFN_SAMPLER_MARCH)
+    return fail(-1, "sampler=%d unknown", c->sampler);
+  if (c->sampler == FFN_SAMPLER_MARCH) {
+    if (c->march_max_steps < 1 || c->march_max_steps > 4096)
+      return fail(-1, "march_max_steps=%d out of [1,4096]", c->march_max_steps);
+    if (!(c->march_dt > 0.0f)) return fail(-1, "march_dt must be > 0");
+    if (!(c->march_T_stop >= 0.0f && c->march_T_stop < 1.0f)) return fail(-1, "march_T_stop must be in [0,1)");
+    if (c->march_q_min < 1 || c->march_q_min > 17) return fail(-1, "march_q_min=%d out of [1,17]", c->march_q_min);
+    if (2 * c->occ_G > 1024) return fail(-1, "the march's bitfield has at most 1024 cells per axis (occ_G <= 512)");
+  }
   return 0;
 }
 
@@ -445,12 +456,32 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
   return 0;
 }
 
+// ffn_train_step with the march sampler: the bitfield from occ_in, then the marched step (or the render)
+static int step_by_march(Handle* h, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
+                         const ffn_step_scalars* sc, const ffn_taps* taps, void* stream) {
+  const int G = h->cfg.occ_G, R = 2 * G;
+  const size_t words = ((size_t)R * R * R + 31) / 32;
+  FFN_HIP(h->m_bits.ensure(sizeof(uint32_t) * words));
+  uint32_t* bits = (uint32_t*)h->m_bits.p;
+  FFN_HIP(ffn::launch_occ_bitfield(h->params.occ_in, G, (uint32_t)h->cfg.march_q_min, bits, (hipStream_t)stream));
+  ffn_march_params mp{};
+  mp.res = R;
+  mp.dt = h->cfg.march_dt;
+  mp.max_steps = (uint32_t)h->cfg.march_max_steps;
+  mp.T_stop = h->cfg.march_T_stop;
+  mp.chunk = 32;
+  mp.sh_multiplier = sc->sh_multiplier;
+  if (!sc->do_train) return ffn_render(h, rays, num_rays, bits, &mp, out_rgb, nullptr, stream);
+  return ffn_train_step_marched(h, rays, targets, out_rgb, num_rays, bits, &mp, sc, taps, nullptr, stream);
+}
+
 int ffn_train_step(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
                    uint32_t spr, const ffn_step_scalars* sc, const ffn_taps* taps, void* stream) {
   Handle* h = as_handle(handle);
   if (!h) return fail(-1, "NULL handle");
   if (!h->bound) return fail(-1, "ffn_bind_params must be called before ffn_train_step");
   if (!sc) return fail(-1, "NULL scalars");
+  if (h->cfg.sampler == FFN_SAMPLER_MARCH) return step_by_march(h, rays, targets, out_rgb, num_rays, sc, taps, stream);
   if (!is_pow2(spr) || spr > FFN_S_MAX) return fail(-1, "samples_per_ray=%u must be a power of two <= %d", spr, FFN_S_MAX);
   if (num_rays == 0) return fail(-1, "num_rays must be > 0");
   if (!rays || !out_rgb) return fail(-1, "NULL rays/out_rgb");

@@ -20,6 +20,7 @@ BG = {"black": 0, "white": 1, "random": 2}
 HASH_OPT = {"sgd": 0, "adam": 1}
 MLP_PRECISION = {"fp32": 0, "fp16": 1}
 TABLE_DTYPE = {"fp32": 0, "fp16": 1}
+SAMPLER = {"resample": 0, "march": 1}
 
 EXPORTS = [
     "ffn_version", "ffn_last_error", "ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step",
@@ -45,7 +46,9 @@ class FfnConfig(C.Structure):
         ("rho_min", C.c_float), ("rho_max", C.c_float), ("dt_min", C.c_float), ("dt_max", C.c_float),
         ("t_near", C.c_float), ("t_far", C.c_float),
         ("background", C.c_int32), ("hash_opt", C.c_int32), ("mlp_precision", C.c_int32),
-        ("table_dtype", C.c_int32), ("reserved", C.c_int32 * 7),
+        ("table_dtype", C.c_int32),
+        ("sampler", C.c_int32), ("march_max_steps", C.c_int32), ("march_dt", C.c_float),
+        ("march_T_stop", C.c_float), ("march_q_min", C.c_int32), ("reserved", C.c_int32 * 2),
     ]
 
 
@@ -198,6 +201,16 @@ def make_config(spec: dict) -> FfnConfig:
     c.mlp_precision = MLP_PRECISION[mp] if isinstance(mp, str) else int(mp)
     td = spec.get("table_dtype", 0)
     c.table_dtype = TABLE_DTYPE[td] if isinstance(td, str) else int(td)
+    sm = spec.get("sampler", 0)
+    c.sampler = SAMPLER[sm] if isinstance(sm, str) else int(sm)
+    if c.sampler == SAMPLER["march"]:
+        # defaults: the reference's inference predicate (nibble >= 3), a lattice step of the box diagonal over
+        # max_steps, and the cfg4 stop
+        c.march_max_steps = int(spec.get("march_max_steps", 1024))
+        ext = max(float(spec["box_max"][i]) - float(spec["box_min"][i]) for i in range(3))
+        c.march_dt = float(spec.get("march_dt") or (3.0 ** 0.5) * ext / c.march_max_steps)
+        c.march_T_stop = float(spec.get("march_T_stop", 1e-4))
+        c.march_q_min = int(spec.get("march_q_min", 4))
     return c
 
 

@@ -163,6 +163,11 @@ class ModelSpec:
     hash_opt: str = "sgd"       # sgd (reference, in-step) | adam
     mlp_precision: str = "fp32"
     table_dtype: str = "fp32"   # fp32 (reference) | fp16: the table's storage; its Adam state stays fp32
+    sampler: str = "resample"   # resample (reference) | march: step() samples by the bitfield march
+    march_max_steps: int = 1024
+    march_dt: float | None = None   # default: the box's largest extent times sqrt(3) / march_max_steps
+    march_T_stop: float = 1e-4
+    march_q_min: int = 4            # cells with occupancy level q >= q_min (the inference predicate)
     init: str = "he"            # he (reference) | xavier
     beta1: float = 0.9
     beta2: float = 0.999
@@ -233,6 +238,8 @@ def spec_dict(spec: ModelSpec, occ: OccParams) -> dict:
         dt_max=float(occ.dt_max), t_near=float(occ.t_near_clip), t_far=float(occ.t_far_clip),
         background=fl.BG[spec.background], hash_opt=fl.HASH_OPT[spec.hash_opt],
         mlp_precision=fl.MLP_PRECISION[spec.mlp_precision], table_dtype=fl.TABLE_DTYPE[spec.table_dtype],
+        sampler=fl.SAMPLER[spec.sampler], march_max_steps=int(spec.march_max_steps), march_dt=spec.march_dt,
+        march_T_stop=float(spec.march_T_stop), march_q_min=int(spec.march_q_min),
     )
 
 
@@ -477,7 +484,8 @@ class Nerf:
         fl.check(lib.ffn_train_step(self.handle.h, fl.ptr(io.rays_buf), fl.ptr(io.targets_buf), fl.ptr(io.out_buf),
                                     io.num_rays, io.samples_per_ray, C.byref(sc),
                                     C.byref(taps) if taps is not None else None, sp), "ffn_train_step")
-        if (do_train and float(occ_update_strength) > 0.0
+        # the march sampler makes no proposals, so the grid it reads is not decayed either
+        if (do_train and float(occ_update_strength) > 0.0 and self.spec.sampler != "march"
                 and self.steps_trained % int(self.occ.maintenance_period) == 0):
             d = 1 - float(occ_update_strength) * (1 - float(self.occ.decay))
             decay_q24 = int(round(d * (1 << 24)))

@@ -53,6 +53,7 @@ enum { FFN_BG_BLACK = 0, FFN_BG_WHITE = 1, FFN_BG_RANDOM = 2 };     /* -DBACKGRO
 enum { FFN_HASH_SGD = 0, FFN_HASH_ADAM = 1 };                       /* table optimizer */
 enum { FFN_MLP_FP32 = 0, FFN_MLP_FP16 = 1 };                        /* MLP arithmetic */
 enum { FFN_TABLE_FP32 = 0, FFN_TABLE_FP16 = 1 };                    /* hash-table storage */
+enum { FFN_SAMPLER_RESAMPLE = 0, FFN_SAMPLER_MARCH = 1 };           /* ffn_train_step's samples */
 
 /* Build-time constants of the reference (ffnerf_OG.cl:16-81,161-200;
  * ffnerf_tools.py:23-69; run_ffnerf_OG.py:1044-1057) as runtime values. */
@@ -70,7 +71,14 @@ typedef struct ffn_config {
   int32_t hash_opt;                     /* FFN_HASH_* */
   int32_t mlp_precision;                /* FFN_MLP_* */
   int32_t table_dtype;                  /* FFN_TABLE_*: the table's storage (its Adam state stays fp32) */
-  int32_t reserved[7];
+  /* FFN_SAMPLER_MARCH: ffn_train_step samples by the bitfield march instead of the reference's
+     importance resampler (no counterpart in the reference; see ffn_train_step) */
+  int32_t sampler;                      /* FFN_SAMPLER_* */
+  int32_t march_max_steps;              /* samples per ray at most (1..4096) */
+  float march_dt;                       /* lattice step (> 0) */
+  float march_T_stop;                   /* compositing stops after the sample that leaves T < T_stop, [0, 1) */
+  int32_t march_q_min;                  /* bitfield predicate: occupancy level q = nibble + 1 >= q_min (1..17) */
+  int32_t reserved[2];
 } ffn_config;
 
 /* Caller-owned device buffers of one model.  Weights are row-major
@@ -135,7 +143,13 @@ int ffn_bind_params(void* handle, const ffn_params* params);
 
 /* One training step (do_train=1) or forward-only render (do_train=0).
  * rays: [num_rays] {float4 o (w=1), float4 d (w=0)} (ffnerf_tools.py:170-172);
- * targets, out_rgb: [num_rays] float4.  samples_per_ray: power of two <= 64. */
+ * targets, out_rgb: [num_rays] float4.  samples_per_ray: power of two <= 64.
+ * With config sampler = FFN_SAMPLER_MARCH the step takes its samples from the
+ * bitfield march instead (samples_per_ray is then ignored): the bitfield of
+ * the (2 occ_G)^3 subcells with q >= march_q_min is built from occ_in, and
+ * the step is ffn_train_step_marched with march_dt, march_max_steps and
+ * march_T_stop (taps index the march's samples; no occupancy proposals); a
+ * forward-only call is ffn_render (out_rgb.w = T_final). */
 int ffn_train_step(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
                    uint32_t samples_per_ray, const ffn_step_scalars* scalars, const ffn_taps* taps,
                    void* stream);

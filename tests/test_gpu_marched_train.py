@@ -98,3 +98,34 @@ def test_marched_step_without_samples(gh, ora):
     for k in ("table", "m_table", "v_table"):
         np.testing.assert_array_equal(st[k], p[k])
     assert not np.array_equal(st["Wd_in"], p["Wd_in"])  # the MLP's Adam moved by its moments
+
+
+@pytest.mark.parametrize("mlp", [0, 1])
+def test_train_step_with_the_march_sampler(gh, ora, mlp):
+    """ffn_config.sampler = march: ffn_train_step builds the bitfield from occ_in (q >= march_q_min) and runs
+    the marched step; the result equals ffn_train_step_marched fed with ffn_occ_bitfield's field, bit for bit
+    (state and colours), and a forward-only call equals ffn_render."""
+    print(f"[case] march sampler through ffn_train_step, mlp_precision={mlp}", flush=True)
+    import ffn_lib as fl
+    spec = spec_cfg0(occ_G=R // 2, hash_opt=1, mlp_precision=mlp, sampler="march", march_max_steps=128,
+                     march_dt=float(DT), march_T_stop=1e-2, march_q_min=4)
+    p = random_params(spec, seed=61)
+    p["bd_out"][0] = 8.0
+    rays = look_at_rays(256, spec, seed=62, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    sc = default_scalars(rng_seed=63, occ_strength=0.0)
+    a = gh.GpuModel(spec, p)
+    out_a, _ = a.train_step(rays, tg, 64, sc)
+    b = gh.GpuModel(spec, p)
+    bits = b.bitfield(p["occ_in"], R // 2, 4)
+    mp = fl.march_params(R, DT, 128, T_stop=1e-2)
+    out_b, used, G = b.train_step_marched(rays, tg, bits, mp, sc)
+    assert G["n_march"].sum() > 1000
+    np.testing.assert_array_equal(out_a, out_b)
+    sa, sb = a.state(), b.state()
+    for k in sa:
+        np.testing.assert_array_equal(sa[k], sb[k], err_msg=k)
+    # forward only
+    out_r, _ = a.train_step(rays, tg, 64, dict(sc, do_train=0))
+    ref, _ = b.render(rays, bits, fl.march_params(R, DT, 128, T_stop=1e-2, chunk=32))
+    np.testing.assert_array_equal(out_r, ref)
