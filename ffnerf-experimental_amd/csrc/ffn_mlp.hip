@@ -334,7 +334,7 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
 
 // MARCHED: the backward over marched samples -- sample b is a.smp[b] of ray a.ray_ids[b], its loss gradients
 // are read (a.in_dLds, a.in_dLdc), and there is no compositing and no proposal
-template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
 __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_mlp(MlpArgs a) {
   using A = Arch<LF, ND, NC>;
   constexpr int KA = LF / 4;  // a0 values per lane (k-steps of the first layer)
@@ -397,9 +397,9 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront makes the tile's proposals
     CompLane CL{};
     if constexpr (!MARCHED) {
-      CL = load_comp_lane(a, tile, lane, prop_wave, n_samples, log2S, proposals);
+      CL = load_comp_lane<SC>(a, tile, lane, prop_wave, n_samples, log2S, proposals);
       if (!taps && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
-        empty_tile<LF, FEAT>(a, CL, lane, wave, b, valid, train, g);
+        empty_tile<LF, FEAT, SC>(a, CL, lane, wave, b, valid, train, g);
         continue;
       }
     }
@@ -440,7 +440,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
       // ------------------------------------------------------------------
       // compositing on 64 lanes: lane j = sample j of the tile (every wave)
       float dLds_j, dLdc_j[3];
-      composite_tile<TAPS>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+      composite_tile<TAPS, SC>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
       if (!train) continue;
       dLds = __shfl(dLds_j, col);
       dLdc0 = __shfl(dLdc_j[0], col);
@@ -550,35 +550,35 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
 static hipError_t launch_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch<LF, ND, NC>;
   const size_t lds = sizeof(float) * (size_t)A::lds_floats(a.do_train != 0);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT, TAPS, MARCHED>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp<LF, ND, NC, FEAT, TAPS, MARCHED, SC>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)(sizeof(float) * (size_t)A::lds_floats(false)));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp<LF, ND, NC, FEAT, TAPS, MARCHED>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp<LF, ND, NC, FEAT, TAPS, MARCHED, SC>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
-template <int LF, int ND, int NC, bool MARCHED>
+template <int LF, int ND, int NC, bool MARCHED, int SC>
 static hipError_t launch_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
   const bool taps = taps_requested(a);
   switch (a.c.F) {
     case 1:
-      return taps ? launch_f<LF, ND, NC, 1, true, MARCHED>(a, n_blocks, st)
-                  : launch_f<LF, ND, NC, 1, false, MARCHED>(a, n_blocks, st);
+      return taps ? launch_f<LF, ND, NC, 1, true, MARCHED, SC>(a, n_blocks, st)
+                  : launch_f<LF, ND, NC, 1, false, MARCHED, SC>(a, n_blocks, st);
     case 2:
-      return taps ? launch_f<LF, ND, NC, 2, true, MARCHED>(a, n_blocks, st)
-                  : launch_f<LF, ND, NC, 2, false, MARCHED>(a, n_blocks, st);
+      return taps ? launch_f<LF, ND, NC, 2, true, MARCHED, SC>(a, n_blocks, st)
+                  : launch_f<LF, ND, NC, 2, false, MARCHED, SC>(a, n_blocks, st);
     case 4:
-      return taps ? launch_f<LF, ND, NC, 4, true, MARCHED>(a, n_blocks, st)
-                  : launch_f<LF, ND, NC, 4, false, MARCHED>(a, n_blocks, st);
+      return taps ? launch_f<LF, ND, NC, 4, true, MARCHED, SC>(a, n_blocks, st)
+                  : launch_f<LF, ND, NC, 4, false, MARCHED, SC>(a, n_blocks, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -688,7 +688,8 @@ hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, co
 
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
 #define X(l, d, n) \
-  if (LF == l && nd == d && nc == n) return launch_t<l, d, n, false>(a, n_blocks, st);
+  if (LF == l && nd == d && nc == n)                                                         \
+    return a.S == 64 ? launch_t<l, d, n, false, 64>(a, n_blocks, st) : launch_t<l, d, n, false, 0>(a, n_blocks, st);
   FFN_MLP_CONFIGS(X)
 #undef X
   return hipErrorInvalidValue;
@@ -696,7 +697,7 @@ hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hi
 
 hipError_t launch_mlp_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
 #define X(l, d, n) \
-  if (LF == l && nd == d && nc == n) return launch_t<l, d, n, true>(a, n_blocks, st);
+  if (LF == l && nd == d && nc == n) return launch_t<l, d, n, true, 0>(a, n_blocks, st);
   FFN_MLP_CONFIGS(X)
 #undef X
   return hipErrorInvalidValue;

@@ -487,7 +487,7 @@ __device__ __forceinline__ int next_busy(const int* flags, int tt) {
 
 // MARCHED: the backward over marched samples (phase C only, every tile busy): the loss gradients are read
 // from a.in_dLds / a.in_dLdc, the samples' rays, times and step from the march; no compositing, no proposals
-template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
 __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_mlp16(MlpArgs a) {
   using A = Arch16<LF, ND, NC>;
   constexpr int KB0 = LF / 16;  // D-layout tiles of the encoding
@@ -554,7 +554,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     int tt = 0;
     if constexpr (!MARCHED) {
       // (0) the compositing inputs of tile tile0 + wave (past the last tile: no valid lane)
-      const CompLane CL = load_comp_lane(a, tile0 + wave, lane, true, n_samples, log2S, proposals);
+      const CompLane CL = load_comp_lane<SC>(a, tile0 + wave, lane, true, n_samples, log2S, proposals);
       const bool busy = TAPS ? __ballot(CL.vj) != 0ull : __ballot(CL.vj && CL.dt_j > 0.0f) != 0ull;
       __syncthreads();  // the previous group is done with sC and the flags
       if (lane == 0) sFlag[wave] = busy ? 1 : 0;
@@ -612,12 +612,12 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
         float* sSig = sC + wave * 256;
         if (busy) {
           float dLds_j, dLdc_j[3];
-          composite_tile<TAPS>(a, sSig, sSig + 64, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
+          composite_tile<TAPS, SC>(a, sSig, sSig + 64, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
           sSig[lane] = dLds_j;
           sSig[64 + 3 * lane] = dLdc_j[0];
           sSig[64 + 3 * lane + 1] = dLdc_j[1];
           sSig[64 + 3 * lane + 2] = dLdc_j[2];
-        } else if ((lane & (a.S - 1)) == 0 && CL.vj) {
+        } else if ((lane & ((SC > 0 ? SC : a.S) - 1)) == 0 && CL.vj) {
           // every alpha is 0: T = 1 and the colour is the background
           float bg[3];
           background(a, CL.rj, train, bg);
@@ -808,34 +808,34 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED>
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
 static hipError_t launch16_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch16<LF, ND, NC>;
   const size_t lds = A::lds_bytes();
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED, SC>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED, SC>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
-template <int LF, int ND, int NC, bool MARCHED>
+template <int LF, int ND, int NC, bool MARCHED, int SC>
 static hipError_t launch16_t(const MlpArgs& a, int n_blocks, hipStream_t st) {
   const bool taps = taps_requested(a);
   switch (a.c.F) {
     case 1:
-      return taps ? launch16_f<LF, ND, NC, 1, true, MARCHED>(a, n_blocks, st)
-                  : launch16_f<LF, ND, NC, 1, false, MARCHED>(a, n_blocks, st);
+      return taps ? launch16_f<LF, ND, NC, 1, true, MARCHED, SC>(a, n_blocks, st)
+                  : launch16_f<LF, ND, NC, 1, false, MARCHED, SC>(a, n_blocks, st);
     case 2:
-      return taps ? launch16_f<LF, ND, NC, 2, true, MARCHED>(a, n_blocks, st)
-                  : launch16_f<LF, ND, NC, 2, false, MARCHED>(a, n_blocks, st);
+      return taps ? launch16_f<LF, ND, NC, 2, true, MARCHED, SC>(a, n_blocks, st)
+                  : launch16_f<LF, ND, NC, 2, false, MARCHED, SC>(a, n_blocks, st);
     case 4:
-      return taps ? launch16_f<LF, ND, NC, 4, true, MARCHED>(a, n_blocks, st)
-                  : launch16_f<LF, ND, NC, 4, false, MARCHED>(a, n_blocks, st);
+      return taps ? launch16_f<LF, ND, NC, 4, true, MARCHED, SC>(a, n_blocks, st)
+                  : launch16_f<LF, ND, NC, 4, false, MARCHED, SC>(a, n_blocks, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -936,7 +936,8 @@ bool mlp16_supported(int LF, int nd, int nc) {
 
 hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
 #define X(l, d, n) \
-  if (LF == l && nd == d && nc == n) return launch16_t<l, d, n, false>(a, n_blocks, st);
+  if (LF == l && nd == d && nc == n)                                                     \
+    return a.S == 64 ? launch16_t<l, d, n, false, 64>(a, n_blocks, st) : launch16_t<l, d, n, false, 0>(a, n_blocks, st);
   FFN_MLP16_CONFIGS(X)
 #undef X
   return hipErrorInvalidValue;
@@ -944,7 +945,7 @@ hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, 
 
 hipError_t launch_mlp16_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
 #define X(l, d, n) \
-  if (LF == l && nd == d && nc == n) return launch16_t<l, d, n, true>(a, n_blocks, st);
+  if (LF == l && nd == d && nc == n) return launch16_t<l, d, n, true, 0>(a, n_blocks, st);
   FFN_MLP16_CONFIGS(X)
 #undef X
   return hipErrorInvalidValue;

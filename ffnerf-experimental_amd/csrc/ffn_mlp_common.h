@@ -54,9 +54,13 @@ __device__ __forceinline__ void occ_grid_pos(const DevCfg& c, const float (&o)[3
   }
 }
 
-// prop_wave: this wavefront makes the tile's occupancy proposals (one wavefront per tile, all 64 lanes)
+// prop_wave: this wavefront makes the tile's occupancy proposals (one wavefront per tile, all 64 lanes).
+// SC: the samples per ray when fixed at compile time (64, the benchmark's), else 0 and a.S at run time; a
+// fixed S turns the segment logic of the compositing's scans into constants.
+template <int SC>
 __device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t tile, int lane, bool prop_wave,
                                                    uint64_t n_samples, int log2S, bool proposals) {
+  const int S = SC > 0 ? SC : a.S;
   CompLane L;
   L.bj = tile * 64 + lane;
   L.vj = (uint64_t)L.bj < n_samples;
@@ -70,7 +74,7 @@ __device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t til
   if (proposals && L.vj) {
     L.t_j = a.Ts[L.bj];
     L.segmask = (uint64_t)a.flags[2 * L.rj] | ((uint64_t)a.flags[2 * L.rj + 1] << 32);
-    const int lid = lane & (a.S - 1);
+    const int lid = lane & (S - 1);
     if (((L.segmask >> lid) & 1ull) && L.dt_j > 0.0f && prop_wave) {
       const float4 ro = a.rays[2 * L.rj], rdv = a.rays[2 * L.rj + 1];
       const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
@@ -134,13 +138,13 @@ __device__ __forceinline__ Seg comp_seg_prefix(Seg v, int lane, int S, Seg* tota
 // output colour (wavefront 0), taps (wavefront 0) and, on the tile's proposal wavefront, the occupancy
 // proposals of all its samples; returns dL/dsigma and dL/dc of lane j's sample.  sSig/sRgb hold
 // sigma[64] and rgb[64][3] of the tile.
-template <bool TAPS>
+template <bool TAPS, int SC>
 __device__ __forceinline__ void composite_tile(const MlpArgs& a, const float* __restrict__ sSig,
                                                const float* __restrict__ sRgb, const CompLane& L, int lane,
                                                int wave, bool prop_wave, bool train, bool proposals, float Dhalf,
                                                float& dLds_j, float (&dLdc_j)[3]) {
   const DevCfg& c = a.c;
-  const int S = a.S;
+  const int S = SC > 0 ? SC : a.S;
   const int64_t bj = L.bj, rj = L.rj;
   const bool vj = L.vj;
   const float dt_j = L.dt_j, t_j = L.t_j;
@@ -367,10 +371,10 @@ __device__ __forceinline__ void store_enc_grad(const MlpArgs& a, int64_t b, int 
 // the background (every alpha is 0, so T = 1 and the colour sum is 0) and every gradient of its samples is
 // zero; this writes what the full path would write for it -- the rays' colours and zero encoding
 // gradients -- so the MLP can be skipped.  Taps, which expose per-sample MLP outputs, take the full path.
-template <int LF, int FEAT>
+template <int LF, int FEAT, int SC>
 __device__ __forceinline__ void empty_tile(const MlpArgs& a, const CompLane& L, int lane, int wave, int64_t b,
                                            bool valid, bool train, int g) {
-  const int lid = lane & (a.S - 1);
+  const int lid = lane & ((SC > 0 ? SC : a.S) - 1);
   if (wave == 0 && lid == 0 && L.vj) {
     float bg[3];
     background(a, L.rj, train, bg);
