@@ -395,8 +395,8 @@ def run_marched_train(args, pool_rays, pool_tg, mlp="fp32"):
             "stages_ms_avg": {k: round(v, 4) for k, v in avg.items()},
             "hash_grid_gbs": (fwd_b + bwd_b) * n_avg / ((avg["hash_fwd"] + avg["hash_bwd"]) * 1e-3) / 1e9,
             "config": "cfg2 model and ray batches (ball scene), 256^3 bitfield of the ball (r 0.25 + one cell "
-                      "diagonal), dt sqrt(3)/1024, <= 1024 samples/ray, T_stop 1e-4; stage 'march' = march count, "
-                      "scan, host wait, emit; 'mlp' = forward, compositing, backward"}
+                      "diagonal), dt sqrt(3)/1024, <= 1024 samples/ray, T_stop 1e-4; stage 'march' = one walk into "
+                      "per-ray slots, scan, host wait, pack; 'mlp' = forward, compositing, backward"}
 
 
 def run_cfg4(args):

@@ -82,6 +82,7 @@ struct Handle {
   // marched training
   Scratch m_Tr, m_dLds, m_dLdc;
   Scratch m_bits;  // the bitfield of ffn_train_step's march sampler
+  Scratch m_slots;  // the marched step's per-ray sample slots (one walk instead of count + emit)
   uint32_t* host_total = nullptr;  // pinned
 };
 
@@ -90,6 +91,15 @@ size_t bin_budget_bytes() {
   const char* e = getenv("FFN_BIN_BUDGET_MB");
   long long mb = e ? atoll(e) : 32768;
   if (mb < 64) mb = 64;
+  if (mb > (1ll << 22)) mb = 1ll << 22;
+  return (size_t)mb << 20;
+}
+
+// Per-ray slot budget of the marched step: FFN_MARCH_SLOT_BUDGET_MB (MiB, default 8 GiB; 0 walks twice)
+size_t march_slot_budget_bytes() {
+  const char* e = getenv("FFN_MARCH_SLOT_BUDGET_MB");
+  long long mb = e ? atoll(e) : 8192;
+  if (mb < 0) mb = 0;
   if (mb > (1ll << 22)) mb = 1ll << 22;
   return (size_t)mb << 20;
 }
@@ -356,7 +366,8 @@ int ffn_destroy(void* handle) {
   h->bin_pairs.release();
   h->bin_max.release();
   for (Scratch* sc : {&h->m_state, &h->m_acc, &h->m_counts, &h->m_offsets, &h->m_sums, &h->m_total, &h->m_samples,
-                      &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb, &h->m_Tr, &h->m_dLds, &h->m_dLdc})
+                      &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb, &h->m_Tr, &h->m_dLds, &h->m_dLdc, &h->m_bits,
+                      &h->m_slots})
     sc->release();
   if (h->host_total) (void)hipHostFree(h->host_total);
   delete h;
@@ -761,7 +772,10 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   hipStream_t st = (hipStream_t)stream;
   const ffn_params& P = h->params;
 
-  // 1. march: count, scan (the step's sample count comes back to size the launches), emit
+  // 1. march.  With room for max_steps samples per ray, one walk writes each ray's samples to its own slots
+  // and its count; the scan of the counts sizes the step (its total comes back to the host) and a copy packs
+  // the slots into the scanned order.  Otherwise the walk runs twice: count, scan, emit to the scanned slots.
+  // Both give the same samples in the same order.
   const size_t n1 = (size_t)num_rays + 1;
   FFN_HIP(h->m_counts.ensure(sizeof(uint32_t) * n1));
   FFN_HIP(h->m_offsets.ensure(sizeof(uint32_t) * n1));
@@ -775,18 +789,34 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   int64_t n = 0;
   {
     StageTimer tm(h, 0, st);
-    FFN_HIP(ffn::launch_march(ma, false, st));
+    const uint64_t slot_n = (uint64_t)num_rays * mp->max_steps;
+    const bool one_walk = slot_n * sizeof(float4) <= march_slot_budget_bytes();
+    if (one_walk) {
+      FFN_HIP(h->m_slots.ensure(sizeof(float4) * (size_t)slot_n));
+      ma.slot_stride = mp->max_steps;
+      ma.samples = (float4*)h->m_slots.p;
+      ma.ray_ids = nullptr;
+      ma.capacity = slot_n;
+      FFN_HIP(ffn::launch_march(ma, true, st));
+    } else {
+      FFN_HIP(ffn::launch_march(ma, false, st));
+    }
     FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, (uint32_t*)h->m_total.p, st));
     FFN_HIP(hipMemcpyAsync(h->host_total, h->m_total.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     FFN_HIP(hipStreamSynchronize(st));
     n = *h->host_total;
     FFN_HIP(h->m_samples.ensure(sizeof(float4) * (size_t)(n > 0 ? n : 1)));
     FFN_HIP(h->m_ids.ensure(sizeof(uint32_t) * (size_t)(n > 0 ? n : 1)));
-    ma.offsets = off;
-    ma.samples = (float4*)h->m_samples.p;
-    ma.ray_ids = (uint32_t*)h->m_ids.p;
-    ma.capacity = (uint64_t)n;
-    FFN_HIP(ffn::launch_march(ma, true, st));
+    if (one_walk) {
+      FFN_HIP(ffn::launch_march_compact(counts, off, (const float4*)h->m_slots.p, mp->max_steps, num_rays,
+                                        (float4*)h->m_samples.p, (uint32_t*)h->m_ids.p, st));
+    } else {
+      ma.offsets = off;
+      ma.samples = (float4*)h->m_samples.p;
+      ma.ray_ids = (uint32_t*)h->m_ids.p;
+      ma.capacity = (uint64_t)n;
+      FFN_HIP(ffn::launch_march(ma, true, st));
+    }
   }
   const float4* smp = (const float4*)h->m_samples.p;
   const uint32_t* ids = (const uint32_t*)h->m_ids.p;

@@ -192,10 +192,16 @@ struct MarchArgs {
   float4* samples;           // emit pass: {x, y, z, t}
   uint32_t* ray_ids;         // emit pass
   uint64_t capacity;         // slots of samples / ray_ids
+  uint32_t slot_stride;      // emit pass into per-ray slots: ray r's samples at r * slot_stride (and its count
+                             // written as the count pass does); 0: at offsets[r]
 };
 
 hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint32_t* bits, hipStream_t st);
 hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st);
+// per-ray slots (ray r's counts[r] samples at slots + r * stride) -> the compacted order (offsets), with ray ids
+hipError_t launch_march_compact(const uint32_t* counts, const uint32_t* offsets, const float4* slots,
+                                uint32_t stride, uint32_t num_rays, float4* samples, uint32_t* ray_ids,
+                                hipStream_t st);
 hipError_t launch_march_init(MarchState* state, float4* acc, uint32_t* n_used, uint32_t num_rays, hipStream_t st);
 hipError_t launch_render_composite(const uint32_t* offsets, const uint32_t* counts, uint32_t num_rays,
                                    const float* sigma, const float* rgb, float dt, float T_stop, MarchState* state,

@@ -77,7 +77,7 @@ struct RayWalk {
     const float4 ro = a.rays[2 * (size_t)r], rd = a.rays[2 * (size_t)r + 1];
     o[0] = ro.x; o[1] = ro.y; o[2] = ro.z;
     d[0] = rd.x; d[1] = rd.y; d[2] = rd.z;
-    base = EMIT ? (uint64_t)a.offsets[r] : 0;
+    base = EMIT ? (a.slot_stride ? (uint64_t)r * a.slot_stride : (uint64_t)a.offsets[r]) : 0;
     float ta, tb;
     if (!ray_aabb(o, d, a.bmin, a.bmax, ta, tb)) {
       done = true;
@@ -149,7 +149,7 @@ struct RayWalk {
           const uint64_t slot = base + emitted;
           if (slot < a.capacity) {
             a.samples[slot] = make_float4(o[0] + tk * d[0], o[1] + tk * d[1], o[2] + tk * d[2], tk);
-            a.ray_ids[slot] = r;
+            if (a.ray_ids) a.ray_ids[slot] = r;
           }
         }
         ++emitted;
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256) void k_march(MarchArgs a) {
       if (rr < r_end) {
         if (w.start(a, rr, cell)) {
           have = true;
-        } else if (!EMIT) {
+        } else if (!EMIT || a.slot_stride) {
           a.counts[rr] = 0u;
         }
       }
@@ -241,9 +241,27 @@ __global__ __launch_bounds__(256) void k_march(MarchArgs a) {
     for (int j = 0; j < MARCH_CELLS_PER_CLAIM; ++j) {
       if (have && w.advance(a, cell)) {
         w.finish_state(a, true);
-        if (!EMIT) a.counts[w.r] = w.emitted;
+        if (!EMIT || a.slot_stride) a.counts[w.r] = w.emitted;
         have = false;
       }
+    }
+  }
+}
+
+// One wavefront per ray at a time: the ray's samples from its slots to its compacted range, 64 at a time
+__global__ __launch_bounds__(256) void k_march_compact(const uint32_t* __restrict__ counts,
+                                                       const uint32_t* __restrict__ offsets,
+                                                       const float4* __restrict__ slots, uint32_t stride,
+                                                       uint32_t num_rays, float4* __restrict__ samples,
+                                                       uint32_t* __restrict__ ray_ids) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t n_waves = gridDim.x * (blockDim.x >> 6);
+  for (uint32_t r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < num_rays; r += n_waves) {
+    const uint32_t c = counts[r], o = offsets[r];
+    const float4* src = slots + (uint64_t)r * stride;
+    for (uint32_t k = lane; k < c; k += 64) {
+      samples[(uint64_t)o + k] = src[k];
+      ray_ids[(uint64_t)o + k] = r;
     }
   }
 }
@@ -387,6 +405,16 @@ hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st) {
     hipLaunchKernelGGL(k_march<true>, grid, block, 0, st, a);
   else
     hipLaunchKernelGGL(k_march<false>, grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_march_compact(const uint32_t* counts, const uint32_t* offsets, const float4* slots,
+                                uint32_t stride, uint32_t num_rays, float4* samples, uint32_t* ray_ids,
+                                hipStream_t st) {
+  if (num_rays == 0) return hipSuccess;
+  const uint32_t blocks = (num_rays + 3) / 4 < 4096 ? (num_rays + 3) / 4 : 4096;
+  hipLaunchKernelGGL(k_march_compact, dim3(blocks), dim3(256), 0, st, counts, offsets, slots, stride, num_rays,
+                     samples, ray_ids);
   return hipGetLastError();
 }
 

@@ -129,3 +129,30 @@ def test_train_step_with_the_march_sampler(gh, ora, mlp):
     out_r, _ = a.train_step(rays, tg, 64, dict(sc, do_train=0))
     ref, _ = b.render(rays, bits, fl.march_params(R, DT, 128, T_stop=1e-2, chunk=32))
     np.testing.assert_array_equal(out_r, ref)
+
+
+@pytest.mark.parametrize("mlp", [0, 1])
+def test_one_walk_march_equals_the_two_walk_march(gh, ora, mlp, monkeypatch):
+    """The marched step walks each ray once into per-ray slots and packs them when num_rays * max_steps
+    samples fit FFN_MARCH_SLOT_BUDGET_MB, else walks twice (count, emit): the same step, bit for bit."""
+    print(f"[case] one-walk vs two-walk march, mlp_precision={mlp}", flush=True)
+    import ffn_lib as fl
+    spec = spec_cfg0(occ_G=R // 2, hash_opt=1, mlp_precision=mlp)
+    p = random_params(spec, seed=71)
+    p["bd_out"][0] = 8.0
+    rays = look_at_rays(512, spec, seed=72, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    bits = shell_bits(R, seed=73, frac=0.2)
+    mp = fl.march_params(R, DT, 128, T_stop=1e-2)
+    sc = default_scalars(rng_seed=74, occ_strength=0.0)
+    res = []
+    for budget in ("8192", "0"):
+        monkeypatch.setenv("FFN_MARCH_SLOT_BUDGET_MB", budget)
+        m = gh.GpuModel(spec, p)
+        out, used, G = m.train_step_marched(rays, tg, bits, mp, sc)
+        res.append((out, used, G["n_march"], m.state()))
+    assert res[0][2].sum() > 2000
+    for a, b in zip(res[0][:3], res[1][:3]):
+        np.testing.assert_array_equal(a, b)
+    for k in res[0][3]:
+        np.testing.assert_array_equal(res[0][3][k], res[1][3][k], err_msg=k)
