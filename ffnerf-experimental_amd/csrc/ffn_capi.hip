@@ -1022,16 +1022,30 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
     w.W[k] = h->params.W[k];
     w.b[k] = h->params.b[k];
   }
+  // Each round walks every live ray once into its own chunk of slots (its count and walk state written by the
+  // same pass), then packs the slots into the scanned order; without room for the slots (the budget of the
+  // marched step) it walks twice, count then emit.  The samples, their order and the walk states agree.
+  const bool one_walk = cap * sizeof(float4) <= march_slot_budget_bytes();
+  if (one_walk) FFN_HIP(h->m_slots.ensure(sizeof(float4) * cap));
+  ffn::MarchArgs a1 = a;
+  a1.slot_stride = mp->chunk;
+  a1.samples = (float4*)h->m_slots.p;
+  a1.ray_ids = nullptr;
   int n_blocks = h->n_cu > 0 ? 2 * h->n_cu : 512;
   const uint32_t rounds = (mp->max_steps + mp->chunk - 1) / mp->chunk;
   for (uint32_t round = 0; round < rounds; ++round) {
-    FFN_HIP(ffn::launch_march(a, false, st));
+    FFN_HIP(ffn::launch_march(one_walk ? a1 : a, one_walk, st));
     FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, total, st));
     FFN_HIP(hipMemcpyAsync(h->host_total, total, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     FFN_HIP(hipStreamSynchronize(st));
     const int64_t n = *h->host_total;
     if (n == 0) break;
-    FFN_HIP(ffn::launch_march(a, true, st));
+    if (one_walk) {
+      FFN_HIP(ffn::launch_march_compact(counts, off, (const float4*)h->m_slots.p, mp->chunk, num_rays, samples, ids,
+                                        st));
+    } else {
+      FFN_HIP(ffn::launch_march(a, true, st));
+    }
     ffn::PosSrc src{(const float*)samples, nullptr, nullptr, 0};
     src.x_stride = 4;
     const ffn::FeatLayout feat = ffn::level_major(n, h->dc.F);

@@ -16,8 +16,11 @@
 //   * One lane per ray.  Empty cells are skipped in one step: the first lattice
 //     index past the cell's exit is computed directly and corrected to the exact
 //     index the one-by-one walk of the specification reaches.
-//   * Compaction is two passes over the same deterministic walk: count, scan,
-//     emit to the scanned slots.  A chunked variant keeps a 16-byte state per
+//   * Compaction: one walk writes each ray's samples to its own fixed run of
+//     slots (max_steps, or the chunk, per ray) and its count; a scan of the
+//     counts and a wavefront-per-ray copy pack them.  Where those slots do not
+//     fit, two passes over the same deterministic walk: count, scan, emit to the
+//     scanned slots.  A chunked variant keeps a 16-byte state per
 //     ray so that the render can march, shade and composite a few samples per
 //     ray per round and retire rays whose transmittance fell below T_stop.
 #include "ffn_device.h"

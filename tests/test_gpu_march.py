@@ -108,3 +108,25 @@ def test_render_matches_oracle():
         if T_stop > 0.1:
             assert np.any(used_ref < [len(ora.march_ray(model.cfg, ora.march_cfg(R, dt, 512), bits, r))
                                       for r in rays])
+
+
+def test_render_one_walk_equals_two_walks(monkeypatch):
+    """Each render round walks its rays once into per-ray chunks of slots when num_rays * chunk samples fit
+    FFN_MARCH_SLOT_BUDGET_MB, else counts then emits: the same image and samples used, bit for bit."""
+    import ffn_lib as fl
+    from gpu_helpers import GpuModel
+    p = random_params(SPEC, seed=5)
+    p["bd_out"][0] = 6.0
+    R = 32
+    bits = shell_bits(R, seed=9, frac=0.05)
+    rays = look_at_rays(700, SPEC, seed=33, miss_frac=0.05)
+    dt = np.float32(np.sqrt(3.0) / 128)
+    for chunk in (16, 512):
+        print(f"[render one/two walks] chunk={chunk}", flush=True)
+        res = []
+        for budget in ("8192", "0"):
+            monkeypatch.setenv("FFN_MARCH_SLOT_BUDGET_MB", budget)
+            res.append(GpuModel(SPEC, p).render(rays, bits, fl.march_params(R, dt, 512, T_stop=1e-2, chunk=chunk)))
+        np.testing.assert_array_equal(res[0][0], res[1][0])
+        np.testing.assert_array_equal(res[0][1], res[1][1])
+        assert res[0][1].sum() > 2000
