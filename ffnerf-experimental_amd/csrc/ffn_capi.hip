@@ -86,27 +86,49 @@ struct Handle {
   uint32_t* host_total = nullptr;  // pinned
 };
 
-// Pair-buffer budget of the scatter: FFN_BIN_BUDGET_MB (MiB, clamped to [64, 2^22]), default 32 GiB
-size_t bin_budget_bytes() {
+// A scratch buffer may grow to `need` bytes when it is no larger than what it already holds plus half of the
+// device memory free now, so that other allocations of the process (a second handle, torch's cache) keep room
+bool growth_fits_free(const Scratch& held, size_t need) {
+  if (need <= held.bytes) return true;
+  size_t fr = 0, tot = 0;
+  if (hipMemGetInfo(&fr, &tot) != hipSuccess) return true;  // unknown: let the allocation itself decide
+  return need <= held.bytes + fr / 2;
+}
+
+// Pair-buffer budget of the scatter: FFN_BIN_BUDGET_MB (MiB, clamped to [64, 2^22]) when set, else 32 GiB
+// limited by growth_fits_free (the levels are then split into more groups)
+size_t bin_budget_bytes(bool* from_env) {
   const char* e = getenv("FFN_BIN_BUDGET_MB");
+  *from_env = e != nullptr;
   long long mb = e ? atoll(e) : 32768;
   if (mb < 64) mb = 64;
   if (mb > (1ll << 22)) mb = 1ll << 22;
   return (size_t)mb << 20;
 }
 
-// Per-ray slot budget of the marched step: FFN_MARCH_SLOT_BUDGET_MB (MiB, default 8 GiB; 0 walks twice)
-size_t march_slot_budget_bytes() {
+// Per-ray slot budget of the marched step and render: FFN_MARCH_SLOT_BUDGET_MB (MiB, default 8 GiB, limited by
+// growth_fits_free; 0 walks twice)
+bool march_slots_fit(const Scratch& held, size_t need) {
   const char* e = getenv("FFN_MARCH_SLOT_BUDGET_MB");
   long long mb = e ? atoll(e) : 8192;
   if (mb < 0) mb = 0;
   if (mb > (1ll << 22)) mb = 1ll << 22;
-  return (size_t)mb << 20;
+  return need <= ((size_t)mb << 20) && growth_fits_free(held, need);
 }
 
 // size the bucketed-scatter scratch for n samples and fill the views
 hipError_t ensure_bins(Handle* h, int64_t n, ffn::BinPlan* plan, ffn::BinScratch* s) {
-  *plan = ffn::plan_bins(h->dc, n, bin_budget_bytes());
+  bool from_env = false;
+  const size_t budget = bin_budget_bytes(&from_env);
+  const size_t pair_bytes = 2 + 4 * (size_t)h->dc.F;
+  *plan = ffn::plan_bins(h->dc, n, budget);
+  if (!from_env && !growth_fits_free(h->bin_pairs, pair_bytes * (size_t)plan->max_pairs)) {
+    size_t fr = 0, tot = 0;
+    if (hipMemGetInfo(&fr, &tot) == hipSuccess) {
+      const size_t cap = h->bin_pairs.bytes + fr / 2;
+      *plan = ffn::plan_bins(h->dc, n, cap < ((size_t)64 << 20) ? ((size_t)64 << 20) : cap);
+    }
+  }
   hipError_t e;
   if ((e = h->bin_meta.ensure(sizeof(uint32_t) * (size_t)plan->meta_elems)) != hipSuccess) return e;
   if ((e = h->bin_meta_t.ensure(sizeof(uint32_t) * (size_t)plan->meta_elems)) != hipSuccess) return e;
@@ -790,7 +812,7 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   {
     StageTimer tm(h, 0, st);
     const uint64_t slot_n = (uint64_t)num_rays * mp->max_steps;
-    const bool one_walk = slot_n * sizeof(float4) <= march_slot_budget_bytes();
+    const bool one_walk = march_slots_fit(h->m_slots, slot_n * sizeof(float4));
     if (one_walk) {
       FFN_HIP(h->m_slots.ensure(sizeof(float4) * (size_t)slot_n));
       ma.slot_stride = mp->max_steps;
@@ -1025,7 +1047,7 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   // Each round walks every live ray once into its own chunk of slots (its count and walk state written by the
   // same pass), then packs the slots into the scanned order; without room for the slots (the budget of the
   // marched step) it walks twice, count then emit.  The samples, their order and the walk states agree.
-  const bool one_walk = cap * sizeof(float4) <= march_slot_budget_bytes();
+  const bool one_walk = march_slots_fit(h->m_slots, cap * sizeof(float4));
   if (one_walk) FFN_HIP(h->m_slots.ensure(sizeof(float4) * cap));
   ffn::MarchArgs a1 = a;
   a1.slot_stride = mp->chunk;

@@ -1,9 +1,9 @@
 // ffn_mlp16.hip -- the fused MLP step on 16-bit MFMAs with fp32 accumulation:
 // forward and backward chains in fp16, weight gradients in bf16 (whose
 // fp32-sized exponent takes the unscaled deltas of all four wavefronts); each
-// layer's fp16 deltas are scaled by a per-wavefront power of two that puts
-// their largest magnitude just below 2^14, so small deltas neither underflow
-// nor lose bits.  Same semantics as the fp32 kernel (ffnerf_OG.cl:1373-2082,
+// layer's fp16 deltas are scaled by a per-sample power of two that puts their
+// largest magnitude just below 2^14, so small deltas neither underflow nor
+// lose bits.  Same semantics as the fp32 kernel (ffnerf_OG.cl:1373-2082,
 // weight_update.cl:210-341): compositing, loss gradient, proposals and output
 // deltas are the shared fp32 code.
 //
@@ -35,6 +35,9 @@
 //     accumulates its tiles over the tile's 64 samples (two K = 32 MFMAs per
 //     tile) in registers for the whole kernel and stores them into the
 //     block's partial at the end.
+//   * The backward's fp16 deltas are scaled per sample (the column of the
+//     next MFMA's B operand) by the power of two that puts the sample's
+//     largest delta in [2^13, 2^14).
 #include "ffn_device.h"
 #include "ffn_kernels.h"
 #include "ffn_mlp_common.h"
@@ -43,6 +46,7 @@ namespace ffn {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -79,6 +83,15 @@ __device__ __forceinline__ half8 to_half8(const floatx4& lo, const floatx4& hi) 
   }
   return h;
 }
+// the same K block in bf16 (two values per v_cvt_pk_bf16_f32)
+__device__ __forceinline__ bf16x8 to_bf16x8(const floatx4& lo, const floatx4& hi) {
+  typedef float float2_ __attribute__((ext_vector_type(2)));
+  const bf16x2 p0 = __builtin_convertvector(float2_{lo[0], lo[1]}, bf16x2);
+  const bf16x2 p1 = __builtin_convertvector(float2_{lo[2], lo[3]}, bf16x2);
+  const bf16x2 p2 = __builtin_convertvector(float2_{hi[0], hi[1]}, bf16x2);
+  const bf16x2 p3 = __builtin_convertvector(float2_{hi[2], hi[3]}, bf16x2);
+  return bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
 __device__ __forceinline__ half8 join8(const half4& lo, const half4& hi) {
   return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
@@ -89,27 +102,32 @@ __device__ __forceinline__ bf16x4 to_bf16x4(const floatx4& v) {
   return h;
 }
 
-// power of two that maps the largest |d| of the wavefront's tiles into [2^13, 2^14) (1 if all zero)
+// power of two per sample (column of the next backward MFMA's B operand, whose K values the sample's four
+// lanes l, l ^ 16, l ^ 32, l ^ 48 hold) that maps the largest |d| of its deltas into [2^13, 2^14) (1 if all
+// zero); *inv its reciprocal
 template <int NT>
-__device__ __forceinline__ float delta_scale(const floatx4 (&d)[NT]) {
+__device__ __forceinline__ float delta_scale(const floatx4 (&d)[NT], float* inv) {
   float m = 0.0f;
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(d[t][r]));
-  m = wave_max_nonneg(m);
-  if (!(m > 0.0f) || !(m < 3.0e38f)) return 1.0f;
-  int e;
-  frexpf(m, &e);  // m < 2^e
-  e = 14 - e;
-  e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  {
+    const unsigned int u = __float_as_uint(m);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const float m2 = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    const unsigned int u2 = __float_as_uint(m2);
+    const auto q = __builtin_amdgcn_permlane16_swap(u2, u2, false, false);
+    m = fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+  }
+  int e = 0;
+  if (m > 0.0f && m < 3.0e38f) {
+    frexpf(m, &e);  // m < 2^e
+    e = 14 - e;
+    e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  }
+  *inv = ldexpf(1.0f, -e);
   return ldexpf(1.0f, e);
-}
-// 1 / sc exactly (sc a power of two)
-__device__ __forceinline__ float inv_pow2(float sc) {
-  int e;
-  frexpf(sc, &e);  // sc = 2^(e - 1)
-  return ldexpf(1.0f, 1 - e);
 }
 
 template <int LF_, int ND_, int NC_>
@@ -173,12 +191,14 @@ __device__ __forceinline__ void fwd_k32(const _Float16* __restrict__ W, int P, c
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[t][r] = B[16 * t + 4 * g + r];
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb)
+  for (int kb = 0; kb < KB; ++kb) {
+    half8 w[OT];  // the K block's weight operands, all read before its MFMAs
 #pragma unroll
-    for (int t = 0; t < OT; ++t) {
-      const half8 w = *reinterpret_cast<const half8*>(W + (16 * t + s) * P + 32 * kb + 8 * g);
-      acc[t] = mfma_k32(w, in[kb], acc[t]);
-    }
+    for (int t = 0; t < OT; ++t) w[t] = *reinterpret_cast<const half8*>(W + (16 * t + s) * P + 32 * kb + 8 * g);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < OT; ++t) acc[t] = mfma_k32(w[t], in[kb], acc[t]);
+  }
 #pragma unroll
   for (int t = 0; t < OT; ++t) {
     if (relu) {
@@ -193,13 +213,16 @@ __device__ __forceinline__ void fwd_k32(const _Float16* __restrict__ W, int P, c
 template <int OT>
 __device__ __forceinline__ void fwd_k16(const _Float16* __restrict__ W, int P, const float* __restrict__ B,
                                         const half4& in, floatx4 (&out)[OT], int g, int s, bool relu) {
+  half4 w[OT];  // every weight operand read before the MFMAs
+#pragma unroll
+  for (int t = 0; t < OT; ++t) w[t] = *reinterpret_cast<const half4*>(W + (16 * t + s) * P + 4 * g);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < OT; ++t) {
     floatx4 acc;
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = B[16 * t + 4 * g + r];
-    const half4 w = *reinterpret_cast<const half4*>(W + (16 * t + s) * P + 4 * g);
-    acc = mfma_k16(w, in, acc);
+    acc = mfma_k16(w[t], in, acc);
     if (relu) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
@@ -208,53 +231,66 @@ __device__ __forceinline__ void fwd_k16(const _Float16* __restrict__ W, int P, c
   }
 }
 
-// backward layer over a 64-wide output (K = 32 blocks): res tiles over input neurons += (W^T . op) / sc, with
-// Wt the K-ordered transposed copy and op the scaled fp16 deltas
-template <int RT>
-__device__ __forceinline__ void bwd_k32(const _Float16* __restrict__ Wt, int P, const half8 (&op)[2], float sc,
+// backward layer over a 64-wide output (K = 32 blocks): res tiles over input neurons += (W^T . op) / sc (= when
+// !ACC), with Wt the K-ordered transposed copy and op the scaled fp16 deltas
+template <int RT, bool ACC = true>
+__device__ __forceinline__ void bwd_k32(const _Float16* __restrict__ Wt, int P, const half8 (&op)[2], float inv,
                                         floatx4 (&res)[RT], int g, int s) {
   floatx4 acc[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < 2; ++kb) {
+    half8 w[RT];  // the K block's weight operands, all read before its MFMAs
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
-      const half8 w = *reinterpret_cast<const half8*>(Wt + (16 * t + s) * P + 32 * kb + 8 * g);
-      acc[t] = mfma_k32(w, op[kb], acc[t]);
-    }
-  const float inv = inv_pow2(sc);
+    for (int t = 0; t < RT; ++t) w[t] = *reinterpret_cast<const half8*>(Wt + (16 * t + s) * P + 32 * kb + 8 * g);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = mfma_k32(w[t], op[kb], acc[t]);
+  }
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) res[t][r] = res[t][r] + acc[t][r] * inv;
+    for (int r = 0; r < 4; ++r) res[t][r] = ACC ? res[t][r] + acc[t][r] * inv : acc[t][r] * inv;
 }
 
 // backward layer over a 16-wide output (K = 16): natural column order
-template <int RT>
-__device__ __forceinline__ void bwd_k16(const _Float16* __restrict__ Wt, int P, const half4& op, float sc,
+template <int RT, bool ACC = true>
+__device__ __forceinline__ void bwd_k16(const _Float16* __restrict__ Wt, int P, const half4& op, float inv,
                                         floatx4 (&res)[RT], int g, int s) {
-  const float inv = inv_pow2(sc);
+  half4 w[RT];  // every weight operand read before the MFMAs
+#pragma unroll
+  for (int t = 0; t < RT; ++t) w[t] = *reinterpret_cast<const half4*>(Wt + (16 * t + s) * P + 4 * g);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    const half4 w = *reinterpret_cast<const half4*>(Wt + (16 * t + s) * P + 4 * g);
-    const floatx4 acc = mfma_k16(w, op, floatx4{0.f, 0.f, 0.f, 0.f});
+    const floatx4 acc = mfma_k16(w[t], op, floatx4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-    for (int r = 0; r < 4; ++r) res[t][r] = res[t][r] + acc[r] * inv;
+    for (int r = 0; r < 4; ++r) res[t][r] = ACC ? res[t][r] + acc[r] * inv : acc[r] * inv;
   }
 }
 
-// zero the deltas of inactive ReLUs (act: the forward's fp16 activations, two tiles per K block)
-__device__ __forceinline__ void relu_mask(floatx4 (&d)[4], const half8 (&act)[2]) {
+// zero the deltas of inactive ReLUs (act: the forward's bf16 activations, two tiles per K block).  An
+// activation is +0 or positive (the ReLU maps everything else to +0), so it is active when its bits are not
+// all zero: tested on the packed words (low half: the low 16 bits; high half: the word above 0xffff)
+__device__ __forceinline__ void relu_mask(floatx4 (&d)[4], const bf16x8 (&act)[2]) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < 4; ++t) {
+    const u32x4 wv = __builtin_bit_cast(u32x4, act[t >> 1]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) d[t][r] = act[t >> 1][4 * (t & 1) + r] > (_Float16)0.0f ? d[t][r] : 0.0f;
+    for (int r = 0; r < 4; ++r) {
+      const unsigned int word = wv[(4 * (t & 1) + r) >> 1];
+      const bool on = (r & 1) ? word > 0xffffu : (unsigned short)word != 0;
+      d[t][r] = on ? d[t][r] : 0.0f;
+    }
+  }
 }
 
 // the next layer's operands from four delta tiles: scale and fp16 K blocks
 __device__ __forceinline__ float make_op4(const floatx4 (&d)[4], half8 (&op)[2]) {
-  const float sc = delta_scale<4>(d);
+  float inv;
+  const float sc = delta_scale<4>(d, &inv);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -262,27 +298,78 @@ __device__ __forceinline__ float make_op4(const floatx4 (&d)[4], half8 (&op)[2])
       op[kb][r] = (_Float16)(d[2 * kb][r] * sc);
       op[kb][4 + r] = (_Float16)(d[2 * kb + 1][r] * sc);
     }
-  return sc;
+  return inv;
 }
 __device__ __forceinline__ float make_op1(const floatx4 (&d)[1], half4& op) {
-  const float sc = delta_scale<1>(d);
+  float inv;
+  const float sc = delta_scale<1>(d, &inv);
 #pragma unroll
   for (int r = 0; r < 4; ++r) op[r] = (_Float16)(d[0][r] * sc);
-  return sc;
+  return inv;
 }
 
-// stash rows row0 + 16 t + 4 g + r, column `col`, of NT D-layout tiles (value(t, r))
+// stash rows row0 + 16 t + 4 g + r, column `col`, of NT D-layout tiles (value(t, r)); two values per
+// conversion (v_cvt_pk_bf16_f32), stored as the low and the high half of the packed word
 template <int NT, typename F>
 __device__ __forceinline__ void stash_rows(__bf16* __restrict__ st, int row0, int g, int col, F value) {
   constexpr int PS = 64 + 8;
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) st[(row0 + 16 * t + 4 * g + r) * PS + col] = (__bf16)value(t, r);
+    for (int r = 0; r < 4; r += 2) {
+      typedef float float2_ __attribute__((ext_vector_type(2)));
+      const bf16x2 p = __builtin_convertvector(float2_{value(t, r), value(t, r + 1)}, bf16x2);
+      const unsigned int w = __builtin_bit_cast(unsigned int, p);
+      unsigned short* row = reinterpret_cast<unsigned short*>(st + (row0 + 16 * t + 4 * g + r) * PS + col);
+      row[0] = (unsigned short)w;
+      row[PS] = (unsigned short)(w >> 16);
+    }
 }
 
-// Weight-gradient tiles of one layer held by one wavefront: tiles i = T * IT + Tp dealt round-robin,
-// wavefront w holding i = 4m + w (D layout) and a per-lane partial of the bias gradient when Tp = 0.
+// stash rows row0 + 16 t + 4 g + r, column `col`, of NT tiles given as packed bf16 words (word(t, r / 2)
+// holds rows r and r + 1): each word's halves go to two rows, no conversion
+template <int NT, typename F>
+__device__ __forceinline__ void stash_words(__bf16* __restrict__ st, int row0, int g, int col, F word) {
+  constexpr int PS = 64 + 8;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; r += 2) {
+      const unsigned int w = word(t, r >> 1);
+      unsigned short* row = reinterpret_cast<unsigned short*>(st + (row0 + 16 * t + 4 * g + r) * PS + col);
+      row[0] = (unsigned short)w;
+      row[PS] = (unsigned short)(w >> 16);
+    }
+}
+// NT bf16 tiles held two per K block (act[t / 2], slots 4 (t % 2) + r)
+template <int NT, int NB>
+__device__ __forceinline__ void stash_act(__bf16* __restrict__ st, int row0, int g, int col, const bf16x8 (&act)[NB]) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  stash_words<NT>(st, row0, g, col, [&](int t, int p) {
+    return __builtin_bit_cast(u32x4, act[t >> 1])[2 * (t & 1) + p];
+  });
+}
+
+// Weight-gradient tiles (T, Tp) of one layer (OT x IT tiles of 16x16) dealt over the four wavefronts:
+// wavefront w's m-th tile.  The tiles with Tp = 0 also sum the bias gradient, so they are spread: with
+// IT = 4 (or 2) every wavefront holds one Tp = 0 tile per four (two) of its tiles.
+template <int IT>
+__device__ __forceinline__ void deal_tile(int m, int wave, int& T, int& Tp) {
+  if constexpr (IT == 4) {
+    T = m;
+    Tp = (wave + m) & 3;
+  } else if constexpr (IT == 2) {
+    T = 2 * m + (wave >> 1);
+    Tp = (wave + (wave >> 1) + m) & 1;
+  } else {
+    static_assert(IT == 1, "16, 32 or 64 input neurons per layer");
+    T = 4 * m + wave;
+    Tp = 0;
+  }
+}
+
+// One wavefront's weight-gradient tiles of a layer (D layout) and, for its Tp = 0 tiles, a per-lane
+// partial of the bias gradient.
 template <int OT, int IT>
 struct WaveGrad16 {
   static constexpr int N = OT * IT / 4;
@@ -305,7 +392,8 @@ __device__ __forceinline__ void layer_dw(const __bf16* __restrict__ st, WaveGrad
                                          int s) {
 #pragma unroll
   for (int m = 0; m < WaveGrad16<OT, IT>::N; ++m) {
-    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    int T, Tp;
+    deal_tile<IT>(m, wave, T, Tp);
     const __bf16* drow = st + (16 * T + s) * PS + 8 * g;
     const __bf16* arow = st + (16 * (OT + Tp) + s) * PS + 8 * g;
     floatx4 c = acc.w[m];
@@ -330,7 +418,8 @@ __device__ __forceinline__ void flush_layer16(float* __restrict__ dst, int O, in
                                               int wave, int g, int s) {
 #pragma unroll
   for (int m = 0; m < WaveGrad16<OT, IT>::N; ++m) {
-    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    int T, Tp;
+    deal_tile<IT>(m, wave, T, Tp);
     const int col = 16 * Tp + s;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -380,80 +469,94 @@ __device__ __forceinline__ void load_a0(const float* __restrict__ a0, const Feat
 }
 
 // The network's forward for this wavefront's 16 samples: a0 (fp16 K blocks, or one K = 16 operand when
-// LF = 16) through the density net, [dout | SH] through the colour net.  Activations in fp16 K blocks
-// (hd, hc), the colour net's input as K block cin; rgb and the density head's first output for the lane.
+// LF = 16) through the density net, [dout | SH] through the colour net, each layer's input an fp16
+// operand.  With KEEP the hidden activations are also kept as bf16 K blocks (hd, hc; the colour net's
+// input cin), which the backward's ReLU masks and weight-gradient stash read; rgb and the density head's
+// first output for the lane.
 template <int LF, int ND, int NC>
 struct Fwd16 {
-  static constexpr int KA = LF >= 32 ? LF / 32 : 1;  // K blocks of the encoding
-  half8 a0k[KA];                                     // LF >= 32
-  half4 a0q;                                         // LF == 16
-  half8 hd[ND][2];
-  half8 cin;
-  half8 hc[NC][2];
+  bf16x8 hd[ND][2];
+  bf16x8 cin;
+  bf16x8 hc[NC][2];
   float rgb[3];
   float dout0;
 };
 
-template <int LF, int ND, int NC, typename A>
+template <int LF, int ND, int NC, typename A, bool KEEP>
 __device__ __forceinline__ void forward16(const _Float16* __restrict__ sWf, const float* __restrict__ sB,
                                           const float (&a0v)[LF / 4], const floatx4& sh, int g, int s,
                                           Fwd16<LF, ND, NC>& f) {
   floatx4 o[4];
   if constexpr (LF >= 32) {
+    half8 a0k[LF / 32];
 #pragma unroll
     for (int kb = 0; kb < LF / 32; ++kb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        f.a0k[kb][j] = (_Float16)a0v[8 * kb + j];          // neuron 32 kb + 4 g + j
-        f.a0k[kb][4 + j] = (_Float16)a0v[8 * kb + 4 + j];  // neuron 32 kb + 16 + 4 g + j
+        a0k[kb][j] = (_Float16)a0v[8 * kb + j];          // neuron 32 kb + 4 g + j
+        a0k[kb][4 + j] = (_Float16)a0v[8 * kb + 4 + j];  // neuron 32 kb + 16 + 4 g + j
       }
-    fwd_k32<4, LF / 32>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), f.a0k, o, g, s, true);
+    fwd_k32<4, LF / 32>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), a0k, o, g, s, true);
   } else {
+    half4 a0q;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.a0q[j] = (_Float16)a0v[j];
-    fwd_k16<4>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), f.a0q, o, g, s, true);
+    for (int j = 0; j < 4; ++j) a0q[j] = (_Float16)a0v[j];
+    fwd_k16<4>(sWf + A::wf_off(FFN_WD_IN), A::pf(FFN_WD_IN), sB + A::b_off(FFN_WD_IN), a0q, o, g, s, true);
   }
-  f.hd[0][0] = to_half8(o[0], o[1]);
-  f.hd[0][1] = to_half8(o[2], o[3]);
+  half8 x[2] = {to_half8(o[0], o[1]), to_half8(o[2], o[3])};  // the next layer's input
+  if constexpr (KEEP) {
+    f.hd[0][0] = to_bf16x8(o[0], o[1]);
+    f.hd[0][1] = to_bf16x8(o[2], o[3]);
+  }
 #pragma unroll
   for (int i = 1; i < ND; ++i) {
     const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
-    fwd_k32<4, 2>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), f.hd[i - 1], o, g, s, true);
-    f.hd[i][0] = to_half8(o[0], o[1]);
-    f.hd[i][1] = to_half8(o[2], o[3]);
+    fwd_k32<4, 2>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), x, o, g, s, true);
+    x[0] = to_half8(o[0], o[1]);
+    x[1] = to_half8(o[2], o[3]);
+    if constexpr (KEEP) {
+      f.hd[i][0] = to_bf16x8(o[0], o[1]);
+      f.hd[i][1] = to_bf16x8(o[2], o[3]);
+    }
   }
   floatx4 dout[1];
-  fwd_k32<1, 2>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), f.hd[ND - 1], dout, g, s,
-                false);
-  f.cin = to_half8(dout[0], sh);
+  fwd_k32<1, 2>(sWf + A::wf_off(FFN_WD_OUT), A::pf(FFN_WD_OUT), sB + A::b_off(FFN_WD_OUT), x, dout, g, s, false);
+  if constexpr (KEEP) f.cin = to_bf16x8(dout[0], sh);
   {
-    const half8 cin[1] = {f.cin};
+    const half8 cin[1] = {to_half8(dout[0], sh)};
     fwd_k32<4, 1>(sWf + A::wf_off(FFN_WC_IN), A::pf(FFN_WC_IN), sB + A::b_off(FFN_WC_IN), cin, o, g, s, true);
   }
-  f.hc[0][0] = to_half8(o[0], o[1]);
-  f.hc[0][1] = to_half8(o[2], o[3]);
+  x[0] = to_half8(o[0], o[1]);
+  x[1] = to_half8(o[2], o[3]);
+  if constexpr (KEEP) {
+    f.hc[0][0] = to_bf16x8(o[0], o[1]);
+    f.hc[0][1] = to_bf16x8(o[2], o[3]);
+  }
 #pragma unroll
   for (int i = 1; i < NC; ++i) {
     const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
-    fwd_k32<4, 2>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), f.hc[i - 1], o, g, s, true);
-    f.hc[i][0] = to_half8(o[0], o[1]);
-    f.hc[i][1] = to_half8(o[2], o[3]);
+    fwd_k32<4, 2>(sWf + A::wf_off(k), A::pf(k), sB + A::b_off(k), x, o, g, s, true);
+    x[0] = to_half8(o[0], o[1]);
+    x[1] = to_half8(o[2], o[3]);
+    if constexpr (KEEP) {
+      f.hc[i][0] = to_bf16x8(o[0], o[1]);
+      f.hc[i][1] = to_bf16x8(o[2], o[3]);
+    }
   }
   floatx4 co[1];
-  fwd_k32<1, 2>(sWf + A::wf_off(FFN_WC_OUT), A::pf(FFN_WC_OUT), sB + A::b_off(FFN_WC_OUT), f.hc[NC - 1], co, g, s,
-                false);
+  fwd_k32<1, 2>(sWf + A::wf_off(FFN_WC_OUT), A::pf(FFN_WC_OUT), sB + A::b_off(FFN_WC_OUT), x, co, g, s, false);
   f.rgb[0] = sigmoid_soft(co[0][0]);
   f.rgb[1] = sigmoid_soft(co[0][1]);
   f.rgb[2] = sigmoid_soft(co[0][2]);
   f.dout0 = dout[0][0];
 }
 
-// ReLU taps from fp16 K blocks (two tiles each)
-__device__ __forceinline__ void tap_relu8(uint32_t* rec, int h, const half8 (&act)[2], int g) {
-  half4 t4[4];
+// ReLU taps from bf16 K blocks (two tiles each)
+__device__ __forceinline__ void tap_relu8(uint32_t* rec, int h, const bf16x8 (&act)[2], int g) {
+  bf16x4 t4[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) t4[t] = half4{act[t >> 1][4 * (t & 1)], act[t >> 1][4 * (t & 1) + 1],
-                                            act[t >> 1][4 * (t & 1) + 2], act[t >> 1][4 * (t & 1) + 3]};
+  for (int t = 0; t < 4; ++t) t4[t] = bf16x4{act[t >> 1][4 * (t & 1)], act[t >> 1][4 * (t & 1) + 1],
+                                             act[t >> 1][4 * (t & 1) + 2], act[t >> 1][4 * (t & 1) + 3]};
   tap_relu(rec, h, t4, g);
 }
 
@@ -582,7 +685,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
 #pragma unroll
         for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
         Fwd16<LF, ND, NC> f;
-        forward16<LF, ND, NC, A>(sWf, sB, cur.a0v, sh, g, s, f);
+        forward16<LF, ND, NC, A, TAPS>(sWf, sB, cur.a0v, sh, g, s, f);
         if constexpr (TAPS) {
           if (a.t_relu) {
             uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
@@ -664,12 +767,16 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
 #pragma unroll
       for (int q = 0; q < LF / 4; ++q) a0v[q] = cur.a0v[q];
       Fwd16<LF, ND, NC> f;
-      forward16<LF, ND, NC, A>(sWf, sB, a0v, sh, g, s, f);
-      bf16x4 a0b[KB0];  // the encoding as the stash holds it (bf16 of the fp32 values)
+      forward16<LF, ND, NC, A, true>(sWf, sB, a0v, sh, g, s, f);
+      unsigned int a0w[KB0][2];  // the encoding as the stash holds it: bf16 of the fp32 values, packed in pairs
 #pragma unroll
       for (int t = 0; t < KB0; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) a0b[t][r] = (__bf16)a0v[4 * t + r];
+        for (int p = 0; p < 2; ++p) {
+          typedef float float2_ __attribute__((ext_vector_type(2)));
+          a0w[t][p] = __builtin_bit_cast(unsigned int, __builtin_convertvector(
+                                                           float2_{a0v[4 * t + 2 * p], a0v[4 * t + 2 * p + 1]}, bf16x2));
+        }
       float dLds, dLdc0, dLdc1, dLdc2;
       if constexpr (MARCHED) {
         dLds = valid ? a.in_dLds[b] : 0.0f;
@@ -708,13 +815,11 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       float dsc;
       floatx4 dc[4];
       stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return dco[t][r]; });
-      stash_rows<4>(sS, 16, g, col, [&](int t, int r) { return (float)f.hc[NC - 1][t >> 1][4 * (t & 1) + r]; });
+      stash_act<4>(sS, 16, g, col, f.hc[NC - 1]);
       {
         half4 cop;
         const float csc = make_op1(dco, cop);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-        bwd_k16<4>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
+        bwd_k16<4, false>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
         relu_mask(dc, f.hc[NC - 1]);
         dsc = make_op4(dc, dop);
       }
@@ -726,10 +831,8 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       for (int i = NC - 1; i >= 1; --i) {
         const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
         stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dc[t][r]; });
-        stash_rows<4>(sS, 64, g, col, [&](int t, int r) { return (float)f.hc[i - 1][t >> 1][4 * (t & 1) + r]; });
-#pragma unroll
-        for (int t = 0; t < 4; ++t) dc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-        bwd_k32<4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
+        stash_act<4>(sS, 64, g, col, f.hc[i - 1]);
+        bwd_k32<4, false>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
         relu_mask(dc, f.hc[i - 1]);
         dsc = make_op4(dc, dop);
         __syncthreads();
@@ -738,7 +841,10 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       }
       // colour input layer: its gradient, and the dout part of its input delta joins the density head's delta
       stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dc[t][r]; });
-      stash_rows<2>(sS, 64, g, col, [&](int t, int r) { return (float)f.cin[4 * t + r]; });
+      {
+        const bf16x8 cin[1] = {f.cin};
+        stash_act<2>(sS, 64, g, col, cin);
+      }
       bwd_k32<1>(sWt + A::wt_off(FFN_WC_IN), A::pt(FFN_WC_IN), dop, dsc, ddo, g, s);
       __syncthreads();
       layer_dw<4, 2, PS>(sS, gc_in, wave, g, s);
@@ -746,13 +852,11 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       // density output layer
       floatx4 dd[4];
       stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return ddo[t][r]; });
-      stash_rows<4>(sS, 16, g, col, [&](int t, int r) { return (float)f.hd[ND - 1][t >> 1][4 * (t & 1) + r]; });
+      stash_act<4>(sS, 16, g, col, f.hd[ND - 1]);
       {
         half4 dd_op;
         const float ssc = make_op1(ddo, dd_op);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-        bwd_k16<4>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
+        bwd_k16<4, false>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
         relu_mask(dd, f.hd[ND - 1]);
         dsc = make_op4(dd, dop);
       }
@@ -764,10 +868,8 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       for (int i = ND - 1; i >= 1; --i) {
         const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
         stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
-        stash_rows<4>(sS, 64, g, col, [&](int t, int r) { return (float)f.hd[i - 1][t >> 1][4 * (t & 1) + r]; });
-#pragma unroll
-        for (int t = 0; t < 4; ++t) dd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-        bwd_k32<4>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
+        stash_act<4>(sS, 64, g, col, f.hd[i - 1]);
+        bwd_k32<4, false>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
         relu_mask(dd, f.hd[i - 1]);
         dsc = make_op4(dd, dop);
         __syncthreads();
@@ -776,12 +878,10 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       }
       // density input layer: deltas and the encoding (bf16 of the fp32 values); dL/da0 = Wd_in^T . delta
       stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
-      stash_rows<KB0>(sS, 64, g, col, [&](int t, int r) { return (float)a0b[t][r]; });
+      stash_words<KB0>(sS, 64, g, col, [&](int t, int p) { return a0w[t][p]; });
       {
         floatx4 ga0[KB0];
-#pragma unroll
-        for (int t = 0; t < KB0; ++t) ga0[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-        bwd_k32<KB0>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
+        bwd_k32<KB0, false>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
         if (valid) store_enc_grad<LF, FEAT>(a, b, g, ga0);
       }
       __syncthreads();
@@ -882,7 +982,7 @@ __global__ __launch_bounds__(256) void k_mlp16_fwd(MlpPtrs wp, const float* __re
 #pragma unroll
     for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * sh_mult;
     Fwd16<LF, ND, NC> f;
-    forward16<LF, ND, NC, A>(sWf, sB, a0v, sh, g, s, f);
+    forward16<LF, ND, NC, A, false>(sWf, sB, a0v, sh, g, s, f);
     if (g == 0 && valid) {
       sigma[b] = softplus(fminf(fmaxf(f.dout0, -10.0f), 10.0f));
       rgb[3 * b] = f.rgb[0];
