@@ -113,11 +113,18 @@ template <int RT, int DT>
 __device__ __forceinline__ void bwd_tiles(const float* __restrict__ W, int P, const floatx4 (&delta)[DT],
                                           floatx4 (&res)[RT], int g, int s) {
 #pragma unroll
-  for (int tp = 0; tp < DT; ++tp)
+  for (int tp = 0; tp < DT; ++tp) {
+    float w[4][RT];  // the delta tile's weights, all read before its MFMAs
 #pragma unroll
     for (int rp = 0; rp < 4; ++rp)
 #pragma unroll
-      for (int t = 0; t < RT; ++t) res[t] = mfma4(W[(16 * tp + 4 * g + rp) * P + 16 * t + s], delta[tp][rp], res[t]);
+      for (int t = 0; t < RT; ++t) w[rp][t] = W[(16 * tp + 4 * g + rp) * P + 16 * t + s];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rp = 0; rp < 4; ++rp)
+#pragma unroll
+      for (int t = 0; t < RT; ++t) res[t] = mfma4(w[rp][t], delta[tp][rp], res[t]);
+  }
 }
 
 // The activation passes through an empty asm first: otherwise the compiler proves act > 0 equal to the
@@ -136,9 +143,9 @@ __device__ __forceinline__ void relu_mask(floatx4 (&d)[NT], const floatx4 (&act)
     }
 }
 
-// Weight-gradient tiles of one layer held by one wavefront.  The layer's 16x16 tiles i = T * IT + Tp
-// (rows 16T.., columns 16Tp..) are dealt round-robin: wavefront w holds i = 4m + w in w[m] (D layout) and
-// in b[m] a per-lane partial of the bias gradient when Tp = 0.
+// Weight-gradient tiles of one layer held by one wavefront: the layer's 16x16 tile (T, Tp) (rows 16T..,
+// columns 16Tp..) dealt to it as its m-th by deal_tile in w[m] (D layout), and in b[m] a per-lane partial
+// of the bias gradient when Tp = 0.
 template <int OT, int IT>
 struct WaveGrad {
   static constexpr int N = OT * IT / 4;
@@ -175,7 +182,8 @@ template <int OT, int IT, int PSF>
 __device__ __forceinline__ void layer_dw(const float* __restrict__ st, WaveGrad<OT, IT>& acc, int wave, int g, int s) {
 #pragma unroll
   for (int m = 0; m < WaveGrad<OT, IT>::N; ++m) {
-    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    int T, Tp;
+    deal_tile<IT>(m, wave, T, Tp);
     const float* drow = st + (16 * T + s) * PSF + 16 * g;
     const float* arow = st + (16 * (OT + Tp) + s) * PSF + 16 * g;
     floatx4 dv[4], av[4];
@@ -205,7 +213,8 @@ __device__ __forceinline__ void flush_layer(float* __restrict__ dst, int O, int 
                                             int wave, int g, int s) {
 #pragma unroll
   for (int m = 0; m < WaveGrad<OT, IT>::N; ++m) {
-    const int i = 4 * m + wave, T = i / IT, Tp = i - T * IT;
+    int T, Tp;
+    deal_tile<IT>(m, wave, T, Tp);
     const int col = 16 * Tp + s;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

@@ -422,6 +422,24 @@ __device__ __forceinline__ void tap_relu(uint32_t* rec, int h, const V (&act)[4]
   }
 }
 
+// Weight-gradient tiles (T, Tp) of one layer (OT x IT tiles of 16x16) dealt over the four wavefronts:
+// wavefront w's m-th tile.  The tiles with Tp = 0 also sum the bias gradient, so they are spread: with
+// IT = 4 (or 2) every wavefront holds one Tp = 0 tile per four (two) of its tiles.
+template <int IT>
+__device__ __forceinline__ void deal_tile(int m, int wave, int& T, int& Tp) {
+  if constexpr (IT == 4) {
+    T = m;
+    Tp = (wave + m) & 3;
+  } else if constexpr (IT == 2) {
+    T = 2 * m + (wave >> 1);
+    Tp = (wave + (wave >> 1) + m) & 1;
+  } else {
+    static_assert(IT == 1, "16, 32 or 64 input neurons per layer");
+    T = 4 * m + wave;
+    Tp = 0;
+  }
+}
+
 __device__ __forceinline__ float half_box_diagonal(const DevCfg& c) {
   const float dx = c.bmax[0] - c.bmin[0], dy = c.bmax[1] - c.bmin[1], dz = c.bmax[2] - c.bmin[2];
   return 0.5f * sqrtf(dx * dx + dy * dy + dz * dz);
