@@ -1094,6 +1094,21 @@ int ffn_make_batch(const float* images, uint32_t n_images, uint32_t width, uint3
   return 0;
 }
 
+int ffn_make_batch_weighted(const float* images, uint32_t n_images, uint32_t width, uint32_t height,
+                            const float* c2w, const float* K, const uint8_t* weights, uint32_t num_rays,
+                            uint32_t uniform_rays, uint32_t max_tries, uint32_t seed, void* rays, void* targets,
+                            uint32_t* pixel_ids, void* stream) {
+  if (!images || !c2w || !K || !weights || !rays || !targets) return fail(-1, "NULL buffer");
+  if (n_images == 0 || width == 0 || height == 0) return fail(-1, "empty image set");
+  if ((uint64_t)n_images * width * height >= ((uint64_t)1 << 32)) return fail(-1, "more than 2^32 - 1 pixels");
+  if (uniform_rays > num_rays) return fail(-1, "uniform_rays=%u exceeds num_rays=%u", uniform_rays, num_rays);
+  if (max_tries == 0 || max_tries > (1u << 20)) return fail(-1, "max_tries=%u out of [1,2^20]", max_tries);
+  FFN_HIP(ffn::launch_make_batch_weighted(images, n_images, width, height, c2w, K, weights, num_rays, uniform_rays,
+                                          max_tries, seed, (float4*)rays, (float4*)targets, pixel_ids,
+                                          (hipStream_t)stream));
+  return 0;
+}
+
 int ffn_set_profiling(void* handle, int32_t enable) {
   Handle* h = as_handle(handle);
   if (!h) return fail(-1, "NULL handle");

@@ -236,6 +236,10 @@ hipError_t launch_composite_marched(const CompMarchArgs& a, hipStream_t st);
 hipError_t launch_make_batch(const float* images, uint32_t n_images, uint32_t W, uint32_t H, const float* c2w,
                              const float* K, uint32_t num_rays, uint32_t seed, float4* rays, float4* targets,
                              uint32_t* pixel_ids, hipStream_t st);
+hipError_t launch_make_batch_weighted(const float* images, uint32_t n_images, uint32_t W, uint32_t H,
+                                      const float* c2w, const float* K, const uint8_t* weights, uint32_t num_rays,
+                                      uint32_t uniform_rays, uint32_t max_tries, uint32_t seed, float4* rays,
+                                      float4* targets, uint32_t* pixel_ids, hipStream_t st);
 
 // forward-only MLP over n samples: encodings a0 (layout feat), view directions from rays[ray_ids[b]];
 // sigma[n], rgb[n][3]

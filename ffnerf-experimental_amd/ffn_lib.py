@@ -26,7 +26,7 @@ EXPORTS = [
     "ffn_version", "ffn_last_error", "ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step",
     "ffn_occ_decay", "ffn_sample", "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam",
     "ffn_set_profiling", "ffn_stage_times", "ffn_occ_bitfield", "ffn_march", "ffn_render", "ffn_make_batch",
-    "ffn_march_noalloc", "ffn_train_step_marched",
+    "ffn_march_noalloc", "ffn_train_step_marched", "ffn_make_batch_weighted",
 ]
 MARCH_NOALLOC_MAX_RAYS = 1 << 20
 RELU_WORDS = 14  # ReLU-branch tap words per sample
@@ -135,12 +135,14 @@ def load(path: Path | str | None = None) -> C.CDLL:
     lib.ffn_render.argtypes = [_vp, _vp, C.c_uint32, _vp, C.POINTER(FfnMarchParams), _vp, _vp, _vp]
     lib.ffn_make_batch.argtypes = [_vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, C.c_uint32, C.c_uint32, _vp,
                                    _vp, _vp, _vp]
+    lib.ffn_make_batch_weighted.argtypes = [_vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, C.c_uint32,
+                                            C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp]
     lib.ffn_set_profiling.argtypes = [_vp, C.c_int32]
     lib.ffn_stage_times.argtypes = [_vp, _fp, C.POINTER(C.c_int32), C.c_int32]
     for name in ("ffn_create", "ffn_destroy", "ffn_bind_params", "ffn_train_step", "ffn_occ_decay", "ffn_sample",
                  "ffn_hash_encode_fwd", "ffn_hash_encode_bwd", "ffn_adam", "ffn_set_profiling", "ffn_stage_times",
                  "ffn_occ_bitfield", "ffn_march", "ffn_render", "ffn_make_batch", "ffn_march_noalloc",
-                 "ffn_train_step_marched"):
+                 "ffn_train_step_marched", "ffn_make_batch_weighted"):
         getattr(lib, name).restype = C.c_int
     if path is None:
         _LIB = lib

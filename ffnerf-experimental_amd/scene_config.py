@@ -4,9 +4,10 @@ The schema and validation rules are those of the reference (scene_config.py:1-76
 the same sections and keys with the same defaults, unknown sections or keys are
 errors, path keys are resolved against the JSON file's directory, and the same
 range checks apply.  This build adds one optional section, "model", for the
-knobs the reference compiles into its kernels (hash-grid shape, table
-optimizer, MLP precision, learning-rate schedule); a reference config, which
-has no such section, loads unchanged.
+knobs the reference compiles into its kernels or hard-wires in its trainer
+(hash-grid shape, table optimizer, MLP precision, learning-rate schedule,
+pixel sampler); a reference config, which has no such section, loads
+unchanged.
 """
 from __future__ import annotations
 
@@ -34,7 +35,7 @@ DEFAULTS = {
     "model": {"n_levels": 16, "f_per_level": 4, "log2_T": None, "base_res": 16.0, "finest_res": 1024.0,
               "nd": 2, "nc": 2, "hash_opt": "sgd", "mlp_precision": "fp32", "init": "he",
               "beta1": 0.9, "beta2": 0.999, "eps": 1e-6, "occ_G": 32, "occ_decay": 0.9,
-              "occ_period": 32, "background": "random", "schedule": "reference"},
+              "occ_period": 32, "background": "random", "schedule": "reference", "pixel_sampler": "adaptive"},
 }
 
 PATH_KEYS = [("data", "reconstruction"), ("data", "images_dir"), ("training", "directory")]
@@ -123,6 +124,8 @@ def validate(cfg: dict) -> None:
         raise ValueError("model.schedule must be 'reference' or 'constant'")
     if m["init"] not in ("he", "xavier"):
         raise ValueError("model.init must be 'he' or 'xavier'")
+    if m["pixel_sampler"] not in ("adaptive", "uniform"):
+        raise ValueError("model.pixel_sampler must be 'adaptive' or 'uniform'")
     for key in ("n_levels", "f_per_level", "nd", "nc", "occ_G", "occ_period"):
         _positive_int(cfg, "model", key)
     if m["log2_T"] is not None and (not isinstance(m["log2_T"], list) or len(m["log2_T"]) != m["n_levels"]):

@@ -9,11 +9,14 @@ for the training step that this package implements on the GPU.  Kept:
     batch's rendered colours,
   * graceful Ctrl+C, checkpoints through Nerf.save (time-throttled during the
     run, unconditional at the end) and resuming with load_id.
-Pixels are drawn uniformly over all training images (the reference's
-error-weighted rejection sampler, run_ffnerf_OG.py:459-683, is not part of
-this build), and the images stay resident on the GPU: every batch's rays and
-targets are produced there by ffn_make_batch, so no per-step host work or
-host-to-device copy remains.  The preview server, viewer and review UI are
+Pixels are drawn as the reference's producer draws them (model.pixel_sampler
+"adaptive", the default): the image uniformly, 20 % of the rays uniformly
+within it and the rest by rejection against per-image uint8 weight maps that
+every loss report updates from the batch's per-ray colour errors
+(run_ffnerf_OG.py:402-686; pixel_weights.py); "uniform" draws every pixel
+uniformly over all images.  The images stay resident on the GPU and every
+batch's rays and targets are produced there (ffn_make_batch_weighted,
+ffn_make_batch), so no per-step host work or host-to-device copy remains.  The preview server, viewer and review UI are
 not part of this build.
 """
 from __future__ import annotations
@@ -28,6 +31,7 @@ import numpy as np
 
 import ffn_lib as fl
 import ffnerf_tools as ft
+import pixel_weights as pw
 
 T_MID = 1500
 LR_FLOOR = 5e-6
@@ -149,6 +153,8 @@ def train(cfg: dict, load_id: str | None = None, log=print, eval_every: int = 0,
     occ = occ_params(cfg, box_min, box_max)
     nerf = ft.Nerf(t["directory"], t["model_id"], spec=spec, occ=occ, load_id=load_id, rng_seed=int(t["seed"]))
     dev = DeviceImages(images, poses, K)
+    weights = pw.PixelWeights(images) if cfg["model"]["pixel_sampler"] == "adaptive" else None
+    pixel_ids = torch.zeros(B, dtype=torch.int32, device="cuda") if weights is not None else None
     constant = cfg["model"]["schedule"] == "constant"
     ios = [ft.RayBatch.init(B, S) for _ in range(2)]
     rng = np.random.default_rng(int(t["seed"]))
@@ -173,7 +179,10 @@ def train(cfg: dict, load_id: str | None = None, log=print, eval_every: int = 0,
                 break
             step = step0 + k + 1
             io = ios[k & 1]
-            dev.make_batch(io, seed=int(rng.integers(0, 2 ** 32)))
+            if weights is not None:
+                weights.make_batch(dev, io, seed=int(rng.integers(0, 2 ** 32)), pixel_ids=pixel_ids)
+            else:
+                dev.make_batch(io, seed=int(rng.integers(0, 2 ** 32)))
             if constant:
                 lr_f, sh, cr, occ_s = np.float32(t["lr"]), 1.0, 1.0, float(occ.occ_update_strength0)
             else:
@@ -187,6 +196,9 @@ def train(cfg: dict, load_id: str | None = None, log=print, eval_every: int = 0,
                 tg = io.targets_buf.detach().cpu().numpy()
                 mse, rmse, l2 = batch_loss(out, tg)
                 write_loss_row(loss_f, time.time() - t0, step, float(lr_f), mse, rmse, l2)
+                if weights is not None:  # the reference's feedback of the reported batch's errors
+                    weights.update(pixel_ids.cpu().numpy().view(np.uint32), pw.ray_errors(out, tg))
+                    weights.upload()
                 history.append((step, mse))
                 log(f"[step {step}] lr_f={float(lr_f):.3e} mse={mse:.6e} rmse_rgb={rmse:.6e} l2mean={l2:.6e}")
             if eval_io is not None and (step % eval_every == 0):
@@ -203,4 +215,4 @@ def train(cfg: dict, load_id: str | None = None, log=print, eval_every: int = 0,
         signal.signal(signal.SIGINT, old)
     log(f"Saved model -> {saved}")
     return dict(steps_trained=int(nerf.steps_trained), loss_log=str(loss_path), checkpoint=str(saved),
-                history=history, evals=evals, nerf=nerf)
+                history=history, evals=evals, nerf=nerf, pixel_weights=weights)

@@ -268,6 +268,23 @@ int ffn_make_batch(const float* images, uint32_t n_images, uint32_t width, uint3
                    const float* K, uint32_t num_rays, uint32_t seed, void* rays, void* targets, uint32_t* pixel_ids,
                    void* stream);
 
+/* An error-weighted training batch (replaces the reference's producer with its
+ * per-image uint8 weight maps and rejection sampler, run_ffnerf_OG.py:490-516,
+ * 585-686): weights [n][H][W] uint8 (the caller's maps, updated from the loss).
+ * Ray r's image is drawn uniformly (im = floor(h0 n / 2^32),
+ * h0 = lowbias32(seed ^ r * 2654435769)); proposal t is pixel
+ * floor(h_t W H / 2^32) of it, h_t = lowbias32(h0 ^ (t + 1) * 0x9E3779B9),
+ * accepted when lowbias32(h_t ^ 0x5BD1E995) & 255 <= its weight (probability
+ * (w + 1) / 256, as the reference's rng.integers(0, 256) <= w).  Rays
+ * r < uniform_rays take proposal 0 (the reference's uniform share); the others
+ * the first accepted proposal, or proposal max_tries - 1.  Outputs as
+ * ffn_make_batch.  Errors: -1 for NULL buffers, uniform_rays > num_rays or
+ * max_tries outside [1, 2^20]. */
+int ffn_make_batch_weighted(const float* images, uint32_t n_images, uint32_t width, uint32_t height,
+                            const float* c2w, const float* K, const uint8_t* weights, uint32_t num_rays,
+                            uint32_t uniform_rays, uint32_t max_tries, uint32_t seed, void* rays, void* targets,
+                            uint32_t* pixel_ids, void* stream);
+
 /* Stage timing (the counterpart of the reference's profiling queue and
  * event_ms, ffnerf_tools.py:11-13,127-138,1521-1530).  When enabled, every
  * ffn_train_step records HIP events around its kernels on the caller's stream;

@@ -56,6 +56,50 @@ def test_make_batch_matches_host_rays(torch):
     assert len(np.unique(im)) == cams.c2w.shape[0]
 
 
+@pytest.mark.parametrize("uniform_rays,max_tries", [(0, 4096), (1000, 4096), (0, 3)])
+def test_make_batch_weighted_matches_oracle(torch, uniform_rays, max_tries):
+    """ffn_make_batch_weighted draws the pixels of the restated sampler (oracle/pixel_sampler.py) bit for bit,
+    from uint8 weight maps with zeros, ones and 255s, and builds the same rays and targets as the host."""
+    print(f"[case] weighted batch uniform_rays={uniform_rays} max_tries={max_tries}", flush=True)
+    import ffnerf_tools as ft
+    import synthetic_scene as sc
+    import trainer
+    import ffn_lib as fl
+    from oracle import pixel_sampler as ps
+    cams = sc.cameras_for("cfg0")
+    rng = np.random.default_rng(5)
+    n = cams.c2w.shape[0]
+    images = rng.random((n, cams.H, cams.W, 3)).astype(np.float32)
+    maps = rng.integers(0, 256, (n, cams.H, cams.W), dtype=np.uint8)
+    maps[0] = 0
+    maps[1] = 255
+    maps[2, ::2] = 1
+    dev = trainer.DeviceImages(images, cams.c2w, cams.K)
+    wdev = torch.from_numpy(maps).cuda()
+    N = 6000
+    io = ft.RayBatch.init(N, 64)
+    ids = torch.zeros(N, dtype=torch.int32, device="cuda")
+    fl.check(dev.lib.ffn_make_batch_weighted(fl.ptr(dev.images), dev.n, dev.W, dev.H, fl.ptr(dev.c2w),
+                                             fl.ptr(dev.K), fl.ptr(wdev), N, uniform_rays, max_tries, 4321,
+                                             fl.ptr(io.rays_buf), fl.ptr(io.targets_buf), fl.ptr(ids),
+                                             fl.stream_ptr()), "ffn_make_batch_weighted")
+    torch.cuda.synchronize()
+    p = ids.cpu().numpy().view(np.uint32).astype(np.int64)
+    np.testing.assert_array_equal(p, ps.draw_weighted(4321, N, n, cams.W, cams.H, maps, uniform_rays, max_tries))
+    im, rem = p // (cams.W * cams.H), p % (cams.W * cams.H)
+    v, u = rem // cams.W, rem % cams.W
+    rays, tg = ft.rays_targets_from_indices(im, u, v, images, cams.c2w, cams.W, cams.H, K=cams.K)
+    np.testing.assert_allclose(io.rays_buf.cpu().numpy(), ft.rays_as_array(rays), atol=2e-6)
+    np.testing.assert_array_equal(io.targets_buf.cpu().numpy(), tg)
+    # argument checks
+    assert dev.lib.ffn_make_batch_weighted(fl.ptr(dev.images), dev.n, dev.W, dev.H, fl.ptr(dev.c2w),
+                                           fl.ptr(dev.K), fl.ptr(wdev), N, N + 1, 16, 1, fl.ptr(io.rays_buf),
+                                           fl.ptr(io.targets_buf), None, fl.stream_ptr()) == -1
+    assert dev.lib.ffn_make_batch_weighted(fl.ptr(dev.images), dev.n, dev.W, dev.H, fl.ptr(dev.c2w),
+                                           fl.ptr(dev.K), fl.ptr(wdev), N, 0, 0, 1, fl.ptr(io.rays_buf),
+                                           fl.ptr(io.targets_buf), None, fl.stream_ptr()) == -1
+
+
 def _config(tmp_path, steps=40, rays=256):
     import synthetic_scene as sc
     npz = sc.write_archive(tmp_path / "scene", "cfg0")
@@ -96,6 +140,24 @@ def test_cli_train_resume_snapshot(torch, tmp_path):
     assert ffnerf_cli.main(["snapshot", "--config", str(path), "--output", str(out), "--view", "2"]) == 0
     img = png_io.read_png(out)
     assert img.shape == (64, 64, 3)  # after 70 steps the view is mostly the black background
+
+
+def test_adaptive_sampler_follows_the_errors(torch, tmp_path):
+    """The trainer's default pixel sampler (the reference's producer): after every loss report the maps move
+    towards the batch's per-ray errors, the device copy follows the host maps, and background pixels stay
+    at or below the cap of 16 while the ball's pixels, which the early model gets wrong, rise above it."""
+    print("[case] adaptive pixel sampler in the trainer", flush=True)
+    import scene_config
+    import trainer
+    cfg = scene_config.load_config(_config(tmp_path, steps=40))
+    assert cfg["model"]["pixel_sampler"] == "adaptive"
+    res = trainer.train(cfg, log=lambda *a: None)
+    w = res["pixel_weights"]
+    np.testing.assert_array_equal(w.dev.cpu().numpy(), w.maps)
+    moved = w.maps != 16
+    assert moved.sum() > 500
+    assert w.maps[~w.fg].max() <= 16
+    assert w.maps[w.fg & moved].mean() > 20
 
 
 def test_checkpoint_round_trip_bit_exact(torch, tmp_path):
