@@ -83,6 +83,7 @@ struct Handle {
   Scratch m_Tr, m_dLds, m_dLdc;
   Scratch m_bits;  // the bitfield of ffn_train_step's march sampler
   Scratch m_slots;  // the marched step's per-ray sample slots (one walk instead of count + emit)
+  Scratch dense;    // dense vertex copies of the coarse levels (the gather's)
   uint32_t* host_total = nullptr;  // pinned
 };
 
@@ -114,6 +115,33 @@ bool march_slots_fit(const Scratch& held, size_t need) {
   if (mb < 0) mb = 0;
   if (mb > (1ll << 22)) mb = 1ll << 22;
   return need <= ((size_t)mb << 20) && growth_fits_free(held, need);
+}
+
+// The gather's dense vertex copies: every level with 2 <= R and R^3 <= FFN_DENSE_MAX_CELLS (default 2^21:
+// 16 MB at F = 2 in fp32) vertices gets one, filled from `table` on the stream (they follow the table, so
+// they are rebuilt before every gather that follows a table update).  At the benchmark shape the copies of
+// levels 0-6 (res 16-111) take the gather from 5.22 to 4.61 ms; adding level 7 (res 154, 29 MB) measured
+// 4.71, all levels up to res 406 6.24 ms.
+hipError_t build_dense_levels(Handle* h, const void* table, ffn::DenseLevels* dl, hipStream_t st) {
+  const char* env = getenv("FFN_DENSE_MAX_CELLS");
+  const long long max_cells = env ? atoll(env) : (1ll << 21);
+  const ffn::DevCfg& c = h->dc;
+  uint64_t total = 0;
+  for (int l = 0; l < FFN_MAX_LEVELS; ++l) dl->off[l] = ffn::DENSE_NONE;
+  for (int l = 0; l < c.L; ++l) {
+    const long long R = c.res[l];
+    if (R >= 2 && R * R * R <= max_cells) {
+      dl->off[l] = (uint32_t)total;
+      total += (uint64_t)((R * R * R + 63) & ~63ll);  // each level's copy starts 256-byte aligned
+    }
+  }
+  dl->grid = nullptr;
+  if (total == 0) return hipSuccess;
+  const size_t elem = c.table_f16 ? 2 : 4;
+  hipError_t e = h->dense.ensure((size_t)total * (size_t)c.F * elem);
+  if (e != hipSuccess) return e;
+  dl->grid = h->dense.p;
+  return ffn::launch_hash_densify(c, table, *dl, st);
 }
 
 // size the bucketed-scatter scratch for n samples and fill the views
@@ -389,7 +417,7 @@ int ffn_destroy(void* handle) {
   h->bin_max.release();
   for (Scratch* sc : {&h->m_state, &h->m_acc, &h->m_counts, &h->m_offsets, &h->m_sums, &h->m_total, &h->m_samples,
                       &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb, &h->m_Tr, &h->m_dLds, &h->m_dLdc, &h->m_bits,
-                      &h->m_slots})
+                      &h->m_slots, &h->dense})
     sc->release();
   if (h->host_total) (void)hipHostFree(h->host_total);
   delete h;
@@ -456,7 +484,9 @@ int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint
   FFN_HIP(h->a0.ensure(sizeof(float) * (size_t)n * h->dc.LF));
   const ffn::FeatLayout lm = ffn::level_major(n, h->dc.F);
   ffn::PosSrc src{x, nullptr, nullptr, 0};
-  FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, (float*)h->a0.p, lm, idx_out, st));
+  ffn::DenseLevels dl;
+  FFN_HIP(build_dense_levels(h, h->params.table, &dl, st));
+  FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, (float*)h->a0.p, lm, idx_out, &dl, st));
   FFN_HIP(ffn::launch_feat_relayout((const float*)h->a0.p, lm, a0, ffn::sample_major(h->dc.L, h->dc.F), n, h->dc.L,
                                     h->dc.F, st));
   return 0;
@@ -567,7 +597,9 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     StageTimer tm(h, 1, st);
     ffn::PosSrc s2 = src;
     s2.Ts = Ts;
-    FFN_HIP(ffn::launch_hash_fwd(h->dc, s2, N, P.table, a0, feat, nullptr, st));
+    ffn::DenseLevels dl;
+    FFN_HIP(build_dense_levels(h, P.table, &dl, st));
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, s2, N, P.table, a0, feat, nullptr, &dl, st));
   }
 
   ffn::MlpArgs a{};
@@ -861,7 +893,9 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   // 2. encode the samples
   {
     StageTimer tm(h, 1, st);
-    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, P.table, a0, feat, nullptr, st));
+    ffn::DenseLevels dl;
+    FFN_HIP(build_dense_levels(h, P.table, &dl, st));
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, P.table, a0, feat, nullptr, &dl, st));
   }
   // 3-5. forward MLP, compositing with early termination and the loss, MLP backward
   const int64_t n_tiles = (n + 63) / 64;
@@ -1055,6 +1089,8 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   a1.ray_ids = nullptr;
   int n_blocks = h->n_cu > 0 ? 2 * h->n_cu : 512;
   const uint32_t rounds = (mp->max_steps + mp->chunk - 1) / mp->chunk;
+  ffn::DenseLevels dl;  // the table does not change during the render: one copy serves every round
+  FFN_HIP(build_dense_levels(h, h->params.table, &dl, st));
   for (uint32_t round = 0; round < rounds; ++round) {
     FFN_HIP(ffn::launch_march(one_walk ? a1 : a, one_walk, st));
     FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, total, st));
@@ -1071,7 +1107,7 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
     ffn::PosSrc src{(const float*)samples, nullptr, nullptr, 0};
     src.x_stride = 4;
     const ffn::FeatLayout feat = ffn::level_major(n, h->dc.F);
-    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, a0, feat, nullptr, st));
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, a0, feat, nullptr, &dl, st));
     int nb = (int)((n + 63) / 64);
     if (nb > n_blocks) nb = n_blocks;
     FFN_HIP(ffn::launch_mlp_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, mp->sh_multiplier, sigma, rgb, LF,

@@ -195,11 +195,14 @@ __device__ __forceinline__ float corner_weight(const LevelCell& lc, int cc) {
   return wx * wy * wz;
 }
 
-__device__ __forceinline__ uint32_t corner_entry(const LevelCell& lc, int cc, int lvl, uint32_t mask) {
-  uint32_t ix = (uint32_t)(lc.i0[0] + (cc & 1));
-  uint32_t iy = (uint32_t)(lc.i0[1] + ((cc >> 1) & 1));
-  uint32_t iz = (uint32_t)(lc.i0[2] + ((cc >> 2) & 1));
+// table entry of grid vertex (ix, iy, iz) at level lvl
+__device__ __forceinline__ uint32_t level_entry(uint32_t ix, uint32_t iy, uint32_t iz, int lvl, uint32_t mask) {
   return hash_u32(ix * 73856093u ^ iy * 19349663u ^ iz * 83492791u ^ (uint32_t)lvl * 2654435761u) & mask;
+}
+
+__device__ __forceinline__ uint32_t corner_entry(const LevelCell& lc, int cc, int lvl, uint32_t mask) {
+  return level_entry((uint32_t)(lc.i0[0] + (cc & 1)), (uint32_t)(lc.i0[1] + ((cc >> 1) & 1)),
+                     (uint32_t)(lc.i0[2] + ((cc >> 2) & 1)), lvl, mask);
 }
 
 // ---------------------------------------------------------------------------

@@ -126,10 +126,54 @@ __device__ __forceinline__ void sample_position(const PosSrc& s, int64_t b, floa
 // ---------------------------------------------------------------------------
 // forward
 
+// Dense copies of the coarse levels.  A level whose R^3 vertices are few gets its vertex values copied
+// out of the hash table before the gather, in vertex order: there the eight corners of a cell are four
+// pairs of x-neighbours, each pair adjacent in memory (one load where the pair fits 16 bytes), and the 64
+// samples of a wavefront, one ray, walk through neighbouring cells, so a load instruction touches a few
+// lines instead of 64 random ones, and no corner is hashed.  The values are the table's, so the gather
+// is unchanged bit for bit.
+template <int F, typename TT>
+__global__ __launch_bounds__(256) void k_hash_densify(DevCfg c, const TT* __restrict__ table, DenseLevels dl) {
+  const int l = (int)blockIdx.y;
+  if (dl.off[l] == DENSE_NONE) return;
+  const uint32_t R = (uint32_t)c.res[l];
+  const uint32_t cells = R * R * R;
+  TT* __restrict__ grid = static_cast<TT*>(dl.grid) + (size_t)dl.off[l] * F;
+  const uint32_t base = c.offset[l], mask = c.mask[l];
+  for (uint32_t v = blockIdx.x * blockDim.x + threadIdx.x; v < cells; v += gridDim.x * blockDim.x) {
+    const uint32_t x = v % R, y = (v / R) % R, z = v / (R * R);
+    const uint32_t e = (base + level_entry(x, y, z, l, mask)) * (uint32_t)F;
+#pragma unroll
+    for (int f = 0; f < F; ++f) grid[(size_t)v * F + f] = table[e + f];
+  }
+}
+
+// the x-neighbour pair of a dense row: one 8- or 16-byte load where the pair has that size
+template <int F, typename TT>
+__device__ __forceinline__ void load_xpair(const TT* p, typename TabVec<F, TT>::V::T& a,
+                                           typename TabVec<F, TT>::V::T& b) {
+  typedef typename TabVec<F, TT>::V::T V;
+  constexpr int BYTES = 2 * F * (int)sizeof(TT);
+  if constexpr (BYTES == 8 || BYTES == 16) {
+    typedef unsigned int W __attribute__((ext_vector_type(BYTES / 4), aligned(BYTES / 2)));
+    struct Pair {
+      V a, b;
+    };
+    static_assert(sizeof(Pair) == BYTES, "two entries, no padding");
+    const Pair pr = __builtin_bit_cast(Pair, *reinterpret_cast<const W*>(p));
+    a = pr.a;
+    b = pr.b;
+  } else {
+    a = *reinterpret_cast<const V*>(p);
+    b = *reinterpret_cast<const V*>(p + F);
+  }
+}
+
 template <int F, typename TT>
 __global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t n, int level0,
                                                   const TT* __restrict__ table, float* __restrict__ a0,
-                                                  FeatLayout lay, uint32_t* __restrict__ idx_out) {
+                                                  FeatLayout lay, uint32_t* __restrict__ idx_out,
+                                                  DenseLevels dl) {
   typedef typename TabVec<F, TT>::V TV;
   typedef typename TV::T V;
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -142,10 +186,23 @@ __global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t 
   const uint32_t mask = c.mask[l], off = c.offset[l];
   uint32_t fb[8];
   V val[8];
+  if (dl.off[l] != DENSE_NONE) {  // the same for the whole block (one level per grid row)
+    const size_t R = (size_t)c.res[l];
+    const TT* g = static_cast<const TT*>(dl.grid) +
+                  ((size_t)dl.off[l] + ((size_t)lc.i0[2] * R + (size_t)lc.i0[1]) * R + (size_t)lc.i0[0]) * F;
 #pragma unroll
-  for (int cc = 0; cc < 8; ++cc) {
-    fb[cc] = (off + corner_entry(lc, cc, l, mask)) * (uint32_t)F;
-    val[cc] = *reinterpret_cast<const V*>(table + fb[cc]);
+    for (int q = 0; q < 4; ++q)  // corners 2q (dx = 0) and 2q + 1 (dx = 1) of row dy = q & 1, dz = q >> 1
+      load_xpair<F, TT>(g + ((size_t)(q >> 1) * R * R + (size_t)(q & 1) * R) * F, val[2 * q], val[2 * q + 1]);
+    if (idx_out) {
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) fb[cc] = (off + corner_entry(lc, cc, l, mask)) * (uint32_t)F;
+    }
+  } else {
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+      fb[cc] = (off + corner_entry(lc, cc, l, mask)) * (uint32_t)F;
+      val[cc] = *reinterpret_cast<const V*>(table + fb[cc]);
+    }
   }
   float acc[F];
 #pragma unroll
@@ -755,23 +812,60 @@ hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_
 
 template <typename TT>
 static hipError_t launch_hash_fwd_t(const DevCfg& c, const PosSrc& src, int64_t n, const TT* table, float* a0,
-                                    const FeatLayout& lay, uint32_t* idx_out, hipStream_t st) {
+                                    const FeatLayout& lay, uint32_t* idx_out, const DenseLevels& dl,
+                                    hipStream_t st) {
   const dim3 grid((unsigned)((n + 255) / 256), (unsigned)c.L), block(256);
   switch (c.F) {
-    case 1: hipLaunchKernelGGL((k_hash_fwd<1, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
-    case 2: hipLaunchKernelGGL((k_hash_fwd<2, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
-    case 4: hipLaunchKernelGGL((k_hash_fwd<4, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out); break;
+    case 1:
+      hipLaunchKernelGGL((k_hash_fwd<1, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out, dl);
+      break;
+    case 2:
+      hipLaunchKernelGGL((k_hash_fwd<2, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out, dl);
+      break;
+    case 4:
+      hipLaunchKernelGGL((k_hash_fwd<4, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out, dl);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const void* table, float* a0,
-                           const FeatLayout& lay, uint32_t* idx_out, hipStream_t st) {
+                           const FeatLayout& lay, uint32_t* idx_out, const DenseLevels* dl, hipStream_t st) {
   if (n <= 0) return hipSuccess;
+  DenseLevels none{};
+  none.grid = nullptr;
+  for (int l = 0; l < FFN_MAX_LEVELS; ++l) none.off[l] = DENSE_NONE;
+  const DenseLevels& d = (dl && dl->grid) ? *dl : none;
   if (c.table_f16)
-    return launch_hash_fwd_t(c, src, n, static_cast<const _Float16*>(table), a0, lay, idx_out, st);
-  return launch_hash_fwd_t(c, src, n, static_cast<const float*>(table), a0, lay, idx_out, st);
+    return launch_hash_fwd_t(c, src, n, static_cast<const _Float16*>(table), a0, lay, idx_out, d, st);
+  return launch_hash_fwd_t(c, src, n, static_cast<const float*>(table), a0, lay, idx_out, d, st);
+}
+
+template <typename TT>
+static hipError_t launch_densify_t(const DevCfg& c, const TT* table, const DenseLevels& dl, hipStream_t st) {
+  uint32_t max_cells = 0;
+  for (int l = 0; l < c.L; ++l)
+    if (dl.off[l] != DENSE_NONE) {
+      const uint32_t R = (uint32_t)c.res[l];
+      max_cells = R * R * R > max_cells ? R * R * R : max_cells;
+    }
+  if (max_cells == 0) return hipSuccess;
+  const unsigned bx = (unsigned)((max_cells + 255) / 256 < 2048 ? (max_cells + 255) / 256 : 2048);
+  const dim3 grid(bx, (unsigned)c.L), block(256);
+  switch (c.F) {
+    case 1: hipLaunchKernelGGL((k_hash_densify<1, TT>), grid, block, 0, st, c, table, dl); break;
+    case 2: hipLaunchKernelGGL((k_hash_densify<2, TT>), grid, block, 0, st, c, table, dl); break;
+    case 4: hipLaunchKernelGGL((k_hash_densify<4, TT>), grid, block, 0, st, c, table, dl); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_hash_densify(const DevCfg& c, const void* table, const DenseLevels& dl, hipStream_t st) {
+  if (!dl.grid) return hipSuccess;
+  if (c.table_f16) return launch_densify_t(c, static_cast<const _Float16*>(table), dl, st);
+  return launch_densify_t(c, static_cast<const float*>(table), dl, st);
 }
 
 BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes) {

@@ -152,8 +152,18 @@ hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays,
                          hipStream_t st);
 
 // table: float, or binary16 when c.table_f16 (widened exactly; the sums are the same fp32 operations)
+// Dense copies of the coarse levels' vertex values: level l's vertex (x, y, z) at grid[(off[l] + (z R + y) R
+// + x) F ..] (the table's element type), or off[l] = DENSE_NONE for a level read through its hash
+constexpr uint32_t DENSE_NONE = 0xFFFFFFFFu;
+struct DenseLevels {
+  void* grid;
+  uint32_t off[FFN_MAX_LEVELS];
+};
+// fill the dense copies from the table (every level with off[l] != DENSE_NONE)
+hipError_t launch_hash_densify(const DevCfg& c, const void* table, const DenseLevels& dl, hipStream_t st);
+// dl (may be NULL): levels with a dense copy gather from it, with the same values and arithmetic
 hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const void* table, float* a0,
-                           const FeatLayout& lay, uint32_t* idx_out, hipStream_t st);
+                           const FeatLayout& lay, uint32_t* idx_out, const DenseLevels* dl, hipStream_t st);
 // BIN_GRAD: dst += scatter(g); BIN_SGD: table += scatter(-lr 2^(-0.1 l) 0.5 g) (reference SGD);
 // BIN_ADAM: Adam on the table with the scattered gradient
 hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* g, const FeatLayout& lay,

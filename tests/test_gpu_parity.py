@@ -528,3 +528,30 @@ def test_train_step_fp16_table(gh, ora, hash_opt, mlp_precision):
     rays = look_at_rays(96, spec, seed=232, miss_frac=0.1)
     m, o = _compare_step(spec, p, rays, sphere_targets(rays, spec), 64, default_scalars(lr=0.05), gh, ora)
     assert not np.array_equal(m.state()["table"], p["table"])
+
+
+def test_dense_level_copies_change_no_bit(gh, monkeypatch):
+    """The gather reads the coarse levels from dense vertex copies (levels with R^3 <= FFN_DENSE_MAX_CELLS):
+    encodings, hash indices and a whole training step are bit-identical with the copies off (0), at the
+    default and with every level of the cfg0 shape dense."""
+    print("[case] dense level copies on/off", flush=True)
+    spec = spec_cfg0(hash_opt=1)
+    p = random_params(spec, seed=201)
+    rays = look_at_rays(128, spec, seed=202, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    x = np.random.default_rng(203).uniform(-0.1, 1.1, (5000, 3)).astype(np.float32)
+    res = []
+    for cells in ("0", str(1 << 21), str(1 << 30)):
+        monkeypatch.setenv("FFN_DENSE_MAX_CELLS", cells)
+        m = gh.GpuModel(spec, p)
+        enc, idx = m.encode(x, with_idx=True)
+        enc_plain = m.encode(x)  # the dense path without the index tap
+        np.testing.assert_array_equal(enc_plain, enc)
+        out, _ = m.train_step(rays, tg, 64, default_scalars())
+        res.append((enc, idx, out, m.state()))
+    for r in res[1:]:
+        np.testing.assert_array_equal(r[0], res[0][0])
+        np.testing.assert_array_equal(r[1], res[0][1])
+        np.testing.assert_array_equal(r[2], res[0][2])
+        for k in res[0][3]:
+            np.testing.assert_array_equal(r[3][k], res[0][3][k], err_msg=k)
