@@ -126,18 +126,31 @@ hipError_t build_dense_levels(Handle* h, const void* table, ffn::DenseLevels* dl
   const char* env = getenv("FFN_DENSE_MAX_CELLS");
   const long long max_cells = env ? atoll(env) : (1ll << 21);
   const ffn::DevCfg& c = h->dc;
+  const size_t elem = c.table_f16 ? 2 : 4;
   uint64_t total = 0;
   for (int l = 0; l < FFN_MAX_LEVELS; ++l) dl->off[l] = ffn::DENSE_NONE;
+  dl->n_multi = 0;
+  bool leading = true;
   for (int l = 0; l < c.L; ++l) {
     const long long R = c.res[l];
     if (R >= 2 && R * R * R <= max_cells) {
       dl->off[l] = (uint32_t)total;
       total += (uint64_t)((R * R * R + 63) & ~63ll);  // each level's copy starts 256-byte aligned
+      // the leading levels whose copies are at most 2 MiB each share one gather pass (FFN_DENSE_MULTI=0: none)
+      if (leading && (size_t)(R * R * R) * (size_t)c.F * elem <= ((size_t)2 << 20)) ++dl->n_multi;
+      else leading = false;
+    } else {
+      leading = false;
     }
   }
+  if (const char* m = getenv("FFN_DENSE_MULTI")) {
+    if (atoi(m) == 0) dl->n_multi = 0;
+  }
   dl->grid = nullptr;
-  if (total == 0) return hipSuccess;
-  const size_t elem = c.table_f16 ? 2 : 4;
+  if (total == 0) {
+    dl->n_multi = 0;
+    return hipSuccess;
+  }
   hipError_t e = h->dense.ensure((size_t)total * (size_t)c.F * elem);
   if (e != hipSuccess) return e;
   dl->grid = h->dense.p;

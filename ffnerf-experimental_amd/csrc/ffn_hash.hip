@@ -169,24 +169,19 @@ __device__ __forceinline__ void load_xpair(const TT* p, typename TabVec<F, TT>::
   }
 }
 
+// one sample at one level: the eight corners (from the dense copy or through the hash), the trilinear sum,
+// the store of the encoding (and of the corner indices when idx_out is given)
 template <int F, typename TT>
-__global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t n, int level0,
-                                                  const TT* __restrict__ table, float* __restrict__ a0,
-                                                  FeatLayout lay, uint32_t* __restrict__ idx_out,
-                                                  DenseLevels dl) {
+__device__ __forceinline__ void gather_level(const DevCfg& c, const float (&p)[3], int l, const TT* __restrict__ table,
+                                             const DenseLevels& dl, int64_t b, float* __restrict__ a0,
+                                             const FeatLayout& lay, uint32_t* __restrict__ idx_out) {
   typedef typename TabVec<F, TT>::V TV;
   typedef typename TV::T V;
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= n) return;
-  const int l = level0 + (int)blockIdx.y;
-  float pos[3], p[3];
-  sample_position(src, b, pos);
-  normalize_pos(c, pos, p);
   const LevelCell lc = level_cell(c.res[l], p);
   const uint32_t mask = c.mask[l], off = c.offset[l];
   uint32_t fb[8];
   V val[8];
-  if (dl.off[l] != DENSE_NONE) {  // the same for the whole block (one level per grid row)
+  if (dl.off[l] != DENSE_NONE) {  // the same for the whole block
     const size_t R = (size_t)c.res[l];
     const TT* g = static_cast<const TT*>(dl.grid) +
                   ((size_t)dl.off[l] + ((size_t)lc.i0[2] * R + (size_t)lc.i0[1]) * R + (size_t)lc.i0[0]) * F;
@@ -222,6 +217,27 @@ __global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t 
   if (idx_out) {
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) idx_out[(b * c.L + l) * 8 + cc] = fb[cc];
+  }
+}
+
+// Grid row y gathers level y + (n_multi - 1) for one sample per thread; with n_multi > 0, row 0 gathers the
+// n_multi coarsest levels (small dense copies, together a working set of a few MB) in one pass, so their
+// sample positions are read and computed once.
+template <int F, typename TT>
+__global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t n, const TT* __restrict__ table,
+                                                  float* __restrict__ a0, FeatLayout lay,
+                                                  uint32_t* __restrict__ idx_out, DenseLevels dl) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= n) return;
+  float pos[3], p[3];
+  sample_position(src, b, pos);
+  normalize_pos(c, pos, p);
+  const int row = (int)blockIdx.y;
+  if (dl.n_multi > 0 && row == 0) {
+#pragma unroll 1
+    for (int l = 0; l < dl.n_multi; ++l) gather_level<F, TT>(c, p, l, table, dl, b, a0, lay, idx_out);
+  } else {
+    gather_level<F, TT>(c, p, row + (dl.n_multi > 0 ? dl.n_multi - 1 : 0), table, dl, b, a0, lay, idx_out);
   }
 }
 
@@ -814,17 +830,12 @@ template <typename TT>
 static hipError_t launch_hash_fwd_t(const DevCfg& c, const PosSrc& src, int64_t n, const TT* table, float* a0,
                                     const FeatLayout& lay, uint32_t* idx_out, const DenseLevels& dl,
                                     hipStream_t st) {
-  const dim3 grid((unsigned)((n + 255) / 256), (unsigned)c.L), block(256);
+  const int rows = dl.n_multi > 0 ? c.L - dl.n_multi + 1 : c.L;
+  const dim3 grid((unsigned)((n + 255) / 256), (unsigned)rows), block(256);
   switch (c.F) {
-    case 1:
-      hipLaunchKernelGGL((k_hash_fwd<1, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out, dl);
-      break;
-    case 2:
-      hipLaunchKernelGGL((k_hash_fwd<2, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out, dl);
-      break;
-    case 4:
-      hipLaunchKernelGGL((k_hash_fwd<4, TT>), grid, block, 0, st, c, src, n, 0, table, a0, lay, idx_out, dl);
-      break;
+    case 1: hipLaunchKernelGGL((k_hash_fwd<1, TT>), grid, block, 0, st, c, src, n, table, a0, lay, idx_out, dl); break;
+    case 2: hipLaunchKernelGGL((k_hash_fwd<2, TT>), grid, block, 0, st, c, src, n, table, a0, lay, idx_out, dl); break;
+    case 4: hipLaunchKernelGGL((k_hash_fwd<4, TT>), grid, block, 0, st, c, src, n, table, a0, lay, idx_out, dl); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -835,6 +846,7 @@ hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
   if (n <= 0) return hipSuccess;
   DenseLevels none{};
   none.grid = nullptr;
+  none.n_multi = 0;
   for (int l = 0; l < FFN_MAX_LEVELS; ++l) none.off[l] = DENSE_NONE;
   const DenseLevels& d = (dl && dl->grid) ? *dl : none;
   if (c.table_f16)

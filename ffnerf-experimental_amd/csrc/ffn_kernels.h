@@ -158,6 +158,7 @@ constexpr uint32_t DENSE_NONE = 0xFFFFFFFFu;
 struct DenseLevels {
   void* grid;
   uint32_t off[FFN_MAX_LEVELS];
+  int n_multi;  // levels 0 .. n_multi - 1 (all with dense copies) are gathered together in one pass
 };
 // fill the dense copies from the table (every level with off[l] != DENSE_NONE)
 hipError_t launch_hash_densify(const DevCfg& c, const void* table, const DenseLevels& dl, hipStream_t st);
