@@ -119,9 +119,9 @@ bool march_slots_fit(const Scratch& held, size_t need) {
 
 // The gather's dense vertex copies: every level with 2 <= R and R^3 <= FFN_DENSE_MAX_CELLS (default 2^21:
 // 16 MB at F = 2 in fp32) vertices gets one, filled from `table` on the stream (they follow the table, so
-// they are rebuilt before every gather that follows a table update).  At the benchmark shape the copies of
-// levels 0-6 (res 16-111) take the gather from 5.22 to 4.61 ms; adding level 7 (res 154, 29 MB) measured
-// 4.71, all levels up to res 406 6.24 ms.
+// they are rebuilt before every gather that follows a table update).  At the benchmark shape the row-major
+// copies of levels 0-6 (res 16-111) took the gather from 5.22 to 4.61 ms (adding level 7, res 154, 4.71;
+// all levels up to res 406 6.24); with levels 5-6 bricked 4.42 (level 7 bricked as well: no change).
 hipError_t build_dense_levels(Handle* h, const void* table, ffn::DenseLevels* dl, hipStream_t st) {
   const char* env = getenv("FFN_DENSE_MAX_CELLS");
   const long long max_cells = env ? atoll(env) : (1ll << 21);
@@ -130,14 +130,20 @@ hipError_t build_dense_levels(Handle* h, const void* table, ffn::DenseLevels* dl
   uint64_t total = 0;
   for (int l = 0; l < FFN_MAX_LEVELS; ++l) dl->off[l] = ffn::DENSE_NONE;
   dl->n_multi = 0;
+  dl->bricked = 0u;
   bool leading = true;
   for (int l = 0; l < c.L; ++l) {
     const long long R = c.res[l];
     if (R >= 2 && R * R * R <= max_cells) {
+      // copies of at most 2 MiB are row-major and the leading ones share one gather pass
+      // (FFN_DENSE_MULTI=0: none); larger copies are bricked (4x4x4 vertices, the grid padded to whole bricks)
+      const bool small = (size_t)(R * R * R) * (size_t)c.F * elem <= ((size_t)2 << 20);
+      const long long NB = (R + 3) / 4;
+      const long long cells = small ? R * R * R : NB * NB * NB * 64;
       dl->off[l] = (uint32_t)total;
-      total += (uint64_t)((R * R * R + 63) & ~63ll);  // each level's copy starts 256-byte aligned
-      // the leading levels whose copies are at most 2 MiB each share one gather pass (FFN_DENSE_MULTI=0: none)
-      if (leading && (size_t)(R * R * R) * (size_t)c.F * elem <= ((size_t)2 << 20)) ++dl->n_multi;
+      total += (uint64_t)((cells + 63) & ~63ll);  // each level's copy starts 256-byte aligned
+      if (!small) dl->bricked |= 1u << l;
+      if (leading && small) ++dl->n_multi;
       else leading = false;
     } else {
       leading = false;

@@ -127,24 +127,40 @@ __device__ __forceinline__ void sample_position(const PosSrc& s, int64_t b, floa
 // forward
 
 // Dense copies of the coarse levels.  A level whose R^3 vertices are few gets its vertex values copied
-// out of the hash table before the gather, in vertex order: there the eight corners of a cell are four
-// pairs of x-neighbours, each pair adjacent in memory (one load where the pair fits 16 bytes), and the 64
-// samples of a wavefront, one ray, walk through neighbouring cells, so a load instruction touches a few
-// lines instead of 64 random ones, and no corner is hashed.  The values are the table's, so the gather
-// is unchanged bit for bit.
+// out of the hash table before the gather, in vertex order: the 64 samples of a wavefront, one ray, walk
+// through neighbouring cells, so a load instruction touches a few lines instead of 64 random ones, and no
+// corner is hashed.  Small copies are row-major ([z][y][x]: the eight corners of a cell are four pairs of
+// x-neighbours, each pair one load where it fits 16 bytes); larger ones (bricked) are stored in 4x4x4
+// bricks of 64 vertices, [brick z][y][x][z & 3][y & 3][x & 3], so that the corners of a cell and the cells
+// a ray crosses share lines in every direction, not only along x.  The values are the table's, so the
+// gather is unchanged bit for bit.
 template <int F, typename TT>
 __global__ __launch_bounds__(256) void k_hash_densify(DevCfg c, const TT* __restrict__ table, DenseLevels dl) {
   const int l = (int)blockIdx.y;
   if (dl.off[l] == DENSE_NONE) return;
   const uint32_t R = (uint32_t)c.res[l];
-  const uint32_t cells = R * R * R;
+  const bool brick = (dl.bricked >> l) & 1u;
+  const uint32_t NB = (R + 3) / 4;
+  const uint32_t cells = brick ? NB * NB * NB * 64 : R * R * R;
   TT* __restrict__ grid = static_cast<TT*>(dl.grid) + (size_t)dl.off[l] * F;
   const uint32_t base = c.offset[l], mask = c.mask[l];
   for (uint32_t v = blockIdx.x * blockDim.x + threadIdx.x; v < cells; v += gridDim.x * blockDim.x) {
-    const uint32_t x = v % R, y = (v / R) % R, z = v / (R * R);
-    const uint32_t e = (base + level_entry(x, y, z, l, mask)) * (uint32_t)F;
+    uint32_t x, y, z;
+    if (brick) {
+      const uint32_t b = v >> 6, i = v & 63;
+      x = (b % NB) * 4 + (i & 3);
+      y = ((b / NB) % NB) * 4 + ((i >> 2) & 3);
+      z = (b / (NB * NB)) * 4 + (i >> 4);
+    } else {
+      x = v % R;
+      y = (v / R) % R;
+      z = v / (R * R);
+    }
+    if (x < R && y < R && z < R) {
+      const uint32_t e = (base + level_entry(x, y, z, l, mask)) * (uint32_t)F;
 #pragma unroll
-    for (int f = 0; f < F; ++f) grid[(size_t)v * F + f] = table[e + f];
+      for (int f = 0; f < F; ++f) grid[(size_t)v * F + f] = table[e + f];
+    }
   }
 }
 
@@ -181,7 +197,25 @@ __device__ __forceinline__ void gather_level(const DevCfg& c, const float (&p)[3
   const uint32_t mask = c.mask[l], off = c.offset[l];
   uint32_t fb[8];
   V val[8];
-  if (dl.off[l] != DENSE_NONE) {  // the same for the whole block
+  if (dl.off[l] != DENSE_NONE && ((dl.bricked >> l) & 1u)) {
+    const uint32_t NB = ((uint32_t)c.res[l] + 3) / 4;
+    uint32_t X[2], Y[2], Z[2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const uint32_t cx = (uint32_t)lc.i0[0] + d, cy = (uint32_t)lc.i0[1] + d, cz = (uint32_t)lc.i0[2] + d;
+      X[d] = (cx >> 2) * 64 + (cx & 3);
+      Y[d] = (cy >> 2) * (NB * 64) + (cy & 3) * 4;
+      Z[d] = (cz >> 2) * (NB * NB * 64) + (cz & 3) * 16;
+    }
+    const TT* g = static_cast<const TT*>(dl.grid) + (size_t)dl.off[l] * F;
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc)
+      val[cc] = *reinterpret_cast<const V*>(g + (size_t)(X[cc & 1] + Y[(cc >> 1) & 1] + Z[cc >> 2]) * F);
+    if (idx_out) {
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) fb[cc] = (off + corner_entry(lc, cc, l, mask)) * (uint32_t)F;
+    }
+  } else if (dl.off[l] != DENSE_NONE) {  // the same for the whole block
     const size_t R = (size_t)c.res[l];
     const TT* g = static_cast<const TT*>(dl.grid) +
                   ((size_t)dl.off[l] + ((size_t)lc.i0[2] * R + (size_t)lc.i0[1]) * R + (size_t)lc.i0[0]) * F;
@@ -847,6 +881,7 @@ hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
   DenseLevels none{};
   none.grid = nullptr;
   none.n_multi = 0;
+  none.bricked = 0u;
   for (int l = 0; l < FFN_MAX_LEVELS; ++l) none.off[l] = DENSE_NONE;
   const DenseLevels& d = (dl && dl->grid) ? *dl : none;
   if (c.table_f16)
@@ -859,8 +894,9 @@ static hipError_t launch_densify_t(const DevCfg& c, const TT* table, const Dense
   uint32_t max_cells = 0;
   for (int l = 0; l < c.L; ++l)
     if (dl.off[l] != DENSE_NONE) {
-      const uint32_t R = (uint32_t)c.res[l];
-      max_cells = R * R * R > max_cells ? R * R * R : max_cells;
+      const uint32_t R = (uint32_t)c.res[l], NB = (R + 3) / 4;
+      const uint32_t cells = ((dl.bricked >> l) & 1u) ? NB * NB * NB * 64 : R * R * R;
+      max_cells = cells > max_cells ? cells : max_cells;
     }
   if (max_cells == 0) return hipSuccess;
   const unsigned bx = (unsigned)((max_cells + 255) / 256 < 2048 ? (max_cells + 255) / 256 : 2048);

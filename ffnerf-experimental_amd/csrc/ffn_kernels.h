@@ -152,13 +152,16 @@ hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays,
                          hipStream_t st);
 
 // table: float, or binary16 when c.table_f16 (widened exactly; the sums are the same fp32 operations)
-// Dense copies of the coarse levels' vertex values: level l's vertex (x, y, z) at grid[(off[l] + (z R + y) R
-// + x) F ..] (the table's element type), or off[l] = DENSE_NONE for a level read through its hash
+// Dense copies of the coarse levels' vertex values (the table's element type, F per vertex) from
+// grid + off[l] F: row-major, vertex (x, y, z) at (z R + y) R + x, or, for a level whose bit is set in
+// `bricked`, in 4x4x4 bricks: ((z/4 NB + y/4) NB + x/4) 64 + (z%4) 16 + (y%4) 4 + x%4 (NB = ceil(R/4));
+// off[l] = DENSE_NONE for a level read through its hash
 constexpr uint32_t DENSE_NONE = 0xFFFFFFFFu;
 struct DenseLevels {
   void* grid;
   uint32_t off[FFN_MAX_LEVELS];
-  int n_multi;  // levels 0 .. n_multi - 1 (all with dense copies) are gathered together in one pass
+  int n_multi;       // levels 0 .. n_multi - 1 (all with row-major copies) are gathered together in one pass
+  uint32_t bricked;  // bit l: level l's copy is bricked
 };
 // fill the dense copies from the table (every level with off[l] != DENSE_NONE)
 hipError_t launch_hash_densify(const DevCfg& c, const void* table, const DenseLevels& dl, hipStream_t st);
