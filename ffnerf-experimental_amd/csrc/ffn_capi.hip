@@ -82,6 +82,7 @@ struct Handle {
   // marched training
   Scratch m_Tr, m_dLds, m_dLdc;
   Scratch m_bits;  // the bitfield of ffn_train_step's march sampler
+  Scratch m_blocks;  // the march's summary of the bitfield per 8^3 block, and its use flag
   Scratch m_slots;  // the marched step's per-ray sample slots (one walk instead of count + emit)
   Scratch dense;    // dense vertex copies of the coarse levels (the gather's)
   uint32_t* host_total = nullptr;  // pinned
@@ -436,7 +437,7 @@ int ffn_destroy(void* handle) {
   h->bin_max.release();
   for (Scratch* sc : {&h->m_state, &h->m_acc, &h->m_counts, &h->m_offsets, &h->m_sums, &h->m_total, &h->m_samples,
                       &h->m_ids, &h->m_a0, &h->m_sigma, &h->m_rgb, &h->m_Tr, &h->m_dLds, &h->m_dLdc, &h->m_bits,
-                      &h->m_slots, &h->dense})
+                      &h->m_blocks, &h->m_slots, &h->dense})
     sc->release();
   if (h->host_total) (void)hipHostFree(h->host_total);
   delete h;
@@ -764,6 +765,26 @@ ffn::MarchArgs march_args(Handle* h, const void* rays, uint32_t num_rays, const 
   return a;
 }
 
+// The walk crosses empty 8^3 blocks in one step from a summary of the bitfield built here, on the stream, for
+// this call's bitfield, when at least half the blocks are empty (decided on the device; FFN_MARCH_BLOCKS=0: no
+// summary, every cell walked).  The samples are the same either way.
+hipError_t set_march_blocks(Handle* h, ffn::MarchArgs& a, hipStream_t st) {
+  const char* env = getenv("FFN_MARCH_BLOCKS");
+  a.blocks = a.blocks_use = nullptr;
+  if (env && env[0] == '0') return hipSuccess;
+  const size_t NB = ((size_t)a.res + 7) / 8;
+  const size_t words = (NB * NB * NB + 31) / 32;
+  hipError_t e = h->m_blocks.ensure(sizeof(uint32_t) * (words + 1));
+  if (e != hipSuccess) return e;
+  uint32_t* b = (uint32_t*)h->m_blocks.p;
+  e = ffn::launch_occ_blocks(a.bits, a.res, b, b + words, st);
+  if (e == hipSuccess) {
+    a.blocks = b;
+    a.blocks_use = b + words;
+  }
+  return e;
+}
+
 }  // namespace
 
 int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits, const ffn_march_params* mp,
@@ -776,6 +797,7 @@ int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t*
   if (num_rays == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
+  FFN_HIP(set_march_blocks(h, a, st));
   a.counts = counts;
   FFN_HIP(ffn::launch_march(a, false, st));
   // offsets needs num_rays + 1 slots for the scan's total; use the handle's buffer for it
@@ -858,6 +880,7 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   uint32_t* counts = (uint32_t*)h->m_counts.p;
   uint32_t* off = (uint32_t*)h->m_offsets.p;
   ffn::MarchArgs ma = march_args(h, rays, num_rays, bits, mp);
+  FFN_HIP(set_march_blocks(h, ma, st));
   ma.counts = counts;
   int64_t n = 0;
   {
@@ -1085,6 +1108,7 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   float* rgb = (float*)h->m_rgb.p;
   FFN_HIP(ffn::launch_march_init(state, acc, n_samples, num_rays, st));
   ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
+  FFN_HIP(set_march_blocks(h, a, st));
   a.chunk = mp->chunk;
   a.state = state;
   a.counts = counts;

@@ -208,9 +208,14 @@ struct MarchArgs {
   uint64_t capacity;         // slots of samples / ray_ids
   uint32_t slot_stride;      // emit pass into per-ray slots: ray r's samples at r * slot_stride (and its count
                              // written as the count pass does); 0: at offsets[r]
+  const uint32_t* blocks;     // summary of `bits` per 8^3 block (launch_occ_blocks), or NULL: no block skipping
+  const uint32_t* blocks_use;  // with it: the walk skips blocks when *blocks_use != 0
 };
 
 hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint32_t* bits, hipStream_t st);
+// one bit per 8^3 block of cells (x fastest, ceil(R / 8) blocks per axis), set when any cell of the block is
+// occupied; *use = 1 when at least half the blocks are empty, else 0
+hipError_t launch_occ_blocks(const uint32_t* bits, int R, uint32_t* blocks, uint32_t* use, hipStream_t st);
 hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st);
 // per-ray slots (ray r's counts[r] samples at slots + r * stride) -> the compacted order (offsets), with ray ids
 hipError_t launch_march_compact(const uint32_t* counts, const uint32_t* offsets, const float4* slots,

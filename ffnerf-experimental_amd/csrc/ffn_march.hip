@@ -16,6 +16,18 @@
 //   * One lane per ray.  Empty cells are skipped in one step: the first lattice
 //     index past the cell's exit is computed directly and corrected to the exact
 //     index the one-by-one walk of the specification reaches.
+//   * Empty 8^3 blocks are crossed in one step: a summary (one bit per block,
+//     4 KiB at 256^3) marks the blocks with any occupied cell, and in an empty
+//     block the walk moves straight to the first cell past the block -- the
+//     same cell, lattice index and step count the one-cell-at-a-time walk
+//     reaches, because every crossing of a cell boundary is an event ordered
+//     by (time, axis) and the block's first face event and the interior events
+//     before it follow from the same boundary-time formula.  A jump costs
+//     several cell steps and diverges from the lanes that step cells, so the
+//     walk uses the summary only when at least half the blocks are empty (a
+//     flag computed on the device with it): a field with isolated occupied
+//     cells scattered everywhere, where nearly every block holds one, walks
+//     cell by cell.
 //   * Compaction: one walk writes each ray's samples to its own fixed run of
 //     slots (max_steps, or the chunk, per ray) and its count; a scan of the
 //     counts and a wavefront-per-ray copy pack them.  Where those slots do not
@@ -47,7 +59,67 @@ __global__ __launch_bounds__(256) void k_occ_bitfield(const uint32_t* __restrict
   bits[w] = out;
 }
 
+// Block summary: bit (bx + NB (by + NB bz)) of `blocks` is set when any cell of the 8^3 block (bx, by, bz) is
+// occupied (NB = ceil(R / 8); the last block of an axis is partial when 8 does not divide R).  One lane per
+// block, 64 blocks (two words) per wavefront.
+__global__ __launch_bounds__(256) void k_occ_blocks(const uint32_t* __restrict__ bits, int R,
+                                                    uint32_t* __restrict__ blocks, int64_t n_blocks) {
+  constexpr int B = 8;
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int NB = (R + B - 1) / B;
+  bool any = false;
+  if (b < n_blocks) {
+    const int bx = (int)(b % NB), by = (int)((b / NB) % NB), bz = (int)(b / ((int64_t)NB * NB));
+    const int x0 = B * bx, n = (R - x0 < B ? R - x0 : B);
+    const uint32_t mask = (1u << n) - 1u;
+    const int y1 = (B * by + B < R ? B * by + B : R), z1 = (B * bz + B < R ? B * bz + B : R);
+    uint32_t acc = 0;
+    for (int z = B * bz; z < z1; ++z)
+      for (int y = B * by; y < y1; ++y) {
+        const int64_t i0 = x0 + (int64_t)R * (y + (int64_t)R * z);
+        const uint32_t sh = (uint32_t)(i0 & 31);
+        uint32_t w = bits[i0 >> 5] >> sh;
+        if (sh + (uint32_t)n > 32u) w |= bits[(i0 >> 5) + 1] << (32u - sh);
+        acc |= w & mask;
+      }
+    any = acc != 0;
+  }
+  const uint64_t bal = __ballot(any);
+  const int lane = threadIdx.x & 63;
+  const int64_t w0 = (b - lane) >> 5;  // the wavefront's first word (64 blocks, 64-aligned)
+  const int64_t n_words = (n_blocks + 31) >> 5;
+  if (lane == 0 && w0 < n_words) blocks[w0] = (uint32_t)bal;
+  if (lane == 32 && w0 + 1 < n_words) blocks[w0 + 1] = (uint32_t)(bal >> 32);
+}
+
+// *use = 1 when at least half of the n_blocks summary bits are clear (one workgroup; fixed-order sum)
+__global__ __launch_bounds__(256) void k_blocks_use(const uint32_t* __restrict__ blocks, int64_t n_blocks,
+                                                    uint32_t* __restrict__ use) {
+  __shared__ uint32_t part[256];
+  const int64_t n_words = (n_blocks + 31) >> 5;
+  uint32_t c = 0;
+  for (int64_t w = threadIdx.x; w < n_words; w += 256) c += (uint32_t)__popc(blocks[w]);
+  part[threadIdx.x] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t t = 0;
+    for (int i = 0; i < 256; ++i) t += part[i];
+    use[0] = 2 * t <= (uint64_t)n_blocks ? 1u : 0u;
+  }
+}
+
 __device__ __forceinline__ float lattice_t(float t0, uint32_t k, float dt) { return t0 + ((float)k + 0.5f) * dt; }
+
+// the first lattice index k' >= k with t_k' >= t_exit, as the one-cell-at-a-time walk reaches it
+__device__ __forceinline__ uint32_t skip_lattice(float t0, uint32_t k, float dt, float t_exit) {
+  if (!(lattice_t(t0, k, dt) < t_exit)) return k;
+  float est = ceilf((t_exit - t0) / dt - 0.5f);
+  uint32_t ke = k + 1;
+  if (est > (float)ke) ke = est < 4.0e9f ? (uint32_t)est : 4000000000u;
+  while (ke > k + 1 && !(lattice_t(t0, ke - 1, dt) < t_exit)) --ke;
+  while (lattice_t(t0, ke, dt) < t_exit) ++ke;
+  return ke;
+}
 
 // Rays per wavefront of k_march.  A lane walks one ray at a time and, when that ray is finished (or paused at
 // the chunk budget), takes the next unclaimed ray of its wavefront's range: walks are 37 % as long as
@@ -119,9 +191,74 @@ struct RayWalk {
     return true;
   }
 
-  // one cell of the walk; returns true when the ray is finished or paused for this call
-  __device__ __forceinline__ bool advance(const MarchArgs& a, const float (&cell)[3]) {
+  // The current cell's 8^3 block is empty: move to the first cell past it.  Every boundary crossing of the
+  // one-cell-at-a-time walk is an event (time, axis) -- the walk takes the smallest time, the lower axis on
+  // ties, and the ray's end t1 before any axis at equal time -- and an axis' crossing times do not decrease
+  // along it.  So the walk leaves the block by the first of the block's faces in that order (or ends inside
+  // it at t1), after exactly the interior crossings that precede that event; each time below is the walk's
+  // own formula for the same boundary.  The caller guarantees at least 24 steps of iteration budget.
+  __device__ __forceinline__ bool jump_block(const MarchArgs& a, const float (&cell)[3]) {
+    constexpr int B = 8;
     const int R = a.res;
+    int face[3];
+    float e_best = t1;
+    int j_best = -1;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int b0 = cc[i] & ~(B - 1), b1 = (b0 + B - 1 < R - 1 ? b0 + B - 1 : R - 1);
+      face[i] = step[i] > 0 ? b1 : b0;
+      if (step[i] == 0) continue;
+      const float bound = a.bmin[i] + (float)(face[i] + (step[i] > 0 ? 1 : 0)) * cell[i];
+      const float te = (bound - o[i]) * invd[i];
+      if (te < e_best) {
+        e_best = te;
+        j_best = i;
+      }
+    }
+    int n_steps = 0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (step[i] == 0) continue;
+      if (i == j_best) {
+        n_steps += (face[i] - cc[i]) * step[i] + 1;
+        cc[i] = face[i] + step[i];
+        continue;
+      }
+      // this axis' crossings before the exit event (at most B - 1: its own face comes after that event)
+      int c = cc[i];
+      for (;;) {
+        const float bound = a.bmin[i] + (float)(c + (step[i] > 0 ? 1 : 0)) * cell[i];
+        const float te = (bound - o[i]) * invd[i];
+        if (!(te < e_best || (te == e_best && i < j_best))) break;
+        c += step[i];
+        ++n_steps;
+      }
+      cc[i] = c;
+    }
+    k = skip_lattice(t0, k, a.dt, e_best);
+    if (j_best < 0) {  // the ray ends inside the block
+      done = true;
+      return true;
+    }
+    if (cc[j_best] < 0 || cc[j_best] >= R) {
+      done = true;
+      return true;
+    }
+    iter += n_steps;
+    return false;
+  }
+
+  // one cell of the walk; returns true when the ray is finished or paused for this call
+  __device__ __forceinline__ bool advance(const MarchArgs& a, const float (&cell)[3], bool use_blocks) {
+    const int R = a.res;
+    // the cell's bit and its block's bit, loaded together
+    const int64_t bi = cc[0] + (int64_t)R * (cc[1] + (int64_t)R * cc[2]);
+    const uint32_t wcell = a.bits[bi >> 5];
+    if (use_blocks && iter + 24 < 3 * R + 2) {
+      const int NB = (R + 7) >> 3;
+      const int64_t bb = (cc[0] >> 3) + (int64_t)NB * ((cc[1] >> 3) + (int64_t)NB * (cc[2] >> 3));
+      if (!((a.blocks[bb >> 5] >> (bb & 31)) & 1u)) return jump_block(a, cell);
+    }
     float t_exit = t1;
     int axis = -1;
 #pragma unroll
@@ -134,8 +271,7 @@ struct RayWalk {
         axis = i;
       }
     }
-    const int64_t bi = cc[0] + (int64_t)R * (cc[1] + (int64_t)R * cc[2]);
-    const bool occ = (a.bits[bi >> 5] >> (bi & 31)) & 1u;
+    const bool occ = (wcell >> (bi & 31)) & 1u;
     if (occ) {
       for (;;) {
         const float tk = lattice_t(t0, k, a.dt);
@@ -159,14 +295,9 @@ struct RayWalk {
         ++k;
       }
       if (done || paused) return true;
-    } else if (lattice_t(t0, k, a.dt) < t_exit) {
+    } else {
       // skip the empty cell: the first k with t_k >= t_exit, exactly as the one-by-one walk finds it
-      float est = ceilf((t_exit - t0) / a.dt - 0.5f);
-      uint32_t ke = k + 1;
-      if (est > (float)ke) ke = est < 4.0e9f ? (uint32_t)est : 4000000000u;
-      while (ke > k + 1 && !(lattice_t(t0, ke - 1, a.dt) < t_exit)) --ke;
-      while (lattice_t(t0, ke, a.dt) < t_exit) ++ke;
-      k = ke;
+      k = skip_lattice(t0, k, a.dt, t_exit);
     }
     if (axis < 0) {
       done = true;
@@ -217,6 +348,7 @@ __global__ __launch_bounds__(256) void k_march(MarchArgs a) {
   float cell[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) cell[i] = (a.bmax[i] - a.bmin[i]) / (float)a.res;
+  const bool use_blocks = a.blocks && *a.blocks_use != 0u;  // the same for every lane
   uint32_t next = (uint32_t)r_begin;  // the wavefront's next unclaimed ray
   RayWalk<EMIT> w;
   bool have = false;  // this lane walks a ray
@@ -242,7 +374,7 @@ __global__ __launch_bounds__(256) void k_march(MarchArgs a) {
     // a few cells per lane between claims: the claim's wavefront-wide bookkeeping is paid once per batch
 #pragma unroll 1
     for (int j = 0; j < MARCH_CELLS_PER_CLAIM; ++j) {
-      if (have && w.advance(a, cell)) {
+      if (have && w.advance(a, cell, use_blocks)) {
         w.finish_state(a, true);
         if (!EMIT || a.slot_stride) a.counts[w.r] = w.emitted;
         have = false;
@@ -397,6 +529,15 @@ hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint3
   const int64_t n_words = (R * R * R + 31) / 32;
   hipLaunchKernelGGL(k_occ_bitfield, dim3((unsigned)((n_words + 255) / 256)), dim3(256), 0, st, occ, G, q_min,
                      bits, n_words);
+  return hipGetLastError();
+}
+
+hipError_t launch_occ_blocks(const uint32_t* bits, int R, uint32_t* blocks, uint32_t* use, hipStream_t st) {
+  const int64_t NB = (R + 7) / 8;
+  const int64_t n_blocks = NB * NB * NB;
+  hipLaunchKernelGGL(k_occ_blocks, dim3((unsigned)((n_blocks + 255) / 256)), dim3(256), 0, st, bits, R, blocks,
+                     n_blocks);
+  hipLaunchKernelGGL(k_blocks_use, dim3(1), dim3(256), 0, st, blocks, n_blocks, use);
   return hipGetLastError();
 }
 

@@ -21,12 +21,12 @@ def gm():
     return GpuModel(SPEC, p), p
 
 
-def shell_bits(R, seed=0, frac=0.02):
+def shell_bits(R, seed=0, frac=0.02, half_width=0.06):
     rng = np.random.default_rng(seed)
     c = (np.arange(R) + 0.5) / R
     z, y, x = np.meshgrid(c, c, c, indexing="ij")
     rad = np.sqrt((x - 0.5) ** 2 + (y - 0.5) ** 2 + (z - 0.5) ** 2)
-    occ = (np.abs(rad - 0.3) <= 0.06) | (rng.random((R, R, R)) < frac)
+    occ = (np.abs(rad - 0.3) <= half_width) | (rng.random((R, R, R)) < frac)
     idx = np.nonzero(occ.reshape(-1))[0]
     bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
     np.bitwise_or.at(bits, idx >> 5, (np.uint32(1) << (idx & 31).astype(np.uint32)))
@@ -43,21 +43,46 @@ def test_bitfield_bit_exact(gm):
             np.testing.assert_array_equal(g.bitfield(occ, G, q_min), ora.occ_bitfield(occ, G, q_min))
 
 
-@pytest.mark.parametrize("R,max_steps", [(32, 4096), (32, 7), (64, 300)])
-def test_march_bit_exact(gm, R, max_steps):
+def special_rays(R):
+    """Rays the walk finds hard: axis-aligned (two direction components zero), along face diagonals and the
+    space diagonal from origins on cell corners (boundary crossings at equal times on two or three axes), and
+    from inside the box (the walk starts in the cell of t_near)."""
+    rays = []
+    dirs = [(1, 0, 0), (0, -1, 0), (0, 0, 1), (1, 1, 0), (0, -1, 1), (1, 1, 1), (-1, 1, -1), (1, 2, 0), (3, 1, 2)]
+    rng = np.random.default_rng(R)
+    for d in dirs:
+        d = np.array(d, np.float64)
+        d /= np.linalg.norm(d)
+        for _ in range(12):
+            corner = rng.integers(0, R + 1, 3) / R  # a cell corner inside or on the box
+            for o in (corner - 2.0 * d, corner - 0.5 * d, corner):
+                r = np.zeros(8, np.float32)
+                r[:3] = o
+                r[3] = 1.0
+                r[4:7] = d
+                rays.append(r)
+    return np.array(rays, np.float32)
+
+
+# (R, max_steps, random-cell fraction, shell half width): the sparse fields leave most 8^3 blocks empty, so
+# the walk crosses them in one step; R = 44 has partial blocks at the grid's far faces
+@pytest.mark.parametrize("R,max_steps,frac,hw", [(32, 4096, 0.02, 0.06), (32, 7, 0.02, 0.06), (64, 300, 0.02, 0.06),
+                                                 (64, 4096, 0.0, 0.03), (44, 4096, 0.0003, 0.02),
+                                                 (128, 9, 0.0, 0.02)])
+def test_march_bit_exact(gm, R, max_steps, frac, hw):
     import ffn_lib as fl
     g, _ = gm
-    bits = shell_bits(R, seed=R)
+    bits = shell_bits(R, seed=R, frac=frac, half_width=hw)
     dt = np.float32(np.sqrt(3.0) / 256)
-    rays = look_at_rays(1500, SPEC, seed=R + max_steps)
-    print(f"[march] R={R} max_steps={max_steps}", flush=True)
+    rays = np.concatenate([look_at_rays(1500, SPEC, seed=R + max_steps), special_rays(R)])
+    print(f"[march] R={R} max_steps={max_steps} frac={frac} hw={hw}", flush=True)
     counts, offsets, samples, ids, total = g.march(rays, bits, fl.march_params(R, dt, max_steps))
     cfg = ora.make_cfg(SPEC)
     m = ora.march_cfg(R, dt, max_steps)
     ref = [ora.march_ray(cfg, m, bits, r) for r in rays]
     np.testing.assert_array_equal(counts, [len(t) for t in ref])
     np.testing.assert_array_equal(offsets, np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint32))
-    assert total == int(counts.sum()) and total > 1000
+    assert total == int(counts.sum()) and total > 200
     for r, t in enumerate(ref):
         sl = slice(int(offsets[r]), int(offsets[r]) + len(t))
         np.testing.assert_array_equal(samples[sl, 3], t)
@@ -130,3 +155,43 @@ def test_render_one_walk_equals_two_walks(monkeypatch):
         np.testing.assert_array_equal(res[0][0], res[1][0])
         np.testing.assert_array_equal(res[0][1], res[1][1])
         assert res[0][1].sum() > 2000
+
+
+def test_march_block_skip_changes_no_sample(gm, monkeypatch):
+    """The walk crosses empty 8^3 blocks in one step (a block summary of the bitfield, used when at least half
+    the blocks are empty): the counts, samples and ray ids are bit-identical with the summary off
+    (FFN_MARCH_BLOCKS=0) on a 256^3 field (a thin shell and sparse random cells, most blocks empty) with ordinary
+    and tie-prone rays, and against the oracle; the render's image and samples used as well."""
+    import ffn_lib as fl
+    g, _ = gm
+    R = 256
+    bits = shell_bits(R, seed=41, frac=0.0003, half_width=0.01)
+    # most 8^3 blocks are empty, so the walk takes the block summary (it does when at least half are)
+    idx = np.arange(R ** 3, dtype=np.int64)
+    occ = ((bits[idx >> 5] >> (idx & 31).astype(np.uint32)) & 1).astype(bool).reshape(R // 8, 8, R // 8, 8, R // 8, 8)
+    assert occ.any(axis=(1, 3, 5)).mean() < 0.3
+    dt = np.float32(np.sqrt(3.0) / 1024)
+    rays = np.concatenate([look_at_rays(3000, SPEC, seed=42), special_rays(R)])
+    mp = fl.march_params(R, dt, 1024)
+    print(f"[march blocks on/off] R={R} rays={len(rays)}", flush=True)
+    res = []
+    for env in ("1", "0"):
+        monkeypatch.setenv("FFN_MARCH_BLOCKS", env)
+        res.append(g.march(rays, bits, mp))
+    for a, b in zip(res[0], res[1]):
+        np.testing.assert_array_equal(a, b)
+    counts, offsets, samples = res[0][0], res[0][1], res[0][2]
+    assert res[0][4] > 10000
+    cfg = ora.make_cfg(SPEC)
+    m = ora.march_cfg(R, dt, 1024)
+    for r in range(0, len(rays), 7):
+        t = ora.march_ray(cfg, m, bits, rays[r])
+        assert counts[r] == len(t)
+        np.testing.assert_array_equal(samples[int(offsets[r]):int(offsets[r]) + len(t), 3], t)
+    # the render's rounds resume each ray from its saved walk state: the same image and samples used
+    out = []
+    for env in ("1", "0"):
+        monkeypatch.setenv("FFN_MARCH_BLOCKS", env)
+        out.append(g.render(rays, bits, fl.march_params(R, dt, 1024, T_stop=1e-2, chunk=16)))
+    np.testing.assert_array_equal(out[0][0], out[1][0])
+    np.testing.assert_array_equal(out[0][1], out[1][1])
