@@ -138,6 +138,11 @@ struct RayWalk {
   uint32_t r, k, emitted;
   uint64_t base;
   int iter;
+  // Exit time of the last empty cell walked, not yet applied to k.  The one-cell-at-a-time walk moves k past
+  // every empty cell's exit time; those times never decrease along the walk and k' = first index >= k with
+  // t_k' >= t is the same whether applied once per cell or once for the last cell of a run, so k is brought up
+  // to date only where it is used: on entering an occupied cell and when the walk state is saved.
+  float t_pend;
   bool done, paused;
 
   // claim ray rr; returns false when the ray has nothing to walk (it is then already finished)
@@ -145,6 +150,7 @@ struct RayWalk {
     r = rr;
     emitted = 0;
     iter = 0;
+    t_pend = -__builtin_huge_valf();
     done = false;
     paused = false;
     st = a.state ? a.state[r] : MarchState{0u, 0u, 0u, MARCH_FRESH};
@@ -235,7 +241,7 @@ struct RayWalk {
       }
       cc[i] = c;
     }
-    k = skip_lattice(t0, k, a.dt, e_best);
+    t_pend = e_best;  // k past the block's cells, where it is next used
     if (j_best < 0) {  // the ray ends inside the block
       done = true;
       return true;
@@ -273,6 +279,7 @@ struct RayWalk {
     }
     const bool occ = (wcell >> (bi & 31)) & 1u;
     if (occ) {
+      k = skip_lattice(t0, k, a.dt, t_pend);
       for (;;) {
         const float tk = lattice_t(t0, k, a.dt);
         if (!(tk < t_exit)) break;
@@ -296,8 +303,7 @@ struct RayWalk {
       }
       if (done || paused) return true;
     } else {
-      // skip the empty cell: the first k with t_k >= t_exit, exactly as the one-by-one walk finds it
-      k = skip_lattice(t0, k, a.dt, t_exit);
+      t_pend = t_exit;  // skip the empty cell (k is brought past t_exit where it is next used)
     }
     if (axis < 0) {
       done = true;
@@ -328,7 +334,7 @@ struct RayWalk {
   __device__ __forceinline__ void finish_state(const MarchArgs& a, bool walked) {
     if (EMIT && a.state) {
       if (walked) {
-        st.k = k;
+        st.k = skip_lattice(t0, k, a.dt, t_pend);
         st.cell = (uint32_t)cc[0] | ((uint32_t)cc[1] << 10) | ((uint32_t)cc[2] << 20);
       }
       st.n += emitted;
