@@ -246,7 +246,11 @@ struct RayWalk {
       done = true;
       return true;
     }
-    if (cc[j_best] < 0 || cc[j_best] >= R) {
+    bool out = false;  // static indices: a dynamic cc[j_best] would put the walk state in scratch memory
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (i == j_best) out = cc[i] < 0 || cc[i] >= R;
+    if (out) {
       done = true;
       return true;
     }
