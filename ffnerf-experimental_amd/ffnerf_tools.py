@@ -243,6 +243,13 @@ def spec_dict(spec: ModelSpec, occ: OccParams) -> dict:
     )
 
 
+def occ_decay_q24(strength: float, decay: float) -> int:
+    """The occupancy decay factor 1 - strength (1 - decay) in 24-bit fixed point, rounded half to even and
+    clamped to [0, 2^24] (ffnerf_tools.py:1453-1457): 2^24 leaves every level as it is, 0 clears it."""
+    d = 1 - float(strength) * (1 - float(decay))
+    return max(0, min(int(round(d * (1 << 24))), 1 << 24))
+
+
 def init_params(spec: ModelSpec, occ: OccParams, rng: np.random.Generator) -> dict:
     """Fresh parameters (float32 numpy), draw order of Nerf._init_fresh
     (ffnerf_tools.py:836-895): table, then weights, then biases."""
@@ -487,9 +494,7 @@ class Nerf:
         # the march sampler makes no proposals, so the grid it reads is not decayed either
         if (do_train and float(occ_update_strength) > 0.0 and self.spec.sampler != "march"
                 and self.steps_trained % int(self.occ.maintenance_period) == 0):
-            d = 1 - float(occ_update_strength) * (1 - float(self.occ.decay))
-            decay_q24 = int(round(d * (1 << 24)))
-            decay_q24 = max(0, min(decay_q24, 1 << 24))
+            decay_q24 = occ_decay_q24(occ_update_strength, self.occ.decay)
             n_words = int(self.occ.G_occ) ** 3
             fl.check(lib.ffn_occ_decay(fl.ptr(self.t["occ_in"]), fl.ptr(self.t["occ_st"]), n_words, decay_q24,
                                        int(rng_u32) & 0xFFFFFFFF, sp), "ffn_occ_decay")

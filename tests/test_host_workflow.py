@@ -127,6 +127,52 @@ def test_schedules_closed_form():
     assert [trainer.color_rel_lr(s) for s in (0, 1500, 2250, 3000)] == [0.15, 0.15, 0.15 + 0.85 * 0.5, 1.0]
 
 
+def test_adam_lr_t_is_the_bias_correction():
+    """lr_t folds Adam's bias corrections into the step size: p - lr_t m / (sqrt(v) + eps) with the raw moments
+    equals p - lr m_hat / (sqrt(v_hat) + eps_hat) with m_hat = m / (1 - b1^t), v_hat = v / (1 - b2^t) and
+    eps_hat = eps / sqrt(1 - b2^t) (Kingma & Ba, section 2).  Checked by running both forms in float64 on a
+    gradient sequence; lr_t itself is float32, so the two agree to float32 rounding."""
+    from types import SimpleNamespace
+    stub = SimpleNamespace(spec=SimpleNamespace(beta1=0.9, beta2=0.99))
+    b1, b2, lr, eps = float(np.float32(0.9)), float(np.float32(0.99)), 1e-2, 1e-15
+    rng = np.random.default_rng(3)
+    g = rng.normal(size=(40, 5)) * np.logspace(-6, 0, 5)
+    p_raw = np.zeros(5)
+    p_hat = np.zeros(5)
+    m = np.zeros(5)
+    v = np.zeros(5)
+    for t in range(1, 41):
+        m = b1 * m + (1 - b1) * g[t - 1]
+        v = b2 * v + (1 - b2) * g[t - 1] ** 2
+        lr_t = ft.Nerf.adam_lr_t(stub, lr, t)
+        assert lr_t.dtype == np.float32
+        p_raw -= float(lr_t) * m / (np.sqrt(v) + eps)
+        c1, c2 = 1 - b1 ** t, 1 - b2 ** t
+        p_hat -= lr * (m / c1) / (np.sqrt(v / c2) + eps / np.sqrt(c2))
+        # each step differs by the float32 rounding of lr_t (6e-8 of a step of at most a few lr)
+        np.testing.assert_allclose(p_raw, p_hat, rtol=0, atol=1e-6 * lr * t)
+    # t = 1: sqrt(1 - b2) / (1 - b1) with the float32 betas; large t: the corrections vanish
+    assert abs(float(ft.Nerf.adam_lr_t(stub, lr, 1)) - lr * np.sqrt(1 - b2) / (1 - b1)) < 1e-9
+    assert abs(float(ft.Nerf.adam_lr_t(stub, lr, 10 ** 5)) - lr) < 1e-8
+
+
+def test_occ_decay_q24():
+    """The decay factor in 24-bit fixed point: no decay at strength 0, the plain decay at strength 1, linear in
+    the strength between, rounded half to even, and clamped (a strength past 1 / (1 - decay) clears)."""
+    one = 1 << 24
+    assert ft.occ_decay_q24(0.0, 0.95) == one
+    assert ft.occ_decay_q24(1.0, 1.0) == one
+    assert ft.occ_decay_q24(1.0, 0.95) == 15938355  # 0.95 * 2^24 = 15938355.2
+    assert ft.occ_decay_q24(0.5, 0.95) == 16357786  # 0.975 * 2^24 = 16357785.6
+    assert ft.occ_decay_q24(1.0, 0.5) == one // 2
+    assert ft.occ_decay_q24(1.0, 1 - 2.5 / one) == one - 2  # 2^24 - 2.5 rounds to the even neighbour
+    assert ft.occ_decay_q24(1.0, 1 - 3.5 / one) == one - 4
+    assert ft.occ_decay_q24(25.0, 0.95) == 0  # 1 - 25 * 0.05 < 0
+    assert ft.occ_decay_q24(-1.0, 0.95) == one  # clamped above
+    for s_ in np.linspace(0.0, 1.0, 11):
+        assert abs(ft.occ_decay_q24(s_, 0.9) - (1 - 0.1 * s_) * one) <= 0.5
+
+
 def test_loss_log_format(tmp_path):
     path, f = trainer.open_loss_log(tmp_path, "m1")
     trainer.write_loss_row(f, 1.5, 10, 1e-3, 0.25, 0.5, 0.75, [2], 3)
