@@ -334,7 +334,7 @@ __device__ __forceinline__ bool level_grad(const DevCfg& c, const float (&v)[F],
 }
 
 // One step of the emit's segmented suffix sum: lane i adds lane i + D's values when both are in its run
-// (take).  Runs lie inside aligned groups of at most 8 lanes, so lane i + D is in the same 16-lane row and
+// (take).  Runs lie inside aligned groups of at most 16 lanes, so lane i + D is in the same 16-lane row and
 // the DPP row shift reaches it.
 template <int D, int F>
 __device__ __forceinline__ void merge_step(float (&v)[8][F], bool take) {
@@ -357,11 +357,12 @@ __device__ __forceinline__ void merge_step(float (&v)[8][F], bool take) {
 // contiguous range for the reduction (with entries and values in separate arrays, a run of a few dozen
 // pairs was two short ranges whose edge sectors were fetched twice).
 // Same-cell samples merge within aligned groups of MERGE_BLK lanes (a run never crosses one), which keeps
-// the merge to log2(MERGE_BLK) register steps; longer groups would merge little more (at the benchmark
-// shape 73 % of the pairs remain with unbounded runs, 76 % with groups of 8).
+// the merge to log2(MERGE_BLK) register steps inside a 16-lane DPP row; longer groups would merge little
+// more (at the benchmark shape 73 % of the pairs remain with unbounded runs, 76 % with groups of 8; groups
+// of 16 took the scatter from 7.23 to 7.19 ms).
 constexpr int PAD_RUN = 8;
 __host__ __device__ constexpr int pair_block_words(int F) { return 2 * F + 1; }
-constexpr int MERGE_BLK = 8;
+constexpr int MERGE_BLK = 16;
 __host__ __device__ constexpr int emit_nt(int F) { return F >= 4 ? 512 : 1024; }
 __device__ __forceinline__ uint32_t pad_run(uint32_t n) { return (n + (PAD_RUN - 1)) & ~(uint32_t)(PAD_RUN - 1); }
 
@@ -437,7 +438,10 @@ __device__ __forceinline__ void emit_prepare(const DevCfg& c, const PosSrc& src,
     merge_step<1, F>(es.v, len > 1);
     if (__ballot(len > 2) != 0ull) {
       merge_step<2, F>(es.v, len > 2);
-      if (__ballot(len > 4) != 0ull) merge_step<4, F>(es.v, len > 4);
+      if (__ballot(len > 4) != 0ull) {
+        merge_step<4, F>(es.v, len > 4);
+        if (__ballot(len > 8) != 0ull) merge_step<8, F>(es.v, len > 8);
+      }
     }
   }
   es.head = act && !cont;
