@@ -428,7 +428,10 @@ __device__ __forceinline__ void emit_prepare(const DevCfg& c, const PosSrc& src,
 #pragma unroll
       for (int f = 0; f < F; ++f) es.v[cc][f] = 0.0f;
   }
-  const int p0 = __shfl_up(lc.i0[0], 1), p1 = __shfl_up(lc.i0[1], 1), p2 = __shfl_up(lc.i0[2], 1);
+  // the previous lane's cell by DPP row_shr:1 (a run never starts a 16-lane row's first lane, which gets -1)
+  const int p0 = __builtin_amdgcn_update_dpp(-1, lc.i0[0], 0x111, 0xF, 0xF, false);
+  const int p1 = __builtin_amdgcn_update_dpp(-1, lc.i0[1], 0x111, 0xF, 0xF, false);
+  const int p2 = __builtin_amdgcn_update_dpp(-1, lc.i0[2], 0x111, 0xF, 0xF, false);
   const bool cont = act && (lane & (MERGE_BLK - 1)) != 0 && p0 == lc.i0[0] && p1 == lc.i0[1] && p2 == lc.i0[2];
   const uint64_t cm = __ballot(cont);
   if (cm != 0ull) {
