@@ -655,7 +655,9 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   __shared__ float wmax[16];
   __shared__ uint32_t wtot[16];
   constexpr int SEG = 16;  // rounds per wavefront step
-  const int j = blockIdx.x;  // bucket, relative to the group
+  // bucket, relative to the group, finest levels first: their buckets hold the most pairs, and the lighter
+  // coarse-level blocks then fill the last wave of blocks (scatter 7.01 -> 6.91 ms at the benchmark shape)
+  const int j = (int)gridDim.x - 1 - (int)blockIdx.x;
   int li = 0;
   while (li + 1 < grp.n_levels && j >= grp.bucket_rel[li + 1]) ++li;
   const int l = grp.level0 + li;
