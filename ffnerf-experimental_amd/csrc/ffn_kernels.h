@@ -88,6 +88,10 @@ struct MlpArgs {
   uint32_t num_rays;
   int S, log2S;
   int64_t n_tiles;
+  // k_mlp: position i of the launch's tile sequence is tile tile_order[i] (launch_tile_order: the busy tiles
+  // first, so that the round-robin deal gives every block the same share of them), or tile i when NULL;
+  // k_mlp16 takes its tiles in index order
+  const uint32_t* tile_order;
   float sh_mult, occ_strength;
   uint32_t seed;
   int do_train;
@@ -271,6 +275,10 @@ bool mlp_supported(int LF, int nd, int nc);
 int mlp_blocks_per_cu(int LF, int nd, int nc);  // blocks of launch_mlp that fit on one CU
 int mlp16_blocks_per_cu(int LF, int nd, int nc);  // blocks of launch_mlp16 that fit on one CU
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+// order[n_tiles]: the tiles with a sample of dt > 0 in index order, then the others; scratch: flags and off
+// n_tiles + 1 words each, sums (n_tiles + 4096) / 4096 + 1 words, total 1 word
+hipError_t launch_tile_order(const float* DTs, int64_t n_samples, int64_t n_tiles, uint32_t* flags, uint32_t* off,
+                             uint32_t* sums, uint32_t* total, uint32_t* order, hipStream_t st);
 // the same kernel's backward over marched samples (a.smp, a.ray_ids, a.in_dLds, a.in_dLdc; a.num_rays = the
 // sample count, log2S = 0): no compositing, no proposals
 hipError_t launch_mlp_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
