@@ -291,7 +291,18 @@ template <int F>
 __device__ __forceinline__ void load_raw(const PosSrc& s, const float* __restrict__ g, const FeatLayout& lay,
                                          int64_t b, int l, RawSample<F>& r) {
   typedef typename FVec<F>::T V;
-  FVec<F>::unpack(*reinterpret_cast<const V*>(g + l * lay.stride_l + b * lay.stride_b), r.g);
+  {
+    // each level's gradients are read by this pass once: streamed past the caches
+    const float* gp = g + l * lay.stride_l + b * lay.stride_b;
+    if constexpr (F == 1) {
+      r.g[0] = __builtin_nontemporal_load(gp);
+    } else {
+      typedef float fv __attribute__((ext_vector_type(F)));
+      const fv v = __builtin_nontemporal_load(reinterpret_cast<const fv*>(gp));
+#pragma unroll
+      for (int f = 0; f < F; ++f) r.g[f] = v[f];
+    }
+  }
   if (s.rays) {
     const int64_t ray = b >> s.log2S;
     r.o = s.rays[2 * ray];
