@@ -62,7 +62,15 @@ struct StageEvent {
   hipEvent_t start, stop;
 };
 
+// the event recorded after the last work a call on the handle enqueued on one stream
+struct StreamUse {
+  hipStream_t st;
+  hipEvent_t ev;
+};
+
 struct Handle {
+  std::vector<StreamUse> uses;  // one per stream the handle has been used on: ffn_destroy waits for these
+  bool uses_lost = false;       // an event could not be created: ffn_destroy waits for the whole device
   bool prof = false;
   std::vector<StageEvent> events;    // recorded, not yet folded into the totals
   std::vector<hipEvent_t> event_pool;  // created events free for reuse
@@ -374,6 +382,33 @@ struct StageTimer {
   }
 };
 
+// Records the handle's last work on stream st (re-recording the stream's event), so that ffn_destroy waits
+// for the work of this handle only, not for the device's other streams.
+void note_use(Handle* h, hipStream_t st) {
+  for (StreamUse& u : h->uses) {
+    if (u.st == st) {
+      if (hipEventRecord(u.ev, st) != hipSuccess) h->uses_lost = true;
+      return;
+    }
+  }
+  hipEvent_t ev;
+  if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+    h->uses_lost = true;
+    return;
+  }
+  h->uses.push_back(StreamUse{st, ev});
+  if (hipEventRecord(ev, st) != hipSuccess) h->uses_lost = true;
+}
+
+// note_use at the end of an entry point's scope (every return path), after everything it enqueued
+struct UseMark {
+  Handle* h;
+  hipStream_t st;
+  ~UseMark() {
+    if (h) note_use(h, st);
+  }
+};
+
 void destroy_events(Handle* h) {
   for (auto& e : h->events) {
     (void)hipEventDestroy(e.start);
@@ -424,7 +459,14 @@ int ffn_create(const ffn_config* cfg, void** handle) {
 int ffn_destroy(void* handle) {
   Handle* h = as_handle(handle);
   if (!h) return 0;
-  (void)hipDeviceSynchronize();
+  // the handle's buffers may still be in use by work it enqueued: wait for that work (the last call's event on
+  // every stream the handle was used on) before freeing them
+  if (h->uses_lost) (void)hipDeviceSynchronize();
+  for (StreamUse& u : h->uses) {
+    (void)hipEventSynchronize(u.ev);
+    (void)hipEventDestroy(u.ev);
+  }
+  h->uses.clear();
   destroy_events(h);
   h->Ts.release();
   h->DTs.release();
@@ -486,6 +528,7 @@ int ffn_sample(void* handle, const void* rays, uint32_t num_rays, uint32_t spr, 
   if (!rays || !Ts || !DTs || !flags) return fail(-1, "NULL buffer");
   if (!h->params.occ_in) return fail(-1, "bind params (occ_in) first");
   if (num_rays == 0) return 0;
+  UseMark um{h, (hipStream_t)stream};
   FFN_HIP(ffn::launch_sample(h->dc, (const float4*)rays, num_rays, (int)spr, rng_seed, h->params.occ_in, do_train, Ts,
                              DTs, flags, (hipStream_t)stream));
   return 0;
@@ -502,6 +545,7 @@ int ffn_hash_encode_fwd(void* handle, const float* x, int64_t n, float* a0, uint
   // tiled transpose makes the caller's sample-major rows: the passes would otherwise write F floats out
   // of every L * F
   const hipStream_t st = (hipStream_t)stream;
+  UseMark um{h, st};
   FFN_HIP(h->a0.ensure(sizeof(float) * (size_t)n * h->dc.LF));
   const ffn::FeatLayout lm = ffn::level_major(n, h->dc.F);
   ffn::PosSrc src{x, nullptr, nullptr, 0};
@@ -522,6 +566,7 @@ int ffn_hash_encode_bwd(void* handle, const float* x, const float* g, int64_t n,
   if (!ffn::scatter_supported(h->dc))
     return fail(-2, "ffn_hash_encode_bwd: the scatter is not built for this table shape (F=%d with %u-entry levels)",
                 h->dc.F, max_level_entries(h->dc));
+  UseMark um{h, (hipStream_t)stream};
   ffn::BinPlan plan;
   ffn::BinScratch bs;
   FFN_HIP(ensure_bins(h, n, &plan, &bs));
@@ -581,6 +626,7 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
     return fail(-2, "ffn_train_step: the scatter is not built for this table shape (F=%d with %u-entry levels)",
                 h->dc.F, max_level_entries(h->dc));
   hipStream_t st = (hipStream_t)stream;
+  UseMark um{h, st};
   int log2S = 0;
   while ((1u << log2S) < spr) ++log2S;
   const int64_t N = (int64_t)num_rays * spr;
@@ -810,6 +856,7 @@ int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t*
   if (!counts || !offsets || !total || (capacity > 0 && (!samples || !ray_ids))) return fail(-1, "NULL buffer");
   if (num_rays == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
+  UseMark um{h, st};
   ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
   FFN_HIP(set_march_blocks(h, a, st));
   a.counts = counts;
@@ -844,6 +891,7 @@ int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const u
   if (!off) return -3;
   uint32_t* sums = off + kNoallocScanWords;
   hipStream_t st = (hipStream_t)stream;
+  UseMark um{h, st};
   ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
   a.counts = counts;
   FFN_HIP(ffn::launch_march(a, false, st));
@@ -868,6 +916,7 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   if (!sc || !targets || !out_rgb) return fail(-1, "NULL scalars/targets/out_rgb");
   if (num_rays == 0) return fail(-1, "num_rays must be > 0");
   if (!sc->do_train) return fail(-1, "ffn_train_step_marched trains; ffn_render is the marched forward render");
+  if (sc->occ_strength > 0.0f && !h->params.occ_st) return fail(-1, "proposals need occ_st");
   if (!(mp->T_stop >= 0.0f && mp->T_stop < 1.0f)) return fail(-1, "T_stop must be in [0,1)");
   if ((uint64_t)num_rays * mp->max_steps >= ((uint64_t)1 << 32))
     return fail(-1, "num_rays * max_steps must stay below 2^32 samples");
@@ -879,6 +928,7 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
     return fail(-2, "ffn_train_step_marched: the scatter is not built for this table shape (F=%d with %u-entry "
                     "levels)", h->dc.F, max_level_entries(h->dc));
   hipStream_t st = (hipStream_t)stream;
+  UseMark um{h, st};
   const ffn_params& P = h->params;
 
   // 1. march.  With room for max_steps samples per ray, one walk writes each ray's samples to its own slots
@@ -993,6 +1043,11 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
     ca.n_used = n_samples;
     ca.T_final = taps ? taps->T_final : nullptr;
     ca.color = taps ? (float4*)taps->color : nullptr;
+    ca.c = h->dc;
+    ca.rays = (const float4*)rays;
+    ca.samples = smp;
+    ca.occ_in = P.occ_in;
+    ca.occ_st = sc->occ_strength > 0.0f ? P.occ_st : nullptr;
     FFN_HIP(ffn::launch_composite_marched(ca, st));
     ffn::MlpArgs a{};
     a.c = h->dc;
@@ -1095,6 +1150,7 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   if (!(mp->T_stop >= 0.0f && mp->T_stop < 1.0f)) return fail(-1, "T_stop must be in [0,1)");
   if (num_rays == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
+  UseMark um{h, st};
   const int LF = h->dc.LF;
   const size_t n1 = (size_t)num_rays + 1;
   const size_t cap = (size_t)num_rays * mp->chunk;

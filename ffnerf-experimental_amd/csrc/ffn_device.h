@@ -553,4 +553,108 @@ __device__ __forceinline__ void occ_nibble_atomic_max(uint32_t* grid, int cell, 
   }
 }
 
+
+// grid coordinates of a point for the occupancy proposals (ffnerf_OG.cl:1660-1690); the same operations
+// serve the early load of the cell's occupancy word, the runs of the marched samples and the proposal itself
+__device__ __forceinline__ void occ_grid_pos(const DevCfg& c, const float (&o)[3], const float (&d)[3], float t,
+                                             float (&gpos)[3]) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float bs = c.bmax[i] - c.bmin[i];
+    const float xi = o[i] + t * d[i];
+    gpos[i] = (xi - c.bmin[i]) * (1.0f / bs) * (float)c.G;
+  }
+}
+
+__device__ __forceinline__ float half_box_diagonal(const DevCfg& c) {
+  const float dx = c.bmax[0] - c.bmin[0], dy = c.bmax[1] - c.bmin[1], dz = c.bmax[2] - c.bmin[2];
+  return 0.5f * sqrtf(dx * dx + dy * dy + dz * dz);
+}
+
+// The occupancy proposal of one run: the samples of ray rj that lie in one subcell, from sample lid (time t_j,
+// transmittance Tr_j arriving at it) to sample `last` (t_last, T_last).  (t_prev, T_prev) is the sample
+// before the run (the run's first when it is the ray's first); (t_nx, T_nx) the first sample after the run
+// when has_next, else the cell's exit and the ray's final transmittance T_final.  The transmittance is
+// interpolated to the cell's entry and exit; 16 times the predicted absorption, rounded stochastically,
+// becomes the proposed level, which raises the subcell's nibble of occ_st (an atomic max) when it exceeds the
+// occ_in level (occ_word: the cell's occ_in word) and the distance-dependent keep draw accepts it
+// (ffnerf_OG.cl:1640-1821).  Dhalf: half the box diagonal.
+__device__ __forceinline__ void occ_propose_run(const DevCfg& c, const float (&o)[3], const float (&d)[3], float t_j,
+                                                float Tr_j, float t_prev, float T_prev, float t_last, float T_last,
+                                                bool has_next, float t_nx, float T_nx, float T_final,
+                                                uint32_t occ_word, uint32_t seed, uint32_t rj, uint32_t lid,
+                                                float Dhalf, uint32_t* occ_st) {
+  const int G = c.G;
+  float gpos[3], cell_size[3];
+  occ_grid_pos(c, o, d, t_j, gpos);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float bs = c.bmax[i] - c.bmin[i];
+    cell_size[i] = bs * (1.0f / (float)G);
+  }
+  const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
+  if (!((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G)) return;
+  uint32_t sub = 0;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) sub += ((gpos[i] - floorf(gpos[i])) >= 0.5f ? 1u : 0u) << i;
+  const int cell = ix + G * (iy + G * iz);
+  float pred = 0.0f;
+  {
+    const int ii[3] = {ix, iy, iz};
+    float cmin[3], cmax[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      cmin[i] = c.bmin[i] + (float)ii[i] * cell_size[i];
+      cmax[i] = cmin[i] + cell_size[i];
+    }
+    float t_enter, t_exit;
+    if (ray_aabb(o, d, cmin, cmax, t_enter, t_exit)) {
+      t_enter = fmaxf(t_enter, c.t_near);
+      t_exit = fminf(t_exit, c.t_far);
+      if (t_exit > t_enter) {
+        const float denom0 = t_j - t_prev;
+        float u0 = (fabsf(denom0) > 1.0e-8f) ? (t_enter - t_prev) / denom0 : 0.0f;
+        u0 = fminf(fmaxf(u0, 0.0f), 1.0f);
+        const float T_enter = T_prev + (Tr_j - T_prev) * u0;
+        const float t_next = has_next ? t_nx : t_exit;
+        const float T_next = has_next ? T_nx : T_final;
+        const float denom1 = t_next - t_last;
+        float u1 = (fabsf(denom1) > 1.0e-8f) ? (t_exit - t_last) / denom1 : 1.0f;
+        u1 = fminf(fmaxf(u1, 0.0f), 1.0f);
+        const float T_exit = T_last + (T_next - T_last) * u1;
+        pred = fminf(1.0f, fmaxf(0.0f, (T_enter - T_exit) / fmaxf(T_enter, 1.0e-12f)));
+      }
+    }
+  }
+  const uint32_t old_q = ((occ_word >> (4u * sub)) & 0xFu) + 1u;
+  uint32_t proposed_q = old_q;
+  const float pred16 = pred * 16.0f;
+  const uint32_t hseed =
+      hash_u32(seed ^ rj * 747796405u ^ lid * 2891336453u ^ (uint32_t)cell * 9781u ^ sub * 6271u);
+  if (pred16 > (float)old_q && old_q < 16u) {
+    const float f0 = floorf(pred16);
+    const float frac = pred16 - f0;
+    const uint32_t q0 = (uint32_t)f0;
+    const uint32_t thresh = (uint32_t)(frac * 16777216.0f);
+    const uint32_t q_stoch = ((hseed & 0x00FFFFFFu) < thresh) ? (q0 + 1u) : q0;
+    proposed_q = q_stoch > 16u ? 16u : q_stoch;
+  }
+  // occ_st equals occ_in after every decay and proposals only raise it, so a proposal that does not exceed
+  // the occ_in nibble cannot change occ_st: skip the keep draw and the atomic
+  if (proposed_q > old_q) {
+    const float lat = (c.bmax[0] - c.bmin[0]) * (1.0f / (float)G);
+    const float tl = t_j / fmaxf(lat, 1.0e-12f);
+    const float Dl = Dhalf / fmaxf(lat, 1.0e-12f);
+    const float num = tl * tl + tl + (1.0f / 3.0f);
+    const float den = Dl * Dl + Dl + (1.0f / 3.0f);
+    const float keep_p = fminf(num / fmaxf(den, 1.0e-12f), 1.0f);
+    bool keep = keep_p >= 1.0f;
+    if (!keep) {
+      uint32_t rk = hseed;
+      keep = rand01(rk) <= keep_p;
+    }
+    if (keep) occ_nibble_atomic_max(occ_st, cell, sub, proposed_q);
+  }
+}
+
 }  // namespace ffn

@@ -252,6 +252,13 @@ struct CompMarchArgs {
   uint32_t* n_used;        // [num_rays] samples composited (optional)
   float* T_final;          // [num_rays] (optional)
   float4* color;           // [num_rays] colour before clamping (optional)
+  // occupancy proposals of the marched runs, made when occ_st is set: the grid (c), the rays, the marched
+  // samples (t in .w) and both occupancy grids
+  DevCfg c;
+  const float4* rays;
+  const float4* samples;
+  const uint32_t* occ_in;
+  uint32_t* occ_st;
 };
 hipError_t launch_composite_marched(const CompMarchArgs& a, hipStream_t st);
 

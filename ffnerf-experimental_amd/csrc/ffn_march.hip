@@ -467,6 +467,54 @@ __global__ __launch_bounds__(256) void k_render_finish(const float4* __restrict_
 // specification, ora_train_step_marched), keeping the transmittance before every sample for the backward
 // sweep, which walks them back to front with dL/dT of the next sample (ffnerf_OG.cl:1593-1634 restated as a
 // sequential recurrence: gT_i = g . (alpha_i c_i) + (1 - alpha_i) gT_(i+1), gT_end = g . bg).
+// (cell, subcell) of the occupancy grid holding the point at time t of ray (o, d), as the proposals compute it;
+// kOutsideGrid for a point outside the grid
+constexpr uint64_t kOutsideGrid = ~(uint64_t)1;
+__device__ __forceinline__ uint64_t occ_run_key(const DevCfg& c, const float (&o)[3], const float (&d)[3], float t) {
+  float gpos[3];
+  occ_grid_pos(c, o, d, t, gpos);
+  const int G = c.G;
+  const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
+  if (!((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G)) return kOutsideGrid;
+  uint32_t sub = 0;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) sub += ((gpos[i] - floorf(gpos[i])) >= 0.5f ? 1u : 0u) << i;
+  return ((uint64_t)(ix + G * (iy + G * iz)) << 3) | sub;
+}
+
+// The occupancy proposals of marched ray r: its samples, in order, fall into runs of one (cell, subcell) of the
+// occupancy grid, and each run inside the grid proposes as a run of the resampled step does
+// (ffnerf_OG.cl:1640-1821), from the compositing's transmittances (T_end past a termination, so those runs
+// propose nothing).
+__device__ void propose_marched_runs(const CompMarchArgs& a, uint32_t r, uint32_t off, uint32_t cnt, float T_end) {
+  if (cnt == 0) return;
+  const float4 ro = a.rays[2 * r], rdv = a.rays[2 * r + 1];
+  const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
+  const float Dhalf = half_box_diagonal(a.c);
+  uint32_t s = 0;
+  float t_s = a.samples[off].w;
+  uint64_t key_s = occ_run_key(a.c, o, d, t_s);
+  for (uint32_t j = 1; j <= cnt; ++j) {
+    float t_j = 0.0f;
+    uint64_t key_j = ~(uint64_t)0;
+    if (j < cnt) {
+      t_j = a.samples[off + j].w;
+      key_j = occ_run_key(a.c, o, d, t_j);
+    }
+    if (key_j == key_s) continue;
+    if (key_s != kOutsideGrid) {  // the run [s, j) ends here
+      const uint32_t prev = s > 0 ? s - 1 : 0;
+      const bool has_next = j < cnt;
+      occ_propose_run(a.c, o, d, t_s, a.Tr[off + s], a.samples[off + prev].w, a.Tr[off + prev],
+                      a.samples[off + j - 1].w, a.Tr[off + j - 1], has_next, t_j, has_next ? a.Tr[off + j] : 0.0f,
+                      T_end, a.occ_in[key_s >> 3], a.seed, r, s, Dhalf, a.occ_st);
+    }
+    s = j;
+    t_s = t_j;
+    key_s = key_j;
+  }
+}
+
 __global__ __launch_bounds__(256) void k_composite_marched(CompMarchArgs a) {
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= a.num_rays) return;
@@ -524,6 +572,7 @@ __global__ __launch_bounds__(256) void k_composite_marched(CompMarchArgs a) {
     a.dLds[b] = 0.0f;
     a.dLdc[3 * (size_t)b] = a.dLdc[3 * (size_t)b + 1] = a.dLdc[3 * (size_t)b + 2] = 0.0f;
   }
+  if (a.occ_st) propose_marched_runs(a, r, off, cnt, T);
 }
 
 hipError_t launch_composite_marched(const CompMarchArgs& a, hipStream_t st) {

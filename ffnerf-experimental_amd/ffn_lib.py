@@ -28,6 +28,7 @@ EXPORTS = [
     "ffn_set_profiling", "ffn_stage_times", "ffn_occ_bitfield", "ffn_march", "ffn_render", "ffn_make_batch",
     "ffn_march_noalloc", "ffn_train_step_marched", "ffn_make_batch_weighted",
 ]
+ABI_VERSION = 2  # FFN_ABI_VERSION of the header these structures and signatures follow
 MARCH_NOALLOC_MAX_RAYS = 1 << 20
 RELU_WORDS = 14  # ReLU-branch tap words per sample
 STAGES = ["sample", "hash_fwd", "mlp", "hash_bwd", "mlp_adam", "table_adam"]
@@ -113,6 +114,9 @@ def load(path: Path | str | None = None) -> C.CDLL:
     import torch  # noqa: F401
     lib = C.CDLL(str(p))
     lib.ffn_version.restype = C.c_int
+    if lib.ffn_version() != ABI_VERSION:
+        raise FfnError(f"{p} has ABI version {lib.ffn_version()}; this binding is written for {ABI_VERSION} "
+                       "(rebuild the library or use the matching binding)")
     lib.ffn_last_error.restype = C.c_char_p
     lib.ffn_create.argtypes = [C.POINTER(FfnConfig), C.POINTER(_vp)]
     lib.ffn_destroy.argtypes = [_vp]

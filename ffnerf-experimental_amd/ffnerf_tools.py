@@ -491,8 +491,9 @@ class Nerf:
         fl.check(lib.ffn_train_step(self.handle.h, fl.ptr(io.rays_buf), fl.ptr(io.targets_buf), fl.ptr(io.out_buf),
                                     io.num_rays, io.samples_per_ray, C.byref(sc),
                                     C.byref(taps) if taps is not None else None, sp), "ffn_train_step")
-        # the march sampler makes no proposals, so the grid it reads is not decayed either
-        if (do_train and float(occ_update_strength) > 0.0 and self.spec.sampler != "march"
+        # the occupancy maintenance of ffnerf_tools.py:1424-1476; with the march sampler the proposals of the
+        # marched runs and this decay keep the grid, so the next steps' bitfield, following the density
+        if (do_train and float(occ_update_strength) > 0.0
                 and self.steps_trained % int(self.occ.maintenance_period) == 0):
             decay_q24 = occ_decay_q24(occ_update_strength, self.occ.decay)
             n_words = int(self.occ.G_occ) ** 3

@@ -39,7 +39,8 @@
 extern "C" {
 #endif
 
-#define FFN_ABI_VERSION 1
+/* 2: ffn_taps gained T_final, relu and color; ffn_params.table became void* (binary16 tables). */
+#define FFN_ABI_VERSION 2
 #define FFN_MAX_LEVELS 32
 
 /* layer slots (reference kernel-argument order, ffnerf_tools.py:1210-1232) */
@@ -138,6 +139,8 @@ int ffn_version(void);
 const char* ffn_last_error(void);
 
 int ffn_create(const ffn_config* cfg, void** handle);
+/* Waits for the work the handle's calls enqueued (on every stream they were
+ * given), then frees the handle and its scratch. */
 int ffn_destroy(void* handle);
 int ffn_bind_params(void* handle, const ffn_params* params);
 
@@ -148,8 +151,10 @@ int ffn_bind_params(void* handle, const ffn_params* params);
  * bitfield march instead (samples_per_ray is then ignored): the bitfield of
  * the (2 occ_G)^3 subcells with q >= march_q_min is built from occ_in, and
  * the step is ffn_train_step_marched with march_dt, march_max_steps and
- * march_T_stop (taps index the march's samples; no occupancy proposals); a
- * forward-only call is ffn_render (out_rgb.w = T_final). */
+ * march_T_stop (taps index the march's samples; the proposals of the marched
+ * runs when occ_strength > 0, so that with the caller's decay the grid, and
+ * the next step's bitfield, follow the density); a forward-only call is
+ * ffn_render (out_rgb.w = T_final). */
 int ffn_train_step(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
                    uint32_t samples_per_ray, const ffn_step_scalars* scalars, const ffn_taps* taps,
                    void* stream);
@@ -234,8 +239,12 @@ int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const u
  * gradient (ffnerf_OG.cl:1505-1634, as a sequential recurrence), the MLP
  * backward, the table update (reference SGD or Adam) and the MLP Adam.  The
  * density penalty of a composited sample is 5e-3 dt / max_steps (the
- * reference's 5e-3 dt / S).  No occupancy proposals: the bitfield is an input
- * (ffn_occ_bitfield).  Specification: ora_train_step_marched (oracle/).
+ * reference's 5e-3 dt / S).  The bitfield is an input (ffn_occ_bitfield).
+ * When scalars->occ_strength > 0 the step makes the occupancy proposals of
+ * its samples into occ_st: each ray's marched samples fall into runs of one
+ * occupancy subcell, and every run proposes as a run of the resampled step
+ * does (ffnerf_OG.cl:1640-1821), from the compositing's transmittances.
+ * Specification: ora_train_step_marched (oracle/).
  * rays, targets, out_rgb as ffn_train_step (out_rgb.w = 4); n_samples
  * (optional) [num_rays] = samples composited per ray.  taps (optional) index
  * the step's samples in march order (ray by ray, front to back; at most

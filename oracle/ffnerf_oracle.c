@@ -976,6 +976,54 @@ void ora_occ_propose_batch(const ora_cfg* c, const float* rays, int32_t num_rays
   }
 }
 
+/* The occupancy proposals of one marched ray (no counterpart in the reference, whose samples come from the
+ * resampler): its n samples at times ts, in march order, are cut into runs of one (cell, subcell) of the
+ * occupancy grid -- the key the resampler's run flags use, from the grid position the proposal computes -- and
+ * the proposal pass above runs over them as over a resampled ray of n samples (every sample's dt positive),
+ * with the compositing's transmittances Tr (T_end after a termination) and T_end as the final one. */
+void ora_occ_propose_marched_ray(const ora_cfg* c, const float* ray, uint32_t ray_id, int n, uint32_t seed,
+                                 const float* ts, const float* Tr, float T_end, const uint32_t* occ_in,
+                                 uint32_t* occ_st) {
+  if (n <= 0) return;
+  const int G = c->occ_G;
+  uint32_t* flags = (uint32_t*)calloc((size_t)(n + 31) / 32, sizeof(uint32_t));
+  float* dts = (float*)malloc(sizeof(float) * (size_t)n);
+  uint64_t prev_key = 0;
+  for (int j = 0; j < n; ++j) {
+    float gpos[3];
+    for (int i = 0; i < 3; ++i) {
+      const float x = ray[i] + ts[j] * ray[4 + i];
+      gpos[i] = (x - c->box_min[i]) * (1.0f / (c->box_max[i] - c->box_min[i])) * (float)G;
+    }
+    const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
+    uint64_t key = ~(uint64_t)1; /* outside the grid */
+    if ((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G) {
+      uint32_t sub = 0;
+      for (int i = 0; i < 3; ++i) sub += (gpos[i] - floorf(gpos[i]) >= 0.5f ? 1u : 0u) << i;
+      key = ((uint64_t)(ix + G * (iy + G * iz)) << 3) | sub;
+    }
+    if (j == 0 || key != prev_key) flags[j >> 5] |= 1u << (j & 31);
+    prev_key = key;
+    dts[j] = 1.0f;
+  }
+  ora_occ_propose_ray(c, ray, ray_id, n, seed, ts, dts, Tr, T_end, flags, occ_in, occ_st);
+  free(flags);
+  free(dts);
+}
+
+/* the proposals of marched rays from another implementation's samples and compositing: counts [num_rays],
+ * ts / Tr [sum of counts] in march order, T_final [num_rays] */
+void ora_occ_propose_marched_batch(const ora_cfg* c, const float* rays, int32_t num_rays, const uint32_t* counts,
+                                   uint32_t seed, const float* ts, const float* Tr, const float* T_final,
+                                   const uint32_t* occ_in, uint32_t* occ_st) {
+  int64_t base = 0;
+  for (int32_t r = 0; r < num_rays; ++r) {
+    ora_occ_propose_marched_ray(c, rays + 8 * (int64_t)r, (uint32_t)r, (int)counts[r], seed, ts + base, Tr + base,
+                                T_final[r], occ_in, occ_st);
+    base += counts[r];
+  }
+}
+
 /* ------------------------------------------------------------------ */
 /* compositing, loss gradient and its backward of one ray (ffnerf_OG.cl:1505-1634) */
 
@@ -1575,7 +1623,8 @@ int ora_composite_marched(const float* sig, const float* rgb, int n, float dt, f
  * parameter updates.  A step without samples leaves the table and its moments as they are (no table update
  * runs) while the MLP's Adam runs on zero gradients.  Taps index samples in march order.
  * n_used (optional) [num_rays] = samples composited; used_in (optional) [num_rays]: composite exactly that
- * many samples per ray (another implementation's termination).  No occupancy proposals. */
+ * many samples per ray (another implementation's termination).  With occ_strength > 0, the occupancy
+ * proposals of every ray's runs (ora_occ_propose_marched_ray). */
 int ora_train_step_marched(const ora_cfg* c, ora_params* P, const ora_march_cfg* m, const uint32_t* bits,
                            const float* rays, const float* targets, float* out_rgb, int32_t num_rays,
                            const ora_scalars* sc, ora_debug* dbg, const uint32_t* used_in, uint32_t* n_used) {
@@ -1663,6 +1712,8 @@ int ora_train_step_marched(const ora_cfg* c, ora_params* P, const ora_march_cfg*
       if (dbg->dL_dsigma) memcpy(dbg->dL_dsigma + base, dLds, sizeof(float) * n);
       if (dbg->dL_dc) memcpy(dbg->dL_dc + 3 * base, dLdc, sizeof(float) * 3 * n);
     }
+    if (sc->occ_strength > 0.0f && P->occ_st)
+      ora_occ_propose_marched_ray(c, ray, (uint32_t)r, n, sc->rng_seed, ts, Tr, T, P->occ_in, P->occ_st);
     for (int j = 0; j < n; ++j) {
       float x[3];
       for (int i = 0; i < 3; ++i) x[i] = ray[i] + ts[j] * ray[4 + i];

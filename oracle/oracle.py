@@ -129,6 +129,10 @@ def load(path: Path = None) -> C.CDLL:
                                         C.c_float, _up, _up, _up]
     lib.ora_occ_propose_batch.argtypes = [C.POINTER(OraCfg), _fp, C.c_int32, C.c_int, C.c_uint32, _fp, _fp, _fp,
                                           _fp, _up, _up, _up]
+    lib.ora_occ_propose_marched_ray.argtypes = [C.POINTER(OraCfg), _fp, C.c_uint32, C.c_int, C.c_uint32, _fp, _fp,
+                                                C.c_float, _up, _up]
+    lib.ora_occ_propose_marched_batch.argtypes = [C.POINTER(OraCfg), _fp, C.c_int32, _up, C.c_uint32, _fp, _fp,
+                                                  _fp, _up, _up]
     lib.ora_composite_ray.argtypes = [C.POINTER(OraCfg), C.c_uint32, C.c_int, C.c_uint32, C.c_int, _fp, _fp, _fp,
                                       _fp, _fp, _fp, _fp, _fp, _fp]
     lib.ora_adam.argtypes = [_fp, _fp, _fp, _fp, C.c_int64, C.c_float, C.c_float, C.c_float, C.c_float]
@@ -299,6 +303,19 @@ def occ_propose(cfg: OraCfg, rays, S: int, seed: int, Ts, DTs, Tr, T_final, flag
     assert arrs[0].size == n * S and arrs[3].size == n and fl.size == 2 * n
     lib().ora_occ_propose_batch(C.byref(cfg), fptr(rays), n, S, seed & 0xFFFFFFFF, *[fptr(a) for a in arrs],
                                 uptr(fl), uptr(np.ascontiguousarray(occ_in, np.uint32).reshape(-1)), uptr(occ_st))
+
+
+def occ_propose_marched(cfg: OraCfg, rays, counts, seed: int, Ts, Tr, T_final, occ_in, occ_st):
+    """The proposal pass over marched rays (counts samples each, Ts / Tr in march order) from given compositing
+    results; raises occ_st in place."""
+    rays = np.ascontiguousarray(rays, np.float32).reshape(-1, 8)
+    n = rays.shape[0]
+    cnt = np.ascontiguousarray(counts, np.uint32).reshape(-1)
+    arrs = [np.ascontiguousarray(a, np.float32).reshape(-1) for a in (Ts, Tr, T_final)]
+    assert cnt.size == n and arrs[0].size == arrs[1].size == int(cnt.sum()) and arrs[2].size == n
+    lib().ora_occ_propose_marched_batch(C.byref(cfg), fptr(rays), n, uptr(cnt), seed & 0xFFFFFFFF,
+                                        *[fptr(a) for a in arrs], uptr(np.ascontiguousarray(occ_in, np.uint32)
+                                                                       .reshape(-1)), uptr(occ_st))
 
 
 def occ_decay(occ_in: np.ndarray, occ_st: np.ndarray, decay_q24: int, seed: int):

@@ -137,3 +137,35 @@ def default_scalars(**kw):
              occ_strength=1.0, beta1=0.9, beta2=0.99, eps=1e-15, rng_seed=12345, do_train=1)
     s.update(kw)
     return s
+
+
+def cfg4_shell_bitfield(R, seed=4, radius=0.3, thickness=0.02, noise=0.007):
+    """BASELINE configs[4]'s occupancy field: the cells whose centre lies within thickness/2 of a sphere of the
+    given radius about the box centre, plus seeded isolated cells (a `noise` fraction), about 3 % set at
+    R = 256.  R^3 bits, x fastest, 32 per word.  Returns (bits, fraction set)."""
+    rng = np.random.default_rng(seed)
+    c = (np.arange(R, dtype=np.float32) + 0.5) / R
+    bits = np.zeros((R ** 3 + 31) // 32, np.uint32)
+    yy, xx = np.meshgrid(c, c, indexing="ij")
+    n_set = 0
+    for z in range(R):  # slab by slab to bound host memory
+        rad = np.sqrt((xx - 0.5) ** 2 + (yy - 0.5) ** 2 + (c[z] - 0.5) ** 2)
+        occ = (np.abs(rad - radius) <= 0.5 * thickness) | (rng.random((R, R)) < noise)
+        idx = np.nonzero(occ.reshape(-1))[0].astype(np.int64) + z * R * R
+        n_set += idx.size
+        np.bitwise_or.at(bits, idx >> 5, (np.uint32(1) << (idx & 31).astype(np.uint32)))
+    return bits, n_set / R ** 3
+
+
+def cfg3_points(n, dist, seed=1):
+    """BASELINE configs[3]'s query points in the unit box: (a) "uniform", or (b) "shell": 90 % on a spherical
+    shell of radius 0.25 +- 0.01 about the centre, 10 % uniform, shuffled."""
+    rng = np.random.default_rng(seed)
+    if dist == "uniform":
+        return rng.random((n, 3), dtype=np.float32)
+    k = n // 10
+    v = rng.normal(size=(n - k, 3))
+    v /= np.linalg.norm(v, axis=1, keepdims=True)
+    r = rng.uniform(0.24, 0.26, (n - k, 1))
+    x = np.concatenate([0.5 + v * r, rng.random((k, 3))]).astype(np.float32)
+    return x[rng.permutation(n)]

@@ -30,7 +30,18 @@ def test_library_exports_every_declared_symbol():
     for n in declared_functions():
         assert hasattr(lib, n), n
     assert sorted(ffn_lib.EXPORTS) == declared_functions()
-    assert ffn_lib.load().ffn_version() == 1
+    assert ffn_lib.load().ffn_version() == ffn_lib.ABI_VERSION == 2
+
+
+def test_binding_refuses_another_abi_version(monkeypatch):
+    """The binding checks ffn_version() on load: a library built from another header (other struct layouts)
+    is refused with an error instead of being called with structures of the wrong size."""
+    import ffn_lib
+    if not ffn_lib.LIB_PATH.exists():
+        pytest.fail("libffnerf_hip.so is not built (run __graft_entry__.build())")
+    monkeypatch.setattr(ffn_lib, "ABI_VERSION", 1)
+    with pytest.raises(ffn_lib.FfnError, match="ABI version 2"):
+        ffn_lib.load(ffn_lib.LIB_PATH)
 
 
 def test_invalid_config_is_an_error_not_a_silent_return():

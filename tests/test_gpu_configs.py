@@ -1,0 +1,205 @@
+"""GPU parity at the shapes of BASELINE configs[3] and configs[4], against the oracle:
+
+- the early-terminated render and the marched training step with the config-1 MLPs (32 encoded
+  features: the LF = 32 instances of the forward-only and the marched backward kernels, fp32 and fp16/bf16
+  MFMA paths) on the 256^3 shell bitfield, <= 1024 steps per ray, T_stop 1e-4; the render of all 2^20 rays
+  equals, ray for ray, the render of a subset that the oracle checks; Adam over the 16 x 2^22 x 2 table
+  parameters with sparse gradients (5 % of the rows N(0, 1e-3)), bit-exact;
+- the hash encoding's forward (bit-exact) and backward (float64 sums) on the 16 x 2^22 fp32 table
+  with uniform and shell-distributed points.
+"""
+import numpy as np
+import pytest
+
+from common import (cfg3_points, cfg4_shell_bitfield, default_scalars, look_at_rays, random_params, spec_cfg1,
+                    sphere_targets, table_floats)
+from parity import TOL, compare_marched_step
+
+pytestmark = pytest.mark.gpu
+
+R4, STEPS4 = 256, 1024
+DT4 = np.float32(np.sqrt(3.0) / STEPS4)
+
+
+@pytest.fixture(scope="module")
+def gh():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("a GPU test ran without a visible GPU")
+    import gpu_helpers
+    return gpu_helpers
+
+
+@pytest.fixture(scope="module")
+def field4():
+    bits, frac = cfg4_shell_bitfield(R4)
+    assert 0.02 < frac < 0.04, frac
+    return bits
+
+
+def _camera_rays(n, seed):
+    """Pixel rays of the config-1 cameras (56 hemisphere poses at radius 1.5, 450 x 800, f = 640)."""
+    import synthetic_scene as sc
+    rays, _ = sc.uniform_batch(sc.cameras_for("cfg1"), n, np.random.default_rng(seed))
+    return rays
+
+
+def _cfg4_rays(n, seed):
+    """Half camera pixels, half rays aimed near the centre (most of them cross the shell twice)."""
+    spec = spec_cfg1()
+    return np.concatenate([_camera_rays(n - n // 2, seed), look_at_rays(n // 2, spec, seed=seed + 1,
+                                                                         miss_frac=0.05)])
+
+
+def _render_params(spec, seed, bias):
+    p = random_params(spec, seed=seed)
+    p["bd_out"][0] = bias  # sigma = softplus(.): about `bias` inside occupied cells
+    return p
+
+
+@pytest.mark.parametrize("mlp", [0, 1])
+@pytest.mark.parametrize("T_stop", [1e-4, 0.7])
+def test_render_cfg4_matches_oracle(gh, ora, field4, mlp, T_stop):
+    """configs[4]'s render (dt = sqrt(3)/1024, <= 1024 steps) at its T_stop 1e-4 and, so that many rays stop
+    early, at T_stop 0.7 (densities are at most softplus(10), so few rays reach 1e-4 within the thin shell):
+    counts of samples used and colours against ora_render_ray.  A ray's stopping sample
+    may move by one where T crosses T_stop within the MLP's rounding: such rays are counted (<= 1 % fp32,
+    <= 5 % fp16); the earlier stop of each must end with T within rounding of T_stop, and the colours differ by at
+    most the weight of the samples only one side composites (the difference of the final T).  Every other ray's colour and final T are within the path's tolerance."""
+    import ffn_lib as fl
+    print(f"[case] cfg4 render mlp={mlp} T_stop={T_stop}", flush=True)
+    spec = spec_cfg1(hash_opt=1, mlp_precision=mlp)
+    p = _render_params(spec, seed=401, bias=8.0)
+    g = gh.GpuModel(spec, p)
+    rays = _cfg4_rays(512, seed=402)
+    out, used = g.render(rays, field4, fl.march_params(R4, DT4, STEPS4, T_stop=T_stop, chunk=64))
+    model = ora.OracleModel(spec, p)
+    ref, used_ref = model.render(rays, field4, ora.march_cfg(R4, DT4, STEPS4, T_stop=T_stop))
+    tol = TOL[mlp]
+    marched = np.array([len(ora.march_ray(model.cfg, ora.march_cfg(R4, DT4, STEPS4), field4, r)) for r in rays])
+    stopped = used_ref < marched
+    same = used == used_ref
+    flips = np.flatnonzero(~same)
+    print(f"samples used {int(used_ref.sum())}, rays stopped early {int(stopped.sum())}, "
+          f"termination flips {flips.size}", flush=True)
+    assert used_ref.sum() > 5000
+    if T_stop > 0.1:
+        assert stopped.sum() > 100
+    assert flips.size <= max(2, (0.01 if mlp == 0 else 0.05) * rays.shape[0]), flips.size
+    band = 50.0 * tol["fwd"]
+    for r in flips:  # the earlier stop ends just below T_stop, where the other side's T was just above it
+        assert min(abs(out[r, 3] / T_stop - 1.0), abs(ref[r, 3] / T_stop - 1.0)) <= band, (r, out[r], ref[r])
+        # the samples one side composites and the other does not carry weights summing to the drop in T
+        assert (np.abs(out[r, :3] - ref[r, :3]) <= abs(out[r, 3] - ref[r, 3]) + tol["out"]).all(), (r, out[r], ref[r])
+    np.testing.assert_allclose(out[same, :3], ref[same, :3], rtol=tol["out"], atol=tol["out"] * 0.2)
+    np.testing.assert_allclose(out[same, 3], ref[same, 3], rtol=50.0 * tol["fwd"], atol=1e-6)
+
+
+@pytest.mark.parametrize("mlp", [0, 1])
+def test_render_cfg4_full_batch_equals_subset(gh, field4, mlp):
+    """All 2^20 rays of configs[4] in one render: every ray's colour, final T and samples used are those of
+    a render of a 1024-ray subset alone, bit for bit (a ray's samples, MLP rows and compositing do not depend
+    on the other rays in the batch); the subset is the kind the oracle test above checks."""
+    import ffn_lib as fl
+    print(f"[case] cfg4 render 2^20 rays vs subset mlp={mlp}", flush=True)
+    spec = spec_cfg1(hash_opt=1, mlp_precision=mlp)
+    g = gh.GpuModel(spec, _render_params(spec, seed=411, bias=8.0))
+    n = 1 << 20
+    rays = _camera_rays(n, seed=412)
+    mp = fl.march_params(R4, DT4, STEPS4, T_stop=1e-4, chunk=64)
+    out, used = g.render(rays, field4, mp)
+    sub = np.random.default_rng(413).choice(n, 1024, replace=False)
+    out_s, used_s = g.render(rays[sub], field4, mp)
+    print(f"samples used {int(used.sum())} over {n} rays", flush=True)
+    assert used.sum() > 2 * n
+    np.testing.assert_array_equal(used[sub], used_s)
+    np.testing.assert_array_equal(out[sub].view(np.uint32), out_s.view(np.uint32))
+
+
+@pytest.mark.parametrize("mlp", [0, 1])
+@pytest.mark.parametrize("T_stop", [1e-4, 0.7])
+def test_marched_steps_cfg4_match_oracle(gh, ora, field4, mlp, T_stop):
+    """The marched training step with the config-1 MLPs (LF = 32) on configs[4]'s field, two steps from the
+    GPU's state, checked as tests/parity.py's compare_marched_step describes.  A fp16 run's ray may stop one
+    sample apart from the fp32 restatement's more often than a fp32 run's (5 % of rays against 1 %)."""
+    import ffn_lib as fl
+    print(f"[case] cfg4 marched train mlp={mlp} T_stop={T_stop}", flush=True)
+    spec = spec_cfg1(hash_opt=1, mlp_precision=mlp)
+    p = _render_params(spec, seed=421, bias=8.0)
+    rays = _cfg4_rays(384, seed=422)
+    tg = sphere_targets(rays, spec)
+    mp = fl.march_params(R4, DT4, STEPS4, T_stop=T_stop)
+    for step in range(2):
+        sc = default_scalars(rng_seed=4000 + step, occ_strength=0.0)
+        m, _, stats = compare_marched_step(spec, p, rays, tg, field4, mp, sc, gh, ora,
+                                           flip_frac=0.01 if mlp == 0 else 0.05)
+        print(f"[step {step}] {stats}", flush=True)
+        assert stats["samples"] > 5000
+        p = m.state()
+        del m
+
+
+def test_adam_cfg4_sparse_rows_bit_exact(gh, ora):
+    """configs[4]'s optimizer pass: Adam over 16 levels x 2^22 entries x 2 features (2^27 parameters) with
+    nonzero moments, where 5 % of the rows (entries) carry N(0, 1e-3) gradients and the rest zero, bit-exact
+    against the restatement (parameters, both moments), and the gradient cleared in the same pass."""
+    import torch
+    import ffn_lib as fl
+    print("[case] cfg4 sparse adam 2^27", flush=True)
+    rng = np.random.default_rng(431)
+    n = 16 * (1 << 22) * 2
+    p = rng.uniform(-1e-4, 1e-4, n).astype(np.float32)
+    m = (rng.normal(size=n) * 1e-4).astype(np.float32)
+    v = (rng.uniform(0.0, 1e-6, n)).astype(np.float32)
+    rows = np.flatnonzero(rng.random(n // 2) < 0.05)
+    g = np.zeros((n // 2, 2), np.float32)
+    g[rows] = (rng.normal(size=(rows.size, 2)) * 1e-3).astype(np.float32)
+    g = g.reshape(-1)
+    t = [gh.to_dev(a) for a in (p, m, v, g)]
+    lr_t = float(np.float32(1e-2 * np.sqrt(1 - 0.99 ** 3) / (1 - 0.9 ** 3)))
+    fl.check(fl.load().ffn_adam(*[fl.ptr(x) for x in t], n, lr_t, 0.9, 0.99, 1e-15, 1, fl.stream_ptr()), "adam")
+    torch.cuda.synchronize()
+    ora.adam(p, m, v, g, lr_t, 0.9, 0.99, 1e-15)
+    for dev, host, name in zip(t[:3], (p, m, v), ("p", "m", "v")):
+        assert np.array_equal(gh.to_np(dev).view(np.uint32), host.view(np.uint32)), name
+    assert not bool(t[3].any())
+
+
+def _spec3():
+    return spec_cfg1(hash_opt=1, log2_T=[22] * 16)
+
+
+@pytest.mark.parametrize("dist", ["uniform", "shell"])
+def test_hash_forward_cfg3_fp32_bit_exact(gh, ora, dist):
+    """configs[3]'s fp32 table (16 x 2^22 x 2, res 16 -> 2048) and point distributions: indices and
+    encodings bit-identical to the oracle's."""
+    print(f"[case] cfg3 hash fwd fp32 {dist}", flush=True)
+    spec = _spec3()
+    p = random_params(spec, seed=441)
+    m = gh.GpuModel(spec, p)
+    x = cfg3_points(30000, dist, seed=442)
+    a0_g, idx_g = m.encode(x, with_idx=True)
+    a0_o, idx_o, _ = ora.hash_encode(ora.make_cfg(spec), p["table"], x, with_idx=True)
+    assert np.array_equal(idx_g, idx_o)
+    assert np.array_equal(a0_g.view(np.uint32), a0_o.view(np.uint32))
+
+
+@pytest.mark.parametrize("dist", ["uniform", "shell"])
+def test_hash_backward_cfg3_fp32(gh, ora, dist):
+    """configs[3]'s scatter-add of N(0, 1) upstream gradients into the 16 x 2^22 x 2 fp32 gradient table:
+    within 1e-5 of the largest entry of the oracle's float64 sums, the same entries touched.  The shell
+    points pile many samples onto the entries of the shell's cells (long runs of equal cells at the coarse
+    levels, many contributions per entry at every level)."""
+    print(f"[case] cfg3 hash bwd fp32 {dist}", flush=True)
+    spec = _spec3()
+    m = gh.GpuModel(spec, random_params(spec, seed=451))
+    n = 40000
+    x = cfg3_points(n, dist, seed=452)
+    LF = spec["n_levels"] * spec["f_per_level"]
+    g = np.random.default_rng(453).normal(size=(n, LF)).astype(np.float32)
+    grad_g = m.encode_bwd(x, g, table_floats(spec))
+    grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
+    scale = np.abs(grad_o).max()
+    assert np.isfinite(grad_g).all()
+    assert np.abs(grad_g - grad_o).max() <= 1e-5 * scale
+    assert ((grad_g != 0) == (grad_o != 0)).mean() > 0.9999

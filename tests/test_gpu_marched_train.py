@@ -2,6 +2,8 @@
 (ora_train_step_marched): samples from the DDA march through an occupancy bitfield instead of the resampler,
 compositing that stops once T < T_stop, the Charbonnier loss, the MLP backward, the table update and the MLP
 Adam.  How each difference is accounted for is described in parity.compare_marched_step."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -36,11 +38,16 @@ def shell_bits(R, seed=0, frac=0.02):
     return bits
 
 
-@pytest.mark.parametrize("T_stop,hash_opt,table,mlp", [(1e-2, 1, "fp32", 0), (0.0, 1, "fp32", 0), (1e-2, 0, "fp32", 0),
-                                                       (1e-2, 1, "fp16", 0), (1e-2, 0, "fp16", 0),
-                                                       (1e-2, 1, "fp32", 1), (0.0, 0, "fp16", 1)])
-def test_marched_steps_match_oracle(gh, ora, T_stop, hash_opt, table, mlp):
-    print(f"[case] marched train T_stop={T_stop} hash_opt={hash_opt} table={table} mlp_precision={mlp}", flush=True)
+@pytest.mark.parametrize("T_stop,hash_opt,table,mlp,occ", [(1e-2, 1, "fp32", 0, 0.0), (0.0, 1, "fp32", 0, 0.0),
+                                                           (1e-2, 0, "fp32", 0, 0.0), (1e-2, 1, "fp16", 0, 0.0),
+                                                           (1e-2, 0, "fp16", 0, 0.0), (1e-2, 1, "fp32", 1, 0.0),
+                                                           (0.0, 0, "fp16", 1, 0.0), (1e-2, 1, "fp32", 0, 1.0),
+                                                           (0.0, 1, "fp32", 1, 1.0)])
+def test_marched_steps_match_oracle(gh, ora, T_stop, hash_opt, table, mlp, occ):
+    """Three marched steps from the GPU's state; with occ = 1 the steps also make the occupancy proposals of
+    their marched runs (checked word for word against the restatement fed the GPU's transmittances)."""
+    print(f"[case] marched train T_stop={T_stop} hash_opt={hash_opt} table={table} mlp_precision={mlp} occ={occ}",
+          flush=True)
     import ffn_lib as fl
     spec = spec_cfg0(occ_G=R // 2, hash_opt=hash_opt, table_dtype=table, mlp_precision=mlp)
     p = random_params(spec, seed=41)
@@ -51,8 +58,9 @@ def test_marched_steps_match_oracle(gh, ora, T_stop, hash_opt, table, mlp):
     tg = sphere_targets(rays, spec)
     bits = shell_bits(R, seed=43, frac=0.2)
     mp = fl.march_params(R, DT, 128, T_stop=T_stop)
+    raised = 0
     for step in range(3):
-        sc = default_scalars(rng_seed=1000 + step, occ_strength=0.0)
+        sc = default_scalars(rng_seed=1000 + step, occ_strength=occ)
         m, _, stats = compare_marched_step(spec, p, rays, tg, bits, mp, sc, gh, ora)
         print(f"[step {step}] {stats}", flush=True)
         assert stats["samples"] > 2000
@@ -60,7 +68,10 @@ def test_marched_steps_match_oracle(gh, ora, T_stop, hash_opt, table, mlp):
             assert stats["composited"] < stats["samples"]  # some rays terminate early
         else:
             assert stats["composited"] == stats["samples"]
+        raised += stats.get("occ_raised", 0)
         p = m.state()  # the next step starts from the GPU's state, as training does
+    if occ > 0.0:
+        assert raised > 20, raised
 
 
 def test_marched_step_without_samples(gh, ora):
@@ -103,8 +114,8 @@ def test_marched_step_without_samples(gh, ora):
 @pytest.mark.parametrize("mlp", [0, 1])
 def test_train_step_with_the_march_sampler(gh, ora, mlp):
     """ffn_config.sampler = march: ffn_train_step builds the bitfield from occ_in (q >= march_q_min) and runs
-    the marched step; the result equals ffn_train_step_marched fed with ffn_occ_bitfield's field, bit for bit
-    (state and colours), and a forward-only call equals ffn_render."""
+    the marched step with its proposals; the result equals ffn_train_step_marched fed with ffn_occ_bitfield's
+    field, bit for bit (state, occupancy grids and colours), and a forward-only call equals ffn_render."""
     print(f"[case] march sampler through ffn_train_step, mlp_precision={mlp}", flush=True)
     import ffn_lib as fl
     spec = spec_cfg0(occ_G=R // 2, hash_opt=1, mlp_precision=mlp, sampler="march", march_max_steps=128,
@@ -113,7 +124,7 @@ def test_train_step_with_the_march_sampler(gh, ora, mlp):
     p["bd_out"][0] = 8.0
     rays = look_at_rays(256, spec, seed=62, miss_frac=0.1)
     tg = sphere_targets(rays, spec)
-    sc = default_scalars(rng_seed=63, occ_strength=0.0)
+    sc = default_scalars(rng_seed=63, occ_strength=1.0)
     a = gh.GpuModel(spec, p)
     out_a, _ = a.train_step(rays, tg, 64, sc)
     b = gh.GpuModel(spec, p)
@@ -156,3 +167,65 @@ def test_one_walk_march_equals_the_two_walk_march(gh, ora, mlp, monkeypatch):
         np.testing.assert_array_equal(a, b)
     for k in res[0][3]:
         np.testing.assert_array_equal(res[0][3][k], res[1][3][k], err_msg=k)
+
+
+def test_march_sampler_grid_follows_the_density(gh):
+    """A fresh model under the march sampler: every subcell starts at level 15 (>= march_q_min 4), so the
+    first bitfield holds the whole box.  Trained through Nerf.step on the analytic ball (cfg0 model shape,
+    1024 rays aimed at the ball per step, proposals every step and the decay 0.9 every 16 steps), the
+    proposals of the marched runs keep the ball's subcells while the decay prunes the empty ones: after 320
+    steps the march takes under half the samples of the first step, the subcell at the ball's centre is still
+    marched, and the model has learned the ball (held-out PSNR well above the black background)."""
+    import tempfile
+    import torch
+    import ffn_lib as fl
+    import ffnerf_tools as ft
+    import trainer
+    print("[case] march sampler on a fresh model: the grid follows the density", flush=True)
+    G, max_steps = 32, 256
+    dt = float(np.float32(np.sqrt(3.0) / max_steps))
+    spec = ft.ModelSpec(n_levels=8, f_per_level=2, log2_T=[14] * 8, res=ft.level_resolutions(8, 16.0, growth=1.5),
+                        nd=1, nc=2, background="black", hash_opt="adam", init="xavier", beta1=0.9, beta2=0.99,
+                        eps=1e-15, sampler="march", march_max_steps=max_steps, march_dt=dt, march_T_stop=1e-4,
+                        march_q_min=4)
+    occ = ft.OccParams(G_occ=G, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32),
+                       occ_update_strength0=1.0, decay=0.9, maintenance_period=16)
+    nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_marchgrid_"), "m", spec=spec, occ=occ, rng_seed=3)
+    box = spec_cfg0()
+    n_rays = 1024
+    io = ft.RayBatch.init(n_rays, 64)
+    probe = look_at_rays(n_rays, box, seed=5, miss_frac=0.0)
+    probe_t = gh.to_dev(probe)
+    mp = fl.march_params(2 * G, dt, max_steps)
+    counts = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    offs = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
+    total = torch.zeros(4, dtype=torch.int32, device="cuda")
+
+    def marched():
+        bits = nerf.occupancy_bitfield(q_min=4)
+        fl.check(nerf.handle.lib.ffn_march(nerf.handle.h, fl.ptr(probe_t), n_rays, fl.ptr(bits), ctypes.byref(mp),
+                                           fl.ptr(counts), fl.ptr(offs), None, None, 0, fl.ptr(total),
+                                           fl.stream_ptr()), "ffn_march")
+        torch.cuda.synchronize()
+        return int(total[0].item()), bits.cpu().numpy().view(np.uint32)
+
+    n0, _ = marched()
+    for step in range(1, 321):
+        rays = look_at_rays(n_rays, box, seed=2000 + step, miss_frac=0.0)
+        io.upload_rays(rays)
+        io.upload_targets(sphere_targets(rays, box))
+        nerf.step(io, lr_f=1e-2, do_train=True, occ_update_strength=1.0)
+    n1, bits = marched()
+    R = 2 * G
+    centre = (R // 2) + R * ((R // 2) + R * (R // 2))
+    ev_rays = look_at_rays(2048, box, seed=7, miss_frac=0.0)
+    ev_tg = sphere_targets(ev_rays, box)
+    ev = ft.RayBatch.init(2048, 64)
+    ev.upload_rays(ev_rays)
+    ev.upload_targets(ev_tg)
+    out, _ = nerf.step(ev, lr_f=0.0, do_train=False, occ_update_strength=0.0, return_output=True)
+    p, black = trainer.psnr(out, ev_tg), trainer.psnr(np.zeros_like(out), ev_tg)
+    print(f"[march grid] samples marched {n0} -> {n1}, PSNR {p:.2f} dB (black {black:.2f} dB)", flush=True)
+    assert n1 < 0.5 * n0
+    assert (bits[centre >> 5] >> (centre & 31)) & 1
+    assert p > black + 3.0

@@ -9,6 +9,9 @@ ffnerf_OG.cl:1640-1821) and of the sampler's proposal weights
   16 * pred, with mean 16 * pred over seeds;
 - the keep probability's closed form against the keep frequency over seeds
   (a ray inside the distance where near-camera proposals are thinned);
+- the marched proposal pass cuts a ray's samples into runs itself: fed a
+  resampled ray's samples, its runs are the resampler's run flags, so it raises
+  the grid exactly as the resampled pass with those flags does;
 - a ray through two occupancy levels: systematic resampling puts
   S * P(first half) samples (to within one) into the first half, where
   P = 0.3 * 1/2 + 0.7 * w_a / (w_a + w_b), w = (rho dt)^1.3 -- in float64,
@@ -234,3 +237,36 @@ def test_sampler_weights_have_power():
     p = _p_first_half(16, 1)
     assert abs(64 * p - 64 * _p_first_half(16, 1, gamma=1.0)) > 2.0
     assert abs(64 * p - 64 * _p_first_half(16, 1, uniform=0.5)) > 2.0
+
+
+def test_marched_runs_are_the_samplers_runs(ora):
+    """ora_occ_propose_marched_ray finds the runs of one (cell, subcell) in a ray's samples by itself.  Fed the
+    samples of resampled rays (every sample active, so that both passes see the same samples), it must raise
+    occ_st exactly as ora_occ_propose_ray does with the resampler's own run flags (the key of the reference's
+    sampler), for transmittances that fall along the ray and low occupancy levels (many proposals)."""
+    from common import look_at_rays
+    spec = spec_cfg0()
+    cfg = ora.make_cfg(spec)
+    rng = np.random.default_rng(17)
+    S = 64
+    occ_in = (rng.integers(0, 3, (G ** 3, 8)).astype(np.uint32) << (4 * np.arange(8, dtype=np.uint32))).sum(
+        axis=1).astype(np.uint32)
+    rays = look_at_rays(300, spec, seed=18, miss_frac=0.0)
+    compared = raised = multi = 0
+    for r, ray in enumerate(rays):
+        seed = 0xC0FFEE + 31 * r
+        Ts, DTs, flags = ora.sample_ray(cfg, ray, r, S, seed, occ_in, True)
+        if not (DTs > 0).all():
+            continue
+        Tr = np.cumprod(np.concatenate([[1.0], rng.uniform(0.6, 1.0, S - 1)])).astype(np.float32)
+        T_final = np.float32(Tr[-1] * rng.uniform(0.5, 1.0))
+        a, b = occ_in.copy(), occ_in.copy()
+        _propose(ora, cfg, ray, S, seed, Ts, DTs, Tr, T_final, flags, occ_in, a)  # as ray 0
+        ora.lib().ora_occ_propose_marched_ray(C.byref(cfg), ora.fptr(np.ascontiguousarray(ray, np.float32)), 0, S,
+                                              seed, ora.fptr(Ts), ora.fptr(Tr), C.c_float(T_final),
+                                              ora.uptr(occ_in), ora.uptr(b))
+        assert np.array_equal(a, b), r
+        compared += 1
+        raised += int((a != occ_in).sum())
+        multi += int(len(_runs(flags, S)) < S)
+    assert compared > 100 and raised > 200 and multi > 50, (compared, raised, multi)

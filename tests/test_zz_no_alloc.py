@@ -1,8 +1,9 @@
 """ffn_march_noalloc -- the march whose scan scratch lives in the library's
 fixed device array instead of handle-owned allocations -- against ffn_march,
-bit for bit, through the C ABI: two calls in a row on one handle, the second
-with fewer rays (the array keeps the first call's contents), and a ray count
-beyond the array refused with an error before any launch."""
+bit for bit, through the C ABI: three calls in a row on one handle, the first
+at the largest ray count the array holds (FFN_MARCH_NOALLOC_MAX_RAYS), the
+next ones with fewer rays (the array keeps the previous call's contents), and
+a ray count beyond the array refused with an error before any launch."""
 import ctypes as C
 
 import numpy as np
@@ -50,11 +51,13 @@ def test_march_noalloc_matches_march():
         pytest.fail("no GPU visible")
     g = GpuModel(SPEC, random_params(SPEC, seed=1))
     lib, h = g.lib, g.h.h
-    R, max_steps = 64, 300
+    R = 64
     bits_t = to_dev(_shell_bits(R, seed=5))
-    mp = fl.march_params(R, np.float32(np.sqrt(3.0) / 256), max_steps)
-    for n in (6000, 1700):  # the second call with fewer rays, on the array the first one left behind
-        print(f"[case] march_noalloc n={n}", flush=True)
+    # the largest accepted call first (its offsets and tile sums fill the array exactly), then calls with fewer
+    # rays on the array the previous one left behind
+    for n, max_steps in ((fl.MARCH_NOALLOC_MAX_RAYS, 4), (6000, 300), (1700, 300)):
+        print(f"[case] march_noalloc n={n} max_steps={max_steps}", flush=True)
+        mp = fl.march_params(R, np.float32(np.sqrt(3.0) / 256), max_steps)
         rays_t = to_dev(look_at_rays(n, SPEC, seed=n).reshape(-1, 8))
         cap = n * max_steps
         ref = _march(lib, "ffn_march", h, rays_t, n, bits_t, mp, cap)
