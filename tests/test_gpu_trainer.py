@@ -237,50 +237,55 @@ def test_psnr_matches_oracle_after_training(torch):
     assert abs(p_g - p_o) < 0.3
 
 
-@pytest.mark.parametrize("mlp", ["fp32", "fp16"])
-def test_full_batch_training_learns(torch, mlp):
+def test_full_batch_training_learns_on_both_mlp_paths(torch):
     """Training at the benchmark's full shape: cfg2 model (16 levels of 2^19 entries, Adam), 2^18 rays x 64
-    samples per step from 16 resident batches of the synthetic ball scene, constant lr 1e-2.  Held-out PSNR
-    on 65536 rays must rise at least 10 dB above the black background within 300 steps.  Observed over
-    three seeds: 31-37 dB at step 300, with the fp32 and fp16 curves within 0.6 dB of each other for two
-    seeds and the third showing the run-to-run spread of the trajectories (fp32 31.2, fp16 36.6 dB)."""
+    samples per step from 16 resident batches of the synthetic ball scene, constant lr 1e-2, proposals every
+    step and the decay 0.95 every 16 steps, on the fp32 and the fp16/bf16 MLP path from the same initial state
+    and rng seed.  Held-out PSNR on 65536 rays must rise at least 10 dB above the black background within 300
+    steps on both paths, and the two must end within 0.5 dB of each other.  Measured over seeds 1-3: 36.60 /
+    36.83, 36.83 / 36.75 and 36.97 / 36.72 dB (fp32 / fp16); a seed's two paths track each other within 0.5 dB
+    at every 50th step while the seeds' early curves differ by up to 12 dB (15.3 against 27.8 dB at step 50)."""
     import tempfile
     import ffnerf_tools as ft
     import synthetic_scene as sc
     import trainer
-    print(f"[case] full-batch training {mlp}", flush=True)
+    print("[case] full-batch training, fp32 and fp16 MLP paths", flush=True)
     L, S, n_rays = 16, 64, 1 << 18
-    spec = ft.ModelSpec(n_levels=L, f_per_level=2, log2_T=[19] * L, res=ft.level_resolutions(L, 16.0, finest=2048.0),
-                        nd=1, nc=2, background="black", hash_opt="adam", mlp_precision=mlp, init="xavier",
-                        beta1=0.9, beta2=0.99, eps=1e-15)
-    occ = ft.OccParams(G_occ=64, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32), rho_min=1.0,
-                       rho_max=16.0, dt_min=np.float32(1.0 / 8192), dt_max=np.float32(12.8 / S / 6), t_near_clip=0.3,
-                       t_far_clip=1e9, occ_update_strength0=1.0, decay=0.95, maintenance_period=16)
-    nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_fulltrain_"), "t", spec=spec, occ=occ, rng_seed=1)
     cams = sc.cameras_for("cfg2")
     rng = np.random.default_rng(321)
-    pool = []
-    for _ in range(16):
-        rays, tg = sc.uniform_batch(cams, n_rays, rng)
-        io = ft.RayBatch.init(n_rays, S)
-        io.upload_rays(rays)
-        io.upload_targets(tg)
-        pool.append(io)
+    batches = [sc.uniform_batch(cams, n_rays, rng) for _ in range(16)]
     ev_rays, ev_tg = sc.uniform_batch(cams, 1 << 16, np.random.default_rng(999))
-    ev = ft.RayBatch.init(1 << 16, S)
-    ev.upload_rays(ev_rays)
-    ev.upload_targets(ev_tg)
     black = trainer.psnr(np.zeros((1 << 16, 4), np.float32), ev_tg)
-    for k in range(1, 301):
-        nerf.step(pool[k % len(pool)], lr_f=1e-2, do_train=True, occ_update_strength=1.0, sh_multiplier=1.0,
-                  color_MLP_rel_lr=1.0)
-    out, _ = nerf.step(ev, lr_f=0.0, do_train=False, occ_update_strength=0.0, return_output=True)
-    p = trainer.psnr(out, ev_tg)
-    print(f"[psnr] {mlp} after 300 full-batch steps: {p:.2f} dB (black {black:.2f} dB)", flush=True)
-    assert np.isfinite(out).all()
-    assert p > black + 10.0
-    del nerf, pool
-    torch.cuda.empty_cache()
+    res = {}
+    for mlp in ("fp32", "fp16"):
+        spec = ft.ModelSpec(n_levels=L, f_per_level=2, log2_T=[19] * L,
+                            res=ft.level_resolutions(L, 16.0, finest=2048.0), nd=1, nc=2, background="black",
+                            hash_opt="adam", mlp_precision=mlp, init="xavier", beta1=0.9, beta2=0.99, eps=1e-15)
+        occ = ft.OccParams(G_occ=64, box_min=np.zeros(3, np.float32), box_max=np.ones(3, np.float32), rho_min=1.0,
+                           rho_max=16.0, dt_min=np.float32(1.0 / 8192), dt_max=np.float32(12.8 / S / 6),
+                           t_near_clip=0.3, t_far_clip=1e9, occ_update_strength0=1.0, decay=0.95,
+                           maintenance_period=16)
+        nerf = ft.Nerf(tempfile.mkdtemp(prefix="ffn_fulltrain_"), "t", spec=spec, occ=occ, rng_seed=1)
+        pool = []
+        for rays, tg in batches:
+            io = ft.RayBatch.init(n_rays, S)
+            io.upload_rays(rays)
+            io.upload_targets(tg)
+            pool.append(io)
+        ev = ft.RayBatch.init(1 << 16, S)
+        ev.upload_rays(ev_rays)
+        ev.upload_targets(ev_tg)
+        for k in range(1, 301):
+            nerf.step(pool[k % len(pool)], lr_f=1e-2, do_train=True, occ_update_strength=1.0, sh_multiplier=1.0,
+                      color_MLP_rel_lr=1.0)
+        out, _ = nerf.step(ev, lr_f=0.0, do_train=False, occ_update_strength=0.0, return_output=True)
+        assert np.isfinite(out).all()
+        res[mlp] = trainer.psnr(out, ev_tg)
+        print(f"[psnr] {mlp} after 300 full-batch steps: {res[mlp]:.2f} dB (black {black:.2f} dB)", flush=True)
+        del nerf, pool
+        torch.cuda.empty_cache()
+    assert min(res.values()) > black + 10.0
+    assert abs(res["fp32"] - res["fp16"]) < 0.5
 
 
 def test_reference_layout_checkpoint_loads_and_steps(torch, tmp_path):
