@@ -55,7 +55,11 @@ __global__ __launch_bounds__(256) void k_make_batch(const float* __restrict__ im
 // floor(h_t W H / 2^32) of that image, h_t = lowbias32(h0 ^ (t + 1) * 0x9E3779B9), accepted when
 // lowbias32(h_t ^ 0x5BD1E995) & 255 <= its weight, i.e. with probability (w + 1) / 256 as the reference's
 // rng.integers(0, 256) <= w.  Rays r < uniform_rays keep proposal 0; the others keep the first accepted
-// proposal, or proposal max_tries - 1 when none is (the reference's bounded sampler does the same).
+// proposal, or proposal max_tries - 1 when none is.  Two deliberate departures from the reference: its
+// rejection loop has no bound (run_ffnerf_OG.py:508-514; at max_tries = 4096 every weight >= 1 leaves a ray
+// on its last proposal with probability <= (254/256)^4096 < 2e-14, all weights 0 <= 1.2e-7), and its uniform
+// share is int(0.2 B_im) rays within each image's group (run_ffnerf_OG.py:503,677), here the first
+// uniform_rays rays of the batch, whose images are drawn like every ray's.
 __global__ __launch_bounds__(256) void k_make_batch_weighted(
     const float* __restrict__ images, uint32_t n_images, uint32_t W, uint32_t H, const float* __restrict__ c2w,
     const float* __restrict__ K, const uint8_t* __restrict__ weights, uint32_t num_rays, uint32_t uniform_rays,

@@ -172,8 +172,22 @@ def fit_within(w: int, h: int, max_side) -> tuple:
 
 
 def read_rgb(path) -> np.ndarray:
-    """uint8 [H, W, 3] RGB."""
-    im = png_io.read_png(path)
+    """uint8 [H, W, 3] RGB.  PNG through the package's own codec; any other format (the JPEGs most SfM
+    archives list, which the reference reads with cv2.imread, sfm_data.py:80,105) through Pillow when it
+    imports, upright by the file's EXIF orientation as cv2.imread leaves it."""
+    with open(path, "rb") as f:
+        is_png = f.read(8) == b"\x89PNG\r\n\x1a\n"
+    if is_png:
+        im = png_io.read_png(path)
+    else:
+        try:
+            from PIL import Image, ImageOps
+        except ImportError:
+            raise ValueError("not a PNG, and Pillow (needed for other image formats) is not installed") from None
+        with Image.open(path) as pim:
+            im = np.asarray(ImageOps.exif_transpose(pim).convert("RGB"), dtype=np.uint8)
+    if im.ndim == 2:
+        im = im[:, :, None]
     if im.shape[2] == 1:
         im = np.repeat(im, 3, axis=2)
     return im[:, :, :3]

@@ -16,8 +16,13 @@ every loss report updates from the batch's per-ray colour errors
 (run_ffnerf_OG.py:402-686; pixel_weights.py); "uniform" draws every pixel
 uniformly over all images.  The images stay resident on the GPU and every
 batch's rays and targets are produced there (ffn_make_batch_weighted,
-ffn_make_batch), so no per-step host work or host-to-device copy remains.  The preview server, viewer and review UI are
-not part of this build.
+ffn_make_batch), so no per-step host work or host-to-device copy remains.
+Training previews are exported as the reference exports them
+(run_ffnerf_OG.py:1160-1190, 1519-1545): the configured views rendered
+forward-only at preview.width x preview.height divided by preview.downscale
+(block centres), side by side in <model_id>_preview_<W>p_step<step>_multiview.png,
+at the first step and every preview.image_seconds.  The preview server,
+viewer and review UI are not part of this build.
 """
 from __future__ import annotations
 
@@ -126,6 +131,50 @@ def occ_params(cfg: dict, box_min, box_max) -> ft.OccParams:
                         decay=float(m["occ_decay"]), maintenance_period=int(m["occ_period"]))
 
 
+def preview_rays(cfg: dict, poses: np.ndarray, K: np.ndarray, W: int, H: int):
+    """Rays of the preview views (run_ffnerf_OG.py:1160-1190): each registered camera of preview.views seen
+    at preview.width x preview.height (K scaled to that size), one ray per block of preview.downscale^2
+    pixels through the block's centre.  Returns ([rays [W_ds * H_ds, 8] per view], W_ds, H_ds)."""
+    p = cfg["preview"]
+    W_prev, H_prev, down = int(p["width"]), int(p["height"]), int(p["downscale"])
+    views = p["views"]
+    if any(type(i) is not int or i < 0 or i >= len(poses) for i in views):
+        raise ValueError("preview.views must contain valid registered-camera indices")
+    K_prev = np.asarray(K, np.float32).copy()
+    K_prev[0] *= W_prev / W
+    K_prev[1] *= H_prev / H
+    W_ds, H_ds = W_prev // down, H_prev // down
+    idx = np.clip(np.tile(np.arange(W_ds, dtype=np.int32), H_ds) * down + down // 2, 0, W_prev - 1)
+    idy = np.clip(np.repeat(np.arange(H_ds, dtype=np.int32), W_ds) * down + down // 2, 0, H_prev - 1)
+    rays = [ft.rays_as_array(ft.rays_from_rt_indices(poses[v], idx, idy, W_prev, H_prev, K=K_prev)) for v in views]
+    return rays, W_ds, H_ds
+
+
+def preview_jobs(cfg: dict, poses: np.ndarray, K: np.ndarray, W: int, H: int) -> list:
+    """The preview views' rays resident on the GPU, one batch per view."""
+    rays, W_ds, H_ds = preview_rays(cfg, poses, K, W, H)
+    jobs = []
+    for v, r in zip(cfg["preview"]["views"], rays):
+        io = ft.RayBatch.init(W_ds * H_ds, int(cfg["preview"]["samples_per_ray"]))
+        io.upload_rays(r)
+        jobs.append(dict(view=v, io=io, W_ds=W_ds, H_ds=H_ds))
+    return jobs
+
+
+def write_preview(nerf: ft.Nerf, jobs: list, training_dir, model_id: str, step: int) -> Path:
+    """Render the preview views forward-only and write them side by side as one 8-bit PNG
+    (run_ffnerf_OG.py:1519-1545)."""
+    import png_io
+    imgs = []
+    for job in jobs:
+        out, _ = nerf.step(job["io"], lr_f=0.0, do_train=False, occ_update_strength=0.0, return_output=True)
+        img = np.clip(out[:, :3].reshape(job["H_ds"], job["W_ds"], 3), 0.0, 1.0)
+        imgs.append((img * 255).astype(np.uint8))
+    path = Path(training_dir) / f"{model_id}_preview_{jobs[0]['W_ds']}p_step{step}_multiview.png"
+    png_io.write_png(path, np.concatenate(imgs, axis=1))
+    return path
+
+
 _STOP = False
 
 
@@ -166,12 +215,15 @@ def train(cfg: dict, load_id: str | None = None, log=print, eval_every: int = 0,
         eval_io = ft.RayBatch.init(eval_rays, S)
         eval_io.upload_rays(rays_e)
         eval_io.upload_targets(tg_e)
+    jobs = preview_jobs(cfg, poses, K, W, H) if cfg["preview"]["views"] else []
     loss_path, loss_f = open_loss_log(t["directory"], t["model_id"])
     old = signal.signal(signal.SIGINT, _on_sigint)
     t0 = time.time()
     last_save = t0
+    last_preview = None  # the first preview is written at the first step
     save_every = float(cfg["preview"]["save_seconds"])
-    history, evals = [], []
+    preview_every = float(cfg["preview"]["image_seconds"])
+    history, evals, previews = [], [], []
     step0 = int(nerf.steps_trained)
     try:
         for k in range(int(t["steps"])):
@@ -208,6 +260,10 @@ def train(cfg: dict, load_id: str | None = None, log=print, eval_every: int = 0,
             if time.time() - last_save > save_every:
                 nerf.save(min_new_file_seconds=300)
                 last_save = time.time()
+            if jobs and (last_preview is None or time.time() - last_preview > preview_every):
+                previews.append(write_preview(nerf, jobs, t["directory"], t["model_id"], step))
+                log(f"[preview] saved {previews[-1]}")
+                last_preview = time.time()
         torch.cuda.synchronize()
     finally:
         saved = nerf.save(min_new_file_seconds=0)
@@ -215,4 +271,5 @@ def train(cfg: dict, load_id: str | None = None, log=print, eval_every: int = 0,
         signal.signal(signal.SIGINT, old)
     log(f"Saved model -> {saved}")
     return dict(steps_trained=int(nerf.steps_trained), loss_log=str(loss_path), checkpoint=str(saved),
-                history=history, evals=evals, nerf=nerf, pixel_weights=weights)
+                history=history, evals=evals, previews=[str(p) for p in previews], nerf=nerf,
+                pixel_weights=weights)

@@ -131,6 +131,9 @@ def test_cli_train_resume_snapshot(torch, tmp_path):
     # (learning itself is checked on held-out rays by the PSNR test)
     assert len(mse) >= 6 and np.all(np.isfinite(mse)) and max(mse[-3:]) < 0.1, mse
     assert (run / "ball_weights_latest.npz").exists()
+    # the training preview of the first step (preview defaults: 360 x 640 / 5, views 0, 1, 2 side by side)
+    prev = sorted(run.glob("ball_preview_72p_step1_multiview.png"))
+    assert len(prev) == 1 and png_io.read_png(prev[0]).shape == (128, 3 * 72, 3)
     print("[case] cli resume", flush=True)
     assert ffnerf_cli.main(["train", "--config", str(path), "--resume", "ball", "--steps", "10"]) == 0
     data = np.load(run / "ball_weights_latest.npz")

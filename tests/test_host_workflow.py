@@ -259,3 +259,97 @@ def test_reference_checkpoint_layout_loads(tmp_path):
             assert np.array_equal(host[pre + name].reshape(-1).view(np.int32), data[pre + name + "_i"]), pre + name
     assert not host["m_table"].any() and not host["v_table"].any()
     assert np.array_equal(host["occ_in"], data["occ_grid_in_u32"])
+
+
+def test_jpeg_archive_reads_back(tmp_path):
+    """An archive that lists JPEGs (as most SfM archives do; the reference reads them with cv2.imread): the
+    images decode through Pillow to the pixels Pillow itself decodes, and a JPEG whose EXIF orientation says
+    "rotate" comes back upright, as cv2.imread returns it."""
+    from PIL import Image
+    from sfm_data import read_rgb
+    rng = np.random.default_rng(5)
+    arrs = [np.clip(rng.normal(120, 40, (48, 32, 3)), 0, 255).astype(np.uint8) for _ in range(2)]
+    for i, a in enumerate(arrs):
+        Image.fromarray(a).save(tmp_path / f"{i}.jpg", quality=95)
+    ref = [np.asarray(Image.open(tmp_path / f"{i}.jpg").convert("RGB")) for i in range(2)]
+    K = np.array([[40, 0, 16], [0, 40, 24], [0, 0, 1]], np.float32)
+    data = {"reconstruction": str(tmp_path / "scene.npz"), "images_dir": str(tmp_path), "sfm_max_side": 0,
+            "max_side": 0}
+    np.savez(data["reconstruction"], K=K, img_paths=np.array(["0.jpg", "1.jpg"]), RT=np.tile(np.eye(4), (2, 1, 1)),
+             rt_dir=np.array(["c2w"]))
+    paths, _, _, _, _ = read_scene(data)
+    images, _, (W, H) = load_images(data, paths, K)
+    assert (W, H) == (32, 48)
+    for i in range(2):
+        np.testing.assert_array_equal(np.round(images[i] * 255).astype(np.uint8), ref[i])
+    # EXIF orientation 6 (rotate 90 degrees clockwise to view): read back 32 x 48 -> 48 rows become columns
+    exif = Image.Exif()
+    exif[0x0112] = 6
+    Image.fromarray(arrs[0]).save(tmp_path / "rot.jpg", quality=95, exif=exif)
+    assert read_rgb(tmp_path / "rot.jpg").shape == (32, 48, 3)
+    (tmp_path / "bad.jpg").write_bytes(b"not an image")
+    with pytest.raises(Exception):
+        read_rgb(tmp_path / "bad.jpg")
+
+
+def test_preview_rays_are_block_centres(tmp_path):
+    """The training previews' rays (run_ffnerf_OG.py:1160-1190): preview.width x preview.height divided by
+    preview.downscale, one ray through each block's centre pixel of the configured view, with the intrinsics
+    scaled from the training image size to the preview size; views outside the registered cameras refused."""
+    cfg = load_config(_synthetic_config(tmp_path))
+    paths, poses, K, _, _ = read_scene(cfg["data"])
+    cfg["preview"].update(width=40, height=24, downscale=4, views=[1, 5])
+    rays, W_ds, H_ds = trainer.preview_rays(cfg, poses, K, 64, 64)
+    assert (W_ds, H_ds) == (10, 6) and len(rays) == 2 and rays[0].shape == (60, 8)
+    K_prev = np.asarray(K, np.float32).copy()
+    K_prev[0] *= 40 / 64
+    K_prev[1] *= 24 / 64
+    r = 1 * 10 + 3  # block (x 3, y 1): its centre pixel (14, 6)
+    want = ft.rays_as_array(ft.rays_from_rt_indices(poses[5], [3 * 4 + 2], [1 * 4 + 2], 40, 24, K=K_prev))
+    np.testing.assert_array_equal(rays[1][r], want[0])
+    cfg["preview"]["views"] = [8]
+    with pytest.raises(ValueError, match="preview.views"):
+        trainer.preview_rays(cfg, poses, K, 64, 64)
+
+
+@pytest.mark.parametrize("init", ["he", "xavier"])
+def test_fresh_init_follows_the_reference(init):
+    """R17, a fresh model (ffnerf_tools.py:836-895 of the reference): the table ~ U(+-1e-4) drawn first from
+    the seeded generator, then the active weights in kernel-argument order (He: N(0, 2 / fan_in), output
+    heads of <= 16 rows N(0, 0.01); Xavier: U(+-sqrt(6 / (fan_in + fan_out)))), the density head's bias
+    bd_out[0] = -2 and, under He, bc_2 ~ N(-2, 0.05); zero moments, every occupancy nibble 14 (words
+    0xEEEEEEEE).  The moments are checked against the distributions' closed forms with bounds a plausible
+    mistake breaks (fan_out for fan_in: the 64 x 32 colour input layer tells them apart)."""
+    spec = ft.ModelSpec(n_levels=16, f_per_level=4, nd=2, nc=3, init=init)
+    occ = ft.OccParams(G_occ=32)
+    occ.finalize()
+    p = ft.init_params(spec, occ, np.random.default_rng(7))
+    n_tab = spec.table_entries() * spec.f_per_level
+    np.testing.assert_array_equal(p["table"], np.random.default_rng(7).uniform(-1e-4, 1e-4, n_tab).astype(np.float32))
+    shapes = spec.layer_shapes()
+    assert set(shapes) == {"Wd_in", "Wd_01", "Wd_out", "Wc_in", "Wc_01", "Wc_12", "Wc_out"}
+    for wn, (rows, fan_in) in shapes.items():
+        w = p[wn].astype(np.float64)
+        assert w.shape == (rows, fan_in)
+        n = w.size
+        if init == "xavier":
+            lim = np.sqrt(6.0 / (rows + fan_in))
+            assert np.abs(w).max() <= lim and np.abs(w).max() > 0.9 * lim, wn
+            var = lim * lim / 3.0
+        else:
+            var = 0.01 ** 2 if rows <= 16 else 2.0 / fan_in
+        sd_var = var * np.sqrt(2.0 / n) * (1.0 if init == "he" else np.sqrt(0.4))  # sd of the sample variance
+        assert abs(w.var() - var) < 5.0 * sd_var, (wn, w.var(), var)
+        assert abs(w.mean()) < 5.0 * np.sqrt(var / n), wn
+    for bn in ("bd_0", "bd_1", "bc_0", "bc_1", "bc_out"):
+        assert not p[bn].any(), bn
+    assert p["bd_out"][0] == np.float32(-2.0) and not p["bd_out"][1:].any()
+    if init == "he":
+        b = p["bc_2"].astype(np.float64)
+        assert abs(b.mean() + 2.0) < 5 * 0.05 / 8 and 0.6 * 0.05 < b.std() < 1.4 * 0.05
+    else:
+        assert not p["bc_2"].any()
+    for k, v in p.items():
+        if k[0] in "mv" and k not in ("table",):
+            assert not v.any(), k
+    assert (p["occ_in"] == 0xEEEEEEEE).all() and (p["occ_st"] == 0xEEEEEEEE).all()
