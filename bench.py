@@ -356,22 +356,7 @@ def run_marched_train(args, pool_rays, pool_tg, mlp="fp32"):
         io.upload_targets(tg)
         pool.append(io)
     used = torch.zeros(n_rays, dtype=torch.int32, device="cuda")
-    one = lambda i: nerf.step_marched(pool[i % len(pool)], 1e-2, bits, R, dt, max_steps=max_steps, T_stop=1e-4,
-                                      n_samples=used)
-    steps = max(1, args.steps // 2)
-    for i in range(args.warmup):
-        one(i)
-    nerf.handle.set_profiling(False)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        one(args.warmup + i)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    composited = int(used.sum().item())  # of the last step
-    stages, ms_prof = profiled_pass(nerf, one, args.warmup + steps, steps)
-    avg = {("march" if k == "sample" else k): (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
-    # samples marched per step (the MLP's work): one march of the same batches
+    # samples marched per step (the MLP's work): one march of each batch
     import ctypes as C
     import ffn_lib as fl
     mp = fl.march_params(R, dt, max_steps)
@@ -385,6 +370,30 @@ def run_marched_train(args, pool_rays, pool_tg, mlp="fp32"):
                                            fl.stream_ptr()))
         torch.cuda.synchronize()
         marched.append(int(total[0].item()))
+    # the step without a host wait: a sample capacity above every batch's total (so no ray is dropped)
+    cap = (int(1.125 * max(marched)) + 4095) // 4096 * 4096
+    one = lambda i, c=0: nerf.step_marched(pool[i % len(pool)], 1e-2, bits, R, dt, max_steps=max_steps,
+                                           T_stop=1e-4, n_samples=used, sample_capacity=c)
+    steps = max(1, args.steps // 2)
+    for i in range(args.warmup):
+        one(i)
+    nerf.handle.set_profiling(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        one(args.warmup + i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    composited = int(used.sum().item())  # of the last step
+    stages, ms_prof = profiled_pass(nerf, one, args.warmup + steps, steps)
+    avg = {("march" if k == "sample" else k): (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
+    one(0, cap)  # the capacity's buffers
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    for i in range(steps):
+        one(args.warmup + i, cap)
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / steps
     n_avg = float(np.mean(marched))
     fwd_b, bwd_b, mlp_flops, _ = algorithmic(spec)
@@ -392,6 +401,7 @@ def run_marched_train(args, pool_rays, pool_tg, mlp="fp32"):
     return {"ms_per_step": ms, "rays": n_rays, "samples_marched_avg": n_avg, "samples_composited_last": composited,
             "value": n_avg / (ms * 1e-3), "unit": "marched samples/s",
             "rays_per_s": n_rays / (ms * 1e-3), "steps": steps, "profiled_ms_per_step": ms_prof,
+            "no_wait": {"ms_per_step": (t3 - t2) * 1e3 / steps, "sample_capacity": cap},
             "stages_ms_avg": {k: round(v, 4) for k, v in avg.items()},
             "hash_grid_gbs": (fwd_b + bwd_b) * n_avg / ((avg["hash_fwd"] + avg["hash_bwd"]) * 1e-3) / 1e9,
             "config": "cfg2 model and ray batches (ball scene), 256^3 bitfield of the ball (r 0.25 + one cell "
@@ -424,6 +434,11 @@ def run_cfg4(args):
                                          n_samples=used)
     t_r = _timed(render, max(1, args.steps // 3), 1)
     n_smp = int(used.sum().item())
+    out_wait = io.out_buf.clone()
+    render_nw = lambda: nerf.render_marched(io, bits, R, dt, max_steps=max_steps, T_stop=1e-4, chunk=chunk,
+                                            n_samples=used, no_wait=True)
+    t_rnw = _timed(render_nw, max(1, args.steps // 3), 1)
+    same_nw = bool(torch.equal(io.out_buf, out_wait)) and int(used.sum().item()) == n_smp
     # march + compaction alone (full march, no termination)
     lib, h = nerf.handle.lib, nerf.handle.h
     mp = fl.march_params(R, dt, max_steps)
@@ -460,6 +475,8 @@ def run_cfg4(args):
                                    "2^20 rays, <=1024 steps/ray, T_stop 1e-4, cfg1 MLPs; Adam over 16x2^22x2 params, "
                                    "5% rows N(0,1e-3)", "rays": n_rays, "bits_set_frac": frac, "chunk": chunk},
             "render": {"ms": t_r, "samples": n_smp, "samples_per_s": n_smp / (t_r * 1e-3)},
+            "render_no_wait": {"ms": t_rnw, "equal_to_waiting": same_nw,
+                               "rounds": (max_steps + chunk - 1) // chunk},
             "march": {"ms": t_m, "samples": cap, "GBps": march_bytes / (t_m * 1e-3) / 1e9,
                       "frac": march_bytes / (t_m * 1e-3) / 1e9 / HBM_PEAK_GBS,
                       "bytes": "40 B/ray (ray + offset, count) + 20 B/sample (xyz t + ray id)"},

@@ -920,6 +920,12 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   if (!(mp->T_stop >= 0.0f && mp->T_stop < 1.0f)) return fail(-1, "T_stop must be in [0,1)");
   if ((uint64_t)num_rays * mp->max_steps >= ((uint64_t)1 << 32))
     return fail(-1, "num_rays * max_steps must stay below 2^32 samples");
+  // sample_capacity > 0: no host wait; buffers and launches for that many samples, the count read on the device
+  const uint32_t cap = mp->sample_capacity;
+  if (cap > 0 && taps) return fail(-1, "taps need sample_capacity = 0 (the per-sample taps are sized on the host)");
+  if ((uint64_t)cap > (uint64_t)num_rays * mp->max_steps)
+    return fail(-1, "sample_capacity=%u exceeds num_rays * max_steps = %llu", cap,
+                (unsigned long long)num_rays * mp->max_steps);
   const int LF = h->dc.LF;
   const bool mlp16 = h->cfg.mlp_precision == FFN_MLP_FP16;
   if (mlp16 ? !ffn::mlp16_supported(LF, h->cfg.nd, h->cfg.nc) : !ffn::mlp_supported(LF, h->cfg.nd, h->cfg.nc))
@@ -934,7 +940,8 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   // 1. march.  With room for max_steps samples per ray, one walk writes each ray's samples to its own slots
   // and its count; the scan of the counts sizes the step (its total comes back to the host) and a copy packs
   // the slots into the scanned order.  Otherwise the walk runs twice: count, scan, emit to the scanned slots.
-  // Both give the same samples in the same order.
+  // Both give the same samples in the same order.  With a sample capacity the total stays on the device: the
+  // rays past the capacity get count 0 (launch_march_clamp) and every later launch reads the kept count.
   const size_t n1 = (size_t)num_rays + 1;
   FFN_HIP(h->m_counts.ensure(sizeof(uint32_t) * n1));
   FFN_HIP(h->m_offsets.ensure(sizeof(uint32_t) * n1));
@@ -946,7 +953,8 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   ffn::MarchArgs ma = march_args(h, rays, num_rays, bits, mp);
   FFN_HIP(set_march_blocks(h, ma, st));
   ma.counts = counts;
-  int64_t n = 0;
+  int64_t n = 0;                     // the samples (waiting) or the capacity
+  const uint32_t* n_dev = nullptr;   // with a capacity: the samples kept, on the device
   {
     StageTimer tm(h, 0, st);
     const uint64_t slot_n = (uint64_t)num_rays * mp->max_steps;
@@ -962,9 +970,16 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
       FFN_HIP(ffn::launch_march(ma, false, st));
     }
     FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, (uint32_t*)h->m_total.p, st));
-    FFN_HIP(hipMemcpyAsync(h->host_total, h->m_total.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    FFN_HIP(hipStreamSynchronize(st));
-    n = *h->host_total;
+    if (cap > 0) {
+      uint32_t* kept = (uint32_t*)h->m_total.p + 1;
+      FFN_HIP(ffn::launch_march_clamp(counts, off, num_rays, cap, kept, st));
+      n = cap;
+      n_dev = kept;
+    } else {
+      FFN_HIP(hipMemcpyAsync(h->host_total, h->m_total.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+      FFN_HIP(hipStreamSynchronize(st));
+      n = *h->host_total;
+    }
     FFN_HIP(h->m_samples.ensure(sizeof(float4) * (size_t)(n > 0 ? n : 1)));
     FFN_HIP(h->m_ids.ensure(sizeof(uint32_t) * (size_t)(n > 0 ? n : 1)));
     if (one_walk) {
@@ -1001,9 +1016,11 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
     StageTimer tm(h, 1, st);
     ffn::DenseLevels dl;
     FFN_HIP(build_dense_levels(h, P.table, &dl, st));
-    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, P.table, a0, feat, nullptr, &dl, st));
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, P.table, a0, feat, nullptr, &dl, st, n_dev));
   }
-  // 3-5. forward MLP, compositing with early termination and the loss, MLP backward
+  // 3-5. forward MLP, compositing with early termination and the loss, MLP backward.  (With a capacity the
+  // blocks are those of the capacity's tiles: a block's tiles and the order of the partials' sum are the same
+  // as for the kept count, the further blocks add zero partials.)
   const int64_t n_tiles = (n + 63) / 64;
   // the fp16 kernel walks groups of four tiles
   const int64_t n_work = mlp16 ? (n_tiles + 3) / 4 : n_tiles;
@@ -1020,10 +1037,10 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
     StageTimer tm(h, 2, st);
     if (mlp16)
       FFN_HIP(ffn::launch_mlp16_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, sc->sh_multiplier, sigma, rgb,
-                                    LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+                                    LF, h->cfg.nd, h->cfg.nc, n_blocks, st, n_dev));
     else
       FFN_HIP(ffn::launch_mlp_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, sc->sh_multiplier, sigma, rgb,
-                                  LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
+                                  LF, h->cfg.nd, h->cfg.nc, n_blocks, st, n_dev));
     ffn::CompMarchArgs ca{};
     ca.offsets = off;
     ca.counts = counts;
@@ -1070,6 +1087,7 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
     a.in_dLds = ca.dLds;
     a.in_dLdc = ca.dLdc;
     a.march_dt = mp->dt;
+    a.n_dev = n_dev;
     if (taps) a.t_relu = taps->relu;
     if (n > 0 && mlp16) FFN_HIP(ffn::launch_mlp16_marched(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
     else if (n > 0) FFN_HIP(ffn::launch_mlp_marched(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
@@ -1108,7 +1126,7 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
       ap.eps = sc->eps;
     }
     // with no samples nothing runs: the table and its moments stay as they are
-    FFN_HIP(ffn::launch_hash_bwd(h->dc, src, n, dLda0, feat, mode, sc->lr, ap, plan, bs, st));
+    FFN_HIP(ffn::launch_hash_bwd(h->dc, src, n, dLda0, feat, mode, sc->lr, ap, plan, bs, st, n_dev));
   }
   // 7. MLP Adam
   ffn::MlpOptArgs o{};
@@ -1148,12 +1166,15 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   if (!h->bound) return fail(-1, "bind params first");
   if (mp->chunk == 0 || mp->chunk > 1024) return fail(-1, "chunk=%u out of [1,1024]", mp->chunk);
   if (!(mp->T_stop >= 0.0f && mp->T_stop < 1.0f)) return fail(-1, "T_stop must be in [0,1)");
+  if (mp->flags & ~FFN_RENDER_NO_WAIT) return fail(-1, "unknown render flags 0x%x", mp->flags);
   if (num_rays == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   UseMark um{h, st};
+  const bool no_wait = (mp->flags & FFN_RENDER_NO_WAIT) != 0;
   const int LF = h->dc.LF;
   const size_t n1 = (size_t)num_rays + 1;
   const size_t cap = (size_t)num_rays * mp->chunk;
+  if (no_wait && cap >= ((size_t)1 << 32)) return fail(-1, "num_rays * chunk must stay below 2^32 samples");
   FFN_HIP(h->m_state.ensure(sizeof(ffn::MarchState) * num_rays));
   FFN_HIP(h->m_acc.ensure(sizeof(float4) * num_rays));
   FFN_HIP(h->m_counts.ensure(sizeof(uint32_t) * n1));
@@ -1176,7 +1197,9 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   float* a0 = (float*)h->m_a0.p;
   float* sigma = (float*)h->m_sigma.p;
   float* rgb = (float*)h->m_rgb.p;
-  FFN_HIP(ffn::launch_march_init(state, acc, n_samples, num_rays, st));
+  // without waits, the scan's total is each round's sample count on the device and the gate of the next round's
+  // launches (primed open here): a round after one without samples does nothing
+  FFN_HIP(ffn::launch_march_init(state, acc, n_samples, num_rays, st, no_wait ? total : nullptr));
   ffn::MarchArgs a = march_args(h, rays, num_rays, bits, mp);
   FFN_HIP(set_march_blocks(h, a, st));
   a.chunk = mp->chunk;
@@ -1196,6 +1219,7 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   // marched step) it walks twice, count then emit.  The samples, their order and the walk states agree.
   const bool one_walk = march_slots_fit(h->m_slots, cap * sizeof(float4));
   if (one_walk) FFN_HIP(h->m_slots.ensure(sizeof(float4) * cap));
+  if (no_wait) a.gate = total;
   ffn::MarchArgs a1 = a;
   a1.slot_stride = mp->chunk;
   a1.samples = (float4*)h->m_slots.p;
@@ -1204,29 +1228,34 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   const uint32_t rounds = (mp->max_steps + mp->chunk - 1) / mp->chunk;
   ffn::DenseLevels dl;  // the table does not change during the render: one copy serves every round
   FFN_HIP(build_dense_levels(h, h->params.table, &dl, st));
+  // (without waits: the round's count is *total, read on the device; n the capacity)
+  const uint32_t* n_dev = no_wait ? total : nullptr;
   for (uint32_t round = 0; round < rounds; ++round) {
     FFN_HIP(ffn::launch_march(one_walk ? a1 : a, one_walk, st));
-    FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, total, st));
-    FFN_HIP(hipMemcpyAsync(h->host_total, total, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    FFN_HIP(hipStreamSynchronize(st));
-    const int64_t n = *h->host_total;
-    if (n == 0) break;
+    FFN_HIP(ffn::launch_scan_u32(counts, num_rays, off, (uint32_t*)h->m_sums.p, total, st, no_wait));
+    int64_t n = (int64_t)cap;
+    if (!no_wait) {
+      FFN_HIP(hipMemcpyAsync(h->host_total, total, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+      FFN_HIP(hipStreamSynchronize(st));
+      n = *h->host_total;
+      if (n == 0) break;
+    }
     if (one_walk) {
       FFN_HIP(ffn::launch_march_compact(counts, off, (const float4*)h->m_slots.p, mp->chunk, num_rays, samples, ids,
-                                        st));
+                                        st, n_dev));
     } else {
       FFN_HIP(ffn::launch_march(a, true, st));
     }
     ffn::PosSrc src{(const float*)samples, nullptr, nullptr, 0};
     src.x_stride = 4;
     const ffn::FeatLayout feat = ffn::level_major(n, h->dc.F);
-    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, a0, feat, nullptr, &dl, st));
+    FFN_HIP(ffn::launch_hash_fwd(h->dc, src, n, h->params.table, a0, feat, nullptr, &dl, st, n_dev));
     int nb = (int)((n + 63) / 64);
     if (nb > n_blocks) nb = n_blocks;
     FFN_HIP(ffn::launch_mlp_fwd(h->dc, w, a0, feat, (const float4*)rays, ids, n, mp->sh_multiplier, sigma, rgb, LF,
-                                h->cfg.nd, h->cfg.nc, nb, st));
+                                h->cfg.nd, h->cfg.nc, nb, st, n_dev));
     FFN_HIP(ffn::launch_render_composite(off, counts, num_rays, sigma, rgb, mp->dt, mp->T_stop, state, acc,
-                                         n_samples, st));
+                                         n_samples, st, n_dev));
   }
   FFN_HIP(ffn::launch_render_finish(acc, num_rays, (float4*)out_rgb, st));
   return 0;

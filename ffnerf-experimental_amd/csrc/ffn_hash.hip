@@ -254,15 +254,11 @@ __device__ __forceinline__ void gather_level(const DevCfg& c, const float (&p)[3
   }
 }
 
-// Grid row y gathers level y + (n_multi - 1) for one sample per thread; with n_multi > 0, row 0 gathers the
-// n_multi coarsest levels (small dense copies, together a working set of a few MB) in one pass, so their
-// sample positions are read and computed once.
+// the grid row's level(s) of sample b
 template <int F, typename TT>
-__global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t n, const TT* __restrict__ table,
-                                                  float* __restrict__ a0, FeatLayout lay,
-                                                  uint32_t* __restrict__ idx_out, DenseLevels dl) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= n) return;
+__device__ __forceinline__ void gather_row(const DevCfg& c, const PosSrc& src, int64_t b, const TT* __restrict__ table,
+                                           float* __restrict__ a0, const FeatLayout& lay,
+                                           uint32_t* __restrict__ idx_out, const DenseLevels& dl) {
   float pos[3], p[3];
   sample_position(src, b, pos);
   normalize_pos(c, pos, p);
@@ -272,6 +268,26 @@ __global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t 
     for (int l = 0; l < dl.n_multi; ++l) gather_level<F, TT>(c, p, l, table, dl, b, a0, lay, idx_out);
   } else {
     gather_level<F, TT>(c, p, row + (dl.n_multi > 0 ? dl.n_multi - 1 : 0), table, dl, b, a0, lay, idx_out);
+  }
+}
+
+// Grid row y gathers level y + (n_multi - 1) for one sample per thread; with n_multi > 0, row 0 gathers the
+// n_multi coarsest levels (small dense copies, together a working set of a few MB) in one pass, so their
+// sample positions are read and computed once.  DEV: the count min(n, *n_dev) is read on the device and the
+// threads walk it with the grid's stride (a grid sized for a capacity n whose use is known only there).
+template <int F, typename TT, bool DEV>
+__global__ __launch_bounds__(256) void k_hash_fwd(DevCfg c, PosSrc src, int64_t n, const TT* __restrict__ table,
+                                                  float* __restrict__ a0, FeatLayout lay,
+                                                  uint32_t* __restrict__ idx_out, DenseLevels dl,
+                                                  const uint32_t* __restrict__ n_dev) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if constexpr (DEV) {
+    const int64_t nd = (int64_t)*n_dev, nn = nd < n ? nd : n;
+    for (int64_t bb = b; bb < nn; bb += (int64_t)gridDim.x * blockDim.x)
+      gather_row<F, TT>(c, src, bb, table, a0, lay, idx_out, dl);
+  } else {
+    if (b >= n) return;
+    gather_row<F, TT>(c, src, b, table, a0, lay, idx_out, dl);
   }
 }
 
@@ -505,11 +521,13 @@ __device__ __forceinline__ void copy_out_round(uint4* __restrict__ pbuf, const B
   }
 }
 
+// n_dev (may be NULL): the sample count is min(n, *n_dev); a block past it writes only its zero bound, and
+// the rounds past it are not read (k_bin_meta_transpose, k_bin_reduce bound them by the same count)
 template <int F, int MODE>
 __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, int64_t n, BinGroup grp,
                                                          const float* __restrict__ g, FeatLayout lay, float lr,
                                                          uint32_t* __restrict__ meta, float* __restrict__ cmax,
-                                                         uint4* __restrict__ pbuf) {
+                                                         uint4* __restrict__ pbuf, const uint32_t* __restrict__ n_dev) {
   typedef typename FVec<F>::T V;
   constexpr int NT = emit_nt(F);
   extern __shared__ uint32_t sm[];
@@ -525,6 +543,10 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
   const int tid = threadIdx.x, lane = tid & 63;
   for (int j = tid; j < nbl; j += NT) lcnt[j] = 0u;
   const uint32_t be_mask = (1u << grp.log2_be) - 1u;
+  if (n_dev) {
+    const int64_t nd = (int64_t)*n_dev;
+    n = nd < n ? nd : n;
+  }
   const int64_t b_begin = (int64_t)chunk * grp.chunk;
   const int64_t b_end = b_begin + grp.chunk < n ? b_begin + grp.chunk : n;
   const int kb = (nbl + 63) >> 6;  // counters per lane in the scan
@@ -637,11 +659,20 @@ __global__ __launch_bounds__(emit_nt(F)) void k_bin_emit(DevCfg c, PosSrc src, i
 // The run table as emit writes it, [level][round][bucket], turned bucket-major, [level][bucket][round],
 // so that each reduce block reads its bucket's runs as one contiguous row (a strided column read costs a
 // memory sector per round once the table outgrows the caches).  64x64 tiles through LDS.
+// the rounds with samples (rounds_used: fewer when the count is read on the device)
+__device__ __forceinline__ int rounds_used(int n_rounds, const uint32_t* n_dev, int nt) {
+  if (!n_dev) return n_rounds;
+  const int64_t r = ((int64_t)*n_dev + nt - 1) / nt;
+  return r < n_rounds ? (int)r : n_rounds;
+}
+
 __global__ __launch_bounds__(256) void k_bin_meta_transpose(const uint32_t* __restrict__ meta,
                                                             uint32_t* __restrict__ meta_t, int n_rounds,
-                                                            int stride) {
+                                                            int stride, const uint32_t* __restrict__ n_dev,
+                                                            int nt) {
   __shared__ uint32_t tile[64][65];
   const int r0 = blockIdx.x * 64, b0 = blockIdx.y * 64, li = blockIdx.z;
+  if (r0 >= rounds_used(n_rounds, n_dev, nt)) return;  // the same for the whole block
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const uint32_t* src = meta + (int64_t)li * n_rounds * stride;
   uint32_t* dst = meta_t + (int64_t)li * stride * n_rounds;
@@ -665,7 +696,8 @@ __global__ __launch_bounds__(256) void k_bin_meta_transpose(const uint32_t* __re
 template <int F, int MODE>
 __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ meta,
                                                      const uint4* __restrict__ pbuf,
-                                                     const float* __restrict__ cmax, BinApply ap) {
+                                                     const float* __restrict__ cmax, BinApply ap,
+                                                     const uint32_t* __restrict__ n_dev) {
   extern __shared__ unsigned long long acc[];
   __shared__ float wmax[16];
   __shared__ uint32_t wtot[16];
@@ -682,14 +714,16 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   const uint32_t level_T = c.mask[l] + 1u;
   const int count = (int)((level_T - entry_lo) < (uint32_t)be ? (level_T - entry_lo) : (uint32_t)be);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < count * F; e += 1024) acc[e] = 0ull;
   const int nr = grp.n_rounds;
+  const int nr_use = rounds_used(nr, n_dev, emit_nt(F));  // rounds with samples
+  if (nr_use == 0) return;  // no samples: nothing is applied (the same for the whole block)
+  for (int e = tid; e < count * F; e += 1024) acc[e] = 0ull;
   const uint32_t* mrow = meta + ((int64_t)li * grp.meta_stride + jb) * nr;  // bucket-major: round rr at mrow[rr]
   // bound on every |value| of the level (the largest of its chunks' bounds) and the bucket's pair count
   float mxl = 0.0f;
   for (int ch = tid; ch < grp.nblk; ch += 1024) mxl = fmaxf(mxl, cmax[(int64_t)li * grp.nblk + ch]);
   uint32_t cnt = 0;
-  for (int rr = tid; rr < nr; rr += 1024) cnt += mrow[rr] & 0xFFFFu;
+  for (int rr = tid; rr < nr_use; rr += 1024) cnt += mrow[rr] & 0xFFFFu;
   mxl = wave_max_nonneg(mxl);
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d);
@@ -720,10 +754,10 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   if (mx > 0.0f) {
     const int64_t bpr = grp.np / PAD_RUN;  // pair blocks per round
     const int64_t blk_lvl = (int64_t)li * nr * bpr;
-    for (int r0 = wave * SEG; r0 < nr; r0 += 16 * SEG) {
+    for (int r0 = wave * SEG; r0 < nr_use; r0 += 16 * SEG) {
       // lanes 0..SEG-1 hold rounds r0 + lane: run offset and block count, then the blocks' running ends
       uint32_t m = 0;
-      if (lane < SEG && r0 + lane < nr) m = mrow[r0 + lane];
+      if (lane < SEG && r0 + lane < nr_use) m = mrow[r0 + lane];
       uint32_t incl = lane < SEG ? (m & 0xFFFFu) / PAD_RUN : 0u;
 #pragma unroll
       for (int d = 1; d < SEG; d <<= 1) {
@@ -800,9 +834,11 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
 // exclusive scan of n uint32 (n + 1 outputs: the last one is the total)
 
 // in has n_in elements; out gets n elements (n >= n_in; the missing inputs count as 0)
+// gate (may be NULL): each of the scan's kernels does nothing when *gate == 0 on entry
 __global__ __launch_bounds__(1024) void k_scan_tiles(const uint32_t* __restrict__ in, int64_t n_in,
                                                      uint32_t* __restrict__ out, int64_t n,
-                                                     uint32_t* __restrict__ tile_sums) {
+                                                     uint32_t* __restrict__ tile_sums, const uint32_t* gate) {
+  if (gate && *gate == 0u) return;
   __shared__ uint32_t wsum[16];
   const int64_t base = (int64_t)blockIdx.x * 4096;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -833,7 +869,8 @@ __global__ __launch_bounds__(1024) void k_scan_tiles(const uint32_t* __restrict_
 }
 
 __global__ __launch_bounds__(1024) void k_scan_sums(uint32_t* __restrict__ sums, int64_t n_tiles,
-                                                    uint32_t* __restrict__ total_out) {
+                                                    uint32_t* total_out, const uint32_t* gate) {
+  if (gate && *gate == 0u) return;
   __shared__ uint32_t wsum[16];
   __shared__ uint32_t carry;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -861,7 +898,8 @@ __global__ __launch_bounds__(1024) void k_scan_sums(uint32_t* __restrict__ sums,
 }
 
 __global__ __launch_bounds__(1024) void k_scan_add(uint32_t* __restrict__ out, int64_t n,
-                                                   const uint32_t* __restrict__ tile_pre) {
+                                                   const uint32_t* __restrict__ tile_pre, const uint32_t* gate) {
+  if (gate && *gate == 0u) return;  // a zero total: every input and every tile prefix is zero
   const int64_t base = (int64_t)blockIdx.x * 4096;
   const uint32_t add = tile_pre[blockIdx.x];
 #pragma unroll
@@ -876,31 +914,46 @@ __global__ __launch_bounds__(1024) void k_scan_add(uint32_t* __restrict__ out, i
 
 // exclusive scan of in[0..n) into out[0..n]; out[n] and *total get the sum; sums has (n + 4096) / 4096 slots
 hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, uint32_t* total,
-                           hipStream_t st) {
+                           hipStream_t st, bool gated) {
   const int64_t tiles = (n + 1 + 4095) / 4096;
-  hipLaunchKernelGGL(k_scan_tiles, dim3((unsigned)tiles), dim3(1024), 0, st, in, n, out, n + 1, sums);
-  hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, st, sums, tiles, total);
-  hipLaunchKernelGGL(k_scan_add, dim3((unsigned)tiles), dim3(1024), 0, st, out, n + 1, sums);
+  const uint32_t* gate = gated ? total : nullptr;
+  hipLaunchKernelGGL(k_scan_tiles, dim3((unsigned)tiles), dim3(1024), 0, st, in, n, out, n + 1, sums, gate);
+  hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, st, sums, tiles, total, gate);
+  hipLaunchKernelGGL(k_scan_add, dim3((unsigned)tiles), dim3(1024), 0, st, out, n + 1, sums, gate);
+  return hipGetLastError();
+}
+
+template <typename TT, bool DEV>
+static hipError_t launch_hash_fwd_d(const DevCfg& c, const PosSrc& src, int64_t n, const TT* table, float* a0,
+                                    const FeatLayout& lay, uint32_t* idx_out, const DenseLevels& dl,
+                                    const uint32_t* n_dev, hipStream_t st) {
+  const int rows = dl.n_multi > 0 ? c.L - dl.n_multi + 1 : c.L;
+  int64_t bx = (n + 255) / 256;
+  if (DEV && bx > HASH_FWD_DEV_BLOCKS) bx = HASH_FWD_DEV_BLOCKS;
+  const dim3 grid((unsigned)bx, (unsigned)rows), block(256);
+#define FFN_FWD(FV) \
+  hipLaunchKernelGGL((k_hash_fwd<FV, TT, DEV>), grid, block, 0, st, c, src, n, table, a0, lay, idx_out, dl, n_dev)
+  switch (c.F) {
+    case 1: FFN_FWD(1); break;
+    case 2: FFN_FWD(2); break;
+    case 4: FFN_FWD(4); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef FFN_FWD
   return hipGetLastError();
 }
 
 template <typename TT>
 static hipError_t launch_hash_fwd_t(const DevCfg& c, const PosSrc& src, int64_t n, const TT* table, float* a0,
                                     const FeatLayout& lay, uint32_t* idx_out, const DenseLevels& dl,
-                                    hipStream_t st) {
-  const int rows = dl.n_multi > 0 ? c.L - dl.n_multi + 1 : c.L;
-  const dim3 grid((unsigned)((n + 255) / 256), (unsigned)rows), block(256);
-  switch (c.F) {
-    case 1: hipLaunchKernelGGL((k_hash_fwd<1, TT>), grid, block, 0, st, c, src, n, table, a0, lay, idx_out, dl); break;
-    case 2: hipLaunchKernelGGL((k_hash_fwd<2, TT>), grid, block, 0, st, c, src, n, table, a0, lay, idx_out, dl); break;
-    case 4: hipLaunchKernelGGL((k_hash_fwd<4, TT>), grid, block, 0, st, c, src, n, table, a0, lay, idx_out, dl); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+                                    hipStream_t st, const uint32_t* n_dev) {
+  if (n_dev) return launch_hash_fwd_d<TT, true>(c, src, n, table, a0, lay, idx_out, dl, n_dev, st);
+  return launch_hash_fwd_d<TT, false>(c, src, n, table, a0, lay, idx_out, dl, nullptr, st);
 }
 
 hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const void* table, float* a0,
-                           const FeatLayout& lay, uint32_t* idx_out, const DenseLevels* dl, hipStream_t st) {
+                           const FeatLayout& lay, uint32_t* idx_out, const DenseLevels* dl, hipStream_t st,
+                           const uint32_t* n_dev) {
   if (n <= 0) return hipSuccess;
   DenseLevels none{};
   none.grid = nullptr;
@@ -909,8 +962,8 @@ hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
   for (int l = 0; l < FFN_MAX_LEVELS; ++l) none.off[l] = DENSE_NONE;
   const DenseLevels& d = (dl && dl->grid) ? *dl : none;
   if (c.table_f16)
-    return launch_hash_fwd_t(c, src, n, static_cast<const _Float16*>(table), a0, lay, idx_out, d, st);
-  return launch_hash_fwd_t(c, src, n, static_cast<const float*>(table), a0, lay, idx_out, d, st);
+    return launch_hash_fwd_t(c, src, n, static_cast<const _Float16*>(table), a0, lay, idx_out, d, st, n_dev);
+  return launch_hash_fwd_t(c, src, n, static_cast<const float*>(table), a0, lay, idx_out, d, st, n_dev);
 }
 
 template <typename TT>
@@ -998,7 +1051,7 @@ bool scatter_supported(const DevCfg& c) {
 
 hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* g, const FeatLayout& lay,
                            int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
-                           hipStream_t st) {
+                           hipStream_t st, const uint32_t* n_dev) {
   if (n <= 0) return hipSuccess;
   // run offsets and lengths are 16-bit, and a round's stage must fit in LDS
   const size_t lds_emit = emit_lds_bytes(plan.max_nbl, c.F);
@@ -1029,11 +1082,11 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
 #define FFN_BIN(FV, MV)                                                                                            \
   do {                                                                                                             \
     hipLaunchKernelGGL((k_bin_emit<FV, MV>), grid_bl, dim3(emit_nt(FV)), lds_emit, st, c, src, n, grp, g, lay,   \
-                       lr, s.meta, s.cmax, s.pairs);                                                               \
+                       lr, s.meta, s.cmax, s.pairs, n_dev);                                                        \
     hipLaunchKernelGGL(k_bin_meta_transpose, grid_tr, dim3(256), 0, st, s.meta, s.meta_t, grp.n_rounds,            \
-                       grp.meta_stride);                                                                           \
+                       grp.meta_stride, n_dev, emit_nt(FV));                                                       \
     hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,         \
-                       s.meta_t, s.pairs, s.cmax, ap);                                                             \
+                       s.meta_t, s.pairs, s.cmax, ap, n_dev);                                                      \
   } while (0)
 #define FFN_BIN_F(MV)                     \
   switch (c.F) {                          \

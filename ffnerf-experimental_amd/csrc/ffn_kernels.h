@@ -111,6 +111,9 @@ struct MlpArgs {
   const float* in_dLds;
   const float* in_dLdc;
   float march_dt;
+  // when set, the sample count is min(*n_dev, num_rays << log2S) read on the device (num_rays << log2S the
+  // capacity the buffers hold) and the kernel walks its tiles; n_tiles is then the capacity's
+  const uint32_t* n_dev;
 };
 
 // bucketed backward scatter
@@ -169,14 +172,19 @@ struct DenseLevels {
 };
 // fill the dense copies from the table (every level with off[l] != DENSE_NONE)
 hipError_t launch_hash_densify(const DevCfg& c, const void* table, const DenseLevels& dl, hipStream_t st);
-// dl (may be NULL): levels with a dense copy gather from it, with the same values and arithmetic
+// dl (may be NULL): levels with a dense copy gather from it, with the same values and arithmetic.
+// n_dev (may be NULL): the sample count is min(n, *n_dev), read on the device (n the capacity); the grid is
+// then sized for at most HASH_FWD_DEV_BLOCKS blocks per level, each walking its samples with a grid stride
+constexpr int64_t HASH_FWD_DEV_BLOCKS = 4096;
 hipError_t launch_hash_fwd(const DevCfg& c, const PosSrc& src, int64_t n, const void* table, float* a0,
-                           const FeatLayout& lay, uint32_t* idx_out, const DenseLevels* dl, hipStream_t st);
+                           const FeatLayout& lay, uint32_t* idx_out, const DenseLevels* dl, hipStream_t st,
+                           const uint32_t* n_dev = nullptr);
 // BIN_GRAD: dst += scatter(g); BIN_SGD: table += scatter(-lr 2^(-0.1 l) 0.5 g) (reference SGD);
-// BIN_ADAM: Adam on the table with the scattered gradient
+// BIN_ADAM: Adam on the table with the scattered gradient.  n_dev (may be NULL): the sample count is
+// min(n, *n_dev), read on the device (the plan made for n, the capacity)
 hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const float* g, const FeatLayout& lay,
                            int mode, float lr, const BinApply& ap, const BinPlan& plan, const BinScratch& s,
-                           hipStream_t st);
+                           hipStream_t st, const uint32_t* n_dev = nullptr);
 hipError_t launch_feat_relayout(const float* src, const FeatLayout& ls, float* dst, const FeatLayout& ld, int64_t n,
                                 int L, int F, hipStream_t st);
 
@@ -214,6 +222,9 @@ struct MarchArgs {
                              // written as the count pass does); 0: at offsets[r]
   const uint32_t* blocks;     // summary of `bits` per 8^3 block (launch_occ_blocks), or NULL: no block skipping
   const uint32_t* blocks_use;  // with it: the walk skips blocks when *blocks_use != 0
+  // (may be NULL) the launch does nothing when *gate == 0: a render round after one without samples (every ray
+  // has stopped, every count is already 0)
+  const uint32_t* gate;
 };
 
 hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint32_t* bits, hipStream_t st);
@@ -222,16 +233,27 @@ hipError_t launch_occ_bitfield(const uint32_t* occ, int G, uint32_t q_min, uint3
 hipError_t launch_occ_blocks(const uint32_t* bits, int R, uint32_t* blocks, uint32_t* use, hipStream_t st);
 hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st);
 // per-ray slots (ray r's counts[r] samples at slots + r * stride) -> the compacted order (offsets), with ray ids
+// (gate: as MarchArgs::gate)
 hipError_t launch_march_compact(const uint32_t* counts, const uint32_t* offsets, const float4* slots,
                                 uint32_t stride, uint32_t num_rays, float4* samples, uint32_t* ray_ids,
-                                hipStream_t st);
-hipError_t launch_march_init(MarchState* state, float4* acc, uint32_t* n_used, uint32_t num_rays, hipStream_t st);
+                                hipStream_t st, const uint32_t* gate = nullptr);
+// sample budget of a step: the rays whose samples all lie below slot cap of the scanned order keep their
+// counts, the others (a suffix of the rays) get count 0; *n_eff = the samples kept.  offsets [num_rays + 1]
+// from launch_scan_u32 (offsets[num_rays] = the total)
+hipError_t launch_march_clamp(uint32_t* counts, const uint32_t* offsets, uint32_t num_rays, uint32_t cap,
+                              uint32_t* n_eff, hipStream_t st);
+// (prime, may be NULL: set to 1, the open gate of a render's first round)
+hipError_t launch_march_init(MarchState* state, float4* acc, uint32_t* n_used, uint32_t num_rays, hipStream_t st,
+                             uint32_t* prime = nullptr);
 hipError_t launch_render_composite(const uint32_t* offsets, const uint32_t* counts, uint32_t num_rays,
                                    const float* sigma, const float* rgb, float dt, float T_stop, MarchState* state,
-                                   float4* acc, uint32_t* n_used, hipStream_t st);
+                                   float4* acc, uint32_t* n_used, hipStream_t st, const uint32_t* gate = nullptr);
 hipError_t launch_render_finish(const float4* acc, uint32_t num_rays, float4* out_rgb, hipStream_t st);
+// exclusive scan of in[0..n) into out[0..n]; out[n] and *total get the sum.  gated: the kernels do nothing
+// while *total == 0 on entry (a render round after one without samples: in is all zero and out already holds
+// its scan)
 hipError_t launch_scan_u32(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, uint32_t* total,
-                           hipStream_t st);
+                           hipStream_t st, bool gated = false);
 
 // compositing of a marched training batch (one lane per ray, front to back, stopping after the sample that
 // leaves T < T_stop), the photometric loss gradient and the compositing backward of every sample
@@ -273,9 +295,11 @@ hipError_t launch_make_batch_weighted(const float* images, uint32_t n_images, ui
 
 // forward-only MLP over n samples: encodings a0 (layout feat), view directions from rays[ray_ids[b]];
 // sigma[n], rgb[n][3]
+// (n_dev may be NULL: the count is then n; else min(n, *n_dev), read on the device)
 hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
                           const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
-                          float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+                          float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st,
+                          const uint32_t* n_dev = nullptr);
 
 // fused MLP forward + compositing + loss + backward + proposals, per 64-sample tile
 bool mlp_supported(int LF, int nd, int nc);
@@ -295,7 +319,8 @@ hipError_t launch_mlp16(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, 
 // the fp16 path of the marched training step: forward only over indexed samples, and the backward
 hipError_t launch_mlp16_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
                             const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
-                            float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st);
+                            float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st,
+                            const uint32_t* n_dev = nullptr);
 hipError_t launch_mlp16_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
 
 // sum the per-block gradient partials and apply Adam to the MLP parameters

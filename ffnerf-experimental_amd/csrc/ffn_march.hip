@@ -350,6 +350,7 @@ struct RayWalk {
 
 template <bool EMIT>
 __global__ __launch_bounds__(256) void k_march(MarchArgs a) {
+  if (a.gate && *a.gate == 0u) return;  // the whole launch: every ray has stopped
   const int lane = threadIdx.x & 63;
   const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const uint64_t r_begin = wave * MARCH_RPW;
@@ -398,7 +399,9 @@ __global__ __launch_bounds__(256) void k_march_compact(const uint32_t* __restric
                                                        const uint32_t* __restrict__ offsets,
                                                        const float4* __restrict__ slots, uint32_t stride,
                                                        uint32_t num_rays, float4* __restrict__ samples,
-                                                       uint32_t* __restrict__ ray_ids) {
+                                                       uint32_t* __restrict__ ray_ids,
+                                                       const uint32_t* __restrict__ gate) {
+  if (gate && *gate == 0u) return;
   const int lane = threadIdx.x & 63;
   const uint32_t n_waves = gridDim.x * (blockDim.x >> 6);
   for (uint32_t r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < num_rays; r += n_waves) {
@@ -411,9 +414,25 @@ __global__ __launch_bounds__(256) void k_march_compact(const uint32_t* __restric
   }
 }
 
-__global__ __launch_bounds__(256) void k_march_init(MarchState* __restrict__ state, float4* __restrict__ acc,
-                                                    uint32_t* __restrict__ n_used, uint32_t num_rays) {
+// sample budget of a marched step (launch_march_clamp): offsets [num_rays + 1], offsets[r + 1] the end of ray r
+__global__ __launch_bounds__(256) void k_march_clamp(uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets,
+                                                     uint32_t num_rays, uint32_t cap, uint32_t* __restrict__ n_eff) {
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= num_rays) return;
+  const uint32_t end = offsets[r + 1];
+  const bool fits = end <= cap;
+  if (!fits) counts[r] = 0u;
+  // the rays that fit are a prefix (offsets never decrease): its last ray writes the samples kept
+  const bool next_fits = r + 1 < num_rays && offsets[r + 2] <= cap;
+  if (fits && !next_fits) *n_eff = end;
+  if (r == 0 && !fits) *n_eff = 0u;
+}
+
+__global__ __launch_bounds__(256) void k_march_init(MarchState* __restrict__ state, float4* __restrict__ acc,
+                                                    uint32_t* __restrict__ n_used, uint32_t num_rays,
+                                                    uint32_t* __restrict__ prime) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (prime && r == 0) *prime = 1u;
   if (r >= num_rays) return;
   state[r] = MarchState{0u, 0u, 0u, MARCH_FRESH};
   acc[r] = make_float4(0.0f, 0.0f, 0.0f, 1.0f);
@@ -427,7 +446,9 @@ __global__ __launch_bounds__(256) void k_render_composite(const uint32_t* __rest
                                                           const float* __restrict__ sigma,
                                                           const float* __restrict__ rgb, float dt, float T_stop,
                                                           MarchState* __restrict__ state, float4* __restrict__ acc,
-                                                          uint32_t* __restrict__ n_used) {
+                                                          uint32_t* __restrict__ n_used,
+                                                          const uint32_t* __restrict__ gate) {
+  if (gate && *gate == 0u) return;
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= num_rays) return;
   const uint32_t cnt = counts[r];
@@ -613,26 +634,36 @@ hipError_t launch_march(const MarchArgs& a, bool emit, hipStream_t st) {
 
 hipError_t launch_march_compact(const uint32_t* counts, const uint32_t* offsets, const float4* slots,
                                 uint32_t stride, uint32_t num_rays, float4* samples, uint32_t* ray_ids,
-                                hipStream_t st) {
+                                hipStream_t st, const uint32_t* gate) {
   if (num_rays == 0) return hipSuccess;
   const uint32_t blocks = (num_rays + 3) / 4 < 4096 ? (num_rays + 3) / 4 : 4096;
   hipLaunchKernelGGL(k_march_compact, dim3(blocks), dim3(256), 0, st, counts, offsets, slots, stride, num_rays,
-                     samples, ray_ids);
+                     samples, ray_ids, gate);
   return hipGetLastError();
 }
 
-hipError_t launch_march_init(MarchState* state, float4* acc, uint32_t* n_used, uint32_t num_rays, hipStream_t st) {
+hipError_t launch_march_clamp(uint32_t* counts, const uint32_t* offsets, uint32_t num_rays, uint32_t cap,
+                              uint32_t* n_eff, hipStream_t st) {
   if (num_rays == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_march_init, dim3((num_rays + 255) / 256), dim3(256), 0, st, state, acc, n_used, num_rays);
+  hipLaunchKernelGGL(k_march_clamp, dim3((num_rays + 255) / 256), dim3(256), 0, st, counts, offsets, num_rays, cap,
+                     n_eff);
+  return hipGetLastError();
+}
+
+hipError_t launch_march_init(MarchState* state, float4* acc, uint32_t* n_used, uint32_t num_rays, hipStream_t st,
+                             uint32_t* prime) {
+  if (num_rays == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_march_init, dim3((num_rays + 255) / 256), dim3(256), 0, st, state, acc, n_used, num_rays,
+                     prime);
   return hipGetLastError();
 }
 
 hipError_t launch_render_composite(const uint32_t* offsets, const uint32_t* counts, uint32_t num_rays,
                                    const float* sigma, const float* rgb, float dt, float T_stop, MarchState* state,
-                                   float4* acc, uint32_t* n_used, hipStream_t st) {
+                                   float4* acc, uint32_t* n_used, hipStream_t st, const uint32_t* gate) {
   if (num_rays == 0) return hipSuccess;
   hipLaunchKernelGGL(k_render_composite, dim3((num_rays + 255) / 256), dim3(256), 0, st, offsets, counts, num_rays,
-                     sigma, rgb, dt, T_stop, state, acc, n_used);
+                     sigma, rgb, dt, T_stop, state, acc, n_used, gate);
   return hipGetLastError();
 }
 

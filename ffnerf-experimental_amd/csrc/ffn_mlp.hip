@@ -357,7 +357,13 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   const bool train = a.do_train != 0;
   const DevCfg& c = a.c;
   const int log2S = a.log2S;
-  const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
+  uint64_t n_samples = (uint64_t)a.num_rays << log2S;
+  int64_t n_tiles = a.n_tiles;
+  if (a.n_dev) {  // the count of a launch sized for a capacity, read on the device
+    const uint64_t nd = *a.n_dev;
+    n_samples = nd < n_samples ? nd : n_samples;
+    n_tiles = (int64_t)((n_samples + 63) / 64);
+  }
 
   stage_weights<LF, ND, NC>(sW, a.w, tid, 256);
   __syncthreads();
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   gd_in.zero();
 
   int parity = 0;
-  for (int64_t ti = blockIdx.x; ti < a.n_tiles; ti += gridDim.x, parity ^= 1) {
+  for (int64_t ti = blockIdx.x; ti < n_tiles; ti += gridDim.x, parity ^= 1) {
     const int64_t tile = a.tile_order ? (int64_t)a.tile_order[ti] : ti;
     float* sSig = sC + (train ? 0 : parity * 256);
     float* sRgb = sSig + 64;
@@ -598,8 +604,13 @@ template <int LF, int ND, int NC, int FEAT>
 __global__ __launch_bounds__(256) void k_mlp_fwd(MlpPtrs wp, const float* __restrict__ a0, FeatLayout feat,
                                                  const float4* __restrict__ rays, const uint32_t* __restrict__ ray_ids,
                                                  int64_t n, float sh_mult, float* __restrict__ sigma,
-                                                 float* __restrict__ rgb) {
+                                                 float* __restrict__ rgb, const uint32_t* __restrict__ n_dev) {
   extern __shared__ float smem[];
+  if (n_dev) {  // the count of a launch sized for a capacity, read on the device
+    const int64_t nd = (int64_t)*n_dev;
+    n = nd < n ? nd : n;
+  }
+  if ((int64_t)blockIdx.x * 64 >= n) return;  // no samples for this block: skip staging the weights
   float* sW = smem;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
   stage_weights<LF, ND, NC>(sW, wp, tid, 256);
@@ -633,7 +644,7 @@ __global__ __launch_bounds__(256) void k_mlp_fwd(MlpPtrs wp, const float* __rest
 template <int LF, int ND, int NC, int FEAT>
 static hipError_t launch_fwd_f(const MlpPtrs& w, const float* a0, const FeatLayout& feat, const float4* rays,
                                const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma, float* rgb,
-                               int n_blocks, hipStream_t st) {
+                               int n_blocks, hipStream_t st, const uint32_t* n_dev) {
   using A = Arch<LF, ND, NC>;
   const size_t lds = sizeof(float) * (size_t)A::w_total();
   static bool attr_set = false;
@@ -644,18 +655,18 @@ static hipError_t launch_fwd_f(const MlpPtrs& w, const float* a0, const FeatLayo
     attr_set = true;
   }
   hipLaunchKernelGGL((k_mlp_fwd<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, w, a0, feat, rays, ray_ids, n,
-                     sh_mult, sigma, rgb);
+                     sh_mult, sigma, rgb, n_dev);
   return hipGetLastError();
 }
 
 template <int LF, int ND, int NC>
 static hipError_t launch_fwd_t(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
                                const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
-                               float* rgb, int n_blocks, hipStream_t st) {
+                               float* rgb, int n_blocks, hipStream_t st, const uint32_t* n_dev) {
   switch (c.F) {
-    case 1: return launch_fwd_f<LF, ND, NC, 1>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
-    case 2: return launch_fwd_f<LF, ND, NC, 2>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
-    case 4: return launch_fwd_f<LF, ND, NC, 4>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
+    case 1: return launch_fwd_f<LF, ND, NC, 1>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st, n_dev);
+    case 2: return launch_fwd_f<LF, ND, NC, 2>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st, n_dev);
+    case 4: return launch_fwd_f<LF, ND, NC, 4>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st, n_dev);
     default: return hipErrorInvalidValue;
   }
 }
@@ -686,11 +697,11 @@ int mlp_blocks_per_cu(int LF, int nd, int nc) {
 
 hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
                           const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
-                          float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+                          float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st, const uint32_t* n_dev) {
   if (n <= 0) return hipSuccess;
 #define X(l, d, nn)                   \
   if (LF == l && nd == d && nc == nn) \
-    return launch_fwd_t<l, d, nn>(c, w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st);
+    return launch_fwd_t<l, d, nn>(c, w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st, n_dev);
   FFN_MLP_CONFIGS(X)
 #undef X
   return hipErrorInvalidValue;

@@ -589,7 +589,13 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   const bool train = a.do_train != 0;
   const DevCfg& c = a.c;
   const int log2S = a.log2S;
-  const uint64_t n_samples = (uint64_t)a.num_rays << log2S;
+  uint64_t n_samples = (uint64_t)a.num_rays << log2S;
+  int64_t n_tiles = a.n_tiles;
+  if (a.n_dev) {  // the count of a launch sized for a capacity, read on the device
+    const uint64_t nd = *a.n_dev;
+    n_samples = nd < n_samples ? nd : n_samples;
+    n_tiles = (int64_t)((n_samples + 63) / 64);
+  }
 
   // weights: fp16 [out_pad][in] and [in][out_pad] (K-ordered columns where K blocks are 32 wide, zero
   // padding), fp32 biases
@@ -632,7 +638,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   for (int i = 0; i < (ND > 1 ? ND - 1 : 1); ++i) gd_h[i].zero();
   gd_in.zero();
 
-  const int64_t n_groups = (a.n_tiles + 3) / 4;
+  const int64_t n_groups = (n_tiles + 3) / 4;
   for (int64_t grp = blockIdx.x; grp < n_groups; grp += gridDim.x) {
     const int64_t tile0 = grp * 4;
     TileIn<LF> cur;
@@ -732,7 +738,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     // (the inputs load at the start of each tile: loaded a tile ahead, they stayed live through the backward
     // and cost more in spills than the latency they hid)
     // marched tiles are all busy up to the last one
-    const int tiles_here = MARCHED ? (int)(a.n_tiles - tile0 < 4 ? a.n_tiles - tile0 : 4) : 4;
+    const int tiles_here = MARCHED ? (int)(n_tiles - tile0 < 4 ? n_tiles - tile0 : 4) : 4;
     tt = MARCHED ? 0 : next_busy(sFlag, 0);
 #pragma unroll 1
     while (tt < tiles_here) {
@@ -929,8 +935,14 @@ template <int LF, int ND, int NC, int FEAT>
 __global__ __launch_bounds__(256) void k_mlp16_fwd(MlpPtrs wp, const float* __restrict__ a0, FeatLayout feat,
                                                    const float4* __restrict__ rays,
                                                    const uint32_t* __restrict__ ray_ids, int64_t n, float sh_mult,
-                                                   float* __restrict__ sigma, float* __restrict__ rgb) {
+                                                   float* __restrict__ sigma, float* __restrict__ rgb,
+                                                   const uint32_t* __restrict__ n_dev) {
   using A = Arch16<LF, ND, NC>;
+  if (n_dev) {  // the count of a launch sized for a capacity, read on the device
+    const int64_t nd = (int64_t)*n_dev;
+    n = nd < n ? nd : n;
+  }
+  if ((int64_t)blockIdx.x * 64 >= n) return;  // no samples for this block: skip staging the weights
   extern __shared__ __align__(16) unsigned char smem16f[];
   _Float16* sWf = reinterpret_cast<_Float16*>(smem16f);
   float* sB = reinterpret_cast<float*>(smem16f + (size_t)A::wf_off(FFN_N_LAYERS) * 2);
@@ -977,7 +989,7 @@ __global__ __launch_bounds__(256) void k_mlp16_fwd(MlpPtrs wp, const float* __re
 template <int LF, int ND, int NC, int FEAT>
 static hipError_t launch16_fwd_f(const MlpPtrs& w, const float* a0, const FeatLayout& feat, const float4* rays,
                                  const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma, float* rgb,
-                                 int n_blocks, hipStream_t st) {
+                                 int n_blocks, hipStream_t st, const uint32_t* n_dev) {
   using A = Arch16<LF, ND, NC>;
   const size_t lds = (size_t)A::wf_off(FFN_N_LAYERS) * 2 + (size_t)A::b_floats() * 4;
   static bool attr_set = false;
@@ -988,7 +1000,7 @@ static hipError_t launch16_fwd_f(const MlpPtrs& w, const float* a0, const FeatLa
     attr_set = true;
   }
   hipLaunchKernelGGL((k_mlp16_fwd<LF, ND, NC, FEAT>), dim3(n_blocks), dim3(256), lds, st, w, a0, feat, rays,
-                     ray_ids, n, sh_mult, sigma, rgb);
+                     ray_ids, n, sh_mult, sigma, rgb, n_dev);
   return hipGetLastError();
 }
 
@@ -1035,14 +1047,14 @@ hipError_t launch_mlp16_marched(const MlpArgs& a, int LF, int nd, int nc, int n_
 
 hipError_t launch_mlp16_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, const FeatLayout& feat,
                             const float4* rays, const uint32_t* ray_ids, int64_t n, float sh_mult, float* sigma,
-                            float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st) {
+                            float* rgb, int LF, int nd, int nc, int n_blocks, hipStream_t st, const uint32_t* n_dev) {
   if (n <= 0) return hipSuccess;
 #define X(l, d, nn)                                                                                             \
   if (LF == l && nd == d && nc == nn) {                                                                         \
     switch (c.F) {                                                                                              \
-      case 1: return launch16_fwd_f<l, d, nn, 1>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st); \
-      case 2: return launch16_fwd_f<l, d, nn, 2>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st); \
-      case 4: return launch16_fwd_f<l, d, nn, 4>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st); \
+      case 1: return launch16_fwd_f<l, d, nn, 1>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st, n_dev); \
+      case 2: return launch16_fwd_f<l, d, nn, 2>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st, n_dev); \
+      case 4: return launch16_fwd_f<l, d, nn, 4>(w, a0, feat, rays, ray_ids, n, sh_mult, sigma, rgb, n_blocks, st, n_dev); \
       default: return hipErrorInvalidValue;                                                                     \
     }                                                                                                           \
   }

@@ -28,7 +28,7 @@ EXPORTS = [
     "ffn_set_profiling", "ffn_stage_times", "ffn_occ_bitfield", "ffn_march", "ffn_render", "ffn_make_batch",
     "ffn_march_noalloc", "ffn_train_step_marched", "ffn_make_batch_weighted",
 ]
-ABI_VERSION = 2  # FFN_ABI_VERSION of the header these structures and signatures follow
+ABI_VERSION = 3  # FFN_ABI_VERSION of the header these structures and signatures follow
 MARCH_NOALLOC_MAX_RAYS = 1 << 20
 RELU_WORDS = 14  # ReLU-branch tap words per sample
 STAGES = ["sample", "hash_fwd", "mlp", "hash_bwd", "mlp_adam", "table_adam"]
@@ -80,14 +80,20 @@ class FfnTaps(C.Structure):
 class FfnMarchParams(C.Structure):
     _fields_ = [
         ("res", C.c_int32), ("dt", C.c_float), ("max_steps", C.c_uint32), ("T_stop", C.c_float),
-        ("chunk", C.c_uint32), ("sh_multiplier", C.c_float), ("reserved", C.c_int32 * 2),
+        ("chunk", C.c_uint32), ("sh_multiplier", C.c_float), ("sample_capacity", C.c_uint32),
+        ("flags", C.c_uint32),
     ]
 
 
-def march_params(res, dt, max_steps, T_stop=1e-4, chunk=32, sh_multiplier=1.0) -> FfnMarchParams:
+RENDER_NO_WAIT = 1  # FFN_RENDER_NO_WAIT
+
+
+def march_params(res, dt, max_steps, T_stop=1e-4, chunk=32, sh_multiplier=1.0, sample_capacity=0,
+                 flags=0) -> FfnMarchParams:
     m = FfnMarchParams()
     m.res, m.dt, m.max_steps, m.T_stop, m.chunk, m.sh_multiplier = int(res), float(dt), int(max_steps), \
         float(T_stop), int(chunk), float(sh_multiplier)
+    m.sample_capacity, m.flags = int(sample_capacity), int(flags)
     return m
 
 

@@ -526,12 +526,15 @@ class Nerf:
 
     def step_marched(self, io: RayBatch, lr_f: float, bits, res: int, dt: float, max_steps: int = 1024,
                      T_stop: float = 1e-4, sh_multiplier: float = 1.0, color_MLP_rel_lr: float = 1.0,
-                     rng_u32: np.uint32 | None = None, n_samples=None, taps: fl.FfnTaps | None = None, stream=None):
+                     rng_u32: np.uint32 | None = None, n_samples=None, taps: fl.FfnTaps | None = None, stream=None,
+                     sample_capacity: int = 0):
         """A training step whose samples come from the bitfield march instead of the resampler (the step of
         ffnerf_tools.py:1446-1530 with ffn_train_step_marched): io's rays and targets, the same learning-rate
         schedule and Adam counter as step().  The occupancy grid is not updated (the bitfield is an input);
-        n_samples (optional, device [num_rays]) gets the samples composited per ray.  Waits on the stream once
-        inside, after the march's count."""
+        n_samples (optional, device [num_rays]) gets the samples composited per ray.  With sample_capacity 0 it
+        waits on the stream once inside, after the march's count; with sample_capacity C > 0 it does not wait
+        and trains the rays whose samples fit into the first C slots of the march order (the later rays are
+        dropped: no samples, background colour)."""
         if rng_u32 is None:
             rng_u32 = self._get_rng_u32()
         self.steps_trained = int(self.steps_trained) + 1
@@ -544,7 +547,8 @@ class Nerf:
         sc.beta1, sc.beta2, sc.eps = float(self.spec.beta1), float(self.spec.beta2), float(self.spec.eps)
         sc.rng_seed = int(rng_u32) & 0xFFFFFFFF
         sc.do_train = 1
-        mp = fl.march_params(res, dt, max_steps, T_stop=T_stop, sh_multiplier=sh_multiplier)
+        mp = fl.march_params(res, dt, max_steps, T_stop=T_stop, sh_multiplier=sh_multiplier,
+                             sample_capacity=sample_capacity)
         fl.check(self.handle.lib.ffn_train_step_marched(
             self.handle.h, fl.ptr(io.rays_buf), fl.ptr(io.targets_buf), fl.ptr(io.out_buf), io.num_rays,
             fl.ptr(bits), C.byref(mp), C.byref(sc), C.byref(taps) if taps is not None else None, fl.ptr(n_samples),
@@ -556,10 +560,13 @@ class Nerf:
         return ev
 
     def render_marched(self, io: RayBatch, bits, res: int, dt: float, max_steps: int = 1024, T_stop: float = 1e-4,
-                       chunk: int = 32, sh_multiplier: float = 1.0, n_samples=None, stream=None):
+                       chunk: int = 32, sh_multiplier: float = 1.0, n_samples=None, stream=None,
+                       no_wait: bool = False):
         """Forward-only render of io's rays: bitfield DDA march, MLPs, front-to-back compositing stopped at
-        T < T_stop.  io.out_buf gets {r, g, b, T_final} per ray (black background)."""
-        mp = fl.march_params(res, dt, max_steps, T_stop=T_stop, chunk=chunk, sh_multiplier=sh_multiplier)
+        T < T_stop.  io.out_buf gets {r, g, b, T_final} per ray (black background).  no_wait: every round is
+        enqueued and sized on the device (no wait on the stream; the same results)."""
+        mp = fl.march_params(res, dt, max_steps, T_stop=T_stop, chunk=chunk, sh_multiplier=sh_multiplier,
+                             flags=fl.RENDER_NO_WAIT if no_wait else 0)
         fl.check(self.handle.lib.ffn_render(self.handle.h, fl.ptr(io.rays_buf), io.num_rays, fl.ptr(bits),
                                             C.byref(mp), fl.ptr(io.out_buf), fl.ptr(n_samples),
                                             fl.stream_ptr(stream)), "ffn_render")

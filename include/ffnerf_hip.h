@@ -39,8 +39,10 @@
 extern "C" {
 #endif
 
-/* 2: ffn_taps gained T_final, relu and color; ffn_params.table became void* (binary16 tables). */
-#define FFN_ABI_VERSION 2
+/* 2: ffn_taps gained T_final, relu and color; ffn_params.table became void* (binary16 tables).
+ * 3: ffn_march_params' reserved words became sample_capacity and flags (zero keeps the version-2
+ *    behaviour). */
+#define FFN_ABI_VERSION 3
 #define FFN_MAX_LEVELS 32
 
 /* layer slots (reference kernel-argument order, ffnerf_tools.py:1210-1232) */
@@ -205,8 +207,14 @@ typedef struct ffn_march_params {
   float T_stop;           /* render: a ray stops after the sample that leaves T < T_stop */
   uint32_t chunk;         /* render: samples marched per ray per round */
   float sh_multiplier;    /* render: SH scale of the colour-net input */
-  int32_t reserved[2];
+  uint32_t sample_capacity; /* marched step: 0, or the most samples a step takes (no host wait, see below) */
+  uint32_t flags;         /* render: FFN_RENDER_NO_WAIT or 0 */
 } ffn_march_params;
+
+/* ffn_render enqueues all ceil(max_steps / chunk) rounds and never waits on
+ * the stream: every launch is sized from device-side counts (rounds after the
+ * last ray retires are empty launches). */
+#define FFN_RENDER_NO_WAIT 1u
 
 /* March every ray through the bitfield (box and t_near/t_far of the handle's
  * config) and compact the samples: counts/offsets [num_rays]; samples
@@ -252,8 +260,17 @@ int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const u
  * the per-ray T_final and color, and the summed gradients.  A step whose
  * march finds no samples returns the background, leaves the table and its
  * moments as they are and runs the MLP's Adam on zero gradients.  Both MLP
- * paths (mlp_precision fp32 or fp16).  Waits on the stream once, after the
- * march's count, to size the step's launches. */
+ * paths (mlp_precision fp32 or fp16).
+ * With mp->sample_capacity = 0 the step waits on the stream once, after the
+ * march's count, to size its buffers and launches.  With sample_capacity = C
+ * > 0 it never waits (it can be captured in a graph): buffers are sized for C
+ * samples and every launch reads the count on the device.  The rays whose
+ * samples all fit into the first C slots of the march order are trained;
+ * the later rays (the first whose samples would pass slot C and every one
+ * after it) are dropped: they get no samples, n_samples 0 and the background
+ * colour, and no gradient.  With C >= the march's total the step is
+ * bit-identical to the waiting one.  taps need sample_capacity = 0; C may not
+ * exceed num_rays * max_steps. */
 int ffn_train_step_marched(void* handle, const void* rays, const void* targets, void* out_rgb, uint32_t num_rays,
                            const uint32_t* bits, const ffn_march_params* mp, const ffn_step_scalars* scalars,
                            const ffn_taps* taps, uint32_t* n_samples, void* stream);
@@ -262,7 +279,9 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
  * ray, encode, run the MLPs, composite front to back, retire rays below
  * T_stop, repeat.  out_rgb [num_rays] float4 {r, g, b, T_final} (black
  * background); n_samples [num_rays] (optional) = samples composited.  Waits
- * on the stream once per round to size the round's launches. */
+ * on the stream once per round to size the round's launches, and stops after
+ * the first round without samples; with mp->flags & FFN_RENDER_NO_WAIT it does
+ * not wait (same results). */
 int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t* bits, const ffn_march_params* mp,
                void* out_rgb, uint32_t* n_samples, void* stream);
 

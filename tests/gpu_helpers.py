@@ -169,6 +169,25 @@ class GpuModel:
         torch.cuda.synchronize()
         return to_np(out), to_np(used)
 
+    def step_marched_plain(self, rays, targets, bits, mp, scalars: dict):
+        """ffn_train_step_marched without taps (so that mp.sample_capacity may be set): (out [N,4], n_used [N])."""
+        rays_t = to_dev(np.ascontiguousarray(rays, np.float32).reshape(-1, 8))
+        tg_t = to_dev(np.ascontiguousarray(targets, np.float32).reshape(-1, 4))
+        bits_t = to_dev(np.ascontiguousarray(bits, np.uint32))
+        N = rays_t.shape[0]
+        out = torch.zeros((N, 4), dtype=torch.float32, device=DEV)
+        used = torch.zeros(N, dtype=torch.int32, device=DEV)
+        sc = fl.FfnStepScalars()
+        for k in ("lr", "lr_t", "color_rel_lr", "sh_multiplier", "occ_strength", "beta1", "beta2", "eps"):
+            setattr(sc, k, float(scalars[k]))
+        sc.rng_seed = int(scalars["rng_seed"]) & 0xFFFFFFFF
+        sc.do_train = 1
+        fl.check(self.lib.ffn_train_step_marched(self.h.h, fl.ptr(rays_t), fl.ptr(tg_t), fl.ptr(out), N,
+                                                 fl.ptr(bits_t), C.byref(mp), C.byref(sc), None, fl.ptr(used),
+                                                 fl.stream_ptr()), "ffn_train_step_marched")
+        torch.cuda.synchronize()
+        return to_np(out), to_np(used, np.uint32)
+
     def train_step_marched(self, rays, targets, bits, mp, scalars: dict):
         """ffn_train_step_marched with every tap.  The step's samples (and so the taps' length) come from an
         ffn_march of the same rays first, which also gives the sample times (Ts), positions (x) and samples

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     for n in declared_functions():
         assert hasattr(lib, n), n
     assert sorted(ffn_lib.EXPORTS) == declared_functions()
-    assert ffn_lib.load().ffn_version() == ffn_lib.ABI_VERSION == 2
+    assert ffn_lib.load().ffn_version() == ffn_lib.ABI_VERSION == 3
 
 
 def test_binding_refuses_another_abi_version(monkeypatch):
@@ -40,7 +40,7 @@ def test_binding_refuses_another_abi_version(monkeypatch):
     if not ffn_lib.LIB_PATH.exists():
         pytest.fail("libffnerf_hip.so is not built (run __graft_entry__.build())")
     monkeypatch.setattr(ffn_lib, "ABI_VERSION", 1)
-    with pytest.raises(ffn_lib.FfnError, match="ABI version 2"):
+    with pytest.raises(ffn_lib.FfnError, match="ABI version 3"):
         ffn_lib.load(ffn_lib.LIB_PATH)
 
 
