@@ -385,6 +385,10 @@ struct StageTimer {
 // Records the handle's last work on stream st (re-recording the stream's event), so that ffn_destroy waits
 // for the work of this handle only, not for the device's other streams.
 void note_use(Handle* h, hipStream_t st) {
+  // a call captured into a graph runs when the graph is launched, not here: the caller orders those launches
+  // before ffn_destroy (no event is recorded into the capture)
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return;
   for (StreamUse& u : h->uses) {
     if (u.st == st) {
       if (hipEventRecord(u.ev, st) != hipSuccess) h->uses_lost = true;

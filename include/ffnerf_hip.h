@@ -142,7 +142,9 @@ const char* ffn_last_error(void);
 
 int ffn_create(const ffn_config* cfg, void** handle);
 /* Waits for the work the handle's calls enqueued (on every stream they were
- * given), then frees the handle and its scratch. */
+ * given), then frees the handle and its scratch.  Calls captured into a HIP
+ * graph run when the caller launches the graph: the caller finishes those
+ * launches before ffn_destroy. */
 int ffn_destroy(void* handle);
 int ffn_bind_params(void* handle, const ffn_params* params);
 

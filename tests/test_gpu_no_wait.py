@@ -191,3 +191,110 @@ def test_render_no_wait_cfg4(gh, mlp):
     assert used.sum() > n
     np.testing.assert_array_equal(out2.view(np.uint32), out.view(np.uint32))
     np.testing.assert_array_equal(used2, used)
+
+
+def _scalars_struct(fl, sc):
+    s = fl.FfnStepScalars()
+    for k in ("lr", "lr_t", "color_rel_lr", "sh_multiplier", "occ_strength", "beta1", "beta2", "eps"):
+        setattr(s, k, float(sc[k]))
+    s.rng_seed = int(sc["rng_seed"]) & 0xFFFFFFFF
+    s.do_train = 1
+    return s
+
+
+@pytest.mark.parametrize("mlp", [0, 1])
+def test_marched_step_with_capacity_replays_from_a_graph(gh, mlp):
+    """What the capacity is for: the marched step captured once in a HIP graph (torch.cuda.CUDAGraph) and
+    replayed three times, with eager work and synchronisations between the replays, leaves after every replay
+    the state, colours and samples used of the same number of eager steps (bit for bit).  A warm-up call
+    sizes the handle's buffers first, so the captured call allocates nothing."""
+    import ctypes as C
+    import ffn_lib as fl
+    import torch
+    print(f"[case] marched step graph replay mlp_precision={mlp}", flush=True)
+    spec = _spec("cfg0", mlp)
+    p = random_params(spec, seed=111)
+    p["bd_out"][0] = 8.0
+    rays = look_at_rays(256, spec, seed=112, miss_frac=0.1)
+    tg = sphere_targets(rays, spec)
+    bits = shell_bits(R, seed=113, frac=0.2)
+    max_steps = 128
+    total = gh.GpuModel(spec, p).march(rays, bits, fl.march_params(R, DT, max_steps))[4]
+    mp = fl.march_params(R, DT, max_steps, T_stop=1e-2, sample_capacity=total + 4096)
+    sc = default_scalars(rng_seed=1100, occ_strength=1.0)
+    eager = gh.GpuModel(spec, p)
+    m = gh.GpuModel(spec, p)
+    N = rays.shape[0]
+    rays_t = gh.to_dev(rays.reshape(-1, 8))
+    tg_t = gh.to_dev(tg.reshape(-1, 4))
+    bits_t = gh.to_dev(bits)
+    out = torch.zeros((N, 4), dtype=torch.float32, device="cuda")
+    used = torch.zeros(N, dtype=torch.int32, device="cuda")
+    scs = _scalars_struct(fl, sc)
+    s = torch.cuda.Stream()
+
+    def call():
+        fl.check(m.lib.ffn_train_step_marched(m.h.h, fl.ptr(rays_t), fl.ptr(tg_t), fl.ptr(out), N, fl.ptr(bits_t),
+                                              C.byref(mp), C.byref(scs), None, fl.ptr(used), fl.stream_ptr()),
+                 "ffn_train_step_marched")
+
+    with torch.cuda.stream(s):
+        call()  # warm-up: the handle's buffers
+    torch.cuda.synchronize()
+    eo, eu = eager.step_marched_plain(rays, tg, bits, mp, sc)
+    assert_same_state(m.state(), eager.state())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        call()
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        eo, eu = eager.step_marched_plain(rays, tg, bits, mp, sc)
+        assert_same_state(m.state(), eager.state())
+        np.testing.assert_array_equal(gh.to_np(out).view(np.uint32), eo.view(np.uint32))
+        np.testing.assert_array_equal(gh.to_np(used, np.uint32), eu)
+        torch.zeros(1 << 20, device="cuda").add_(1.0)  # eager work between the replays
+
+
+def test_render_no_wait_replays_from_a_graph(gh):
+    """The no-wait render captured once and replayed three times on changing inputs (the rays' buffer is
+    refilled between replays) gives each time the waiting render's image of those rays."""
+    import ctypes as C
+    import ffn_lib as fl
+    import torch
+    print("[case] render no-wait graph replay", flush=True)
+    spec = spec_cfg0(hash_opt=1)
+    p = random_params(spec, seed=121)
+    p["bd_out"][0] = 6.0
+    g = gh.GpuModel(spec, p)
+    ref = gh.GpuModel(spec, p)
+    bits = shell_bits(R, seed=122, frac=0.05)
+    N = 600
+    mp = fl.march_params(R, DT, 512, T_stop=1e-2, chunk=32, flags=fl.RENDER_NO_WAIT)
+    mp_wait = fl.march_params(R, DT, 512, T_stop=1e-2, chunk=32)
+    rays_t = gh.to_dev(look_at_rays(N, spec, seed=123, miss_frac=0.05).reshape(-1, 8))
+    bits_t = gh.to_dev(bits)
+    out = torch.zeros((N, 4), dtype=torch.float32, device="cuda")
+    used = torch.zeros(N, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+
+    def call():
+        fl.check(g.lib.ffn_render(g.h.h, fl.ptr(rays_t), N, fl.ptr(bits_t), C.byref(mp), fl.ptr(out),
+                                  fl.ptr(used), fl.stream_ptr()), "ffn_render")
+
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        call()
+    for rep in range(3):
+        rays = look_at_rays(N, spec, seed=130 + rep, miss_frac=0.05)
+        rays_t.copy_(gh.to_dev(rays.reshape(-1, 8)))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        o_ref, u_ref = ref.render(rays, bits, mp_wait)
+        np.testing.assert_array_equal(gh.to_np(out).view(np.uint32), o_ref.view(np.uint32))
+        np.testing.assert_array_equal(gh.to_np(used), u_ref)
+        assert u_ref.sum() > 1000
