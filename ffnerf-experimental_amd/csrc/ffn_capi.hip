@@ -266,6 +266,17 @@ ffn::DevCfg make_devcfg(const ffn_config* c) {
     const float bs = d.bmax[i] - d.bmin[i];
     int e = 0;
     d.inv_extent[i] = (std::isfinite(bs) && bs > 0.0f && std::frexp(bs, &e) == 0.5f) ? std::ldexp(1.0f, 1 - e) : 0.0f;
+    // the occupancy grid's uniform constants, in the device code's single-precision operations
+    d.inv_bs[i] = 1.0f / bs;
+    d.occ_cell[i] = bs * (1.0f / (float)c->occ_G);
+  }
+  d.Gf = (float)c->occ_G;
+  {
+    const float dx = d.bmax[0] - d.bmin[0], dy = d.bmax[1] - d.bmin[1], dz = d.bmax[2] - d.bmin[2];
+    d.dhalf = 0.5f * std::sqrt(dx * dx + dy * dy + dz * dz);
+    d.occ_lat = std::fmax(d.occ_cell[0], 1.0e-12f);
+    const float Dl = d.dhalf / d.occ_lat;
+    d.occ_den = std::fmax(Dl * Dl + Dl + (1.0f / 3.0f), 1.0e-12f);
   }
   d.rho_min = c->rho_min;
   d.rho_max = c->rho_max;
@@ -807,6 +818,7 @@ int check_march(Handle* h, const void* rays, const uint32_t* bits, const ffn_mar
   if (mp->res < 1 || mp->res > 1024) return fail(-1, "march res=%d out of [1,1024]", mp->res);
   if (!(mp->dt > 0.0f)) return fail(-1, "march dt must be > 0");
   if (mp->max_steps == 0 || mp->max_steps > (1u << 20)) return fail(-1, "max_steps=%u out of [1,2^20]", mp->max_steps);
+  if (mp->flags & ~FFN_RENDER_NO_WAIT) return fail(-1, "unknown march flags 0x%x", mp->flags);
   return 0;
 }
 
@@ -858,6 +870,7 @@ int ffn_march(void* handle, const void* rays, uint32_t num_rays, const uint32_t*
   int rc = check_march(h, rays, bits, mp);
   if (rc) return rc;
   if (!counts || !offsets || !total || (capacity > 0 && (!samples || !ray_ids))) return fail(-1, "NULL buffer");
+  if (mp->sample_capacity) return fail(-1, "sample_capacity is the marched step's (the march takes `capacity`)");
   if (num_rays == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   UseMark um{h, st};
@@ -887,6 +900,7 @@ int ffn_march_noalloc(void* handle, const void* rays, uint32_t num_rays, const u
   int rc = check_march(h, rays, bits, mp);
   if (rc) return rc;
   if (!counts || !offsets || !total || (capacity > 0 && (!samples || !ray_ids))) return fail(-1, "NULL buffer");
+  if (mp->sample_capacity) return fail(-1, "sample_capacity is the marched step's (the march takes `capacity`)");
   if (num_rays > FFN_MARCH_NOALLOC_MAX_RAYS)
     return fail(-1, "ffn_march_noalloc: num_rays=%u exceeds its scratch of %u rays (use ffn_march)", num_rays,
                 (uint32_t)FFN_MARCH_NOALLOC_MAX_RAYS);
@@ -1170,7 +1184,7 @@ int ffn_render(void* handle, const void* rays, uint32_t num_rays, const uint32_t
   if (!h->bound) return fail(-1, "bind params first");
   if (mp->chunk == 0 || mp->chunk > 1024) return fail(-1, "chunk=%u out of [1,1024]", mp->chunk);
   if (!(mp->T_stop >= 0.0f && mp->T_stop < 1.0f)) return fail(-1, "T_stop must be in [0,1)");
-  if (mp->flags & ~FFN_RENDER_NO_WAIT) return fail(-1, "unknown render flags 0x%x", mp->flags);
+  if (mp->sample_capacity) return fail(-1, "sample_capacity is the marched step's (the render sizes its rounds)");
   if (num_rays == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   UseMark um{h, st};

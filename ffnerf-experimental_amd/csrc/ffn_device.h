@@ -31,6 +31,16 @@ struct DevCfg {
   int nd, nc, G;
   float bmin[3], bmax[3];
   float inv_extent[3];  // 1 / (bmax - bmin) when that extent is a power of two (exact), else 0
+  // Uniform constants of the occupancy grid and the proposals, computed on the host with the same single-
+  // precision operations the device code would use (IEEE division and square root), so that they arrive
+  // as kernel arguments (scalar registers) instead of being recomputed on the vector ALU and held, or
+  // spilled, in vector registers for a whole kernel
+  float inv_bs[3];   // 1.0f / (bmax - bmin)
+  float occ_cell[3]; // (bmax - bmin) * (1.0f / G): an occupancy cell's extent
+  float Gf;          // (float)G
+  float dhalf;       // half the box diagonal, 0.5f * sqrtf(dx dx + dy dy + dz dz)
+  float occ_lat;     // fmaxf(occ_cell[0], 1e-12f): the proposals' lattice step
+  float occ_den;     // fmaxf(Dl Dl + Dl + 1/3, 1e-12f) with Dl = dhalf / occ_lat: the keep draw's denominator
   float rho_min, rho_max, dt_min, dt_max, t_near, t_far;
   int background, hash_opt;
   int table_f16;  // the table is IEEE binary16 (FFN_TABLE_FP16)
@@ -562,14 +572,11 @@ __device__ __forceinline__ void occ_grid_pos(const DevCfg& c, const float (&o)[3
   for (int i = 0; i < 3; ++i) {
     const float bs = c.bmax[i] - c.bmin[i];
     const float xi = o[i] + t * d[i];
-    gpos[i] = (xi - c.bmin[i]) * (1.0f / bs) * (float)c.G;
+    gpos[i] = (xi - c.bmin[i]) * c.inv_bs[i] * c.Gf;
   }
 }
 
-__device__ __forceinline__ float half_box_diagonal(const DevCfg& c) {
-  const float dx = c.bmax[0] - c.bmin[0], dy = c.bmax[1] - c.bmin[1], dz = c.bmax[2] - c.bmin[2];
-  return 0.5f * sqrtf(dx * dx + dy * dy + dz * dz);
-}
+__device__ __forceinline__ float half_box_diagonal(const DevCfg& c) { return c.dhalf; }
 
 // The occupancy proposal of one run: the samples of ray rj that lie in one subcell, from sample lid (time t_j,
 // transmittance Tr_j arriving at it) to sample `last` (t_last, T_last).  (t_prev, T_prev) is the sample
@@ -585,13 +592,8 @@ __device__ __forceinline__ void occ_propose_run(const DevCfg& c, const float (&o
                                                 uint32_t occ_word, uint32_t seed, uint32_t rj, uint32_t lid,
                                                 float Dhalf, uint32_t* occ_st) {
   const int G = c.G;
-  float gpos[3], cell_size[3];
+  float gpos[3];
   occ_grid_pos(c, o, d, t_j, gpos);
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const float bs = c.bmax[i] - c.bmin[i];
-    cell_size[i] = bs * (1.0f / (float)G);
-  }
   const int ix = (int)floorf(gpos[0]), iy = (int)floorf(gpos[1]), iz = (int)floorf(gpos[2]);
   if (!((uint32_t)ix < (uint32_t)G && (uint32_t)iy < (uint32_t)G && (uint32_t)iz < (uint32_t)G)) return;
   uint32_t sub = 0;
@@ -604,8 +606,8 @@ __device__ __forceinline__ void occ_propose_run(const DevCfg& c, const float (&o
     float cmin[3], cmax[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      cmin[i] = c.bmin[i] + (float)ii[i] * cell_size[i];
-      cmax[i] = cmin[i] + cell_size[i];
+      cmin[i] = c.bmin[i] + (float)ii[i] * c.occ_cell[i];
+      cmax[i] = cmin[i] + c.occ_cell[i];
     }
     float t_enter, t_exit;
     if (ray_aabb(o, d, cmin, cmax, t_enter, t_exit)) {
@@ -642,12 +644,10 @@ __device__ __forceinline__ void occ_propose_run(const DevCfg& c, const float (&o
   // occ_st equals occ_in after every decay and proposals only raise it, so a proposal that does not exceed
   // the occ_in nibble cannot change occ_st: skip the keep draw and the atomic
   if (proposed_q > old_q) {
-    const float lat = (c.bmax[0] - c.bmin[0]) * (1.0f / (float)G);
-    const float tl = t_j / fmaxf(lat, 1.0e-12f);
-    const float Dl = Dhalf / fmaxf(lat, 1.0e-12f);
+    (void)Dhalf;  // in c.occ_den
+    const float tl = t_j / c.occ_lat;
     const float num = tl * tl + tl + (1.0f / 3.0f);
-    const float den = Dl * Dl + Dl + (1.0f / 3.0f);
-    const float keep_p = fminf(num / fmaxf(den, 1.0e-12f), 1.0f);
+    const float keep_p = fminf(num / c.occ_den, 1.0f);
     bool keep = keep_p >= 1.0f;
     if (!keep) {
       uint32_t rk = hseed;

@@ -48,9 +48,7 @@ __device__ __forceinline__ SampleOut sample_lane(const DevCfg& c, const float4* 
   uint32_t rng0 = hash_u32(seed ^ ray_id * 1597334677u);
   const float u0 = rand01(rng0) * (1.0f / (float)WG);
 
-  float inv_box[3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) inv_box[i] = 1.0f / (c.bmax[i] - c.bmin[i]);
+  const float* inv_box = c.inv_bs;  // 1.0f / (bmax - bmin), computed on the host
   const int G = c.G;
 
   uint32_t rng = hash_u32(seed ^ ray_id * 747796405u ^ (uint32_t)lid * 2891336453u);

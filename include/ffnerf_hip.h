@@ -209,8 +209,10 @@ typedef struct ffn_march_params {
   float T_stop;           /* render: a ray stops after the sample that leaves T < T_stop */
   uint32_t chunk;         /* render: samples marched per ray per round */
   float sh_multiplier;    /* render: SH scale of the colour-net input */
-  uint32_t sample_capacity; /* marched step: 0, or the most samples a step takes (no host wait, see below) */
-  uint32_t flags;         /* render: FFN_RENDER_NO_WAIT or 0 */
+  uint32_t sample_capacity; /* marched step: 0, or the most samples a step takes (no host wait, see below);
+                             ffn_march and ffn_render refuse a nonzero value */
+  uint32_t flags;         /* render: FFN_RENDER_NO_WAIT or 0 (the other entry points ignore that bit);
+                             other bits are refused */
 } ffn_march_params;
 
 /* ffn_render enqueues all ceil(max_steps / chunk) rounds and never waits on

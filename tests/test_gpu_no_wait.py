@@ -145,6 +145,16 @@ def test_marched_step_capacity_checks(gh):
     rc = m.lib.ffn_train_step_marched(m.h.h, fl.ptr(rays_t), fl.ptr(tg_t), fl.ptr(out), 16, fl.ptr(bits_t),
                                       C.byref(mp), C.byref(sc), C.byref(tp), None, fl.stream_ptr())
     assert rc != 0 and b"taps" in fl.load().ffn_last_error()
+    # the capacity belongs to the marched step; flags other than FFN_RENDER_NO_WAIT are refused everywhere
+    for bad, what in ((fl.march_params(R, DT, 8, sample_capacity=64), "sample_capacity"),
+                      (fl.march_params(R, DT, 8, flags=2), "flags")):
+        with pytest.raises(fl.FfnError, match=what):
+            m.render(rays, shell_bits(R), bad)
+        with pytest.raises(fl.FfnError, match=what):
+            m.march(rays, shell_bits(R), bad)
+    with pytest.raises(fl.FfnError, match="flags"):
+        m.step_marched_plain(rays, sphere_targets(rays, spec), shell_bits(R), fl.march_params(R, DT, 8, flags=2),
+                             default_scalars())
 
 
 @pytest.mark.parametrize("chunk", [16, 512])
