@@ -91,13 +91,15 @@ def test_marched_step_capacity_equals_waiting(gh, mlp, shape):
     assert not np.array_equal(st0["occ_st"], p["occ_st"])  # the proposals raised some words
 
 
-@pytest.mark.parametrize("mlp", [0, 1])
-def test_marched_step_capacity_drops_the_later_rays(gh, mlp):
+@pytest.mark.parametrize("mlp,budget", [(0, "8192"), (1, "8192"), (0, "0")])
+def test_marched_step_capacity_drops_the_later_rays(gh, monkeypatch, mlp, budget):
     """A capacity below the total: the rays whose samples all fit into the first `cap` slots of the march
     order are trained exactly as a waiting step on those rays alone; every later ray gets no sample and the
-    (white) background."""
+    (white) background.  With FFN_MARCH_SLOT_BUDGET_MB=0 the march walks twice (count, then emit into the
+    scanned slots, where a dropped ray's first samples may land past the kept count, unread)."""
     import ffn_lib as fl
-    print(f"[case] marched step capacity < total mlp_precision={mlp}", flush=True)
+    print(f"[case] marched step capacity < total mlp_precision={mlp} slot budget {budget}", flush=True)
+    monkeypatch.setenv("FFN_MARCH_SLOT_BUDGET_MB", budget)
     spec = _spec("cfg0", mlp)
     p = random_params(spec, seed=71)
     p["bd_out"][0] = 8.0
@@ -157,12 +159,14 @@ def test_marched_step_capacity_checks(gh):
                              default_scalars())
 
 
-@pytest.mark.parametrize("chunk", [16, 512])
-def test_render_no_wait_equals_waiting(gh, chunk):
+@pytest.mark.parametrize("chunk,budget", [(16, "8192"), (512, "8192"), (16, "0")])
+def test_render_no_wait_equals_waiting(gh, monkeypatch, chunk, budget):
     """cfg0 model: the no-wait render (every round enqueued, empty ones gated off on the device) against the
-    waiting render, twice on one handle (the gate of the first round is opened again by every call)."""
+    waiting render, twice on one handle (the gate of the first round is opened again by every call); with
+    FFN_MARCH_SLOT_BUDGET_MB=0 each round walks twice (count, emit), both walks gated."""
     import ffn_lib as fl
-    print(f"[case] render no-wait chunk={chunk}", flush=True)
+    print(f"[case] render no-wait chunk={chunk} slot budget {budget}", flush=True)
+    monkeypatch.setenv("FFN_MARCH_SLOT_BUDGET_MB", budget)
     spec = spec_cfg0(hash_opt=1)
     p = random_params(spec, seed=91)
     p["bd_out"][0] = 6.0
