@@ -243,6 +243,15 @@ __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp
 
 // log(1 + e^x): log1p of y = e^x as log(u) * y / (u - 1), u = 1 + y (exact for the rounded u, so accurate
 // for small y; Goldberg's method), on v_log_f32 and v_rcp_f32
+// ReLU as one integer maximum of the bit pattern: a float with the sign bit clear is a non-negative integer,
+// one with it set a negative one, so max_i32(bits, 0) keeps x > 0 (and +0) and maps every negative value and
+// -0 to +0 -- the values of x > 0 ? x : 0.  Written as a float comparison, the compiler lowers it to an IEEE
+// maximum that first canonicalises its MFMA-produced operand (two vector instructions per value).
+__device__ __forceinline__ float relu_f(float x) {
+  const int b = __float_as_int(x);
+  return __int_as_float(b > 0 ? b : 0);
+}
+
 __device__ __forceinline__ float softplus(float x) {
   if (x > 20.0f) return x;
   const float y = fast_exp(x);

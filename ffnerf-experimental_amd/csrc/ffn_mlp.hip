@@ -102,7 +102,7 @@ __device__ __forceinline__ void fwd_tiles(const float* __restrict__ W, const flo
   for (int t = 0; t < OT; ++t) {
     if (relu) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] = acc[t][r] > 0.0f ? acc[t][r] : 0.0f;
+      for (int r = 0; r < 4; ++r) acc[t][r] = relu_f(acc[t][r]);
     }
     out[t] = acc[t];
   }
@@ -305,7 +305,7 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
         for (int kk = 0; kk < 4; ++kk) acc = mfma4(w4[kk], a0r[kq + kk], acc);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
+      for (int r = 0; r < 4; ++r) acc[r] = relu_f(acc[r]);
       hd[0][t] = acc;
     }
   }

@@ -203,7 +203,7 @@ __device__ __forceinline__ void fwd_k32(const _Float16* __restrict__ W, int P, c
   for (int t = 0; t < OT; ++t) {
     if (relu) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] = acc[t][r] > 0.0f ? acc[t][r] : 0.0f;
+      for (int r = 0; r < 4; ++r) acc[t][r] = relu_f(acc[t][r]);
     }
     out[t] = acc[t];
   }
@@ -225,7 +225,7 @@ __device__ __forceinline__ void fwd_k16(const _Float16* __restrict__ W, int P, c
     acc = mfma_k16(w[t], in, acc);
     if (relu) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = acc[r] > 0.0f ? acc[r] : 0.0f;
+      for (int r = 0; r < 4; ++r) acc[r] = relu_f(acc[r]);
     }
     out[t] = acc;
   }
