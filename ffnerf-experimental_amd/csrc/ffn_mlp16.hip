@@ -113,12 +113,13 @@ __device__ __forceinline__ float delta_scale(const floatx4 (&d)[NT], float* inv)
 #pragma unroll
     for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(d[t][r]));
   {
+    // the maxima of non-negative floats as unsigned maxima of their bit patterns (the float form
+    // canonicalises both swapped operands first)
     const unsigned int u = __float_as_uint(m);
     const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    const float m2 = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-    const unsigned int u2 = __float_as_uint(m2);
+    const unsigned int u2 = p[0] > p[1] ? p[0] : p[1];
     const auto q = __builtin_amdgcn_permlane16_swap(u2, u2, false, false);
-    m = fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+    m = __uint_as_float(q[0] > q[1] ? q[0] : q[1]);
   }
   int e = 0;
   if (m > 0.0f && m < 3.0e38f) {
