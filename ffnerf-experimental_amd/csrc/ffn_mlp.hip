@@ -144,20 +144,18 @@ __device__ __forceinline__ void relu_mask(floatx4 (&d)[NT], const floatx4 (&act)
 }
 
 // Weight-gradient tiles of one layer held by one wavefront: the layer's 16x16 tile (T, Tp) (rows 16T..,
-// columns 16Tp..) dealt to it as its m-th by deal_tile in w[m] (D layout), and in b[m] a per-lane partial
-// of the bias gradient when Tp = 0.
+// columns 16Tp..) dealt to it as its m-th by deal_tile in w[m] (D layout), and in b a per-lane partial
+// of the bias gradient of its tile with Tp = 0 (deal_tile gives a wavefront at most one per layer).
 template <int OT, int IT>
 struct WaveGrad {
   static constexpr int N = OT * IT / 4;
   static_assert(OT * IT % 4 == 0, "a layer's gradient tiles split evenly over four wavefronts");
   floatx4 w[N];
-  float b[N];
+  float b;
   __device__ __forceinline__ void zero() {
 #pragma unroll
-    for (int m = 0; m < N; ++m) {
-      w[m] = floatx4{0.f, 0.f, 0.f, 0.f};
-      b[m] = 0.0f;
-    }
+    for (int m = 0; m < N; ++m) w[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+    b = 0.0f;
   }
 };
 
@@ -202,7 +200,7 @@ __device__ __forceinline__ void layer_dw(const float* __restrict__ st, WaveGrad<
       float bs = 0.0f;
 #pragma unroll
       for (int q = 0; q < 4; ++q) bs += (dv[q][0] + dv[q][1]) + (dv[q][2] + dv[q][3]);
-      acc.b[m] += bs;
+      acc.b += bs;
     }
   }
 }
@@ -222,7 +220,7 @@ __device__ __forceinline__ void flush_layer(float* __restrict__ dst, int O, int 
       if (row < O && col < In) dst[row * In + col] = acc.w[m][r];
     }
     if (Tp == 0) {
-      float bs = acc.b[m];
+      float bs = acc.b;
       bs += __shfl_xor(bs, 16);
       bs += __shfl_xor(bs, 32);
       if (g == 0 && 16 * T + s < O) dst[O * In + 16 * T + s] = bs;

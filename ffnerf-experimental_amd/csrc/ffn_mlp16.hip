@@ -351,20 +351,18 @@ __device__ __forceinline__ void stash_act(__bf16* __restrict__ st, int row0, int
   });
 }
 
-// One wavefront's weight-gradient tiles of a layer (D layout) and, for its Tp = 0 tiles, a per-lane
+// One wavefront's weight-gradient tiles of a layer (D layout) and, for its tile with Tp = 0, a per-lane
 // partial of the bias gradient.
 template <int OT, int IT>
 struct WaveGrad16 {
   static constexpr int N = OT * IT / 4;
   static_assert(OT * IT % 4 == 0, "a layer's gradient tiles split evenly over four wavefronts");
   floatx4 w[N];
-  float b[N];
+  float b;  // the bias partial of the wavefront's tile with Tp = 0 (at most one per layer, deal_tile)
   __device__ __forceinline__ void zero() {
 #pragma unroll
-    for (int m = 0; m < N; ++m) {
-      w[m] = floatx4{0.f, 0.f, 0.f, 0.f};
-      b[m] = 0.0f;
-    }
+    for (int m = 0; m < N; ++m) w[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+    b = 0.0f;
   }
 };
 
@@ -380,7 +378,7 @@ __device__ __forceinline__ void layer_dw(const __bf16* __restrict__ st, WaveGrad
     const __bf16* drow = st + (16 * T + s) * PS + 8 * g;
     const __bf16* arow = st + (16 * (OT + Tp) + s) * PS + 8 * g;
     floatx4 c = acc.w[m];
-    float bs = acc.b[m];
+    float bs = acc.b;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const bf16x8 dv = *reinterpret_cast<const bf16x8*>(drow + 32 * q);
@@ -391,7 +389,7 @@ __device__ __forceinline__ void layer_dw(const __bf16* __restrict__ st, WaveGrad
               (((float)dv[4] + (float)dv[5]) + ((float)dv[6] + (float)dv[7]));
     }
     acc.w[m] = c;
-    acc.b[m] = bs;
+    if (Tp == 0) acc.b = bs;
   }
 }
 
@@ -410,7 +408,7 @@ __device__ __forceinline__ void flush_layer16(float* __restrict__ dst, int O, in
       if (row < O && col < In) dst[row * In + col] = acc.w[m][r];
     }
     if (Tp == 0) {
-      float bs = acc.b[m];
+      float bs = acc.b;
       bs += __shfl_xor(bs, 16);
       bs += __shfl_xor(bs, 32);
       if (g == 0 && 16 * T + s < O) dst[O * In + 16 * T + s] = bs;

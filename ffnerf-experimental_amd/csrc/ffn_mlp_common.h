@@ -94,24 +94,34 @@ __device__ __forceinline__ Seg seg_dpp(const Seg& v) {  // identity (1, 0) where
              dpp_or<CTRL, ROW_MASK>(0.0f, v.v1), dpp_or<CTRL, ROW_MASK>(0.0f, v.v2)};
 }
 
+// v read from the lane CTRL selects, 0 where the source lane is invalid (bound_ctrl): for the row shifts
+// whose result the invalid lanes discard, so the read needs no copy of an `old` value and can fold into
+// the combine's arithmetic
+template <int CTRL>
+__device__ __forceinline__ Seg seg_dpp_z(const Seg& v) {
+  auto z = [](float x) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true)); };
+  return Seg{z(v.a), z(v.v0), z(v.v1), z(v.v2)};
+}
+
 // exclusive prefix of seg_combine over each segment (identity at its first lane); *total = the segment's
 // combination of all its lanes
 __device__ __forceinline__ Seg comp_seg_prefix(Seg v, int lane, int S, Seg* total) {
   const int key = lane & 15 & (S - 1);  // position inside the segment's part of the row
+  // row_shr:k: lanes with key < k (the row's first k lanes among them) keep v, so their reads are unused
   if (S > 1) {
-    const Seg n = seg_combine(seg_dpp<0x111>(v), v);  // row_shr:1
+    const Seg n = seg_combine(seg_dpp_z<0x111>(v), v);  // row_shr:1
     if (key >= 1) v = n;
   }
   if (S > 2) {
-    const Seg n = seg_combine(seg_dpp<0x112>(v), v);
+    const Seg n = seg_combine(seg_dpp_z<0x112>(v), v);
     if (key >= 2) v = n;
   }
   if (S > 4) {
-    const Seg n = seg_combine(seg_dpp<0x114>(v), v);
+    const Seg n = seg_combine(seg_dpp_z<0x114>(v), v);
     if (key >= 4) v = n;
   }
   if (S > 8) {
-    const Seg n = seg_combine(seg_dpp<0x118>(v), v);
+    const Seg n = seg_combine(seg_dpp_z<0x118>(v), v);
     if (key >= 8) v = n;
   }
   if (S >= 32) v = seg_combine(seg_dpp<0x142, 0xA>(v), v);  // row_bcast:15 into rows 1 and 3
