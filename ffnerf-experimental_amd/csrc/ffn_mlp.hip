@@ -456,10 +456,19 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
       float dLds_j, dLdc_j[3];
       composite_tile<TAPS, SC>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
       if (!train) continue;
-      dLds = __shfl(dLds_j, col);
-      dLdc0 = __shfl(dLdc_j[0], col);
-      dLdc1 = __shfl(dLdc_j[1], col);
-      dLdc2 = __shfl(dLdc_j[2], col);
+      // this wave's samples are lanes 16 wave .. 16 wave + 15 of the compositing; only the g == 0 lanes
+      // (lane s = sample 16 wave + s) use them (output deltas): row `wave` moved to row 0 by the row swaps
+      // (uniform branches, vector ALU, no LDS round trip)
+      const int wv = __builtin_amdgcn_readfirstlane(wave);  // scalar: the branches below are uniform
+      auto to_row0 = [&](float x) {
+        if (wv & 1) x = from_upper<16>(x);  // row 0 <- row 1 (and row 2 <- row 3)
+        if (wv & 2) x = from_upper<32>(x);  // rows 0, 1 <- rows 2, 3
+        return x;
+      };
+      dLds = to_row0(dLds_j);
+      dLdc0 = to_row0(dLdc_j[0]);
+      dLdc1 = to_row0(dLdc_j[1]);
+      dLdc2 = to_row0(dLdc_j[2]);
     }
 
     // ------------------------------------------------------------------

@@ -126,7 +126,12 @@ __device__ __forceinline__ Seg comp_seg_prefix(Seg v, int lane, int S, Seg* tota
   }
   if (S >= 32) v = seg_combine(seg_dpp<0x142, 0xA>(v), v);  // row_bcast:15 into rows 1 and 3
   if (S >= 64) v = seg_combine(seg_dpp<0x143, 0xC>(v), v);  // row_bcast:31 into rows 2 and 3
-  *total = shfl_seg(v, (lane & ~(S - 1)) + S - 1);
+  if (S == 64) {  // one segment: its total is lane 63's, read into scalar registers (no LDS round trip)
+    auto rl = [](float x) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63)); };
+    *total = Seg{rl(v.a), rl(v.v0), rl(v.v1), rl(v.v2)};
+  } else {
+    *total = shfl_seg(v, (lane & ~(S - 1)) + S - 1);
+  }
   Seg e = seg_dpp<0x138>(v);  // wave_shr:1
   if ((lane & (S - 1)) == 0) e = Seg{1.0f, 0.0f, 0.0f, 0.0f};
   return e;
