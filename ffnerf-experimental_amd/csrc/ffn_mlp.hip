@@ -452,23 +452,26 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
       __syncthreads();
 
       // ------------------------------------------------------------------
-      // compositing on 64 lanes: lane j = sample j of the tile (every wave)
-      float dLds_j, dLdc_j[3];
-      composite_tile<TAPS, SC>(a, sSig, sRgb, CL, lane, wave, prop_wave, train, proposals, Dhalf, dLds_j, dLdc_j);
+      // compositing on 64 lanes (lane j = sample j of the tile) by one wavefront, the tile's proposal
+      // wavefront, which also writes the output colour (and taps); its loss gradients replace sigma and rgb
+      // in LDS (only it reads them), and after a barrier every wavefront reads its own samples'.  The other
+      // three wavefronts' SIMDs meanwhile run the CU's other block.
+      if (prop_wave) {
+        float dLds_j, dLdc_j[3];
+        composite_tile<TAPS, SC>(a, sSig, sRgb, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
+        if (train) {
+          sSig[lane] = dLds_j;
+          sRgb[3 * lane] = dLdc_j[0];
+          sRgb[3 * lane + 1] = dLdc_j[1];
+          sRgb[3 * lane + 2] = dLdc_j[2];
+        }
+      }
       if (!train) continue;
-      // this wave's samples are lanes 16 wave .. 16 wave + 15 of the compositing; only the g == 0 lanes
-      // (lane s = sample 16 wave + s) use them (output deltas): row `wave` moved to row 0 by the row swaps
-      // (uniform branches, vector ALU, no LDS round trip)
-      const int wv = __builtin_amdgcn_readfirstlane(wave);  // scalar: the branches below are uniform
-      auto to_row0 = [&](float x) {
-        if (wv & 1) x = from_upper<16>(x);  // row 0 <- row 1 (and row 2 <- row 3)
-        if (wv & 2) x = from_upper<32>(x);  // rows 0, 1 <- rows 2, 3
-        return x;
-      };
-      dLds = to_row0(dLds_j);
-      dLdc0 = to_row0(dLdc_j[0]);
-      dLdc1 = to_row0(dLdc_j[1]);
-      dLdc2 = to_row0(dLdc_j[2]);
+      __syncthreads();
+      dLds = sSig[col];
+      dLdc0 = sRgb[3 * col];
+      dLdc1 = sRgb[3 * col + 1];
+      dLdc2 = sRgb[3 * col + 2];
     }
 
     // ------------------------------------------------------------------
