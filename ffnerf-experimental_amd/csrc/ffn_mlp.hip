@@ -17,8 +17,10 @@
 //     and the weights are read with the same permutation.  Activations and
 //     deltas therefore never move between lanes.
 //   * Compositing needs the whole ray: sigma/rgb go to LDS, one barrier, and
-//     every wavefront runs the reference's scan trees on 64 lanes (one lane
-//     per sample, S lanes per ray) and picks its own samples' gradients.
+//     one wavefront per tile (rotating) runs the reference's scan trees on 64
+//     lanes (one lane per sample, S lanes per ray) and leaves the loss
+//     gradients in LDS; after a second barrier every wavefront reads its own
+//     samples'.
 //   * Weight gradients dW = sum_s delta[o][s] act[i][s] need the samples as
 //     K.  Layer by layer in the backward, every wavefront writes its 16
 //     samples' deltas and input activations into a block-shared fp32 stash
