@@ -42,7 +42,8 @@ struct CompLane {
   uint32_t occ_word;  // occ_in word of the sample's cell (proposal lanes), loaded early for its latency
 };
 
-// prop_wave: this wavefront makes the tile's occupancy proposals (one wavefront per tile, all 64 lanes).
+// prop_wave: this wavefront composites the tile and makes its occupancy proposals (one wavefront per tile,
+// all 64 lanes); the others load only what the empty-tile test needs (validity and dt).
 // SC: the samples per ray when fixed at compile time (64, the benchmark's), else 0 and a.S at run time; a
 // fixed S turns the segment logic of the compositing's scans into constants.
 template <int SC>
@@ -55,15 +56,15 @@ __device__ __forceinline__ CompLane load_comp_lane(const MlpArgs& a, int64_t til
   L.rj = L.vj ? (L.bj >> log2S) : 0;
   L.dt_j = L.vj ? a.DTs[L.bj] : 0.0f;
   L.tg = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (L.vj && a.targets) L.tg = a.targets[L.rj];
+  if (prop_wave && L.vj && a.targets) L.tg = a.targets[L.rj];
   L.t_j = 0.0f;
   L.segmask = 0;
   L.occ_word = 0;
-  if (proposals && L.vj) {
+  if (prop_wave && proposals && L.vj) {
     L.t_j = a.Ts[L.bj];
     L.segmask = (uint64_t)a.flags[2 * L.rj] | ((uint64_t)a.flags[2 * L.rj + 1] << 32);
     const int lid = lane & (S - 1);
-    if (((L.segmask >> lid) & 1ull) && L.dt_j > 0.0f && prop_wave) {
+    if (((L.segmask >> lid) & 1ull) && L.dt_j > 0.0f) {
       const float4 ro = a.rays[2 * L.rj], rdv = a.rays[2 * L.rj + 1];
       const float o[3] = {ro.x, ro.y, ro.z}, d[3] = {rdv.x, rdv.y, rdv.z};
       float gpos[3];
