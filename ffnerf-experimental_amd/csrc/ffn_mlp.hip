@@ -90,15 +90,35 @@ __device__ __forceinline__ void fwd_tiles(const float* __restrict__ W, const flo
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[t][r] = B[16 * t + 4 * g + r];
   const float* wrow = W + s * P + 4 * g;
+  // Software-pipelined weight reads: output tile t's four k-steps of input tile tp run back to back (each
+  // accumulator still takes its k-steps in (tp, rp) order, the same sums), and the registers they free take
+  // tile t's weights of input tile tp + 1 while the other output tiles' MFMAs run, so no read waits at the
+  // head of the next k block.  A single output tile (the 16-row heads) double-buffers its weights instead.
+  auto wread = [&](int t, int tp) { return *reinterpret_cast<const floatx4*>(wrow + 16 * t * P + 16 * tp); };
+  if constexpr (OT == 1) {
+    floatx4 w_cur = wread(0, 0);
 #pragma unroll
-  for (int tp = 0; tp < IT; ++tp) {
+    for (int tp = 0; tp < IT; ++tp) {
+      floatx4 w_nxt = w_cur;
+      if (tp + 1 < IT) w_nxt = wread(0, tp + 1);
+#pragma unroll
+      for (int rp = 0; rp < 4; ++rp) acc[0] = mfma4(w_cur[rp], in[tp][rp], acc[0]);
+      w_cur = w_nxt;
+    }
+  } else {
     floatx4 w4[OT];
 #pragma unroll
-    for (int t = 0; t < OT; ++t) w4[t] = *reinterpret_cast<const floatx4*>(wrow + 16 * t * P + 16 * tp);
+    for (int t = 0; t < OT; ++t) w4[t] = wread(t, 0);
 #pragma unroll
-    for (int rp = 0; rp < 4; ++rp)
+    for (int tp = 0; tp < IT; ++tp) {
 #pragma unroll
-      for (int t = 0; t < OT; ++t) acc[t] = mfma4(w4[t][rp], in[tp][rp], acc[t]);
+      for (int t = 0; t < OT; ++t) {
+#pragma unroll
+        for (int rp = 0; rp < 4; ++rp) acc[t] = mfma4(w4[t][rp], in[tp][rp], acc[t]);
+        if (tp + 1 < IT) w4[t] = wread(t, tp + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   }
 #pragma unroll
   for (int t = 0; t < OT; ++t) {
