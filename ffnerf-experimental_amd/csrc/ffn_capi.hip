@@ -710,16 +710,12 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   a.occ_strength = sc->occ_strength;
   a.seed = sc->rng_seed;
   a.do_train = train ? 1 : 0;
-  // the fp32 MLP's tile order: the busy tiles first, so that every block gets the same share of them
-  // (fp32 MLP 8.41 -> 8.30 ms at the benchmark shape; the fp16 kernel, whose groups of four consecutive
-  // tiles then all hold busy tiles, measured 4.14 -> 4.20 ms and keeps the index order)
+  // the MLP's tile order: the busy tiles first, so that every block gets the same share of them (fp32 MLP
+  // 8.41 -> 8.30 ms at the benchmark shape)
   const size_t nt1 = (size_t)n_tiles + 1, n_sums = ((size_t)n_tiles + 4096) / 4096 + 2;
-  uint32_t* tile_flags = nullptr;
-  if (!mlp16) {
-    FFN_HIP(h->tile_sched.ensure(sizeof(uint32_t) * (3 * nt1 + n_sums + 4)));
-    tile_flags = (uint32_t*)h->tile_sched.p;
-    a.tile_order = tile_flags + 2 * nt1;
-  }
+  FFN_HIP(h->tile_sched.ensure(sizeof(uint32_t) * (3 * nt1 + n_sums + 4)));
+  uint32_t* tile_flags = (uint32_t*)h->tile_sched.p;
+  a.tile_order = tile_flags + 2 * nt1;
   if (taps) {
     a.t_sigma = taps->sigma;
     a.t_rgb = taps->rgb;
@@ -732,9 +728,8 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   }
   {
     StageTimer tm(h, 2, st);
-    if (!mlp16)
-      FFN_HIP(ffn::launch_tile_order(DTs, (int64_t)N, n_tiles, tile_flags, tile_flags + nt1, tile_flags + 3 * nt1,
-                                     tile_flags + 3 * nt1 + n_sums, const_cast<uint32_t*>(a.tile_order), st));
+    FFN_HIP(ffn::launch_tile_order(DTs, (int64_t)N, n_tiles, tile_flags, tile_flags + nt1, tile_flags + 3 * nt1,
+                                   tile_flags + 3 * nt1 + n_sums, const_cast<uint32_t*>(a.tile_order), st));
     if (mlp16)
       FFN_HIP(ffn::launch_mlp16(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));
     else
@@ -1040,11 +1035,9 @@ int ffn_train_step_marched(void* handle, const void* rays, const void* targets, 
   // blocks are those of the capacity's tiles: a block's tiles and the order of the partials' sum are the same
   // as for the kept count, the further blocks add zero partials.)
   const int64_t n_tiles = (n + 63) / 64;
-  // the fp16 kernel walks groups of four tiles
-  const int64_t n_work = mlp16 ? (n_tiles + 3) / 4 : n_tiles;
   int n_blocks = (h->n_cu > 0 ? h->n_cu : 256) * (mlp16 ? ffn::mlp16_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc)
                                                          : ffn::mlp_blocks_per_cu(LF, h->cfg.nd, h->cfg.nc));
-  if (n_blocks > n_work) n_blocks = (int)(n_work > 0 ? n_work : 1);
+  if (n_blocks > n_tiles) n_blocks = (int)(n_tiles > 0 ? n_tiles : 1);
   FFN_HIP(h->partials.ensure(sizeof(float) * (size_t)n_blocks * h->lay.total));
   ffn::MlpPtrs w{};
   for (int k = 0; k < FFN_N_LAYERS; ++k) {

@@ -88,9 +88,9 @@ struct MlpArgs {
   uint32_t num_rays;
   int S, log2S;
   int64_t n_tiles;
-  // k_mlp: position i of the launch's tile sequence is tile tile_order[i] (launch_tile_order: the busy tiles
-  // first, so that the round-robin deal gives every block the same share of them), or tile i when NULL;
-  // k_mlp16 takes its tiles in index order
+  // k_mlp, k_mlp16: position i of the launch's tile sequence is tile tile_order[i] (launch_tile_order: the
+  // busy tiles first, so that the round-robin deal gives every block the same share of them), or tile i when
+  // NULL
   const uint32_t* tile_order;
   float sh_mult, occ_strength;
   uint32_t seed;

@@ -8,8 +8,8 @@
 // deltas are the shared fp32 code.
 //
 // MI355X design
-//   * A 256-thread block (4 wavefronts) walks groups of four 64-sample tiles.
-//     Each wavefront runs the layers for its 16 samples of every tile; a
+//   * A 256-thread block (4 wavefronts) walks 64-sample tiles in a persistent
+//     loop.  Each wavefront runs the layers for its 16 samples of the tile; a
 //     layer's output tile (lane (g, s) holds neurons 16t + 4g + r of sample s)
 //     is exactly one half of the next layer's B operand.
 //   * gfx950's K = 32 MFMAs (v_mfma_f32_16x16x32_f16 / _bf16): lane group g
@@ -20,13 +20,12 @@
 //     stored with their K columns in that order, so every A operand is one
 //     16-byte LDS read.  Layers with K = 16 (the output layers' backward, a
 //     16-wide encoding) keep v_mfma_f32_16x16x16.
-//   * Per group: (0) wavefront w loads the compositing inputs of the group's
-//     tile w; (A) every wavefront runs the forward of its samples of the four
-//     tiles and leaves sigma and rgb in LDS; (B) wavefront w composites tile
-//     w alone (64 lanes, its proposals too) and leaves dL/dsigma, dL/dc in LDS
-//     -- one compositing per tile, not one per wavefront; (C) per tile, the
-//     forward again (the activations are not held across the compositing:
-//     registers) and the backward.
+//   * Per tile: every wavefront runs the forward of its samples, keeping the
+//     hidden activations as bf16 K blocks, and leaves sigma and rgb in LDS;
+//     after a barrier the tile's proposal wavefront composites it alone (64
+//     lanes, its proposals too) and leaves dL/dsigma, dL/dc in LDS -- one
+//     compositing per tile, not one per wavefront; the other SIMDs run the
+//     CU's other block meanwhile.  After a second barrier, the backward.
 //   * Weight gradients dW = delta . act^T need the samples as K.  Layer by
 //     layer in the backward, every wavefront writes its deltas and the layer's
 //     input activations, transposed, into a block-shared bf16 stash (rows =
@@ -173,9 +172,10 @@ struct Arch16 {
     return o;
   }
   static constexpr int g_total() { return g_off(FFN_N_LAYERS); }
-  // per tile of the group: sigma[64] + rgb[64][3] (the compositing overwrites them with dL/dsigma, dL/dc);
-  // then the group's four busy flags
-  static constexpr int comp_floats = 4 * 256 + 4;
+  // sigma[64] + rgb[64][3] of the tile (the compositing overwrites them with dL/dsigma, dL/dc): one slot
+  // when training (the stash barriers separate a tile's compositing from the next tile's writes), two
+  // alternating slots for a forward-only launch
+  static constexpr int comp_floats = 512;
   static constexpr size_t lds_bytes() {
     return (size_t)w_halves() * 2 + (size_t)b_floats() * 4 + (size_t)stash_halves() * 2 + comp_floats * 4;
   }
@@ -563,14 +563,9 @@ __device__ __forceinline__ void load_tile_in(const MlpArgs& a, int64_t b, bool v
     in.t = valid ? a.Ts[b] : 0.0f;
   }
 }
-// the first busy tile of the group at or after tt (4 if none)
-__device__ __forceinline__ int next_busy(const int* flags, int tt) {
-  while (tt < 4 && !flags[tt]) ++tt;
-  return tt;
-}
 
-// MARCHED: the backward over marched samples (phase C only, every tile busy): the loss gradients are read
-// from a.in_dLds / a.in_dLdc, the samples' rays, times and step from the march; no compositing, no proposals
+// MARCHED: the backward over marched samples (every tile busy): the loss gradients are read from a.in_dLds /
+// a.in_dLdc, the samples' rays, times and step from the march; no compositing, no proposals
 template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
 __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_mlp16(MlpArgs a) {
   using A = Arch16<LF, ND, NC>;
@@ -582,7 +577,6 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   __bf16* sS = reinterpret_cast<__bf16*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4);
   float* sC = reinterpret_cast<float*>(smem16 + (size_t)A::w_halves() * 2 + (size_t)A::b_floats() * 4 +
                                        (size_t)A::stash_halves() * 2);
-  int* sFlag = reinterpret_cast<int*>(sC + 4 * 256);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
   const int col = wave * 16 + s;  // this lane's sample column in a tile
   const bool train = a.do_train != 0;
@@ -637,245 +631,177 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   for (int i = 0; i < (ND > 1 ? ND - 1 : 1); ++i) gd_h[i].zero();
   gd_in.zero();
 
-  const int64_t n_groups = (n_tiles + 3) / 4;
-  for (int64_t grp = blockIdx.x; grp < n_groups; grp += gridDim.x) {
-    const int64_t tile0 = grp * 4;
-    TileIn<LF> cur;
-    int tt = 0;
-    if constexpr (!MARCHED) {
-      // (0) the compositing inputs of tile tile0 + wave (past the last tile: no valid lane)
-      const CompLane CL = load_comp_lane<SC>(a, tile0 + wave, lane, true, n_samples, log2S, proposals);
-      const bool busy = TAPS ? __ballot(CL.vj) != 0ull : __ballot(CL.vj && CL.dt_j > 0.0f) != 0ull;
-      __syncthreads();  // the previous group is done with sC and the flags
-      if (lane == 0) sFlag[wave] = busy ? 1 : 0;
-      __syncthreads();
-
-      // (A) forward of this wavefront's samples of every busy tile: sigma and rgb into sC; each tile's inputs
-      // are loaded while the previous tile's forward runs
-      tt = next_busy(sFlag, 0);
-      if (tt < 4) {
-        const int64_t b = (tile0 + tt) * 64 + col;
-        load_tile_in<LF, FEAT, MARCHED>(a, b, (uint64_t)b < n_samples, g, log2S, cur);
-      }
+  int parity = 0;
 #pragma unroll 1
-      while (tt < 4) {
-        const int64_t b = (tile0 + tt) * 64 + col;
-        const bool valid = (uint64_t)b < n_samples;
-        const int tn = next_busy(sFlag, tt + 1);
-        TileIn<LF> nxt;
-        if (tn < 4) {
-          const int64_t bn = (tile0 + tn) * 64 + col;
-          load_tile_in<LF, FEAT, MARCHED>(a, bn, (uint64_t)bn < n_samples, g, log2S, nxt);
-        }
-        const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
-        floatx4 sh;
+  for (int64_t ti = blockIdx.x; ti < n_tiles; ti += gridDim.x, parity ^= 1) {
+    const int64_t tile = a.tile_order ? (int64_t)a.tile_order[ti] : ti;
+    float* sSig = sC + (train ? 0 : parity * 256);
+    float* sRgb = sSig + 64;
+    const int64_t b = tile * 64 + col;
+    const bool valid = (uint64_t)b < n_samples;
+    TileIn<LF> cur;
+    load_tile_in<LF, FEAT, MARCHED>(a, b, valid, g, log2S, cur);
+    // per-sample inputs of the compositing (lane j = sample j of the tile), loaded before the forward so
+    // that their latency hides behind it
+    const bool prop_wave = (int)(tile & 3) == wave;  // this wavefront composites the tile
+    CompLane CL{};
+    if constexpr (!MARCHED) {
+      CL = load_comp_lane<SC>(a, tile, lane, prop_wave, n_samples, log2S, proposals);
+      if (!TAPS && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
+        empty_tile<LF, FEAT, SC>(a, CL, lane, wave, b, valid, train, g);
+        continue;
+      }
+    }
+    const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
+    floatx4 sh;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
-        Fwd16<LF, ND, NC> f;
-        forward16<LF, ND, NC, A, TAPS>(sWf, sB, cur.a0v, sh, g, s, f);
-        if constexpr (TAPS) {
-          if (a.t_relu) {
-            uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
+    for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
+    const float dt_b = cur.dt, t_b = cur.t;
+    Fwd16<LF, ND, NC> f;
+    forward16<LF, ND, NC, A, true>(sWf, sB, cur.a0v, sh, g, s, f);
+    if constexpr (TAPS) {
+      if (a.t_relu) {
+        uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
 #pragma unroll
-            for (int i = 0; i < ND; ++i) tap_relu8(rec, i, f.hd[i], g);
+        for (int i = 0; i < ND; ++i) tap_relu8(rec, i, f.hd[i], g);
 #pragma unroll
-            for (int i = 0; i < NC; ++i) tap_relu8(rec, 3 + i, f.hc[i], g);
-          }
-        }
-        if (g == 0) {
-          float sig = softplus(fminf(fmaxf(f.dout0, -10.0f), 10.0f));
-          if (cur.dt <= 0.0f) sig = 0.0f;
-          float* sSig = sC + tt * 256;
-          sSig[col] = sig;
-          sSig[64 + col * 3 + 0] = f.rgb[0];
-          sSig[64 + col * 3 + 1] = f.rgb[1];
-          sSig[64 + col * 3 + 2] = f.rgb[2];
-        }
-        cur = nxt;
-        tt = tn;
+        for (int i = 0; i < NC; ++i) tap_relu8(rec, 3 + i, f.hc[i], g);
+      }
+    }
+    unsigned int a0w[KB0][2];  // the encoding as the stash holds it: bf16 of the fp32 values, packed in pairs
+#pragma unroll
+    for (int t = 0; t < KB0; ++t)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        typedef float float2_ __attribute__((ext_vector_type(2)));
+        a0w[t][p] = __builtin_bit_cast(unsigned int, __builtin_convertvector(
+                                                         float2_{cur.a0v[4 * t + 2 * p], cur.a0v[4 * t + 2 * p + 1]},
+                                                         bf16x2));
+      }
+    float dLds, dLdc0, dLdc1, dLdc2;
+    if constexpr (MARCHED) {
+      __syncthreads();  // the previous tile's last gradient tiles have read the stash
+      dLds = valid ? a.in_dLds[b] : 0.0f;
+      dLdc0 = valid ? a.in_dLdc[3 * b] : 0.0f;
+      dLdc1 = valid ? a.in_dLdc[3 * b + 1] : 0.0f;
+      dLdc2 = valid ? a.in_dLdc[3 * b + 2] : 0.0f;
+    } else {
+      if (g == 0) {
+        float sig = softplus(fminf(fmaxf(f.dout0, -10.0f), 10.0f));
+        if (dt_b <= 0.0f) sig = 0.0f;
+        sSig[col] = sig;
+        sRgb[col * 3 + 0] = f.rgb[0];
+        sRgb[col * 3 + 1] = f.rgb[1];
+        sRgb[col * 3 + 2] = f.rgb[2];
       }
       __syncthreads();
-
-      // (B) this wavefront composites tile tile0 + wave (all its 64 samples, proposals included); lane j's
-      // loss gradients replace its sigma and rgb
-      {
-        float* sSig = sC + wave * 256;
-        if (busy) {
-          float dLds_j, dLdc_j[3];
-          composite_tile<TAPS, SC>(a, sSig, sSig + 64, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
+      // compositing on 64 lanes by the tile's proposal wavefront, which also writes the output colour (and
+      // taps); its loss gradients replace sigma and rgb in LDS (only it reads them), and after a barrier
+      // every wavefront reads its own samples'.  The other three SIMDs meanwhile run the CU's other block.
+      if (prop_wave) {
+        float dLds_j, dLdc_j[3];
+        composite_tile<TAPS, SC>(a, sSig, sRgb, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
+        if (train) {
           sSig[lane] = dLds_j;
-          sSig[64 + 3 * lane] = dLdc_j[0];
-          sSig[64 + 3 * lane + 1] = dLdc_j[1];
-          sSig[64 + 3 * lane + 2] = dLdc_j[2];
-        } else if ((lane & ((SC > 0 ? SC : a.S) - 1)) == 0 && CL.vj) {
-          // every alpha is 0: T = 1 and the colour is the background
-          float bg[3];
-          background(a, CL.rj, train, bg);
-          a.out_rgb[CL.rj] = make_float4(fminf(fmaxf(bg[0], 0.0f), 1.0f), fminf(fmaxf(bg[1], 0.0f), 1.0f),
-                                         fminf(fmaxf(bg[2], 0.0f), 1.0f), train ? 4.0f : 0.0f);
+          sRgb[3 * lane] = dLdc_j[0];
+          sRgb[3 * lane + 1] = dLdc_j[1];
+          sRgb[3 * lane + 2] = dLdc_j[2];
         }
       }
       if (!train) continue;
       __syncthreads();
+      dLds = sSig[col];
+      dLdc0 = sRgb[3 * col];
+      dLdc1 = sRgb[3 * col + 1];
+      dLdc2 = sRgb[3 * col + 2];
     }
-
-    // (C) per busy tile: the forward again, then the backward (fp16 chain with per-wavefront delta scaling,
-    // fp32 accumulation); every layer's deltas and inputs go through the stash for the block's bf16
-    // weight-gradient tiles (barrier, this wave's tiles, barrier before the stash is reused).  First the
-    // zero encoding gradients of the idle tiles' samples.
-    if constexpr (!MARCHED) {
-#pragma unroll 1
-      for (int ti = 0; ti < 4; ++ti) {
-        const int64_t b = (tile0 + ti) * 64 + col;
-        if (sFlag[ti] || (uint64_t)b >= n_samples) continue;
-        floatx4 z[KB0];
-#pragma unroll
-        for (int t = 0; t < KB0; ++t) z[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-        store_enc_grad<LF, FEAT>(a, b, g, z);
-      }
+    floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
+    floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
+    if (g == 0 && valid) {
+      float d3[3], dd0;
+      output_deltas(t_b, dt_b, Dhalf, dLds, dLdc0, dLdc1, dLdc2, f.rgb, f.dout0, d3, dd0);
+      dco[0][0] = d3[0];
+      dco[0][1] = d3[1];
+      dco[0][2] = d3[2];
+      ddo[0][0] = dd0;
     }
-    // (the inputs load at the start of each tile: loaded a tile ahead, they stayed live through the backward
-    // and cost more in spills than the latency they hid)
-    // marched tiles are all busy up to the last one
-    const int tiles_here = MARCHED ? (int)(n_tiles - tile0 < 4 ? n_tiles - tile0 : 4) : 4;
-    tt = MARCHED ? 0 : next_busy(sFlag, 0);
-#pragma unroll 1
-    while (tt < tiles_here) {
-      const int64_t b = (tile0 + tt) * 64 + col;
-      const bool valid = (uint64_t)b < n_samples;
-      const int tn = MARCHED ? tt + 1 : next_busy(sFlag, tt + 1);
-      load_tile_in<LF, FEAT, MARCHED>(a, b, valid, g, log2S, cur);
-      const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
-      floatx4 sh;
+    // colour output layer
+    half8 dop[2];
+    float dsc;
+    floatx4 dc[4];
+    stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return dco[t][r]; });
+    stash_act<4>(sS, 16, g, col, f.hc[NC - 1]);
+    {
+      half4 cop;
+      const float csc = make_op1(dco, cop);
+      bwd_k16<4, false>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
+      relu_mask(dc, f.hc[NC - 1]);
+      dsc = make_op4(dc, dop);
+    }
+    __syncthreads();
+    layer_dw<1, 4, PS>(sS, gc_out, wave, g, s);
+    __syncthreads();
+    // hidden colour layers (Wc_23, Wc_12, Wc_01): delta dc of layer i's output, input hc[i - 1]
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sh[r] = sh_component(dirv, 4 * g + r) * a.sh_mult;
-      const float dt_b = cur.dt, t_b = cur.t;
-      float a0v[LF / 4];
-#pragma unroll
-      for (int q = 0; q < LF / 4; ++q) a0v[q] = cur.a0v[q];
-      Fwd16<LF, ND, NC> f;
-      forward16<LF, ND, NC, A, true>(sWf, sB, a0v, sh, g, s, f);
-      unsigned int a0w[KB0][2];  // the encoding as the stash holds it: bf16 of the fp32 values, packed in pairs
-#pragma unroll
-      for (int t = 0; t < KB0; ++t)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          typedef float float2_ __attribute__((ext_vector_type(2)));
-          a0w[t][p] = __builtin_bit_cast(unsigned int, __builtin_convertvector(
-                                                           float2_{a0v[4 * t + 2 * p], a0v[4 * t + 2 * p + 1]}, bf16x2));
-        }
-      float dLds, dLdc0, dLdc1, dLdc2;
-      if constexpr (MARCHED) {
-        dLds = valid ? a.in_dLds[b] : 0.0f;
-        dLdc0 = valid ? a.in_dLdc[3 * b] : 0.0f;
-        dLdc1 = valid ? a.in_dLdc[3 * b + 1] : 0.0f;
-        dLdc2 = valid ? a.in_dLdc[3 * b + 2] : 0.0f;
-        if constexpr (TAPS) {
-          if (a.t_relu) {
-            uint32_t* rec = valid ? a.t_relu + (int64_t)RELU_WORDS * b : nullptr;
-#pragma unroll
-            for (int i = 0; i < ND; ++i) tap_relu8(rec, i, f.hd[i], g);
-#pragma unroll
-            for (int i = 0; i < NC; ++i) tap_relu8(rec, 3 + i, f.hc[i], g);
-          }
-        }
-      } else {
-        const float* sD = sC + tt * 256;
-        dLds = sD[col];
-        dLdc0 = sD[64 + 3 * col];
-        dLdc1 = sD[64 + 3 * col + 1];
-        dLdc2 = sD[64 + 3 * col + 2];
-      }
-      floatx4 dco[1] = {{0.f, 0.f, 0.f, 0.f}};
-      floatx4 ddo[1] = {{0.f, 0.f, 0.f, 0.f}};
-      if (g == 0 && valid) {
-        float d3[3], dd0;
-        output_deltas(t_b, dt_b, Dhalf, dLds, dLdc0, dLdc1, dLdc2, f.rgb, f.dout0, d3, dd0);
-        dco[0][0] = d3[0];
-        dco[0][1] = d3[1];
-        dco[0][2] = d3[2];
-        ddo[0][0] = dd0;
-      }
-      __syncthreads();  // the previous tile's last gradient tiles have read the stash
-      // colour output layer
-      half8 dop[2];
-      float dsc;
-      floatx4 dc[4];
-      stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return dco[t][r]; });
-      stash_act<4>(sS, 16, g, col, f.hc[NC - 1]);
-      {
-        half4 cop;
-        const float csc = make_op1(dco, cop);
-        bwd_k16<4, false>(sWt + A::wt_off(FFN_WC_OUT), A::pt(FFN_WC_OUT), cop, csc, dc, g, s);
-        relu_mask(dc, f.hc[NC - 1]);
-        dsc = make_op4(dc, dop);
-      }
-      __syncthreads();
-      layer_dw<1, 4, PS>(sS, gc_out, wave, g, s);
-      __syncthreads();
-      // hidden colour layers (Wc_23, Wc_12, Wc_01): delta dc of layer i's output, input hc[i - 1]
-#pragma unroll
-      for (int i = NC - 1; i >= 1; --i) {
-        const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
-        stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dc[t][r]; });
-        stash_act<4>(sS, 64, g, col, f.hc[i - 1]);
-        bwd_k32<4, false>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
-        relu_mask(dc, f.hc[i - 1]);
-        dsc = make_op4(dc, dop);
-        __syncthreads();
-        layer_dw<4, 4, PS>(sS, gc_h[i - 1], wave, g, s);
-        __syncthreads();
-      }
-      // colour input layer: its gradient, and the dout part of its input delta joins the density head's delta
+    for (int i = NC - 1; i >= 1; --i) {
+      const int k = i == 1 ? FFN_WC_01 : (i == 2 ? FFN_WC_12 : FFN_WC_23);
       stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dc[t][r]; });
-      {
-        const bf16x8 cin[1] = {f.cin};
-        stash_act<2>(sS, 64, g, col, cin);
-      }
-      bwd_k32<1>(sWt + A::wt_off(FFN_WC_IN), A::pt(FFN_WC_IN), dop, dsc, ddo, g, s);
+      stash_act<4>(sS, 64, g, col, f.hc[i - 1]);
+      bwd_k32<4, false>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dc, g, s);
+      relu_mask(dc, f.hc[i - 1]);
+      dsc = make_op4(dc, dop);
       __syncthreads();
-      layer_dw<4, 2, PS>(sS, gc_in, wave, g, s);
+      layer_dw<4, 4, PS>(sS, gc_h[i - 1], wave, g, s);
       __syncthreads();
-      // density output layer
-      floatx4 dd[4];
-      stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return ddo[t][r]; });
-      stash_act<4>(sS, 16, g, col, f.hd[ND - 1]);
-      {
-        half4 dd_op;
-        const float ssc = make_op1(ddo, dd_op);
-        bwd_k16<4, false>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
-        relu_mask(dd, f.hd[ND - 1]);
-        dsc = make_op4(dd, dop);
-      }
-      __syncthreads();
-      layer_dw<1, 4, PS>(sS, gd_out, wave, g, s);
-      __syncthreads();
-      // hidden density layers (Wd_12, Wd_01)
-#pragma unroll
-      for (int i = ND - 1; i >= 1; --i) {
-        const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
-        stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
-        stash_act<4>(sS, 64, g, col, f.hd[i - 1]);
-        bwd_k32<4, false>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
-        relu_mask(dd, f.hd[i - 1]);
-        dsc = make_op4(dd, dop);
-        __syncthreads();
-        layer_dw<4, 4, PS>(sS, gd_h[i - 1], wave, g, s);
-        __syncthreads();
-      }
-      // density input layer: deltas and the encoding (bf16 of the fp32 values); dL/da0 = Wd_in^T . delta
-      stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
-      stash_words<KB0>(sS, 64, g, col, [&](int t, int p) { return a0w[t][p]; });
-      {
-        floatx4 ga0[KB0];
-        bwd_k32<KB0, false>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
-        if (valid) store_enc_grad<LF, FEAT>(a, b, g, ga0);
-      }
-      __syncthreads();
-      layer_dw<4, KB0, PS>(sS, gd_in, wave, g, s);
-      // no barrier: the stash is next written after the next tile's barrier
-      tt = tn;
     }
+    // colour input layer: its gradient, and the dout part of its input delta joins the density head's delta
+    stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dc[t][r]; });
+    {
+      const bf16x8 cin[1] = {f.cin};
+      stash_act<2>(sS, 64, g, col, cin);
+    }
+    bwd_k32<1>(sWt + A::wt_off(FFN_WC_IN), A::pt(FFN_WC_IN), dop, dsc, ddo, g, s);
+    __syncthreads();
+    layer_dw<4, 2, PS>(sS, gc_in, wave, g, s);
+    __syncthreads();
+    // density output layer
+    floatx4 dd[4];
+    stash_rows<1>(sS, 0, g, col, [&](int t, int r) { return ddo[t][r]; });
+    stash_act<4>(sS, 16, g, col, f.hd[ND - 1]);
+    {
+      half4 dd_op;
+      const float ssc = make_op1(ddo, dd_op);
+      bwd_k16<4, false>(sWt + A::wt_off(FFN_WD_OUT), A::pt(FFN_WD_OUT), dd_op, ssc, dd, g, s);
+      relu_mask(dd, f.hd[ND - 1]);
+      dsc = make_op4(dd, dop);
+    }
+    __syncthreads();
+    layer_dw<1, 4, PS>(sS, gd_out, wave, g, s);
+    __syncthreads();
+    // hidden density layers (Wd_12, Wd_01)
+#pragma unroll
+    for (int i = ND - 1; i >= 1; --i) {
+      const int k = i == 1 ? FFN_WD_01 : FFN_WD_12;
+      stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
+      stash_act<4>(sS, 64, g, col, f.hd[i - 1]);
+      bwd_k32<4, false>(sWt + A::wt_off(k), A::pt(k), dop, dsc, dd, g, s);
+      relu_mask(dd, f.hd[i - 1]);
+      dsc = make_op4(dd, dop);
+      __syncthreads();
+      layer_dw<4, 4, PS>(sS, gd_h[i - 1], wave, g, s);
+      __syncthreads();
+    }
+    // density input layer: deltas and the encoding (bf16 of the fp32 values); dL/da0 = Wd_in^T . delta
+    stash_rows<4>(sS, 0, g, col, [&](int t, int r) { return dd[t][r]; });
+    stash_words<KB0>(sS, 64, g, col, [&](int t, int p) { return a0w[t][p]; });
+    {
+      floatx4 ga0[KB0];
+      bwd_k32<KB0, false>(sWt + A::wt_off(FFN_WD_IN), A::pt(FFN_WD_IN), dop, dsc, ga0, g, s);
+      if (valid) store_enc_grad<LF, FEAT>(a, b, g, ga0);
+    }
+    __syncthreads();
+    layer_dw<4, KB0, PS>(sS, gd_in, wave, g, s);
+    // no barrier: the stash is next written after the next tile's compositing barriers
   }
 
   if (train) {
