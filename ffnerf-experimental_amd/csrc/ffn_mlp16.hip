@@ -191,14 +191,33 @@ __device__ __forceinline__ void fwd_k32(const _Float16* __restrict__ W, int P, c
   for (int t = 0; t < OT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[t][r] = B[16 * t + 4 * g + r];
+  // Software-pipelined weight reads: the first K block's operands are all read before its MFMAs; then each
+  // MFMA's weight register takes the next K block's operand of the same output tile while the other tiles'
+  // MFMAs run (a single output tile double-buffers instead)
+  auto wread = [&](int t, int kb) { return *reinterpret_cast<const half8*>(W + (16 * t + s) * P + 32 * kb + 8 * g); };
+  if constexpr (OT == 1) {
+    half8 w_cur = wread(0, 0);
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    half8 w[OT];  // the K block's weight operands, all read before its MFMAs
+    for (int kb = 0; kb < KB; ++kb) {
+      half8 w_nxt = w_cur;
+      if (kb + 1 < KB) w_nxt = wread(0, kb + 1);
+      acc[0] = mfma_k32(w_cur, in[kb], acc[0]);
+      w_cur = w_nxt;
+    }
+  } else {
+    half8 w[OT];
 #pragma unroll
-    for (int t = 0; t < OT; ++t) w[t] = *reinterpret_cast<const half8*>(W + (16 * t + s) * P + 32 * kb + 8 * g);
+    for (int t = 0; t < OT; ++t) w[t] = wread(t, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < OT; ++t) acc[t] = mfma_k32(w[t], in[kb], acc[t]);
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int t = 0; t < OT; ++t) {
+        acc[t] = mfma_k32(w[t], in[kb], acc[t]);
+        if (kb + 1 < KB) w[t] = wread(t, kb + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   }
 #pragma unroll
   for (int t = 0; t < OT; ++t) {
@@ -240,14 +259,26 @@ __device__ __forceinline__ void bwd_k32(const _Float16* __restrict__ Wt, int P, 
   floatx4 acc[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // weight reads pipelined as in fwd_k32
+  auto wread = [&](int t, int kb) { return *reinterpret_cast<const half8*>(Wt + (16 * t + s) * P + 32 * kb + 8 * g); };
+  if constexpr (RT == 1) {
+    const half8 w0 = wread(0, 0), w1 = wread(0, 1);
+    acc[0] = mfma_k32(w0, op[0], acc[0]);
+    acc[0] = mfma_k32(w1, op[1], acc[0]);
+  } else {
+    half8 w[RT];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    half8 w[RT];  // the K block's weight operands, all read before its MFMAs
-#pragma unroll
-    for (int t = 0; t < RT; ++t) w[t] = *reinterpret_cast<const half8*>(Wt + (16 * t + s) * P + 32 * kb + 8 * g);
+    for (int t = 0; t < RT; ++t) w[t] = wread(t, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t] = mfma_k32(w[t], op[kb], acc[t]);
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        acc[t] = mfma_k32(w[t], op[kb], acc[t]);
+        if (kb == 0) w[t] = wread(t, 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   }
 #pragma unroll
   for (int t = 0; t < RT; ++t)
