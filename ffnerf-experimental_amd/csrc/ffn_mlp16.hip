@@ -340,38 +340,43 @@ __device__ __forceinline__ float make_op1(const floatx4 (&d)[1], half4& op) {
   return inv;
 }
 
+// One packed word per lane into the stash: lane (g, s) holds rows n, n + 1 (n = row0 + 16 t + 4 g + r, r
+// even) of sample column `col` as the low and high half.  Neighbouring lanes s, s ^ 1 swap their words (DPP
+// quad permutation [1, 0, 3, 2]); the even lane then writes row n and the odd lane row n + 1, each for the
+// column pair (col & ~1, col | 1) as one 32-bit store (sel: the byte selector stash_sel(s) gives the lane).
+__device__ __forceinline__ unsigned int stash_sel(int s) { return (s & 1) ? 0x03020706u : 0x05040100u; }
+__device__ __forceinline__ void stash_pair(__bf16* __restrict__ st, int n, int col, unsigned int sel,
+                                           unsigned int w) {
+  constexpr int PS = 64 + 8;
+  const unsigned int nb = (unsigned int)__builtin_amdgcn_update_dpp((int)w, (int)w, 0xB1, 0xF, 0xF, false);
+  const unsigned int v = __builtin_amdgcn_perm(nb, w, sel);
+  *reinterpret_cast<unsigned int*>(st + (n + (col & 1)) * PS + (col & ~1)) = v;
+}
+
 // stash rows row0 + 16 t + 4 g + r, column `col`, of NT D-layout tiles (value(t, r)); two values per
-// conversion (v_cvt_pk_bf16_f32), stored as the low and the high half of the packed word
+// conversion (v_cvt_pk_bf16_f32), the low and the high half of the packed word
 template <int NT, typename F>
 __device__ __forceinline__ void stash_rows(__bf16* __restrict__ st, int row0, int g, int col, F value) {
-  constexpr int PS = 64 + 8;
+  const unsigned int sel = stash_sel(col);
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; r += 2) {
       typedef float float2_ __attribute__((ext_vector_type(2)));
       const bf16x2 p = __builtin_convertvector(float2_{value(t, r), value(t, r + 1)}, bf16x2);
-      const unsigned int w = __builtin_bit_cast(unsigned int, p);
-      unsigned short* row = reinterpret_cast<unsigned short*>(st + (row0 + 16 * t + 4 * g + r) * PS + col);
-      row[0] = (unsigned short)w;
-      row[PS] = (unsigned short)(w >> 16);
+      stash_pair(st, row0 + 16 * t + 4 * g + r, col, sel, __builtin_bit_cast(unsigned int, p));
     }
 }
 
 // stash rows row0 + 16 t + 4 g + r, column `col`, of NT tiles given as packed bf16 words (word(t, r / 2)
-// holds rows r and r + 1): each word's halves go to two rows, no conversion
+// holds rows r and r + 1), no conversion
 template <int NT, typename F>
 __device__ __forceinline__ void stash_words(__bf16* __restrict__ st, int row0, int g, int col, F word) {
-  constexpr int PS = 64 + 8;
+  const unsigned int sel = stash_sel(col);
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; r += 2) {
-      const unsigned int w = word(t, r >> 1);
-      unsigned short* row = reinterpret_cast<unsigned short*>(st + (row0 + 16 * t + 4 * g + r) * PS + col);
-      row[0] = (unsigned short)w;
-      row[PS] = (unsigned short)(w >> 16);
-    }
+    for (int r = 0; r < 4; r += 2) stash_pair(st, row0 + 16 * t + 4 * g + r, col, sel, word(t, r >> 1));
 }
 // NT bf16 tiles held two per K block (act[t / 2], slots 4 (t % 2) + r)
 template <int NT, int NB>
