@@ -716,6 +716,7 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   FFN_HIP(h->tile_sched.ensure(sizeof(uint32_t) * (3 * nt1 + n_sums + 4)));
   uint32_t* tile_flags = (uint32_t*)h->tile_sched.p;
   a.tile_order = tile_flags + 2 * nt1;
+  a.n_busy = tile_flags + nt1 + n_tiles;  // the scan's total (offsets[n_tiles])
   if (taps) {
     a.t_sigma = taps->sigma;
     a.t_rgb = taps->rgb;

@@ -92,6 +92,10 @@ struct MlpArgs {
   // busy tiles first, so that the round-robin deal gives every block the same share of them), or tile i when
   // NULL
   const uint32_t* tile_order;
+  // with tile_order: the number of busy tiles (a sample with dt > 0), which the order puts first; the
+  // kernels composite the later positions' tiles to the background without the MLP (NULL: every tile takes
+  // the full path)
+  const uint32_t* n_busy;
   float sh_mult, occ_strength;
   uint32_t seed;
   int do_train;

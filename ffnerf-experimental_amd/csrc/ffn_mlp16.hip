@@ -601,9 +601,11 @@ __device__ __forceinline__ void load_tile_in(const MlpArgs& a, int64_t b, bool v
 }
 
 // MARCHED: the backward over marched samples (every tile busy): the loss gradients are read from a.in_dLds /
-// a.in_dLdc, the samples' rays, times and step from the march; no compositing, no proposals
-template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
+// a.in_dLdc, the samples' rays, times and step from the march; no compositing, no proposals.  TRAIN
+// (a.do_train) is a template parameter for the reason given at k_mlp.
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC, bool TRAIN>
 __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_mlp16(MlpArgs a) {
+  static_assert(TRAIN || !MARCHED, "marched launches train");
   using A = Arch16<LF, ND, NC>;
   constexpr int KB0 = LF / 16;  // D-layout tiles of the encoding
   extern __shared__ __align__(16) unsigned char smem16[];
@@ -615,7 +617,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
                                        (size_t)A::stash_halves() * 2);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
   const int col = wave * 16 + s;  // this lane's sample column in a tile
-  const bool train = a.do_train != 0;
+  constexpr bool train = TRAIN;
   const DevCfg& c = a.c;
   const int log2S = a.log2S;
   uint64_t n_samples = (uint64_t)a.num_rays << log2S;
@@ -667,9 +669,16 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
   for (int i = 0; i < (ND > 1 ? ND - 1 : 1); ++i) gd_h[i].zero();
   gd_in.zero();
 
+  // The busy tiles (a sample with dt > 0), which the tile order puts first, take the full path; a tile
+  // whose samples are all inactive (e.g. a ray that misses the box) composites to exactly the background
+  // and all its gradients are zero, so the later positions only write that (empty_tile).  Taps, which expose
+  // per-sample MLP outputs, take the full path for every tile.  (Two loops: an exit from the full path for
+  // the empty tiles had the register allocator copy the gradient accumulators on every tile.)
+  const int64_t n_full = (TAPS || MARCHED || !a.n_busy) ? n_tiles : (int64_t)*a.n_busy;
   int parity = 0;
+  int64_t ti = blockIdx.x;
 #pragma unroll 1
-  for (int64_t ti = blockIdx.x; ti < n_tiles; ti += gridDim.x, parity ^= 1) {
+  for (; ti < n_full; ti += gridDim.x, parity ^= 1) {
     const int64_t tile = a.tile_order ? (int64_t)a.tile_order[ti] : ti;
     float* sSig = sC + (train ? 0 : parity * 256);
     float* sRgb = sSig + 64;
@@ -683,10 +692,6 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     CompLane CL{};
     if constexpr (!MARCHED) {
       CL = load_comp_lane<SC>(a, tile, lane, prop_wave, n_samples, log2S, proposals);
-      if (!TAPS && __ballot(CL.vj && CL.dt_j > 0.0f) == 0ull) {  // the same on every wavefront of the block
-        empty_tile<LF, FEAT, SC>(a, CL, lane, wave, b, valid, train, g);
-        continue;
-      }
     }
     const float dirv[3] = {cur.rd.x, cur.rd.y, cur.rd.z};
     floatx4 sh;
@@ -839,6 +844,15 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
     layer_dw<4, KB0, PS>(sS, gd_in, wave, g, s);
     // no barrier: the stash is next written after the next tile's compositing barriers
   }
+  if constexpr (!MARCHED) {
+#pragma unroll 1
+    for (; ti < n_tiles; ti += gridDim.x) {
+      const int64_t tile = a.tile_order ? (int64_t)a.tile_order[ti] : ti;
+      const int64_t b = tile * 64 + col;
+      const CompLane CL = load_comp_lane<SC>(a, tile, lane, false, n_samples, log2S, false);
+      empty_tile<LF, FEAT, SC>(a, CL, lane, wave, b, (uint64_t)b < n_samples, train, g);
+    }
+  }
 
   if (train) {
     // every wavefront stores its tiles into the block's partial gradient
@@ -857,19 +871,29 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
 
 // ---------------------------------------------------------------------------
 
-template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
-static hipError_t launch16_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC, bool TRAIN>
+static hipError_t launch16_k(const MlpArgs& a, int n_blocks, hipStream_t st) {
   using A = Arch16<LF, ND, NC>;
   const size_t lds = A::lds_bytes();
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED, SC>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED, SC, TRAIN>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED, SC>), dim3(n_blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_mlp16<LF, ND, NC, FEAT, TAPS, MARCHED, SC, TRAIN>), dim3(n_blocks), dim3(256), lds, st, a);
   return hipGetLastError();
+}
+
+template <int LF, int ND, int NC, int FEAT, bool TAPS, bool MARCHED, int SC>
+static hipError_t launch16_f(const MlpArgs& a, int n_blocks, hipStream_t st) {
+  if constexpr (MARCHED) {
+    return launch16_k<LF, ND, NC, FEAT, TAPS, true, SC, true>(a, n_blocks, st);
+  } else {
+    return a.do_train ? launch16_k<LF, ND, NC, FEAT, TAPS, false, SC, true>(a, n_blocks, st)
+                      : launch16_k<LF, ND, NC, FEAT, TAPS, false, SC, false>(a, n_blocks, st);
+  }
 }
 
 template <int LF, int ND, int NC, bool MARCHED, int SC>
