@@ -149,6 +149,24 @@ __device__ __forceinline__ void bwd_tiles(const float* __restrict__ W, int P, co
   }
 }
 
+// The colour output layer's backward: res tiles = W^T . delta over the 64 hidden units, with the delta's
+// three rows held by lane group 0 (r = 0, 1, 2; the padded tile's other rows are zero).  Rows 1 and 2 move to
+// lane groups 1 and 2 (permlane row swaps with a zero partner, so every other row stays zero), which makes
+// the delta one K = 4 step (K index g, row 3 of the padded weights zero): four MFMAs where the padded tile's
+// four k-steps took sixteen.
+__device__ __forceinline__ void bwd_color_out(const float* __restrict__ W, int P, const floatx4 (&delta)[1],
+                                              floatx4 (&res)[4], int g, int s) {
+  const int d1 = __float_as_int(delta[0][1]), d2 = __float_as_int(delta[0][2]);
+  const int m1 = (int)__builtin_amdgcn_permlane16_swap(0, d1, false, false)[0];  // row 1 <- row 0
+  const int m2 = (int)__builtin_amdgcn_permlane32_swap(0, d2, false, false)[0];  // row 2 <- row 0
+  const float bk = __int_as_float(__float_as_int(delta[0][0]) | m1 | m2);
+  float w[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) w[t] = W[g * P + 16 * t + s];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) res[t] = mfma4(w[t], bk, floatx4{0.f, 0.f, 0.f, 0.f});
+}
+
 // The activation passes through an empty asm first: otherwise the compiler proves act > 0 equal to the
 // forward ReLU's own comparison and keeps that lane mask (two SGPRs per value, 48 values) live from the
 // forward to the backward, which spilled SGPRs to VGPR lanes by the hundred per tile.  Here the test is
@@ -520,9 +538,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     // colour output layer
     floatx4 dc[NC][4];
     stash_layer<1, 4, PSF>(sS, dco, hc[NC - 1], g, col);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) dc[NC - 1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    bwd_tiles<4, 1>(sW + A::w_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), dco, dc[NC - 1], g, s);
+    bwd_color_out(sW + A::w_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), dco, dc[NC - 1], g, s);
     relu_mask(dc[NC - 1], hc[NC - 1]);
     __syncthreads();
     layer_dw<1, 4, PSF>(sS, gc_out, wave, g, s);
