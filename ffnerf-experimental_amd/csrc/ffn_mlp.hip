@@ -245,6 +245,57 @@ __device__ __forceinline__ void layer_dw(const float* __restrict__ st, WaveGrad<
   }
 }
 
+// The colour output layer's weight gradient dW[o][k] = sum_s delta[o][s] act[k][s] (three rows, 64 inputs)
+// on v_mfma_f32_4x4x1f32 (layout at fwd_color_out): wavefront w takes inputs 16w .. 16w + 15; lane l = 16 kq +
+// 4 sg + j is lane j of block 4 kq + sg and supplies, at step n, delta row j of sample 16 sg + n (A; row 3 is
+// the padding's zero row) and the activation of input 16w + 4 kq + j for that sample (B), so its register o
+// accumulates sample group sg's share of dW[o][16w + 4 kq + j]; the groups are summed at the flush.  16
+// instructions of 8 cycles where the padded 16-row tile took 16 of 32.  Wavefront 0 also sums the bias
+// gradient (lane l: delta row j over sample group sg).  The stash holds the 16 delta rows, then the inputs.
+template <int PSF>
+__device__ __forceinline__ void layer_dw_color_out(const float* __restrict__ st, WaveGrad<1, 4>& acc, int wave,
+                                                   int lane) {
+  const int j = lane & 3, sg = (lane >> 2) & 3, kq = lane >> 4;
+  const float* drow = st + j * PSF + 16 * sg;
+  const float* arow = st + (16 + 16 * wave + 4 * kq + j) * PSF + 16 * sg;
+  floatx4 dv[4], av[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    dv[q] = *reinterpret_cast<const floatx4*>(drow + 4 * q);
+    av[q] = *reinterpret_cast<const floatx4*>(arow + 4 * q);
+  }
+  floatx4 c = acc.w[0];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_4x4x1f32(dv[q][e], av[q][e], c, 0, 0, 0);
+  acc.w[0] = c;
+  if (wave == 0) {
+    float bs = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bs += (dv[q][0] + dv[q][1]) + (dv[q][2] + dv[q][3]);
+    acc.b += bs;
+  }
+}
+__device__ __forceinline__ void flush_color_out(float* __restrict__ dst, const WaveGrad<1, 4>& acc, int wave,
+                                                int lane) {
+  constexpr int O = FFN_C_OUT, In = FFN_M;
+  const int j = lane & 3, sg = (lane >> 2) & 3, kq = lane >> 4;
+#pragma unroll
+  for (int o = 0; o < O; ++o) {
+    float v = acc.w[0][o];
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 8);
+    if (sg == 0) dst[o * In + 16 * wave + 4 * kq + j] = v;
+  }
+  if (wave == 0) {
+    float bs = acc.b;
+    bs += __shfl_xor(bs, 4);
+    bs += __shfl_xor(bs, 8);
+    if (lane < O) dst[O * In + lane] = bs;
+  }
+}
+
 // store this wavefront's tiles of a layer into the block's partial gradient (packed [O][In] + [O])
 template <int OT, int IT>
 __device__ __forceinline__ void flush_layer(float* __restrict__ dst, int O, int In, const WaveGrad<OT, IT>& acc,
@@ -317,6 +368,34 @@ __device__ __forceinline__ void load_a0(const float* __restrict__ a0, const Feat
   }
 }
 
+// The colour output layer's forward (three rows of 64 inputs) on v_mfma_f32_4x4x1f32, whose 16 blocks of
+// four lanes each add a 4x4 outer product (block b: lane 4b + i supplies row i of A, lane 4b + j column j of
+// B, and lane 4b + j receives column j in its four registers; pinned by a probe).  Lane (g, s) is lane j =
+// s % 4 of block 4g + s / 4: it supplies weight row s % 4 (row 3 is the padding's zero row) of input unit
+// 16t + 4g + r and the activation of that unit for its sample, so after the 16 (t, r) steps it holds lane
+// group g's share of its sample's three outputs (and a zero fourth); two row swaps sum the four groups.
+// 16 instructions of 8 cycles where the padded 16-row tile took 16 of 32.  Every lane gets its sample's
+// colours.
+__device__ __forceinline__ void fwd_color_out(const float* __restrict__ W, const float* __restrict__ B, int P,
+                                              const floatx4 (&act)[4], int g, int s, float (&rgb)[3]) {
+  floatx4 part = {0.f, 0.f, 0.f, 0.f};
+  const float* wrow = W + (s & 3) * P + 4 * g;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const floatx4 w4 = *reinterpret_cast<const floatx4*>(wrow + 16 * t);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part = __builtin_amdgcn_mfma_f32_4x4x1f32(w4[r], act[t][r], part, 0, 0, 0);
+  }
+#pragma unroll
+  for (int o = 0; o < 3; ++o) {
+    const int x = __float_as_int(part[o]);
+    const auto h = __builtin_amdgcn_permlane32_swap(x, x, false, false);  // {lower half twice, upper half twice}
+    const int y = __float_as_int(__int_as_float((int)h[0]) + __int_as_float((int)h[1]));
+    const auto q = __builtin_amdgcn_permlane16_swap(y, y, false, false);  // {even rows twice, odd rows twice}
+    rgb[o] = sigmoid_soft((__int_as_float((int)q[0]) + __int_as_float((int)q[1])) + B[o]);
+  }
+}
+
 // forward of the wavefront's 16 samples through both MLPs (ffnerf_OG.cl:1373-1466): hidden activations
 // (kept for the backward), the colour-net input [dout | SH * mult] and the sigmoid colours
 template <int LF, int ND, int NC>
@@ -371,12 +450,7 @@ __device__ __forceinline__ void mlp_fwd_tile(const float* __restrict__ sW, const
   if constexpr (NC >= 4)
     fwd_tiles<4, 4>(sW + A::w_off(FFN_WC_23), sW + A::b_off(FFN_WC_23), A::pitch(FFN_WC_23), hc[2], hc[3], g, s,
                     true);
-  floatx4 co[1];
-  fwd_tiles<1, 4>(sW + A::w_off(FFN_WC_OUT), sW + A::b_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), hc[NC - 1], co, g, s,
-                  false);
-  rgb_s[0] = sigmoid_soft(co[0][0]);
-  rgb_s[1] = sigmoid_soft(co[0][1]);
-  rgb_s[2] = sigmoid_soft(co[0][2]);
+  fwd_color_out(sW + A::w_off(FFN_WC_OUT), sW + A::b_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), hc[NC - 1], g, s, rgb_s);
 }
 
 // MARCHED: the backward over marched samples -- sample b is a.smp[b] of ray a.ray_ids[b], its loss gradients
@@ -541,7 +615,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     bwd_color_out(sW + A::w_off(FFN_WC_OUT), A::pitch(FFN_WC_OUT), dco, dc[NC - 1], g, s);
     relu_mask(dc[NC - 1], hc[NC - 1]);
     __syncthreads();
-    layer_dw<1, 4, PSF>(sS, gc_out, wave, g, s);
+    layer_dw_color_out<PSF>(sS, gc_out, wave, lane);
     __syncthreads();
     // hidden colour layers (Wc_23, Wc_12, Wc_01)
 #pragma unroll
@@ -617,7 +691,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   if (train) {
     // every wavefront stores its tiles into the block's partial gradient
     float* dst = a.partials + (int64_t)blockIdx.x * A::g_total();
-    flush_layer(dst + A::g_off(FFN_WC_OUT), FFN_C_OUT, FFN_M, gc_out, wave, g, s);
+    flush_color_out(dst + A::g_off(FFN_WC_OUT), gc_out, wave, lane);
     if constexpr (NC >= 2) flush_layer(dst + A::g_off(FFN_WC_01), FFN_M, FFN_M, gc_h[0], wave, g, s);
     if constexpr (NC >= 3) flush_layer(dst + A::g_off(FFN_WC_12), FFN_M, FFN_M, gc_h[1], wave, g, s);
     if constexpr (NC >= 4) flush_layer(dst + A::g_off(FFN_WC_23), FFN_M, FFN_M, gc_h[2], wave, g, s);
