@@ -511,8 +511,18 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   const int64_t n_full = (TAPS || MARCHED || !a.n_busy) ? n_tiles : (int64_t)*a.n_busy;
   int parity = 0;
   int64_t ti = blockIdx.x;
+  // Issue priority.  The two blocks a CU holds (blocks b and b + gridDim.x / 2, as the dispatcher deals
+  // the grid) take turns, tile by tile, at the higher of two levels: the favoured block's wavefronts reach
+  // its barriers together while the other block fills the issue slots they leave (fp32 MFMAs and vector
+  // instructions never issue together), where equal levels let both blocks' wavefronts drift apart and
+  // wait at every barrier for the slowest (fp32 MLP 7.29 -> 7.13-7.19 ms; alternating every 2 or 4 tiles
+  // 7.20-7.22 ms).  The compositing wavefront, which the rest of its block waits for, runs above both.
+  const int gang = (int)(blockIdx.x >= gridDim.x / 2);
 #pragma unroll 1
   for (; ti < n_full; ti += gridDim.x, parity ^= 1) {
+    const bool gang_hi = (parity ^ gang) != 0;
+    if (gang_hi) __builtin_amdgcn_s_setprio(2);
+    else __builtin_amdgcn_s_setprio(1);
     const int64_t tile = a.tile_order ? (int64_t)a.tile_order[ti] : ti;
     float* sSig = sC + (train ? 0 : parity * 256);
     float* sRgb = sSig + 64;
@@ -580,6 +590,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
       // three wavefronts' SIMDs meanwhile run the CU's other block.
       if (prop_wave) {
         float dLds_j, dLdc_j[3];
+        __builtin_amdgcn_s_setprio(3);
         composite_tile<TAPS, SC>(a, sSig, sRgb, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
         if (train) {
           sSig[lane] = dLds_j;
@@ -587,6 +598,8 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
           sRgb[3 * lane + 1] = dLdc_j[1];
           sRgb[3 * lane + 2] = dLdc_j[2];
         }
+        if (gang_hi) __builtin_amdgcn_s_setprio(2);
+        else __builtin_amdgcn_s_setprio(1);
       }
       if (!train) continue;
       __syncthreads();

@@ -739,8 +739,12 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
       // compositing on 64 lanes by the tile's proposal wavefront, which also writes the output colour (and
       // taps); its loss gradients replace sigma and rgb in LDS (only it reads them), and after a barrier
       // every wavefront reads its own samples'.  The other three SIMDs meanwhile run the CU's other block.
+      // The compositing wavefront runs at a raised issue priority: the rest of its block waits for it
+      // (3.44 -> 3.37 ms).  Turns of the two blocks at two levels, which the fp32 kernel takes, measured
+      // 3.46-3.49 ms here, where MFMAs and vector instructions of the two blocks issue together.
       if (prop_wave) {
         float dLds_j, dLdc_j[3];
+        __builtin_amdgcn_s_setprio(3);
         composite_tile<TAPS, SC>(a, sSig, sRgb, CL, lane, 0, true, train, proposals, Dhalf, dLds_j, dLdc_j);
         if (train) {
           sSig[lane] = dLds_j;
@@ -748,6 +752,7 @@ __global__ __launch_bounds__(256, (Arch16<LF, ND, NC>::blocks_per_cu())) void k_
           sRgb[3 * lane + 1] = dLdc_j[1];
           sRgb[3 * lane + 2] = dLdc_j[2];
         }
+        __builtin_amdgcn_s_setprio(0);
       }
       if (!train) continue;
       __syncthreads();
