@@ -523,6 +523,7 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
     const bool gang_hi = (parity ^ gang) != 0;
     if (gang_hi) __builtin_amdgcn_s_setprio(2);
     else __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_sched_barrier(0);  // the turn starts here (the scheduler would sink it to the forward's end)
     const int64_t tile = a.tile_order ? (int64_t)a.tile_order[ti] : ti;
     float* sSig = sC + (train ? 0 : parity * 256);
     float* sRgb = sSig + 64;
