@@ -348,7 +348,9 @@ __device__ __forceinline__ unsigned int stash_sel(int s) { return (s & 1) ? 0x03
 __device__ __forceinline__ void stash_pair(__bf16* __restrict__ st, int n, int col, unsigned int sel,
                                            unsigned int w) {
   constexpr int PS = 64 + 8;
-  const unsigned int nb = (unsigned int)__builtin_amdgcn_update_dpp((int)w, (int)w, 0xB1, 0xF, 0xF, false);
+  // every lane receives a neighbour's word, so the move needs no old value (update_dpp with old = w had the
+  // compiler copy w into the destination first: one more instruction per stashed word; 3.38 -> 3.33 ms)
+  const unsigned int nb = (unsigned int)__builtin_amdgcn_mov_dpp((int)w, 0xB1, 0xF, 0xF, false);
   const unsigned int v = __builtin_amdgcn_perm(nb, w, sel);
   *reinterpret_cast<unsigned int*>(st + (n + (col & 1)) * PS + (col & ~1)) = v;
 }
