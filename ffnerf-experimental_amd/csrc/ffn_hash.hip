@@ -690,10 +690,11 @@ __global__ __launch_bounds__(256) void k_bin_meta_transpose(const uint32_t* __re
 // One block per bucket: sum its pairs in 64-bit fixed point in LDS, then apply the mode's update to the
 // bucket's slice of the table.  The bucket's pairs are one run in each round's slots (its row of the
 // bucket-major run table gives offset and length); a first pass over the row counts them (for the
-// fixed-point scale), the second
-// walks 16 rounds per wavefront at a time with every lane on one block of 8 pairs.  Zero pairs (the run
-// padding) are skipped.
-template <int F, int MODE>
+// fixed-point scale), the second walks SEG rounds per wavefront at a time with every lane on one block of 8
+// pairs: 16 rounds for long runs (a run's block found by selects over the 16 running ends in scalars), 64
+// for short ones (a binary search over the lanes' running ends).  Zero pairs (the run padding) are
+// skipped.
+template <int F, int MODE, int SEG>
 __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ meta,
                                                      const uint4* __restrict__ pbuf,
                                                      const float* __restrict__ cmax, BinApply ap,
@@ -701,7 +702,6 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   extern __shared__ unsigned long long acc[];
   __shared__ float wmax[16];
   __shared__ uint32_t wtot[16];
-  constexpr int SEG = 16;  // rounds per wavefront step
   // bucket, relative to the group, finest levels first: their buckets hold the most pairs, and the lighter
   // coarse-level blocks then fill the last wave of blocks (scatter 7.01 -> 6.91 ms at the benchmark shape)
   const int j = (int)gridDim.x - 1 - (int)blockIdx.x;
@@ -751,55 +751,83 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
   auto add = [&](uint32_t e, float v, int f) {
     if (v != 0.0f) atomicAdd(&acc[e * F + f], (unsigned long long)__double2ll_rn((double)v * scale));
   };
+  // one block of PAD_RUN pairs: PAD_RUN * F values, then the PAD_RUN entries
+  auto add_block = [&](const uint4* src) {
+    float v[PAD_RUN * F];
+#pragma unroll
+    for (int qq = 0; qq < 2 * F; ++qq) {
+      const float4 t4 = *reinterpret_cast<const float4*>(src + qq);
+      v[4 * qq] = t4.x;
+      v[4 * qq + 1] = t4.y;
+      v[4 * qq + 2] = t4.z;
+      v[4 * qq + 3] = t4.w;
+    }
+    const uint4 e8 = src[2 * F];
+    const uint32_t ev[PAD_RUN] = {e8.x & 0xFFFFu, e8.x >> 16, e8.y & 0xFFFFu, e8.y >> 16,
+                                  e8.z & 0xFFFFu, e8.z >> 16, e8.w & 0xFFFFu, e8.w >> 16};
+#pragma unroll
+    for (int p = 0; p < PAD_RUN; ++p)
+#pragma unroll
+      for (int f = 0; f < F; ++f) add(ev[p], v[p * F + f], f);
+  };
   if (mx > 0.0f) {
     const int64_t bpr = grp.np / PAD_RUN;  // pair blocks per round
     const int64_t blk_lvl = (int64_t)li * nr * bpr;
     for (int r0 = wave * SEG; r0 < nr_use; r0 += 16 * SEG) {
-      // lanes 0..SEG-1 hold rounds r0 + lane: run offset and block count, then the blocks' running ends
-      uint32_t m = 0;
-      if (lane < SEG && r0 + lane < nr_use) m = mrow[r0 + lane];
-      uint32_t incl = lane < SEG ? (m & 0xFFFFu) / PAD_RUN : 0u;
+      if constexpr (SEG == 16) {
+        // lanes 0..SEG-1 hold rounds r0 + lane: run offset and block count, then the blocks' running ends
+        uint32_t m = 0;
+        if (lane < SEG && r0 + lane < nr_use) m = mrow[r0 + lane];
+        uint32_t incl = lane < SEG ? (m & 0xFFFFu) / PAD_RUN : 0u;
 #pragma unroll
-      for (int d = 1; d < SEG; d <<= 1) {
-        const uint32_t o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
-      }
-      uint32_t ends[SEG], offs[SEG];
+        for (int d = 1; d < SEG; d <<= 1) {
+          const uint32_t o = __shfl_up(incl, d);
+          if (lane >= d) incl += o;
+        }
+        uint32_t ends[SEG], offs[SEG];
 #pragma unroll
-      for (int t = 0; t < SEG; ++t) {
-        ends[t] = __builtin_amdgcn_readlane(incl, t);
-        offs[t] = __builtin_amdgcn_readlane(m >> 16, t);
-      }
-      for (uint32_t q = (uint32_t)lane; q < ends[SEG - 1]; q += 64) {
-        // the run holding block q: the last round whose running start is <= q
-        uint32_t qb = 0, off = offs[0];
-        int sg = 0;
+        for (int t = 0; t < SEG; ++t) {
+          ends[t] = __builtin_amdgcn_readlane(incl, t);
+          offs[t] = __builtin_amdgcn_readlane(m >> 16, t);
+        }
+        for (uint32_t q = (uint32_t)lane; q < ends[SEG - 1]; q += 64) {
+          // the run holding block q: the last round whose running start is <= q
+          uint32_t qb = 0, off = offs[0];
+          int sg = 0;
 #pragma unroll
-        for (int t = 1; t < SEG; ++t) {
-          if (q >= ends[t - 1]) {
-            qb = ends[t - 1];
-            off = offs[t];
-            sg = t;
+          for (int t = 1; t < SEG; ++t) {
+            if (q >= ends[t - 1]) {
+              qb = ends[t - 1];
+              off = offs[t];
+              sg = t;
+            }
           }
+          add_block(pbuf + (blk_lvl + (int64_t)(r0 + sg) * bpr + off / PAD_RUN + (q - qb)) * pair_block_words(F));
         }
-        const uint4* src =
-            pbuf + (blk_lvl + (int64_t)(r0 + sg) * bpr + off / PAD_RUN + (q - qb)) * pair_block_words(F);
-        float v[PAD_RUN * F];
+      } else {
+        // short runs (a few blocks each): lane t holds round r0 + t, and the wavefront's blocks are dealt over
+        // its lanes in order; block q belongs to the first round whose running end exceeds q, found by a
+        // binary search over the lanes' running ends.  Every lane runs every search step (the loop count is
+        // the same for the whole wavefront), so the shuffles never read an inactive lane.
+        uint32_t m = 0;
+        if (r0 + lane < nr_use) m = mrow[r0 + lane];
+        const uint32_t nb = (m & 0xFFFFu) / PAD_RUN;
+        const uint32_t incl = wave_incl_sum(nb);
+        const uint32_t excl = incl - nb;
+        const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
+        for (uint32_t q0 = 0; q0 < total; q0 += 64) {
+          const uint32_t q = q0 + (uint32_t)lane;
+          int t = 0;
 #pragma unroll
-        for (int qq = 0; qq < 2 * F; ++qq) {
-          const float4 t4 = *reinterpret_cast<const float4*>(src + qq);
-          v[4 * qq] = t4.x;
-          v[4 * qq + 1] = t4.y;
-          v[4 * qq + 2] = t4.z;
-          v[4 * qq + 3] = t4.w;
+          for (int step = 32; step >= 1; step >>= 1) {
+            const uint32_t v = (uint32_t)__shfl((int)incl, t + step - 1);
+            if (v <= q) t += step;
+          }
+          const uint32_t qb = (uint32_t)__shfl((int)excl, t);
+          const uint32_t off = (uint32_t)__shfl((int)(m >> 16), t);
+          if (q < total)
+            add_block(pbuf + (blk_lvl + (int64_t)(r0 + t) * bpr + off / PAD_RUN + (q - qb)) * pair_block_words(F));
         }
-        const uint4 e8 = src[2 * F];
-        const uint32_t ev[PAD_RUN] = {e8.x & 0xFFFFu, e8.x >> 16, e8.y & 0xFFFFu, e8.y >> 16,
-                                      e8.z & 0xFFFFu, e8.z >> 16, e8.w & 0xFFFFu, e8.w >> 16};
-#pragma unroll
-        for (int p = 0; p < PAD_RUN; ++p)
-#pragma unroll
-          for (int f = 0; f < F; ++f) add(ev[p], v[p * F + f], f);
       }
     }
   }
@@ -1076,6 +1104,12 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     }
     grp.bucket_rel[grp.n_levels] = rel;
     const int n_buckets = rel;
+    // Runs of a few pair blocks (many buckets per level, as with 2^22-entry levels: 512 buckets of 8192
+    // entries): 64 rounds per wavefront step, so that every lane gets a block (16 rounds of ~2 blocks left
+    // half the lanes idle); cfg3 backward 15.2 -> 14.2 ms (uniform points), 16.9 -> 16.1 ms (shell).
+    // FFN_REDUCE_SHORT_RUNS=0 keeps the 16-round walk (the sums are exact, so both give the same table).
+    const char* sr_env = getenv("FFN_REDUCE_SHORT_RUNS");
+    const bool short_runs = plan.max_nbl >= 256 && !(sr_env && atoi(sr_env) == 0);
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
     const dim3 grid_tr((unsigned)((plan.n_rounds + 63) / 64), (unsigned)((plan.max_nbl + 63) / 64),
                        (unsigned)grp.n_levels);
@@ -1085,8 +1119,12 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                        lr, s.meta, s.cmax, s.pairs, n_dev);                                                        \
     hipLaunchKernelGGL(k_bin_meta_transpose, grid_tr, dim3(256), 0, st, s.meta, s.meta_t, grp.n_rounds,            \
                        grp.meta_stride, n_dev, emit_nt(FV));                                                       \
-    hipLaunchKernelGGL((k_bin_reduce<FV, MV>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,         \
-                       s.meta_t, s.pairs, s.cmax, ap, n_dev);                                                      \
+    if (short_runs)                                                                                                \
+      hipLaunchKernelGGL((k_bin_reduce<FV, MV, 64>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,   \
+                         s.meta_t, s.pairs, s.cmax, ap, n_dev);                                                    \
+    else                                                                                                           \
+      hipLaunchKernelGGL((k_bin_reduce<FV, MV, 16>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,   \
+                         s.meta_t, s.pairs, s.cmax, ap, n_dev);                                                    \
   } while (0)
 #define FFN_BIN_F(MV)                     \
   switch (c.F) {                          \

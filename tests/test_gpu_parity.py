@@ -405,6 +405,35 @@ def test_scatter_level_groups_bit_identical(gh, monkeypatch):
     assert np.array_equal(one_group.view(np.uint32), grouped.view(np.uint32))
 
 
+@pytest.mark.parametrize("points", ["uniform", "rays"])
+def test_scatter_short_run_walk_bit_identical(gh, ora, monkeypatch, points):
+    """Levels of 2^22 entries have 512 buckets, so a bucket's run of an emit round is a few pair blocks and
+    the reduce walks 64 rounds per wavefront step (a binary search finds each lane's run).  Its fixed-point
+    sums are exact, so the table gradient equals the 16-round walk's (FFN_REDUCE_SHORT_RUNS=0) bit for bit,
+    with runs of every length (points along rays at the coarse level, uniform points at the fine one); and
+    both are the oracle's float64 sums."""
+    print(f"[case] scatter short-run walk {points}", flush=True)
+    spec = spec_cfg0(n_levels=2, log2_T=[22, 22], res=[64.0, 2048.0])
+    p = random_params(spec, seed=141)
+    rng = np.random.default_rng(142)
+    lo, hi = np.array(spec["box_min"]), np.array(spec["box_max"])
+    if points == "rays":
+        x = _ray_walk_points(rng, lo, hi, 1024, 64)
+    else:
+        x = (lo + (hi - lo) * rng.uniform(0, 1, (70000, 3))).astype(np.float32)
+    LF = spec["n_levels"] * spec["f_per_level"]
+    g = rng.normal(size=(x.shape[0], LF)).astype(np.float32)
+    m = gh.GpuModel(spec, p)
+    short = m.encode_bwd(x, g, table_floats(spec))
+    monkeypatch.setenv("FFN_REDUCE_SHORT_RUNS", "0")
+    long16 = m.encode_bwd(x, g, table_floats(spec))
+    monkeypatch.delenv("FFN_REDUCE_SHORT_RUNS")
+    assert np.abs(short).max() > 0
+    assert np.array_equal(short.view(np.uint32), long16.view(np.uint32))
+    grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
+    assert np.abs(short - grad_o).max() <= 1e-5 * np.abs(grad_o).max()
+
+
 def test_stage_times(gh):
     """ffn_set_profiling / ffn_stage_times (the reference's profiling queue and event_ms,
     ffnerf_tools.py:11-13,127-138): with profiling on, each stage of a training step is bracketed by
