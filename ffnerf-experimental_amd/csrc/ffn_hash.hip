@@ -691,9 +691,8 @@ __global__ __launch_bounds__(256) void k_bin_meta_transpose(const uint32_t* __re
 // bucket's slice of the table.  The bucket's pairs are one run in each round's slots (its row of the
 // bucket-major run table gives offset and length); a first pass over the row counts them (for the
 // fixed-point scale), the second walks SEG rounds per wavefront at a time with every lane on one block of 8
-// pairs: 16 rounds for long runs (a run's block found by selects over the 16 running ends in scalars), 64
-// for short ones (a binary search over the lanes' running ends).  Zero pairs (the run padding) are
-// skipped.
+// pairs: 16 rounds (a block's run found by selects over the 16 running ends in scalars) or 64 (a binary
+// search over the lanes' running ends).  Zero pairs (the run padding) are skipped.
 template <int F, int MODE, int SEG>
 __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, const uint32_t* __restrict__ meta,
                                                      const uint4* __restrict__ pbuf,
@@ -805,10 +804,10 @@ __global__ __launch_bounds__(1024) void k_bin_reduce(DevCfg c, BinGroup grp, con
           add_block(pbuf + (blk_lvl + (int64_t)(r0 + sg) * bpr + off / PAD_RUN + (q - qb)) * pair_block_words(F));
         }
       } else {
-        // short runs (a few blocks each): lane t holds round r0 + t, and the wavefront's blocks are dealt over
-        // its lanes in order; block q belongs to the first round whose running end exceeds q, found by a
-        // binary search over the lanes' running ends.  Every lane runs every search step (the loop count is
-        // the same for the whole wavefront), so the shuffles never read an inactive lane.
+        // lane t holds round r0 + t, and the wavefront's blocks are dealt over its lanes in order; block q
+        // belongs to the first round whose running end exceeds q, found by a binary search over the lanes'
+        // running ends.  Every lane runs every search step (the loop count is the same for the whole
+        // wavefront), so the shuffles never read an inactive lane.
         uint32_t m = 0;
         if (r0 + lane < nr_use) m = mrow[r0 + lane];
         const uint32_t nb = (m & 0xFFFFu) / PAD_RUN;
@@ -1104,12 +1103,14 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
     }
     grp.bucket_rel[grp.n_levels] = rel;
     const int n_buckets = rel;
-    // Runs of a few pair blocks (many buckets per level, as with 2^22-entry levels: 512 buckets of 8192
-    // entries): 64 rounds per wavefront step, so that every lane gets a block (16 rounds of ~2 blocks left
-    // half the lanes idle); cfg3 backward 15.2 -> 14.2 ms (uniform points), 16.9 -> 16.1 ms (shell).
-    // FFN_REDUCE_SHORT_RUNS=0 keeps the 16-round walk (the sums are exact, so both give the same table).
-    const char* sr_env = getenv("FFN_REDUCE_SHORT_RUNS");
-    const bool short_runs = plan.max_nbl >= 256 && !(sr_env && atoi(sr_env) == 0);
+    // The reduce walks 64 rounds per wavefront step where a level has many buckets (2^22-entry levels: 512
+    // buckets of 8192 entries, runs of about two pair blocks, which left half the lanes of a 16-round step
+    // idle; cfg3 backward 15.2 -> 14.2 ms uniform, 16.9 -> 16.1 ms shell) or enough rounds to give every
+    // wavefront of a block 64 (the benchmark shape: 16,384 rounds, scatter 6.83 -> 6.74 ms); small batches
+    // keep 16 rounds so that their few rounds spread over the block's wavefronts.  FFN_REDUCE_WALK64=0
+    // keeps the 16-round walk everywhere (the sums are exact, so both give the same table bit for bit).
+    const char* w_env = getenv("FFN_REDUCE_WALK64");
+    const bool walk64 = (plan.max_nbl >= 256 || plan.n_rounds >= 16 * 64) && !(w_env && atoi(w_env) == 0);
     const dim3 grid_bl((unsigned)plan.nblk, (unsigned)grp.n_levels);
     const dim3 grid_tr((unsigned)((plan.n_rounds + 63) / 64), (unsigned)((plan.max_nbl + 63) / 64),
                        (unsigned)grp.n_levels);
@@ -1119,7 +1120,7 @@ hipError_t launch_hash_bwd(const DevCfg& c, const PosSrc& src, int64_t n, const 
                        lr, s.meta, s.cmax, s.pairs, n_dev);                                                        \
     hipLaunchKernelGGL(k_bin_meta_transpose, grid_tr, dim3(256), 0, st, s.meta, s.meta_t, grp.n_rounds,            \
                        grp.meta_stride, n_dev, emit_nt(FV));                                                       \
-    if (short_runs)                                                                                                \
+    if (walk64)                                                                                                    \
       hipLaunchKernelGGL((k_bin_reduce<FV, MV, 64>), dim3((unsigned)n_buckets), dim3(1024), lds_acc, st, c, grp,   \
                          s.meta_t, s.pairs, s.cmax, ap, n_dev);                                                    \
     else                                                                                                           \

@@ -405,33 +405,38 @@ def test_scatter_level_groups_bit_identical(gh, monkeypatch):
     assert np.array_equal(one_group.view(np.uint32), grouped.view(np.uint32))
 
 
-@pytest.mark.parametrize("points", ["uniform", "rays"])
-def test_scatter_short_run_walk_bit_identical(gh, ora, monkeypatch, points):
-    """Levels of 2^22 entries have 512 buckets, so a bucket's run of an emit round is a few pair blocks and
-    the reduce walks 64 rounds per wavefront step (a binary search finds each lane's run).  Its fixed-point
-    sums are exact, so the table gradient equals the 16-round walk's (FFN_REDUCE_SHORT_RUNS=0) bit for bit,
-    with runs of every length (points along rays at the coarse level, uniform points at the fine one); and
-    both are the oracle's float64 sums."""
-    print(f"[case] scatter short-run walk {points}", flush=True)
-    spec = spec_cfg0(n_levels=2, log2_T=[22, 22], res=[64.0, 2048.0])
+@pytest.mark.parametrize("case", ["uniform22", "rays22", "cfg2_shape"])
+def test_scatter_walk64_bit_identical(gh, ora, monkeypatch, case):
+    """The reduce walks 64 rounds per wavefront step (a binary search finds each lane's run) where a level
+    has many buckets (2^22 entries: 512 buckets, runs of a few pair blocks) or the batch has at least 1024
+    emit rounds (the benchmark shape's 16 levels of 2^19), 16 rounds otherwise.  Its fixed-point sums are
+    exact, so the table gradient equals the 16-round walk's (FFN_REDUCE_WALK64=0) bit for bit, with runs of
+    every length (points along rays at a coarse level, uniform points at a fine one); the 2^22 cases are the
+    oracle's float64 sums as well."""
+    print(f"[case] scatter walk64 {case}", flush=True)
+    if case == "cfg2_shape":
+        spec = spec_cfg1(hash_opt=1)
+    else:
+        spec = spec_cfg0(n_levels=2, log2_T=[22, 22], res=[64.0, 2048.0])
     p = random_params(spec, seed=141)
     rng = np.random.default_rng(142)
     lo, hi = np.array(spec["box_min"]), np.array(spec["box_max"])
-    if points == "rays":
-        x = _ray_walk_points(rng, lo, hi, 1024, 64)
-    else:
+    if case == "uniform22":
         x = (lo + (hi - lo) * rng.uniform(0, 1, (70000, 3))).astype(np.float32)
+    else:
+        x = _ray_walk_points(rng, lo, hi, 1024 if case == "rays22" else 16400, 64)  # cfg2_shape: 1025 rounds
     LF = spec["n_levels"] * spec["f_per_level"]
     g = rng.normal(size=(x.shape[0], LF)).astype(np.float32)
     m = gh.GpuModel(spec, p)
-    short = m.encode_bwd(x, g, table_floats(spec))
-    monkeypatch.setenv("FFN_REDUCE_SHORT_RUNS", "0")
-    long16 = m.encode_bwd(x, g, table_floats(spec))
-    monkeypatch.delenv("FFN_REDUCE_SHORT_RUNS")
-    assert np.abs(short).max() > 0
-    assert np.array_equal(short.view(np.uint32), long16.view(np.uint32))
-    grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
-    assert np.abs(short - grad_o).max() <= 1e-5 * np.abs(grad_o).max()
+    w64 = m.encode_bwd(x, g, table_floats(spec))
+    monkeypatch.setenv("FFN_REDUCE_WALK64", "0")
+    w16 = m.encode_bwd(x, g, table_floats(spec))
+    monkeypatch.delenv("FFN_REDUCE_WALK64")
+    assert np.abs(w64).max() > 0
+    assert np.array_equal(w64.view(np.uint32), w16.view(np.uint32))
+    if case != "cfg2_shape":
+        grad_o = ora.hash_backward(ora.make_cfg(spec), x, g, table_floats(spec))
+        assert np.abs(w64 - grad_o).max() <= 1e-5 * np.abs(grad_o).max()
 
 
 def test_stage_times(gh):
