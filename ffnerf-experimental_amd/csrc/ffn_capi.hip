@@ -670,10 +670,14 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   float* dLda0 = (float*)h->dLda0.p;
   const ffn_params& P = h->params;
 
+  // the MLP's tile order (below): the sampler writes the tiles' busy flags
+  const size_t nt1 = (size_t)n_tiles + 1, n_sums = ((size_t)n_tiles + 4096) / 4096 + 2;
+  FFN_HIP(h->tile_sched.ensure(sizeof(uint32_t) * (3 * nt1 + n_sums + 4)));
+  uint32_t* tile_flags = (uint32_t*)h->tile_sched.p;
   {
     StageTimer tm(h, 0, st);
     FFN_HIP(ffn::launch_sample(h->dc, (const float4*)rays, num_rays, (int)spr, sc->rng_seed, P.occ_in,
-                               train ? 1 : 0, Ts, DTs, flags, st));
+                               train ? 1 : 0, Ts, DTs, flags, st, tile_flags));
   }
   {
     StageTimer tm(h, 1, st);
@@ -712,9 +716,6 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   a.do_train = train ? 1 : 0;
   // the MLP's tile order: the busy tiles first, so that every block gets the same share of them (fp32 MLP
   // 8.41 -> 8.30 ms at the benchmark shape)
-  const size_t nt1 = (size_t)n_tiles + 1, n_sums = ((size_t)n_tiles + 4096) / 4096 + 2;
-  FFN_HIP(h->tile_sched.ensure(sizeof(uint32_t) * (3 * nt1 + n_sums + 4)));
-  uint32_t* tile_flags = (uint32_t*)h->tile_sched.p;
   a.tile_order = tile_flags + 2 * nt1;
   a.n_busy = tile_flags + nt1 + n_tiles;  // the scan's total (offsets[n_tiles])
   if (taps) {
@@ -729,7 +730,7 @@ int ffn_train_step(void* handle, const void* rays, const void* targets, void* ou
   }
   {
     StageTimer tm(h, 2, st);
-    FFN_HIP(ffn::launch_tile_order(DTs, (int64_t)N, n_tiles, tile_flags, tile_flags + nt1, tile_flags + 3 * nt1,
+    FFN_HIP(ffn::launch_tile_order(n_tiles, tile_flags, tile_flags + nt1, tile_flags + 3 * nt1,
                                    tile_flags + 3 * nt1 + n_sums, const_cast<uint32_t*>(a.tile_order), st));
     if (mlp16)
       FFN_HIP(ffn::launch_mlp16(a, LF, h->cfg.nd, h->cfg.nc, n_blocks, st));

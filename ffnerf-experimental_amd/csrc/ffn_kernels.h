@@ -158,9 +158,10 @@ BinPlan plan_bins(const DevCfg& c, int64_t n, size_t pair_budget_bytes);
 // offsets in 16 bits (F = 4 with 2^22-entry levels does not)
 bool scatter_supported(const DevCfg& c);
 
+// tile_busy (may be NULL): word t = 1 when one of samples 64t .. 64t + 63 has dt > 0 (the MLP's busy tiles)
 hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays, int S, uint32_t seed,
                          const uint32_t* occ_in, int do_train, float* Ts, float* DTs, uint32_t* flags,
-                         hipStream_t st);
+                         hipStream_t st, uint32_t* tile_busy = nullptr);
 
 // table: float, or binary16 when c.table_f16 (widened exactly; the sums are the same fp32 operations)
 // Dense copies of the coarse levels' vertex values (the table's element type, F per vertex) from
@@ -312,8 +313,9 @@ int mlp16_blocks_per_cu(int LF, int nd, int nc);  // blocks of launch_mlp16 that
 hipError_t launch_mlp(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);
 // order[n_tiles]: the tiles with a sample of dt > 0 in index order, then the others; scratch: flags and off
 // n_tiles + 1 words each, sums (n_tiles + 4096) / 4096 + 1 words, total 1 word
-hipError_t launch_tile_order(const float* DTs, int64_t n_samples, int64_t n_tiles, uint32_t* flags, uint32_t* off,
-                             uint32_t* sums, uint32_t* total, uint32_t* order, hipStream_t st);
+// flags: the tiles' busy flags (launch_sample's tile_busy)
+hipError_t launch_tile_order(int64_t n_tiles, const uint32_t* flags, uint32_t* off, uint32_t* sums, uint32_t* total,
+                             uint32_t* order, hipStream_t st);
 // the same kernel's backward over marched samples (a.smp, a.ray_ids, a.in_dLds, a.in_dLdc; a.num_rays = the
 // sample count, log2S = 0): no compositing, no proposals
 hipError_t launch_mlp_marched(const MlpArgs& a, int LF, int nd, int nc, int n_blocks, hipStream_t st);

@@ -869,22 +869,11 @@ hipError_t launch_mlp_fwd(const DevCfg& c, const MlpPtrs& w, const float* a0, co
   return hipErrorInvalidValue;
 }
 
-// Tile order of a step: one wavefront per tile flags whether any of its samples has dt > 0 (the tiles the
-// MLP computes; the others composite to the background); the scan of the flags places the busy tiles first,
-// in index order, then the others.  With the busy tiles dealt round-robin the blocks get equal shares of
-// them (with tiles dealt in index order, a quarter of the rays missing the box left the busiest of 512
-// blocks 8.5 % above the mean).  The order depends on the data alone, so steps stay deterministic.
-__global__ __launch_bounds__(256) void k_tile_busy(const float* __restrict__ DTs, int64_t n_samples,
-                                                   int64_t n_tiles, uint32_t* __restrict__ flags) {
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (t >= n_tiles) return;  // the same for the whole wavefront
-  const int64_t b = t * 64 + lane;
-  const bool busy = b < n_samples && DTs[b] > 0.0f;
-  const uint64_t m = __ballot(busy);
-  if (lane == 0) flags[t] = m != 0ull ? 1u : 0u;
-}
-
+// Tile order of a step: the sampler flags each 64-sample tile with a sample of dt > 0 (the tiles the MLP
+// computes; the others composite to the background); the scan of the flags places the busy tiles first, in
+// index order, then the others.  With the busy tiles dealt round-robin the blocks get equal shares of them
+// (with tiles dealt in index order, a quarter of the rays missing the box left the busiest of 512 blocks
+// 8.5 % above the mean).  The order depends on the data alone, so steps stay deterministic.
 __global__ __launch_bounds__(256) void k_tile_place(const uint32_t* __restrict__ flags,
                                                     const uint32_t* __restrict__ off, int64_t n_tiles,
                                                     uint32_t* __restrict__ order) {
@@ -894,11 +883,9 @@ __global__ __launch_bounds__(256) void k_tile_place(const uint32_t* __restrict__
   order[flags[t] ? o : n_busy + ((uint32_t)t - o)] = (uint32_t)t;
 }
 
-hipError_t launch_tile_order(const float* DTs, int64_t n_samples, int64_t n_tiles, uint32_t* flags, uint32_t* off,
-                             uint32_t* sums, uint32_t* total, uint32_t* order, hipStream_t st) {
+hipError_t launch_tile_order(int64_t n_tiles, const uint32_t* flags, uint32_t* off, uint32_t* sums, uint32_t* total,
+                             uint32_t* order, hipStream_t st) {
   if (n_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_tile_busy, dim3((unsigned)((n_tiles + 3) / 4)), dim3(256), 0, st, DTs, n_samples, n_tiles,
-                     flags);
   hipError_t e = launch_scan_u32(flags, n_tiles, off, sums, total, st);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_tile_place, dim3((unsigned)((n_tiles + 255) / 256)), dim3(256), 0, st, flags, off, n_tiles,

@@ -149,7 +149,7 @@ __device__ __forceinline__ SampleOut sample_lane(const DevCfg& c, const float4* 
 __global__ __launch_bounds__(256) void k_sample(DevCfg c, const float4* __restrict__ rays, uint32_t num_rays,
                                                 int S, int log2S, uint32_t seed, const uint32_t* __restrict__ occ_in,
                                                 int do_train, float* __restrict__ Ts, float* __restrict__ DTs,
-                                                uint32_t* __restrict__ flags) {
+                                                uint32_t* __restrict__ flags, uint32_t* __restrict__ tile_busy) {
   const uint64_t gtid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int lane = threadIdx.x & 63;
   const int lid = lane & (S - 1);
@@ -159,6 +159,9 @@ __global__ __launch_bounds__(256) void k_sample(DevCfg c, const float4* __restri
   const uint32_t ray_id = valid ? (uint32_t)ray64 : 0u;
   SampleOut so = sample_lane(c, rays, ray_id, valid, lid, S, base, seed, occ_in, do_train);
   const uint64_t bal = __ballot(so.run_start);
+  // a wavefront's 64 lanes are the 64 samples of one MLP tile: whether any of them is active (dt > 0)
+  const uint64_t busy = __ballot(valid && so.dt > 0.0f);
+  if (tile_busy && lane == 0 && (uint64_t)(gtid >> log2S) < num_rays) tile_busy[gtid >> 6] = busy != 0ull ? 1u : 0u;
   if (!valid) return;
   Ts[gtid] = so.t;
   DTs[gtid] = so.dt;
@@ -171,13 +174,13 @@ __global__ __launch_bounds__(256) void k_sample(DevCfg c, const float4* __restri
 
 hipError_t launch_sample(const DevCfg& c, const float4* rays, uint32_t num_rays, int S, uint32_t seed,
                          const uint32_t* occ_in, int do_train, float* Ts, float* DTs, uint32_t* flags,
-                         hipStream_t st) {
+                         hipStream_t st, uint32_t* tile_busy) {
   int log2S = 0;
   while ((1 << log2S) < S) ++log2S;
   const uint64_t threads = (uint64_t)num_rays * (uint64_t)S;
   const uint64_t blocks = (threads + 255) / 256;
   hipLaunchKernelGGL(k_sample, dim3((unsigned)blocks), dim3(256), 0, st, c, rays, num_rays, S, log2S, seed, occ_in,
-                     do_train, Ts, DTs, flags);
+                     do_train, Ts, DTs, flags, tile_busy);
   return hipGetLastError();
 }
 
