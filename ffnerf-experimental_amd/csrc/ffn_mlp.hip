@@ -512,11 +512,12 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
   int parity = 0;
   int64_t ti = blockIdx.x;
   // Issue priority.  The two blocks a CU holds (blocks b and b + gridDim.x / 2, as the dispatcher deals
-  // the grid) take turns, tile by tile, at the higher of two levels: the favoured block's wavefronts reach
-  // its barriers together while the other block fills the issue slots they leave (fp32 MFMAs and vector
-  // instructions never issue together), where equal levels let both blocks' wavefronts drift apart and
-  // wait at every barrier for the slowest (fp32 MLP 7.29 -> 7.13-7.19 ms; alternating every 2 or 4 tiles
-  // 7.20-7.22 ms).  The compositing wavefront, which the rest of its block waits for, runs above both.
+  // the grid) take turns at the higher of two levels, twice a tile (the forward with the compositing, then
+  // the backward): the favoured block's wavefronts reach its barriers together while the other block fills
+  // the issue slots they leave (fp32 MFMAs and vector instructions never issue together), where equal levels
+  // let both blocks' wavefronts drift apart and wait at every barrier for the slowest (fp32 MLP 7.29 ->
+  // 7.13-7.19 ms with one turn per tile, 7.09-7.11 with two; one turn every 2 or 4 tiles 7.20-7.22, four per
+  // tile 7.14-7.30).  The compositing wavefront, which the rest of its block waits for, runs above both.
   const int gang = (int)(blockIdx.x >= gridDim.x / 2);
 #pragma unroll 1
   for (; ti < n_full; ti += gridDim.x, parity ^= 1) {
@@ -599,9 +600,10 @@ __global__ __launch_bounds__(256, (Arch<LF, ND, NC>::blocks_per_cu())) void k_ml
           sRgb[3 * lane + 1] = dLdc_j[1];
           sRgb[3 * lane + 2] = dLdc_j[2];
         }
-        if (gang_hi) __builtin_amdgcn_s_setprio(2);
-        else __builtin_amdgcn_s_setprio(1);
       }
+      // the tile's second turn: the block that led the forward yields the backward
+      if (gang_hi) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(2);
       if (!train) continue;
       __syncthreads();
       dLds = sSig[col];
