@@ -17,8 +17,9 @@ What is compared, and how every difference is accounted for:
 - Adam: the GPU's updated parameter, m and v are Adam of the GPU's own summed
   gradient bit for bit (``ora.adam`` on the tapped gradient).  Against the
   restatement's parameters, the entries whose update differs by more than
-  the path's tolerance are counted and bounded in number (2 % of a layer on
-  the fp32 path, 10 % on the fp16 path), each is at most two Adam steps, and
+  the path's tolerance are counted and bounded in number (0.1 % of a layer,
+  at least 4 entries, on the fp32 path; 10 % on the fp16 path), each is at
+  most two Adam steps, and
   each has a gradient within the layer's gradient tolerance (a gradient
   within rounding of zero, where Adam's step is sign-like, or a cancelling
   first moment);
@@ -36,10 +37,14 @@ import numpy as np
 
 from common import BIASES, LAYERS, layer_shapes
 
-# tolerances per MLP path (fp32 MFMA; fp16/bf16 MFMA)
+# tolerances per MLP path (fp32 MFMA; fp16/bf16 MFMA).  The counted allowances (ReLU flips, Adam updates
+# outside the tolerance) sit 5-10x above the largest counts the GPU suite produces (fp32: at most 1.7e-6 of
+# the units flip, at most 2e-6 of a table's entries or one entry of an MLP layer move apart; fp16: 9.3e-5 of
+# the units with |pre-activation| <= 3.3e-4 of the layer's largest, 4.8 % of a layer's entries); the kernels
+# are deterministic, so the suite reproduces those counts exactly
 TOL = {
-    0: dict(fwd=1e-4, out=1e-4, loss=1e-3, grad=1e-3, table=1e-3, flip_z=1e-5, flip_frac=1e-4, undet_frac=0.02),
-    1: dict(fwd=1e-2, out=1e-2, loss=1e-2, grad=1e-2, table=1e-2, flip_z=3e-2, flip_frac=1e-2, undet_frac=0.10),
+    0: dict(fwd=1e-4, out=1e-4, loss=1e-3, grad=1e-3, table=1e-3, flip_z=1e-5, flip_frac=2e-5, undet_frac=1e-3),
+    1: dict(fwd=1e-2, out=1e-2, loss=1e-2, grad=1e-2, table=1e-2, flip_z=3e-3, flip_frac=1e-3, undet_frac=0.10),
 }
 
 

@@ -121,7 +121,8 @@ def test_render_cfg4_full_batch_equals_subset(gh, field4, mlp):
 def test_marched_steps_cfg4_match_oracle(gh, ora, field4, mlp, T_stop):
     """The marched training step with the config-1 MLPs (LF = 32) on configs[4]'s field, two steps from the
     GPU's state, checked as tests/parity.py's compare_marched_step describes.  A fp16 run's ray may stop one
-    sample apart from the fp32 restatement's more often than a fp32 run's (5 % of rays against 1 %)."""
+    sample apart from the fp32 restatement's more often than a fp32 run's (allowed: 1 % of rays against 0.5 %,
+    at least two; none does in these runs)."""
     import ffn_lib as fl
     print(f"[case] cfg4 marched train mlp={mlp} T_stop={T_stop}", flush=True)
     spec = spec_cfg1(hash_opt=1, mlp_precision=mlp)
@@ -132,7 +133,7 @@ def test_marched_steps_cfg4_match_oracle(gh, ora, field4, mlp, T_stop):
     for step in range(2):
         sc = default_scalars(rng_seed=4000 + step, occ_strength=0.0)
         m, _, stats = compare_marched_step(spec, p, rays, tg, field4, mp, sc, gh, ora,
-                                           flip_frac=0.01 if mlp == 0 else 0.05)
+                                           flip_frac=0.005 if mlp == 0 else 0.01)
         print(f"[step {step}] {stats}", flush=True)
         assert stats["samples"] > 5000
         p = m.state()
